@@ -1,0 +1,270 @@
+"""Benchmark of the smooth-attn hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+
+A step is one forward + backward pass of the causal squareplus
+normalisation over BASELINE config 2 at L=4096 (x = randn/sqrt(128) and
+dy = randn, bf16 [4,16,4096,4096], family alpha=2, theta=0.5, p=2), run
+through the public autograd API.  ``value`` is algorithmic HBM bytes per
+step / step time.  Algorithmic bytes: the forward reads the causal triangle
+of x and writes the full output; the backward reads the triangle of x and
+dy and writes the full dx (2 bytes per element).
+
+The same JSON line carries the fused-attention figure the metric also names
+(config 3, TFLOP/s over the causal triangle), the roofline of the dominant
+kernel (from HIP events around each launch), and the CPU baseline: the
+reference's eager CPU path restated in oracle/ (fp32 torch on the host
+cores), timed on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "smooth-attn_amd"))
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2516.6
+FP8_PEAK_TFLOPS = 5033.2
+METRIC = "causal-norm fwd+bwd HBM GB/s (% peak); fused attn TFLOP/s, L=4096 D=128"
+
+
+def tri(n):
+    return n * (n + 1) // 2
+
+
+def norm_bytes(B, H, L, elem=2):
+    fwd = B * H * elem * (tri(L) + L * L)
+    bwd = B * H * elem * (2 * tri(L) + L * L)
+    return fwd, bwd
+
+
+def attn_flops(B, H, L, D):
+    return 4 * B * H * D * tri(L)
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_model():
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor()
+
+
+def time_events(torch, fn, iters):
+    """Per-launch durations (ms) from HIP events on the current stream."""
+    st = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
+    for a, b in evs:
+        a.record(st)
+        fn()
+        b.record(st)
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) for a, b in evs]
+
+
+def bench_norm(torch, sa, steps, warmup):
+    from smooth_attn import FamilyConfig, kernels
+
+    B, H, L = 4, 16, 4096
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(2)
+    x = (torch.randn(B, H, L, L, generator=gen, device=dev) / math.sqrt(128)).to(torch.bfloat16)
+    dy = torch.randn(B, H, L, L, generator=gen, device=dev).to(torch.bfloat16)
+    xg = x.detach().requires_grad_(True)
+    fam = FamilyConfig()
+
+    def step():
+        y = sa.softplus_norm_causal(xg, family=fam)
+        (dx,) = torch.autograd.grad(y, xg, dy)
+        return dx
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / steps
+
+    # Kernel-level timing: HIP events around each launch on the launch stream.
+    out = torch.empty_like(x)
+    n_ev = max(steps, 10)
+    fwd_ms = time_events(torch, lambda: sa.softplus_norm_causal_triton_out(out, x, family=fam), n_ev)
+    bwd_ms = time_events(torch, lambda: kernels._softplus_norm_causal_backward(x, dy, fam), n_ev)
+    fwd_b, bwd_b = norm_bytes(B, H, L)
+    fwd_avg = sum(fwd_ms) / len(fwd_ms)
+    bwd_avg = sum(bwd_ms) / len(bwd_ms)
+    sample = x[0, 0].cpu(), dy[0, 0].cpu()
+    del x, dy, xg, out
+    torch.cuda.empty_cache()
+    return {
+        "shape": [B, H, L, L],
+        "ms_per_step": ms_per_step,
+        "gbs": (fwd_b + bwd_b) / (ms_per_step * 1e-3) / 1e9,
+        "fwd_bytes": fwd_b,
+        "bwd_bytes": bwd_b,
+        "fwd_us": fwd_avg * 1e3,
+        "bwd_us": bwd_avg * 1e3,
+        "fwd_gbs": fwd_b / (fwd_avg * 1e-3) / 1e9,
+        "bwd_gbs": bwd_b / (bwd_avg * 1e-3) / 1e9,
+        "sample": sample,
+    }
+
+
+def bench_attention(torch, sa, iters):
+    from smooth_attn import kernels
+
+    B, H, L, D = 4, 32, 4096, 128
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(3)
+    q = torch.randn(B, H, L, D, generator=gen, device=dev).to(torch.bfloat16)
+    k = torch.randn(B, H, L, D, generator=gen, device=dev).to(torch.bfloat16)
+    v = torch.randn(B, H, L, D, generator=gen, device=dev).to(torch.bfloat16)
+    scale = 1.0 / math.sqrt(D)
+    try:
+        kernels._sp2norm_flash_fwd(q, k, v, scale)
+    except RuntimeError as exc:
+        return {"status": f"not built: {exc}"}
+    for _ in range(3):
+        kernels._sp2norm_flash_fwd(q, k, v, scale)
+    ms = time_events(torch, lambda: kernels._sp2norm_flash_fwd(q, k, v, scale), iters)
+    avg = sum(ms) / len(ms)
+    flops = attn_flops(B, H, L, D)
+    return {
+        "config": "config3 fused causal attention fwd bf16 [4,32,4096,128]",
+        "us": avg * 1e3,
+        "tflops": flops / (avg * 1e-3) / 1e12,
+        "frac_bf16_peak": flops / (avg * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+        "flops": flops,
+    }
+
+
+def cpu_baseline(torch, sample, budget_s=20.0):
+    """The reference's eager CPU path (oracle restatement, fp32 torch) on one
+    [L, L] matrix of the benchmark input: forward + autograd backward."""
+    from oracle import eager
+
+    x, dy = sample
+    L = x.shape[-1]
+    threads = torch.get_num_threads()
+
+    def run():
+        xr = x.detach().clone().requires_grad_(True)
+        y = eager.softplus_norm_causal_eager(xr.float()).to(x.dtype)
+        y.backward(dy)
+        return xr.grad
+
+    run()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 5 and (time.perf_counter() - t_start) < budget_s:
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    fwd_b, bwd_b = norm_bytes(1, 1, L)
+    return {
+        "value": (fwd_b + bwd_b) / med / 1e9,
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"1 of 64 [{L},{L}] bf16 matrices of the same input, eager fp32 fwd + autograd bwd, "
+                  f"median of {len(times)} runs ({med * 1e3:.0f} ms each), host '{cpu_model()}', "
+                  f"torch threads {threads}",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the smooth-attn hot path has no multi-GPU component "
+              "(run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import smooth_attn as sa
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(1)
+
+    log("bench: causal norm fwd+bwd [4,16,4096,4096] bf16")
+    norm = bench_norm(torch, sa, args.steps, args.warmup)
+    log(f"bench: norm {norm['ms_per_step']:.3f} ms/step, fwd {norm['fwd_us']:.1f} us, bwd {norm['bwd_us']:.1f} us")
+    attn = None
+    if not args.no_extra:
+        log("bench: fused attention config 3")
+        attn = bench_attention(torch, sa, max(args.steps, 10))
+        log(f"bench: attention {attn}")
+    cpu = None
+    if not args.no_cpu:
+        log("bench: cpu baseline")
+        cpu = cpu_baseline(torch, norm["sample"])
+        log(f"bench: cpu {cpu['value']:.3f} GB/s")
+
+    dominant = "bwd" if norm["bwd_us"] >= norm["fwd_us"] else "fwd"
+    achieved = norm[f"{dominant}_gbs"]
+    line = {
+        "metric": METRIC,
+        "value": round(norm["gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(norm["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "config2: causal squareplus-norm fwd+bwd, bf16 [4,16,4096,4096], alpha=2 theta=0.5 p=2",
+            "algorithmic_bytes_per_step": norm["fwd_bytes"] + norm["bwd_bytes"],
+            "fwd_us": round(norm["fwd_us"], 2),
+            "bwd_us": round(norm["bwd_us"], 2),
+            "fwd_GBs": round(norm["fwd_gbs"], 1),
+            "bwd_GBs": round(norm["bwd_gbs"], 1),
+            "frac_hbm_peak_step": round(norm["gbs"] / HBM_PEAK_GBS, 4),
+            "compute_dtype": "f32",
+        },
+        "roofline": {
+            "kernel": f"norm_{dominant}_vec (causal, bf16, L=4096)",
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+        "attention": attn,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,190 @@
+/*
+ * smooth_attn_amd.h — C ABI of the MI355X (gfx950) smooth-attn hot path.
+ *
+ * Plain pointers, sizes and element strides; no torch types.  Every entry
+ * point is asynchronous on the given HIP stream, allocates nothing, and
+ * returns a status:
+ *      0            success
+ *     < 0           invalid argument (see sa_status_string)
+ *     > 0           a hipError_t from the launch
+ * Device pointers must stay valid until the stream reaches the launched work.
+ *
+ * Squareplus family: y = squareplus(alpha * (x - theta))^power,
+ *   squareplus(a) = (a + sqrt(a^2 + 4)) / 2,  power in {1, 2, 3}.
+ * Fused attention and decode use the default family (alpha=2, theta=0.5, p=2),
+ * as the reference's fused kernels do.
+ *
+ * Citations are path:line into the reference (NoSelection/smooth-attn).
+ */
+#ifndef SMOOTH_ATTN_AMD_H
+#define SMOOTH_ATTN_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* sa_stream_t; /* == hipStream_t */
+
+/* Element types (also used for the fp8 storage type). */
+enum {
+    SA_F32 = 0,
+    SA_F16 = 1,
+    SA_BF16 = 2,
+    SA_FP8_E4M3FN = 3
+};
+
+/* Status codes < 0. */
+enum {
+    SA_ERR_NULL_POINTER = -1,
+    SA_ERR_BAD_SHAPE = -2,
+    SA_ERR_BAD_DTYPE = -3,
+    SA_ERR_BAD_FAMILY = -4,
+    SA_ERR_BAD_STRIDE = -5,
+    SA_ERR_UNSUPPORTED = -6,
+    SA_ERR_WORKSPACE = -7
+};
+
+/* Human-readable text for a status code (static storage). */
+const char* sa_status_string(int status);
+
+/*
+ * Row-wise or causal squareplus normalisation forward over the rows of a 2-D
+ * view x[n_rows, n_cols] (element row strides; columns contiguous).
+ *   causal == 0: y_ij = w_ij / (sum_j w_ij + 1e-12)
+ *   causal != 0: row r attends to columns j <= (r mod n_cols); the rest of the
+ *                row is written as exact zeros.
+ * dtype: SA_F32 / SA_F16 / SA_BF16 for both x and y; fp32 arithmetic.
+ * n_cols <= 8192.
+ * Replaces the launches of _softplus_norm_fwd (kernels.py:494-531, launched
+ * by _launch_row_kernel_out :887-939), _softplus_norm_causal_fwd (:565-604),
+ * _winner_squareplus_p2_causal_fwd (:607-637) and the tiered path
+ * (:640-676, :1042-1094), reached from softplus_norm_triton_out (:1006-1031)
+ * and softplus_norm_causal_triton_out (:1274-1297).
+ */
+int sa_norm_fwd(const void* x, void* y, int64_t n_rows, int64_t n_cols,
+                int64_t x_row_stride, int64_t y_row_stride, int dtype,
+                int causal, float alpha, float theta, int power,
+                sa_stream_t stream);
+
+/*
+ * Fused backward of sa_norm_fwd:
+ *   dx_j = dw_j/dx_j / S * (dy_j - sum_k dy_k P_k),  S = sum w + 1e-12, P = w/S
+ * recomputing w from x.  Causal rows write exact zeros above the diagonal.
+ * x_dtype is the dtype of x and dx; dy_dtype may be SA_F32 or x_dtype.
+ * Replaces _softplus_norm_causal_backward (kernels.py:1197-1230) with its
+ * kernels _softplus_norm_causal_bwd (:679-743),
+ * _winner_squareplus_p2_causal_bwd (:746-794) and the tiered backward
+ * (:797-849, :1097-1121); the row-wise case replaces autograd of
+ * softplus_norm_eager (:1332-1346), for which the reference has no kernel.
+ */
+int sa_norm_bwd(const void* x, const void* dy, void* dx, int64_t n_rows,
+                int64_t n_cols, int64_t x_row_stride, int64_t dy_row_stride,
+                int64_t dx_row_stride, int x_dtype, int dy_dtype, int causal,
+                float alpha, float theta, int power, sa_stream_t stream);
+
+/*
+ * Fused causal squareplus attention forward (bf16 or fp16 q/k/v/o):
+ *   O_i = sum_{j<=i, i-j<W} y_ij V_j / (sum_j y_ij + 1e-12),
+ *   y = squareplus(2 s - 1)^2,  s = scale * q_i . k_j
+ * q,o: [B, Hq, T, D]; k,v: [B, Hkv, T, D]; Hq % Hkv == 0 (query head h reads
+ * KV head h / (Hq/Hkv)).  *_strides are element strides for (b, h, t, d) and
+ * the d stride must be 1.  row_sums (nullable): fp32 [B, Hq, T] contiguous,
+ * receives sum_j y_ij + 1e-12.  window_size 0 = full causal.  D in {32, 64,
+ * 128}.  exact_math != 0 selects a correctly rounded sqrt.
+ * Replaces _sp2norm_flash_fwd (kernels.py:1912-1931) and its kernel
+ * _sp2norm_flash_fwd_with_rowsum_kernel (:1536-1631).
+ */
+int sa_flash_fwd(const void* q, const void* k, const void* v, void* o,
+                 float* row_sums, int B, int Hq, int Hkv, int T, int D,
+                 const int64_t* q_strides, const int64_t* k_strides,
+                 const int64_t* v_strides, const int64_t* o_strides,
+                 float scale, int window_size, int exact_math, int dtype,
+                 sa_stream_t stream);
+
+/*
+ * Fused attention backward: dq, dk, dv of sa_flash_fwd given o, do and the
+ * forward's row_sums.  Same layouts and constraints as sa_flash_fwd; dq has
+ * q's strides argument dq_strides, dk/dv have KV shape.  delta_ws: fp32
+ * workspace of B*Hq*T floats (receives rowsum(do * o)).
+ * Replaces _sp2norm_flash_bwd (kernels.py:1934-1989) with its kernels
+ * _sp2norm_flash_bwd_dq_kernel (:1667-1784) and
+ * _sp2norm_flash_bwd_dkv_kernel (:1787-1909).
+ */
+int sa_flash_bwd(const void* q, const void* k, const void* v, const void* o,
+                 const void* dout, const float* row_sums, void* dq, void* dk,
+                 void* dv, float* delta_ws, int B, int Hq, int Hkv, int T,
+                 int D, const int64_t* q_strides, const int64_t* k_strides,
+                 const int64_t* v_strides, const int64_t* o_strides,
+                 const int64_t* do_strides, const int64_t* dq_strides,
+                 const int64_t* dk_strides, const int64_t* dv_strides,
+                 float scale, int window_size, int exact_math, int dtype,
+                 sa_stream_t stream);
+
+/*
+ * Per-tensor absmax quantisation to float8_e4m3fn, entirely on the device:
+ *   scale = max(amax|x| / 448, 1e-12);  x8 = e4m3fn(clamp(x / scale, +-448))
+ * x: n contiguous elements of dtype (SA_F32/SA_F16/SA_BF16); x8: n bytes.
+ * amax_ws: one fp32 of workspace; scale_out: one fp32 (device) receiving
+ * the scale.  No host synchronisation.
+ * Replaces _quantize_to_fp8 (kernels.py:2592-2601), which syncs via .item().
+ */
+int sa_fp8_quantize(const void* x, void* x8, int64_t n, int dtype,
+                    float* amax_ws, float* scale_out, sa_stream_t stream);
+
+/*
+ * fp8 fused causal attention forward.  q8, k8: float8_e4m3fn; v: e4m3fn
+ * (v_dtype SA_FP8_E4M3FN, as the reference entry point quantises V) or bf16
+ * (v_dtype SA_BF16).  Scales are device pointers to one fp32 each (v_scale
+ * ignored, may be NULL, for bf16 v).  Scores = (q8 . k8) * q_s * k_s *
+ * attn_scale on fp8 MFMA; y rounded to bf16 and multiplied with v (as bf16)
+ * on bf16 MFMA, times v_s.  o: bf16 [B, Hq, T, D]; row_sums nullable.
+ * Layout rules as sa_flash_fwd.
+ * Replaces _sp2norm_fp8_flash_fwd (kernels.py:2604-2627) and its kernel
+ * _sp2norm_fp8_flash_fwd_kernel (:2498-2589).
+ */
+int sa_flash_fp8_fwd(const void* q8, const void* k8, const void* v, void* o,
+                     float* row_sums, const float* q_scale,
+                     const float* k_scale, const float* v_scale, int B,
+                     int Hq, int Hkv, int T, int D, const int64_t* q_strides,
+                     const int64_t* k_strides, const int64_t* v_strides,
+                     const int64_t* o_strides, float attn_scale,
+                     int window_size, int v_dtype, sa_stream_t stream);
+
+/*
+ * Bytes of fp32 workspace sa_paged_decode needs for these sizes.
+ */
+int64_t sa_paged_decode_workspace_size(int B, int Hq, int D, int max_pages,
+                                       int page_size);
+
+/*
+ * Paged single-token decode through a block table.
+ *   q: [B, Hq, 1, D] (strides q_strides, d stride 1)
+ *   k_cache, v_cache: [n_pages, Hkv, page_size, D] (strides kv_strides /
+ *     vv_strides, d stride 1)
+ *   block_table: int32 [B, max_pages] (row stride bt_stride, unit col stride)
+ *   context_lens: int32 [B], each in [0, max_pages * page_size]
+ *   out: bf16 [B, Hq, D] (strides o_strides)
+ * out[b,h] = sum_{t<ctx_b} y_t V_t / (sum_t y_t + 1e-12) with
+ * K_t = k_cache[block_table[b, t/P], h/(Hq/Hkv), t%P].  dtype (q and cache):
+ * SA_BF16 or SA_F16.  D in {32, 64, 128}; page_size in {8,16,32,64}.
+ * workspace: fp32, at least sa_paged_decode_workspace_size() bytes.
+ * Replaces sp2norm_paged_attention (kernels.py:2776-2829) and its kernel
+ * _sp2norm_paged_attention_kernel (:2681-2773).
+ */
+int sa_paged_decode(const void* q, const void* k_cache, const void* v_cache,
+                    void* out, const int32_t* block_table,
+                    const int32_t* context_lens, int B, int Hq, int Hkv,
+                    int D, int page_size, int max_pages,
+                    const int64_t* q_strides, const int64_t* kv_strides,
+                    const int64_t* vv_strides, const int64_t* o_strides,
+                    int64_t bt_stride, float scale, int dtype,
+                    float* workspace, int64_t workspace_bytes,
+                    sa_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SMOOTH_ATTN_AMD_H */

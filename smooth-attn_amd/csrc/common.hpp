@@ -1,0 +1,126 @@
+// Shared device helpers for the gfx950 smooth-attn kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "smooth_attn_amd.h"
+
+namespace sa {
+
+using bf16 = __bf16;
+using f16 = _Float16;
+
+// Epsilon added to every row sum (reference kernels.py:57, :529, :1584).
+constexpr float kEps = 1e-12f;
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(f16 x) { return static_cast<float>(x); }
+__device__ __forceinline__ float to_f32(bf16 x) { return static_cast<float>(x); }
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float x) { return static_cast<T>(x); }
+
+// v_sqrt_f32.  Every argument on this path is a^2 + 4 >= 4, so the denormal
+// pre-scaling of the correctly rounded sqrtf sequence is never needed.
+__device__ __forceinline__ float fast_sqrt(float x) { return __builtin_amdgcn_sqrtf(x); }
+__device__ __forceinline__ float fast_rsqrt(float x) { return __builtin_amdgcn_rsqf(x); }
+
+// Lane-to-lane moves inside a 16-lane DPP row.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+// Sum over the 64 lanes of a wavefront; every lane receives the total.
+// quad_perm xor1 / xor2, then half-row and row mirrors give each 16-lane row
+// its own sum in all of its lanes; the four row sums are combined with
+// v_readlane in a fixed order, so the result is deterministic.
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_mov<0x141>(v);  // row_half_mirror
+    v += dpp_mov<0x140>(v);  // row_mirror
+    const int b = __float_as_int(v);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(b, 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(b, 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(b, 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(b, 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
+// 16-byte vector type used for coalesced global traffic.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+__device__ __forceinline__ u32x4 load16(const T* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+template <typename T>
+__device__ __forceinline__ void store16(T* p, u32x4 v) {
+    __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+}
+
+// Element i of a row fragment held as 32-bit words (16-bit types pack two
+// elements per word, low half first).
+template <typename T>
+__device__ __forceinline__ float elem(const uint32_t* words, int i);
+
+template <>
+__device__ __forceinline__ float elem<float>(const uint32_t* words, int i) {
+    return __uint_as_float(words[i]);
+}
+template <>
+__device__ __forceinline__ float elem<bf16>(const uint32_t* words, int i) {
+    const uint32_t w = words[i >> 1];
+    return __uint_as_float((i & 1) ? (w & 0xFFFF0000u) : (w << 16));
+}
+template <>
+__device__ __forceinline__ float elem<f16>(const uint32_t* words, int i) {
+    const uint32_t w = words[i >> 1];
+    const uint16_t h = (i & 1) ? static_cast<uint16_t>(w >> 16) : static_cast<uint16_t>(w & 0xFFFFu);
+    return static_cast<float>(__builtin_bit_cast(f16, h));
+}
+
+// Two floats packed into one 32-bit word of a 16-bit type (RNE), or one float.
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<T>(lo))) |
+           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<T>(hi))) << 16);
+}
+
+// Load 16 bytes into words[0..3] / store words[0..3] as 16 bytes.
+template <typename T>
+__device__ __forceinline__ void load_words(const T* p, uint32_t* words) {
+    const u32x4 v = load16(p);
+    words[0] = v.x;
+    words[1] = v.y;
+    words[2] = v.z;
+    words[3] = v.w;
+}
+template <typename T>
+__device__ __forceinline__ void store_words(T* p, const uint32_t* words) {
+    store16(p, u32x4{words[0], words[1], words[2], words[3]});
+}
+
+// Pack VEC = 16 / sizeof(T) floats into 4 words of T.
+template <typename T>
+__device__ __forceinline__ void pack_row16(const float* in, uint32_t* words) {
+    if constexpr (sizeof(T) == 4) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) words[i] = __float_as_uint(in[i]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) words[i] = pack2<T>(in[2 * i], in[2 * i + 1]);
+    }
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline int status_from_launch() {
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : static_cast<int>(e);
+}
+
+}  // namespace sa

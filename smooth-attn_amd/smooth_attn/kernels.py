@@ -1,0 +1,667 @@
+"""Public API of smooth-attn on MI355X: same names, signatures, argument
+meaning and error behaviour as the reference's ``src/smooth_attn/kernels.py``,
+backed by hand-written gfx950 HIP kernels through the C ABI
+(include/smooth_attn_amd.h).  There is no Triton and no fallback path: if the
+HIP library is missing every GPU entry point raises ``RuntimeError``.
+
+Citations are ``path:line`` into the reference.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+
+# kernels.py:24-29
+SUPPORTED_POWERS = (1, 2, 3)
+SUPPORTED_DTYPES = {
+    "fp32": torch.float32,
+    "fp16": torch.float16,
+    "bf16": torch.bfloat16,
+}
+# kernels.py:57
+EPS = 1e-12
+# Longest row the fused normalisation kernels take (the reference stops at
+# 4096, kernels.py:236-240; the gfx950 kernels hold up to 8192 in registers).
+MAX_ROW_COLS = 8192
+
+_DTYPE_CODE = {torch.float32: _lib.SA_F32, torch.float16: _lib.SA_F16, torch.bfloat16: _lib.SA_BF16}
+
+
+@dataclass(frozen=True)
+class FamilyConfig:
+    """squareplus(alpha * (x - theta))^power / sum — kernels.py:65-89."""
+
+    alpha: float = 2.0
+    theta: float = 0.5
+    power: int = 2
+
+    def __post_init__(self):
+        if self.power not in SUPPORTED_POWERS:
+            raise ValueError(f"power must be one of {SUPPORTED_POWERS}, got {self.power}")
+
+    @property
+    def cache_key(self):
+        return (float(self.alpha), float(self.theta), int(self.power))
+
+    @property
+    def kernel_kwargs(self):
+        return {"ALPHA": float(self.alpha), "THETA": float(self.theta), "POWER": int(self.power)}
+
+    @property
+    def label(self):
+        return f"squareplus({self.alpha:g} * (x - {self.theta:g}))^{self.power} / sum"
+
+
+@dataclass(frozen=True)
+class RowwiseBenchmarkResult:
+    """kernels.py:92-97."""
+
+    shape: tuple
+    torch_softmax_us: float
+    triton_softmax_us: float
+    family_us: float
+
+
+@dataclass(frozen=True)
+class CausalBenchmarkResult:
+    """kernels.py:100-114."""
+
+    dtype: torch.dtype
+    batch: int
+    heads: int
+    seq_len: int
+    torch_softmax_us: float
+    triton_softmax_us: float
+    family_us: float
+    softmax_err: float
+    family_err: float
+    softmax_sums_ok: bool
+    family_sums_ok: bool
+    softmax_meta: dict
+    family_meta: dict
+
+
+DEFAULT_FAMILY = FamilyConfig()
+BENCH_ALPHA = DEFAULT_FAMILY.alpha
+BENCH_THETA = DEFAULT_FAMILY.theta
+BENCH_POWER = DEFAULT_FAMILY.power
+
+
+# ---------------------------------------------------------------------------
+# Validation (kernels.py:167-240), same messages and exception types.
+# ---------------------------------------------------------------------------
+def _resolve_family(alpha, theta, power, family):
+    if family is None:
+        return FamilyConfig(alpha=alpha, theta=theta, power=power)
+    if (alpha, theta, power) != (DEFAULT_FAMILY.alpha, DEFAULT_FAMILY.theta, DEFAULT_FAMILY.power):
+        raise ValueError("pass either family=... or alpha/theta/power overrides, not both")
+    return family
+
+
+def _validate_cuda_tensor(x, *, name):
+    if not isinstance(x, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if not x.is_cuda:
+        raise ValueError(f"{name} must be a CUDA tensor")
+    if x.dtype not in SUPPORTED_DTYPES.values():
+        raise ValueError(f"{name} dtype must be one of {tuple(SUPPORTED_DTYPES.values())}, got {x.dtype}")
+
+
+def _prepare_rowwise_input(x):
+    _validate_cuda_tensor(x, name="x")
+    if x.ndim != 2:
+        raise ValueError(f"row-wise kernels expect a 2D tensor, got shape {tuple(x.shape)}")
+    return x if x.is_contiguous() else x.contiguous()
+
+
+def _prepare_attention_input(x):
+    _validate_cuda_tensor(x, name="x")
+    if x.ndim < 2:
+        raise ValueError("attention scores must have at least 2 dimensions")
+    if x.shape[-1] != x.shape[-2]:
+        raise ValueError("causal attention expects square score matrices on the last two dims")
+    return x if x.is_contiguous() else x.contiguous()
+
+
+def _prepare_output(out, reference):
+    _validate_cuda_tensor(out, name="out")
+    if out.shape != reference.shape:
+        raise ValueError(f"out shape {tuple(out.shape)} must match input shape {tuple(reference.shape)}")
+    if out.dtype != reference.dtype:
+        raise ValueError(f"out dtype {out.dtype} must match input dtype {reference.dtype}")
+    if out.device != reference.device:
+        raise ValueError("out and input must live on the same CUDA device")
+    if out.is_contiguous():
+        return out, None
+    return torch.empty_like(reference), out
+
+
+def _finalize_output(kernel_out, user_out):
+    if user_out is None:
+        return kernel_out
+    user_out.copy_(kernel_out)
+    return user_out
+
+
+def _check_row_length(n_cols):
+    if n_cols > MAX_ROW_COLS:
+        raise ValueError(f"n_cols={n_cols} is too large for this fused row kernel")
+
+
+def _stream(t):
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _is_winner_family(family):
+    return family.cache_key == DEFAULT_FAMILY.cache_key
+
+
+def _row_launch_meta(variant, n_rows, n_cols, dtype):
+    vec = 16 // torch.empty((), dtype=dtype).element_size()
+    chunks = 1
+    while chunks * 64 * vec < n_cols:
+        chunks *= 2
+    return {
+        "variant": variant,
+        "block_size": chunks * 64 * vec,
+        "num_warps": 4,
+        "num_stages": 1,
+        "num_programs": (n_rows + 3) // 4,
+        "rows_per_wave": 1,
+        "occupancy": None,
+        "n_regs": None,
+        "shared_mem": 0,
+        "time_us": None,
+    }
+
+
+# ---------------------------------------------------------------------------
+# Row-wise and causal normalisation (forward and fused backward).
+# ---------------------------------------------------------------------------
+def _norm_fwd_2d(x2d, out2d, family, causal):
+    n_rows, n_cols = x2d.shape
+    _check_row_length(n_cols)
+    lib = _lib.load()
+    with torch.cuda.device(x2d.device):
+        st = lib.sa_norm_fwd(
+            x2d.data_ptr(), out2d.data_ptr(), n_rows, n_cols, x2d.stride(0), out2d.stride(0),
+            _DTYPE_CODE[x2d.dtype], 1 if causal else 0, float(family.alpha), float(family.theta),
+            int(family.power), _stream(x2d),
+        )
+    _lib.check(st, "sa_norm_fwd")
+
+
+def _norm_bwd_2d(x2d, g2d, dx2d, family, causal):
+    n_rows, n_cols = x2d.shape
+    _check_row_length(n_cols)
+    lib = _lib.load()
+    with torch.cuda.device(x2d.device):
+        st = lib.sa_norm_bwd(
+            x2d.data_ptr(), g2d.data_ptr(), dx2d.data_ptr(), n_rows, n_cols, x2d.stride(0),
+            g2d.stride(0), dx2d.stride(0), _DTYPE_CODE[x2d.dtype], _DTYPE_CODE[g2d.dtype],
+            1 if causal else 0, float(family.alpha), float(family.theta), int(family.power), _stream(x2d),
+        )
+    _lib.check(st, "sa_norm_bwd")
+
+
+def softplus_norm_triton(x, alpha=DEFAULT_FAMILY.alpha, theta=DEFAULT_FAMILY.theta,
+                         power=DEFAULT_FAMILY.power, *, family=None, return_meta=False):
+    """Row-wise forward into a new tensor — kernels.py:985-1003."""
+    family = _resolve_family(alpha, theta, power, family)
+    x_row = _prepare_rowwise_input(x)
+    out = torch.empty_like(x_row)
+    _norm_fwd_2d(x_row, out, family, causal=False)
+    if return_meta:
+        return out, _row_launch_meta("softplus_norm", *x_row.shape, x_row.dtype)
+    return out
+
+
+def softplus_norm_triton_out(out, x, alpha=DEFAULT_FAMILY.alpha, theta=DEFAULT_FAMILY.theta,
+                             power=DEFAULT_FAMILY.power, *, family=None, return_meta=False):
+    """Row-wise forward into ``out`` — kernels.py:1006-1031."""
+    family = _resolve_family(alpha, theta, power, family)
+    x_row = _prepare_rowwise_input(x)
+    kernel_out, user_out = _prepare_output(out, x_row)
+    _norm_fwd_2d(x_row, kernel_out, family, causal=False)
+    result = _finalize_output(kernel_out, user_out)
+    if return_meta:
+        return result, _row_launch_meta("softplus_norm", *x_row.shape, x_row.dtype)
+    return result
+
+
+def sp2norm_triton(x, return_meta=False):
+    """kernels.py:1034-1035."""
+    return softplus_norm_triton(x, family=DEFAULT_FAMILY, return_meta=return_meta)
+
+
+def softplus_norm_causal_triton_out(out, x, alpha=DEFAULT_FAMILY.alpha, theta=DEFAULT_FAMILY.theta,
+                                    power=DEFAULT_FAMILY.power, *, family=None, return_meta=False):
+    """Causal forward into ``out`` — kernels.py:1274-1297.
+
+    One kernel for every family and length: the reference's tiered launches
+    and full-matrix ``zero_()`` (kernels.py:1042-1094) are subsumed by causal
+    chunk skipping and in-kernel zero fill.
+    """
+    family = _resolve_family(alpha, theta, power, family)
+    x_attn = _prepare_attention_input(x)
+    kernel_out, user_out = _prepare_output(out, x_attn)
+    seq_len = x_attn.shape[-1]
+    x2d = x_attn.view(-1, seq_len)
+    o2d = kernel_out.view(-1, seq_len)
+    _norm_fwd_2d(x2d, o2d, family, causal=True)
+    result = _finalize_output(kernel_out, user_out)
+    if return_meta:
+        variant = "squareplus_winner" if _is_winner_family(family) else "softplus_norm_causal"
+        return result, _row_launch_meta(variant, x2d.shape[0], seq_len, x2d.dtype)
+    return result
+
+
+def softplus_norm_causal_triton(x, alpha=DEFAULT_FAMILY.alpha, theta=DEFAULT_FAMILY.theta,
+                                power=DEFAULT_FAMILY.power, *, family=None, return_meta=False):
+    """Causal forward into a new tensor — kernels.py:1254-1271."""
+    family = _resolve_family(alpha, theta, power, family)
+    x_attn = _prepare_attention_input(x)
+    out = torch.empty_like(x_attn)
+    return softplus_norm_causal_triton_out(out, x_attn, family=family, return_meta=return_meta)
+
+
+def _softplus_norm_causal_backward(x, grad_output, family):
+    """Fused causal backward — replaces kernels.py:1197-1230 (dx has x's dtype).
+
+    dy may be fp32 or x's dtype; the kernel reads it directly (no upcast pass).
+    """
+    seq_len = x.shape[-1]
+    x2d = x.reshape(-1, seq_len)
+    g = grad_output
+    if g.dtype not in (torch.float32, x.dtype):
+        g = g.float()
+    g2d = g.reshape(-1, seq_len)
+    if not g2d.is_contiguous():
+        g2d = g2d.contiguous()
+    dx = torch.empty_like(x2d)
+    _norm_bwd_2d(x2d, g2d, dx, family, causal=True)
+    return dx.view_as(x)
+
+
+def _softplus_norm_backward(x, grad_output, family):
+    """Fused row-wise backward (the reference has only eager autograd, :1332-1346)."""
+    g = grad_output if grad_output.dtype in (torch.float32, x.dtype) else grad_output.float()
+    g = g.contiguous()
+    dx = torch.empty_like(x)
+    _norm_bwd_2d(x, g, dx, family, causal=False)
+    return dx
+
+
+class _SoftplusNormCausalAutogradFn(torch.autograd.Function):
+    """kernels.py:1373-1398."""
+
+    @staticmethod
+    def forward(ctx, x, alpha, theta, power):
+        family = FamilyConfig(alpha=float(alpha), theta=float(theta), power=int(power))
+        x_attn = _prepare_attention_input(x)
+        out = torch.empty_like(x_attn)
+        result = softplus_norm_causal_triton_out(out, x_attn, family=family)
+        ctx.family = family
+        ctx.save_for_backward(x_attn)
+        return result
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        if not ctx.needs_input_grad[0]:
+            return None, None, None, None
+        (saved_x,) = ctx.saved_tensors
+        grad_x = _softplus_norm_causal_backward(saved_x, grad_output.contiguous(), ctx.family)
+        return grad_x, None, None, None
+
+
+def softplus_norm_causal(x, alpha=DEFAULT_FAMILY.alpha, theta=DEFAULT_FAMILY.theta,
+                         power=DEFAULT_FAMILY.power, *, family=None, implementation="triton"):
+    """kernels.py:1401-1420.  ``implementation="triton"`` selects the HIP kernels
+    (the name is kept for drop-in compatibility); ``"eager"`` is the reference's
+    eager formula in fp32, cast back to x's dtype."""
+    family = _resolve_family(alpha, theta, power, family)
+    if implementation == "triton":
+        return _SoftplusNormCausalAutogradFn.apply(x, family.alpha, family.theta, family.power)
+    if implementation == "eager":
+        return softplus_norm_causal_eager(x.float(), family=family).to(x.dtype)
+    raise ValueError("implementation must be 'triton' or 'eager'")
+
+
+class SoftplusNormCausal(torch.nn.Module):
+    """kernels.py:1423-1442."""
+
+    def __init__(self, alpha=DEFAULT_FAMILY.alpha, theta=DEFAULT_FAMILY.theta, power=DEFAULT_FAMILY.power,
+                 *, family=None, implementation="triton"):
+        super().__init__()
+        self.family = _resolve_family(alpha, theta, power, family)
+        self.implementation = implementation
+
+    def forward(self, x):
+        return softplus_norm_causal(x, family=self.family, implementation=self.implementation)
+
+
+# ---------------------------------------------------------------------------
+# Eager formulas (public API of the reference, kernels.py:1328-1370).  These
+# are plain torch expressions on whatever device the input lives on; they are
+# part of the API surface, not the measured path.
+# ---------------------------------------------------------------------------
+def _causal_mask(seq_len, device):
+    return torch.triu(torch.ones(seq_len, seq_len, device=device, dtype=torch.bool), diagonal=1)
+
+
+def _apply_family_activation_eager(arg):
+    return 0.5 * (arg + torch.sqrt(arg * arg + 4.0))
+
+
+def softplus_norm_eager(x, alpha=DEFAULT_FAMILY.alpha, theta=DEFAULT_FAMILY.theta,
+                        power=DEFAULT_FAMILY.power, *, family=None):
+    family = _resolve_family(alpha, theta, power, family)
+    y = _apply_family_activation_eager(family.alpha * (x - family.theta))
+    if family.power == 2:
+        y = y * y
+    elif family.power == 3:
+        y = y * y * y
+    return y / (y.sum(dim=-1, keepdim=True) + EPS)
+
+
+def softplus_norm_causal_eager(x, alpha=DEFAULT_FAMILY.alpha, theta=DEFAULT_FAMILY.theta,
+                               power=DEFAULT_FAMILY.power, *, family=None):
+    family = _resolve_family(alpha, theta, power, family)
+    mask = _causal_mask(x.shape[-1], x.device)
+    y = _apply_family_activation_eager(family.alpha * (x - family.theta))
+    if family.power == 2:
+        y = y * y
+    elif family.power == 3:
+        y = y * y * y
+    y = y.masked_fill(mask, 0.0)
+    return y / (y.sum(dim=-1, keepdim=True) + EPS)
+
+
+def softmax_causal_eager(x):
+    mask = _causal_mask(x.shape[-1], x.device)
+    return F.softmax(x.masked_fill(mask, float("-inf")), dim=-1)
+
+
+def sp2norm_flash_attention_eager(q, k, v, *, scale=None, window_size=0):
+    """Materialised attention — kernels.py:2053-2084."""
+    B, H_q, T, D = q.shape
+    H_kv = k.shape[1]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    if H_kv < H_q:
+        n_groups = H_q // H_kv
+        k = k.unsqueeze(2).expand(B, H_kv, n_groups, T, D).reshape(B, H_q, T, D)
+        v = v.unsqueeze(2).expand(B, H_kv, n_groups, T, D).reshape(B, H_q, T, D)
+    scores = torch.matmul(q.float(), k.float().transpose(-2, -1).contiguous()) * scale
+    arg = 2.0 * scores - 1.0
+    sp = 0.5 * (arg + torch.sqrt(arg * arg + 4.0))
+    y = sp * sp
+    y = y.masked_fill(_causal_mask(T, q.device), 0.0)
+    if window_size > 0:
+        positions = torch.arange(T, device=q.device)
+        window_mask = (positions[:, None] - positions[None, :]) >= window_size
+        y = y.masked_fill(window_mask.unsqueeze(0).unsqueeze(0), 0.0)
+    attn = y / (y.sum(dim=-1, keepdim=True) + EPS)
+    return torch.matmul(attn, v.float()).to(q.dtype)
+
+
+# ---------------------------------------------------------------------------
+# Fused attention (bf16 / fp16 MFMA).
+# ---------------------------------------------------------------------------
+_FLASH_HEAD_DIMS = (32, 64, 128)
+
+
+def _flash_operand(t):
+    """Unit stride along D is all the kernels need; anything else is copied."""
+    return t if t.stride(-1) == 1 else t.contiguous()
+
+
+def _sp2norm_flash_fwd(q, k, v, scale, n_kv_groups=1, window_size=0, use_fast_sqrt=True):
+    """(o, row_sums) of the fused forward — replaces kernels.py:1912-1931."""
+    B, H_q, T, D = q.shape
+    H_kv = k.shape[1]
+    if q.dtype not in (torch.bfloat16, torch.float16) or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError(f"fused attention expects bf16 or fp16 q/k/v of one dtype, got "
+                         f"{q.dtype}/{k.dtype}/{v.dtype}")
+    if D not in _FLASH_HEAD_DIMS:
+        raise ValueError(f"fused attention supports head dims {_FLASH_HEAD_DIMS}, got {D}")
+    if H_kv * n_kv_groups != H_q:
+        raise ValueError("n_kv_groups must equal H_q // H_kv")
+    q, k, v = _flash_operand(q), _flash_operand(k), _flash_operand(v)
+    o = torch.empty_like(q)
+    if o.stride(-1) != 1:
+        o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    row_sums = torch.empty(B, H_q, T, device=q.device, dtype=torch.float32)
+    lib = _lib.load()
+    with torch.cuda.device(q.device):
+        st = lib.sa_flash_fwd(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), row_sums.data_ptr(),
+            B, H_q, H_kv, T, D, _lib.strides(q), _lib.strides(k), _lib.strides(v), _lib.strides(o),
+            float(scale), int(window_size), 0 if use_fast_sqrt else 1, _DTYPE_CODE[q.dtype], _stream(q),
+        )
+    _lib.check(st, "sa_flash_fwd")
+    return o, row_sums
+
+
+def _sp2norm_flash_bwd(q, k, v, o, do, row_sums, scale, n_kv_groups=1, window_size=0, use_fast_sqrt=True):
+    """(dq, dk, dv) of the fused attention — replaces kernels.py:1934-1989."""
+    B, H_q, T, D = q.shape
+    H_kv = k.shape[1]
+    q, k, v, o = _flash_operand(q), _flash_operand(k), _flash_operand(v), _flash_operand(o)
+    do = do if (do.dtype == q.dtype and do.stride(-1) == 1) else do.to(q.dtype).contiguous()
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    delta = torch.empty(B, H_q, T, device=q.device, dtype=torch.float32)
+    rs = row_sums.contiguous()
+    lib = _lib.load()
+    with torch.cuda.device(q.device):
+        st = lib.sa_flash_bwd(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(), rs.data_ptr(),
+            dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr(), B, H_q, H_kv, T, D,
+            _lib.strides(q), _lib.strides(k), _lib.strides(v), _lib.strides(o), _lib.strides(do),
+            _lib.strides(dq), _lib.strides(dk), _lib.strides(dv), float(scale), int(window_size),
+            0 if use_fast_sqrt else 1, _DTYPE_CODE[q.dtype], _stream(q),
+        )
+    _lib.check(st, "sa_flash_bwd")
+    return dq, dk, dv
+
+
+class _SP2NormFlashAttentionFn(torch.autograd.Function):
+    """kernels.py:1992-2013."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, scale, n_kv_groups, window_size, use_fast_sqrt):
+        o, row_sums = _sp2norm_flash_fwd(q, k, v, scale, n_kv_groups, window_size, use_fast_sqrt=use_fast_sqrt)
+        ctx.save_for_backward(q, k, v, o, row_sums)
+        ctx.scale = scale
+        ctx.n_kv_groups = n_kv_groups
+        ctx.window_size = window_size
+        ctx.use_fast_sqrt = use_fast_sqrt
+        return o
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        q, k, v, o, row_sums = ctx.saved_tensors
+        dq, dk, dv = _sp2norm_flash_bwd(q, k, v, o, grad_output, row_sums, ctx.scale, ctx.n_kv_groups,
+                                        ctx.window_size, use_fast_sqrt=ctx.use_fast_sqrt)
+        return dq, dk, dv, None, None, None, None
+
+
+def sp2norm_flash_attention(q, k, v, *, scale=None, window_size=0, exact_math=False):
+    """Fused causal squareplus attention with autograd, GQA and sliding
+    windows — kernels.py:2016-2050."""
+    assert q.ndim == 4 and k.ndim == 4 and v.ndim == 4
+    B, H_q, T, D = q.shape
+    H_kv = k.shape[1]
+    assert k.shape == (B, H_kv, T, D) and v.shape == (B, H_kv, T, D)
+    assert H_q % H_kv == 0, f"H_q ({H_q}) must be divisible by H_kv ({H_kv})"
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    n_kv_groups = H_q // H_kv
+    return _SP2NormFlashAttentionFn.apply(q, k, v, scale, n_kv_groups, window_size, not exact_math)
+
+
+# ---------------------------------------------------------------------------
+# fp8 fused attention.
+# ---------------------------------------------------------------------------
+FP8_MAX = 448.0
+
+
+def _quantize_to_fp8_device(x):
+    """(x8, scale) with the scale left on the device (no host sync)."""
+    if x.dtype not in _DTYPE_CODE:
+        raise ValueError(f"cannot quantise dtype {x.dtype}")
+    xc = x.detach().contiguous()
+    x8 = torch.empty(xc.shape, dtype=torch.float8_e4m3fn, device=x.device)
+    ws = torch.empty(2, dtype=torch.float32, device=x.device)
+    lib = _lib.load()
+    with torch.cuda.device(x.device):
+        st = lib.sa_fp8_quantize(xc.data_ptr(), x8.data_ptr(), xc.numel(), _DTYPE_CODE[xc.dtype],
+                                 ws.data_ptr(), ws.data_ptr() + 4, _stream(xc))
+    _lib.check(st, "sa_fp8_quantize")
+    return x8, ws[1]
+
+
+def _quantize_to_fp8(x):
+    """kernels.py:2592-2601: returns (x_fp8, python float scale)."""
+    x8, scale = _quantize_to_fp8_device(x)
+    return x8, scale.item()
+
+
+def _scale_tensor(s, device):
+    if isinstance(s, torch.Tensor):
+        return s.reshape(1).to(device=device, dtype=torch.float32)
+    return torch.tensor([float(s)], dtype=torch.float32, device=device)
+
+
+def _sp2norm_fp8_flash_fwd(q_fp8, k_fp8, v_fp8, q_scale, k_scale, v_scale, attn_scale, n_kv_groups=1,
+                           window_size=0):
+    """(o, row_sums) of the fp8 forward — replaces kernels.py:2604-2627.
+
+    Scales may be Python floats or device scalars.  ``v_fp8`` may also be a
+    bf16 tensor, in which case ``v_scale`` is ignored (PV on bf16 V).
+    """
+    B, H_q, T, D = q_fp8.shape
+    H_kv = k_fp8.shape[1]
+    if D not in _FLASH_HEAD_DIMS:
+        raise ValueError(f"fused attention supports head dims {_FLASH_HEAD_DIMS}, got {D}")
+    if q_fp8.dtype != torch.float8_e4m3fn or k_fp8.dtype != torch.float8_e4m3fn:
+        raise ValueError("q and k must be float8_e4m3fn")
+    if v_fp8.dtype == torch.float8_e4m3fn:
+        v_code = _lib.SA_FP8_E4M3FN
+    elif v_fp8.dtype == torch.bfloat16:
+        v_code = _lib.SA_BF16
+    else:
+        raise ValueError("v must be float8_e4m3fn or bfloat16")
+    dev = q_fp8.device
+    q8, k8, v8 = _flash_operand(q_fp8), _flash_operand(k_fp8), _flash_operand(v_fp8)
+    o = torch.empty(B, H_q, T, D, device=dev, dtype=torch.bfloat16)
+    row_sums = torch.empty(B, H_q, T, device=dev, dtype=torch.float32)
+    qs, ks = _scale_tensor(q_scale, dev), _scale_tensor(k_scale, dev)
+    vs = _scale_tensor(1.0 if v_scale is None else v_scale, dev)
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        st = lib.sa_flash_fp8_fwd(
+            q8.data_ptr(), k8.data_ptr(), v8.data_ptr(), o.data_ptr(), row_sums.data_ptr(), qs.data_ptr(),
+            ks.data_ptr(), vs.data_ptr(), B, H_q, H_kv, T, D, _lib.strides(q8), _lib.strides(k8),
+            _lib.strides(v8), _lib.strides(o), float(attn_scale), int(window_size), v_code, _stream(q8),
+        )
+    _lib.check(st, "sa_flash_fp8_fwd")
+    return o, row_sums
+
+
+def sp2norm_fp8_flash_attention(q, k, v, *, scale=None, window_size=0, quantize_v=True):
+    """fp8 fused causal attention — kernels.py:2630-2673.
+
+    Q, K (and V unless ``quantize_v=False``) are quantised per tensor on the
+    device; QK^T runs on fp8 MFMA, PV on bf16 MFMA.  ``quantize_v`` (default
+    True, as in the reference entry point) is an addition: False keeps V in
+    bf16.  Returns bf16; no autograd graph (as in the reference).
+    """
+    assert q.ndim == 4 and k.ndim == 4 and v.ndim == 4
+    B, H_q, T, D = q.shape
+    H_kv = k.shape[1]
+    assert k.shape == (B, H_kv, T, D) and v.shape == (B, H_kv, T, D)
+    assert H_q % H_kv == 0, f"H_q ({H_q}) must be divisible by H_kv ({H_kv})"
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    n_kv_groups = H_q // H_kv
+    q8, q_s = _quantize_to_fp8_device(q)
+    k8, k_s = _quantize_to_fp8_device(k)
+    if quantize_v:
+        v8, v_s = _quantize_to_fp8_device(v)
+    else:
+        v8, v_s = v.detach().to(torch.bfloat16), None
+    o, _row_sums = _sp2norm_fp8_flash_fwd(q8, k8, v8, q_s, k_s, v_s, scale, n_kv_groups, window_size)
+    return o
+
+
+# ---------------------------------------------------------------------------
+# Paged decode.
+# ---------------------------------------------------------------------------
+def sp2norm_paged_attention(q, k_cache, v_cache, block_table, context_lens, *, scale=None, block_size=16):
+    """Paged single-token decode — kernels.py:2776-2829 (output bf16 [B, Hq, D])."""
+    assert q.ndim == 4 and q.shape[2] == 1, "Decode: q must be [B, H, 1, D]"
+    B, H_q, _, D = q.shape
+    H_kv = k_cache.shape[1]
+    assert H_q % H_kv == 0
+    assert k_cache.shape[2] == block_size and v_cache.shape[2] == block_size
+    max_blocks_per_seq = block_table.shape[1]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    if q.dtype not in (torch.bfloat16, torch.float16) or k_cache.dtype != q.dtype or v_cache.dtype != q.dtype:
+        raise ValueError("paged decode expects bf16 or fp16 q and caches of one dtype")
+    q = _flash_operand(q)
+    k_cache = _flash_operand(k_cache)
+    v_cache = _flash_operand(v_cache)
+    block_table = block_table.to(torch.int32)
+    if block_table.stride(-1) != 1:
+        block_table = block_table.contiguous()
+    context_lens = context_lens.to(torch.int32).contiguous()
+    out = torch.empty(B, H_q, D, device=q.device, dtype=torch.bfloat16)
+    lib = _lib.load()
+    ws_bytes = lib.sa_paged_decode_workspace_size(B, H_q, D, max_blocks_per_seq, block_size)
+    ws = torch.empty(max(1, (ws_bytes + 3) // 4), dtype=torch.float32, device=q.device)
+    with torch.cuda.device(q.device):
+        st = lib.sa_paged_decode(
+            q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(), block_table.data_ptr(),
+            context_lens.data_ptr(), B, H_q, H_kv, D, block_size, max_blocks_per_seq, _lib.strides(q),
+            _lib.strides(k_cache), _lib.strides(v_cache), _lib.strides(out), block_table.stride(0),
+            float(scale), _DTYPE_CODE[q.dtype], ws.data_ptr(), ws.numel() * 4, _stream(q),
+        )
+    _lib.check(st, "sa_paged_decode")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Timing helpers (kernels.py:322-336, :2832-2838): one event pair per
+# iteration on the current stream, median in microseconds.
+# ---------------------------------------------------------------------------
+def _median_cuda_us(fn, warmup=300, iters=1000):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
+    for i in range(iters):
+        starts[i].record()
+        fn()
+        ends[i].record()
+    torch.cuda.synchronize()
+    times = sorted(s.elapsed_time(e) * 1000.0 for s, e in zip(starts, ends))
+    return times[len(times) // 2]
+
+
+def bench(fn, x=None, warmup=300, iters=1000):
+    callback = (lambda: fn(x)) if x is not None else fn
+    return _median_cuda_us(callback, warmup=warmup, iters=iters)
+
+
+def bench_out(fn, out, x, warmup=300, iters=1000):
+    return _median_cuda_us(lambda: fn(out, x), warmup=warmup, iters=iters)

@@ -1,0 +1,39 @@
+"""The C-ABI library loads and exports every entry point the header declares —
+CPU only (no kernel launch; sa_status_string is host code)."""
+import re
+from pathlib import Path
+
+import pytest
+
+from smooth_attn import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "smooth_attn_amd.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(sa_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_entry_points():
+    names = declared_functions()
+    for n in ["sa_norm_fwd", "sa_norm_bwd", "sa_flash_fwd", "sa_flash_bwd", "sa_fp8_quantize", "sa_flash_fp8_fwd",
+              "sa_paged_decode", "sa_paged_decode_workspace_size", "sa_status_string"]:
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, f"missing exports: {missing}"
+    # the ctypes signature table covers exactly the declared functions
+    assert sorted(_lib.SIGNATURES) == declared_functions()
+
+
+def test_status_strings():
+    lib = _lib.load()
+    assert lib.sa_status_string(0) == b"success"
+    assert b"dtype" in lib.sa_status_string(-3)
+    with pytest.raises(RuntimeError, match="dtype"):
+        _lib.check(-3, "probe")

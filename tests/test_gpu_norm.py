@@ -1,0 +1,178 @@
+"""Parity of the HIP normalisation kernels with the CPU oracle (GPU).
+
+Tolerances: relative error max|HIP - oracle| /
+max|oracle| <= 1e-2 for bf16/fp16 outputs and <= 1e-5 for fp32 outputs,
+against the float64 oracle on the same seeded inputs; causal zeros exact.
+The reference's own test tolerances (tests/test_training_api.py:36-78: atol
+5e-3, rtol 5e-2 vs eager) are checked as well where they apply.
+"""
+import pytest
+import torch
+
+import smooth_attn
+from oracle import eager
+from smooth_attn import FamilyConfig, kernels
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+REL_TOL = {torch.bfloat16: 1e-2, torch.float16: 1e-2, torch.float32: 1e-5}
+FAMILIES = [FamilyConfig(), FamilyConfig(alpha=1.5, theta=0.25, power=3), FamilyConfig(alpha=0.75, theta=-0.5, power=1)]
+
+
+def _g(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def rel_err(got, ref):
+    got = got.detach().double().cpu()
+    ref = ref.detach().double().cpu()
+    return float((got - ref).abs().max() / ref.abs().max().clamp(min=1e-30))
+
+
+def _randn(shape, dtype, seed, scale=1.0):
+    return (torch.randn(shape, generator=_g(seed)) * scale).to(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("L", [1, 7, 64, 100, 512, 1024])
+@pytest.mark.parametrize("fam", FAMILIES, ids=["default", "a1.5t.25p3", "a.75t-.5p1"])
+def test_causal_forward_matches_oracle(dtype, L, fam):
+    x = _randn((2, 3, L, L), dtype, seed=L)
+    out = torch.empty(x.shape, dtype=dtype, device=DEV)
+    y, meta = smooth_attn.softplus_norm_causal_triton_out(out, x.to(DEV), family=fam, return_meta=True)
+    assert y.data_ptr() == out.data_ptr()
+    ref = eager.softplus_norm_causal_eager(x.double(), fam.alpha, fam.theta, fam.power)
+    assert rel_err(y, ref) <= REL_TOL[dtype]
+    yc = y.cpu()
+    upper = torch.triu(torch.ones(L, L, dtype=torch.bool), 1)
+    assert bool((yc[..., upper] == 0).all()), "causal zeros must be exact"
+    torch.testing.assert_close(yc.float(), ref.float(), atol=7e-3, rtol=5e-2)
+    if fam == FamilyConfig():
+        assert meta["variant"].startswith("squareplus_winner")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("L", [64, 512, 2048])
+def test_rowwise_forward_matches_oracle(dtype, L):
+    x = _randn((33, L), dtype, seed=L + 1)
+    y = smooth_attn.softplus_norm_triton(x.to(DEV))
+    ref = eager.softplus_norm_eager(x.double())
+    assert rel_err(y, ref) <= REL_TOL[dtype]
+    out = torch.empty(x.shape, dtype=dtype, device=DEV)
+    y2 = smooth_attn.softplus_norm_triton_out(out, x.to(DEV), family=FamilyConfig(power=3))
+    assert rel_err(y2, eager.softplus_norm_eager(x.double(), power=3)) <= REL_TOL[dtype]
+    y3 = smooth_attn.sp2norm_triton(x.to(DEV))
+    assert torch.equal(y3, y)
+
+
+@pytest.mark.parametrize("dtype,gdtype", [(torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float32),
+                                          (torch.float16, torch.float16), (torch.float32, torch.float32)])
+@pytest.mark.parametrize("L", [5, 32, 256, 1024])
+@pytest.mark.parametrize("fam", FAMILIES[:2], ids=["default", "a1.5t.25p3"])
+def test_causal_backward_matches_oracle(dtype, gdtype, L, fam):
+    x = _randn((2, 2, L, L), dtype, seed=3 * L)
+    dy = _randn((2, 2, L, L), gdtype, seed=3 * L + 1)
+    dx = kernels._softplus_norm_causal_backward(x.to(DEV), dy.to(DEV), fam)
+    assert dx.dtype == dtype
+    ref = eager.softplus_norm_backward(x.double(), dy.double(), fam.alpha, fam.theta, fam.power, causal=True)
+    assert rel_err(dx, ref) <= REL_TOL[dtype]
+    upper = torch.triu(torch.ones(L, L, dtype=torch.bool), 1)
+    assert bool((dx.cpu()[..., upper] == 0).all())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("L", [48, 1024])
+def test_rowwise_backward_matches_oracle(dtype, L):
+    x = _randn((40, L), dtype, seed=5 * L)
+    dy = _randn((40, L), dtype, seed=5 * L + 1)
+    dx = kernels._softplus_norm_backward(x.to(DEV), dy.to(DEV), FamilyConfig())
+    ref = eager.softplus_norm_backward(x.double(), dy.double(), causal=False)
+    assert rel_err(dx, ref) <= REL_TOL[dtype]
+
+
+def test_autograd_module_matches_reference_test():
+    # tests/test_training_api.py:63-78 with a seed
+    x = _randn((1, 2, 32, 32), torch.bfloat16, seed=11).to(DEV).requires_grad_(True)
+    upstream = torch.randn(1, 2, 32, 32, generator=_g(12)).to(DEV)
+    y = smooth_attn.SoftplusNormCausal(family=FamilyConfig())(x)
+    assert y.shape == x.shape
+    (y.float() * upstream).sum().backward()
+    xr = x.detach().cpu().double().requires_grad_(True)
+    (eager.softplus_norm_causal_eager(xr) * upstream.cpu().double()).sum().backward()
+    torch.testing.assert_close(x.grad.cpu().float(), xr.grad.float(), atol=5e-3, rtol=5e-2)
+    assert rel_err(x.grad, xr.grad) <= 1e-2
+
+
+def test_noncontiguous_out_and_input():
+    x = _randn((2, 64, 64), torch.bfloat16, seed=21).to(DEV)
+    xt = x.transpose(-1, -2)  # non-contiguous input: copied by the wrapper
+    out = torch.empty(2, 64, 64, dtype=torch.bfloat16, device=DEV).transpose(-1, -2)  # non-contiguous out
+    y = smooth_attn.softplus_norm_causal_triton_out(out, xt)
+    assert y is out
+    ref = eager.softplus_norm_causal_eager(xt.cpu().double())
+    assert rel_err(y, ref) <= 1e-2
+
+
+def test_row_stride_wider_than_row():
+    base = _randn((16, 160), torch.float32, seed=22).to(DEV)
+    x = base[:, :96]  # row stride 160, 16-byte aligned rows
+    out = torch.zeros(16, 200, device=DEV)
+    kernels._norm_fwd_2d(x, out[:, :96], FamilyConfig(), causal=False)
+    assert rel_err(out[:, :96], eager.softplus_norm_eager(x.cpu().double())) <= 1e-5
+    assert bool((out[:, 96:] == 0).all()), "columns past n_cols must not be written"
+    x2 = base[:, 1:97]  # misaligned rows -> element-wise kernel
+    kernels._norm_fwd_2d(x2, out[:, :96], FamilyConfig(), causal=True)
+    assert rel_err(out[:, :96], eager.softplus_norm_causal_eager(x2.cpu().double())) <= 1e-5
+
+
+def test_masked_scores_above_diagonal_are_ignored():
+    L = 128
+    x = _randn((1, 4, L, L), torch.bfloat16, seed=23)
+    upper = torch.triu(torch.ones(L, L, dtype=torch.bool), 1)
+    xm = x.clone()
+    xm[..., upper] = float("-inf")
+    y = smooth_attn.softplus_norm_causal_triton(xm.to(DEV))
+    assert bool(torch.isfinite(y).all())
+    assert torch.equal(y.cpu(), smooth_attn.softplus_norm_causal_triton(x.to(DEV)).cpu())
+    dy = _randn((1, 4, L, L), torch.bfloat16, seed=24)
+    dy[..., upper] = float("nan")
+    dx = kernels._softplus_norm_causal_backward(x.to(DEV), dy.to(DEV), FamilyConfig())
+    assert bool(torch.isfinite(dx).all())
+    assert bool((dx.cpu()[..., upper] == 0).all())
+
+
+def test_empty_and_limits():
+    x = torch.empty(0, 64, dtype=torch.bfloat16, device=DEV)
+    assert smooth_attn.softplus_norm_triton(x).shape == (0, 64)
+    with pytest.raises(ValueError, match="too large"):
+        smooth_attn.softplus_norm_triton(torch.zeros(2, 8200, device=DEV))
+    x = _randn((2, 8192), torch.bfloat16, seed=25)
+    y = smooth_attn.softplus_norm_triton(x.to(DEV))
+    assert rel_err(y, eager.softplus_norm_eager(x.double())) <= 1e-2
+
+
+@pytest.mark.parametrize("L", [2048, 4096])
+def test_full_size_config2_properties(L):
+    """BASELINE config 2 at full size [4,16,L,L]: size-independent properties
+    on the whole output, oracle parity on sampled rows."""
+    B, H = 4, 16
+    gen = torch.Generator(device=DEV).manual_seed(L)
+    x = (torch.randn(B, H, L, L, generator=gen, device=DEV) / 128 ** 0.5).to(torch.bfloat16)
+    y = smooth_attn.softplus_norm_causal_triton(x)
+    sums = y.float().sum(-1)
+    assert float((sums - 1).abs().max()) < 2e-2  # bf16 rounding of up to L terms
+    up = torch.triu(torch.ones(L, L, dtype=torch.bool, device=DEV), 1)
+    assert int(y[0, 0][up].count_nonzero()) == 0 and int(y[-1, -1][up].count_nonzero()) == 0
+    rows = [0, 1, L // 2, L - 2, L - 1]
+    for b, h in [(0, 0), (B - 1, H - 1), (2, 7)]:
+        ref = eager.softplus_norm_causal_eager(x[b, h].cpu().double())
+        assert rel_err(y[b, h, rows], ref[rows]) <= 1e-2
+    dy = torch.randn(B, H, L, L, generator=gen, device=DEV).to(torch.bfloat16)
+    dx = kernels._softplus_norm_causal_backward(x, dy, FamilyConfig())
+    assert int(dx[1, 3][up].count_nonzero()) == 0
+    # sum_j dx_ij * P-weighted identity: sum over a row of dx_j * r_j / (alpha p w_j/S') == sum (dy - T) P ... checked
+    # directly against the oracle on sampled rows instead:
+    for b, h in [(0, 0), (3, 15)]:
+        ref = eager.softplus_norm_backward(x[b, h].cpu().double(), dy[b, h].cpu().double(), causal=True)
+        assert rel_err(dx[b, h, rows], ref[rows]) <= 1e-2

@@ -1,0 +1,107 @@
+"""Host-side behaviour of the drop-in API — CPU only, no kernel launches.
+
+Mirrors the reference's CPU-runnable tests (tests/test_family_config.py:4-19)
+and the validation errors it raises before any launch (kernels.py:71-73,
+150-240, 1420, 2032-2036, 2795-2799).
+"""
+import inspect
+
+import pytest
+import torch
+
+import smooth_attn
+from smooth_attn import FamilyConfig, kernels
+
+REFERENCE_EXPORTS = [
+    "BENCH_ALPHA", "BENCH_POWER", "BENCH_THETA", "DEFAULT_FAMILY", "CausalBenchmarkResult", "FamilyConfig",
+    "RowwiseBenchmarkResult", "SoftplusNormCausal", "bench", "bench_out", "benchmark_causal_suite",
+    "benchmark_rowwise_suite", "main", "softmax_causal_eager", "softmax_causal_triton",
+    "softmax_causal_triton_out", "softmax_triton", "softmax_triton_out", "softplus_norm_causal",
+    "softplus_norm_causal_eager", "softplus_norm_causal_triton", "softplus_norm_causal_triton_out",
+    "softplus_norm_eager", "softplus_norm_triton", "softplus_norm_triton_out", "sp2norm_flash_attention",
+    "sp2norm_flash_attention_eager", "sp2norm_fp8_flash_attention", "sp2norm_rope_flash_attention",
+    "sp2norm_rope_flash_attention_proj", "sp2norm_paged_attention", "precompute_rope_cos_sin", "sp2norm_triton",
+]
+
+
+def test_export_list_matches_reference():
+    assert sorted(smooth_attn.__all__) == sorted(REFERENCE_EXPORTS)
+    for name in REFERENCE_EXPORTS:
+        assert hasattr(smooth_attn, name), name
+
+
+def test_family_config_rejects_bad_power():
+    with pytest.raises(ValueError):
+        FamilyConfig(power=4)
+
+
+def test_family_config_rejects_removed_activation_kwarg():
+    with pytest.raises(TypeError):
+        FamilyConfig(activation="softplus")
+
+
+def test_family_config_properties():
+    f = FamilyConfig(alpha=1.5, theta=0.25, power=3)
+    assert f.cache_key == (1.5, 0.25, 3)
+    assert f.kernel_kwargs == {"ALPHA": 1.5, "THETA": 0.25, "POWER": 3}
+    assert f.label == "squareplus(1.5 * (x - 0.25))^3 / sum"
+    assert smooth_attn.DEFAULT_FAMILY == FamilyConfig()
+    assert (smooth_attn.BENCH_ALPHA, smooth_attn.BENCH_THETA, smooth_attn.BENCH_POWER) == (2.0, 0.5, 2)
+
+
+def test_family_and_overrides_conflict():
+    with pytest.raises(ValueError, match="not both"):
+        kernels._resolve_family(1.0, 0.5, 2, FamilyConfig())
+    assert kernels._resolve_family(2.0, 0.5, 2, FamilyConfig(power=3)).power == 3
+
+
+def test_signatures_match_reference():
+    sig = inspect.signature(smooth_attn.softplus_norm_causal_triton_out)
+    assert list(sig.parameters) == ["out", "x", "alpha", "theta", "power", "family", "return_meta"]
+    sig = inspect.signature(smooth_attn.sp2norm_flash_attention)
+    assert list(sig.parameters) == ["q", "k", "v", "scale", "window_size", "exact_math"]
+    sig = inspect.signature(smooth_attn.sp2norm_paged_attention)
+    assert list(sig.parameters) == ["q", "k_cache", "v_cache", "block_table", "context_lens", "scale",
+                                    "block_size"]
+    sig = inspect.signature(smooth_attn.SoftplusNormCausal.__init__)
+    assert list(sig.parameters) == ["self", "alpha", "theta", "power", "family", "implementation"]
+
+
+def test_rejects_non_tensor_and_cpu_tensor():
+    with pytest.raises(TypeError):
+        smooth_attn.softplus_norm_triton([1.0, 2.0])
+    with pytest.raises(ValueError, match="CUDA tensor"):
+        smooth_attn.softplus_norm_triton(torch.zeros(4, 4))
+    with pytest.raises(ValueError, match="CUDA tensor"):
+        smooth_attn.softplus_norm_causal_triton(torch.zeros(1, 4, 4))
+
+
+def test_implementation_switch():
+    x = torch.randn(1, 2, 8, 8).to(torch.bfloat16)
+    y = smooth_attn.softplus_norm_causal(x, implementation="eager")
+    assert y.dtype == torch.bfloat16 and y.shape == x.shape
+    with pytest.raises(ValueError, match="implementation"):
+        smooth_attn.softplus_norm_causal(x, implementation="cuda")
+
+
+def test_eager_functions_run_on_cpu():
+    x = torch.randn(2, 6, 6)
+    torch.testing.assert_close(smooth_attn.softplus_norm_causal_eager(x).sum(-1), torch.ones(2, 6), atol=1e-5,
+                               rtol=0)
+    q = torch.randn(1, 2, 5, 4)
+    o = smooth_attn.sp2norm_flash_attention_eager(q, q, q)
+    assert o.shape == q.shape
+    s = smooth_attn.softmax_causal_eager(x)
+    torch.testing.assert_close(s.sum(-1), torch.ones(2, 6))
+
+
+def test_flash_asserts_shapes():
+    q = torch.zeros(1, 4, 8, 16)
+    with pytest.raises(AssertionError):
+        smooth_attn.sp2norm_flash_attention(q, torch.zeros(1, 3, 8, 16), torch.zeros(1, 3, 8, 16))
+    with pytest.raises(AssertionError):
+        smooth_attn.sp2norm_flash_attention(q[0], q[0], q[0])
+    with pytest.raises(AssertionError):
+        smooth_attn.sp2norm_paged_attention(torch.zeros(1, 4, 2, 16), torch.zeros(2, 4, 16, 16),
+                                            torch.zeros(2, 4, 16, 16), torch.zeros(1, 2, dtype=torch.int32),
+                                            torch.zeros(1, dtype=torch.int32))
