@@ -1,0 +1,72 @@
+// Shared pieces of the fused squareplus attention kernels (gfx950 MFMA).
+//
+// Operand layouts of the MFMAs used here (checked on the device):
+//  v_mfma_f32_32x32x16_{bf16,f16}: A (32 x 16) lane l holds row l%32 and k
+//    8*(l/32) .. +7; B (16 x 32) lane l holds column l%32 and the same k;
+//    C/D (32 x 32 fp32, 16 per lane) lane l holds column l%32 and rows
+//    (v/4)*8 + (l/32)*4 + v%4 for v = 0..15.
+//  ds_read_b64_tr_b16: inside each group of 16 lanes, lane i receives element
+//    j = 0..3 from the address supplied by lane 4j + i/4, plus i%4 elements.
+//
+// The kernels compute S^T = K Q^T (keys as rows), so each lane ends up with
+// one query column and 16 keys of a 32 x 32 tile.  Those scores, once turned
+// into weights and rounded, are already laid out as the B operand of
+// O^T += V^T P^T, so P never leaves registers.  V^T is read from a row-major
+// V tile in LDS with the transposing LDS load.
+#pragma once
+
+#include "common.hpp"
+
+namespace sa {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+template <typename T>
+struct MfmaOps;
+
+template <>
+struct MfmaOps<bf16> {
+    using vec8 = bf16x8;
+    static __device__ __forceinline__ f32x16 mma(vec8 a, vec8 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+};
+
+template <>
+struct MfmaOps<f16> {
+    using vec8 = f16x8;
+    static __device__ __forceinline__ f32x16 mma(vec8 a, vec8 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+};
+
+// Reinterpret 4 words as an 8-element MFMA operand.
+template <typename V>
+__device__ __forceinline__ V as_vec8(u32x4 w) {
+    return __builtin_bit_cast(V, w);
+}
+
+// Transposing 8-byte LDS read (4 x 16-bit elements); p points into LDS.
+__device__ __forceinline__ uint2 lds_read_tr16(const void* p) {
+    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+    typedef __attribute__((address_space(3))) char lds_char;
+    const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)((lds_char*)(p)));
+    return __builtin_bit_cast(uint2, v);
+}
+
+// squareplus(a)^2 with a = scale * s - 1/2 already folded in:
+//   squareplus(2 s scale - 1) = (2 s scale - 1 + sqrt((2 s scale - 1)^2 + 4)) / 2
+//                             = a + sqrt(a^2 + 1),   a = s scale - 1/2.
+template <bool EXACT>
+__device__ __forceinline__ float sp2_weight(float a) {
+    const float u = __builtin_fmaf(a, a, 1.f);
+    const float r = EXACT ? __builtin_sqrtf(u) : fast_sqrt(u);
+    const float sp = a + r;
+    return sp * sp;
+}
+
+}  // namespace sa

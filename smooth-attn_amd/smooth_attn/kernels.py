@@ -417,8 +417,11 @@ _FLASH_HEAD_DIMS = (32, 64, 128)
 
 
 def _flash_operand(t):
-    """Unit stride along D is all the kernels need; anything else is copied."""
-    return t if t.stride(-1) == 1 else t.contiguous()
+    """The kernels take any (b, h, t) strides that are multiples of 8 elements
+    with a unit stride along D and a 16-byte aligned base; anything else is
+    copied to a contiguous tensor first."""
+    ok = t.stride(-1) == 1 and all(s % 8 == 0 for s in t.stride()[:-1]) and t.data_ptr() % 16 == 0
+    return t if ok else t.contiguous()
 
 
 def _sp2norm_flash_fwd(q, k, v, scale, n_kv_groups=1, window_size=0, use_fast_sqrt=True):
