@@ -245,14 +245,15 @@ def fp8_flash_attention_eager(q8, k8, v, q_scale, k_scale, v_scale, attn_scale, 
     scores = (q8 . k8) * q_scale * k_scale * attn_scale   (:2534, :2565)
     O = sum y * (v * v_scale) / (sum y + EPS)            (:2579-2581)
     ``v`` may be fp8 (the reference entry point, :2666) or bf16 (v_scale = 1).
+    Evaluated in float64 on the exactly dequantised codes.
 
     pinned by: reduces to flash_attention_eager on dequantised inputs (the
     function is exactly that composition); tests check the composition against
     brute.attention.
     """
-    qd = q8.float()
-    kd = k8.float()
-    vd = v.float() * float(v_scale)
+    qd = q8.double()
+    kd = k8.double()
+    vd = v.double() * float(v_scale)
     mult = float(q_scale) * float(k_scale) * float(attn_scale)
     return flash_attention_eager(qd, kd, vd, score_scale=mult, window_size=window_size,
                                  return_row_sums=return_row_sums)

@@ -1,19 +1,23 @@
-// Fused causal squareplus attention forward, bf16 / fp16 on gfx950 MFMA.
+// Fused causal squareplus attention forward on gfx950 MFMA: bf16 / fp16, and
+// fp8 e4m3fn QK^T with bf16 P V.
 //
 // O_i = sum_{j <= i, i - j < W} y_ij V_j / (sum_j y_ij + 1e-12),
-// y = squareplus(2 s - 1)^2, s = scale q_i . k_j   (reference kernels.py:1536-1631)
+// y = squareplus(2 s - 1)^2, s = scale q_i . k_j
+//   (reference kernels.py:1536-1631 bf16, :2498-2589 fp8)
 //
 // Squareplus needs no running maximum, so the weights are accumulated
-// linearly (sum y in fp32, P V on MFMA with P rounded to the input type, as
-// the reference does at :1617-1621) and divided once at the end.
+// linearly (sum y in fp32; P V on MFMA with P rounded to the 16-bit type,
+// as the reference does at :1617-1621 and :2579) and divided once at the end.
 //
 // Work decomposition: a block of 4 waves owns 128 query rows of one
 // (batch, query head); wave w owns rows [32w, 32w+32).  K and V tiles of 64
 // keys are staged through LDS (double buffered, one barrier per tile):
 // global -> registers for tile j+1 while tile j is computed, then registers
-// -> LDS.  Per wave and tile: S^T = K Q^T (2 x D/16 MFMA 32x32x16), the
-// squareplus weights on the VALU (masks only on tiles crossing the diagonal
-// or the window edge), then O^T += V^T P^T (4 x D/32 MFMA).
+// -> LDS.  Per wave and tile: S^T = K Q^T on MFMA, the squareplus weights on
+// the VALU (masks only on tiles crossing the diagonal or the window edge),
+// then O^T += V^T P^T on MFMA.  fp8 V is widened to the 16-bit type while it
+// is staged (exact: e4m3fn values are representable in bf16) and v_scale is
+// applied once at the end.
 // Blocks are issued heaviest first (last query blocks first) and, because the
 // block index runs over (batch, head) fastest, every query block of one head
 // lands on the same XCD when B*Hq is a multiple of 8 (shared K/V in L2).
@@ -24,7 +28,7 @@ namespace {
 
 constexpr int kBQ = 128;   // query rows per block
 constexpr int kBKV = 64;   // keys per tile
-constexpr int kWaves = 4;  // 32 query rows per wave
+constexpr int kThreads = 256;
 
 struct FlashParams {
     const void* q;
@@ -32,34 +36,62 @@ struct FlashParams {
     const void* v;
     void* o;
     float* row_sums;
+    const float* q_scale;  // fp8 only (device scalars)
+    const float* k_scale;
+    const float* v_scale;
     int64_t qs[4], ks[4], vs[4], os[4];
     int B, Hq, Hkv, T, G, window, nqb;
     float scale;
 };
 
-template <int D>
-struct TileGeom {
-    static constexpr int RSK = D + 8;    // K row stride in LDS (elements)
-    static constexpr int RSV = D + 8;    // V row stride in LDS (elements)
-    static constexpr int KT = kBKV * RSK;
-    static constexpr int VT = kBKV * RSV;
-    static constexpr int CPR = D / 8;                 // 16-byte chunks per row
-    static constexpr int NL = kBKV * CPR / (64 * kWaves);  // chunks per thread per tensor
+// T: 16-bit type of P V (and of q/k/v unless fp8).  QK8: q, k are e4m3fn.
+// V8: v is e4m3fn.
+template <typename T, int D, bool QK8, bool V8>
+struct Geom {
+    static constexpr int QKB = QK8 ? 1 : 2;         // bytes per q/k element
+    static constexpr int RSK = D * QKB + 16;        // K row stride in LDS (bytes)
+    static constexpr int RSV = D + 8;               // V row stride in LDS (elements of T)
+    static constexpr int KT = kBKV * RSK;           // bytes per K tile
+    static constexpr int VT = kBKV * RSV * 2;       // bytes per V tile
+    static constexpr int KCPR = D * QKB / 16;       // 16-byte global chunks per K row
+    static constexpr int VCPR = D * (V8 ? 1 : 2) / 16;
+    static constexpr int KNL = (kBKV * KCPR + kThreads - 1) / kThreads;
+    static constexpr int VNL = (kBKV * VCPR + kThreads - 1) / kThreads;
+    static constexpr int NQC = QK8 ? (D + 63) / 64 : D / 16;  // MFMAs per 32x32 score tile
 };
 
-template <typename T, int D, bool EXACT>
+__device__ __forceinline__ f32x16 mma_fp8(i32x8 a, i32x8 b, f32x16 c) {
+    // e4m3 x e4m3, unit block scales (E8M0 127 = 2^0)
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+}
+
+// Widen 16 e4m3fn values (one 16-byte word) to 16 bf16 / f16 values (two words).
+template <typename T>
+__device__ __forceinline__ void widen_fp8x16(u32x4 in, u32x4& lo, u32x4& hi) {
+    uint32_t out[8];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const int word = static_cast<int>(in[w]);
+        out[2 * w] = pack2<T>(__builtin_amdgcn_cvt_f32_fp8(word, 0), __builtin_amdgcn_cvt_f32_fp8(word, 1));
+        out[2 * w + 1] = pack2<T>(__builtin_amdgcn_cvt_f32_fp8(word, 2), __builtin_amdgcn_cvt_f32_fp8(word, 3));
+    }
+    lo = u32x4{out[0], out[1], out[2], out[3]};
+    hi = u32x4{out[4], out[5], out[6], out[7]};
+}
+
+template <typename T, int D, bool QK8, bool V8, bool EXACT>
 __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FlashParams p) {
-    using G = TileGeom<D>;
+    using Gm = Geom<T, D, QK8, V8>;
     using Ops = MfmaOps<T>;
-    using V8 = typename Ops::vec8;
-    __shared__ __attribute__((aligned(16))) T lds[2 * (G::KT + G::VT)];
-    T* ldsK = lds;                 // [2][64][RSK]
-    T* ldsV = lds + 2 * G::KT;     // [2][64][RSV]
+    using Vec = typename Ops::vec8;
+    __shared__ __attribute__((aligned(16))) unsigned char lds[2 * (Gm::KT + Gm::VT)];
+    unsigned char* ldsK = lds;                 // [2][64][RSK bytes]
+    T* ldsV = reinterpret_cast<T*>(lds + 2 * Gm::KT);  // [2][64][RSV]
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int hi = lane >> 5;      // lane half
+    const int hi = lane >> 5;  // lane half
     const int l32 = lane & 31;
 
     const int BH = p.B * p.Hq;
@@ -71,10 +103,14 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FlashParams p) {
     const int hk = hq / p.G;
     const int T_ = p.T;
 
-    const T* qp = static_cast<const T*>(p.q) + b * p.qs[0] + hq * p.qs[1];
-    const T* kp = static_cast<const T*>(p.k) + b * p.ks[0] + hk * p.ks[1];
-    const T* vp = static_cast<const T*>(p.v) + b * p.vs[0] + hk * p.vs[1];
+    const unsigned char* qp = static_cast<const unsigned char*>(p.q) + (b * p.qs[0] + hq * p.qs[1]) * Gm::QKB;
+    const unsigned char* kp = static_cast<const unsigned char*>(p.k) + (b * p.ks[0] + hk * p.ks[1]) * Gm::QKB;
+    const unsigned char* vp =
+        static_cast<const unsigned char*>(p.v) + (b * p.vs[0] + hk * p.vs[1]) * (V8 ? 1 : 2);
     T* op = static_cast<T*>(p.o) + b * p.os[0] + hq * p.os[1];
+    const int64_t qrs = p.qs[2] * Gm::QKB;  // row strides in bytes
+    const int64_t krs = p.ks[2] * Gm::QKB;
+    const int64_t vrs = p.vs[2] * (V8 ? 1 : 2);
 
     const int q_start = qb * kBQ;
     const int wq0 = q_start + wave * 32;
@@ -83,15 +119,30 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FlashParams p) {
     const int kv_end = min((q_start + kBQ + kBKV - 1) / kBKV, n_kv);
     const int kv_begin = W > 0 ? max(0, q_start - W + 1) / kBKV : 0;
 
-    // Q^T as the B operand: lane holds query row wq0 + l32, d = 16 dc + 8 hi .. +7.
-    u32x4 qreg[D / 16];
+    // Q^T as the B operand.  16-bit: chunk dc holds d = 16 dc + 8 hi .. +7.
+    // fp8: chunk dc holds d = 64 dc + 32 hi .. +31 (zero past D).
+    u32x4 qreg[Gm::NQC][QK8 ? 2 : 1];
     {
         const int qrow = wq0 + l32;
 #pragma unroll
-        for (int dc = 0; dc < D / 16; ++dc) {
-            qreg[dc] = qrow < T_ ? load16(qp + qrow * p.qs[2] + dc * 16 + hi * 8) : u32x4{0u, 0u, 0u, 0u};
+        for (int dc = 0; dc < Gm::NQC; ++dc) {
+            if constexpr (QK8) {
+                const int d0 = 64 * dc + 32 * hi;
+#pragma unroll
+                for (int w = 0; w < 2; ++w) {
+                    const bool in = qrow < T_ && d0 + 16 * w < D;
+                    qreg[dc][w] = in ? load16(qp + qrow * qrs + d0 + 16 * w) : u32x4{0u, 0u, 0u, 0u};
+                }
+            } else {
+                qreg[dc][0] = qrow < T_ ? load16(qp + qrow * qrs + (dc * 16 + hi * 8) * 2) : u32x4{0u, 0u, 0u, 0u};
+            }
         }
     }
+
+    float sc = p.scale;
+    float vsc = 1.f;
+    if constexpr (QK8) sc *= p.q_scale[0] * p.k_scale[0];
+    if constexpr (V8) vsc = p.v_scale[0];
 
     f32x16 oacc[D / 32];
 #pragma unroll
@@ -99,39 +150,56 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FlashParams p) {
     float ssum = 0.f;
 
     // Global -> register staging of one K/V tile.
-    u32x4 kst[G::NL], vst[G::NL];
+    u32x4 kst[Gm::KNL], vst[Gm::VNL];
     auto load_tile = [&](int j) {
         const int k0 = j * kBKV;
 #pragma unroll
-        for (int i = 0; i < G::NL; ++i) {
-            const int ci = tid + 256 * i;
-            const int row = ci / G::CPR;
-            const int c8 = ci - row * G::CPR;
-            const int key = k0 + row;
-            if (key < T_) {
-                kst[i] = load16(kp + key * p.ks[2] + c8 * 8);
-                vst[i] = load16(vp + key * p.vs[2] + c8 * 8);
-            } else {
-                kst[i] = u32x4{0u, 0u, 0u, 0u};
-                vst[i] = u32x4{0u, 0u, 0u, 0u};
-            }
+        for (int i = 0; i < Gm::KNL; ++i) {
+            const int ci = tid + kThreads * i;
+            const int row = ci / Gm::KCPR;
+            const int c = ci - row * Gm::KCPR;
+            const bool in = ci < kBKV * Gm::KCPR && k0 + row < T_;
+            kst[i] = in ? load16(kp + (k0 + row) * krs + c * 16) : u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int i = 0; i < Gm::VNL; ++i) {
+            const int ci = tid + kThreads * i;
+            const int row = ci / Gm::VCPR;
+            const int c = ci - row * Gm::VCPR;
+            const bool in = ci < kBKV * Gm::VCPR && k0 + row < T_;
+            vst[i] = in ? load16(vp + (k0 + row) * vrs + c * 16) : u32x4{0u, 0u, 0u, 0u};
         }
     };
     auto store_tile = [&](int buf) {
 #pragma unroll
-        for (int i = 0; i < G::NL; ++i) {
-            const int ci = tid + 256 * i;
-            const int row = ci / G::CPR;
-            const int c8 = ci - row * G::CPR;
-            *reinterpret_cast<u32x4*>(ldsK + buf * G::KT + row * G::RSK + c8 * 8) = kst[i];
-            *reinterpret_cast<u32x4*>(ldsV + buf * G::VT + row * G::RSV + c8 * 8) = vst[i];
+        for (int i = 0; i < Gm::KNL; ++i) {
+            const int ci = tid + kThreads * i;
+            const int row = ci / Gm::KCPR;
+            const int c = ci - row * Gm::KCPR;
+            if (ci < kBKV * Gm::KCPR)
+                *reinterpret_cast<u32x4*>(ldsK + buf * Gm::KT + row * Gm::RSK + c * 16) = kst[i];
+        }
+#pragma unroll
+        for (int i = 0; i < Gm::VNL; ++i) {
+            const int ci = tid + kThreads * i;
+            const int row = ci / Gm::VCPR;
+            const int c = ci - row * Gm::VCPR;
+            if (ci < kBKV * Gm::VCPR) {
+                T* dst = ldsV + buf * (Gm::VT / 2) + row * Gm::RSV;
+                if constexpr (V8) {
+                    u32x4 lo, hi16;
+                    widen_fp8x16<T>(vst[i], lo, hi16);
+                    *reinterpret_cast<u32x4*>(dst + c * 16) = lo;
+                    *reinterpret_cast<u32x4*>(dst + c * 16 + 8) = hi16;
+                } else {
+                    *reinterpret_cast<u32x4*>(dst + c * 8) = vst[i];
+                }
+            }
         }
     };
 
-    // Per-lane element offset of the transposing V read (key part + d part);
-    // see flash_common.hpp for the derivation.
-    const int v_tr_off = ((lane >> 5) * 4 + ((lane & 15) >> 2)) * G::RSV + ((lane >> 4) & 1) * 16 + 4 * (lane & 3);
-    const float scale = p.scale;
+    // Per-lane element offset of the transposing V read; see flash_common.hpp.
+    const int v_tr_off = ((lane >> 5) * 4 + ((lane & 15) >> 2)) * Gm::RSV + ((lane >> 4) & 1) * 16 + 4 * (lane & 3);
 
     if (kv_begin < kv_end) {
         load_tile(kv_begin);
@@ -146,16 +214,32 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FlashParams p) {
         const int k0 = j * kBKV;
         const bool active = (k0 <= wq0 + 31) && !(W > 0 && k0 + kBKV - 1 <= wq0 - W);
         if (active) {
-            const T* Kb = ldsK + buf * G::KT;
-            const T* Vb = ldsV + buf * G::VT;
+            const unsigned char* Kb = ldsK + buf * Gm::KT;
+            const T* Vb = ldsV + buf * (Gm::VT / 2);
             f32x16 s[2];
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt) {
                 s[kt] = f32x16{};
+                const unsigned char* krow = Kb + (kt * 32 + l32) * Gm::RSK;
 #pragma unroll
-                for (int dc = 0; dc < D / 16; ++dc) {
-                    const u32x4 a = *reinterpret_cast<const u32x4*>(Kb + (kt * 32 + l32) * G::RSK + dc * 16 + hi * 8);
-                    s[kt] = Ops::mma(as_vec8<V8>(a), as_vec8<V8>(qreg[dc]), s[kt]);
+                for (int dc = 0; dc < Gm::NQC; ++dc) {
+                    if constexpr (QK8) {
+                        const int d0 = 64 * dc + 32 * hi;
+                        u32x4 a0 = u32x4{0u, 0u, 0u, 0u}, a1 = u32x4{0u, 0u, 0u, 0u};
+                        if (d0 < D) {
+                            a0 = *reinterpret_cast<const u32x4*>(krow + d0);
+                            a1 = *reinterpret_cast<const u32x4*>(krow + d0 + 16);
+                        }
+                        const i32x8 av{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w,
+                                       (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+                        const i32x8 bv{(int)qreg[dc][0].x, (int)qreg[dc][0].y, (int)qreg[dc][0].z,
+                                       (int)qreg[dc][0].w, (int)qreg[dc][1].x, (int)qreg[dc][1].y,
+                                       (int)qreg[dc][1].z, (int)qreg[dc][1].w};
+                        s[kt] = mma_fp8(av, bv, s[kt]);
+                    } else {
+                        const u32x4 a = *reinterpret_cast<const u32x4*>(krow + (dc * 16 + hi * 8) * 2);
+                        s[kt] = Ops::mma(as_vec8<Vec>(a), as_vec8<Vec>(qreg[dc][0]), s[kt]);
+                    }
                 }
             }
             const bool edge = (k0 + kBKV - 1 > wq0) || (W > 0 && k0 <= wq0 + 31 - W);
@@ -165,7 +249,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FlashParams p) {
             for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
-                    float w = sp2_weight<EXACT>(__builtin_fmaf(s[kt][v], scale, -0.5f));
+                    float w = sp2_weight<EXACT>(__builtin_fmaf(s[kt][v], sc, -0.5f));
                     if (edge) {
                         const int key = k0 + kt * 32 + (v >> 2) * 8 + hi * 4 + (v & 3);
                         const bool ok = key <= qi && (W <= 0 || qi - key < W);
@@ -177,22 +261,20 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FlashParams p) {
             }
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                float pv[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) pv[e] = y[c >> 1][(c & 1) * 8 + e];
+                const float* pv = &y[c >> 1][(c & 1) * 8];
                 u32x4 pw;
                 pw.x = pack2<T>(pv[0], pv[1]);
                 pw.y = pack2<T>(pv[2], pv[3]);
                 pw.z = pack2<T>(pv[4], pv[5]);
                 pw.w = pack2<T>(pv[6], pv[7]);
-                const V8 bop = as_vec8<V8>(pw);
+                const Vec bop = as_vec8<Vec>(pw);
 #pragma unroll
                 for (int dt = 0; dt < D / 32; ++dt) {
-                    const T* base = Vb + (16 * c) * G::RSV + dt * 32 + v_tr_off;
+                    const T* base = Vb + (16 * c) * Gm::RSV + dt * 32 + v_tr_off;
                     const uint2 lo = lds_read_tr16(base);
-                    const uint2 hi8 = lds_read_tr16(base + 8 * G::RSV);
+                    const uint2 hi8 = lds_read_tr16(base + 8 * Gm::RSV);
                     const u32x4 aw{lo.x, lo.y, hi8.x, hi8.y};
-                    oacc[dt] = Ops::mma(as_vec8<V8>(aw), bop, oacc[dt]);
+                    oacc[dt] = Ops::mma(as_vec8<Vec>(aw), bop, oacc[dt]);
                 }
             }
         }
@@ -202,7 +284,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FlashParams p) {
 
     // Row sums: lanes l and l^32 hold the two key halves of one query column.
     const float stot = ssum + __shfl_xor(ssum, 32) + kEps;
-    const float inv = 1.f / stot;
+    const float inv = vsc / stot;
     const int qi = wq0 + l32;
     if (qi < T_) {
         T* orow = op + qi * p.os[2];
@@ -221,37 +303,43 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FlashParams p) {
     }
 }
 
-template <typename T, int D>
+template <typename T, int D, bool QK8, bool V8>
 int launch_flash(const FlashParams& prm, int exact, hipStream_t st) {
     const dim3 grid(static_cast<unsigned>(prm.nqb) * prm.B * prm.Hq);
-    const dim3 block(256);
+    const dim3 block(kThreads);
     if (exact)
-        flash_fwd_kernel<T, D, true><<<grid, block, 0, st>>>(prm);
+        flash_fwd_kernel<T, D, QK8, V8, true><<<grid, block, 0, st>>>(prm);
     else
-        flash_fwd_kernel<T, D, false><<<grid, block, 0, st>>>(prm);
+        flash_fwd_kernel<T, D, QK8, V8, false><<<grid, block, 0, st>>>(prm);
     return status_from_launch();
 }
 
-bool strides_ok(const int64_t* s) {
-    return s[3] == 1 && s[0] % 8 == 0 && s[1] % 8 == 0 && s[2] % 8 == 0;
+template <typename T, bool QK8, bool V8>
+int launch_flash_d(const FlashParams& prm, int D, int exact, hipStream_t st) {
+    switch (D) {
+        case 32: return launch_flash<T, 32, QK8, V8>(prm, exact, st);
+        case 64: return launch_flash<T, 64, QK8, V8>(prm, exact, st);
+        case 128: return launch_flash<T, 128, QK8, V8>(prm, exact, st);
+        default: return SA_ERR_UNSUPPORTED;
+    }
 }
 
-}  // namespace
-}  // namespace sa
+// (b, h, t) strides must keep every row start 16-byte aligned; d stride 1.
+bool strides_ok(const int64_t* s, int elem_bytes) {
+    const int64_t a = 16 / elem_bytes;
+    return s[3] == 1 && s[0] % a == 0 && s[1] % a == 0 && s[2] % a == 0;
+}
 
-extern "C" int sa_flash_fwd(const void* q, const void* k, const void* v, void* o, float* row_sums, int B, int Hq,
-                            int Hkv, int T, int D, const int64_t* q_strides, const int64_t* k_strides,
-                            const int64_t* v_strides, const int64_t* o_strides, float scale, int window_size,
-                            int exact_math, int dtype, sa_stream_t stream) {
-    using namespace sa;
+int fill_params(FlashParams& prm, const void* q, const void* k, const void* v, void* o, float* row_sums, int B,
+                int Hq, int Hkv, int T, int D, const int64_t* q_strides, const int64_t* k_strides,
+                const int64_t* v_strides, const int64_t* o_strides, float scale, int window_size, int qk_bytes,
+                int v_bytes) {
     if (B < 0 || Hq <= 0 || Hkv <= 0 || T < 0 || Hq % Hkv != 0 || window_size < 0) return SA_ERR_BAD_SHAPE;
-    if (B == 0 || T == 0) return 0;
     if (!q || !k || !v || !o || !q_strides || !k_strides || !v_strides || !o_strides) return SA_ERR_NULL_POINTER;
     if (D != 32 && D != 64 && D != 128) return SA_ERR_UNSUPPORTED;
-    if (!strides_ok(q_strides) || !strides_ok(k_strides) || !strides_ok(v_strides) || !strides_ok(o_strides) ||
-        !aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
+    if (!strides_ok(q_strides, qk_bytes) || !strides_ok(k_strides, qk_bytes) || !strides_ok(v_strides, v_bytes) ||
+        !strides_ok(o_strides, 2) || !aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
         return SA_ERR_BAD_STRIDE;
-    FlashParams prm{};
     prm.q = q;
     prm.k = k;
     prm.v = v;
@@ -271,21 +359,47 @@ extern "C" int sa_flash_fwd(const void* q, const void* k, const void* v, void* o
     prm.window = window_size;
     prm.nqb = (T + kBQ - 1) / kBQ;
     prm.scale = scale;
-    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    return 0;
+}
+
+}  // namespace
+}  // namespace sa
+
+extern "C" int sa_flash_fwd(const void* q, const void* k, const void* v, void* o, float* row_sums, int B, int Hq,
+                            int Hkv, int T, int D, const int64_t* q_strides, const int64_t* k_strides,
+                            const int64_t* v_strides, const int64_t* o_strides, float scale, int window_size,
+                            int exact_math, int dtype, sa_stream_t stream) {
+    using namespace sa;
+    if (dtype != SA_BF16 && dtype != SA_F16) return SA_ERR_BAD_DTYPE;
+    FlashParams prm{};
+    const int st = fill_params(prm, q, k, v, o, row_sums, B, Hq, Hkv, T, D, q_strides, k_strides, v_strides,
+                               o_strides, scale, window_size, 2, 2);
+    if (st != 0) return st;
+    if (B == 0 || T == 0) return 0;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int ex = exact_math ? 1 : 0;
-    if (dtype == SA_BF16) {
-        switch (D) {
-            case 32: return launch_flash<bf16, 32>(prm, ex, st);
-            case 64: return launch_flash<bf16, 64>(prm, ex, st);
-            default: return launch_flash<bf16, 128>(prm, ex, st);
-        }
-    }
-    if (dtype == SA_F16) {
-        switch (D) {
-            case 32: return launch_flash<f16, 32>(prm, ex, st);
-            case 64: return launch_flash<f16, 64>(prm, ex, st);
-            default: return launch_flash<f16, 128>(prm, ex, st);
-        }
-    }
-    return SA_ERR_BAD_DTYPE;
+    if (dtype == SA_BF16) return launch_flash_d<bf16, false, false>(prm, D, ex, s);
+    return launch_flash_d<f16, false, false>(prm, D, ex, s);
+}
+
+extern "C" int sa_flash_fp8_fwd(const void* q8, const void* k8, const void* v, void* o, float* row_sums,
+                                const float* q_scale, const float* k_scale, const float* v_scale, int B, int Hq,
+                                int Hkv, int T, int D, const int64_t* q_strides, const int64_t* k_strides,
+                                const int64_t* v_strides, const int64_t* o_strides, float attn_scale,
+                                int window_size, int v_dtype, sa_stream_t stream) {
+    using namespace sa;
+    if (v_dtype != SA_FP8_E4M3FN && v_dtype != SA_BF16) return SA_ERR_BAD_DTYPE;
+    const bool v8 = v_dtype == SA_FP8_E4M3FN;
+    if (!q_scale || !k_scale || (v8 && !v_scale)) return SA_ERR_NULL_POINTER;
+    FlashParams prm{};
+    const int st = fill_params(prm, q8, k8, v, o, row_sums, B, Hq, Hkv, T, D, q_strides, k_strides, v_strides,
+                               o_strides, attn_scale, window_size, 1, v8 ? 1 : 2);
+    if (st != 0) return st;
+    if (B == 0 || T == 0) return 0;
+    prm.q_scale = q_scale;
+    prm.k_scale = k_scale;
+    prm.v_scale = v_scale;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (v8) return launch_flash_d<bf16, true, true>(prm, D, 0, s);
+    return launch_flash_d<bf16, true, false>(prm, D, 0, s);
 }

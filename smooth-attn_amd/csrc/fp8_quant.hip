@@ -1,0 +1,106 @@
+// Per-tensor absmax quantisation to float8_e4m3fn, entirely on the device
+// (reference kernels.py:2592-2601, which synchronises through .item()):
+//   scale = max(amax|x| / 448, 1e-12);  x8 = e4m3fn(clamp(x / scale, +-448))
+// Three launches on one stream: zero the amax word, reduce amax with one
+// atomicMax per block (non-negative floats order like their bit patterns),
+// then quantise.  x / scale is a true division so the codes match torch's
+// fp32 division followed by the round-to-nearest-even e4m3fn cast.
+#include "common.hpp"
+
+namespace sa {
+namespace {
+
+constexpr int kQThreads = 256;
+
+__global__ void fill_zero_u32(uint32_t* p) { p[0] = 0u; }
+
+template <typename T>
+__device__ __forceinline__ float ld(const T* p, int64_t i) { return to_f32(p[i]); }
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    return v;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kQThreads) void amax_kernel(const T* __restrict__ x, int64_t n, uint32_t* amax_bits) {
+    __shared__ float part[kQThreads / 64];
+    float m = 0.f;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kQThreads;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kQThreads + threadIdx.x; i < n; i += stride)
+        m = fmaxf(m, fabsf(ld(x, i)));
+    m = wave_max(m);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float b = part[0];
+        for (int w = 1; w < kQThreads / 64; ++w) b = fmaxf(b, part[w]);
+        atomicMax(amax_bits, __float_as_uint(b));
+    }
+}
+
+__device__ __forceinline__ float quant_scale(const uint32_t* amax_bits) {
+    const float amax = __uint_as_float(amax_bits[0]);
+    return fmaxf(amax / 448.f, 1e-12f);
+}
+
+// Round-to-nearest-even conversion of a value already clamped to +-448.
+__device__ __forceinline__ uint32_t to_e4m3(float v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(v, v, 0, false)) & 0xFFu;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kQThreads) void quant_kernel(const T* __restrict__ x, uint8_t* __restrict__ x8, int64_t n,
+                                                          const uint32_t* amax_bits, float* scale_out) {
+    const float scale = quant_scale(amax_bits);
+    if (blockIdx.x == 0 && threadIdx.x == 0) scale_out[0] = scale;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kQThreads;
+    // four elements per thread and step, one 32-bit store
+    const int64_t n4 = n / 4;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kQThreads + threadIdx.x; i < n4; i += stride) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float v = fminf(fmaxf(ld(x, 4 * i + e) / scale, -448.f), 448.f);
+            word |= to_e4m3(v) << (8 * e);
+        }
+        reinterpret_cast<uint32_t*>(x8)[i] = word;
+    }
+    if (blockIdx.x == 0) {
+        for (int64_t i = 4 * n4 + threadIdx.x; i < n; i += kQThreads) {
+            const float v = fminf(fmaxf(ld(x, i) / scale, -448.f), 448.f);
+            x8[i] = static_cast<uint8_t>(to_e4m3(v));
+        }
+    }
+}
+
+template <typename T>
+int launch_quant(const void* x, void* x8, int64_t n, float* amax_ws, float* scale_out, hipStream_t st) {
+    uint32_t* ab = reinterpret_cast<uint32_t*>(amax_ws);
+    fill_zero_u32<<<1, 1, 0, st>>>(ab);
+    const int64_t want = (n + kQThreads * 8 - 1) / (kQThreads * 8);
+    const unsigned blocks = static_cast<unsigned>(want < 1 ? 1 : (want > 4096 ? 4096 : want));
+    amax_kernel<T><<<blocks, kQThreads, 0, st>>>(static_cast<const T*>(x), n, ab);
+    quant_kernel<T><<<blocks, kQThreads, 0, st>>>(static_cast<const T*>(x), static_cast<uint8_t*>(x8), n, ab,
+                                                  scale_out);
+    return status_from_launch();
+}
+
+}  // namespace
+}  // namespace sa
+
+extern "C" int sa_fp8_quantize(const void* x, void* x8, int64_t n, int dtype, float* amax_ws, float* scale_out,
+                               sa_stream_t stream) {
+    using namespace sa;
+    if (n < 0) return SA_ERR_BAD_SHAPE;
+    if (!amax_ws || !scale_out || (n > 0 && (!x || !x8))) return SA_ERR_NULL_POINTER;
+    if ((reinterpret_cast<uintptr_t>(x8) & 3u) != 0) return SA_ERR_BAD_STRIDE;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    switch (dtype) {
+        case SA_F32: return launch_quant<float>(x, x8, n, amax_ws, scale_out, st);
+        case SA_F16: return launch_quant<f16>(x, x8, n, amax_ws, scale_out, st);
+        case SA_BF16: return launch_quant<bf16>(x, x8, n, amax_ws, scale_out, st);
+        default: return SA_ERR_BAD_DTYPE;
+    }
+}

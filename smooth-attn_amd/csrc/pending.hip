@@ -7,10 +7,6 @@ extern "C" int sa_flash_bwd(const void*, const void*, const void*, const void*, 
                             const int64_t*, float, int, int, int, sa_stream_t) {
     return SA_ERR_UNSUPPORTED;
 }
-extern "C" int sa_fp8_quantize(const void*, void*, int64_t, int, float*, float*, sa_stream_t) { return SA_ERR_UNSUPPORTED; }
-extern "C" int sa_flash_fp8_fwd(const void*, const void*, const void*, void*, float*, const float*, const float*,
-                                const float*, int, int, int, int, int, const int64_t*, const int64_t*,
-                                const int64_t*, const int64_t*, float, int, int, sa_stream_t) { return SA_ERR_UNSUPPORTED; }
 extern "C" int64_t sa_paged_decode_workspace_size(int, int, int, int, int) { return 0; }
 extern "C" int sa_paged_decode(const void*, const void*, const void*, void*, const int32_t*, const int32_t*, int, int,
                                int, int, int, int, const int64_t*, const int64_t*, const int64_t*, const int64_t*,
