@@ -163,8 +163,11 @@ int64_t sa_paged_decode_workspace_size(int B, int Hq, int D, int max_pages,
  *   q: [B, Hq, 1, D] (strides q_strides, d stride 1)
  *   k_cache, v_cache: [n_pages, Hkv, page_size, D] (strides kv_strides /
  *     vv_strides, d stride 1)
- *   block_table: int32 [B, max_pages] (row stride bt_stride, unit col stride)
+ *   block_table: int32 [B, max_pages] (row stride bt_stride, unit col stride),
+ *     entries in [0, n_pages) for the pages a sequence uses
  *   context_lens: int32 [B], each in [0, max_pages * page_size]
+ * Out-of-range page ids and context lengths are clamped on the device (the
+ * result is then meaningless but no memory outside the cache is read).
  *   out: bf16 [B, Hq, D] (strides o_strides)
  * out[b,h] = sum_{t<ctx_b} y_t V_t / (sum_t y_t + 1e-12) with
  * K_t = k_cache[block_table[b, t/P], h/(Hq/Hkv), t%P].  dtype (q and cache):
@@ -176,7 +179,7 @@ int64_t sa_paged_decode_workspace_size(int B, int Hq, int D, int max_pages,
 int sa_paged_decode(const void* q, const void* k_cache, const void* v_cache,
                     void* out, const int32_t* block_table,
                     const int32_t* context_lens, int B, int Hq, int Hkv,
-                    int D, int page_size, int max_pages,
+                    int D, int page_size, int max_pages, int n_pages,
                     const int64_t* q_strides, const int64_t* kv_strides,
                     const int64_t* vv_strides, const int64_t* o_strides,
                     int64_t bt_stride, float scale, int dtype,

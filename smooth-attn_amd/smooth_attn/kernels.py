@@ -634,7 +634,8 @@ def sp2norm_paged_attention(q, k_cache, v_cache, block_table, context_lens, *, s
     with torch.cuda.device(q.device):
         st = lib.sa_paged_decode(
             q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(), block_table.data_ptr(),
-            context_lens.data_ptr(), B, H_q, H_kv, D, block_size, max_blocks_per_seq, _lib.strides(q),
+            context_lens.data_ptr(), B, H_q, H_kv, D, block_size, max_blocks_per_seq, k_cache.shape[0],
+            _lib.strides(q),
             _lib.strides(k_cache), _lib.strides(v_cache), _lib.strides(out), block_table.stride(0),
             float(scale), _DTYPE_CODE[q.dtype], ws.data_ptr(), ws.numel() * 4, _stream(q),
         )

@@ -1,0 +1,123 @@
+"""Paged decode on the GPU against the CPU oracle (oracle.eager.paged_decode_eager,
+pinned in test_oracle.py against the last row of causal attention).
+
+Tolerance: bf16 output max|HIP - oracle| / max|oracle| <= 1e-2 against the
+float64 oracle on the same seeded inputs; the reference's own bounds
+(tests/test_paged_attention.py: max error < 0.05; test_paged_long_context.py:
+< 0.1 up to 8K, finite at 16K-32K) are checked as well.
+"""
+import math
+
+import pytest
+import torch
+
+import smooth_attn
+from oracle import eager, paging
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _g(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def rel_err(got, ref):
+    got = got.detach().double().cpu()
+    ref = ref.detach().double().cpu()
+    return float((got - ref).abs().max() / ref.abs().max().clamp(min=1e-30))
+
+
+def run(q, kc, vc, table, lens, page_size, dtype=torch.bfloat16):
+    out = smooth_attn.sp2norm_paged_attention(q.to(dtype).to(DEV), kc.to(dtype).to(DEV), vc.to(dtype).to(DEV),
+                                              table.to(DEV), lens.to(DEV), block_size=page_size)
+    assert out.dtype == torch.bfloat16 and out.shape == (q.shape[0], q.shape[1], q.shape[3])
+    return out
+
+
+def case(B, Hq, Hkv, T, D, seed, dtype=torch.bfloat16):
+    g = _g(seed)
+    q = torch.randn(B, Hq, 1, D, generator=g).to(dtype)
+    k = torch.randn(B, Hkv, T, D, generator=g).to(dtype)
+    v = torch.randn(B, Hkv, T, D, generator=g).to(dtype)
+    return q, k, v
+
+
+@pytest.mark.parametrize("B,H,T,D,BS", [(1, 4, 64, 32, 16), (2, 4, 128, 32, 16), (2, 8, 256, 64, 16),
+                                        (1, 4, 48, 32, 16), (3, 4, 1000, 128, 16), (2, 4, 1, 64, 8)])
+@pytest.mark.parametrize("shuffle", [False, True])
+def test_paged_matches_oracle(B, H, T, D, BS, shuffle):
+    q, k, v = case(B, H, H, T, D, seed=T + D + B)
+    kc, vc, table, lens = paging.build_paged_cache(k, v, page_size=BS, shuffle=shuffle, generator=_g(1))
+    out = run(q, kc, vc, table, lens, BS)
+    ref = eager.paged_decode_eager(q.double(), kc.double(), vc.double(), table, lens)
+    assert rel_err(out, ref) <= 1e-2
+    assert float((out.double().cpu() - ref).abs().max()) < 0.05
+
+
+@pytest.mark.parametrize("hq,hkv", [(8, 2), (32, 8), (4, 1), (32, 1)])
+def test_paged_gqa(hq, hkv):
+    q, k, v = case(2, hq, hkv, 300, 128, seed=hq + hkv)
+    kc, vc, table, lens = paging.build_paged_cache(k, v, page_size=16, shuffle=True, generator=_g(2))
+    out = run(q, kc, vc, table, lens, 16)
+    ref = eager.paged_decode_eager(q.double(), kc.double(), vc.double(), table, lens)
+    assert rel_err(out, ref) <= 1e-2
+
+
+def test_paged_variable_context_lengths():
+    # tests/test_paged_attention.py:175-221 with a seed, plus zero and split-crossing lengths
+    lens = [32, 64, 48, 128, 0, 513, 1, 1024]
+    T = max(lens)
+    q, k, v = case(len(lens), 4, 4, T, 64, seed=3)
+    kc, vc, table, lens_t = paging.build_paged_cache(k, v, page_size=16, shuffle=True, generator=_g(4),
+                                                     context_lens=lens)
+    out = run(q, kc, vc, table, lens_t, 16)
+    ref = eager.paged_decode_eager(q.double(), kc.double(), vc.double(), table, lens_t)
+    assert rel_err(out, ref) <= 1e-2
+    assert bool((out[4] == 0).all())  # empty context -> 0 / eps = 0 (reference: o_acc / 1e-12)
+
+
+@pytest.mark.parametrize("BS", [8, 16, 32, 64])
+def test_paged_block_sizes_agree(BS):
+    q, k, v = case(2, 4, 4, 128, 32, seed=5)
+    kc, vc, table, lens = paging.build_paged_cache(k, v, page_size=BS, shuffle=True, generator=_g(BS))
+    out = run(q, kc, vc, table, lens, BS)
+    ref = eager.paged_decode_eager(q.double(), kc.double(), vc.double(), table, lens)
+    assert rel_err(out, ref) <= 1e-2
+
+
+def test_paged_fp16():
+    q, k, v = case(2, 8, 2, 200, 64, seed=6, dtype=torch.float16)
+    kc, vc, table, lens = paging.build_paged_cache(k, v, page_size=16, shuffle=True, generator=_g(6))
+    out = run(q, kc, vc, table, lens, 16, dtype=torch.float16)
+    ref = eager.paged_decode_eager(q.double(), kc.double(), vc.double(), table, lens)
+    assert rel_err(out, ref) <= 1e-2
+
+
+def test_paged_long_context():
+    # tests/test_paged_long_context.py:83-161: 8K parity, 32K finite
+    for T, hq, hkv, D in [(8192, 8, 2, 64), (32768, 32, 8, 128)]:
+        q, k, v = case(1, hq, hkv, T, D, seed=T)
+        kc, vc, table, lens = paging.build_paged_cache(k, v, page_size=16, shuffle=True, generator=_g(T))
+        out = run(q, kc, vc, table, lens, 16)
+        assert bool(torch.isfinite(out).all())
+        ref = eager.paged_decode_eager(q.double(), kc.double(), vc.double(), table, lens)
+        assert rel_err(out, ref) <= 1e-2
+        assert float((out.double().cpu() - ref).abs().max()) < 0.1
+
+
+def test_paged_config5():
+    """64 sequences, ctx ~ U[512, 16384], Hq 32 / Hkv 8,
+    D 128, page 16, block table a seeded permutation of all pages."""
+    g = _g(5)
+    B, Hq, Hkv, D, P = 64, 32, 8, 128, 16
+    lens = torch.randint(512, 16385, (B,), generator=g)
+    table, n_pages = paging.random_paged_layout(lens.tolist(), P, generator=g)
+    kc = torch.randn(n_pages, Hkv, P, D, generator=g).to(torch.bfloat16)
+    vc = torch.randn(n_pages, Hkv, P, D, generator=g).to(torch.bfloat16)
+    q = torch.randn(B, Hq, 1, D, generator=g).to(torch.bfloat16)
+    out = run(q, kc, vc, table, lens.to(torch.int32), P)
+    sel = [0, 17, 63]
+    ref = eager.paged_decode_eager(q[sel].double(), kc.double(), vc.double(), table[sel], lens[sel])
+    assert rel_err(out[sel], ref) <= 1e-2
+    assert bool(torch.isfinite(out).all())
