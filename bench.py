@@ -155,6 +155,82 @@ def bench_attention(torch, sa, iters):
     }
 
 
+def bench_fp8(torch, iters):
+    """Config 4: fp8 e4m3fn Q/K (per-tensor scales), bf16 V, GQA 32/8, L=8192.
+    Kernel-only timing on pre-quantised inputs (as tests/bench_fp8_kernel.py
+    times the reference), plus the full entry point with device quantisation."""
+    from smooth_attn import kernels
+
+    B, Hq, Hkv, L, D = 2, 32, 8, 8192, 128
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(4)
+    q = torch.randn(B, Hq, L, D, generator=gen, device=dev).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, L, D, generator=gen, device=dev).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, L, D, generator=gen, device=dev).to(torch.bfloat16)
+    q8, qs = kernels._quantize_to_fp8_device(q)
+    k8, ks = kernels._quantize_to_fp8_device(k)
+    scale = 1.0 / math.sqrt(D)
+    fn = lambda: kernels._sp2norm_fp8_flash_fwd(q8, k8, v, qs, ks, None, scale, Hq // Hkv)
+    for _ in range(3):
+        fn()
+    ms = time_events(torch, fn, iters)
+    avg = sum(ms) / len(ms)
+    full = time_events(torch, lambda: __import__("smooth_attn").sp2norm_fp8_flash_attention(
+        q, k, v, quantize_v=False), max(3, iters // 3))
+    qk_flops = 2 * B * Hq * D * tri(L)
+    ideal_us = qk_flops / (FP8_PEAK_TFLOPS * 1e12) * 1e6 + qk_flops / (BF16_PEAK_TFLOPS * 1e12) * 1e6
+    return {
+        "config": "config4 fp8 e4m3fn QK^T + bf16 PV, GQA 32/8, [2,32|8,8192,128]",
+        "us": avg * 1e3,
+        "tflops_total": 2 * qk_flops / (avg * 1e-3) / 1e12,
+        "frac_of_mfma_roofline": ideal_us / (avg * 1e3),
+        "ideal_us": ideal_us,
+        "entry_point_us_incl_quantisation": sum(full) / len(full) * 1e3,
+    }
+
+
+def bench_paged(torch, iters):
+    """Config 5: 64 sequences, ctx ~ U[512, 16384] (seeded), Hq 32 / Hkv 8,
+    D 128, page 16, block table a seeded permutation of all pages."""
+    import smooth_attn as sa
+
+    B, Hq, Hkv, D, P = 64, 32, 8, 128, 16
+    g = torch.Generator().manual_seed(5)
+    lens = torch.randint(512, 16385, (B,), generator=g)
+    # serving-style table: a seeded permutation of all pages, handed out in order
+    npg_seq = [(int(c) + P - 1) // P for c in lens]
+    n_pages = sum(npg_seq)
+    perm = torch.randperm(n_pages, generator=g).to(torch.int32)
+    table = torch.zeros(B, max(npg_seq), dtype=torch.int32)
+    pos = 0
+    for i, n in enumerate(npg_seq):
+        table[i, :n] = perm[pos:pos + n]
+        pos += n
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(5)
+    kc = torch.randn(n_pages, Hkv, P, D, generator=gen, device=dev).to(torch.bfloat16)
+    vc = torch.randn(n_pages, Hkv, P, D, generator=gen, device=dev).to(torch.bfloat16)
+    q = torch.randn(B, Hq, 1, D, generator=gen, device=dev).to(torch.bfloat16)
+    table_d = table.to(dev)
+    lens_d = lens.to(torch.int32).to(dev)
+    fn = lambda: sa.sp2norm_paged_attention(q, kc, vc, table_d, lens_d, block_size=P)
+    for _ in range(3):
+        fn()
+    ms = time_events(torch, fn, iters)
+    avg = sum(ms) / len(ms)
+    tot = int(lens.sum())
+    npg = sum((int(c) + P - 1) // P for c in lens)
+    nbytes = 4096 * tot + 4 * npg + B * Hq * D * 2 * 2 + 4 * B
+    return {
+        "config": "config5 paged decode, 64 seqs ctx~U[512,16384], Hq32/Hkv8, D128, page16",
+        "us": avg * 1e3,
+        "bytes": nbytes,
+        "gbs": nbytes / (avg * 1e-3) / 1e9,
+        "frac_hbm_peak": nbytes / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "sum_ctx": tot,
+    }
+
+
 def cpu_baseline(torch, sample, budget_s=20.0):
     """The reference's eager CPU path (oracle restatement, fp32 torch) on one
     [L, L] matrix of the benchmark input: forward + autograd backward."""
@@ -215,11 +291,17 @@ def main():
     log("bench: causal norm fwd+bwd [4,16,4096,4096] bf16")
     norm = bench_norm(torch, sa, args.steps, args.warmup)
     log(f"bench: norm {norm['ms_per_step']:.3f} ms/step, fwd {norm['fwd_us']:.1f} us, bwd {norm['bwd_us']:.1f} us")
-    attn = None
+    attn = fp8 = paged = None
     if not args.no_extra:
         log("bench: fused attention config 3")
         attn = bench_attention(torch, sa, max(args.steps, 10))
         log(f"bench: attention {attn}")
+        log("bench: fp8 attention config 4")
+        fp8 = bench_fp8(torch, max(args.steps, 10))
+        log(f"bench: fp8 {fp8}")
+        log("bench: paged decode config 5")
+        paged = bench_paged(torch, max(args.steps, 20))
+        log(f"bench: paged {paged}")
     cpu = None
     if not args.no_cpu:
         log("bench: cpu baseline")
@@ -262,6 +344,8 @@ def main():
         },
         "cpu_baseline": cpu,
         "attention": attn,
+        "fp8_attention": fp8,
+        "paged_decode": paged,
     }
     print(json.dumps(line), flush=True)
 

@@ -9,9 +9,11 @@
 // One wavefront per (sequence b, KV head, split of kSplitTok tokens).  The
 // wave walks its split in tiles of 32 tokens and reads every K/V row once
 // for all G query heads that share the KV head (the reference grid
-// (B, Hq) rereads each page G times).  Scores are S^T = K Q^T on MFMA with
-// the G query heads as columns; the squareplus weights land in the B-operand
-// layout of O^T += V^T P^T, and V^T comes from a wave-private row-major LDS
+// (B, Hq) rereads each page G times).  Tiles are fetched with coalesced
+// 16-byte loads (one 1 KB span per instruction) one tile ahead of the
+// compute and staged in wave-private LDS.  Scores are S^T = K Q^T on MFMA
+// with the G query heads as columns; the squareplus weights land in the
+// B-operand layout of O^T += V^T P^T, and V^T comes from the row-major LDS
 // tile through the transposing LDS read (see flash_common.hpp).
 // Each wave writes its unnormalised partial (O, S); a second kernel sums the
 // partials of a sequence in split order (squareplus needs no running
@@ -35,16 +37,23 @@ struct PagedParams {
     float* ws_s;  // [B][Hq][n_splits]
     int64_t qs[4], ks[4], vs[4], os[3];
     int64_t bt_stride;
-    int B, Hq, Hkv, G, P, max_pages, n_pages, n_splits;
+    int B, Hq, Hkv, G, P, logP, max_pages, n_pages, n_splits;
     float scale;
 };
 
-template <typename T, int D>
+// UNIFORM: every load instruction's tokens lie in one page (64 / (D/8)
+// tokens per instruction divide the page size), so the page base is
+// wave-uniform and comes from v_readlane of the split's page-id register.
+template <typename T, int D, bool UNIFORM>
 __global__ __launch_bounds__(64) void paged_partial_kernel(PagedParams p) {
     using Ops = MfmaOps<T>;
     using Vec = typename Ops::vec8;
-    constexpr int RSV = D + 8;
-    __shared__ __attribute__((aligned(16))) T ldsV[kTile * RSV];
+    constexpr int RS = D + 8;              // LDS row stride (elements)
+    constexpr int CPT = D / 8;             // 16-byte chunks per token row
+    constexpr int TPI = 64 / CPT;          // tokens per load instruction
+    constexpr int NC = kTile * CPT / 64;   // chunks per lane per tile and tensor
+    __shared__ __attribute__((aligned(16))) T ldsK[kTile * RS];
+    __shared__ __attribute__((aligned(16))) T ldsV[kTile * RS];
 
     const int lane = threadIdx.x;
     const int hi = lane >> 5;
@@ -58,10 +67,20 @@ __global__ __launch_bounds__(64) void paged_partial_kernel(PagedParams p) {
     const int t_begin = split * kSplitTok;
     if (t_begin >= ctx) return;  // whole wave: nothing in this split
     const int t_end = min(ctx, t_begin + kSplitTok);
+    const int logP = p.logP;
+    const int pmask = p.P - 1;
 
     const T* kc = static_cast<const T*>(p.k) + hk * p.ks[1];
     const T* vc = static_cast<const T*>(p.v) + hk * p.vs[1];
-    const int32_t* table = p.table + b * p.bt_stride;
+
+    // Page ids of this split, one per lane (a split spans <= 64 pages).
+    int page_id;
+    {
+        const int first = t_begin >> logP;
+        const int npg = ((t_end - 1) >> logP) - first + 1;
+        page_id = lane < npg ? min(max(p.table[b * p.bt_stride + first + lane], 0), p.n_pages - 1) : 0;
+    }
+    const int first_page = t_begin >> logP;
 
     // Q^T as the B operand: column = query head hk*G + l32 (zero past G).
     u32x4 qreg[D / 16];
@@ -73,56 +92,72 @@ __global__ __launch_bounds__(64) void paged_partial_kernel(PagedParams p) {
             qreg[dc] = live ? load16(qrow + dc * 16 + hi * 8) : u32x4{0u, 0u, 0u, 0u};
     }
 
+    // Coalesced tile loads: instruction i of lane l fetches 16-byte chunk
+    // c = 64 i + l of the tile (token c / CPT, columns 8 (c % CPT) .. +7).
+    const int lane_tok = lane / CPT;
+    const int lane_col = (lane % CPT) * 8;
+    u32x4 kbuf[NC], vbuf[NC];
+    auto load_tile = [&](int t0) {
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            const int t = t0 + i * TPI + lane_tok;
+            int phys;
+            int64_t koff, voff;
+            if constexpr (UNIFORM) {
+                const int tu = t0 + i * TPI;  // first token of the instruction
+                phys = __builtin_amdgcn_readlane(page_id, (tu >> logP) - first_page);
+                const int r = tu & pmask;
+                koff = phys * p.ks[0] + (r + lane_tok) * p.ks[2];
+                voff = phys * p.vs[0] + (r + lane_tok) * p.vs[2];
+            } else {
+                phys = __shfl(page_id, (t >> logP) - first_page);
+                koff = phys * p.ks[0] + (t & pmask) * p.ks[2];
+                voff = phys * p.vs[0] + (t & pmask) * p.vs[2];
+            }
+            if (t < t_end) {
+                kbuf[i] = load16(kc + koff + lane_col);
+                vbuf[i] = load16(vc + voff + lane_col);
+            } else {
+                kbuf[i] = u32x4{0u, 0u, 0u, 0u};
+                vbuf[i] = u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+    };
+    auto store_tile = [&]() {
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            const int tok = i * TPI + lane_tok;
+            *reinterpret_cast<u32x4*>(ldsK + tok * RS + lane_col) = kbuf[i];
+            *reinterpret_cast<u32x4*>(ldsV + tok * RS + lane_col) = vbuf[i];
+        }
+    };
+
     f32x16 oacc[D / 32];
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) oacc[dt] = f32x16{};
     float ssum = 0.f;
+    const int v_tr_off = ((lane >> 5) * 4 + ((lane & 15) >> 2)) * RS + ((lane >> 4) & 1) * 16 + 4 * (lane & 3);
 
-    const int v_tr_off = ((lane >> 5) * 4 + ((lane & 15) >> 2)) * RSV + ((lane >> 4) & 1) * 16 + 4 * (lane & 3);
-    const int P = p.P;
-
+    load_tile(t_begin);
     for (int t0 = t_begin; t0 < t_end; t0 += kTile) {
-        // K operand rows: token t0 + l32.
-        u32x4 kreg[D / 16];
-        {
-            const int t = t0 + l32;
-            if (t < t_end) {
-                const int phys = min(max(table[t / P], 0), p.n_pages - 1);
-                const T* row = kc + static_cast<int64_t>(phys) * p.ks[0] + (t % P) * p.ks[2];
-#pragma unroll
-                for (int dc = 0; dc < D / 16; ++dc) kreg[dc] = load16(row + dc * 16 + hi * 8);
-            } else {
-#pragma unroll
-                for (int dc = 0; dc < D / 16; ++dc) kreg[dc] = u32x4{0u, 0u, 0u, 0u};
-            }
-        }
-        // V rows: lane covers token t0 + lane/2, half (lane & 1) of the row.
-        {
-            const int tv = lane >> 1;
-            const int part = lane & 1;
-            const int t = t0 + tv;
-            T* dst = ldsV + tv * RSV + part * (D / 2);
-            if (t < t_end) {
-                const int phys = min(max(table[t / P], 0), p.n_pages - 1);
-                const T* row = vc + static_cast<int64_t>(phys) * p.vs[0] + (t % P) * p.vs[2] + part * (D / 2);
-#pragma unroll
-                for (int c = 0; c < D / 16; ++c) *reinterpret_cast<u32x4*>(dst + c * 8) = load16(row + c * 8);
-            } else {
-#pragma unroll
-                for (int c = 0; c < D / 16; ++c) *reinterpret_cast<u32x4*>(dst + c * 8) = u32x4{0u, 0u, 0u, 0u};
-            }
-        }
-        __syncthreads();
+        // The block is one wavefront: LDS accesses of a wave complete in
+        // issue order, so a wave-level scheduling barrier is all the ordering
+        // needed (a workgroup barrier would also drain the prefetch below).
+        store_tile();
+        __builtin_amdgcn_wave_barrier();
+        if (t0 + kTile < t_end) load_tile(t0 + kTile);
 
         f32x16 s = f32x16{};
 #pragma unroll
-        for (int dc = 0; dc < D / 16; ++dc) s = Ops::mma(as_vec8<Vec>(kreg[dc]), as_vec8<Vec>(qreg[dc]), s);
-
+        for (int dc = 0; dc < D / 16; ++dc) {
+            const u32x4 a = *reinterpret_cast<const u32x4*>(ldsK + l32 * RS + dc * 16 + hi * 8);
+            s = Ops::mma(as_vec8<Vec>(a), as_vec8<Vec>(qreg[dc]), s);
+        }
         float y[16];
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
             const int t = t0 + (v >> 2) * 8 + hi * 4 + (v & 3);
-            const float w = sp2_weight<true>(__builtin_fmaf(s[v], p.scale, -0.5f));
+            const float w = sp2_weight<false>(__builtin_fmaf(s[v], p.scale, -0.5f));
             y[v] = t < t_end ? w : 0.f;
             ssum += y[v];
         }
@@ -136,14 +171,14 @@ __global__ __launch_bounds__(64) void paged_partial_kernel(PagedParams p) {
             const Vec bop = as_vec8<Vec>(pw);
 #pragma unroll
             for (int dt = 0; dt < D / 32; ++dt) {
-                const T* base = ldsV + (16 * c) * RSV + dt * 32 + v_tr_off;
+                const T* base = ldsV + (16 * c) * RS + dt * 32 + v_tr_off;
                 const uint2 lo = lds_read_tr16(base);
-                const uint2 hi8 = lds_read_tr16(base + 8 * RSV);
+                const uint2 hi8 = lds_read_tr16(base + 8 * RS);
                 const u32x4 aw{lo.x, lo.y, hi8.x, hi8.y};
                 oacc[dt] = Ops::mma(as_vec8<Vec>(aw), bop, oacc[dt]);
             }
         }
-        __syncthreads();
+        __builtin_amdgcn_wave_barrier();
     }
 
     const float stot = ssum + __shfl_xor(ssum, 32);
@@ -185,7 +220,10 @@ __global__ __launch_bounds__(D) void paged_merge_kernel(PagedParams p) {
 template <typename T, int D>
 int launch_paged(const PagedParams& prm, hipStream_t st) {
     const unsigned units = static_cast<unsigned>(prm.B) * prm.Hkv * prm.n_splits;
-    paged_partial_kernel<T, D><<<units, 64, 0, st>>>(prm);
+    if (prm.P * (D / 8) >= 64)
+        paged_partial_kernel<T, D, true><<<units, 64, 0, st>>>(prm);
+    else
+        paged_partial_kernel<T, D, false><<<units, 64, 0, st>>>(prm);
     paged_merge_kernel<D><<<static_cast<unsigned>(prm.B) * prm.Hq, D, 0, st>>>(prm);
     return status_from_launch();
 }
@@ -252,6 +290,7 @@ extern "C" int sa_paged_decode(const void* q, const void* k_cache, const void* v
     prm.Hkv = Hkv;
     prm.G = Hq / Hkv;
     prm.P = page_size;
+    prm.logP = __builtin_ctz(static_cast<unsigned>(page_size));
     prm.max_pages = max_pages;
     prm.n_pages = n_pages;
     prm.scale = scale;
