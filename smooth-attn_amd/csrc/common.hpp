@@ -83,11 +83,20 @@ __device__ __forceinline__ float elem<f16>(const uint32_t* words, int i) {
     return static_cast<float>(__builtin_bit_cast(f16, h));
 }
 
-// Two floats packed into one 32-bit word of a 16-bit type (RNE), or one float.
+// Two floats packed into one 32-bit word of a 16-bit type (RNE); a
+// two-element vector conversion is a single v_cvt_pk_{bf16,f16}_f32.
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 template <typename T>
-__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<T>(lo))) |
-           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<T>(hi))) << 16);
+__device__ __forceinline__ uint32_t pack2(float lo, float hi);
+template <>
+__device__ __forceinline__ uint32_t pack2<bf16>(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo, hi}), bf16x2));
+}
+template <>
+__device__ __forceinline__ uint32_t pack2<f16>(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo, hi}), f16x2));
 }
 
 // Load 16 bytes into words[0..3] / store words[0..3] as 16 bytes.

@@ -21,12 +21,13 @@
 // Blocks are issued heaviest first (last query blocks first) and, because the
 // block index runs over (batch, head) fastest, every query block of one head
 // lands on the same XCD when B*Hq is a multiple of 8 (shared K/V in L2).
+#include <type_traits>
+
 #include "flash_common.hpp"
 
 namespace sa {
 namespace {
 
-constexpr int kBQ = 128;   // query rows per block
 constexpr int kBKV = 64;   // keys per tile
 constexpr int kThreads = 256;
 
@@ -46,11 +47,14 @@ struct FlashParams {
 
 // T: 16-bit type of P V (and of q/k/v unless fp8).  QK8: q, k are e4m3fn.
 // V8: v is e4m3fn.
+#ifndef SA_FLASH_VPAD
+#define SA_FLASH_VPAD 8
+#endif
 template <typename T, int D, bool QK8, bool V8>
 struct Geom {
     static constexpr int QKB = QK8 ? 1 : 2;         // bytes per q/k element
     static constexpr int RSK = D * QKB + 16;        // K row stride in LDS (bytes)
-    static constexpr int RSV = D + 8;               // V row stride in LDS (elements of T)
+    static constexpr int RSV = D + SA_FLASH_VPAD;   // V row stride in LDS (elements of T)
     static constexpr int KT = kBKV * RSK;           // bytes per K tile
     static constexpr int VT = kBKV * RSV * 2;       // bytes per V tile
     static constexpr int KCPR = D * QKB / 16;       // 16-byte global chunks per K row
@@ -79,18 +83,28 @@ __device__ __forceinline__ void widen_fp8x16(u32x4 in, u32x4& lo, u32x4& hi) {
     hi = u32x4{out[4], out[5], out[6], out[7]};
 }
 
+#ifndef SA_FLASH_QT
+#define SA_FLASH_QT 2
+#endif
+// Query tiles (32 rows each) per wave.  With QT = 2 every K and V^T operand
+// read from LDS feeds two independent MFMAs and every staged K/V tile serves
+// 256 query rows; wave w owns query tiles w and w + 4 of the block, which
+// balances the causal work of the four waves.
+constexpr int kQT = SA_FLASH_QT;
+constexpr int kBQ2 = 32 * 4 * kQT;  // query rows per block
+
 template <typename T, int D, bool QK8, bool V8, bool EXACT>
-__global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FlashParams p) {
+__global__ __launch_bounds__(256, kQT == 1 ? 2 : 1) void flash_fwd_kernel(FlashParams p) {
     using Gm = Geom<T, D, QK8, V8>;
     using Ops = MfmaOps<T>;
     using Vec = typename Ops::vec8;
     __shared__ __attribute__((aligned(16))) unsigned char lds[2 * (Gm::KT + Gm::VT)];
-    unsigned char* ldsK = lds;                 // [2][64][RSK bytes]
+    unsigned char* ldsK = lds;                         // [2][64][RSK bytes]
     T* ldsV = reinterpret_cast<T*>(lds + 2 * Gm::KT);  // [2][64][RSV]
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     const int hi = lane >> 5;  // lane half
     const int l32 = lane & 31;
 
@@ -112,29 +126,38 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FlashParams p) {
     const int64_t krs = p.ks[2] * Gm::QKB;
     const int64_t vrs = p.vs[2] * (V8 ? 1 : 2);
 
-    const int q_start = qb * kBQ;
-    const int wq0 = q_start + wave * 32;
+    const int q_start = qb * kBQ2;
+    int wq0[kQT];  // first query row of each of this wave's tiles
+#pragma unroll
+    for (int qt = 0; qt < kQT; ++qt) wq0[qt] = q_start + 32 * (wave + 4 * qt);
     const int W = p.window;
     const int n_kv = (T_ + kBKV - 1) / kBKV;
-    const int kv_end = min((q_start + kBQ + kBKV - 1) / kBKV, n_kv);
+    const int kv_end = min((q_start + kBQ2 + kBKV - 1) / kBKV, n_kv);
     const int kv_begin = W > 0 ? max(0, q_start - W + 1) / kBKV : 0;
 
+    // Loads are unconditional with row indices clamped to T-1: rows past T
+    // only ever meet masked (zero) weights, and branch-free loads let the
+    // compiler count outstanding memory operations exactly, so the tile
+    // prefetch below is not drained early.
     // Q^T as the B operand.  16-bit: chunk dc holds d = 16 dc + 8 hi .. +7.
     // fp8: chunk dc holds d = 64 dc + 32 hi .. +31 (zero past D).
-    u32x4 qreg[Gm::NQC][QK8 ? 2 : 1];
-    {
-        const int qrow = wq0 + l32;
+    u32x4 qreg[kQT][Gm::NQC][QK8 ? 2 : 1];
+#pragma unroll
+    for (int qt = 0; qt < kQT; ++qt) {
+        const int qrow = min(wq0[qt] + l32, T_ - 1);
 #pragma unroll
         for (int dc = 0; dc < Gm::NQC; ++dc) {
             if constexpr (QK8) {
                 const int d0 = 64 * dc + 32 * hi;
 #pragma unroll
                 for (int w = 0; w < 2; ++w) {
-                    const bool in = qrow < T_ && d0 + 16 * w < D;
-                    qreg[dc][w] = in ? load16(qp + qrow * qrs + d0 + 16 * w) : u32x4{0u, 0u, 0u, 0u};
+                    // columns past D (D = 32) read the row's first 16 bytes and are zeroed
+                    const int col = d0 + 16 * w < D ? d0 + 16 * w : 0;
+                    const u32x4 raw = load16(qp + qrow * qrs + col);
+                    qreg[qt][dc][w] = d0 + 16 * w < D ? raw : u32x4{0u, 0u, 0u, 0u};
                 }
             } else {
-                qreg[dc][0] = qrow < T_ ? load16(qp + qrow * qrs + (dc * 16 + hi * 8) * 2) : u32x4{0u, 0u, 0u, 0u};
+                qreg[qt][dc][0] = load16(qp + qrow * qrs + (dc * 16 + hi * 8) * 2);
             }
         }
     }
@@ -144,10 +167,14 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FlashParams p) {
     if constexpr (QK8) sc *= p.q_scale[0] * p.k_scale[0];
     if constexpr (V8) vsc = p.v_scale[0];
 
-    f32x16 oacc[D / 32];
+    f32x16 oacc[kQT][D / 32];
+    float ssum[kQT];
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) oacc[dt] = f32x16{};
-    float ssum = 0.f;
+    for (int qt = 0; qt < kQT; ++qt) {
+        ssum[qt] = 0.f;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) oacc[qt][dt] = f32x16{};
+    }
 
     // Global -> register staging of one K/V tile.
     u32x4 kst[Gm::KNL], vst[Gm::VNL];
@@ -155,19 +182,17 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FlashParams p) {
         const int k0 = j * kBKV;
 #pragma unroll
         for (int i = 0; i < Gm::KNL; ++i) {
-            const int ci = tid + kThreads * i;
+            const int ci = min(tid + kThreads * i, kBKV * Gm::KCPR - 1);
             const int row = ci / Gm::KCPR;
             const int c = ci - row * Gm::KCPR;
-            const bool in = ci < kBKV * Gm::KCPR && k0 + row < T_;
-            kst[i] = in ? load16(kp + (k0 + row) * krs + c * 16) : u32x4{0u, 0u, 0u, 0u};
+            kst[i] = load16(kp + min(k0 + row, T_ - 1) * krs + c * 16);
         }
 #pragma unroll
         for (int i = 0; i < Gm::VNL; ++i) {
-            const int ci = tid + kThreads * i;
+            const int ci = min(tid + kThreads * i, kBKV * Gm::VCPR - 1);
             const int row = ci / Gm::VCPR;
             const int c = ci - row * Gm::VCPR;
-            const bool in = ci < kBKV * Gm::VCPR && k0 + row < T_;
-            vst[i] = in ? load16(vp + (k0 + row) * vrs + c * 16) : u32x4{0u, 0u, 0u, 0u};
+            vst[i] = load16(vp + min(k0 + row, T_ - 1) * vrs + c * 16);
         }
     };
     auto store_tile = [&](int buf) {
@@ -176,7 +201,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FlashParams p) {
             const int ci = tid + kThreads * i;
             const int row = ci / Gm::KCPR;
             const int c = ci - row * Gm::KCPR;
-            if (ci < kBKV * Gm::KCPR)
+            if ((kBKV * Gm::KCPR) % kThreads == 0 || ci < kBKV * Gm::KCPR)
                 *reinterpret_cast<u32x4*>(ldsK + buf * Gm::KT + row * Gm::RSK + c * 16) = kst[i];
         }
 #pragma unroll
@@ -184,7 +209,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FlashParams p) {
             const int ci = tid + kThreads * i;
             const int row = ci / Gm::VCPR;
             const int c = ci - row * Gm::VCPR;
-            if (ci < kBKV * Gm::VCPR) {
+            if ((kBKV * Gm::VCPR) % kThreads == 0 || ci < kBKV * Gm::VCPR) {
                 T* dst = ldsV + buf * (Gm::VT / 2) + row * Gm::RSV;
                 if constexpr (V8) {
                     u32x4 lo, hi16;
@@ -200,106 +225,152 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(FlashParams p) {
 
     // Per-lane element offset of the transposing V read; see flash_common.hpp.
     const int v_tr_off = ((lane >> 5) * 4 + ((lane & 15) >> 2)) * Gm::RSV + ((lane >> 4) & 1) * 16 + 4 * (lane & 3);
+    const unsigned weff = W > 0 ? static_cast<unsigned>(W) : 0x7FFFFFFFu;
 
-    if (kv_begin < kv_end) {
-        load_tile(kv_begin);
-        store_tile(0);
-    }
-    __syncthreads();
-
-    for (int j = kv_begin; j < kv_end; ++j) {
-        const int buf = (j - kv_begin) & 1;
-        const bool has_next = j + 1 < kv_end;
-        if (has_next) load_tile(j + 1);
-        const int k0 = j * kBKV;
-        const bool active = (k0 <= wq0 + 31) && !(W > 0 && k0 + kBKV - 1 <= wq0 - W);
-        if (active) {
-            const unsigned char* Kb = ldsK + buf * Gm::KT;
-            const T* Vb = ldsV + buf * (Gm::VT / 2);
-            f32x16 s[2];
+    // One K/V tile for all of this wave's query tiles.  EDGE: some tile of
+    // the wave crosses the diagonal or the window edge (per-tile activity
+    // and masks are evaluated); otherwise every query tile is fully inside.
+    auto tile_step = [&](auto edge_tag, int buf, int k0) {
+        constexpr bool EDGE = decltype(edge_tag)::value;
+        bool act[kQT], msk[kQT];
 #pragma unroll
-            for (int kt = 0; kt < 2; ++kt) {
-                s[kt] = f32x16{};
-                const unsigned char* krow = Kb + (kt * 32 + l32) * Gm::RSK;
+        for (int qt = 0; qt < kQT; ++qt) {
+            act[qt] = !EDGE || ((k0 <= wq0[qt] + 31) && !(W > 0 && k0 + kBKV - 1 <= wq0[qt] - W));
+            msk[qt] = EDGE && ((k0 + kBKV - 1 > wq0[qt]) || (W > 0 && k0 <= wq0[qt] + 31 - W));
+        }
+        const unsigned char* Kb = ldsK + buf * Gm::KT;
+        const T* Vb = ldsV + buf * (Gm::VT / 2);
+        // One 32-key half at a time: S^T tiles, weights, then the two P V
+        // chunks of the half.
 #pragma unroll
-                for (int dc = 0; dc < Gm::NQC; ++dc) {
-                    if constexpr (QK8) {
-                        const int d0 = 64 * dc + 32 * hi;
-                        u32x4 a0 = u32x4{0u, 0u, 0u, 0u}, a1 = u32x4{0u, 0u, 0u, 0u};
-                        if (d0 < D) {
-                            a0 = *reinterpret_cast<const u32x4*>(krow + d0);
-                            a1 = *reinterpret_cast<const u32x4*>(krow + d0 + 16);
-                        }
-                        const i32x8 av{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w,
-                                       (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
-                        const i32x8 bv{(int)qreg[dc][0].x, (int)qreg[dc][0].y, (int)qreg[dc][0].z,
-                                       (int)qreg[dc][0].w, (int)qreg[dc][1].x, (int)qreg[dc][1].y,
-                                       (int)qreg[dc][1].z, (int)qreg[dc][1].w};
-                        s[kt] = mma_fp8(av, bv, s[kt]);
-                    } else {
-                        const u32x4 a = *reinterpret_cast<const u32x4*>(krow + (dc * 16 + hi * 8) * 2);
-                        s[kt] = Ops::mma(as_vec8<Vec>(a), as_vec8<Vec>(qreg[dc][0]), s[kt]);
+        for (int kt = 0; kt < 2; ++kt) {
+            f32x16 s[kQT];
+#pragma unroll
+            for (int qt = 0; qt < kQT; ++qt) s[qt] = f32x16{};
+            const unsigned char* krow = Kb + (kt * 32 + l32) * Gm::RSK;
+#pragma unroll
+            for (int dc = 0; dc < Gm::NQC; ++dc) {
+                if constexpr (QK8) {
+                    const int d0 = 64 * dc + 32 * hi;
+                    u32x4 a0 = u32x4{0u, 0u, 0u, 0u}, a1 = u32x4{0u, 0u, 0u, 0u};
+                    if (d0 < D) {
+                        a0 = *reinterpret_cast<const u32x4*>(krow + d0);
+                        a1 = *reinterpret_cast<const u32x4*>(krow + d0 + 16);
+                    }
+                    const i32x8 av{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w,
+                                   (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+#pragma unroll
+                    for (int qt = 0; qt < kQT; ++qt) {
+                        if (!act[qt]) continue;
+                        const i32x8 bv{(int)qreg[qt][dc][0].x, (int)qreg[qt][dc][0].y, (int)qreg[qt][dc][0].z,
+                                       (int)qreg[qt][dc][0].w, (int)qreg[qt][dc][1].x, (int)qreg[qt][dc][1].y,
+                                       (int)qreg[qt][dc][1].z, (int)qreg[qt][dc][1].w};
+                        s[qt] = mma_fp8(av, bv, s[qt]);
+                    }
+                } else {
+                    const u32x4 a = *reinterpret_cast<const u32x4*>(krow + (dc * 16 + hi * 8) * 2);
+#pragma unroll
+                    for (int qt = 0; qt < kQT; ++qt) {
+                        if (!act[qt]) continue;
+                        s[qt] = Ops::mma(as_vec8<Vec>(a), as_vec8<Vec>(qreg[qt][dc][0]), s[qt]);
                     }
                 }
             }
-            const bool edge = (k0 + kBKV - 1 > wq0) || (W > 0 && k0 <= wq0 + 31 - W);
-            const int qi = wq0 + l32;
-            float y[2][16];
+            Vec bop[kQT][2];
 #pragma unroll
-            for (int kt = 0; kt < 2; ++kt) {
+            for (int qt = 0; qt < kQT; ++qt) {
+                if (!act[qt]) continue;
+                // valid(key) <=> 0 <= qi - key < W_eff (W_eff = W, or INT_MAX
+                // for full causal): one unsigned compare per element.
+                const int dbase = wq0[qt] + l32 - k0 - hi * 4;
+                float y[16];
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
-                    float w = sp2_weight<EXACT>(__builtin_fmaf(s[kt][v], sc, -0.5f));
-                    if (edge) {
-                        const int key = k0 + kt * 32 + (v >> 2) * 8 + hi * 4 + (v & 3);
-                        const bool ok = key <= qi && (W <= 0 || qi - key < W);
-                        w = ok ? w : 0.f;
+                    float w = sp2_weight<EXACT>(__builtin_fmaf(s[qt][v], sc, -0.5f));
+                    if (EDGE && msk[qt]) {
+                        const int cv = kt * 32 + (v >> 2) * 8 + (v & 3);
+                        w = static_cast<unsigned>(dbase - cv) < weff ? w : 0.f;
                     }
-                    y[kt][v] = w;
-                    ssum += w;
+                    y[v] = w;
+                    ssum[qt] += w;
+                }
+#pragma unroll
+                for (int ch = 0; ch < 2; ++ch) {
+                    u32x4 pw;
+                    pw.x = pack2<T>(y[8 * ch + 0], y[8 * ch + 1]);
+                    pw.y = pack2<T>(y[8 * ch + 2], y[8 * ch + 3]);
+                    pw.z = pack2<T>(y[8 * ch + 4], y[8 * ch + 5]);
+                    pw.w = pack2<T>(y[8 * ch + 6], y[8 * ch + 7]);
+                    bop[qt][ch] = as_vec8<Vec>(pw);
                 }
             }
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const float* pv = &y[c >> 1][(c & 1) * 8];
-                u32x4 pw;
-                pw.x = pack2<T>(pv[0], pv[1]);
-                pw.y = pack2<T>(pv[2], pv[3]);
-                pw.z = pack2<T>(pv[4], pv[5]);
-                pw.w = pack2<T>(pv[6], pv[7]);
-                const Vec bop = as_vec8<Vec>(pw);
+            for (int ch = 0; ch < 2; ++ch) {
+                const int c = 2 * kt + ch;  // 16-key chunk of the tile
 #pragma unroll
                 for (int dt = 0; dt < D / 32; ++dt) {
                     const T* base = Vb + (16 * c) * Gm::RSV + dt * 32 + v_tr_off;
                     const uint2 lo = lds_read_tr16(base);
                     const uint2 hi8 = lds_read_tr16(base + 8 * Gm::RSV);
                     const u32x4 aw{lo.x, lo.y, hi8.x, hi8.y};
-                    oacc[dt] = Ops::mma(as_vec8<Vec>(aw), bop, oacc[dt]);
+#pragma unroll
+                    for (int qt = 0; qt < kQT; ++qt) {
+                        if (!act[qt]) continue;
+                        oacc[qt][dt] = Ops::mma(as_vec8<Vec>(aw), bop[qt][ch], oacc[qt][dt]);
+                    }
                 }
             }
+        }
+    };
+
+    // kv_begin < kv_end for every block (q_start < T), so the first tile is
+    // always staged.
+    load_tile(kv_begin);
+    store_tile(0);
+    __syncthreads();
+
+    const int wlast = wq0[kQT - 1];  // the wave's latest query tile
+    const int wfirst = wq0[0];
+    for (int j = kv_begin; j < kv_end; ++j) {
+        const int buf = (j - kv_begin) & 1;
+        const bool has_next = j + 1 < kv_end;
+        if (has_next) load_tile(j + 1);
+        const int k0 = j * kBKV;
+        // some query tile of the wave sees this key tile
+        const bool any = (k0 <= wlast + 31) && !(W > 0 && k0 + kBKV - 1 <= wfirst - W);
+        // every query tile fully sees it (no masks, no inactive tile)
+        const bool interior = (k0 + kBKV - 1 <= wfirst) && !(W > 0 && k0 <= wlast + 31 - W);
+        if (any) {
+            if (interior)
+                tile_step(std::false_type{}, buf, k0);
+            else
+                tile_step(std::true_type{}, buf, k0);
         }
         if (has_next) store_tile(buf ^ 1);
         __syncthreads();
     }
 
-    // Row sums: lanes l and l^32 hold the two key halves of one query column.
-    const float stot = ssum + __shfl_xor(ssum, 32) + kEps;
-    const float inv = vsc / stot;
-    const int qi = wq0 + l32;
-    if (qi < T_) {
-        T* orow = op + qi * p.os[2];
 #pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt) {
+    for (int qt = 0; qt < kQT; ++qt) {
+        // Row sums: lanes l and l^32 hold the two key halves of one query column.
+        const float stot = ssum[qt] + __shfl_xor(ssum[qt], 32) + kEps;
+        const float inv = vsc / stot;
+        const int qi = wq0[qt] + l32;
+        if (qi < T_) {
+            T* orow = op + qi * p.os[2];
 #pragma unroll
-            for (int vg = 0; vg < 4; ++vg) {
-                const int d0 = dt * 32 + vg * 8 + hi * 4;
-                uint2 w;
-                w.x = pack2<T>(oacc[dt][vg * 4 + 0] * inv, oacc[dt][vg * 4 + 1] * inv);
-                w.y = pack2<T>(oacc[dt][vg * 4 + 2] * inv, oacc[dt][vg * 4 + 3] * inv);
-                *reinterpret_cast<uint2*>(orow + d0) = w;
+            for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+                for (int vg = 0; vg < 4; ++vg) {
+                    const int d0 = dt * 32 + vg * 8 + hi * 4;
+                    uint2 w;
+                    w.x = pack2<T>(oacc[qt][dt][vg * 4 + 0] * inv, oacc[qt][dt][vg * 4 + 1] * inv);
+                    w.y = pack2<T>(oacc[qt][dt][vg * 4 + 2] * inv, oacc[qt][dt][vg * 4 + 3] * inv);
+                    *reinterpret_cast<uint2*>(orow + d0) = w;
+                }
             }
+            if (hi == 0 && p.row_sums != nullptr) p.row_sums[static_cast<int64_t>(bh) * T_ + qi] = stot;
         }
-        if (hi == 0 && p.row_sums != nullptr) p.row_sums[static_cast<int64_t>(bh) * T_ + qi] = stot;
     }
 }
 
@@ -357,7 +428,7 @@ int fill_params(FlashParams& prm, const void* q, const void* k, const void* v, v
     prm.T = T;
     prm.G = Hq / Hkv;
     prm.window = window_size;
-    prm.nqb = (T + kBQ - 1) / kBQ;
+    prm.nqb = (T + kBQ2 - 1) / kBQ2;
     prm.scale = scale;
     return 0;
 }

@@ -11,7 +11,10 @@ import threading
 from ctypes import POINTER, c_float, c_int, c_int32, c_int64, c_void_p
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "libsmooth_attn_amd.so"
+import os
+
+# SMOOTH_ATTN_LIB selects an alternate build of the same library (tuning runs).
+LIB_PATH = Path(os.environ.get("SMOOTH_ATTN_LIB") or Path(__file__).resolve().parent / "libsmooth_attn_amd.so")
 
 # Element-type codes (SA_F32 ... in the header).
 SA_F32, SA_F16, SA_BF16, SA_FP8_E4M3FN = 0, 1, 2, 3
