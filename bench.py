@@ -34,6 +34,12 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2516.6
 FP8_PEAK_TFLOPS = 5033.2
+# HBM bytes per launch of the causal-norm kernels on this workload, measured
+# with rocprofv3 FETCH_SIZE and WRITE_SIZE passes over this script
+# (--copy-calibration) and scaled by what the same counters read for a plain
+# 1 GiB device copy: FETCH_SIZE x 2.000, WRITE_SIZE x 1.000.  The counter
+# summary and commands are kept under profiles/.
+NORM_TRAFFIC_BYTES = {"fwd": 3.2525e9, "bwd": 4.3557e9}
 METRIC = "causal-norm fwd+bwd HBM GB/s (% peak); fused attn TFLOP/s, L=4096 D=128"
 
 
@@ -267,6 +273,20 @@ def cpu_baseline(torch, sample, budget_s=20.0):
     }
 
 
+def copy_calibration(torch, nbytes=1 << 30):
+    """Three plain device-to-device copies of ``nbytes``: under a counter
+    profiler their FETCH_SIZE / WRITE_SIZE per dispatch give the scale between
+    the counters and bytes moved (each copy reads and writes ``nbytes``)."""
+    src = torch.ones(nbytes // 2, dtype=torch.bfloat16, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"bench: copy calibration, 3 copies of {nbytes} bytes")
+    del src, dst
+    torch.cuda.empty_cache()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -274,6 +294,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run three plain 1 GiB device copies (reference point for HBM counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the smooth-attn hot path has no multi-GPU component "
@@ -288,6 +310,8 @@ def main():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(1)
 
+    if args.copy_calibration:
+        copy_calibration(torch)
     log("bench: causal norm fwd+bwd [4,16,4096,4096] bf16")
     norm = bench_norm(torch, sa, args.steps, args.warmup)
     log(f"bench: norm {norm['ms_per_step']:.3f} ms/step, fwd {norm['fwd_us']:.1f} us, bwd {norm['bwd_us']:.1f} us")
@@ -340,7 +364,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": NORM_TRAFFIC_BYTES[dominant],
         },
         "cpu_baseline": cpu,
         "attention": attn,
