@@ -221,6 +221,50 @@ def flash_attention_grads(q, k, v, do, *, scale=None, window_size=0):
     return qr.grad, kr.grad, vr.grad
 
 
+def flash_attention_bwd(q, k, v, o, do, *, scale=None, window_size=0):
+    """(dq, dk, dv) by the reference backward's own formula, given the
+    forward output ``o`` — kernels.py:1667-1784 (dQ; delta = rowsum(dO * O)
+    from the stored O, :1722-1727) and :1787-1909 (dK, dV summed over the
+    GQA group):
+        R = sum_j y_ij + EPS, P = y / R, dP = dO V^T,
+        dS = (dP - delta) / R * 4 sp sp' scale,  sp' = (1 + a / sqrt(a^2 + 4)) / 2,
+        dQ = dS K, dK = dS^T Q, dV = P^T dO.
+    Work dtype float64 for float64 inputs.  With ``o`` taken from a forward
+    that rounded P (the fused kernels do), delta carries that rounding, as it
+    does in the reference; this matters where the true gradient vanishes
+    (one visible key: dQ = dK = 0 up to that rounding).
+
+    pinned by: equals flash_attention_grads (autograd) when ``o`` is the
+    exact eager output, causal / window / GQA (tests/test_oracle.py).
+    """
+    wd = _work_dtype(q)
+    B, Hq, T, D = q.shape
+    Hkv = k.shape[1]
+    G = Hq // Hkv
+    sc = scale if scale is not None else 1.0 / math.sqrt(D)
+    qf, kf, vf, of, dof = (t.detach().to(wd) for t in (q, k, v, o, do))
+    ke = _expand_kv(kf, Hq)
+    ve = _expand_kv(vf, Hq)
+    cm = causal_mask(T)
+    if window_size > 0:
+        pos = torch.arange(T)
+        cm = cm | ((pos[:, None] - pos[None, :]) >= window_size)
+    s = torch.matmul(qf, ke.transpose(-2, -1)) * sc
+    a = 2.0 * s - 1.0
+    r4 = torch.sqrt(a * a + 4.0)
+    sp = 0.5 * (a + r4)
+    y = (sp * sp).masked_fill(cm, 0.0)
+    R = y.sum(-1, keepdim=True) + EPS
+    P = y / R
+    dP = torch.matmul(dof, ve.transpose(-2, -1))
+    delta = (dof * of).sum(-1, keepdim=True)
+    dS = ((dP - delta) / R * 4.0 * sp * (0.5 * (1.0 + a / r4)) * sc).masked_fill(cm, 0.0)
+    dq = torch.matmul(dS, ke)
+    dk = torch.matmul(dS.transpose(-2, -1), qf).view(B, Hkv, G, T, D).sum(2)
+    dv = torch.matmul(P.transpose(-2, -1), dof).view(B, Hkv, G, T, D).sum(2)
+    return dq, dk, dv
+
+
 def quantize_to_fp8(x: torch.Tensor):
     """Per-tensor absmax e4m3fn quantiser — kernels.py:2592-2601.
 

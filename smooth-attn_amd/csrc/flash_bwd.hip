@@ -1,0 +1,539 @@
+// Fused causal squareplus attention backward on gfx950 MFMA (bf16 / fp16).
+//
+// With s = q_i . k_j (raw dot product), a = scale s - 1/2, r = sqrt(a^2 + 1),
+// y = (a + r)^2 (= squareplus(2 scale s - 1)^2), R_i = sum_j y_ij + 1e-12 (the
+// forward's row sums), P = y / R and O = P V:
+//   dP_ij    = dO_i . V_j
+//   delta_i  = dO_i . O_i                      (= sum_j P_ij dP_ij)
+//   dS_ij    = (dP_ij - delta_i) / R_i * dy/ds = 2 scale (dP_ij - delta_i) y_ij / (r_ij R_i)
+//   dQ_i = sum_j dS_ij K_j,  dK_j = sum_i dS_ij Q_i,  dV_j = sum_i P_ij dO_i
+// (reference kernels.py:1667-1784 dQ + delta, :1787-1909 dK/dV; the
+// reference writes dy/ds as 4 sp sp' scale with sp' = (1 + arg/sqrt(arg^2+4))/2,
+// arg = 2a, which equals 2 scale y / r).  P and dS are rounded to the 16-bit
+// type before their products, as the reference does.
+//
+// Two kernels, as in the reference:
+//  * flash_bwd_dq_kernel: a block of 4 waves owns 128 query rows of one
+//    (batch, query head).  Each wave keeps Q and dO of its 32 rows in
+//    registers (B operands), computes delta for them (written to the
+//    workspace), and walks the key tiles: S^T = K Q^T and dP^T = V dO^T on
+//    MFMA with K, V from LDS, dS^T on the VALU, then dQ^T += K^T dS^T with
+//    K^T read from the same LDS tile by the transposing LDS load.
+//  * flash_bwd_dkdv_kernel: a block of 4 waves owns 128 key rows of one
+//    (batch, KV head); wave w owns keys [32w, 32w+32) and keeps K, V of them
+//    in registers.  It walks every query head of the GQA group and every
+//    query tile of 64 rows that sees its keys: S = Q K^T and dP = dO V^T with
+//    Q, dO from LDS, P and dS on the VALU (their C layout is the B operand of
+//    the next products), then dV^T += dO^T P and dK^T += Q^T dS with dO^T,
+//    Q^T from the transposing LDS load.
+// Tiles are staged global -> registers -> LDS, double buffered with one
+// barrier per tile, as in the forward.
+#include "flash_common.hpp"
+
+namespace sa {
+namespace {
+
+constexpr int kBwdThreads = 256;
+constexpr int kBwdBQ = 128;   // query rows per dQ block (32 per wave)
+constexpr int kBwdKT = 64;    // keys per staged tile in the dQ kernel
+constexpr int kBwdBK = 128;   // key rows per dK/dV block (32 per wave)
+constexpr int kBwdQT = 64;    // query rows per staged tile in the dK/dV kernel
+
+struct BwdParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    const void* o;
+    const void* dout;
+    const float* rs;  // [B, Hq, T] row sums of the forward (contiguous)
+    void* dq;
+    void* dk;
+    void* dv;
+    float* delta;  // [B, Hq, T] workspace (contiguous)
+    int64_t qs[4], ks[4], vs[4], os[4], dos[4], dqs[4], dks[4], dvs[4];
+    int B, Hq, Hkv, T, G, window;
+    float scale;
+};
+
+// Plain (cached) 16-byte global load: tiles here are re-read by many blocks.
+__device__ __forceinline__ u32x4 ldg16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+// Per-lane element offset of the transposing read of a row-major [rows][RS]
+// tile as the A operand (rows of the tile become the MFMA k index, in the
+// order the C -> B operand reuse produces; see flash_common.hpp).
+template <int RS>
+__device__ __forceinline__ int tr_offset(int lane) {
+    return ((lane >> 5) * 4 + ((lane & 15) >> 2)) * RS + ((lane >> 4) & 1) * 16 + 4 * (lane & 3);
+}
+
+// A operand = (16 rows x 32 columns of a row-major tile)^T via two transposing reads.
+template <typename Vec, int RS, typename T>
+__device__ __forceinline__ Vec tr_operand(const T* base) {
+    const uint2 lo = lds_read_tr16(base);
+    const uint2 hi = lds_read_tr16(base + 8 * RS);
+    return as_vec8<Vec>(u32x4{lo.x, lo.y, hi.x, hi.y});
+}
+
+template <bool EXACT>
+__device__ __forceinline__ void weight_and_rr(float s, float sc, float& y, float& rr) {
+    const float a = __builtin_fmaf(s, sc, -0.5f);
+    const float u = __builtin_fmaf(a, a, 1.f);
+    rr = fast_rsqrt(u);
+    const float r = EXACT ? __builtin_sqrtf(u) : u * rr;
+    const float sp = a + r;
+    y = sp * sp;
+}
+
+// ---------------------------------------------------------------------------
+// dQ (and delta)
+// ---------------------------------------------------------------------------
+template <typename T, int D, bool EXACT>
+__global__ __launch_bounds__(kBwdThreads) void flash_bwd_dq_kernel(BwdParams p) {
+    using Ops = MfmaOps<T>;
+    using Vec = typename Ops::vec8;
+    constexpr int RS = D + 8;            // LDS row stride (elements)
+    constexpr int TILE = kBwdKT * RS;    // elements per staged tile
+    constexpr int CPR = D / 8;           // 16-byte chunks per row
+    constexpr int NL = kBwdKT * CPR / kBwdThreads;  // chunks per thread per tile
+    static_assert(NL >= 1 && (kBwdKT * CPR) % kBwdThreads == 0, "tile must split evenly");
+    __shared__ __attribute__((aligned(16))) T lds[2][2][TILE];  // [buf][K, V]
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int hi = lane >> 5;
+    const int l32 = lane & 31;
+
+    const int nqb = (p.T + kBwdBQ - 1) / kBwdBQ;
+    const int BH = p.B * p.Hq;
+    const int id = blockIdx.x;
+    const int qb = nqb - 1 - id / BH;  // heaviest (latest) query blocks first
+    const int bh = id % BH;
+    const int b = bh / p.Hq;
+    const int hq = bh - b * p.Hq;
+    const int hk = hq / p.G;
+    const int T_ = p.T;
+
+    const T* qp = static_cast<const T*>(p.q) + b * p.qs[0] + hq * p.qs[1];
+    const T* kp = static_cast<const T*>(p.k) + b * p.ks[0] + hk * p.ks[1];
+    const T* vp = static_cast<const T*>(p.v) + b * p.vs[0] + hk * p.vs[1];
+    const T* op = static_cast<const T*>(p.o) + b * p.os[0] + hq * p.os[1];
+    const T* dop = static_cast<const T*>(p.dout) + b * p.dos[0] + hq * p.dos[1];
+    T* dqp = static_cast<T*>(p.dq) + b * p.dqs[0] + hq * p.dqs[1];
+
+    const int q_start = qb * kBwdBQ;
+    const int wq0 = q_start + 32 * wave;
+    const int qi = wq0 + l32;
+    const int qrow = min(qi, T_ - 1);
+
+    // Q and dO rows as B operands (chunk dc: d = 16 dc + 8 hi .. +7); delta
+    // from the matching chunks of O (lanes l and l ^ 32 hold the two halves).
+    u32x4 qreg[D / 16], doreg[D / 16];
+    float dpart = 0.f;
+#pragma unroll
+    for (int dc = 0; dc < D / 16; ++dc) {
+        const int d0 = dc * 16 + hi * 8;
+        qreg[dc] = ldg16(qp + qrow * p.qs[2] + d0);
+        doreg[dc] = ldg16(dop + qrow * p.dos[2] + d0);
+        const u32x4 ov = ldg16(op + qrow * p.os[2] + d0);
+        const uint32_t dw[4] = {doreg[dc].x, doreg[dc].y, doreg[dc].z, doreg[dc].w};
+        const uint32_t ow[4] = {ov.x, ov.y, ov.z, ov.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dpart = __builtin_fmaf(elem<T>(dw, e), elem<T>(ow, e), dpart);
+    }
+    const float dl = dpart + __shfl_xor(dpart, 32);
+    const int64_t rbase = static_cast<int64_t>(bh) * T_;
+    if (qi < T_ && hi == 0) p.delta[rbase + qi] = dl;
+    const float inv_r = 1.f / p.rs[rbase + qrow];
+
+    f32x16 acc[D / 32];
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) acc[dt] = f32x16{};
+
+    const int W = p.window;
+    const unsigned weff = W > 0 ? static_cast<unsigned>(W) : 0x7FFFFFFFu;
+    const int n_kv = (T_ + kBwdKT - 1) / kBwdKT;
+    const int kv_end = min((q_start + kBwdBQ + kBwdKT - 1) / kBwdKT, n_kv);
+    const int kv_begin = W > 0 ? max(0, q_start - W + 1) / kBwdKT : 0;
+    const float sc = p.scale;
+
+    u32x4 kst[NL], vst[NL];
+    auto load_tile = [&](int j) {
+        const int k0 = j * kBwdKT;
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            const int ci = tid + kBwdThreads * i;
+            const int row = ci / CPR;
+            const int c = ci - row * CPR;
+            const int gr = min(k0 + row, T_ - 1);
+            kst[i] = ldg16(kp + gr * p.ks[2] + c * 8);
+            vst[i] = ldg16(vp + gr * p.vs[2] + c * 8);
+        }
+    };
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            const int ci = tid + kBwdThreads * i;
+            const int row = ci / CPR;
+            const int c = ci - row * CPR;
+            *reinterpret_cast<u32x4*>(&lds[buf][0][row * RS + c * 8]) = kst[i];
+            *reinterpret_cast<u32x4*>(&lds[buf][1][row * RS + c * 8]) = vst[i];
+        }
+    };
+
+    const int troff = tr_offset<RS>(lane);
+    load_tile(kv_begin);
+    store_tile(0);
+    __syncthreads();
+    for (int j = kv_begin; j < kv_end; ++j) {
+        const int buf = (j - kv_begin) & 1;
+        const bool has_next = j + 1 < kv_end;
+        if (has_next) load_tile(j + 1);
+        const int k0 = j * kBwdKT;
+        const T* Kb = lds[buf][0];
+        const T* Vb = lds[buf][1];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            const int kh0 = k0 + kt * 32;
+            // the wave's rows see some key of this half
+            const bool act = (kh0 <= wq0 + 31) && !(W > 0 && kh0 + 31 <= wq0 - W);
+            if (!act) continue;
+            f32x16 s = f32x16{}, dp = f32x16{};
+            const T* krow = Kb + (kt * 32 + l32) * RS + hi * 8;
+            const T* vrow = Vb + (kt * 32 + l32) * RS + hi * 8;
+#pragma unroll
+            for (int dc = 0; dc < D / 16; ++dc) {
+                const u32x4 ka = *reinterpret_cast<const u32x4*>(krow + dc * 16);
+                const u32x4 va = *reinterpret_cast<const u32x4*>(vrow + dc * 16);
+                s = Ops::mma(as_vec8<Vec>(ka), as_vec8<Vec>(qreg[dc]), s);
+                dp = Ops::mma(as_vec8<Vec>(va), as_vec8<Vec>(doreg[dc]), dp);
+            }
+            // C layout: column = query l32, rows = keys kh0 + (v/4)*8 + 4 hi + v%4.
+            const int dbase = qi - kh0 - hi * 4;
+            float ds[16];
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                float y, rr;
+                weight_and_rr<EXACT>(s[v], sc, y, rr);
+                const int cv = (v >> 2) * 8 + (v & 3);
+                const float g = (dp[v] - dl) * y * rr;
+                ds[v] = static_cast<unsigned>(dbase - cv) < weff ? g : 0.f;
+            }
+#pragma unroll
+            for (int ch = 0; ch < 2; ++ch) {
+                u32x4 pw;
+                pw.x = pack2<T>(ds[8 * ch + 0], ds[8 * ch + 1]);
+                pw.y = pack2<T>(ds[8 * ch + 2], ds[8 * ch + 3]);
+                pw.z = pack2<T>(ds[8 * ch + 4], ds[8 * ch + 5]);
+                pw.w = pack2<T>(ds[8 * ch + 6], ds[8 * ch + 7]);
+                const Vec bop = as_vec8<Vec>(pw);
+                const int c = 2 * kt + ch;  // 16-key chunk of the tile
+#pragma unroll
+                for (int dt = 0; dt < D / 32; ++dt)
+                    acc[dt] = Ops::mma(tr_operand<Vec, RS>(Kb + 16 * c * RS + dt * 32 + troff), bop, acc[dt]);
+            }
+        }
+        if (has_next) store_tile(buf ^ 1);
+        __syncthreads();
+    }
+
+    // dS was kept without its per-row factor 2 scale / R_i (applied here).
+    if (qi < T_) {
+        const float f = 2.f * sc * inv_r;
+        T* row = dqp + qi * p.dqs[2];
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+            for (int vg = 0; vg < 4; ++vg) {
+                const int d0 = dt * 32 + vg * 8 + hi * 4;
+                uint2 w;
+                w.x = pack2<T>(acc[dt][vg * 4 + 0] * f, acc[dt][vg * 4 + 1] * f);
+                w.y = pack2<T>(acc[dt][vg * 4 + 2] * f, acc[dt][vg * 4 + 3] * f);
+                *reinterpret_cast<uint2*>(row + d0) = w;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// dK, dV
+// ---------------------------------------------------------------------------
+template <typename T, int D, bool EXACT>
+__global__ __launch_bounds__(kBwdThreads) void flash_bwd_dkdv_kernel(BwdParams p) {
+    using Ops = MfmaOps<T>;
+    using Vec = typename Ops::vec8;
+    constexpr int RS = D + 8;
+    constexpr int TILE = kBwdQT * RS;
+    constexpr int CPR = D / 8;
+    constexpr int NL = kBwdQT * CPR / kBwdThreads;
+    static_assert(NL >= 1 && (kBwdQT * CPR) % kBwdThreads == 0, "tile must split evenly");
+    __shared__ __attribute__((aligned(16))) T lds[2][2][TILE];         // [buf][Q, dO]
+    __shared__ __attribute__((aligned(16))) float ldr[2][2][kBwdQT];   // [buf][1/R, delta]
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int hi = lane >> 5;
+    const int l32 = lane & 31;
+
+    const int BHk = p.B * p.Hkv;
+    const int id = blockIdx.x;
+    const int kb = id / BHk;  // earliest key blocks see the most queries: first
+    const int bhk = id % BHk;
+    const int b = bhk / p.Hkv;
+    const int hk = bhk - b * p.Hkv;
+    const int T_ = p.T;
+
+    const T* kp = static_cast<const T*>(p.k) + b * p.ks[0] + hk * p.ks[1];
+    const T* vp = static_cast<const T*>(p.v) + b * p.vs[0] + hk * p.vs[1];
+    T* dkp = static_cast<T*>(p.dk) + b * p.dks[0] + hk * p.dks[1];
+    T* dvp = static_cast<T*>(p.dv) + b * p.dvs[0] + hk * p.dvs[1];
+
+    const int k_start = kb * kBwdBK;
+    const int wk0 = k_start + 32 * wave;
+    const int kj = wk0 + l32;
+    const int krow = min(kj, T_ - 1);
+
+    // K and V rows of the wave as B operands (column = key l32).
+    u32x4 kreg[D / 16], vreg[D / 16];
+#pragma unroll
+    for (int dc = 0; dc < D / 16; ++dc) {
+        kreg[dc] = ldg16(kp + krow * p.ks[2] + dc * 16 + hi * 8);
+        vreg[dc] = ldg16(vp + krow * p.vs[2] + dc * 16 + hi * 8);
+    }
+
+    f32x16 dkacc[D / 32], dvacc[D / 32];
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+        dkacc[dt] = f32x16{};
+        dvacc[dt] = f32x16{};
+    }
+
+    const int W = p.window;
+    const unsigned weff = W > 0 ? static_cast<unsigned>(W) : 0x7FFFFFFFu;
+    const int n_qt = (T_ + kBwdQT - 1) / kBwdQT;
+    const int qt_begin = k_start / kBwdQT;
+    const int qt_end = W > 0 ? min(n_qt, (k_start + kBwdBK - 1 + W - 1) / kBwdQT + 1) : n_qt;
+    const int nq = qt_end - qt_begin;  // >= 1 (k_start < T)
+    const int n_it = p.G * nq;
+    const float sc = p.scale;
+
+    u32x4 qst[NL], dst[NL];
+    float rst = 0.f;
+    auto load_tile = [&](int it) {
+        const int g = it / nq;
+        const int qt = qt_begin + (it - g * nq);
+        const int hq = hk * p.G + g;
+        const T* qp = static_cast<const T*>(p.q) + b * p.qs[0] + hq * p.qs[1];
+        const T* dop = static_cast<const T*>(p.dout) + b * p.dos[0] + hq * p.dos[1];
+        const int q0 = qt * kBwdQT;
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            const int ci = tid + kBwdThreads * i;
+            const int row = ci / CPR;
+            const int c = ci - row * CPR;
+            const int gr = min(q0 + row, T_ - 1);
+            qst[i] = ldg16(qp + gr * p.qs[2] + c * 8);
+            dst[i] = ldg16(dop + gr * p.dos[2] + c * 8);
+        }
+        if (tid < 2 * kBwdQT) {
+            const int r = tid & (kBwdQT - 1);
+            const int64_t idx = (static_cast<int64_t>(b) * p.Hq + hq) * T_ + min(q0 + r, T_ - 1);
+            rst = tid < kBwdQT ? 1.f / p.rs[idx] : p.delta[idx];
+        }
+    };
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            const int ci = tid + kBwdThreads * i;
+            const int row = ci / CPR;
+            const int c = ci - row * CPR;
+            *reinterpret_cast<u32x4*>(&lds[buf][0][row * RS + c * 8]) = qst[i];
+            *reinterpret_cast<u32x4*>(&lds[buf][1][row * RS + c * 8]) = dst[i];
+        }
+        if (tid < 2 * kBwdQT) ldr[buf][tid / kBwdQT][tid & (kBwdQT - 1)] = rst;
+    };
+
+    const int troff = tr_offset<RS>(lane);
+    load_tile(0);
+    store_tile(0);
+    __syncthreads();
+    for (int it = 0; it < n_it; ++it) {
+        const int buf = it & 1;
+        const bool has_next = it + 1 < n_it;
+        if (has_next) load_tile(it + 1);
+        const int g = it / nq;
+        const int q0 = (qt_begin + (it - g * nq)) * kBwdQT;
+        const T* Qb = lds[buf][0];
+        const T* Ob = lds[buf][1];
+#pragma unroll
+        for (int qh = 0; qh < 2; ++qh) {
+            const int qh0 = q0 + qh * 32;
+            // some query of this half sees some key of the wave
+            const bool act = (qh0 + 31 >= wk0) && !(W > 0 && qh0 - (wk0 + 31) >= W) && qh0 < T_;
+            if (!act) continue;
+            f32x16 s = f32x16{}, dp = f32x16{};
+            const T* qrow = Qb + (qh * 32 + l32) * RS + hi * 8;
+            const T* orow = Ob + (qh * 32 + l32) * RS + hi * 8;
+#pragma unroll
+            for (int dc = 0; dc < D / 16; ++dc) {
+                const u32x4 qa = *reinterpret_cast<const u32x4*>(qrow + dc * 16);
+                const u32x4 oa = *reinterpret_cast<const u32x4*>(orow + dc * 16);
+                s = Ops::mma(as_vec8<Vec>(qa), as_vec8<Vec>(kreg[dc]), s);
+                dp = Ops::mma(as_vec8<Vec>(oa), as_vec8<Vec>(vreg[dc]), dp);
+            }
+            // C layout: column = key kj, rows = queries qh0 + (v/4)*8 + 4 hi + v%4.
+            float pv[16], ds[16];
+            const int dbase = qh0 + hi * 4 - kj;
+            const int qlim = T_ - (qh0 + hi * 4);  // row offsets below this are real queries
+#pragma unroll
+            for (int vg = 0; vg < 4; ++vg) {
+                const int roff = qh * 32 + vg * 8 + hi * 4;
+                const float4 ir = *reinterpret_cast<const float4*>(&ldr[buf][0][roff]);
+                const float4 dl = *reinterpret_cast<const float4*>(&ldr[buf][1][roff]);
+                const float irv[4] = {ir.x, ir.y, ir.z, ir.w};
+                const float dlv[4] = {dl.x, dl.y, dl.z, dl.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int v = vg * 4 + e;
+                    float y, rr;
+                    weight_and_rr<EXACT>(s[v], sc, y, rr);
+                    const int cv = vg * 8 + e;
+                    const bool ok = (static_cast<unsigned>(dbase + cv) < weff) && (cv < qlim);
+                    const float yi = y * irv[e];
+                    pv[v] = ok ? yi : 0.f;
+                    ds[v] = ok ? (dp[v] - dlv[e]) * yi * rr : 0.f;
+                }
+            }
+#pragma unroll
+            for (int ch = 0; ch < 2; ++ch) {
+                u32x4 pw, sw;
+                pw.x = pack2<T>(pv[8 * ch + 0], pv[8 * ch + 1]);
+                pw.y = pack2<T>(pv[8 * ch + 2], pv[8 * ch + 3]);
+                pw.z = pack2<T>(pv[8 * ch + 4], pv[8 * ch + 5]);
+                pw.w = pack2<T>(pv[8 * ch + 6], pv[8 * ch + 7]);
+                sw.x = pack2<T>(ds[8 * ch + 0], ds[8 * ch + 1]);
+                sw.y = pack2<T>(ds[8 * ch + 2], ds[8 * ch + 3]);
+                sw.z = pack2<T>(ds[8 * ch + 4], ds[8 * ch + 5]);
+                sw.w = pack2<T>(ds[8 * ch + 6], ds[8 * ch + 7]);
+                const Vec bp = as_vec8<Vec>(pw);
+                const Vec bs = as_vec8<Vec>(sw);
+                const int c = 2 * qh + ch;  // 16-query chunk of the tile
+#pragma unroll
+                for (int dt = 0; dt < D / 32; ++dt) {
+                    dvacc[dt] = Ops::mma(tr_operand<Vec, RS>(Ob + 16 * c * RS + dt * 32 + troff), bp, dvacc[dt]);
+                    dkacc[dt] = Ops::mma(tr_operand<Vec, RS>(Qb + 16 * c * RS + dt * 32 + troff), bs, dkacc[dt]);
+                }
+            }
+        }
+        if (has_next) store_tile(buf ^ 1);
+        __syncthreads();
+    }
+
+    // dS was kept without its factor 2 scale (1/R_i is already in).
+    if (kj < T_) {
+        const float f = 2.f * sc;
+        T* krw = dkp + kj * p.dks[2];
+        T* vrw = dvp + kj * p.dvs[2];
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+            for (int vg = 0; vg < 4; ++vg) {
+                const int d0 = dt * 32 + vg * 8 + hi * 4;
+                uint2 wk, wv;
+                wk.x = pack2<T>(dkacc[dt][vg * 4 + 0] * f, dkacc[dt][vg * 4 + 1] * f);
+                wk.y = pack2<T>(dkacc[dt][vg * 4 + 2] * f, dkacc[dt][vg * 4 + 3] * f);
+                wv.x = pack2<T>(dvacc[dt][vg * 4 + 0], dvacc[dt][vg * 4 + 1]);
+                wv.y = pack2<T>(dvacc[dt][vg * 4 + 2], dvacc[dt][vg * 4 + 3]);
+                *reinterpret_cast<uint2*>(krw + d0) = wk;
+                *reinterpret_cast<uint2*>(vrw + d0) = wv;
+            }
+        }
+    }
+}
+
+template <typename T, int D>
+int launch_bwd(const BwdParams& prm, int exact, hipStream_t st) {
+    const unsigned nqb = static_cast<unsigned>((prm.T + kBwdBQ - 1) / kBwdBQ);
+    const unsigned nkb = static_cast<unsigned>((prm.T + kBwdBK - 1) / kBwdBK);
+    const dim3 gq(nqb * prm.B * prm.Hq), gk(nkb * prm.B * prm.Hkv), blk(kBwdThreads);
+    if (exact) {
+        flash_bwd_dq_kernel<T, D, true><<<gq, blk, 0, st>>>(prm);
+        flash_bwd_dkdv_kernel<T, D, true><<<gk, blk, 0, st>>>(prm);
+    } else {
+        flash_bwd_dq_kernel<T, D, false><<<gq, blk, 0, st>>>(prm);
+        flash_bwd_dkdv_kernel<T, D, false><<<gk, blk, 0, st>>>(prm);
+    }
+    return status_from_launch();
+}
+
+template <typename T>
+int launch_bwd_d(const BwdParams& prm, int D, int exact, hipStream_t st) {
+    switch (D) {
+        case 32: return launch_bwd<T, 32>(prm, exact, st);
+        case 64: return launch_bwd<T, 64>(prm, exact, st);
+        case 128: return launch_bwd<T, 128>(prm, exact, st);
+        default: return SA_ERR_UNSUPPORTED;
+    }
+}
+
+// (b, h, t) strides keep every row 16-byte aligned; d stride 1.
+bool bwd_strides_ok(const int64_t* s) { return s[3] == 1 && s[0] % 8 == 0 && s[1] % 8 == 0 && s[2] % 8 == 0; }
+
+}  // namespace
+}  // namespace sa
+
+extern "C" int sa_flash_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                            const float* row_sums, void* dq, void* dk, void* dv, float* delta_ws, int B, int Hq,
+                            int Hkv, int T, int D, const int64_t* q_strides, const int64_t* k_strides,
+                            const int64_t* v_strides, const int64_t* o_strides, const int64_t* do_strides,
+                            const int64_t* dq_strides, const int64_t* dk_strides, const int64_t* dv_strides,
+                            float scale, int window_size, int exact_math, int dtype, sa_stream_t stream) {
+    using namespace sa;
+    if (dtype != SA_BF16 && dtype != SA_F16) return SA_ERR_BAD_DTYPE;
+    if (B < 0 || Hq <= 0 || Hkv <= 0 || T < 0 || Hq % Hkv != 0 || window_size < 0) return SA_ERR_BAD_SHAPE;
+    if (!q || !k || !v || !o || !dout || !row_sums || !dq || !dk || !dv || !delta_ws) return SA_ERR_NULL_POINTER;
+    if (!q_strides || !k_strides || !v_strides || !o_strides || !do_strides || !dq_strides || !dk_strides ||
+        !dv_strides)
+        return SA_ERR_NULL_POINTER;
+    if (D != 32 && D != 64 && D != 128) return SA_ERR_UNSUPPORTED;
+    const int64_t* all[8] = {q_strides, k_strides, v_strides, o_strides, do_strides, dq_strides, dk_strides, dv_strides};
+    for (const int64_t* s : all)
+        if (!bwd_strides_ok(s)) return SA_ERR_BAD_STRIDE;
+    const void* ptrs[8] = {q, k, v, o, dout, dq, dk, dv};
+    for (const void* ptr : ptrs)
+        if (!aligned16(ptr)) return SA_ERR_BAD_STRIDE;
+    if (B == 0 || T == 0) return 0;
+    BwdParams prm{};
+    prm.q = q;
+    prm.k = k;
+    prm.v = v;
+    prm.o = o;
+    prm.dout = dout;
+    prm.rs = row_sums;
+    prm.dq = dq;
+    prm.dk = dk;
+    prm.dv = dv;
+    prm.delta = delta_ws;
+    for (int i = 0; i < 4; ++i) {
+        prm.qs[i] = q_strides[i];
+        prm.ks[i] = k_strides[i];
+        prm.vs[i] = v_strides[i];
+        prm.os[i] = o_strides[i];
+        prm.dos[i] = do_strides[i];
+        prm.dqs[i] = dq_strides[i];
+        prm.dks[i] = dk_strides[i];
+        prm.dvs[i] = dv_strides[i];
+    }
+    prm.B = B;
+    prm.Hq = Hq;
+    prm.Hkv = Hkv;
+    prm.T = T;
+    prm.G = Hq / Hkv;
+    prm.window = window_size;
+    prm.scale = scale;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const int ex = exact_math ? 1 : 0;
+    if (dtype == SA_BF16) return launch_bwd_d<bf16>(prm, D, ex, s);
+    return launch_bwd_d<f16>(prm, D, ex, s);
+}

@@ -421,7 +421,7 @@ def _flash_operand(t):
     with a unit stride along D and a 16-byte aligned base; anything else is
     copied to a contiguous tensor first."""
     ok = t.stride(-1) == 1 and all(s % 8 == 0 for s in t.stride()[:-1]) and t.data_ptr() % 16 == 0
-    return t if ok else t.contiguous()
+    return t if ok else t.clone(memory_format=torch.contiguous_format)
 
 
 def _sp2norm_flash_fwd(q, k, v, scale, n_kv_groups=1, window_size=0, use_fast_sqrt=True):
@@ -456,7 +456,7 @@ def _sp2norm_flash_bwd(q, k, v, o, do, row_sums, scale, n_kv_groups=1, window_si
     B, H_q, T, D = q.shape
     H_kv = k.shape[1]
     q, k, v, o = _flash_operand(q), _flash_operand(k), _flash_operand(v), _flash_operand(o)
-    do = do if (do.dtype == q.dtype and do.stride(-1) == 1) else do.to(q.dtype).contiguous()
+    do = _flash_operand(do.to(q.dtype))
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)

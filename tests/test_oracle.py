@@ -197,6 +197,36 @@ def test_attention_grads_vs_finite_differences():
     np.testing.assert_allclose(dv.numpy(), fd_v, rtol=1e-5, atol=1e-8)
 
 
+@pytest.mark.parametrize("hq,hkv,window,T", [(2, 2, 0, 1), (2, 2, 0, 37), (4, 2, 5, 37), (6, 2, 1, 20),
+                                             (3, 1, 64, 50)])
+def test_backward_formula_vs_autograd(hq, hkv, window, T):
+    # the reference's backward formula given the exact forward output equals
+    # autograd of the eager attention
+    q = torch.randn(2, hq, T, 8, generator=_g(40 + T), dtype=DTYPE)
+    k = torch.randn(2, hkv, T, 8, generator=_g(41 + T), dtype=DTYPE)
+    v = torch.randn(2, hkv, T, 8, generator=_g(42 + T), dtype=DTYPE)
+    do = torch.randn(2, hq, T, 8, generator=_g(43 + T), dtype=DTYPE)
+    o = eager.flash_attention_eager(q, k, v, window_size=window)
+    got = eager.flash_attention_bwd(q, k, v, o, do, window_size=window)
+    ref = eager.flash_attention_grads(q, k, v, do, window_size=window)
+    for g_, r_ in zip(got, ref):
+        torch.testing.assert_close(g_, r_, rtol=1e-10, atol=1e-12)
+
+
+def test_backward_formula_single_key_rows():
+    # one visible key per row (window 1): dQ = dK = 0 and dV = dO exactly when
+    # o is exact; a perturbed o moves only dQ / dK, through delta
+    q, k, v, do = (torch.randn(1, 2, 9, 4, generator=_g(50 + i), dtype=DTYPE) for i in range(4))
+    o = eager.flash_attention_eager(q, k, v, window_size=1)
+    dq, dk, dv = eager.flash_attention_bwd(q, k, v, o, do, window_size=1)
+    # (nonzero only through EPS: dP - delta = dP * EPS / (y + EPS))
+    assert float(dq.abs().max()) < 1e-9 and float(dk.abs().max()) < 1e-9
+    torch.testing.assert_close(dv, do, rtol=1e-9, atol=1e-9)
+    dq2, _, dv2 = eager.flash_attention_bwd(q, k, v, o * (1 + 2 ** -9), do, window_size=1)
+    assert float(dq2.abs().max()) > 1e-6
+    torch.testing.assert_close(dv2, dv, rtol=0, atol=0)
+
+
 # ---------------------------------------------------------------------------
 # fp8 quantiser
 # ---------------------------------------------------------------------------
