@@ -152,12 +152,28 @@ def bench_attention(torch, sa, iters):
     ms = time_events(torch, lambda: kernels._sp2norm_flash_fwd(q, k, v, scale), iters)
     avg = sum(ms) / len(ms)
     flops = attn_flops(B, H, L, D)
+    # Backward (dQ + delta kernel, then dK/dV kernel) on the forward's o and
+    # row sums with a seeded upstream gradient.  FLOPs counted as 2.5 x the
+    # forward's (the usual convention: dQ, dK, dV, dP and one S product); the
+    # two-kernel scheme executes 3.5 x (S and dP are recomputed in both).
+    do = torch.randn(B, H, L, D, generator=gen, device=dev).to(torch.bfloat16)
+    o, rs = kernels._sp2norm_flash_fwd(q, k, v, scale)
+    bwd = lambda: kernels._sp2norm_flash_bwd(q, k, v, o, do, rs, scale)
+    for _ in range(2):
+        bwd()
+    bms = time_events(torch, bwd, iters)
+    bavg = sum(bms) / len(bms)
+    bflops = 2.5 * flops
     return {
         "config": "config3 fused causal attention fwd bf16 [4,32,4096,128]",
         "us": avg * 1e3,
         "tflops": flops / (avg * 1e-3) / 1e12,
         "frac_bf16_peak": flops / (avg * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
         "flops": flops,
+        "bwd_us": bavg * 1e3,
+        "bwd_tflops": bflops / (bavg * 1e-3) / 1e12,
+        "bwd_frac_bf16_peak": bflops / (bavg * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+        "bwd_flops": bflops,
     }
 
 

@@ -153,6 +153,37 @@ int sa_flash_fp8_fwd(const void* q8, const void* k8, const void* v, void* o,
                      int window_size, int v_dtype, sa_stream_t stream);
 
 /*
+ * Bytes of workspace sa_flash_rope_fwd needs (the rotated K, contiguous
+ * [B, Hkv, T, D] of the 16-bit type).  -1 for negative sizes.
+ */
+int64_t sa_flash_rope_workspace_size(int B, int Hkv, int T, int D);
+
+/*
+ * Fused attention forward with rotate-half RoPE on Q and K (V unrotated).
+ *   cos_table, sin_table: fp32 contiguous [T, D/2], 16-byte aligned
+ *     (precompute_rope_cos_sin); position t of every (b, h) row uses row t.
+ *   k_rot_ws: workspace of sa_flash_rope_workspace_size() bytes; receives the
+ *     rotated K (rotated once per row there; Q is rotated in registers).
+ * Rotation in fp32, a' = a cos - b sin, b' = b cos + a sin for the pair
+ * (d, d + D/2), rounded to the 16-bit type; everything else as sa_flash_fwd
+ * (exact_math off).  dtype: SA_BF16 or SA_F16 (the reference rounds rotated
+ * values to bf16 whatever the input type).
+ * Replaces sp2norm_rope_flash_attention (kernels.py:2373-2426) and its kernel
+ * _sp2norm_rope_flash_fwd_kernel (:2104-2224).  The RoPE + W_o variant
+ * (kernels.py:2429-2487) is this entry point writing O in [B, T, Hq, D]
+ * order (o_strides) followed by one library GEMM O[B*T, Hq*D] x
+ * W_o[Hq*D, D_model] with fp32 accumulation, in place of the reference's
+ * per-head bf16 atomic adds.
+ */
+int sa_flash_rope_fwd(const void* q, const void* k, const void* v,
+                      const float* cos_table, const float* sin_table, void* o,
+                      float* row_sums, void* k_rot_ws, int64_t ws_bytes, int B,
+                      int Hq, int Hkv, int T, int D, const int64_t* q_strides,
+                      const int64_t* k_strides, const int64_t* v_strides,
+                      const int64_t* o_strides, float scale, int window_size,
+                      int dtype, sa_stream_t stream);
+
+/*
  * Bytes of fp32 workspace sa_paged_decode needs for these sizes.
  */
 int64_t sa_paged_decode_workspace_size(int B, int Hq, int D, int max_pages,

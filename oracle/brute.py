@@ -139,3 +139,21 @@ def e4m3fn_round(x: float) -> int:
         else:  # tie: even mantissa
             code = int(grid[i - 1, 0]) if int(grid[i - 1, 0]) % 2 == 0 else int(grid[i, 0])
     return sign | code
+
+
+def rope(x: np.ndarray, base: float = 10000.0) -> np.ndarray:
+    """Rotate-half RoPE of x [..., T, D] as a complex rotation: the pair
+    (x[d], x[d + D/2]) is z = x[d] + i x[d + D/2], multiplied by
+    exp(i t base^(-2d/D)) at position t (float64)."""
+    x = np.asarray(x, dtype=np.float64)
+    T, D = x.shape[-2], x.shape[-1]
+    h = D // 2
+    out = np.empty_like(x)
+    for idx in np.ndindex(x.shape[:-2]):
+        for t in range(T):
+            for d in range(h):
+                ang = t * base ** (-2.0 * d / D)
+                z = complex(x[idx + (t, d)], x[idx + (t, d + h)]) * complex(math.cos(ang), math.sin(ang))
+                out[idx + (t, d)] = z.real
+                out[idx + (t, d + h)] = z.imag
+    return out

@@ -265,6 +265,68 @@ def flash_attention_bwd(q, k, v, o, do, *, scale=None, window_size=0):
     return dq, dk, dv
 
 
+def rope_cos_sin(dim, seq_len, base=10000.0, dtype=torch.float32):
+    """cos / sin tables [seq_len, dim/2] — kernels.py:2093-2101 (fp32 math,
+    as the reference).
+
+    pinned by: cos(t * base^(-2i/dim)) / sin(...) evaluated in float64.
+    """
+    inv_freq = 1.0 / (base ** (torch.arange(0, dim, 2).float() / dim))
+    t = torch.arange(seq_len, dtype=torch.float32)
+    freqs = torch.outer(t, inv_freq)
+    return freqs.cos().to(dtype), freqs.sin().to(dtype)
+
+
+def apply_rope(x, cos, sin):
+    """Rotate-half RoPE over the last dim, position = index along dim -2 —
+    the reference test's ``apply_rope_eager`` (tests/test_rope_proj.py:15-30):
+    x * [cos, cos] + [-x2, x1] * [sin, sin].
+
+    pinned by: complex multiplication (x_a + i x_b) e^{i theta} (brute.rope);
+    identity at position 0; pairwise norms preserved; dot products of rotated
+    vectors depend only on the position difference.
+    """
+    T, D = x.shape[-2], x.shape[-1]
+    c = cos[:T].to(x.dtype)
+    s = sin[:T].to(x.dtype)
+    cf = torch.cat([c, c], dim=-1)
+    sf = torch.cat([s, s], dim=-1)
+    x1 = x[..., : D // 2]
+    x2 = x[..., D // 2:]
+    return x * cf + torch.cat([-x2, x1], dim=-1) * sf
+
+
+def rope_flash_attention_eager(q, k, v, cos, sin, *, scale=None, window_size=0, round_to=torch.bfloat16):
+    """The reference test's oracle for the RoPE forward
+    (tests/test_rope_proj.py:46-63): rotate q and k in fp32, round them to
+    ``round_to`` (None keeps them), then eager attention in the work dtype.
+
+    pinned by: apply_rope and flash_attention_eager (each pinned).
+    """
+    wd = _work_dtype(q)
+    qr = apply_rope(q.to(wd), cos.to(wd), sin.to(wd))
+    kr = apply_rope(k.to(wd), cos.to(wd), sin.to(wd))
+    if round_to is not None:
+        qr = qr.to(round_to).to(wd)
+        kr = kr.to(round_to).to(wd)
+    return flash_attention_eager(qr, kr, v.to(wd), scale=scale, window_size=window_size)
+
+
+def rope_proj_eager(q, k, v, w_o, cos, sin, *, scale=None, window_size=0, round_to=torch.bfloat16):
+    """RoPE attention then sum_h O_h W_o[h] -> [B, T, D_model] — the
+    reference test's projection oracle (tests/test_rope_proj.py:117-146).
+
+    pinned by: equals one matmul of O in [B, T, H*D] order with W_o
+    reshaped to [H*D, D_model].
+    """
+    o = rope_flash_attention_eager(q, k, v, cos, sin, scale=scale, window_size=window_size, round_to=round_to)
+    B, H, T, D = o.shape
+    out = torch.zeros(B, T, w_o.shape[2], dtype=o.dtype)
+    for h in range(H):
+        out += o[:, h] @ w_o[h].to(o.dtype)
+    return out
+
+
 def quantize_to_fp8(x: torch.Tensor):
     """Per-tensor absmax e4m3fn quantiser — kernels.py:2592-2601.
 

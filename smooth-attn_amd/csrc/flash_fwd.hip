@@ -40,6 +40,8 @@ struct FlashParams {
     const float* q_scale;  // fp8 only (device scalars)
     const float* k_scale;
     const float* v_scale;
+    const float* rope_cos;  // RoPE tables [T, D/2] fp32 (RoPE variant only)
+    const float* rope_sin;
     int64_t qs[4], ks[4], vs[4], os[4];
     int B, Hq, Hkv, T, G, window, nqb;
     float scale;
@@ -83,6 +85,58 @@ __device__ __forceinline__ void widen_fp8x16(u32x4 in, u32x4& lo, u32x4& hi) {
     hi = u32x4{out[4], out[5], out[6], out[7]};
 }
 
+// Rotate-half RoPE of one pair of 8-element chunks, a = x[d .. d+7] and
+// b = x[d + D/2 .. +7] with d < D/2 (reference kernels.py:2150-2158):
+//   a' = a cos - b sin,  b' = b cos + a sin   (fp32, rounded to T).
+template <typename T>
+__device__ __forceinline__ void rope_rotate8(u32x4& a, u32x4& b, const float* cs, const float* sn) {
+    const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
+    const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
+    float ra[8], rb[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float av = elem<T>(aw, e), bv = elem<T>(bw, e);
+        ra[e] = av * cs[e] - bv * sn[e];
+        rb[e] = bv * cs[e] + av * sn[e];
+    }
+    a = u32x4{pack2<T>(ra[0], ra[1]), pack2<T>(ra[2], ra[3]), pack2<T>(ra[4], ra[5]), pack2<T>(ra[6], ra[7])};
+    b = u32x4{pack2<T>(rb[0], rb[1]), pack2<T>(rb[2], rb[3]), pack2<T>(rb[4], rb[5]), pack2<T>(rb[6], rb[7])};
+}
+
+// Rotates every row of K once into a contiguous [B, Hkv, T, D] buffer for the
+// RoPE forward (each K tile is re-read by every query block of its head, so
+// rotating K once beats rotating it in each block).  One thread per pair of
+// 16-byte chunks (d, d + D/2).
+template <typename T, int D>
+__global__ __launch_bounds__(256) void rope_rotate_rows(const T* __restrict__ k, T* __restrict__ out,
+                                                        const float* __restrict__ cs, const float* __restrict__ sn,
+                                                        int Hkv, int T_, int64_t s0, int64_t s1, int64_t s2,
+                                                        int64_t n_pairs) {
+    constexpr int PPR = D / 16;  // chunk pairs per row
+    const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (gid >= n_pairs) return;
+    const int64_t row = gid / PPR;
+    const int c = static_cast<int>(gid - row * PPR);
+    const int64_t bh = row / T_;
+    const int t = static_cast<int>(row - bh * T_);
+    const int b = static_cast<int>(bh / Hkv);
+    const int h = static_cast<int>(bh - static_cast<int64_t>(b) * Hkv);
+    const T* src = k + b * s0 + h * s1 + t * s2 + c * 8;
+    u32x4 a = load16(src);
+    u32x4 bb = load16(src + D / 2);
+    float cv[8], sv[8];
+    const float* cr = cs + static_cast<int64_t>(t) * (D / 2) + c * 8;
+    const float* sr = sn + static_cast<int64_t>(t) * (D / 2) + c * 8;
+    *reinterpret_cast<float4*>(cv) = *reinterpret_cast<const float4*>(cr);
+    *reinterpret_cast<float4*>(cv + 4) = *reinterpret_cast<const float4*>(cr + 4);
+    *reinterpret_cast<float4*>(sv) = *reinterpret_cast<const float4*>(sr);
+    *reinterpret_cast<float4*>(sv + 4) = *reinterpret_cast<const float4*>(sr + 4);
+    rope_rotate8<T>(a, bb, cv, sv);
+    T* dst = out + row * D + c * 8;
+    *reinterpret_cast<u32x4*>(dst) = a;
+    *reinterpret_cast<u32x4*>(dst + D / 2) = bb;
+}
+
 #ifndef SA_FLASH_QT
 #define SA_FLASH_QT 2
 #endif
@@ -93,7 +147,7 @@ __device__ __forceinline__ void widen_fp8x16(u32x4 in, u32x4& lo, u32x4& hi) {
 constexpr int kQT = SA_FLASH_QT;
 constexpr int kBQ2 = 32 * 4 * kQT;  // query rows per block
 
-template <typename T, int D, bool QK8, bool V8, bool EXACT>
+template <typename T, int D, bool QK8, bool V8, bool EXACT, bool ROPE>
 __global__ __launch_bounds__(256, kQT == 1 ? 2 : 1) void flash_fwd_kernel(FlashParams p) {
     using Gm = Geom<T, D, QK8, V8>;
     using Ops = MfmaOps<T>;
@@ -158,6 +212,23 @@ __global__ __launch_bounds__(256, kQT == 1 ? 2 : 1) void flash_fwd_kernel(FlashP
                 }
             } else {
                 qreg[qt][dc][0] = load16(qp + qrow * qrs + (dc * 16 + hi * 8) * 2);
+            }
+        }
+        if constexpr (ROPE && !QK8) {
+            // Rotate-half RoPE in registers: chunk dc (d < D/2) pairs with
+            // chunk dc + D/32 (d + D/2) of the same lane; both use the table
+            // entries [qrow][d], and the result is rounded to T.
+#pragma unroll
+            for (int dc = 0; dc < D / 32; ++dc) {
+                const int d0 = dc * 16 + hi * 8;
+                const float* cr = p.rope_cos + static_cast<int64_t>(qrow) * (D / 2) + d0;
+                const float* sr = p.rope_sin + static_cast<int64_t>(qrow) * (D / 2) + d0;
+                float cs[8], sn[8];
+                *reinterpret_cast<float4*>(cs) = *reinterpret_cast<const float4*>(cr);
+                *reinterpret_cast<float4*>(cs + 4) = *reinterpret_cast<const float4*>(cr + 4);
+                *reinterpret_cast<float4*>(sn) = *reinterpret_cast<const float4*>(sr);
+                *reinterpret_cast<float4*>(sn + 4) = *reinterpret_cast<const float4*>(sr + 4);
+                rope_rotate8<T>(qreg[qt][dc][0], qreg[qt][dc + D / 32][0], cs, sn);
             }
         }
     }
@@ -379,9 +450,29 @@ int launch_flash(const FlashParams& prm, int exact, hipStream_t st) {
     const dim3 grid(static_cast<unsigned>(prm.nqb) * prm.B * prm.Hq);
     const dim3 block(kThreads);
     if (exact)
-        flash_fwd_kernel<T, D, QK8, V8, true><<<grid, block, 0, st>>>(prm);
+        flash_fwd_kernel<T, D, QK8, V8, true, false><<<grid, block, 0, st>>>(prm);
     else
-        flash_fwd_kernel<T, D, QK8, V8, false><<<grid, block, 0, st>>>(prm);
+        flash_fwd_kernel<T, D, QK8, V8, false, false><<<grid, block, 0, st>>>(prm);
+    return status_from_launch();
+}
+
+// RoPE forward: K rotated into k_rot (contiguous [B, Hkv, T, D]), then the
+// forward with Q rotated in registers.
+template <typename T, int D>
+int launch_rope(FlashParams prm, T* k_rot, hipStream_t st) {
+    const int64_t n_pairs = static_cast<int64_t>(prm.B) * prm.Hkv * prm.T * (D / 16);
+    const dim3 rgrid(static_cast<unsigned>((n_pairs + 255) / 256));
+    rope_rotate_rows<T, D><<<rgrid, 256, 0, st>>>(static_cast<const T*>(prm.k), k_rot, prm.rope_cos, prm.rope_sin,
+                                                  prm.Hkv, prm.T, prm.ks[0], prm.ks[1], prm.ks[2], n_pairs);
+    int stt = status_from_launch();
+    if (stt != 0) return stt;
+    prm.k = k_rot;
+    prm.ks[0] = static_cast<int64_t>(prm.Hkv) * prm.T * D;
+    prm.ks[1] = static_cast<int64_t>(prm.T) * D;
+    prm.ks[2] = D;
+    prm.ks[3] = 1;
+    const dim3 grid(static_cast<unsigned>(prm.nqb) * prm.B * prm.Hq);
+    flash_fwd_kernel<T, D, false, false, false, true><<<grid, dim3(kThreads), 0, st>>>(prm);
     return status_from_launch();
 }
 
@@ -473,4 +564,39 @@ extern "C" int sa_flash_fp8_fwd(const void* q8, const void* k8, const void* v, v
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     if (v8) return launch_flash_d<bf16, true, true>(prm, D, 0, s);
     return launch_flash_d<bf16, true, false>(prm, D, 0, s);
+}
+
+extern "C" int64_t sa_flash_rope_workspace_size(int B, int Hkv, int T, int D) {
+    if (B < 0 || Hkv < 0 || T < 0 || D < 0) return -1;
+    return static_cast<int64_t>(B) * Hkv * T * D * 2;
+}
+
+extern "C" int sa_flash_rope_fwd(const void* q, const void* k, const void* v, const float* cos_table,
+                                 const float* sin_table, void* o, float* row_sums, void* k_rot_ws,
+                                 int64_t ws_bytes, int B, int Hq, int Hkv, int T, int D,
+                                 const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                                 const int64_t* o_strides, float scale, int window_size, int dtype,
+                                 sa_stream_t stream) {
+    using namespace sa;
+    if (dtype != SA_BF16 && dtype != SA_F16) return SA_ERR_BAD_DTYPE;
+    if (!cos_table || !sin_table || !k_rot_ws) return SA_ERR_NULL_POINTER;
+    FlashParams prm{};
+    const int st = fill_params(prm, q, k, v, o, row_sums, B, Hq, Hkv, T, D, q_strides, k_strides, v_strides,
+                               o_strides, scale, window_size, 2, 2);
+    if (st != 0) return st;
+    if (B == 0 || T == 0) return 0;
+    if (ws_bytes < sa_flash_rope_workspace_size(B, Hkv, T, D)) return SA_ERR_WORKSPACE;
+    if (!aligned16(cos_table) || !aligned16(sin_table) || !aligned16(k_rot_ws)) return SA_ERR_BAD_STRIDE;
+    prm.rope_cos = cos_table;
+    prm.rope_sin = sin_table;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    switch (D) {
+        case 32: return dtype == SA_BF16 ? launch_rope<bf16, 32>(prm, static_cast<bf16*>(k_rot_ws), s)
+                                         : launch_rope<f16, 32>(prm, static_cast<f16*>(k_rot_ws), s);
+        case 64: return dtype == SA_BF16 ? launch_rope<bf16, 64>(prm, static_cast<bf16*>(k_rot_ws), s)
+                                         : launch_rope<f16, 64>(prm, static_cast<f16*>(k_rot_ws), s);
+        case 128: return dtype == SA_BF16 ? launch_rope<bf16, 128>(prm, static_cast<bf16*>(k_rot_ws), s)
+                                          : launch_rope<f16, 128>(prm, static_cast<f16*>(k_rot_ws), s);
+        default: return SA_ERR_UNSUPPORTED;
+    }
 }

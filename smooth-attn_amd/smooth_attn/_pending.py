@@ -1,7 +1,6 @@
 """Exports of the reference outside the measured hot path that have no gfx950
 implementation yet: the softmax comparison kernels and benchmark CLI
-(reference kernels.py:534-562, 852-884, 1233-1325, 2832-3132) and the RoPE /
-W_o-fused attention forwards (kernels.py:2093-2490).  They are importable so
+(reference kernels.py:534-562, 852-884, 1233-1325, 2832-3132).  They are importable so
 that ``from smooth_attn import *`` keeps working, and raise when called."""
 from __future__ import annotations
 
@@ -21,6 +20,3 @@ softmax_causal_triton_out = _missing("softmax_causal_triton_out")
 benchmark_rowwise_suite = _missing("benchmark_rowwise_suite")
 benchmark_causal_suite = _missing("benchmark_causal_suite")
 main = _missing("main")
-precompute_rope_cos_sin = _missing("precompute_rope_cos_sin")
-sp2norm_rope_flash_attention = _missing("sp2norm_rope_flash_attention")
-sp2norm_rope_flash_attention_proj = _missing("sp2norm_rope_flash_attention_proj")

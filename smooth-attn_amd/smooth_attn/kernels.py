@@ -511,6 +511,96 @@ def sp2norm_flash_attention(q, k, v, *, scale=None, window_size=0, exact_math=Fa
 
 
 # ---------------------------------------------------------------------------
+# RoPE-fused attention forwards.
+# ---------------------------------------------------------------------------
+def precompute_rope_cos_sin(dim, seq_len, base=10000.0, device="cuda", dtype=torch.float32):
+    """cos / sin tables [seq_len, dim/2] of rotate-half RoPE — kernels.py:2093-2101."""
+    inv_freq = 1.0 / (base ** (torch.arange(0, dim, 2, device=device).float() / dim))
+    t = torch.arange(seq_len, device=device, dtype=torch.float32)
+    freqs = torch.outer(t, inv_freq)
+    return freqs.cos().to(dtype), freqs.sin().to(dtype)
+
+
+def _rope_tables(cos, sin, T, D):
+    """fp32 contiguous, 16-byte aligned tables for the kernel."""
+    def fix(t):
+        t = t.to(torch.float32)
+        ok = t.is_contiguous() and t.data_ptr() % 16 == 0
+        return t if ok else t.clone(memory_format=torch.contiguous_format)
+    return fix(cos), fix(sin)
+
+
+def _sp2norm_rope_flash_fwd(q, k, v, cos, sin, scale, n_kv_groups=1, window_size=0, o=None):
+    """(o, row_sums) of the RoPE forward; ``o`` may be a caller view (e.g. of a
+    [B, T, Hq, D] buffer) with 16-byte aligned rows."""
+    B, H_q, T, D = q.shape
+    H_kv = k.shape[1]
+    if q.dtype not in (torch.bfloat16, torch.float16) or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError(f"RoPE attention expects bf16 or fp16 q/k/v of one dtype, got "
+                         f"{q.dtype}/{k.dtype}/{v.dtype}")
+    if D not in _FLASH_HEAD_DIMS:
+        raise ValueError(f"fused attention supports head dims {_FLASH_HEAD_DIMS}, got {D}")
+    q, k, v = _flash_operand(q), _flash_operand(k), _flash_operand(v)
+    cos, sin = _rope_tables(cos, sin, T, D)
+    if o is None:
+        o = torch.empty_like(q)
+    row_sums = torch.empty(B, H_q, T, device=q.device, dtype=torch.float32)
+    lib = _lib.load()
+    ws = torch.empty(max(int(lib.sa_flash_rope_workspace_size(B, H_kv, T, D)), 16), dtype=torch.uint8,
+                     device=q.device)
+    with torch.cuda.device(q.device):
+        st = lib.sa_flash_rope_fwd(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), cos.data_ptr(), sin.data_ptr(), o.data_ptr(),
+            row_sums.data_ptr(), ws.data_ptr(), ws.numel(), B, H_q, H_kv, T, D, _lib.strides(q), _lib.strides(k),
+            _lib.strides(v), _lib.strides(o), float(scale), int(window_size), _DTYPE_CODE[q.dtype], _stream(q),
+        )
+    _lib.check(st, "sa_flash_rope_fwd")
+    return o, row_sums
+
+
+def sp2norm_rope_flash_attention(q, k, v, cos, sin, *, scale=None, window_size=0):
+    """Fused rotate-half RoPE + squareplus attention forward — kernels.py:2373-2426.
+
+    q, k are un-rotated; cos / sin are [T, D/2] tables
+    (precompute_rope_cos_sin).  Q is rotated in registers, K once into a
+    workspace; rotated values are rounded to the input type (the reference
+    rounds them to bf16 for any input type)."""
+    assert q.ndim == 4 and k.ndim == 4 and v.ndim == 4
+    B, H_q, T, D = q.shape
+    H_kv = k.shape[1]
+    assert H_q % H_kv == 0
+    assert D % 2 == 0
+    assert cos.shape == (T, D // 2) and sin.shape == (T, D // 2)
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    o, _ = _sp2norm_rope_flash_fwd(q, k, v, cos, sin, scale, H_q // H_kv, window_size)
+    return o
+
+
+def sp2norm_rope_flash_attention_proj(q, k, v, w_o, cos, sin, *, scale=None, window_size=0):
+    """RoPE attention followed by the output projection, [B, T, D_model] —
+    kernels.py:2429-2487.
+
+    The attention writes O straight into [B, T, Hq, D] order; the projection
+    is then one GEMM O[B*T, Hq*D] x W_o[Hq*D, D_model] with fp32
+    accumulation over every head (deterministic), where the reference adds
+    per-head bf16 products with atomics."""
+    assert q.ndim == 4 and k.ndim == 4 and v.ndim == 4
+    B, H_q, T, D = q.shape
+    H_kv = k.shape[1]
+    assert H_q % H_kv == 0
+    assert D % 2 == 0
+    assert w_o.shape[0] == H_q and w_o.shape[1] == D
+    D_model = w_o.shape[2]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    o_bthd = torch.empty(B, T, H_q, D, device=q.device, dtype=q.dtype)
+    _sp2norm_rope_flash_fwd(q, k, v, cos, sin, scale, H_q // H_kv, window_size, o=o_bthd.transpose(1, 2))
+    w = w_o.to(q.dtype).reshape(H_q * D, D_model)
+    return torch.matmul(o_bthd.view(B * T, H_q * D), w).view(B, T, D_model)
+
+
+# ---------------------------------------------------------------------------
 # fp8 fused attention.
 # ---------------------------------------------------------------------------
 FP8_MAX = 448.0

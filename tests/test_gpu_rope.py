@@ -1,0 +1,117 @@
+"""Parity of the RoPE-fused attention forwards (HIP) with the CPU oracle (GPU).
+
+Oracle: the reference test's own construction (tests/test_rope_proj.py:46-146)
+restated in oracle.eager — rotate q, k in fp32, round to the input type,
+eager attention (and the per-head projection sum) in float64.  Tolerances:
+max|HIP - oracle| / max|oracle| <= 1e-2 for the attention output, <= 2e-2
+for the projected output (O is rounded to 16 bits before the projection, as
+in the reference); fp32 row sums <= 1e-5; plus the reference tests' absolute
+bounds (max error < 0.05 attention, < 0.1 projection).
+"""
+import math
+
+import pytest
+import torch
+
+import smooth_attn
+from oracle import eager
+from smooth_attn import kernels
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _g(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def rel_err(got, ref):
+    got = got.detach().double().cpu()
+    ref = ref.detach().double().cpu()
+    return float((got - ref).abs().max() / ref.abs().max().clamp(min=1e-30))
+
+
+def inputs(B, Hq, Hkv, T, D, dtype, seed, layout="bhtd"):
+    g = _g(seed)
+    if layout == "bthd":
+        q, k, v = (torch.randn(B, T, H, D, generator=g).to(dtype).transpose(1, 2) for H in (Hq, Hkv, Hkv))
+    else:
+        q, k, v = (torch.randn(B, H, T, D, generator=g).to(dtype) for H in (Hq, Hkv, Hkv))
+    return q, k, v
+
+
+def check_rope(q, k, v, window=0, tol=1e-2):
+    T, D = q.shape[2], q.shape[3]
+    cos, sin = smooth_attn.precompute_rope_cos_sin(D, T, device=DEV)
+    out = smooth_attn.sp2norm_rope_flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), cos, sin, window_size=window)
+    ref = eager.rope_flash_attention_eager(q.double(), k.double(), v.double(), cos.cpu(), sin.cpu(),
+                                           window_size=window, round_to=q.dtype)
+    assert out.shape == q.shape and out.dtype == q.dtype
+    assert not out.isnan().any()
+    assert rel_err(out, ref) <= tol
+    assert float((out.float().cpu() - ref.float()).abs().max()) < 0.05  # tests/test_rope_proj.py:69
+    return out
+
+
+@pytest.mark.parametrize("B,H,T,D", [(1, 4, 64, 32), (2, 4, 128, 32), (2, 8, 256, 64), (1, 2, 200, 128),
+                                     (1, 2, 1, 64), (1, 2, 100, 128)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_rope_forward_matches_oracle(B, H, T, D, dtype):
+    # tests/test_rope_proj.py:46-70 shapes, plus D=128, ragged T and T=1
+    check_rope(*inputs(B, H, H, T, D, dtype, seed=T + D + B))
+
+
+def test_rope_forward_gqa():
+    # tests/test_rope_proj.py:73-95
+    check_rope(*inputs(2, 8, 2, 128, 32, torch.bfloat16, seed=21))
+
+
+@pytest.mark.parametrize("window", [1, 64])
+def test_rope_forward_window(window):
+    # tests/test_rope_proj.py:98-114
+    check_rope(*inputs(2, 4, 4, 128, 32, torch.bfloat16, seed=22 + window), window=window)
+
+
+def test_rope_forward_noncontiguous_and_row_sums():
+    q, k, v = inputs(1, 4, 2, 96, 64, torch.bfloat16, seed=23, layout="bthd")
+    assert not q.is_contiguous()
+    D, T = 64, 96
+    cos, sin = smooth_attn.precompute_rope_cos_sin(D, T, device=DEV)
+    o, rs = kernels._sp2norm_rope_flash_fwd(q.to(DEV), k.to(DEV), v.to(DEV), cos, sin, 1 / math.sqrt(D), 2)
+    qr = eager.apply_rope(q.double(), cos.cpu().double(), sin.cpu().double()).to(torch.bfloat16).double()
+    kr = eager.apply_rope(k.double(), cos.cpu().double(), sin.cpu().double()).to(torch.bfloat16).double()
+    ref, ref_rs = eager.flash_attention_eager(qr, kr, v.double(), return_row_sums=True)
+    assert rel_err(o, ref) <= 1e-2
+    assert rel_err(rs, ref_rs) <= 1e-5
+
+
+def test_rope_identity_tables_equal_plain_forward():
+    # cos = 1, sin = 0 rotates nothing: the RoPE path must give the plain forward's output
+    q, k, v = (t.to(DEV) for t in inputs(1, 4, 4, 160, 128, torch.bfloat16, seed=24))
+    cos = torch.ones(160, 64, device=DEV)
+    sin = torch.zeros(160, 64, device=DEV)
+    o_rope, rs_rope = kernels._sp2norm_rope_flash_fwd(q, k, v, cos, sin, 1 / math.sqrt(128))
+    o, rs = kernels._sp2norm_flash_fwd(q, k, v, 1 / math.sqrt(128))
+    assert rel_err(o_rope, o) <= 4e-3
+    assert rel_err(rs_rope, rs) <= 1e-6
+
+
+@pytest.mark.parametrize("B,H,Hkv,T,D,M,window", [(2, 4, 4, 64, 32, 128, 0), (1, 8, 2, 130, 64, 96, 32),
+                                                  (1, 4, 4, 256, 128, 512, 0)])
+def test_rope_proj_matches_oracle(B, H, Hkv, T, D, M, window):
+    # tests/test_rope_proj.py:117-146 (first case), GQA / window / D=128 cases
+    q, k, v = inputs(B, H, Hkv, T, D, torch.bfloat16, seed=25 + M)
+    w_o = (torch.randn(H, D, M, generator=_g(26)) * 0.02).to(torch.bfloat16)
+    cos, sin = smooth_attn.precompute_rope_cos_sin(D, T, device=DEV)
+    out = smooth_attn.sp2norm_rope_flash_attention_proj(q.to(DEV), k.to(DEV), v.to(DEV), w_o.to(DEV), cos, sin,
+                                                        window_size=window)
+    ref = eager.rope_proj_eager(q.double(), k.double(), v.double(), w_o.double(), cos.cpu(), sin.cpu(),
+                                window_size=window)
+    assert out.shape == (B, T, M) and out.dtype == torch.bfloat16
+    assert not out.isnan().any()
+    assert rel_err(out, ref) <= 2e-2
+    assert float((out.float().cpu() - ref.float()).abs().max()) < 0.1  # tests/test_rope_proj.py:143
+    # deterministic: the projection is one fp32-accumulating GEMM, no atomics
+    out2 = smooth_attn.sp2norm_rope_flash_attention_proj(q.to(DEV), k.to(DEV), v.to(DEV), w_o.to(DEV), cos, sin,
+                                                         window_size=window)
+    assert torch.equal(out, out2)

@@ -312,3 +312,52 @@ def test_paged_decode_layout_independence():
     kc2, vc2, table2, lens2 = paging.build_paged_cache(k[1:2, :, :17], v[1:2, :, :17], page_size=8)
     torch.testing.assert_close(o[1], eager.paged_decode_eager(q[1:2], kc2, vc2, table2, lens2)[0],
                                rtol=1e-12, atol=1e-12)
+
+
+# ---------------------------------------------------------------------------
+# RoPE
+# ---------------------------------------------------------------------------
+def test_rope_tables_closed_form():
+    cos, sin = eager.rope_cos_sin(16, 40)
+    t = np.arange(40)[:, None]
+    ang = t * 10000.0 ** (-np.arange(0, 16, 2)[None, :] / 16.0)
+    np.testing.assert_allclose(cos.numpy(), np.cos(ang), rtol=0, atol=2e-6)
+    np.testing.assert_allclose(sin.numpy(), np.sin(ang), rtol=0, atol=2e-6)
+
+
+def test_rope_vs_complex_rotation():
+    x = torch.randn(2, 3, 9, 8, generator=_g(60), dtype=DTYPE)
+    cos, sin = eager.rope_cos_sin(8, 9, dtype=DTYPE)
+    got = eager.apply_rope(x, cos, sin).numpy()
+    # the fp32 tables carry ~1e-7 relative error at these angles
+    np.testing.assert_allclose(got, brute.rope(x.numpy()), rtol=0, atol=2e-6)
+
+
+def test_rope_invariants():
+    D, T = 16, 12
+    cos, sin = eager.rope_cos_sin(D, T, dtype=DTYPE)
+    x = torch.randn(1, 1, T, D, generator=_g(61), dtype=DTYPE)
+    r = eager.apply_rope(x, cos, sin)
+    torch.testing.assert_close(r[..., 0, :], x[..., 0, :], rtol=0, atol=0)  # position 0: identity
+    pair = lambda z: z[..., : D // 2] ** 2 + z[..., D // 2:] ** 2
+    # rotations keep pair norms (cos^2 + sin^2 = 1 to the fp32 tables' precision)
+    torch.testing.assert_close(pair(r), pair(x), rtol=1e-6, atol=1e-9)
+    # <R_m q, R_n k> depends only on m - n: put the same q / k at every position
+    q = torch.randn(D, generator=_g(62), dtype=DTYPE).expand(1, 1, T, D)
+    k = torch.randn(D, generator=_g(63), dtype=DTYPE).expand(1, 1, T, D)
+    rq, rk = eager.apply_rope(q, cos, sin)[0, 0], eager.apply_rope(k, cos, sin)[0, 0]
+    dots = rq @ rk.T
+    for off in range(-3, 4):
+        d = torch.diagonal(dots, offset=off)
+        torch.testing.assert_close(d, d[:1].expand_as(d), rtol=1e-5, atol=1e-5)
+
+
+def test_rope_proj_is_one_gemm():
+    B, H, T, D, M = 2, 3, 10, 8, 5
+    q, k, v = (torch.randn(B, H, T, D, generator=_g(64 + i), dtype=DTYPE) for i in range(3))
+    w = torch.randn(H, D, M, generator=_g(67), dtype=DTYPE)
+    cos, sin = eager.rope_cos_sin(D, T, dtype=DTYPE)
+    got = eager.rope_proj_eager(q, k, v, w, cos, sin, round_to=None)
+    o = eager.rope_flash_attention_eager(q, k, v, cos, sin, round_to=None)
+    ref = o.transpose(1, 2).reshape(B, T, H * D) @ w.reshape(H * D, M)
+    torch.testing.assert_close(got, ref, rtol=1e-12, atol=1e-12)
