@@ -85,6 +85,19 @@ int sa_norm_bwd(const void* x, const void* dy, void* dx, int64_t n_rows,
                 float alpha, float theta, int power, sa_stream_t stream);
 
 /*
+ * Softmax over each row of a [n_rows, n_cols] matrix (the comparison
+ * baseline).  causal != 0: row r sees columns 0 .. r mod n_cols (others are
+ * written as 0).  fp32 arithmetic, exp(x - rowmax) / sum.  dtype as
+ * sa_norm_fwd; n_cols <= 8192.
+ * Replaces softmax_triton[_out] / softmax_causal_triton[_out]
+ * (kernels.py:1233-1325) and the kernels _softmax_fwd (:534-562) and
+ * _softmax_causal_fwd (:852-884).
+ */
+int sa_softmax_fwd(const void* x, void* y, int64_t n_rows, int64_t n_cols,
+                   int64_t x_row_stride, int64_t y_row_stride, int dtype,
+                   int causal, sa_stream_t stream);
+
+/*
  * Fused causal squareplus attention forward (bf16 or fp16 q/k/v/o):
  *   O_i = sum_{j<=i, i-j<W} y_ij V_j / (sum_j y_ij + 1e-12),
  *   y = squareplus(2 s - 1)^2,  s = scale * q_i . k_j

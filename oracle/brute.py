@@ -157,3 +157,17 @@ def rope(x: np.ndarray, base: float = 10000.0) -> np.ndarray:
                 out[idx + (t, d)] = z.real
                 out[idx + (t, d + h)] = z.imag
     return out
+
+
+def softmax(x: np.ndarray) -> np.ndarray:
+    """exp(x_j - max) / sum over the last axis, element by element."""
+    x = np.asarray(x, dtype=np.float64)
+    out = np.empty_like(x)
+    for idx in np.ndindex(x.shape[:-1]):
+        row = [float(v) for v in x[idx]]
+        m = max(row)
+        e = [math.exp(v - m) for v in row]
+        s = sum(e)
+        for j, v in enumerate(e):
+            out[idx + (j,)] = v / s
+    return out

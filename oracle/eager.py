@@ -90,6 +90,27 @@ def softplus_norm_causal_cpu_path(x, alpha=2.0, theta=0.5, power=2):
     return softplus_norm_causal_eager(x.float(), alpha, theta, power).to(x.dtype)
 
 
+def softmax_eager(x):
+    """Row-wise softmax in the work dtype — the comparison baseline of
+    kernels.py:534-562 (F.softmax over the last dim).
+
+    pinned by: brute.softmax (float64 loops); rows sum to 1; invariance under
+    a per-row shift.
+    """
+    return torch.softmax(x.to(_work_dtype(x)), dim=-1)
+
+
+def softmax_causal_eager(x):
+    """Causal softmax: strict upper triangle masked to -inf, then softmax —
+    kernels.py:1368-1370 (and the kernel :852-884, which writes 0 there).
+
+    pinned by: brute.softmax on each visible prefix; exact zeros above the
+    diagonal; row 0 is e0.
+    """
+    xw = x.to(_work_dtype(x))
+    return torch.softmax(xw.masked_fill(causal_mask(x.shape[-1]), float("-inf")), dim=-1)
+
+
 def softplus_norm_backward(x, dy, alpha=2.0, theta=0.5, power=2, *, causal=True):
     """Closed-form gradient of the (causal or row-wise) normalisation.
 

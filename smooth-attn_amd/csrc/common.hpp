@@ -49,6 +49,20 @@ __device__ __forceinline__ float wave_sum(float v) {
     return (r0 + r1) + (r2 + r3);
 }
 
+// Maximum over the 64 lanes of a wavefront (same pattern as wave_sum).
+__device__ __forceinline__ float wave_max(float v) {
+    v = __builtin_fmaxf(v, dpp_mov<0xB1>(v));
+    v = __builtin_fmaxf(v, dpp_mov<0x4E>(v));
+    v = __builtin_fmaxf(v, dpp_mov<0x141>(v));
+    v = __builtin_fmaxf(v, dpp_mov<0x140>(v));
+    const int b = __float_as_int(v);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(b, 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(b, 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(b, 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(b, 48));
+    return __builtin_fmaxf(__builtin_fmaxf(r0, r1), __builtin_fmaxf(r2, r3));
+}
+
 // 16-byte vector type used for coalesced global traffic.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 

@@ -28,6 +28,7 @@ SIGNATURES = {
                             c_float, c_float, c_int, c_void_p]),
     "sa_norm_bwd": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64,
                             c_int, c_int, c_int, c_float, c_float, c_int, c_void_p]),
+    "sa_softmax_fwd": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int, c_int, c_void_p]),
     "sa_flash_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int,
                              c_int, _I64P, _I64P, _I64P, _I64P, c_float, c_int, c_int, c_int, c_void_p]),
     "sa_flash_bwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,

@@ -382,6 +382,61 @@ def softplus_norm_causal_eager(x, alpha=DEFAULT_FAMILY.alpha, theta=DEFAULT_FAMI
     return y / (y.sum(dim=-1, keepdim=True) + EPS)
 
 
+# ---------------------------------------------------------------------------
+# Softmax comparison baselines (kernels.py:1233-1325).
+# ---------------------------------------------------------------------------
+def _softmax_2d(x2d, out2d, causal):
+    n_rows, n_cols = x2d.shape
+    _check_row_length(n_cols)
+    lib = _lib.load()
+    with torch.cuda.device(x2d.device):
+        st = lib.sa_softmax_fwd(x2d.data_ptr(), out2d.data_ptr(), n_rows, n_cols, x2d.stride(0), out2d.stride(0),
+                                _DTYPE_CODE[x2d.dtype], 1 if causal else 0, _stream(x2d))
+    _lib.check(st, "sa_softmax_fwd")
+
+
+def softmax_triton(x, return_meta=False):
+    """Row-wise softmax into a new tensor — kernels.py:1233-1235."""
+    x_row = _prepare_rowwise_input(x)
+    out = torch.empty_like(x_row)
+    _softmax_2d(x_row, out, causal=False)
+    if return_meta:
+        return out, _row_launch_meta("softmax", *x_row.shape, x_row.dtype)
+    return out
+
+
+def softmax_triton_out(out, x, return_meta=False):
+    """Row-wise softmax into ``out`` — kernels.py:1238-1251."""
+    x_row = _prepare_rowwise_input(x)
+    kernel_out, user_out = _prepare_output(out, x_row)
+    _softmax_2d(x_row, kernel_out, causal=False)
+    result = _finalize_output(kernel_out, user_out)
+    if return_meta:
+        return result, _row_launch_meta("softmax", *x_row.shape, x_row.dtype)
+    return result
+
+
+def softmax_causal_triton_out(out, x, return_meta=False):
+    """Causal softmax over [..., L, L] into ``out`` (zeros above the
+    diagonal) — kernels.py:1312-1325."""
+    x_attn = _prepare_attention_input(x)
+    kernel_out, user_out = _prepare_output(out, x_attn)
+    seq_len = x_attn.shape[-1]
+    x2d = x_attn.view(-1, seq_len)
+    _softmax_2d(x2d, kernel_out.view(-1, seq_len), causal=True)
+    result = _finalize_output(kernel_out, user_out)
+    if return_meta:
+        return result, _row_launch_meta("softmax_causal", x2d.shape[0], seq_len, x2d.dtype)
+    return result
+
+
+def softmax_causal_triton(x, return_meta=False):
+    """Causal softmax into a new tensor — kernels.py:1300-1309."""
+    x_attn = _prepare_attention_input(x)
+    out = torch.empty_like(x_attn)
+    return softmax_causal_triton_out(out, x_attn, return_meta=return_meta)
+
+
 def softmax_causal_eager(x):
     mask = _causal_mask(x.shape[-1], x.device)
     return F.softmax(x.masked_fill(mask, float("-inf")), dim=-1)
@@ -759,3 +814,32 @@ def bench(fn, x=None, warmup=300, iters=1000):
 
 def bench_out(fn, out, x, warmup=300, iters=1000):
     return _median_cuda_us(lambda: fn(out, x), warmup=warmup, iters=iters)
+
+
+# ---------------------------------------------------------------------------
+# Benchmark harness entry points, also reachable from this module as in the
+# reference (console script ``smooth_attn.kernels:main``, pyproject.toml:37);
+# the implementation lives in smooth_attn.cli.
+# ---------------------------------------------------------------------------
+def benchmark_rowwise_suite(family, shapes=None, warmup=50, iters=200):
+    """kernels.py:2841-2867."""
+    from . import cli
+    return cli.benchmark_rowwise_suite(family, shapes=shapes, warmup=warmup, iters=iters)
+
+
+def benchmark_causal_suite(family, dtypes, lengths, batch=2, heads=8, warmup=50, iters=200):
+    """kernels.py:2870-2932."""
+    from . import cli
+    return cli.benchmark_causal_suite(family, dtypes, lengths, batch=batch, heads=heads, warmup=warmup, iters=iters)
+
+
+def validate_causal_backward(family, dtypes, seq_len=128, batch=2, heads=4):
+    """kernels.py:2935-2967."""
+    from . import cli
+    return cli.validate_causal_backward(family, dtypes, seq_len=seq_len, batch=batch, heads=heads)
+
+
+def main(argv=None):
+    """kernels.py:3078-3128."""
+    from . import cli
+    return cli.main(argv)

@@ -105,3 +105,34 @@ def test_flash_asserts_shapes():
         smooth_attn.sp2norm_paged_attention(torch.zeros(1, 4, 2, 16), torch.zeros(2, 4, 16, 16),
                                             torch.zeros(2, 4, 16, 16), torch.zeros(1, 2, dtype=torch.int32),
                                             torch.zeros(1, dtype=torch.int32))
+
+
+def test_cli_parsing_matches_reference_defaults():
+    # kernels.py:3061-3075 options and defaults; :150-164 list parsing
+    from smooth_attn import cli
+    a = cli.parse_args([])
+    assert (a.mode, a.dtypes, a.lengths, a.batch, a.heads, a.warmup, a.iters) == \
+        ("causal", "bf16", "128,256,512,1024", 2, 8, 50, 200)
+    assert (a.alpha, a.theta, a.power, a.quick, a.check_backward) == (2.0, 0.5, 2, False, False)
+    a = cli.parse_args(["--mode", "all", "--dtypes", "fp32,bf16", "--quick", "--check-backward"])
+    assert a.mode == "all" and a.quick and a.check_backward
+    assert cli._parse_dtype_list(" FP32, bf16 ,fp16") == [torch.float32, torch.bfloat16, torch.float16]
+    assert cli._parse_int_list("128, 256,") == [128, 256]
+    with pytest.raises(ValueError):
+        cli._parse_dtype_list("fp64")
+    with pytest.raises(ValueError):
+        cli._parse_int_list(" , ")
+    assert cli._dtype_label(torch.bfloat16) == "bf16" and cli._dtype_label(torch.int8) == "int8"
+    assert len(cli.DEFAULT_ROWWISE_SHAPES) == 24
+    with pytest.raises(SystemExit):
+        cli.parse_args(["--mode", "bogus"])
+
+
+def test_softmax_entry_points_validate_before_launch():
+    import smooth_attn
+    with pytest.raises(TypeError):
+        smooth_attn.softmax_triton([1.0, 2.0])
+    with pytest.raises(ValueError):
+        smooth_attn.softmax_triton(torch.zeros(2, 2))  # not a device tensor
+    with pytest.raises(ValueError):
+        smooth_attn.softmax_causal_triton(torch.zeros(2, 3))

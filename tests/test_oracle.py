@@ -361,3 +361,26 @@ def test_rope_proj_is_one_gemm():
     o = eager.rope_flash_attention_eager(q, k, v, cos, sin, round_to=None)
     ref = o.transpose(1, 2).reshape(B, T, H * D) @ w.reshape(H * D, M)
     torch.testing.assert_close(got, ref, rtol=1e-12, atol=1e-12)
+
+
+# ---------------------------------------------------------------------------
+# Softmax baselines
+# ---------------------------------------------------------------------------
+def test_softmax_vs_brute_and_invariants():
+    x = torch.randn(5, 13, generator=_g(70), dtype=DTYPE) * 4
+    y = eager.softmax_eager(x)
+    np.testing.assert_allclose(y.numpy(), brute.softmax(x.numpy()), rtol=1e-13, atol=0)
+    torch.testing.assert_close(y.sum(-1), torch.ones(5, dtype=DTYPE), rtol=0, atol=1e-14)
+    torch.testing.assert_close(eager.softmax_eager(x + 123.0), y, rtol=1e-12, atol=1e-15)
+
+
+def test_softmax_causal_vs_brute_prefixes():
+    L = 9
+    x = torch.randn(2, L, L, generator=_g(71), dtype=DTYPE) * 3
+    y = eager.softmax_causal_eager(x)
+    upper = torch.triu(torch.ones(L, L, dtype=torch.bool), 1)
+    assert bool((y[:, upper] == 0).all())
+    torch.testing.assert_close(y[:, 0, 0], torch.ones(2, dtype=DTYPE), rtol=0, atol=0)
+    for i in range(L):
+        np.testing.assert_allclose(y[:, i, : i + 1].numpy(), brute.softmax(x[:, i, : i + 1].numpy()),
+                                   rtol=1e-13, atol=0)
