@@ -137,13 +137,77 @@ __global__ __launch_bounds__(256) void rope_rotate_rows(const T* __restrict__ k,
     *reinterpret_cast<u32x4*>(dst + D / 2) = bb;
 }
 
-#ifndef SA_FLASH_QT
-#define SA_FLASH_QT 2
+#ifndef SA_FLASH_SKIPQT
+#define SA_FLASH_SKIPQT 1
 #endif
-// Query tiles (32 rows each) per wave.  With QT = 2 every K and V^T operand
-// read from LDS feeds two independent MFMAs and every staged K/V tile serves
-// 256 query rows; wave w owns query tiles w and w + 4 of the block, which
-// balances the causal work of the four waves.
+#ifndef SA_FLASH_SPLIT
+#define SA_FLASH_SPLIT 1
+#endif
+#ifndef SA_FLASH_TILE_NT
+#define SA_FLASH_TILE_NT 0
+#endif
+// K/V tile loads: every tile is read by all query blocks of its head, so
+// these loads are cached (a nontemporal load would stream past L2).
+template <typename T>
+__device__ __forceinline__ u32x4 tile_load16(const T* p) {
+    if (SA_FLASH_TILE_NT) return load16(p);
+    return *reinterpret_cast<const u32x4*>(p);
+}
+
+#ifndef SA_FLASH_MAP
+#define SA_FLASH_MAP 2
+#endif
+// Block -> (query block, batch, query head).  Blocks are dealt to the 8 XCDs
+// round-robin by index.  When B*Hkv is a multiple of 8, XCD x gets the KV
+// heads u = x, x+8, ... together with all G query heads that read them (so
+// each KV head is fetched into one XCD's L2 only), and on every XCD blocks
+// run heaviest query block first across its heads (short tail).  Otherwise
+// heaviest query block first across all heads.
+__device__ __forceinline__ void block_coords(const FlashParams& p, int& qb, int& b, int& hq) {
+    const int id = blockIdx.x;
+    const int BHk = p.B * p.Hkv;
+    if (SA_FLASH_MAP == 1 && (BHk & 7) == 0) {
+        const int x = id & 7;
+        const int j = id >> 3;
+        const int per_kv = p.G * p.nqb;
+        const int kvl = j / per_kv;
+        const int rem = j - kvl * per_kv;
+        const int u = kvl * 8 + x;  // (b, hk)
+        b = u / p.Hkv;
+        const int hk = u - b * p.Hkv;
+        qb = p.nqb - 1 - rem / p.G;
+        hq = hk * p.G + (rem - (rem / p.G) * p.G);
+    } else if (SA_FLASH_MAP == 2 && (BHk & 7) == 0) {
+        const int x = id & 7;
+        const int j = id >> 3;
+        const int nh = (BHk >> 3) * p.G;  // query heads per XCD
+        const int step = j / nh;
+        const int r = j - step * nh;
+        const int kvl = r / p.G;
+        const int u = kvl * 8 + x;  // (b, hk)
+        b = u / p.Hkv;
+        const int hk = u - b * p.Hkv;
+        qb = p.nqb - 1 - step;
+        hq = hk * p.G + (r - kvl * p.G);
+    } else {
+        const int BH = p.B * p.Hq;
+        qb = p.nqb - 1 - id / BH;
+        const int bh = id - (id / BH) * BH;
+        b = bh / p.Hq;
+        hq = bh - b * p.Hq;
+    }
+}
+
+#ifndef SA_FLASH_QT
+#define SA_FLASH_QT 1
+#endif
+// Query tiles (32 rows each) per wave.  QT = 1 (the default) keeps a wave
+// within 256 VGPRs, so two blocks (8 waves) share each CU and no register
+// traffic goes through AGPRs; QT = 2 reuses every K / V^T operand for two
+// MFMAs but needs more than 256 registers, and the AGPR copies that the
+// compiler then emits cost more than the reuse saves (measured: 987 vs
+// 906 us on [4,32,4096,128]).  With QT = 2, wave w owns query tiles w and
+// w + 4 of the block, which balances the causal work of the four waves.
 constexpr int kQT = SA_FLASH_QT;
 constexpr int kBQ2 = 32 * 4 * kQT;  // query rows per block
 
@@ -162,12 +226,9 @@ __global__ __launch_bounds__(256, kQT == 1 ? 2 : 1) void flash_fwd_kernel(FlashP
     const int hi = lane >> 5;  // lane half
     const int l32 = lane & 31;
 
-    const int BH = p.B * p.Hq;
-    const int id = blockIdx.x;
-    const int qb = p.nqb - 1 - id / BH;
-    const int bh = id % BH;
-    const int b = bh / p.Hq;
-    const int hq = bh - b * p.Hq;
+    int qb, b, hq;
+    block_coords(p, qb, b, hq);
+    const int bh = b * p.Hq + hq;
     const int hk = hq / p.G;
     const int T_ = p.T;
 
@@ -256,14 +317,14 @@ __global__ __launch_bounds__(256, kQT == 1 ? 2 : 1) void flash_fwd_kernel(FlashP
             const int ci = min(tid + kThreads * i, kBKV * Gm::KCPR - 1);
             const int row = ci / Gm::KCPR;
             const int c = ci - row * Gm::KCPR;
-            kst[i] = load16(kp + min(k0 + row, T_ - 1) * krs + c * 16);
+            kst[i] = tile_load16(kp + min(k0 + row, T_ - 1) * krs + c * 16);
         }
 #pragma unroll
         for (int i = 0; i < Gm::VNL; ++i) {
             const int ci = min(tid + kThreads * i, kBKV * Gm::VCPR - 1);
             const int row = ci / Gm::VCPR;
             const int c = ci - row * Gm::VCPR;
-            vst[i] = load16(vp + min(k0 + row, T_ - 1) * vrs + c * 16);
+            vst[i] = tile_load16(vp + min(k0 + row, T_ - 1) * vrs + c * 16);
         }
     };
     auto store_tile = [&](int buf) {
@@ -332,7 +393,7 @@ __global__ __launch_bounds__(256, kQT == 1 ? 2 : 1) void flash_fwd_kernel(FlashP
                                    (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
 #pragma unroll
                     for (int qt = 0; qt < kQT; ++qt) {
-                        if (!act[qt]) continue;
+                        if (SA_FLASH_SKIPQT && !act[qt]) continue;
                         const i32x8 bv{(int)qreg[qt][dc][0].x, (int)qreg[qt][dc][0].y, (int)qreg[qt][dc][0].z,
                                        (int)qreg[qt][dc][0].w, (int)qreg[qt][dc][1].x, (int)qreg[qt][dc][1].y,
                                        (int)qreg[qt][dc][1].z, (int)qreg[qt][dc][1].w};
@@ -342,7 +403,7 @@ __global__ __launch_bounds__(256, kQT == 1 ? 2 : 1) void flash_fwd_kernel(FlashP
                     const u32x4 a = *reinterpret_cast<const u32x4*>(krow + (dc * 16 + hi * 8) * 2);
 #pragma unroll
                     for (int qt = 0; qt < kQT; ++qt) {
-                        if (!act[qt]) continue;
+                        if (SA_FLASH_SKIPQT && !act[qt]) continue;
                         s[qt] = Ops::mma(as_vec8<Vec>(a), as_vec8<Vec>(qreg[qt][dc][0]), s[qt]);
                     }
                 }
@@ -350,7 +411,7 @@ __global__ __launch_bounds__(256, kQT == 1 ? 2 : 1) void flash_fwd_kernel(FlashP
             Vec bop[kQT][2];
 #pragma unroll
             for (int qt = 0; qt < kQT; ++qt) {
-                if (!act[qt]) continue;
+                if (SA_FLASH_SKIPQT && !act[qt]) continue;
                 // valid(key) <=> 0 <= qi - key < W_eff (W_eff = W, or INT_MAX
                 // for full causal): one unsigned compare per element.
                 const int dbase = wq0[qt] + l32 - k0 - hi * 4;
@@ -386,7 +447,7 @@ __global__ __launch_bounds__(256, kQT == 1 ? 2 : 1) void flash_fwd_kernel(FlashP
                     const u32x4 aw{lo.x, lo.y, hi8.x, hi8.y};
 #pragma unroll
                     for (int qt = 0; qt < kQT; ++qt) {
-                        if (!act[qt]) continue;
+                        if (SA_FLASH_SKIPQT && !act[qt]) continue;
                         oacc[qt][dt] = Ops::mma(as_vec8<Vec>(aw), bop[qt][ch], oacc[qt][dt]);
                     }
                 }
@@ -412,7 +473,7 @@ __global__ __launch_bounds__(256, kQT == 1 ? 2 : 1) void flash_fwd_kernel(FlashP
         // every query tile fully sees it (no masks, no inactive tile)
         const bool interior = (k0 + kBKV - 1 <= wfirst) && !(W > 0 && k0 <= wlast + 31 - W);
         if (any) {
-            if (interior)
+            if (SA_FLASH_SPLIT && interior)
                 tile_step(std::false_type{}, buf, k0);
             else
                 tile_step(std::true_type{}, buf, k0);
