@@ -11,16 +11,15 @@
 //
 // Work decomposition: a block of 4 waves owns 128 query rows of one
 // (batch, query head); wave w owns rows [32w, 32w+32).  K and V tiles of 64
-// keys are staged through LDS (double buffered, one barrier per tile):
-// global -> registers for tile j+1 while tile j is computed, then registers
-// -> LDS.  Per wave and tile: S^T = K Q^T on MFMA, the squareplus weights on
-// the VALU (masks only on tiles crossing the diagonal or the window edge),
-// then O^T += V^T P^T on MFMA.  fp8 V is widened to the 16-bit type while it
-// is staged (exact: e4m3fn values are representable in bf16) and v_scale is
-// applied once at the end.
-// Blocks are issued heaviest first (last query blocks first) and, because the
-// block index runs over (batch, head) fastest, every query block of one head
-// lands on the same XCD when B*Hq is a multiple of 8 (shared K/V in L2).
+// keys go straight from global memory into LDS (global_load_lds, double
+// buffered, one barrier per tile; no staging registers): tile j+1 is in
+// flight while tile j is computed.  Per wave and tile: S^T = K Q^T on MFMA,
+// the squareplus weights on the VALU (masks only on tiles crossing the
+// diagonal or the window edge), then O^T += V^T P^T on MFMA.  fp8 V is
+// widened to the 16-bit type while it is staged through registers (exact:
+// e4m3fn values are representable in bf16) and v_scale is applied once at
+// the end.
+// Block order: see block_coords (XCD-aware, heaviest query blocks first).
 #include <type_traits>
 
 #include "flash_common.hpp"
@@ -28,7 +27,13 @@
 namespace sa {
 namespace {
 
-constexpr int kBKV = 64;   // keys per tile
+#ifndef SA_FLASH_BKV
+#define SA_FLASH_BKV 64
+#endif
+#ifndef SA_FLASH_MINB
+#define SA_FLASH_MINB 2
+#endif
+constexpr int kBKV = SA_FLASH_BKV;  // keys per tile (multiple of 32)
 constexpr int kThreads = 256;
 
 struct FlashParams {
@@ -49,22 +54,46 @@ struct FlashParams {
 
 // T: 16-bit type of P V (and of q/k/v unless fp8).  QK8: q, k are e4m3fn.
 // V8: v is e4m3fn.
-#ifndef SA_FLASH_VPAD
-#define SA_FLASH_VPAD 8
-#endif
+//
+// LDS tiles are unpadded rows of 16-byte chunks, filled by direct
+// global->LDS loads (global_load_lds_dwordx4: lane i of a wave writes bytes
+// [16 i, 16 i + 16) after the wave's base, so one instruction fills 1 KB of
+// consecutive chunks).  Bank conflicts are avoided by storing logical chunk
+// c of row r at chunk c ^ swz(r):
+//  * K (read as 16-byte A-operand rows, 8 rows per LDS cycle): swz_k spreads
+//    8 consecutive rows over the 8 16-byte bank groups of 128 bytes;
+//  * V (read by ds_read_b64_tr_b16: per 16 lanes, 4 rows x 32 bytes): swz_v
+//    moves the 4 rows' 32-byte pairs to different 32-byte slots.
 template <typename T, int D, bool QK8, bool V8>
 struct Geom {
-    static constexpr int QKB = QK8 ? 1 : 2;         // bytes per q/k element
-    static constexpr int RSK = D * QKB + 16;        // K row stride in LDS (bytes)
-    static constexpr int RSV = D + SA_FLASH_VPAD;   // V row stride in LDS (elements of T)
-    static constexpr int KT = kBKV * RSK;           // bytes per K tile
-    static constexpr int VT = kBKV * RSV * 2;       // bytes per V tile
-    static constexpr int KCPR = D * QKB / 16;       // 16-byte global chunks per K row
-    static constexpr int VCPR = D * (V8 ? 1 : 2) / 16;
-    static constexpr int KNL = (kBKV * KCPR + kThreads - 1) / kThreads;
-    static constexpr int VNL = (kBKV * VCPR + kThreads - 1) / kThreads;
+    static constexpr int QKB = QK8 ? 1 : 2;             // bytes per q/k element
+    static constexpr int KROWB = D * QKB;               // K row bytes in LDS
+    static constexpr int VROWB = D * 2;                 // V row bytes in LDS (16-bit)
+    static constexpr int KT = kBKV * KROWB;             // bytes per K tile
+    static constexpr int VT = kBKV * VROWB;             // bytes per V tile
+    static constexpr int KCPR = KROWB / 16;             // 16-byte chunks per K row
+    static constexpr int VCPRL = VROWB / 16;            // chunks per V row in LDS
+    static constexpr int VCPRG = D * (V8 ? 1 : 2) / 16; // chunks per V row in global memory
+    static constexpr int KNI = (kBKV * KCPR + kThreads - 1) / kThreads;   // K DMA loads per lane
+    static constexpr int VNI = (kBKV * VCPRL + kThreads - 1) / kThreads;  // V DMA loads per lane
+    static constexpr int VNL = (kBKV * VCPRG + kThreads - 1) / kThreads;  // staged fp8 V loads
     static constexpr int NQC = QK8 ? (D + 63) / 64 : D / 16;  // MFMAs per 32x32 score tile
+    static __device__ __forceinline__ int swz_k(int r) {
+        return KCPR >= 8 ? (r & (KCPR - 1)) : ((r / (8 / KCPR)) & (KCPR - 1));
+    }
+    static __device__ __forceinline__ int swz_v(int r) { return VCPRL >= 8 ? 2 * (r & 3) : 2 * ((r >> 1) & 1); }
 };
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glb_void_t;
+
+// One 16-byte global -> LDS load per lane; lds_base must be wave-uniform.
+__device__ __forceinline__ void dma16(const void* g, void* lds_base) {
+    __builtin_amdgcn_global_load_lds((glb_void_t*)(g), (lds_void_t*)(lds_base), 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(0): this wave's direct-to-LDS loads have landed.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 __device__ __forceinline__ f32x16 mma_fp8(i32x8 a, i32x8 b, f32x16 c) {
     // e4m3 x e4m3, unit block scales (E8M0 127 = 2^0)
@@ -212,13 +241,13 @@ constexpr int kQT = SA_FLASH_QT;
 constexpr int kBQ2 = 32 * 4 * kQT;  // query rows per block
 
 template <typename T, int D, bool QK8, bool V8, bool EXACT, bool ROPE>
-__global__ __launch_bounds__(256, kQT == 1 ? 2 : 1) void flash_fwd_kernel(FlashParams p) {
+__global__ __launch_bounds__(256, kQT == 1 ? SA_FLASH_MINB : 1) void flash_fwd_kernel(FlashParams p) {
     using Gm = Geom<T, D, QK8, V8>;
     using Ops = MfmaOps<T>;
     using Vec = typename Ops::vec8;
-    __shared__ __attribute__((aligned(16))) unsigned char lds[2 * (Gm::KT + Gm::VT)];
-    unsigned char* ldsK = lds;                         // [2][64][RSK bytes]
-    T* ldsV = reinterpret_cast<T*>(lds + 2 * Gm::KT);  // [2][64][RSV]
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[2 * (Gm::KT + Gm::VT)];
+    unsigned char* ldsK = lds;                 // [2][kBKV][KROWB], swizzled chunks
+    unsigned char* ldsVb = lds + 2 * Gm::KT;   // [2][kBKV][VROWB], swizzled chunks
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -308,55 +337,78 @@ __global__ __launch_bounds__(256, kQT == 1 ? 2 : 1) void flash_fwd_kernel(FlashP
         for (int dt = 0; dt < D / 32; ++dt) oacc[qt][dt] = f32x16{};
     }
 
-    // Global -> register staging of one K/V tile.
-    u32x4 kst[Gm::KNL], vst[Gm::VNL];
-    auto load_tile = [&](int j) {
+    // Tile j into buffer buf: K (and 16-bit V) by direct global->LDS loads,
+    // fp8 V staged through registers (widened to T in finish_tile).  Slot s
+    // of a tile is written by wave (s / 64) % 4, instruction s / 256.
+    u32x4 vst[V8 ? Gm::VNL : 1];
+    auto issue_tile = [&](int j, int buf) {
         const int k0 = j * kBKV;
 #pragma unroll
-        for (int i = 0; i < Gm::KNL; ++i) {
-            const int ci = min(tid + kThreads * i, kBKV * Gm::KCPR - 1);
-            const int row = ci / Gm::KCPR;
-            const int c = ci - row * Gm::KCPR;
-            kst[i] = tile_load16(kp + min(k0 + row, T_ - 1) * krs + c * 16);
+        for (int i = 0; i < Gm::KNI; ++i) {
+            const int sbase = (i * 4 + wave) * 64;
+            if ((kBKV * Gm::KCPR) % kThreads == 0 || sbase < kBKV * Gm::KCPR) {
+                const int sl = sbase + lane;
+                const int row = sl / Gm::KCPR;
+                const int c = (sl - row * Gm::KCPR) ^ Gm::swz_k(row);
+                dma16(kp + min(k0 + row, T_ - 1) * krs + c * 16, ldsK + buf * Gm::KT + sbase * 16);
+            }
         }
+        if constexpr (!V8) {
 #pragma unroll
-        for (int i = 0; i < Gm::VNL; ++i) {
-            const int ci = min(tid + kThreads * i, kBKV * Gm::VCPR - 1);
-            const int row = ci / Gm::VCPR;
-            const int c = ci - row * Gm::VCPR;
-            vst[i] = tile_load16(vp + min(k0 + row, T_ - 1) * vrs + c * 16);
+            for (int i = 0; i < Gm::VNI; ++i) {
+                const int sbase = (i * 4 + wave) * 64;
+                if ((kBKV * Gm::VCPRL) % kThreads == 0 || sbase < kBKV * Gm::VCPRL) {
+                    const int sl = sbase + lane;
+                    const int row = sl / Gm::VCPRL;
+                    const int c = (sl - row * Gm::VCPRL) ^ Gm::swz_v(row);
+                    dma16(vp + min(k0 + row, T_ - 1) * vrs + c * 16, ldsVb + buf * Gm::VT + sbase * 16);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < Gm::VNL; ++i) {
+                const int ci = min(tid + kThreads * i, kBKV * Gm::VCPRG - 1);
+                const int row = ci / Gm::VCPRG;
+                const int c = ci - row * Gm::VCPRG;
+                vst[i] = tile_load16(vp + min(k0 + row, T_ - 1) * vrs + c * 16);
+            }
         }
     };
-    auto store_tile = [&](int buf) {
+    auto finish_tile = [&](int buf) {
+        if constexpr (V8) {
 #pragma unroll
-        for (int i = 0; i < Gm::KNL; ++i) {
-            const int ci = tid + kThreads * i;
-            const int row = ci / Gm::KCPR;
-            const int c = ci - row * Gm::KCPR;
-            if ((kBKV * Gm::KCPR) % kThreads == 0 || ci < kBKV * Gm::KCPR)
-                *reinterpret_cast<u32x4*>(ldsK + buf * Gm::KT + row * Gm::RSK + c * 16) = kst[i];
-        }
-#pragma unroll
-        for (int i = 0; i < Gm::VNL; ++i) {
-            const int ci = tid + kThreads * i;
-            const int row = ci / Gm::VCPR;
-            const int c = ci - row * Gm::VCPR;
-            if ((kBKV * Gm::VCPR) % kThreads == 0 || ci < kBKV * Gm::VCPR) {
-                T* dst = ldsV + buf * (Gm::VT / 2) + row * Gm::RSV;
-                if constexpr (V8) {
+            for (int i = 0; i < Gm::VNL; ++i) {
+                const int ci = tid + kThreads * i;
+                const int row = ci / Gm::VCPRG;
+                const int c = ci - row * Gm::VCPRG;
+                if ((kBKV * Gm::VCPRG) % kThreads == 0 || ci < kBKV * Gm::VCPRG) {
+                    // 16 fp8 values = LDS chunks 2c, 2c + 1 (swz_v is even, so they stay adjacent)
+                    unsigned char* dst = ldsVb + buf * Gm::VT + row * Gm::VROWB + ((2 * c) ^ Gm::swz_v(row)) * 16;
                     u32x4 lo, hi16;
                     widen_fp8x16<T>(vst[i], lo, hi16);
-                    *reinterpret_cast<u32x4*>(dst + c * 16) = lo;
-                    *reinterpret_cast<u32x4*>(dst + c * 16 + 8) = hi16;
-                } else {
-                    *reinterpret_cast<u32x4*>(dst + c * 8) = vst[i];
+                    *reinterpret_cast<u32x4*>(dst) = lo;
+                    *reinterpret_cast<u32x4*>(dst + 16) = hi16;
                 }
             }
         }
     };
 
     // Per-lane element offset of the transposing V read; see flash_common.hpp.
-    const int v_tr_off = ((lane >> 5) * 4 + ((lane & 15) >> 2)) * Gm::RSV + ((lane >> 4) & 1) * 16 + 4 * (lane & 3);
+    // Byte offsets (within a 16-key chunk of the V tile) of this lane's
+    // transposing reads, one per 32-column block dt: row (lane>>5)*4 +
+    // ((lane&15)>>2), columns dt*32 + ((lane>>4)&1)*16 + 4*(lane&3).
+    int v_tr_off[D / 32];
+    {
+        const int vr = (lane >> 5) * 4 + ((lane & 15) >> 2);
+        const int vsw = Gm::swz_v(vr);
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) {
+            const int chunk = (dt * 4 + ((lane >> 4) & 1) * 2 + ((lane & 3) >> 1)) ^ vsw;
+            v_tr_off[dt] = vr * Gm::VROWB + chunk * 16 + (lane & 1) * 8;
+        }
+    }
+    // K A-operand chunk swizzle of this lane's rows (kt * 32 + l32; the same for every kt).
+    const int kswz = Gm::swz_k(l32);
     const unsigned weff = W > 0 ? static_cast<unsigned>(W) : 0x7FFFFFFFu;
 
     // One K/V tile for all of this wave's query tiles.  EDGE: some tile of
@@ -371,23 +423,23 @@ __global__ __launch_bounds__(256, kQT == 1 ? 2 : 1) void flash_fwd_kernel(FlashP
             msk[qt] = EDGE && ((k0 + kBKV - 1 > wq0[qt]) || (W > 0 && k0 <= wq0[qt] + 31 - W));
         }
         const unsigned char* Kb = ldsK + buf * Gm::KT;
-        const T* Vb = ldsV + buf * (Gm::VT / 2);
+        const unsigned char* Vb = ldsVb + buf * Gm::VT;
         // One 32-key half at a time: S^T tiles, weights, then the two P V
         // chunks of the half.
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
+        for (int kt = 0; kt < kBKV / 32; ++kt) {
             f32x16 s[kQT];
 #pragma unroll
             for (int qt = 0; qt < kQT; ++qt) s[qt] = f32x16{};
-            const unsigned char* krow = Kb + (kt * 32 + l32) * Gm::RSK;
+            const unsigned char* krow = Kb + (kt * 32 + l32) * Gm::KROWB;
 #pragma unroll
             for (int dc = 0; dc < Gm::NQC; ++dc) {
                 if constexpr (QK8) {
                     const int d0 = 64 * dc + 32 * hi;
                     u32x4 a0 = u32x4{0u, 0u, 0u, 0u}, a1 = u32x4{0u, 0u, 0u, 0u};
                     if (d0 < D) {
-                        a0 = *reinterpret_cast<const u32x4*>(krow + d0);
-                        a1 = *reinterpret_cast<const u32x4*>(krow + d0 + 16);
+                        a0 = *reinterpret_cast<const u32x4*>(krow + ((d0 / 16) ^ kswz) * 16);
+                        a1 = *reinterpret_cast<const u32x4*>(krow + ((d0 / 16 + 1) ^ kswz) * 16);
                     }
                     const i32x8 av{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w,
                                    (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
@@ -400,7 +452,7 @@ __global__ __launch_bounds__(256, kQT == 1 ? 2 : 1) void flash_fwd_kernel(FlashP
                         s[qt] = mma_fp8(av, bv, s[qt]);
                     }
                 } else {
-                    const u32x4 a = *reinterpret_cast<const u32x4*>(krow + (dc * 16 + hi * 8) * 2);
+                    const u32x4 a = *reinterpret_cast<const u32x4*>(krow + ((dc * 2 + hi) ^ kswz) * 16);
 #pragma unroll
                     for (int qt = 0; qt < kQT; ++qt) {
                         if (SA_FLASH_SKIPQT && !act[qt]) continue;
@@ -441,9 +493,9 @@ __global__ __launch_bounds__(256, kQT == 1 ? 2 : 1) void flash_fwd_kernel(FlashP
                 const int c = 2 * kt + ch;  // 16-key chunk of the tile
 #pragma unroll
                 for (int dt = 0; dt < D / 32; ++dt) {
-                    const T* base = Vb + (16 * c) * Gm::RSV + dt * 32 + v_tr_off;
+                    const unsigned char* base = Vb + (16 * c) * Gm::VROWB + v_tr_off[dt];
                     const uint2 lo = lds_read_tr16(base);
-                    const uint2 hi8 = lds_read_tr16(base + 8 * Gm::RSV);
+                    const uint2 hi8 = lds_read_tr16(base + 8 * Gm::VROWB);
                     const u32x4 aw{lo.x, lo.y, hi8.x, hi8.y};
 #pragma unroll
                     for (int qt = 0; qt < kQT; ++qt) {
@@ -457,8 +509,9 @@ __global__ __launch_bounds__(256, kQT == 1 ? 2 : 1) void flash_fwd_kernel(FlashP
 
     // kv_begin < kv_end for every block (q_start < T), so the first tile is
     // always staged.
-    load_tile(kv_begin);
-    store_tile(0);
+    issue_tile(kv_begin, 0);
+    finish_tile(0);
+    wait_vmem();
     __syncthreads();
 
     const int wlast = wq0[kQT - 1];  // the wave's latest query tile
@@ -466,7 +519,7 @@ __global__ __launch_bounds__(256, kQT == 1 ? 2 : 1) void flash_fwd_kernel(FlashP
     for (int j = kv_begin; j < kv_end; ++j) {
         const int buf = (j - kv_begin) & 1;
         const bool has_next = j + 1 < kv_end;
-        if (has_next) load_tile(j + 1);
+        if (has_next) issue_tile(j + 1, buf ^ 1);
         const int k0 = j * kBKV;
         // some query tile of the wave sees this key tile
         const bool any = (k0 <= wlast + 31) && !(W > 0 && k0 + kBKV - 1 <= wfirst - W);
@@ -478,7 +531,8 @@ __global__ __launch_bounds__(256, kQT == 1 ? 2 : 1) void flash_fwd_kernel(FlashP
             else
                 tile_step(std::true_type{}, buf, k0);
         }
-        if (has_next) store_tile(buf ^ 1);
+        if (has_next) finish_tile(buf ^ 1);
+        wait_vmem();
         __syncthreads();
     }
 
