@@ -103,7 +103,7 @@ int sa_softmax_fwd(const void* x, void* y, int64_t n_rows, int64_t n_cols,
  *   y = squareplus(2 s - 1)^2,  s = scale * q_i . k_j
  * q,o: [B, Hq, T, D]; k,v: [B, Hkv, T, D]; Hq % Hkv == 0 (query head h reads
  * KV head h / (Hq/Hkv)).  *_strides are element strides for (b, h, t, d) and
- * the d stride must be 1.  row_sums (nullable): fp32 [B, Hq, T] contiguous,
+ * the d stride must be 1 (K and V row strides at most 16 MiB).  row_sums (nullable): fp32 [B, Hq, T] contiguous,
  * receives sum_j y_ij + 1e-12.  window_size 0 = full causal.  D in {32, 64,
  * 128}.  exact_math != 0 selects a correctly rounded sqrt.
  * Replaces _sp2norm_flash_fwd (kernels.py:1912-1931) and its kernel

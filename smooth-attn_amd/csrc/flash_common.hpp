@@ -58,6 +58,20 @@ __device__ __forceinline__ uint2 lds_read_tr16(const void* p) {
     return __builtin_bit_cast(uint2, v);
 }
 
+// Two transposing reads assembled into one 8-element MFMA operand (elements
+// 0-3 from p0, 4-7 from p1) with a vector shuffle, so the two 64-bit results
+// can land directly in the operand's register quad.
+template <typename V>
+__device__ __forceinline__ V lds_read_tr16_pair(const void* p0, const void* p1) {
+    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+    typedef __attribute__((address_space(3))) char lds_char;
+    typedef short s16x8 __attribute__((ext_vector_type(8)));
+    const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)((lds_char*)(p0)));
+    const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)((lds_char*)(p1)));
+    const s16x8 ab = __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(V, ab);
+}
+
 // squareplus(a)^2 with a = scale * s - 1/2 already folded in:
 //   squareplus(2 s scale - 1) = (2 s scale - 1 + sqrt((2 s scale - 1)^2 + 4)) / 2
 //                             = a + sqrt(a^2 + 1),   a = s scale - 1/2.

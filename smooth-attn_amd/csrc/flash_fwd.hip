@@ -341,8 +341,15 @@ __global__ __launch_bounds__(256, kQT == 1 ? SA_FLASH_MINB : 1) void flash_fwd_k
     // fp8 V staged through registers (widened to T in finish_tile).  Slot s
     // of a tile is written by wave (s / 64) % 4, instruction s / 256.
     u32x4 vst[V8 ? Gm::VNL : 1];
+    // Per-lane byte offsets of the DMA loads inside a tile (rows past T are
+    // clamped per tile below), so each load is a wave-uniform 64-bit tile
+    // base plus a 32-bit lane offset.
     auto issue_tile = [&](int j, int buf) {
         const int k0 = j * kBKV;
+        const int rmax = T_ - 1 - k0;  // last valid row of this tile
+        const unsigned char* kt_base = kp + static_cast<int64_t>(k0) * krs;
+        const unsigned char* vt_base = vp + static_cast<int64_t>(k0) * vrs;
+        const int krs32 = static_cast<int>(krs), vrs32 = static_cast<int>(vrs);
 #pragma unroll
         for (int i = 0; i < Gm::KNI; ++i) {
             const int sbase = (i * 4 + wave) * 64;
@@ -350,7 +357,7 @@ __global__ __launch_bounds__(256, kQT == 1 ? SA_FLASH_MINB : 1) void flash_fwd_k
                 const int sl = sbase + lane;
                 const int row = sl / Gm::KCPR;
                 const int c = (sl - row * Gm::KCPR) ^ Gm::swz_k(row);
-                dma16(kp + min(k0 + row, T_ - 1) * krs + c * 16, ldsK + buf * Gm::KT + sbase * 16);
+                dma16(kt_base + (min(row, rmax) * krs32 + c * 16), ldsK + buf * Gm::KT + sbase * 16);
             }
         }
         if constexpr (!V8) {
@@ -361,7 +368,7 @@ __global__ __launch_bounds__(256, kQT == 1 ? SA_FLASH_MINB : 1) void flash_fwd_k
                     const int sl = sbase + lane;
                     const int row = sl / Gm::VCPRL;
                     const int c = (sl - row * Gm::VCPRL) ^ Gm::swz_v(row);
-                    dma16(vp + min(k0 + row, T_ - 1) * vrs + c * 16, ldsVb + buf * Gm::VT + sbase * 16);
+                    dma16(vt_base + (min(row, rmax) * vrs32 + c * 16), ldsVb + buf * Gm::VT + sbase * 16);
                 }
             }
         } else {
@@ -494,13 +501,11 @@ __global__ __launch_bounds__(256, kQT == 1 ? SA_FLASH_MINB : 1) void flash_fwd_k
 #pragma unroll
                 for (int dt = 0; dt < D / 32; ++dt) {
                     const unsigned char* base = Vb + (16 * c) * Gm::VROWB + v_tr_off[dt];
-                    const uint2 lo = lds_read_tr16(base);
-                    const uint2 hi8 = lds_read_tr16(base + 8 * Gm::VROWB);
-                    const u32x4 aw{lo.x, lo.y, hi8.x, hi8.y};
+                    const Vec aw = lds_read_tr16_pair<Vec>(base, base + 8 * Gm::VROWB);
 #pragma unroll
                     for (int qt = 0; qt < kQT; ++qt) {
                         if (SA_FLASH_SKIPQT && !act[qt]) continue;
-                        oacc[qt][dt] = Ops::mma(as_vec8<Vec>(aw), bop[qt][ch], oacc[qt][dt]);
+                        oacc[qt][dt] = Ops::mma(aw, bop[qt][ch], oacc[qt][dt]);
                     }
                 }
             }
@@ -601,6 +606,9 @@ int launch_flash_d(const FlashParams& prm, int D, int exact, hipStream_t st) {
     }
 }
 
+// Largest K / V row stride (bytes) the tile loads address with 32-bit offsets.
+constexpr int64_t kMaxRowStrideBytes = int64_t(1) << 24;
+
 // (b, h, t) strides must keep every row start 16-byte aligned; d stride 1.
 bool strides_ok(const int64_t* s, int elem_bytes) {
     const int64_t a = 16 / elem_bytes;
@@ -616,6 +624,9 @@ int fill_params(FlashParams& prm, const void* q, const void* k, const void* v, v
     if (D != 32 && D != 64 && D != 128) return SA_ERR_UNSUPPORTED;
     if (!strides_ok(q_strides, qk_bytes) || !strides_ok(k_strides, qk_bytes) || !strides_ok(v_strides, v_bytes) ||
         !strides_ok(o_strides, 2) || !aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
+        return SA_ERR_BAD_STRIDE;
+    // K / V tile loads use 32-bit offsets within a tile of kBKV rows.
+    if (k_strides[2] * qk_bytes > kMaxRowStrideBytes || v_strides[2] * v_bytes > kMaxRowStrideBytes)
         return SA_ERR_BAD_STRIDE;
     prm.q = q;
     prm.k = k;

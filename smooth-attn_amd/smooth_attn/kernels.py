@@ -471,11 +471,17 @@ def sp2norm_flash_attention_eager(q, k, v, *, scale=None, window_size=0):
 _FLASH_HEAD_DIMS = (32, 64, 128)
 
 
+# Row strides above this are copied first (the kernels address K / V tiles
+# with 32-bit offsets).
+_MAX_ROW_STRIDE_BYTES = 1 << 24
+
+
 def _flash_operand(t):
     """The kernels take any (b, h, t) strides that are multiples of 8 elements
-    with a unit stride along D and a 16-byte aligned base; anything else is
-    copied to a contiguous tensor first."""
-    ok = t.stride(-1) == 1 and all(s % 8 == 0 for s in t.stride()[:-1]) and t.data_ptr() % 16 == 0
+    with a unit stride along D, a 16-byte aligned base and rows at most
+    16 MiB apart; anything else is copied to a contiguous tensor first."""
+    ok = (t.stride(-1) == 1 and all(s % 8 == 0 for s in t.stride()[:-1]) and t.data_ptr() % 16 == 0
+          and t.stride(-2) * t.element_size() <= _MAX_ROW_STRIDE_BYTES)
     return t if ok else t.clone(memory_format=torch.contiguous_format)
 
 
