@@ -230,6 +230,26 @@ int sa_paged_decode(const void* q, const void* k_cache, const void* v_cache,
                     float* workspace, int64_t workspace_bytes,
                     sa_stream_t stream);
 
+/*
+ * Paged-KV cache writer (the step before sa_paged_decode): for sequence b
+ * with current length context_lens[b] and new rows t < n_new,
+ *   pos = context_lens[b] + t,  page = block_table[b, pos / page_size]
+ *   k_cache[page, h, pos % page_size, :] = k_new[b, h, t, :]   (and v)
+ * k_new, v_new: [B, Hkv, n_new, D] (new_strides, d stride 1); caches as in
+ * sa_paged_decode.  Rows whose page index reaches max_pages or whose table
+ * entry is outside [0, n_pages) are skipped.  context_lens is not updated
+ * (the caller adds n_new).  dtype SA_BF16 or SA_F16; D a multiple of 8.
+ * No reference kernel: the reference fills caches with Python loops in its
+ * tests (tests/test_paged_attention.py:10-73).
+ */
+int sa_paged_kv_append(const void* k_new, const void* v_new, void* k_cache,
+                       void* v_cache, const int32_t* block_table,
+                       const int32_t* context_lens, int B, int Hkv, int n_new,
+                       int D, int page_size, int max_pages, int n_pages,
+                       const int64_t* new_strides, const int64_t* kc_strides,
+                       const int64_t* vc_strides, int64_t bt_stride, int dtype,
+                       sa_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

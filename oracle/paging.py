@@ -58,3 +58,31 @@ def random_paged_layout(context_lens, page_size, *, generator):
         table[b, :n] = perm[pos:pos + n]
         pos += n
     return table, total
+
+
+def append_kv(k_cache, v_cache, k_new, v_new, block_table, context_lens):
+    """Reference semantics of the paged-KV append, element by element on the
+    CPU (the reference fills caches with the same index arithmetic in its
+    test builders, tests/test_paged_attention.py:10-73): row t of sequence b
+    goes to page block_table[b, (ctx_b + t) // P], slot (ctx_b + t) % P;
+    rows whose page index is past the table or whose entry is outside the
+    cache are dropped.  Returns new (k_cache, v_cache) copies.
+
+    pinned by: appending a whole sequence into an empty cache reproduces
+    build_paged_cache, and appends in pieces equal one append.
+    """
+    kc, vc = k_cache.clone(), v_cache.clone()
+    n_pages, _, P, _ = kc.shape
+    B, H, n_new, _ = k_new.shape
+    for b in range(B):
+        for t in range(n_new):
+            pos = int(context_lens[b]) + t
+            pi = pos // P
+            if pi >= block_table.shape[1]:
+                continue
+            phys = int(block_table[b, pi])
+            if phys < 0 or phys >= n_pages:
+                continue
+            kc[phys, :, pos % P] = k_new[b, :, t]
+            vc[phys, :, pos % P] = v_new[b, :, t]
+    return kc, vc

@@ -46,6 +46,9 @@ SIGNATURES = {
     "sa_paged_decode": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
                                 c_int, c_int, c_int, c_int, c_int, _I64P, _I64P, _I64P, _I64P, c_int64, c_float,
                                 c_int, c_void_p, c_int64, c_void_p]),
+    "sa_paged_kv_append": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
+                                   c_int, c_int, c_int, c_int, c_int, _I64P, _I64P, _I64P, c_int64, c_int,
+                                   c_void_p]),
 }
 
 _lock = threading.Lock()

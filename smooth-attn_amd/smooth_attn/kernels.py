@@ -794,6 +794,44 @@ def sp2norm_paged_attention(q, k_cache, v_cache, block_table, context_lens, *, s
     return out
 
 
+def sp2norm_paged_kv_append(k_cache, v_cache, k_new, v_new, block_table, context_lens, *, block_size=16):
+    """Write ``n_new`` new tokens per sequence into the paged caches, at
+    positions ``context_lens[b] .. context_lens[b] + n_new - 1`` through the
+    block table; returns ``context_lens + n_new`` (a new int32 tensor).
+
+    k_new, v_new: [B, Hkv, n_new, D]; caches [n_pages, Hkv, block_size, D].
+    No counterpart in the reference, which builds its caches with Python
+    loops (tests/test_paged_attention.py:10-73)."""
+    assert k_new.ndim == 4 and v_new.shape == k_new.shape
+    B, H_kv, n_new, D = k_new.shape
+    assert k_cache.shape[1] == H_kv and k_cache.shape[3] == D and v_cache.shape == k_cache.shape
+    assert k_cache.shape[2] == block_size
+    if k_cache.dtype not in (torch.bfloat16, torch.float16) or v_cache.dtype != k_cache.dtype:
+        raise ValueError("paged caches must be bf16 or fp16 of one dtype")
+    for t in (k_cache, v_cache):
+        if t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:-1]) or t.data_ptr() % 16:
+            raise ValueError("paged caches need 16-byte aligned rows with unit stride along D")
+    k_new = _flash_operand(k_new.to(k_cache.dtype))
+    v_new = _flash_operand(v_new.to(k_cache.dtype))
+    if v_new.stride() != k_new.stride():  # one stride set serves both
+        k_new = k_new.clone(memory_format=torch.contiguous_format)
+        v_new = v_new.clone(memory_format=torch.contiguous_format)
+    block_table = block_table.to(torch.int32)
+    if block_table.stride(-1) != 1:
+        block_table = block_table.contiguous()
+    context_lens = context_lens.to(torch.int32).contiguous()
+    lib = _lib.load()
+    with torch.cuda.device(k_cache.device):
+        st = lib.sa_paged_kv_append(
+            k_new.data_ptr(), v_new.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), block_table.data_ptr(),
+            context_lens.data_ptr(), B, H_kv, n_new, D, block_size, block_table.shape[1], k_cache.shape[0],
+            _lib.strides(k_new), _lib.strides(k_cache), _lib.strides(v_cache), block_table.stride(0),
+            _DTYPE_CODE[k_cache.dtype], _stream(k_cache),
+        )
+    _lib.check(st, "sa_paged_kv_append")
+    return context_lens + n_new
+
+
 # ---------------------------------------------------------------------------
 # Timing helpers (kernels.py:322-336, :2832-2838): one event pair per
 # iteration on the current stream, median in microseconds.

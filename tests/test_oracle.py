@@ -384,3 +384,29 @@ def test_softmax_causal_vs_brute_prefixes():
     for i in range(L):
         np.testing.assert_allclose(y[:, i, : i + 1].numpy(), brute.softmax(x[:, i, : i + 1].numpy()),
                                    rtol=1e-13, atol=0)
+
+
+def test_append_kv_rebuilds_cache_and_composes():
+    B, H, T, D, P = 2, 3, 37, 8, 8
+    k = torch.randn(B, H, T, D, generator=_g(80), dtype=DTYPE)
+    v = torch.randn(B, H, T, D, generator=_g(81), dtype=DTYPE)
+    kc, vc, table, lens = paging.build_paged_cache(k, v, P, shuffle=True, generator=_g(82))
+    empty_k, empty_v = torch.zeros_like(kc), torch.zeros_like(vc)
+    zero = torch.zeros(B, dtype=torch.int32)
+    k1, v1 = paging.append_kv(empty_k, empty_v, k, v, table, zero)
+    torch.testing.assert_close(k1, kc, rtol=0, atol=0)
+    torch.testing.assert_close(v1, vc, rtol=0, atol=0)
+    # two appends (20 rows, then 17) equal one
+    k2, v2 = paging.append_kv(empty_k, empty_v, k[:, :, :20], v[:, :, :20], table, zero)
+    k2, v2 = paging.append_kv(k2, v2, k[:, :, 20:], v[:, :, 20:], table, zero + 20)
+    torch.testing.assert_close(k2, kc, rtol=0, atol=0)
+    torch.testing.assert_close(v2, vc, rtol=0, atol=0)
+    # rows past the table (page index >= max_pages) are dropped, nothing else changes
+    full = torch.full((B,), table.shape[1] * P, dtype=torch.int32)
+    k3, _ = paging.append_kv(kc, vc, k[:, :, :4], v[:, :, :4], table, full)
+    torch.testing.assert_close(k3, kc, rtol=0, atol=0)
+    # table entries outside the cache are dropped too
+    bad = table.clone()
+    bad[:, 0] = -1
+    k4, _ = paging.append_kv(empty_k, empty_v, k[:, :, :P], v[:, :, :P], bad, zero)
+    assert float(k4.abs().max()) == 0.0
