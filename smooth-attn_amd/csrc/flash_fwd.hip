@@ -34,7 +34,11 @@ namespace {
 #define SA_FLASH_MINB 2
 #endif
 constexpr int kBKV = SA_FLASH_BKV;  // keys per tile (multiple of 32)
-constexpr int kThreads = 256;
+#ifndef SA_FLASH_WAVES
+#define SA_FLASH_WAVES 4
+#endif
+constexpr int kWaves = SA_FLASH_WAVES;  // waves per block (each owns 32 query rows per tile)
+constexpr int kThreads = 64 * kWaves;
 
 struct FlashParams {
     const void* q;
@@ -166,26 +170,13 @@ __global__ __launch_bounds__(256) void rope_rotate_rows(const T* __restrict__ k,
     *reinterpret_cast<u32x4*>(dst + D / 2) = bb;
 }
 
-#ifndef SA_FLASH_SKIPQT
-#define SA_FLASH_SKIPQT 1
-#endif
-#ifndef SA_FLASH_SPLIT
-#define SA_FLASH_SPLIT 1
-#endif
-#ifndef SA_FLASH_TILE_NT
-#define SA_FLASH_TILE_NT 0
-#endif
 // K/V tile loads: every tile is read by all query blocks of its head, so
 // these loads are cached (a nontemporal load would stream past L2).
 template <typename T>
 __device__ __forceinline__ u32x4 tile_load16(const T* p) {
-    if (SA_FLASH_TILE_NT) return load16(p);
     return *reinterpret_cast<const u32x4*>(p);
 }
 
-#ifndef SA_FLASH_MAP
-#define SA_FLASH_MAP 2
-#endif
 // Block -> (query block, batch, query head).  Blocks are dealt to the 8 XCDs
 // round-robin by index.  When B*Hkv is a multiple of 8, XCD x gets the KV
 // heads u = x, x+8, ... together with all G query heads that read them (so
@@ -195,18 +186,7 @@ __device__ __forceinline__ u32x4 tile_load16(const T* p) {
 __device__ __forceinline__ void block_coords(const FlashParams& p, int& qb, int& b, int& hq) {
     const int id = blockIdx.x;
     const int BHk = p.B * p.Hkv;
-    if (SA_FLASH_MAP == 1 && (BHk & 7) == 0) {
-        const int x = id & 7;
-        const int j = id >> 3;
-        const int per_kv = p.G * p.nqb;
-        const int kvl = j / per_kv;
-        const int rem = j - kvl * per_kv;
-        const int u = kvl * 8 + x;  // (b, hk)
-        b = u / p.Hkv;
-        const int hk = u - b * p.Hkv;
-        qb = p.nqb - 1 - rem / p.G;
-        hq = hk * p.G + (rem - (rem / p.G) * p.G);
-    } else if (SA_FLASH_MAP == 2 && (BHk & 7) == 0) {
+    if ((BHk & 7) == 0) {
         const int x = id & 7;
         const int j = id >> 3;
         const int nh = (BHk >> 3) * p.G;  // query heads per XCD
@@ -238,10 +218,10 @@ __device__ __forceinline__ void block_coords(const FlashParams& p, int& qb, int&
 // 906 us on [4,32,4096,128]).  With QT = 2, wave w owns query tiles w and
 // w + 4 of the block, which balances the causal work of the four waves.
 constexpr int kQT = SA_FLASH_QT;
-constexpr int kBQ2 = 32 * 4 * kQT;  // query rows per block
+constexpr int kBQ2 = 32 * kWaves * kQT;  // query rows per block
 
 template <typename T, int D, bool QK8, bool V8, bool EXACT, bool ROPE>
-__global__ __launch_bounds__(256, kQT == 1 ? SA_FLASH_MINB : 1) void flash_fwd_kernel(FlashParams p) {
+__global__ __launch_bounds__(kThreads, kQT == 1 ? SA_FLASH_MINB * 4 / kWaves : 1) void flash_fwd_kernel(FlashParams p) {
     using Gm = Geom<T, D, QK8, V8>;
     using Ops = MfmaOps<T>;
     using Vec = typename Ops::vec8;
@@ -273,7 +253,7 @@ __global__ __launch_bounds__(256, kQT == 1 ? SA_FLASH_MINB : 1) void flash_fwd_k
     const int q_start = qb * kBQ2;
     int wq0[kQT];  // first query row of each of this wave's tiles
 #pragma unroll
-    for (int qt = 0; qt < kQT; ++qt) wq0[qt] = q_start + 32 * (wave + 4 * qt);
+    for (int qt = 0; qt < kQT; ++qt) wq0[qt] = q_start + 32 * (wave + kWaves * qt);
     const int W = p.window;
     const int n_kv = (T_ + kBKV - 1) / kBKV;
     const int kv_end = min((q_start + kBQ2 + kBKV - 1) / kBKV, n_kv);
@@ -352,7 +332,7 @@ __global__ __launch_bounds__(256, kQT == 1 ? SA_FLASH_MINB : 1) void flash_fwd_k
         const int krs32 = static_cast<int>(krs), vrs32 = static_cast<int>(vrs);
 #pragma unroll
         for (int i = 0; i < Gm::KNI; ++i) {
-            const int sbase = (i * 4 + wave) * 64;
+            const int sbase = (i * kWaves + wave) * 64;
             if ((kBKV * Gm::KCPR) % kThreads == 0 || sbase < kBKV * Gm::KCPR) {
                 const int sl = sbase + lane;
                 const int row = sl / Gm::KCPR;
@@ -363,7 +343,7 @@ __global__ __launch_bounds__(256, kQT == 1 ? SA_FLASH_MINB : 1) void flash_fwd_k
         if constexpr (!V8) {
 #pragma unroll
             for (int i = 0; i < Gm::VNI; ++i) {
-                const int sbase = (i * 4 + wave) * 64;
+                const int sbase = (i * kWaves + wave) * 64;
                 if ((kBKV * Gm::VCPRL) % kThreads == 0 || sbase < kBKV * Gm::VCPRL) {
                     const int sl = sbase + lane;
                     const int row = sl / Gm::VCPRL;
@@ -452,7 +432,7 @@ __global__ __launch_bounds__(256, kQT == 1 ? SA_FLASH_MINB : 1) void flash_fwd_k
                                    (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
 #pragma unroll
                     for (int qt = 0; qt < kQT; ++qt) {
-                        if (SA_FLASH_SKIPQT && !act[qt]) continue;
+                        if (!act[qt]) continue;
                         const i32x8 bv{(int)qreg[qt][dc][0].x, (int)qreg[qt][dc][0].y, (int)qreg[qt][dc][0].z,
                                        (int)qreg[qt][dc][0].w, (int)qreg[qt][dc][1].x, (int)qreg[qt][dc][1].y,
                                        (int)qreg[qt][dc][1].z, (int)qreg[qt][dc][1].w};
@@ -462,7 +442,7 @@ __global__ __launch_bounds__(256, kQT == 1 ? SA_FLASH_MINB : 1) void flash_fwd_k
                     const u32x4 a = *reinterpret_cast<const u32x4*>(krow + ((dc * 2 + hi) ^ kswz) * 16);
 #pragma unroll
                     for (int qt = 0; qt < kQT; ++qt) {
-                        if (SA_FLASH_SKIPQT && !act[qt]) continue;
+                        if (!act[qt]) continue;
                         s[qt] = Ops::mma(as_vec8<Vec>(a), as_vec8<Vec>(qreg[qt][dc][0]), s[qt]);
                     }
                 }
@@ -470,7 +450,7 @@ __global__ __launch_bounds__(256, kQT == 1 ? SA_FLASH_MINB : 1) void flash_fwd_k
             Vec bop[kQT][2];
 #pragma unroll
             for (int qt = 0; qt < kQT; ++qt) {
-                if (SA_FLASH_SKIPQT && !act[qt]) continue;
+                if (!act[qt]) continue;
                 // valid(key) <=> 0 <= qi - key < W_eff (W_eff = W, or INT_MAX
                 // for full causal): one unsigned compare per element.
                 const int dbase = wq0[qt] + l32 - k0 - hi * 4;
@@ -504,7 +484,7 @@ __global__ __launch_bounds__(256, kQT == 1 ? SA_FLASH_MINB : 1) void flash_fwd_k
                     const Vec aw = lds_read_tr16_pair<Vec>(base, base + 8 * Gm::VROWB);
 #pragma unroll
                     for (int qt = 0; qt < kQT; ++qt) {
-                        if (SA_FLASH_SKIPQT && !act[qt]) continue;
+                        if (!act[qt]) continue;
                         oacc[qt][dt] = Ops::mma(aw, bop[qt][ch], oacc[qt][dt]);
                     }
                 }
@@ -531,7 +511,7 @@ __global__ __launch_bounds__(256, kQT == 1 ? SA_FLASH_MINB : 1) void flash_fwd_k
         // every query tile fully sees it (no masks, no inactive tile)
         const bool interior = (k0 + kBKV - 1 <= wfirst) && !(W > 0 && k0 <= wlast + 31 - W);
         if (any) {
-            if (SA_FLASH_SPLIT && interior)
+            if (interior)
                 tile_step(std::false_type{}, buf, k0);
             else
                 tile_step(std::true_type{}, buf, k0);
