@@ -26,14 +26,21 @@
 //    Q, dO from LDS, P and dS on the VALU (their C layout is the B operand of
 //    the next products), then dV^T += dO^T P and dK^T += Q^T dS with dO^T,
 //    Q^T from the transposing LDS load.
-// Tiles are staged global -> registers -> LDS, double buffered with one
-// barrier per tile, as in the forward.
+// Tiles go straight from global memory into LDS (global_load_lds, double
+// buffered, one barrier per tile), as in the forward.
 #include "flash_common.hpp"
 
 namespace sa {
 namespace {
 
 constexpr int kBwdThreads = 256;
+// Two blocks per CU for both kernels: the register budget is then 256 per
+// lane and the compiler keeps every MFMA in the VGPR form (with one block per
+// CU it moves the accumulators through AGPRs, which costs more than the few
+// dK/dV registers that now spill).
+#ifndef SA_BWD_DKDV_MINB
+#define SA_BWD_DKDV_MINB 2
+#endif
 constexpr int kBwdBQ = 128;   // query rows per dQ block (32 per wave)
 constexpr int kBwdKT = 64;    // keys per staged tile in the dQ kernel
 constexpr int kBwdBK = 128;   // key rows per dK/dV block (32 per wave)
@@ -58,20 +65,68 @@ struct BwdParams {
 // Plain (cached) 16-byte global load: tiles here are re-read by many blocks.
 __device__ __forceinline__ u32x4 ldg16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 
-// Per-lane element offset of the transposing read of a row-major [rows][RS]
-// tile as the A operand (rows of the tile become the MFMA k index, in the
-// order the C -> B operand reuse produces; see flash_common.hpp).
-template <int RS>
-__device__ __forceinline__ int tr_offset(int lane) {
-    return ((lane >> 5) * 4 + ((lane & 15) >> 2)) * RS + ((lane >> 4) & 1) * 16 + 4 * (lane & 3);
+// Staged tiles are unpadded [64 rows][D] of the 16-bit type, filled by direct
+// global->LDS loads (one 1 KB span of consecutive 16-byte chunks per wave
+// instruction).  Each tile is read two ways: as 16-byte A-operand rows (8
+// consecutive rows per LDS cycle, same chunk) and through the transposing
+// read (per 16 lanes: 4 consecutive rows x 32 bytes).  Storing logical chunk
+// c of row r at c ^ f(r), with f(r) built from bits 0-2 of r, keeps both
+// patterns free of bank conflicts: f takes 8 distinct values on 8
+// consecutive rows, and f >> 1 takes 4 distinct values on rows 4k..4k+3.
+template <int D>
+struct SwzTile {
+    static constexpr int ROWB = D * 2;     // bytes per row
+    static constexpr int CPR = D / 8;      // 16-byte chunks per row
+    static constexpr int BYTES = 64 * ROWB;
+    static constexpr int NI = 64 * CPR / kBwdThreads;  // DMA loads per lane per tile
+    static __device__ __forceinline__ int f(int r) {
+        if constexpr (CPR >= 8) return ((r & 3) << 1) | ((r >> 2) & 1);
+        else return (((r >> 1) & 1) << 1) | ((r >> 2) & 1);
+    }
+    // Byte offset of A-operand chunk c of row r.
+    static __device__ __forceinline__ int row_off(int r, int c) { return r * ROWB + ((c ^ f(r)) << 4); }
+    // Per-lane byte offset of the transposing reads of 32-column block dt
+    // (rows vr and vr + 8 of each 16-row chunk; f is the same for both).
+    static __device__ __forceinline__ int tr_off(int lane, int dt) {
+        const int vr = (lane >> 5) * 4 + ((lane & 15) >> 2);
+        const int chunk = (dt * 4 + ((lane >> 4) & 1) * 2 + ((lane & 3) >> 1)) ^ f(vr);
+        return vr * ROWB + chunk * 16 + (lane & 1) * 8;
+    }
+};
+
+// A operand = (16 rows x 32 columns of a tile)^T via two transposing reads;
+// p points at row 16c of the tile plus the lane's tr_off.
+template <typename Vec, int ROWB>
+__device__ __forceinline__ Vec tr_operand(const unsigned char* p) {
+    return lds_read_tr16_pair<Vec>(p, p + 8 * ROWB);
 }
 
-// A operand = (16 rows x 32 columns of a row-major tile)^T via two transposing reads.
-template <typename Vec, int RS, typename T>
-__device__ __forceinline__ Vec tr_operand(const T* base) {
-    const uint2 lo = lds_read_tr16(base);
-    const uint2 hi = lds_read_tr16(base + 8 * RS);
-    return as_vec8<Vec>(u32x4{lo.x, lo.y, hi.x, hi.y});
+typedef __attribute__((address_space(3))) void bwd_lds_void_t;
+typedef __attribute__((address_space(1))) void bwd_glb_void_t;
+
+// One 16-byte global -> LDS load per lane at lds_base + 16 * lane (wave-uniform base).
+__device__ __forceinline__ void dma16(const void* g, void* lds_base) {
+    __builtin_amdgcn_global_load_lds((bwd_glb_void_t*)(g), (bwd_lds_void_t*)(lds_base), 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(0): this wave's direct-to-LDS loads have landed.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Issue the DMA loads of one [64][D] tile: rows row0 .. row0 + 63 of the
+// matrix at `base` (row stride rsb bytes), rows past `rmax` (relative)
+// clamped, into the swizzled LDS tile at `dst`.
+template <int D>
+__device__ __forceinline__ void issue_swz_tile(const unsigned char* base, int rsb, int rmax, unsigned char* dst,
+                                               int wave, int lane) {
+    using Tl = SwzTile<D>;
+#pragma unroll
+    for (int i = 0; i < Tl::NI; ++i) {
+        const int sbase = (i * 4 + wave) * 64;
+        const int sl = sbase + lane;
+        const int row = sl / Tl::CPR;
+        const int c = (sl - row * Tl::CPR) ^ Tl::f(row);
+        dma16(base + (min(row, rmax) * rsb + c * 16), dst + sbase * 16);
+    }
 }
 
 template <bool EXACT>
@@ -88,15 +143,11 @@ __device__ __forceinline__ void weight_and_rr(float s, float sc, float& y, float
 // dQ (and delta)
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool EXACT>
-__global__ __launch_bounds__(kBwdThreads) void flash_bwd_dq_kernel(BwdParams p) {
+__global__ __launch_bounds__(kBwdThreads, 2) void flash_bwd_dq_kernel(BwdParams p) {
     using Ops = MfmaOps<T>;
     using Vec = typename Ops::vec8;
-    constexpr int RS = D + 8;            // LDS row stride (elements)
-    constexpr int TILE = kBwdKT * RS;    // elements per staged tile
-    constexpr int CPR = D / 8;           // 16-byte chunks per row
-    constexpr int NL = kBwdKT * CPR / kBwdThreads;  // chunks per thread per tile
-    static_assert(NL >= 1 && (kBwdKT * CPR) % kBwdThreads == 0, "tile must split evenly");
-    __shared__ __attribute__((aligned(16))) T lds[2][2][TILE];  // [buf][K, V]
+    using Tl = SwzTile<D>;
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[2 * 2 * Tl::BYTES];  // [buf][K, V]
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -157,41 +208,25 @@ __global__ __launch_bounds__(kBwdThreads) void flash_bwd_dq_kernel(BwdParams p) 
     const int kv_begin = W > 0 ? max(0, q_start - W + 1) / kBwdKT : 0;
     const float sc = p.scale;
 
-    u32x4 kst[NL], vst[NL];
-    auto load_tile = [&](int j) {
+    const int ksb = static_cast<int>(p.ks[2] * 2), vsb = static_cast<int>(p.vs[2] * 2);  // row strides (bytes)
+    auto issue_tile = [&](int j, int buf) {
         const int k0 = j * kBwdKT;
-#pragma unroll
-        for (int i = 0; i < NL; ++i) {
-            const int ci = tid + kBwdThreads * i;
-            const int row = ci / CPR;
-            const int c = ci - row * CPR;
-            const int gr = min(k0 + row, T_ - 1);
-            kst[i] = ldg16(kp + gr * p.ks[2] + c * 8);
-            vst[i] = ldg16(vp + gr * p.vs[2] + c * 8);
-        }
-    };
-    auto store_tile = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < NL; ++i) {
-            const int ci = tid + kBwdThreads * i;
-            const int row = ci / CPR;
-            const int c = ci - row * CPR;
-            *reinterpret_cast<u32x4*>(&lds[buf][0][row * RS + c * 8]) = kst[i];
-            *reinterpret_cast<u32x4*>(&lds[buf][1][row * RS + c * 8]) = vst[i];
-        }
+        issue_swz_tile<D>(reinterpret_cast<const unsigned char*>(kp) + static_cast<int64_t>(k0) * ksb, ksb,
+                          T_ - 1 - k0, lds + (2 * buf) * Tl::BYTES, wave, lane);
+        issue_swz_tile<D>(reinterpret_cast<const unsigned char*>(vp) + static_cast<int64_t>(k0) * vsb, vsb,
+                          T_ - 1 - k0, lds + (2 * buf + 1) * Tl::BYTES, wave, lane);
     };
 
-    const int troff = tr_offset<RS>(lane);
-    load_tile(kv_begin);
-    store_tile(0);
+    issue_tile(kv_begin, 0);
+    wait_vmem();
     __syncthreads();
     for (int j = kv_begin; j < kv_end; ++j) {
         const int buf = (j - kv_begin) & 1;
         const bool has_next = j + 1 < kv_end;
-        if (has_next) load_tile(j + 1);
+        if (has_next) issue_tile(j + 1, buf ^ 1);
         const int k0 = j * kBwdKT;
-        const T* Kb = lds[buf][0];
-        const T* Vb = lds[buf][1];
+        const unsigned char* Kb = lds + (2 * buf) * Tl::BYTES;
+        const unsigned char* Vb = lds + (2 * buf + 1) * Tl::BYTES;
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
             const int kh0 = k0 + kt * 32;
@@ -199,16 +234,16 @@ __global__ __launch_bounds__(kBwdThreads) void flash_bwd_dq_kernel(BwdParams p) 
             const bool act = (kh0 <= wq0 + 31) && !(W > 0 && kh0 + 31 <= wq0 - W);
             if (!act) continue;
             f32x16 s = f32x16{}, dp = f32x16{};
-            const T* krow = Kb + (kt * 32 + l32) * RS + hi * 8;
-            const T* vrow = Vb + (kt * 32 + l32) * RS + hi * 8;
+            const int r = kt * 32 + l32;
 #pragma unroll
             for (int dc = 0; dc < D / 16; ++dc) {
-                const u32x4 ka = *reinterpret_cast<const u32x4*>(krow + dc * 16);
-                const u32x4 va = *reinterpret_cast<const u32x4*>(vrow + dc * 16);
+                const int off = Tl::row_off(r, dc * 2 + hi);
+                const u32x4 ka = *reinterpret_cast<const u32x4*>(Kb + off);
+                const u32x4 va = *reinterpret_cast<const u32x4*>(Vb + off);
                 s = Ops::mma(as_vec8<Vec>(ka), as_vec8<Vec>(qreg[dc]), s);
                 dp = Ops::mma(as_vec8<Vec>(va), as_vec8<Vec>(doreg[dc]), dp);
             }
-            // C layout: column = query l32, rows = keys kh0 + (v/4)*8 + 4 hi + v%4.
+        // C layout: column = query l32, rows = keys kh0 + (v/4)*8 + 4 hi + v%4.
             const int dbase = qi - kh0 - hi * 4;
             float ds[16];
 #pragma unroll
@@ -230,10 +265,11 @@ __global__ __launch_bounds__(kBwdThreads) void flash_bwd_dq_kernel(BwdParams p) 
                 const int c = 2 * kt + ch;  // 16-key chunk of the tile
 #pragma unroll
                 for (int dt = 0; dt < D / 32; ++dt)
-                    acc[dt] = Ops::mma(tr_operand<Vec, RS>(Kb + 16 * c * RS + dt * 32 + troff), bop, acc[dt]);
+                    acc[dt] = Ops::mma(tr_operand<Vec, Tl::ROWB>(Kb + 16 * c * Tl::ROWB + Tl::tr_off(lane, dt)), bop,
+                                       acc[dt]);
             }
         }
-        if (has_next) store_tile(buf ^ 1);
+        wait_vmem();
         __syncthreads();
     }
 
@@ -259,15 +295,12 @@ __global__ __launch_bounds__(kBwdThreads) void flash_bwd_dq_kernel(BwdParams p) 
 // dK, dV
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool EXACT>
-__global__ __launch_bounds__(kBwdThreads) void flash_bwd_dkdv_kernel(BwdParams p) {
+__global__ __launch_bounds__(kBwdThreads, SA_BWD_DKDV_MINB) void flash_bwd_dkdv_kernel(BwdParams p) {
     using Ops = MfmaOps<T>;
     using Vec = typename Ops::vec8;
-    constexpr int RS = D + 8;
-    constexpr int TILE = kBwdQT * RS;
-    constexpr int CPR = D / 8;
-    constexpr int NL = kBwdQT * CPR / kBwdThreads;
-    static_assert(NL >= 1 && (kBwdQT * CPR) % kBwdThreads == 0, "tile must split evenly");
-    __shared__ __attribute__((aligned(16))) T lds[2][2][TILE];         // [buf][Q, dO]
+    using Tl = SwzTile<D>;
+    static_assert(kBwdQT == 64, "query tiles are 64 rows");
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[2 * 2 * Tl::BYTES];  // [buf][Q, dO]
     __shared__ __attribute__((aligned(16))) float ldr[2][2][kBwdQT];   // [buf][1/R, delta]
 
     const int tid = threadIdx.x;
@@ -318,54 +351,43 @@ __global__ __launch_bounds__(kBwdThreads) void flash_bwd_dkdv_kernel(BwdParams p
     const int n_it = p.G * nq;
     const float sc = p.scale;
 
-    u32x4 qst[NL], dst[NL];
+    const int qsb = static_cast<int>(p.qs[2] * 2), dsb = static_cast<int>(p.dos[2] * 2);  // row strides (bytes)
     float rst = 0.f;
-    auto load_tile = [&](int it) {
+    auto issue_tile = [&](int it, int buf) {
         const int g = it / nq;
         const int qt = qt_begin + (it - g * nq);
         const int hq = hk * p.G + g;
-        const T* qp = static_cast<const T*>(p.q) + b * p.qs[0] + hq * p.qs[1];
-        const T* dop = static_cast<const T*>(p.dout) + b * p.dos[0] + hq * p.dos[1];
+        const unsigned char* qp = reinterpret_cast<const unsigned char*>(static_cast<const T*>(p.q) + b * p.qs[0] +
+                                                                          hq * p.qs[1]);
+        const unsigned char* dop = reinterpret_cast<const unsigned char*>(static_cast<const T*>(p.dout) +
+                                                                           b * p.dos[0] + hq * p.dos[1]);
         const int q0 = qt * kBwdQT;
-#pragma unroll
-        for (int i = 0; i < NL; ++i) {
-            const int ci = tid + kBwdThreads * i;
-            const int row = ci / CPR;
-            const int c = ci - row * CPR;
-            const int gr = min(q0 + row, T_ - 1);
-            qst[i] = ldg16(qp + gr * p.qs[2] + c * 8);
-            dst[i] = ldg16(dop + gr * p.dos[2] + c * 8);
-        }
+        issue_swz_tile<D>(qp + static_cast<int64_t>(q0) * qsb, qsb, T_ - 1 - q0, lds + (2 * buf) * Tl::BYTES, wave,
+                          lane);
+        issue_swz_tile<D>(dop + static_cast<int64_t>(q0) * dsb, dsb, T_ - 1 - q0, lds + (2 * buf + 1) * Tl::BYTES,
+                          wave, lane);
         if (tid < 2 * kBwdQT) {
             const int r = tid & (kBwdQT - 1);
             const int64_t idx = (static_cast<int64_t>(b) * p.Hq + hq) * T_ + min(q0 + r, T_ - 1);
             rst = tid < kBwdQT ? 1.f / p.rs[idx] : p.delta[idx];
         }
     };
-    auto store_tile = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < NL; ++i) {
-            const int ci = tid + kBwdThreads * i;
-            const int row = ci / CPR;
-            const int c = ci - row * CPR;
-            *reinterpret_cast<u32x4*>(&lds[buf][0][row * RS + c * 8]) = qst[i];
-            *reinterpret_cast<u32x4*>(&lds[buf][1][row * RS + c * 8]) = dst[i];
-        }
+    auto store_rs = [&](int buf) {
         if (tid < 2 * kBwdQT) ldr[buf][tid / kBwdQT][tid & (kBwdQT - 1)] = rst;
     };
 
-    const int troff = tr_offset<RS>(lane);
-    load_tile(0);
-    store_tile(0);
+    issue_tile(0, 0);
+    store_rs(0);
+    wait_vmem();
     __syncthreads();
     for (int it = 0; it < n_it; ++it) {
         const int buf = it & 1;
         const bool has_next = it + 1 < n_it;
-        if (has_next) load_tile(it + 1);
+        if (has_next) issue_tile(it + 1, buf ^ 1);
         const int g = it / nq;
         const int q0 = (qt_begin + (it - g * nq)) * kBwdQT;
-        const T* Qb = lds[buf][0];
-        const T* Ob = lds[buf][1];
+        const unsigned char* Qb = lds + (2 * buf) * Tl::BYTES;
+        const unsigned char* Ob = lds + (2 * buf + 1) * Tl::BYTES;
 #pragma unroll
         for (int qh = 0; qh < 2; ++qh) {
             const int qh0 = q0 + qh * 32;
@@ -373,12 +395,12 @@ __global__ __launch_bounds__(kBwdThreads) void flash_bwd_dkdv_kernel(BwdParams p
             const bool act = (qh0 + 31 >= wk0) && !(W > 0 && qh0 - (wk0 + 31) >= W) && qh0 < T_;
             if (!act) continue;
             f32x16 s = f32x16{}, dp = f32x16{};
-            const T* qrow = Qb + (qh * 32 + l32) * RS + hi * 8;
-            const T* orow = Ob + (qh * 32 + l32) * RS + hi * 8;
+            const int r = qh * 32 + l32;
 #pragma unroll
             for (int dc = 0; dc < D / 16; ++dc) {
-                const u32x4 qa = *reinterpret_cast<const u32x4*>(qrow + dc * 16);
-                const u32x4 oa = *reinterpret_cast<const u32x4*>(orow + dc * 16);
+                const int off = Tl::row_off(r, dc * 2 + hi);
+                const u32x4 qa = *reinterpret_cast<const u32x4*>(Qb + off);
+                const u32x4 oa = *reinterpret_cast<const u32x4*>(Ob + off);
                 s = Ops::mma(as_vec8<Vec>(qa), as_vec8<Vec>(kreg[dc]), s);
                 dp = Ops::mma(as_vec8<Vec>(oa), as_vec8<Vec>(vreg[dc]), dp);
             }
@@ -421,12 +443,14 @@ __global__ __launch_bounds__(kBwdThreads) void flash_bwd_dkdv_kernel(BwdParams p
                 const int c = 2 * qh + ch;  // 16-query chunk of the tile
 #pragma unroll
                 for (int dt = 0; dt < D / 32; ++dt) {
-                    dvacc[dt] = Ops::mma(tr_operand<Vec, RS>(Ob + 16 * c * RS + dt * 32 + troff), bp, dvacc[dt]);
-                    dkacc[dt] = Ops::mma(tr_operand<Vec, RS>(Qb + 16 * c * RS + dt * 32 + troff), bs, dkacc[dt]);
+                    const int to = 16 * c * Tl::ROWB + Tl::tr_off(lane, dt);
+                    dvacc[dt] = Ops::mma(tr_operand<Vec, Tl::ROWB>(Ob + to), bp, dvacc[dt]);
+                    dkacc[dt] = Ops::mma(tr_operand<Vec, Tl::ROWB>(Qb + to), bs, dkacc[dt]);
                 }
             }
         }
-        if (has_next) store_tile(buf ^ 1);
+        if (has_next) store_rs(buf ^ 1);
+        wait_vmem();
         __syncthreads();
     }
 
@@ -500,6 +524,9 @@ extern "C" int sa_flash_bwd(const void* q, const void* k, const void* v, const v
     const int64_t* all[8] = {q_strides, k_strides, v_strides, o_strides, do_strides, dq_strides, dk_strides, dv_strides};
     for (const int64_t* s : all)
         if (!bwd_strides_ok(s)) return SA_ERR_BAD_STRIDE;
+    // Q / K / V / dO tiles are addressed with 32-bit offsets within 64 rows.
+    for (const int64_t* st : {q_strides, k_strides, v_strides, do_strides})
+        if (st[2] * 2 > (int64_t(1) << 24)) return SA_ERR_BAD_STRIDE;
     const void* ptrs[8] = {q, k, v, o, dout, dq, dk, dv};
     for (const void* ptr : ptrs)
         if (!aligned16(ptr)) return SA_ERR_BAD_STRIDE;
