@@ -10,11 +10,14 @@ step / step time.  Algorithmic bytes: the forward reads the causal triangle
 of x and writes the full output; the backward reads the triangle of x and
 dy and writes the full dx (2 bytes per element).
 
-The same JSON line carries the fused-attention figure the metric also names
-(config 3, TFLOP/s over the causal triangle), the roofline of the dominant
-kernel (from HIP events around each launch), and the CPU baseline: the
-reference's eager CPU path restated in oracle/ (fp32 torch on the host
-cores), timed on a bounded sample of the same workload.
+The same JSON line carries the fused-attention figures the metric also names
+(config 3 forward and backward, TFLOP/s over the causal triangle), config 4
+(fp8), config 5 (paged decode), config 2 at L = 1024 / 2048 with its
+row-wise fp32 variant, config 1's shape on the GPU, the roofline of the
+dominant kernel (from HIP events around each launch), and the CPU
+baselines: the reference's eager CPU path restated in oracle/ (fp32 torch
+on the host cores), timed on a bounded sample of the config 2 workload and
+on config 1 at full shape.
 """
 from __future__ import annotations
 
@@ -253,6 +256,74 @@ def bench_paged(torch, iters):
     }
 
 
+def bench_norm_sizes(torch, sa, iters):
+    """Config 2 at the other lengths (causal bf16, L = 1024, 2048), its
+    row-wise fp32 variant (x, dy fp32 [64 L, L], L = 1024, 2048, 4096) and
+    config 1's shape on the GPU: kernel times from HIP events."""
+    from smooth_attn import FamilyConfig, kernels
+
+    fam = FamilyConfig()
+    dev = torch.device("cuda:0")
+    out = {"causal_bf16": [], "rowwise_fp32": []}
+    for L in (1024, 2048):
+        gen = torch.Generator(device=dev).manual_seed(20 + L)
+        x = (torch.randn(4, 16, L, L, generator=gen, device=dev) / math.sqrt(128)).to(torch.bfloat16)
+        dy = torch.randn(4, 16, L, L, generator=gen, device=dev).to(torch.bfloat16)
+        y = torch.empty_like(x)
+        f = time_events(torch, lambda: sa.softplus_norm_causal_triton_out(y, x, family=fam), iters)
+        b = time_events(torch, lambda: kernels._softplus_norm_causal_backward(x, dy, fam), iters)
+        fb, bb = norm_bytes(4, 16, L)
+        fus, bus = 1e3 * sum(f) / len(f), 1e3 * sum(b) / len(b)
+        out["causal_bf16"].append({"L": L, "fwd_us": round(fus, 2), "bwd_us": round(bus, 2),
+                                   "GBs": round((fb + bb) / ((fus + bus) * 1e-6) / 1e9, 1),
+                                   "frac_hbm_peak": round((fb + bb) / ((fus + bus) * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+        del x, dy, y
+    for L in (1024, 2048, 4096):
+        gen = torch.Generator(device=dev).manual_seed(30 + L)
+        x = torch.randn(64 * L, L, generator=gen, device=dev) / math.sqrt(128)
+        dy = torch.randn(64 * L, L, generator=gen, device=dev)
+        y = torch.empty_like(x)
+        dx = torch.empty_like(x)
+        f = time_events(torch, lambda: sa.softplus_norm_triton_out(y, x, family=fam), iters)
+        b = time_events(torch, lambda: kernels._norm_bwd_2d(x, dy, dx, fam, causal=False), iters)
+        fb, bb = 64 * 8 * L * L, 64 * 12 * L * L
+        fus, bus = 1e3 * sum(f) / len(f), 1e3 * sum(b) / len(b)
+        out["rowwise_fp32"].append({"L": L, "fwd_us": round(fus, 2), "bwd_us": round(bus, 2),
+                                    "GBs": round((fb + bb) / ((fus + bus) * 1e-6) / 1e9, 1),
+                                    "frac_hbm_peak": round((fb + bb) / ((fus + bus) * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+        del x, dy, y, dx
+    torch.cuda.empty_cache()
+    gen = torch.Generator(device=dev).manual_seed(1)
+    x1 = torch.randn(2, 8, 512, 512, generator=gen, device=dev).to(torch.bfloat16)
+    y1 = torch.empty_like(x1)
+    t1 = time_events(torch, lambda: sa.softplus_norm_causal_triton_out(y1, x1, family=fam), iters)
+    b1 = 16 * (2 * tri(512) + 2 * 512 * 512)
+    us1 = 1e3 * sum(t1) / len(t1)
+    out["config1_gpu_fwd"] = {"shape": [2, 8, 512, 512], "us": round(us1, 2), "bytes": b1,
+                              "GBs": round(b1 / (us1 * 1e-6) / 1e9, 1)}
+    return out
+
+
+def cpu_config1(torch, budget_s=10.0):
+    """Config 1: the reference's CPU eager forward at full shape
+    ([2,8,512,512] bf16), the oracle restatement, median of <= 7 runs."""
+    from oracle import eager
+
+    x = torch.randn(2, 8, 512, 512, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
+    eager.softplus_norm_causal_cpu_path(x)
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 7 and (time.perf_counter() - t_start) < budget_s:
+        t0 = time.perf_counter()
+        eager.softplus_norm_causal_cpu_path(x)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    b1 = 16 * (2 * tri(512) + 2 * 512 * 512)
+    return {"shape": [2, 8, 512, 512], "ms": round(med * 1e3, 3), "GBs": round(b1 / med / 1e9, 3),
+            "threads": torch.get_num_threads()}
+
+
 def cpu_baseline(torch, sample, budget_s=20.0):
     """The reference's eager CPU path (oracle restatement, fp32 torch) on one
     [L, L] matrix of the benchmark input: forward + autograd backward."""
@@ -331,7 +402,7 @@ def main():
     log("bench: causal norm fwd+bwd [4,16,4096,4096] bf16")
     norm = bench_norm(torch, sa, args.steps, args.warmup)
     log(f"bench: norm {norm['ms_per_step']:.3f} ms/step, fwd {norm['fwd_us']:.1f} us, bwd {norm['bwd_us']:.1f} us")
-    attn = fp8 = paged = None
+    attn = fp8 = paged = sizes = None
     if not args.no_extra:
         log("bench: fused attention config 3")
         attn = bench_attention(torch, sa, max(args.steps, 10))
@@ -342,11 +413,16 @@ def main():
         log("bench: paged decode config 5")
         paged = bench_paged(torch, max(args.steps, 20))
         log(f"bench: paged {paged}")
+        log("bench: config 2 other lengths, row-wise fp32, config 1 shape")
+        sizes = bench_norm_sizes(torch, sa, max(args.steps, 10))
+        log(f"bench: sizes {sizes}")
     cpu = None
     if not args.no_cpu:
         log("bench: cpu baseline")
         cpu = cpu_baseline(torch, norm["sample"])
         log(f"bench: cpu {cpu['value']:.3f} GB/s")
+        if sizes is not None:
+            sizes["config1_cpu_eager_fwd"] = cpu_config1(torch)
 
     dominant = "bwd" if norm["bwd_us"] >= norm["fwd_us"] else "fwd"
     achieved = norm[f"{dominant}_gbs"]
@@ -386,6 +462,7 @@ def main():
         "attention": attn,
         "fp8_attention": fp8,
         "paged_decode": paged,
+        "norm_other_sizes": sizes,
     }
     print(json.dumps(line), flush=True)
 
