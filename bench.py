@@ -42,7 +42,7 @@ FP8_PEAK_TFLOPS = 5033.2
 # (--copy-calibration) and scaled by what the same counters read for a plain
 # 1 GiB device copy: FETCH_SIZE x 2.000, WRITE_SIZE x 1.000.  The counter
 # summary and commands are kept under profiles/.
-NORM_TRAFFIC_BYTES = {"fwd": 3.2525e9, "bwd": 4.3557e9}
+NORM_TRAFFIC_BYTES = {"fwd": 3.2393e9, "bwd": 4.3325e9}
 METRIC = "causal-norm fwd+bwd HBM GB/s (% peak); fused attn TFLOP/s, L=4096 D=128"
 
 
@@ -450,7 +450,7 @@ def main():
             "compute_dtype": "f32",
         },
         "roofline": {
-            "kernel": f"norm_{dominant}_vec (causal, bf16, L=4096)",
+            "kernel": f"norm_{dominant}_split<R=4> (causal, bf16, L=4096)",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
