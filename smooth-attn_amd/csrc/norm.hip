@@ -218,17 +218,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<T
 // keeps only NCH / R chunks in registers.  Shorter per-wave work keeps the
 // rows in flight in a denser address window.
 // ---------------------------------------------------------------------------
+template <int R>
+constexpr int split_block_waves() { return R > kWavesPerBlock ? R : kWavesPerBlock; }
+
 template <typename T, int NCH, int POWER, int R>
-__global__ __launch_bounds__(256) void norm_fwd_split(const T* __restrict__ x, T* __restrict__ y, int64_t n_rows,
+__global__ __launch_bounds__(64 * split_block_waves<R>()) void norm_fwd_split(const T* __restrict__ x, T* __restrict__ y, int64_t n_rows,
                                                       int n_cols, int64_t xs, int64_t ys, int causal, float alpha,
                                                       float neg_alpha_theta, float eps_scaled) {
     constexpr int VEC = 16 / sizeof(T);
     constexpr int NW = NCH / R;  // chunks per wave
-    __shared__ float red[kWavesPerBlock];
+    constexpr int SW = split_block_waves<R>();
+    __shared__ float red[SW];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wr = wave % R;
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * (kWavesPerBlock / R) + wave / R;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * (SW / R) + wave / R;
     const bool valid = row < n_rows;
     const int qpos = valid ? (causal ? static_cast<int>(row % n_cols) : n_cols - 1) : -1;
     const int limit = qpos + 1;
@@ -290,18 +294,19 @@ __global__ __launch_bounds__(256) void norm_fwd_split(const T* __restrict__ x, T
 }
 
 template <typename T, typename TG, int NCH, int POWER, int R>
-__global__ __launch_bounds__(256) void norm_bwd_split(const T* __restrict__ x, const TG* __restrict__ dy,
+__global__ __launch_bounds__(64 * split_block_waves<R>()) void norm_bwd_split(const T* __restrict__ x, const TG* __restrict__ dy,
                                                       T* __restrict__ dx, int64_t n_rows, int n_cols, int64_t xs,
                                                       int64_t gs, int64_t dxs, int causal, float alpha,
                                                       float neg_alpha_theta, float eps_scaled) {
     constexpr int VEC = 16 / sizeof(T);
     constexpr int GW = (VEC * static_cast<int>(sizeof(TG))) / 16;
     constexpr int NW = NCH / R;
-    __shared__ float red[kWavesPerBlock][2];
+    constexpr int SW = split_block_waves<R>();
+    __shared__ float red[SW][2];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wr = wave % R;
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * (kWavesPerBlock / R) + wave / R;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * (SW / R) + wave / R;
     const bool valid = row < n_rows;
     const int qpos = valid ? (causal ? static_cast<int>(row % n_cols) : n_cols - 1) : -1;
     const int limit = qpos + 1;
@@ -463,7 +468,14 @@ constexpr int kMaxCols = 8192;
 // chunks up.  Measured: causal bf16 L=4096 fwd 3-4% and bwd 1-3% faster,
 // row-wise fp32 L=2048 6% faster; for rows of 2-4 chunks (causal bf16
 // L=1024/2048) splitting was 11-17% slower, so those keep one wave per row.
+// (8 waves per row, one chunk per wave at bf16 L=4096, measured 17% slower.)
 constexpr int split_for(int nch) { return nch >= 8 ? 4 : 1; }
+
+template <int R>
+dim3 split_grid(int64_t n_rows) {
+    constexpr int rows = split_block_waves<R>() / R;  // rows per block
+    return dim3(static_cast<unsigned>((n_rows + rows - 1) / rows));
+}
 
 int chunks_for(int n_cols, int vec) {
     const int need = (n_cols + 64 * vec - 1) / (64 * vec);
@@ -493,8 +505,8 @@ int launch_fwd_t(const void* x, void* y, int64_t n_rows, int n_cols, int64_t xs,
 #define SA_FWD_CASE(N)                                                                                  \
     case N:                                                                                             \
         if constexpr (split_for(N) > 1)                                                                 \
-            norm_fwd_split<T, N, POWER, split_for(N)>                                                   \
-                <<<dim3((n_rows + 4 / split_for(N) - 1) / (4 / split_for(N))), block, 0, st>>>(          \
+            norm_fwd_split<T, N, POWER, split_for(N)><<<split_grid<split_for(N)>(n_rows),              \
+                                                            64 * split_block_waves<split_for(N)>(), 0, st>>>( \
                     xp, yp, n_rows, n_cols, xs, ys, causal, alpha, nat, eps);                           \
         else                                                                                            \
             norm_fwd_vec<T, N, POWER><<<grid, block, 0, st>>>(xp, yp, n_rows, n_cols, xs, ys, causal, alpha, \
@@ -547,8 +559,8 @@ int launch_bwd_t(const void* x, const void* dy, void* dx, int64_t n_rows, int n_
 #define SA_BWD_CASE(N)                                                                                   \
     case N:                                                                                              \
         if constexpr (split_for(N) > 1)                                                                  \
-            norm_bwd_split<T, TG, N, POWER, split_for(N)>                                                \
-                <<<dim3((n_rows + 4 / split_for(N) - 1) / (4 / split_for(N))), block, 0, st>>>(          \
+            norm_bwd_split<T, TG, N, POWER, split_for(N)><<<split_grid<split_for(N)>(n_rows),           \
+                                                                64 * split_block_waves<split_for(N)>(), 0, st>>>( \
                     xp, gp, dp, n_rows, n_cols, xs, gs, dxs, causal, alpha, nat, eps);                   \
         else                                                                                             \
             norm_bwd_vec<T, TG, N, POWER><<<grid, block, 0, st>>>(xp, gp, dp, n_rows, n_cols, xs, gs, dxs, \
