@@ -67,12 +67,15 @@ __device__ __forceinline__ u32x4 ldg16(const void* p) { return *reinterpret_cast
 
 // Staged tiles are unpadded [64 rows][D] of the 16-bit type, filled by direct
 // global->LDS loads (one 1 KB span of consecutive 16-byte chunks per wave
-// instruction).  Each tile is read two ways: as 16-byte A-operand rows (8
-// consecutive rows per LDS cycle, same chunk) and through the transposing
-// read (per 16 lanes: 4 consecutive rows x 32 bytes).  Storing logical chunk
-// c of row r at c ^ f(r), with f(r) built from bits 0-2 of r, keeps both
-// patterns free of bank conflicts: f takes 8 distinct values on 8
-// consecutive rows, and f >> 1 takes 4 distinct values on rows 4k..4k+3.
+// instruction).  Each tile is read two ways: as 16-byte A-operand rows (16
+// consecutive rows per LDS cycle, same logical chunk) and through the
+// transposing read (per 32 lanes: 4 consecutive rows x 64 bytes).  The LDS
+// has 64 banks of 4 bytes, so a cycle is conflict-free when its lanes cover
+// 256 distinct bytes modulo 256.  Storing logical chunk c of row r at
+// c ^ f(r) achieves both: for 256-byte rows (D = 128), f(r) = (r & 3) << 2 |
+// (r >> 2) & 3 takes 16 distinct values on 16 consecutive rows, and its
+// 64-byte group (f >> 2) 4 distinct values on rows 4k..4k+3; shorter rows
+// share a 256-byte window and f uses the row bits above the window.
 template <int D>
 struct SwzTile {
     static constexpr int ROWB = D * 2;     // bytes per row
@@ -80,25 +83,27 @@ struct SwzTile {
     static constexpr int BYTES = 64 * ROWB;
     static constexpr int NI = 64 * CPR / kBwdThreads;  // DMA loads per lane per tile
     static __device__ __forceinline__ int f(int r) {
-        if constexpr (CPR >= 8) return ((r & 3) << 1) | ((r >> 2) & 1);
-        else return (((r >> 1) & 1) << 1) | ((r >> 2) & 1);
+        if constexpr (CPR >= 16) return ((r & 3) << 2) | ((r >> 2) & 3);
+        else if constexpr (CPR == 8) return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+        else return (r >> 2) & 3;
     }
     // Byte offset of A-operand chunk c of row r.
     static __device__ __forceinline__ int row_off(int r, int c) { return r * ROWB + ((c ^ f(r)) << 4); }
-    // Per-lane byte offset of the transposing reads of 32-column block dt
-    // (rows vr and vr + 8 of each 16-row chunk; f is the same for both).
-    static __device__ __forceinline__ int tr_off(int lane, int dt) {
-        const int vr = (lane >> 5) * 4 + ((lane & 15) >> 2);
+    // Per-lane byte offset (from row 16c of the tile) of the transposing
+    // read of 32-column block dt, half h: row vr + 8h of the 16-row chunk
+    // (f depends on bits 0-3 of the row only, so it is the same for every c).
+    static __device__ __forceinline__ int tr_off(int lane, int dt, int h) {
+        const int vr = (lane >> 5) * 4 + ((lane & 15) >> 2) + 8 * h;
         const int chunk = (dt * 4 + ((lane >> 4) & 1) * 2 + ((lane & 3) >> 1)) ^ f(vr);
         return vr * ROWB + chunk * 16 + (lane & 1) * 8;
     }
 };
 
 // A operand = (16 rows x 32 columns of a tile)^T via two transposing reads;
-// p points at row 16c of the tile plus the lane's tr_off.
-template <typename Vec, int ROWB>
-__device__ __forceinline__ Vec tr_operand(const unsigned char* p) {
-    return lds_read_tr16_pair<Vec>(p, p + 8 * ROWB);
+// p points at row 16c of the tile.
+template <typename Vec, typename Tl>
+__device__ __forceinline__ Vec tr_operand(const unsigned char* p, int lane, int dt) {
+    return lds_read_tr16_pair<Vec>(p + Tl::tr_off(lane, dt, 0), p + Tl::tr_off(lane, dt, 1));
 }
 
 typedef __attribute__((address_space(3))) void bwd_lds_void_t;
@@ -265,7 +270,7 @@ __global__ __launch_bounds__(kBwdThreads, 2) void flash_bwd_dq_kernel(BwdParams 
                 const int c = 2 * kt + ch;  // 16-key chunk of the tile
 #pragma unroll
                 for (int dt = 0; dt < D / 32; ++dt)
-                    acc[dt] = Ops::mma(tr_operand<Vec, Tl::ROWB>(Kb + 16 * c * Tl::ROWB + Tl::tr_off(lane, dt)), bop,
+                    acc[dt] = Ops::mma(tr_operand<Vec, Tl>(Kb + 16 * c * Tl::ROWB, lane, dt), bop,
                                        acc[dt]);
             }
         }
@@ -443,9 +448,9 @@ __global__ __launch_bounds__(kBwdThreads, SA_BWD_DKDV_MINB) void flash_bwd_dkdv_
                 const int c = 2 * qh + ch;  // 16-query chunk of the tile
 #pragma unroll
                 for (int dt = 0; dt < D / 32; ++dt) {
-                    const int to = 16 * c * Tl::ROWB + Tl::tr_off(lane, dt);
-                    dvacc[dt] = Ops::mma(tr_operand<Vec, Tl::ROWB>(Ob + to), bp, dvacc[dt]);
-                    dkacc[dt] = Ops::mma(tr_operand<Vec, Tl::ROWB>(Qb + to), bs, dkacc[dt]);
+                    const int to = 16 * c * Tl::ROWB;
+                    dvacc[dt] = Ops::mma(tr_operand<Vec, Tl>(Ob + to, lane, dt), bp, dvacc[dt]);
+                    dkacc[dt] = Ops::mma(tr_operand<Vec, Tl>(Qb + to, lane, dt), bs, dkacc[dt]);
                 }
             }
         }

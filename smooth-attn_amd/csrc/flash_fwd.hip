@@ -9,16 +9,19 @@
 // linearly (sum y in fp32; P V on MFMA with P rounded to the 16-bit type,
 // as the reference does at :1617-1621 and :2579) and divided once at the end.
 //
-// Work decomposition: a block of 4 waves owns 128 query rows of one
-// (batch, query head); wave w owns rows [32w, 32w+32).  K and V tiles of 64
-// keys go straight from global memory into LDS (global_load_lds, double
-// buffered, one barrier per tile; no staging registers): tile j+1 is in
-// flight while tile j is computed.  Per wave and tile: S^T = K Q^T on MFMA,
-// the squareplus weights on the VALU (masks only on tiles crossing the
-// diagonal or the window edge), then O^T += V^T P^T on MFMA.  fp8 V is
-// widened to the 16-bit type while it is staged through registers (exact:
-// e4m3fn values are representable in bf16) and v_scale is applied once at
-// the end.
+// Work decomposition: a block of 8 waves (2 per SIMD) owns 256 query rows of
+// one (batch, query head); wave w owns rows [32w, 32w+32).  K and V tiles of
+// 64 keys go straight from global memory into a 3-stage LDS ring
+// (global_load_lds, no staging registers), one barrier per tile.  Per wave
+// and tile: S^T = K Q^T on MFMA, the squareplus weights on the VALU (masks
+// only on tiles crossing the diagonal or the window edge), then
+// O^T += V^T P^T on MFMA.  The walk is software-pipelined over 32-key
+// halves, across the tile boundary too: the barrier that publishes tile t+1
+// comes in the middle of tile t, so the first S^T MFMAs of tile t+1 overlap
+// the weights and P V of tile t's second half (the third stage keeps tile t
+// readable while tile t+2 is in flight).  fp8 V is widened to the 16-bit
+// type while it is staged through registers (exact: e4m3fn values are
+// representable in bf16) and v_scale is applied once at the end.
 // Block order: see block_coords (XCD-aware, heaviest query blocks first).
 #include <type_traits>
 
@@ -30,15 +33,14 @@ namespace {
 #ifndef SA_FLASH_BKV
 #define SA_FLASH_BKV 64
 #endif
-#ifndef SA_FLASH_MINB
-#define SA_FLASH_MINB 2
+constexpr int kBKV = SA_FLASH_BKV;  // keys per tile (a multiple of 32)
+#ifndef SA_FLASH_QT
+#define SA_FLASH_QT 1
 #endif
-constexpr int kBKV = SA_FLASH_BKV;  // keys per tile (multiple of 32)
-#ifndef SA_FLASH_WAVES
-#define SA_FLASH_WAVES 4
-#endif
-constexpr int kWaves = SA_FLASH_WAVES;  // waves per block (each owns 32 query rows per tile)
+constexpr int kQT = SA_FLASH_QT;       // 32-row query tiles per wave
+constexpr int kWaves = 8 / kQT;       // waves per block (256 query rows)
 constexpr int kThreads = 64 * kWaves;
+constexpr int kStages = 3;    // LDS ring of K/V tiles
 
 struct FlashParams {
     const void* q;
@@ -62,12 +64,16 @@ struct FlashParams {
 // LDS tiles are unpadded rows of 16-byte chunks, filled by direct
 // global->LDS loads (global_load_lds_dwordx4: lane i of a wave writes bytes
 // [16 i, 16 i + 16) after the wave's base, so one instruction fills 1 KB of
-// consecutive chunks).  Bank conflicts are avoided by storing logical chunk
-// c of row r at chunk c ^ swz(r):
-//  * K (read as 16-byte A-operand rows, 8 rows per LDS cycle): swz_k spreads
-//    8 consecutive rows over the 8 16-byte bank groups of 128 bytes;
-//  * V (read by ds_read_b64_tr_b16: per 16 lanes, 4 rows x 32 bytes): swz_v
-//    moves the 4 rows' 32-byte pairs to different 32-byte slots.
+// consecutive chunks).  The LDS has 64 banks of 4 bytes (256 bytes per
+// cycle): a 16-byte read is served 16 lanes per cycle, an 8-byte
+// (transposing) read 32 lanes per cycle, and each group is conflict-free
+// when its lanes cover 256 distinct bytes modulo 256.  Storing logical chunk
+// c of row r at chunk c ^ swz(r) achieves that:
+//  * K (16-byte A-operand rows, 16 consecutive rows per cycle at the same
+//    logical chunk): swz_k gives the 16 rows 16 distinct 16-byte slots of
+//    the 256-byte bank window;
+//  * V (ds_read_b64_tr_b16: per 32 lanes, 4 consecutive rows x 64 bytes):
+//    swz_v moves the 4 rows' 64-byte groups to 4 distinct 64-byte slots.
 template <typename T, int D, bool QK8, bool V8>
 struct Geom {
     static constexpr int QKB = QK8 ? 1 : 2;             // bytes per q/k element
@@ -82,18 +88,34 @@ struct Geom {
     static constexpr int VNI = (kBKV * VCPRL + kThreads - 1) / kThreads;  // V DMA loads per lane
     static constexpr int VNL = (kBKV * VCPRG + kThreads - 1) / kThreads;  // staged fp8 V loads
     static constexpr int NQC = QK8 ? (D + 63) / 64 : D / 16;  // MFMAs per 32x32 score tile
-    static __device__ __forceinline__ int swz_k(int r) {
-        return KCPR >= 8 ? (r & (KCPR - 1)) : ((r / (8 / KCPR)) & (KCPR - 1));
-    }
-    static __device__ __forceinline__ int swz_v(int r) { return VCPRL >= 8 ? 2 * (r & 3) : 2 * ((r >> 1) & 1); }
+    // rows sharing one 256-byte bank window
+    static constexpr int KRPW = KCPR >= 16 ? 1 : 16 / KCPR;
+    static constexpr int VRPW = VCPRL >= 16 ? 1 : 16 / VCPRL;
+    static __device__ __forceinline__ int swz_k(int r) { return (r / KRPW) & (KCPR - 1); }
+    static __device__ __forceinline__ int swz_v(int r) { return 4 * ((r / VRPW) & (VCPRL / 4 - 1)); }
 };
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void glb_void_t;
 
-// One 16-byte global -> LDS load per lane; lds_base must be wave-uniform.
-__device__ __forceinline__ void dma16(const void* g, void* lds_base) {
-    __builtin_amdgcn_global_load_lds((glb_void_t*)(g), (lds_void_t*)(lds_base), 16, 0, 0);
+// Buffer resource over the nbytes bytes from base (raw, no stride): loads at
+// or past nbytes return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, int nbytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, nbytes, 0x00020000);
+}
+
+// One 16-byte buffer -> LDS load per lane: lane i writes bytes [16 i, 16 i + 16)
+// after lds_base (wave-uniform), read from byte voff of the resource.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, int voff, void* lds_base) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(lds_base), 16, voff, 0, 0, 0);
+}
+
+// p, computed from wave-uniform values, as a scalar.
+__device__ __forceinline__ const unsigned char* uniform_ptr(const unsigned char* p) {
+    const uint64_t u = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
+    return reinterpret_cast<const unsigned char*>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
 // s_waitcnt vmcnt(0): this wave's direct-to-LDS loads have landed.
@@ -180,24 +202,34 @@ __device__ __forceinline__ u32x4 tile_load16(const T* p) {
 // Block -> (query block, batch, query head).  Blocks are dealt to the 8 XCDs
 // round-robin by index.  When B*Hkv is a multiple of 8, XCD x gets the KV
 // heads u = x, x+8, ... together with all G query heads that read them (so
-// each KV head is fetched into one XCD's L2 only), and on every XCD blocks
-// run heaviest query block first across its heads (short tail).  Otherwise
-// heaviest query block first across all heads.
+// each KV head is fetched into one XCD's L2 only).  On each XCD the heads
+// are taken a few KV heads at a time (a group holds at least
+// kBlocksPerXcd blocks, one per CU), heaviest query block first within the
+// group: the blocks in flight then share a handful of K/V streams, and the
+// group's heavy blocks still start early enough not to form a tail.
+// Otherwise heaviest query block first across all heads.
+constexpr int kBlocksPerXcd = 32;
 __device__ __forceinline__ void block_coords(const FlashParams& p, int& qb, int& b, int& hq) {
     const int id = blockIdx.x;
     const int BHk = p.B * p.Hkv;
     if ((BHk & 7) == 0) {
         const int x = id & 7;
         const int j = id >> 3;
-        const int nh = (BHk >> 3) * p.G;  // query heads per XCD
-        const int step = j / nh;
-        const int r = j - step * nh;
-        const int kvl = r / p.G;
+        const int G = p.G;
+        const int nh = (BHk >> 3) * G;  // query heads per XCD
+        const int gkv = min(max(1, (kBlocksPerXcd + G * p.nqb - 1) / (G * p.nqb)), BHk >> 3);
+        const int gh = gkv * G;  // query heads per group
+        const int grp = j / (gh * p.nqb);
+        const int r = j - grp * (gh * p.nqb);
+        const int ghs = min(gh, nh - grp * gh);  // heads in this group (the last may be short)
+        const int step = r / ghs;
+        const int hl = grp * gh + (r - step * ghs);  // query head on this XCD
+        const int kvl = hl / G;
         const int u = kvl * 8 + x;  // (b, hk)
         b = u / p.Hkv;
         const int hk = u - b * p.Hkv;
         qb = p.nqb - 1 - step;
-        hq = hk * p.G + (r - kvl * p.G);
+        hq = hk * G + (hl - kvl * G);
     } else {
         const int BH = p.B * p.Hq;
         qb = p.nqb - 1 - id / BH;
@@ -207,27 +239,22 @@ __device__ __forceinline__ void block_coords(const FlashParams& p, int& qb, int&
     }
 }
 
-#ifndef SA_FLASH_QT
-#define SA_FLASH_QT 1
-#endif
-// Query tiles (32 rows each) per wave.  QT = 1 (the default) keeps a wave
-// within 256 VGPRs, so two blocks (8 waves) share each CU and no register
-// traffic goes through AGPRs; QT = 2 reuses every K / V^T operand for two
-// MFMAs but needs more than 256 registers, and the AGPR copies that the
-// compiler then emits cost more than the reuse saves (measured: 987 vs
-// 906 us on [4,32,4096,128]).  With QT = 2, wave w owns query tiles w and
-// w + 4 of the block, which balances the causal work of the four waves.
-constexpr int kQT = SA_FLASH_QT;
 constexpr int kBQ2 = 32 * kWaves * kQT;  // query rows per block
 
+// One block per CU: with one query tile per wave, 8 waves (2 per SIMD, 256
+// VGPRs per lane); with two, 4 waves (1 per SIMD, 512 registers per lane,
+// the O accumulators in AGPRs).
 template <typename T, int D, bool QK8, bool V8, bool EXACT, bool ROPE>
-__global__ __launch_bounds__(kThreads, kQT == 1 ? SA_FLASH_MINB * 4 / kWaves : 1) void flash_fwd_kernel(FlashParams p) {
+__global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashParams p) {
     using Gm = Geom<T, D, QK8, V8>;
     using Ops = MfmaOps<T>;
     using Vec = typename Ops::vec8;
-    __shared__ __attribute__((aligned(1024))) unsigned char lds[2 * (Gm::KT + Gm::VT)];
-    unsigned char* ldsK = lds;                 // [2][kBKV][KROWB], swizzled chunks
-    unsigned char* ldsVb = lds + 2 * Gm::KT;   // [2][kBKV][VROWB], swizzled chunks
+    using KFrag = std::conditional_t<QK8, i32x8, Vec>;  // A operand of one S^T MFMA
+    static_assert(kBKV % 32 == 0, "the pipeline below walks 32-key parts of a tile");
+    constexpr int NH = kBKV / 32;  // 32-key parts per tile
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[kStages * (Gm::KT + Gm::VT)];
+    unsigned char* ldsK = lds;                       // [kStages][kBKV][KROWB], swizzled chunks
+    unsigned char* ldsVb = lds + kStages * Gm::KT;   // [kStages][kBKV][VROWB], swizzled chunks
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -242,16 +269,20 @@ __global__ __launch_bounds__(kThreads, kQT == 1 ? SA_FLASH_MINB * 4 / kWaves : 1
     const int T_ = p.T;
 
     const unsigned char* qp = static_cast<const unsigned char*>(p.q) + (b * p.qs[0] + hq * p.qs[1]) * Gm::QKB;
-    const unsigned char* kp = static_cast<const unsigned char*>(p.k) + (b * p.ks[0] + hk * p.ks[1]) * Gm::QKB;
+    // head bases as scalars (the tile loads build scalar resources from them)
+    const unsigned char* kp =
+        uniform_ptr(static_cast<const unsigned char*>(p.k) + (b * p.ks[0] + hk * p.ks[1]) * Gm::QKB);
     const unsigned char* vp =
-        static_cast<const unsigned char*>(p.v) + (b * p.vs[0] + hk * p.vs[1]) * (V8 ? 1 : 2);
+        uniform_ptr(static_cast<const unsigned char*>(p.v) + (b * p.vs[0] + hk * p.vs[1]) * (V8 ? 1 : 2));
     T* op = static_cast<T*>(p.o) + b * p.os[0] + hq * p.os[1];
     const int64_t qrs = p.qs[2] * Gm::QKB;  // row strides in bytes
     const int64_t krs = p.ks[2] * Gm::QKB;
     const int64_t vrs = p.vs[2] * (V8 ? 1 : 2);
 
     const int q_start = qb * kBQ2;
-    int wq0[kQT];  // first query row of each of this wave's tiles
+    // Query tile qt of wave w: rows q_start + 32 (w + kWaves qt) .. +31, so
+    // the causal work of the waves stays balanced.
+    int wq0[kQT];
 #pragma unroll
     for (int qt = 0; qt < kQT; ++qt) wq0[qt] = q_start + 32 * (wave + kWaves * qt);
     const int W = p.window;
@@ -309,47 +340,56 @@ __global__ __launch_bounds__(kThreads, kQT == 1 ? SA_FLASH_MINB * 4 / kWaves : 1
     if constexpr (V8) vsc = p.v_scale[0];
 
     f32x16 oacc[kQT][D / 32];
-    float ssum[kQT];
+    // Four partial row sums per query tile (element v adds to ssum[v & 3])
+    // keep the accumulation off one serial dependency chain.
+    float ssum[kQT][4];
 #pragma unroll
     for (int qt = 0; qt < kQT; ++qt) {
-        ssum[qt] = 0.f;
 #pragma unroll
         for (int dt = 0; dt < D / 32; ++dt) oacc[qt][dt] = f32x16{};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ssum[qt][i] = 0.f;
     }
 
-    // Tile j into buffer buf: K (and 16-bit V) by direct global->LDS loads,
-    // fp8 V staged through registers (widened to T in finish_tile).  Slot s
-    // of a tile is written by wave (s / 64) % 4, instruction s / 256.
+    // Tile j into ring stage buf: K (and 16-bit V) by direct global->LDS
+    // loads, fp8 V staged through registers (widened to T in finish_tile).
+    // Slot s of a tile is written by wave (s / 64) % kWaves, instruction
+    // s / kThreads.
     u32x4 vst[V8 ? Gm::VNL : 1];
-    // Per-lane byte offsets of the DMA loads inside a tile (rows past T are
-    // clamped per tile below), so each load is a wave-uniform 64-bit tile
-    // base plus a 32-bit lane offset.
+    // Per-lane byte offsets of the DMA loads inside a tile, fixed for the
+    // whole walk: each load is a per-tile scalar resource (the tile's first
+    // row, sized to the rows before T, so rows past T read as zeros: they
+    // only meet masked weights) plus this offset.
+    int koff[Gm::KNI], voff[Gm::VNI];
+#pragma unroll
+    for (int i = 0; i < Gm::KNI; ++i) {
+        const int sl = (i * kWaves + wave) * 64 + lane;
+        const int row = min(sl / Gm::KCPR, kBKV - 1);
+        koff[i] = row * static_cast<int>(krs) + ((sl - row * Gm::KCPR) ^ Gm::swz_k(row)) * 16;
+    }
+#pragma unroll
+    for (int i = 0; i < Gm::VNI; ++i) {
+        const int sl = (i * kWaves + wave) * 64 + lane;
+        const int row = min(sl / Gm::VCPRL, kBKV - 1);
+        voff[i] = row * static_cast<int>(vrs) + ((sl - row * Gm::VCPRL) ^ Gm::swz_v(row)) * 16;
+    }
     auto issue_tile = [&](int j, int buf) {
         const int k0 = j * kBKV;
-        const int rmax = T_ - 1 - k0;  // last valid row of this tile
-        const unsigned char* kt_base = kp + static_cast<int64_t>(k0) * krs;
-        const unsigned char* vt_base = vp + static_cast<int64_t>(k0) * vrs;
-        const int krs32 = static_cast<int>(krs), vrs32 = static_cast<int>(vrs);
+        const int nrows = min(T_ - k0, kBKV);  // rows of this tile before T
+        const __amdgpu_buffer_rsrc_t krs_ = tile_rsrc(kp + static_cast<int64_t>(k0) * krs, nrows * static_cast<int>(krs));
 #pragma unroll
         for (int i = 0; i < Gm::KNI; ++i) {
             const int sbase = (i * kWaves + wave) * 64;
-            if ((kBKV * Gm::KCPR) % kThreads == 0 || sbase < kBKV * Gm::KCPR) {
-                const int sl = sbase + lane;
-                const int row = sl / Gm::KCPR;
-                const int c = (sl - row * Gm::KCPR) ^ Gm::swz_k(row);
-                dma16(kt_base + (min(row, rmax) * krs32 + c * 16), ldsK + buf * Gm::KT + sbase * 16);
-            }
+            if ((kBKV * Gm::KCPR) % kThreads == 0 || sbase < kBKV * Gm::KCPR)
+                dma16(krs_, koff[i], ldsK + buf * Gm::KT + sbase * 16);
         }
         if constexpr (!V8) {
+            const __amdgpu_buffer_rsrc_t vrs_ = tile_rsrc(vp + static_cast<int64_t>(k0) * vrs, nrows * static_cast<int>(vrs));
 #pragma unroll
             for (int i = 0; i < Gm::VNI; ++i) {
                 const int sbase = (i * kWaves + wave) * 64;
-                if ((kBKV * Gm::VCPRL) % kThreads == 0 || sbase < kBKV * Gm::VCPRL) {
-                    const int sl = sbase + lane;
-                    const int row = sl / Gm::VCPRL;
-                    const int c = (sl - row * Gm::VCPRL) ^ Gm::swz_v(row);
-                    dma16(vt_base + (min(row, rmax) * vrs32 + c * 16), ldsVb + buf * Gm::VT + sbase * 16);
-                }
+                if ((kBKV * Gm::VCPRL) % kThreads == 0 || sbase < kBKV * Gm::VCPRL)
+                    dma16(vrs_, voff[i], ldsVb + buf * Gm::VT + sbase * 16);
             }
         } else {
 #pragma unroll
@@ -380,7 +420,6 @@ __global__ __launch_bounds__(kThreads, kQT == 1 ? SA_FLASH_MINB * 4 / kWaves : 1
         }
     };
 
-    // Per-lane element offset of the transposing V read; see flash_common.hpp.
     // Byte offsets (within a 16-key chunk of the V tile) of this lane's
     // transposing reads, one per 32-column block dt: row (lane>>5)*4 +
     // ((lane&15)>>2), columns dt*32 + ((lane>>4)&1)*16 + 4*(lane&3).
@@ -398,133 +437,184 @@ __global__ __launch_bounds__(kThreads, kQT == 1 ? SA_FLASH_MINB * 4 / kWaves : 1
     const int kswz = Gm::swz_k(l32);
     const unsigned weff = W > 0 ? static_cast<unsigned>(W) : 0x7FFFFFFFu;
 
-    // One K/V tile for all of this wave's query tiles.  EDGE: some tile of
-    // the wave crosses the diagonal or the window edge (per-tile activity
-    // and masks are evaluated); otherwise every query tile is fully inside.
-    auto tile_step = [&](auto edge_tag, int buf, int k0) {
-        constexpr bool EDGE = decltype(edge_tag)::value;
-        bool act[kQT], msk[kQT];
+    // K fragments (A operands) of the S^T MFMAs of 32-key half kt.
+    auto load_k = [&](const unsigned char* Kb, int kt, KFrag (&kf)[Gm::NQC]) {
+        const unsigned char* krow = Kb + (kt * 32 + l32) * Gm::KROWB;
 #pragma unroll
-        for (int qt = 0; qt < kQT; ++qt) {
-            act[qt] = !EDGE || ((k0 <= wq0[qt] + 31) && !(W > 0 && k0 + kBKV - 1 <= wq0[qt] - W));
-            msk[qt] = EDGE && ((k0 + kBKV - 1 > wq0[qt]) || (W > 0 && k0 <= wq0[qt] + 31 - W));
-        }
-        const unsigned char* Kb = ldsK + buf * Gm::KT;
-        const unsigned char* Vb = ldsVb + buf * Gm::VT;
-        // One 32-key half at a time: S^T tiles, weights, then the two P V
-        // chunks of the half.
-#pragma unroll
-        for (int kt = 0; kt < kBKV / 32; ++kt) {
-            f32x16 s[kQT];
-#pragma unroll
-            for (int qt = 0; qt < kQT; ++qt) s[qt] = f32x16{};
-            const unsigned char* krow = Kb + (kt * 32 + l32) * Gm::KROWB;
-#pragma unroll
-            for (int dc = 0; dc < Gm::NQC; ++dc) {
-                if constexpr (QK8) {
-                    const int d0 = 64 * dc + 32 * hi;
-                    u32x4 a0 = u32x4{0u, 0u, 0u, 0u}, a1 = u32x4{0u, 0u, 0u, 0u};
-                    if (d0 < D) {
-                        a0 = *reinterpret_cast<const u32x4*>(krow + ((d0 / 16) ^ kswz) * 16);
-                        a1 = *reinterpret_cast<const u32x4*>(krow + ((d0 / 16 + 1) ^ kswz) * 16);
-                    }
-                    const i32x8 av{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w,
-                                   (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
-#pragma unroll
-                    for (int qt = 0; qt < kQT; ++qt) {
-                        if (!act[qt]) continue;
-                        const i32x8 bv{(int)qreg[qt][dc][0].x, (int)qreg[qt][dc][0].y, (int)qreg[qt][dc][0].z,
-                                       (int)qreg[qt][dc][0].w, (int)qreg[qt][dc][1].x, (int)qreg[qt][dc][1].y,
-                                       (int)qreg[qt][dc][1].z, (int)qreg[qt][dc][1].w};
-                        s[qt] = mma_fp8(av, bv, s[qt]);
-                    }
-                } else {
-                    const u32x4 a = *reinterpret_cast<const u32x4*>(krow + ((dc * 2 + hi) ^ kswz) * 16);
-#pragma unroll
-                    for (int qt = 0; qt < kQT; ++qt) {
-                        if (!act[qt]) continue;
-                        s[qt] = Ops::mma(as_vec8<Vec>(a), as_vec8<Vec>(qreg[qt][dc][0]), s[qt]);
-                    }
+        for (int dc = 0; dc < Gm::NQC; ++dc) {
+            if constexpr (QK8) {
+                const int d0 = 64 * dc + 32 * hi;
+                u32x4 a0 = u32x4{0u, 0u, 0u, 0u}, a1 = u32x4{0u, 0u, 0u, 0u};
+                if (d0 < D) {
+                    a0 = *reinterpret_cast<const u32x4*>(krow + ((d0 / 16) ^ kswz) * 16);
+                    a1 = *reinterpret_cast<const u32x4*>(krow + ((d0 / 16 + 1) ^ kswz) * 16);
                 }
+                kf[dc] = i32x8{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+            } else {
+                kf[dc] = as_vec8<Vec>(*reinterpret_cast<const u32x4*>(krow + ((dc * 2 + hi) ^ kswz) * 16));
             }
-            Vec bop[kQT][2];
+        }
+    };
+    // S^T (32 keys x 32 queries) of one half for every query tile; each K
+    // fragment feeds one MFMA per query tile.
+    struct STiles {
+        f32x16 v[kQT];
+    };
+    auto s_tile = [&](const KFrag (&kf)[Gm::NQC]) {
+        STiles s;
+#pragma unroll
+        for (int qt = 0; qt < kQT; ++qt) s.v[qt] = f32x16{};
+#pragma unroll
+        for (int dc = 0; dc < Gm::NQC; ++dc) {
 #pragma unroll
             for (int qt = 0; qt < kQT; ++qt) {
-                if (!act[qt]) continue;
-                // valid(key) <=> 0 <= qi - key < W_eff (W_eff = W, or INT_MAX
-                // for full causal): one unsigned compare per element.
-                const int dbase = wq0[qt] + l32 - k0 - hi * 4;
-                float y[16];
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    float w = sp2_weight<EXACT>(__builtin_fmaf(s[qt][v], sc, -0.5f));
-                    if (EDGE && msk[qt]) {
-                        const int cv = kt * 32 + (v >> 2) * 8 + (v & 3);
-                        w = static_cast<unsigned>(dbase - cv) < weff ? w : 0.f;
-                    }
-                    y[v] = w;
-                    ssum[qt] += w;
-                }
-#pragma unroll
-                for (int ch = 0; ch < 2; ++ch) {
-                    u32x4 pw;
-                    pw.x = pack2<T>(y[8 * ch + 0], y[8 * ch + 1]);
-                    pw.y = pack2<T>(y[8 * ch + 2], y[8 * ch + 3]);
-                    pw.z = pack2<T>(y[8 * ch + 4], y[8 * ch + 5]);
-                    pw.w = pack2<T>(y[8 * ch + 6], y[8 * ch + 7]);
-                    bop[qt][ch] = as_vec8<Vec>(pw);
+                if constexpr (QK8) {
+                    const i32x8 bv{(int)qreg[qt][dc][0].x, (int)qreg[qt][dc][0].y, (int)qreg[qt][dc][0].z,
+                                   (int)qreg[qt][dc][0].w, (int)qreg[qt][dc][1].x, (int)qreg[qt][dc][1].y,
+                                   (int)qreg[qt][dc][1].z, (int)qreg[qt][dc][1].w};
+                    s.v[qt] = mma_fp8(kf[dc], bv, s.v[qt]);
+                } else {
+                    s.v[qt] = Ops::mma(kf[dc], as_vec8<Vec>(qreg[qt][dc][0]), s.v[qt]);
                 }
             }
+        }
+        return s;
+    };
+    // Squareplus weights of one half, added to the row sums and rounded to
+    // T as the two B operands (16-key chunks) of O^T += V^T P^T.  MASK: keep
+    // key (k0 + kt*32 + cv) iff 0 <= q - key < W_eff (W_eff = W, or INT_MAX
+    // for full causal), one unsigned compare per element.
+    auto weights = [&](auto mask_tag, const f32x16& s, int qt, int k0, int kt, Vec (&bop)[2]) {
+        constexpr bool MASK = decltype(mask_tag)::value;
+        const int dbase = wq0[qt] + l32 - k0 - hi * 4 - kt * 32;
+        float y[16];
 #pragma unroll
-            for (int ch = 0; ch < 2; ++ch) {
-                const int c = 2 * kt + ch;  // 16-key chunk of the tile
+        for (int v = 0; v < 16; ++v) {
+            float w = sp2_weight<EXACT>(__builtin_fmaf(s[v], sc, -0.5f));
+            if constexpr (MASK) {
+                const int cv = (v >> 2) * 8 + (v & 3);
+                w = static_cast<unsigned>(dbase - cv) < weff ? w : 0.f;
+            }
+            y[v] = w;
+            ssum[qt][v & 3] += w;
+        }
 #pragma unroll
-                for (int dt = 0; dt < D / 32; ++dt) {
-                    const unsigned char* base = Vb + (16 * c) * Gm::VROWB + v_tr_off[dt];
-                    const Vec aw = lds_read_tr16_pair<Vec>(base, base + 8 * Gm::VROWB);
+        for (int ch = 0; ch < 2; ++ch) {
+            u32x4 pw;
+            pw.x = pack2<T>(y[8 * ch + 0], y[8 * ch + 1]);
+            pw.y = pack2<T>(y[8 * ch + 2], y[8 * ch + 3]);
+            pw.z = pack2<T>(y[8 * ch + 4], y[8 * ch + 5]);
+            pw.w = pack2<T>(y[8 * ch + 6], y[8 * ch + 7]);
+            bop[ch] = as_vec8<Vec>(pw);
+        }
+    };
+    // O^T += V^T P^T for the two 16-key chunks of half kt; each V^T
+    // fragment feeds one MFMA per query tile.
+    auto pv = [&](const unsigned char* Vb, int kt, const Vec (&bop)[kQT][2]) {
 #pragma unroll
-                    for (int qt = 0; qt < kQT; ++qt) {
-                        if (!act[qt]) continue;
-                        oacc[qt][dt] = Ops::mma(aw, bop[qt][ch], oacc[qt][dt]);
-                    }
-                }
+        for (int ch = 0; ch < 2; ++ch) {
+            const int c = 2 * kt + ch;  // 16-key chunk of the tile
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt) {
+                const unsigned char* base = Vb + (16 * c) * Gm::VROWB + v_tr_off[dt];
+                const Vec aw = lds_read_tr16_pair<Vec>(base, base + 8 * Gm::VROWB);
+#pragma unroll
+                for (int qt = 0; qt < kQT; ++qt) oacc[qt][dt] = Ops::mma(aw, bop[qt][ch], oacc[qt][dt]);
             }
         }
     };
 
-    // kv_begin < kv_end for every block (q_start < T), so the first tile is
-    // always staged.
-    issue_tile(kv_begin, 0);
-    finish_tile(0);
-    wait_vmem();
-    __syncthreads();
-
-    const int wlast = wq0[kQT - 1];  // the wave's latest query tile
-    const int wfirst = wq0[0];
-    for (int j = kv_begin; j < kv_end; ++j) {
-        const int buf = (j - kv_begin) & 1;
-        const bool has_next = j + 1 < kv_end;
-        if (has_next) issue_tile(j + 1, buf ^ 1);
-        const int k0 = j * kBKV;
-        // some query tile of the wave sees this key tile
-        const bool any = (k0 <= wlast + 31) && !(W > 0 && k0 + kBKV - 1 <= wfirst - W);
-        // every query tile fully sees it (no masks, no inactive tile)
-        const bool interior = (k0 + kBKV - 1 <= wfirst) && !(W > 0 && k0 <= wlast + 31 - W);
-        if (any) {
-            if (interior)
-                tile_step(std::false_type{}, buf, k0);
-            else
-                tile_step(std::true_type{}, buf, k0);
+    auto stage_of = [&](int t) { return (t - kv_begin) % kStages; };
+    // S^T of 32-key half h of tile t.
+    auto s_half = [&](int t, int h) {
+        KFrag kf[Gm::NQC];
+        load_k(ldsK + stage_of(t) * Gm::KT, h, kf);
+        return s_tile(kf);
+    };
+    // Barrier B(t+1): tile t+1 has landed (this wave's loads, then every
+    // wave's) and is published; then tile t+2 is requested into the stage of
+    // tile t-1, which every wave finished reading before B(t+1).  Every wave
+    // calls this exactly once per tile of the block, active or not.
+    auto boundary = [&](int t) {
+        if (t + 1 < kv_end) {
+            wait_vmem();
+            finish_tile(stage_of(t + 1));
+            __syncthreads();
+            if (t + 2 < kv_end) issue_tile(t + 2, stage_of(t + 2));
         }
-        if (has_next) finish_tile(buf ^ 1);
-        wait_vmem();
-        __syncthreads();
+    };
+    // Tile t of the wave with s_cur = S^T of its first 32-key part: for each
+    // part h, S^T of part h+1 is issued before the weights and P V of part
+    // h; before the last part comes B(t+1), then S^T of the first part of
+    // tile t+1 (NEXT), so s_cur holds it on exit.
+    auto active_tile = [&](auto mask_tag, auto next_tag, int t, STiles& s_cur) {
+        constexpr bool NEXT = decltype(next_tag)::value;
+        const int k0 = t * kBKV;
+        const unsigned char* Vb = ldsVb + stage_of(t) * Gm::VT;
+        Vec bop[kQT][2];
+#pragma unroll
+        for (int h = 0; h + 1 < NH; ++h) {
+            const STiles s_nx = s_half(t, h + 1);
+#pragma unroll
+            for (int qt = 0; qt < kQT; ++qt) weights(mask_tag, s_cur.v[qt], qt, k0, h, bop[qt]);
+            pv(Vb, h, bop);
+            s_cur = s_nx;
+        }
+        const STiles s_last = s_cur;
+        boundary(t);
+        if constexpr (NEXT) s_cur = s_half(t + 1, 0);
+#pragma unroll
+        for (int qt = 0; qt < kQT; ++qt) weights(mask_tag, s_last.v[qt], qt, k0, NH - 1, bop[qt]);
+        pv(Vb, NH - 1, bop);
+    };
+
+    // Prologue: tile kv_begin staged and published, tile kv_begin + 1 in
+    // flight.  kv_begin < kv_end for every block (q_start < T).
+    issue_tile(kv_begin, 0);
+    wait_vmem();
+    finish_tile(0);
+    __syncthreads();
+    if (kv_begin + 1 < kv_end) issue_tile(kv_begin + 1, 1);
+
+    // The wave's tiles: [t_first, t_last] see some key (before t_first only
+    // the window has passed, after t_last only keys past the wave's last
+    // row); inside, [ja, jb) need no masks (every row sees every key: jb
+    // ends at the wave's first row, ja starts past the window edge of its
+    // last row).  Separate loops per kind keep the accumulators in fixed
+    // registers.  Waves whose rows all lie past T only keep the barriers.
+    // With two query tiles, the span runs from the first tile's first row
+    // (wf) to the last tile's last row (wl).
+    const int wf = wq0[0], wl = wq0[kQT - 1] + 31;
+    int t_first = kv_begin;
+    if (W > 0 && wf - W + 1 > 0) t_first = max(t_first, (wf - W + 1) / kBKV);
+    const int t_last = wf < T_ ? min(wl / kBKV, kv_end - 1) : t_first - 1;
+    int ja = t_first;
+    if (W > 0 && wl - W >= 0) ja = max(ja, (wl - W) / kBKV + 1);
+    const int jb = (wf + 1) / kBKV;
+    int t = kv_begin;
+    for (; t < t_first; ++t) boundary(t);
+    if (t_first <= t_last) {
+        using Y = std::true_type;
+        using N = std::false_type;
+        STiles s_cur = s_half(t_first, 0);
+        for (; t < min(ja, t_last); ++t) active_tile(Y{}, Y{}, t, s_cur);
+        for (; t < min(jb, t_last); ++t) active_tile(N{}, Y{}, t, s_cur);
+        for (; t < t_last; ++t) active_tile(Y{}, Y{}, t, s_cur);
+        // t == t_last: it holds the wave's diagonal (or window edge) unless
+        // the interior reaches it.
+        if (t >= ja && t < jb)
+            active_tile(N{}, N{}, t, s_cur);
+        else
+            active_tile(Y{}, N{}, t, s_cur);
+        ++t;
     }
+    for (; t < kv_end; ++t) boundary(t);
 
 #pragma unroll
     for (int qt = 0; qt < kQT; ++qt) {
         // Row sums: lanes l and l^32 hold the two key halves of one query column.
-        const float stot = ssum[qt] + __shfl_xor(ssum[qt], 32) + kEps;
+        const float part = (ssum[qt][0] + ssum[qt][1]) + (ssum[qt][2] + ssum[qt][3]);
+        const float stot = part + __shfl_xor(part, 32) + kEps;
         const float inv = vsc / stot;
         const int qi = wq0[qt] + l32;
         if (qi < T_) {

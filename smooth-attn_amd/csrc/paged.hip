@@ -48,12 +48,20 @@ template <typename T, int D, bool UNIFORM>
 __global__ __launch_bounds__(64) void paged_partial_kernel(PagedParams p) {
     using Ops = MfmaOps<T>;
     using Vec = typename Ops::vec8;
-    constexpr int RS = D + 8;              // LDS row stride (elements)
+    // Padded LDS rows.  The LDS has 64 banks of 4 bytes; a 16-byte read is
+    // served 16 lanes per cycle, an 8-byte transposing read 32 lanes per
+    // cycle.  K (read as 16-byte rows, 16 consecutive rows per cycle at one
+    // column): a stride of 2D + 16 bytes puts the 16 rows in 16 distinct
+    // 16-byte bank slots.  V (transposing reads: per 32 lanes, 4 consecutive
+    // rows x 64 bytes): a stride of 64 bytes modulo 256 puts the 4 rows in 4
+    // distinct 64-byte slots.
+    constexpr int RS = D + 8;                            // K row stride (elements)
+    constexpr int RSV = (2 * D) % 256 == 64 ? D : D + 32;  // V row stride (elements)
     constexpr int CPT = D / 8;             // 16-byte chunks per token row
     constexpr int TPI = 64 / CPT;          // tokens per load instruction
     constexpr int NC = kTile * CPT / 64;   // chunks per lane per tile and tensor
     __shared__ __attribute__((aligned(16))) T ldsK[kTile * RS];
-    __shared__ __attribute__((aligned(16))) T ldsV[kTile * RS];
+    __shared__ __attribute__((aligned(16))) T ldsV[kTile * RSV];
 
     const int lane = threadIdx.x;
     const int hi = lane >> 5;
@@ -128,7 +136,7 @@ __global__ __launch_bounds__(64) void paged_partial_kernel(PagedParams p) {
         for (int i = 0; i < NC; ++i) {
             const int tok = i * TPI + lane_tok;
             *reinterpret_cast<u32x4*>(ldsK + tok * RS + lane_col) = kbuf[i];
-            *reinterpret_cast<u32x4*>(ldsV + tok * RS + lane_col) = vbuf[i];
+            *reinterpret_cast<u32x4*>(ldsV + tok * RSV + lane_col) = vbuf[i];
         }
     };
 
@@ -136,7 +144,7 @@ __global__ __launch_bounds__(64) void paged_partial_kernel(PagedParams p) {
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) oacc[dt] = f32x16{};
     float ssum = 0.f;
-    const int v_tr_off = ((lane >> 5) * 4 + ((lane & 15) >> 2)) * RS + ((lane >> 4) & 1) * 16 + 4 * (lane & 3);
+    const int v_tr_off = ((lane >> 5) * 4 + ((lane & 15) >> 2)) * RSV + ((lane >> 4) & 1) * 16 + 4 * (lane & 3);
 
     load_tile(t_begin);
     for (int t0 = t_begin; t0 < t_end; t0 += kTile) {
@@ -171,9 +179,9 @@ __global__ __launch_bounds__(64) void paged_partial_kernel(PagedParams p) {
             const Vec bop = as_vec8<Vec>(pw);
 #pragma unroll
             for (int dt = 0; dt < D / 32; ++dt) {
-                const T* base = ldsV + (16 * c) * RS + dt * 32 + v_tr_off;
+                const T* base = ldsV + (16 * c) * RSV + dt * 32 + v_tr_off;
                 const uint2 lo = lds_read_tr16(base);
-                const uint2 hi8 = lds_read_tr16(base + 8 * RS);
+                const uint2 hi8 = lds_read_tr16(base + 8 * RSV);
                 const u32x4 aw{lo.x, lo.y, hi8.x, hi8.y};
                 oacc[dt] = Ops::mma(as_vec8<Vec>(aw), bop, oacc[dt]);
             }
