@@ -6,25 +6,32 @@
 //   (reference kernels.py:2681-2773 and the decode references of
 //    tests/test_paged_long_context.py:39-65)
 //
-// One wavefront per (sequence b, KV head, split of kSplitTok tokens).  The
-// wave walks its split in tiles of 32 tokens and reads every K/V row once
-// for all G query heads that share the KV head (the reference grid
-// (B, Hq) rereads each page G times).  Tiles are fetched with coalesced
-// 16-byte loads (one 1 KB span per instruction) one tile ahead of the
-// compute and staged in wave-private LDS.  Scores are S^T = K Q^T on MFMA
-// with the G query heads as columns; the squareplus weights land in the
-// B-operand layout of O^T += V^T P^T, and V^T comes from the row-major LDS
-// tile through the transposing LDS read (see flash_common.hpp).
-// Each wave writes its unnormalised partial (O, S); a second kernel sums the
-// partials of a sequence in split order (squareplus needs no running
-// maximum, so merging is a plain sum) and divides once.
+// Work split (stream-K style, balanced whatever the context lengths): a
+// plan kernel counts each sequence's 32-token tiles, prefix-sums them over
+// (sequence, KV head) in that order and fixes the number of active waves
+// Ne; a persistent grid of one-wave blocks then gives wave w the tiles
+// [floor(w Tt / Ne), floor((w+1) Tt / Ne)) of the Tt in total.  A wave's
+// range is cut at (sequence, KV head) boundaries into pieces; each piece is
+// walked in tiles of 32 tokens, reading every K/V row once for all G query
+// heads that share the KV head (the reference grid (B, Hq) rereads each
+// page G times).  Tiles are fetched with coalesced 16-byte loads (one 1 KB
+// span per instruction) one tile ahead of the compute and staged in
+// wave-private LDS.  Scores are S^T = K Q^T on MFMA with the G query heads
+// as columns; the squareplus weights land in the B-operand layout of
+// O^T += V^T P^T, and V^T comes from the row-major LDS tile through the
+// transposing LDS read (see flash_common.hpp).  Each piece writes its
+// unnormalised partial (O, S) into slot k of its (sequence, query head),
+// k = its wave minus the wave that owns the segment's first tile; a merge
+// kernel sums the slots in order (squareplus needs no running maximum, so
+// merging is a plain sum) and divides once.
 #include "flash_common.hpp"
 
 namespace sa {
 namespace {
 
-constexpr int kSplitTok = 512;  // tokens per work unit
+constexpr int kSplitTok = 512;  // minimum tokens per wave (bounds the pieces per segment)
 constexpr int kTile = 32;       // tokens per MFMA tile
+constexpr int kWinPages = 64;   // page ids held per wave at a time (one per lane)
 
 struct PagedParams {
     const void* q;
@@ -33,17 +40,55 @@ struct PagedParams {
     bf16* out;
     const int32_t* table;
     const int32_t* ctx;
-    float* ws_o;  // [B][Hq][n_splits][D]
-    float* ws_s;  // [B][Hq][n_splits]
+    int* plan;    // [B + 2]: prefix of Hkv * tiles over sequences (plan[B] = Tt), plan[B + 1] = Ne
+    float* ws_o;  // [B][Hq][n_slots][D]
+    float* ws_s;  // [B][Hq][n_slots]
     int64_t qs[4], ks[4], vs[4], os[3];
     int64_t bt_stride;
-    int B, Hq, Hkv, G, P, logP, max_pages, n_pages, n_splits;
+    int B, Hq, Hkv, G, P, logP, max_pages, n_pages, n_slots, n_waves;
     float scale;
 };
 
+// Context length of sequence b as the kernels use it (clamped to the table).
+__device__ __forceinline__ int ctx_of(const PagedParams& p, int b) {
+    return min(max(p.ctx[b], 0), p.max_pages * p.P);
+}
+
+// Plan: plan[b] = sum_{b' < b} Hkv * ceil(ctx_b' / 32) for b <= B (plan[B] =
+// Tt, the tiles of all (sequence, KV head) segments), plan[B + 1] = Ne, the
+// waves that get work: every wave's range holds at least kSplitTok / kTile
+// tiles (so a segment of c tokens is cut into at most ceil(c / kSplitTok) + 1
+// pieces), and at most n_waves waves run.  One block.
+__global__ __launch_bounds__(256) void paged_plan_kernel(PagedParams p) {
+    __shared__ int part[256];
+    const int tid = threadIdx.x;
+    int carry = 0;
+    for (int b0 = 0; b0 < p.B; b0 += 256) {
+        const int b = b0 + tid;
+        const int n = b < p.B ? p.Hkv * ((ctx_of(p, b) + kTile - 1) / kTile) : 0;
+        part[tid] = n;
+        __syncthreads();
+        // inclusive scan of part[] (Hillis-Steele)
+        for (int off = 1; off < 256; off <<= 1) {
+            const int v = tid >= off ? part[tid - off] : 0;
+            __syncthreads();
+            part[tid] += v;
+            __syncthreads();
+        }
+        if (b < p.B) p.plan[b] = carry + part[tid] - n;
+        carry += part[255];
+        __syncthreads();
+    }
+    if (tid == 0) {
+        p.plan[p.B] = carry;
+        const int per = kSplitTok / kTile;
+        p.plan[p.B + 1] = carry == 0 ? 0 : max(1, min(p.n_waves, carry / per));
+    }
+}
+
 // UNIFORM: every load instruction's tokens lie in one page (64 / (D/8)
 // tokens per instruction divide the page size), so the page base is
-// wave-uniform and comes from v_readlane of the split's page-id register.
+// wave-uniform and comes from v_readlane of the window's page-id register.
 template <typename T, int D, bool UNIFORM>
 __global__ __launch_bounds__(64) void paged_partial_kernel(PagedParams p) {
     using Ops = MfmaOps<T>;
@@ -66,188 +111,255 @@ __global__ __launch_bounds__(64) void paged_partial_kernel(PagedParams p) {
     const int lane = threadIdx.x;
     const int hi = lane >> 5;
     const int l32 = lane & 31;
-    const int unit = blockIdx.x;
-    const int split = unit % p.n_splits;
-    const int bk = unit / p.n_splits;
-    const int b = bk / p.Hkv;
-    const int hk = bk - b * p.Hkv;
-    const int ctx = min(max(p.ctx[b], 0), p.max_pages * p.P);
-    const int t_begin = split * kSplitTok;
-    if (t_begin >= ctx) return;  // whole wave: nothing in this split
-    const int t_end = min(ctx, t_begin + kSplitTok);
+    const int w = blockIdx.x;
+    const int Tt = p.plan[p.B];
+    const int Ne = p.plan[p.B + 1];
+    if (w >= Ne) return;  // no work for this wave (tiny problems)
+    const int x_end = static_cast<int>(static_cast<int64_t>(w + 1) * Tt / Ne);
+    int x = static_cast<int>(static_cast<int64_t>(w) * Tt / Ne);
     const int logP = p.logP;
     const int pmask = p.P - 1;
 
-    const T* kc = static_cast<const T*>(p.k) + hk * p.ks[1];
-    const T* vc = static_cast<const T*>(p.v) + hk * p.vs[1];
-
-    // Page ids of this split, one per lane (a split spans <= 64 pages).
-    int page_id;
-    {
-        const int first = t_begin >> logP;
-        const int npg = ((t_end - 1) >> logP) - first + 1;
-        page_id = lane < npg ? min(max(p.table[b * p.bt_stride + first + lane], 0), p.n_pages - 1) : 0;
-    }
-    const int first_page = t_begin >> logP;
-
-    // Q^T as the B operand: column = query head hk*G + l32 (zero past G).
-    u32x4 qreg[D / 16];
-    {
-        const bool live = l32 < p.G;
-        const T* qrow = static_cast<const T*>(p.q) + b * p.qs[0] + (hk * p.G + (live ? l32 : 0)) * p.qs[1];
-#pragma unroll
-        for (int dc = 0; dc < D / 16; ++dc)
-            qreg[dc] = live ? load16(qrow + dc * 16 + hi * 8) : u32x4{0u, 0u, 0u, 0u};
+    // Sequence b of tile x: the last b with plan[b] <= x (plan[b] ascending).
+    int b = 0;
+    for (int b0 = 0; b0 < p.B; b0 += 64) {
+        const int bi = b0 + lane;
+        const bool le = bi < p.B && p.plan[bi] <= x;
+        const unsigned long long m = __ballot(le);
+        if (m == 0) break;
+        b = b0 + 63 - __builtin_clzll(m);
     }
 
-    // Coalesced tile loads: instruction i of lane l fetches 16-byte chunk
-    // c = 64 i + l of the tile (token c / CPT, columns 8 (c % CPT) .. +7).
-    const int lane_tok = lane / CPT;
-    const int lane_col = (lane % CPT) * 8;
-    u32x4 kbuf[NC], vbuf[NC];
-    auto load_tile = [&](int t0) {
+    while (x < x_end) {
+        // Segment (b, hk) holding tile x; skip sequences with no tiles.
+        while (p.plan[b + 1] <= x) ++b;
+        const int seg0 = p.plan[b];
+        const int n_b = (p.plan[b + 1] - seg0) / p.Hkv;  // tiles per KV head of b
+        const int rel = x - seg0;
+        const int hk = rel / n_b;
+        const int seg_start = seg0 + hk * n_b;
+        const int piece_end = min(x_end, seg_start + n_b);
+        const int ctx = ctx_of(p, b);
+        const int t_begin = (x - seg_start) * kTile;
+        const int t_end = min(ctx, (piece_end - seg_start) * kTile);
+        // slot: this wave minus the owner of the segment's first tile
+        const int owner0 = static_cast<int>((static_cast<int64_t>(seg_start + 1) * Ne - 1) / Tt);
+        const int slot_k = w - owner0;
+
+        const T* kc = static_cast<const T*>(p.k) + hk * p.ks[1];
+        const T* vc = static_cast<const T*>(p.v) + hk * p.vs[1];
+        const int32_t* trow = p.table + b * p.bt_stride;
+
+        // Q^T as the B operand: column = query head hk*G + l32 (zero past G).
+        u32x4 qreg[D / 16];
+        {
+            const bool live = l32 < p.G;
+            const T* qrow = static_cast<const T*>(p.q) + b * p.qs[0] + (hk * p.G + (live ? l32 : 0)) * p.qs[1];
 #pragma unroll
-        for (int i = 0; i < NC; ++i) {
-            const int t = t0 + i * TPI + lane_tok;
-            int phys;
-            int64_t koff, voff;
-            if constexpr (UNIFORM) {
-                const int tu = t0 + i * TPI;  // first token of the instruction
-                phys = __builtin_amdgcn_readlane(page_id, (tu >> logP) - first_page);
-                const int r = tu & pmask;
-                koff = phys * p.ks[0] + (r + lane_tok) * p.ks[2];
-                voff = phys * p.vs[0] + (r + lane_tok) * p.vs[2];
-            } else {
-                phys = __shfl(page_id, (t >> logP) - first_page);
-                koff = phys * p.ks[0] + (t & pmask) * p.ks[2];
-                voff = phys * p.vs[0] + (t & pmask) * p.vs[2];
+            for (int dc = 0; dc < D / 16; ++dc)
+                qreg[dc] = live ? load16(qrow + dc * 16 + hi * 8) : u32x4{0u, 0u, 0u, 0u};
+        }
+
+        f32x16 oacc[D / 32];
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) oacc[dt] = f32x16{};
+        float ssum = 0.f;
+        const int v_tr_off = ((lane >> 5) * 4 + ((lane & 15) >> 2)) * RSV + ((lane >> 4) & 1) * 16 + 4 * (lane & 3);
+
+        // The piece in windows of whole tiles whose pages fit kWinPages.
+        for (int ws = t_begin; ws < t_end;) {
+            const int first_page = ws >> logP;
+            const int we = min(t_end, ws + ((((first_page + kWinPages) << logP) - ws) & ~(kTile - 1)));
+            int page_id;
+            {
+                const int npg = ((we - 1) >> logP) - first_page + 1;
+                page_id = lane < npg ? min(max(trow[first_page + lane], 0), p.n_pages - 1) : 0;
             }
-            if (t < t_end) {
-                kbuf[i] = load16(kc + koff + lane_col);
-                vbuf[i] = load16(vc + voff + lane_col);
-            } else {
-                kbuf[i] = u32x4{0u, 0u, 0u, 0u};
-                vbuf[i] = u32x4{0u, 0u, 0u, 0u};
+
+            // Coalesced tile loads: instruction i of lane l fetches 16-byte chunk
+            // c = 64 i + l of the tile (token c / CPT, columns 8 (c % CPT) .. +7).
+            const int lane_tok = lane / CPT;
+            const int lane_col = (lane % CPT) * 8;
+            u32x4 kbuf[NC], vbuf[NC];
+            auto load_tile = [&](int t0) {
+#pragma unroll
+                for (int i = 0; i < NC; ++i) {
+                    const int t = t0 + i * TPI + lane_tok;
+                    int phys;
+                    int64_t koff, voff;
+                    if constexpr (UNIFORM) {
+                        const int tu = t0 + i * TPI;  // first token of the instruction
+                        phys = __builtin_amdgcn_readlane(page_id, min((tu >> logP) - first_page, kWinPages - 1));
+                        const int r = tu & pmask;
+                        koff = phys * p.ks[0] + (r + lane_tok) * p.ks[2];
+                        voff = phys * p.vs[0] + (r + lane_tok) * p.vs[2];
+                    } else {
+                        phys = __shfl(page_id, min((t >> logP) - first_page, kWinPages - 1));
+                        koff = phys * p.ks[0] + (t & pmask) * p.ks[2];
+                        voff = phys * p.vs[0] + (t & pmask) * p.vs[2];
+                    }
+                    if (t < we) {
+                        kbuf[i] = load16(kc + koff + lane_col);
+                        vbuf[i] = load16(vc + voff + lane_col);
+                    } else {
+                        kbuf[i] = u32x4{0u, 0u, 0u, 0u};
+                        vbuf[i] = u32x4{0u, 0u, 0u, 0u};
+                    }
+                }
+            };
+            auto store_tile = [&]() {
+#pragma unroll
+                for (int i = 0; i < NC; ++i) {
+                    const int tok = i * TPI + lane_tok;
+                    *reinterpret_cast<u32x4*>(ldsK + tok * RS + lane_col) = kbuf[i];
+                    *reinterpret_cast<u32x4*>(ldsV + tok * RSV + lane_col) = vbuf[i];
+                }
+            };
+
+            load_tile(ws);
+            for (int t0 = ws; t0 < we; t0 += kTile) {
+                // The block is one wavefront: LDS accesses of a wave complete
+                // in issue order, so a wave-level scheduling barrier is all
+                // the ordering needed.
+                store_tile();
+                __builtin_amdgcn_wave_barrier();
+                if (t0 + kTile < we) load_tile(t0 + kTile);
+
+                f32x16 s = f32x16{};
+#pragma unroll
+                for (int dc = 0; dc < D / 16; ++dc) {
+                    const u32x4 a = *reinterpret_cast<const u32x4*>(ldsK + l32 * RS + dc * 16 + hi * 8);
+                    s = Ops::mma(as_vec8<Vec>(a), as_vec8<Vec>(qreg[dc]), s);
+                }
+                float y[16];
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int t = t0 + (v >> 2) * 8 + hi * 4 + (v & 3);
+                    const float wgt = sp2_weight<false>(__builtin_fmaf(s[v], p.scale, -0.5f));
+                    y[v] = t < we ? wgt : 0.f;
+                    ssum += y[v];
+                }
+#pragma unroll
+                for (int c = 0; c < 2; ++c) {
+                    u32x4 pw;
+                    pw.x = pack2<T>(y[8 * c + 0], y[8 * c + 1]);
+                    pw.y = pack2<T>(y[8 * c + 2], y[8 * c + 3]);
+                    pw.z = pack2<T>(y[8 * c + 4], y[8 * c + 5]);
+                    pw.w = pack2<T>(y[8 * c + 6], y[8 * c + 7]);
+                    const Vec bop = as_vec8<Vec>(pw);
+#pragma unroll
+                    for (int dt = 0; dt < D / 32; ++dt) {
+                        const T* base = ldsV + (16 * c) * RSV + dt * 32 + v_tr_off;
+                        const uint2 lo = lds_read_tr16(base);
+                        const uint2 hi8 = lds_read_tr16(base + 8 * RSV);
+                        const u32x4 aw{lo.x, lo.y, hi8.x, hi8.y};
+                        oacc[dt] = Ops::mma(as_vec8<Vec>(aw), bop, oacc[dt]);
+                    }
+                }
+                __builtin_amdgcn_wave_barrier();
             }
+            ws = we;
         }
-    };
-    auto store_tile = [&]() {
-#pragma unroll
-        for (int i = 0; i < NC; ++i) {
-            const int tok = i * TPI + lane_tok;
-            *reinterpret_cast<u32x4*>(ldsK + tok * RS + lane_col) = kbuf[i];
-            *reinterpret_cast<u32x4*>(ldsV + tok * RSV + lane_col) = vbuf[i];
-        }
-    };
 
-    f32x16 oacc[D / 32];
-#pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) oacc[dt] = f32x16{};
-    float ssum = 0.f;
-    const int v_tr_off = ((lane >> 5) * 4 + ((lane & 15) >> 2)) * RSV + ((lane >> 4) & 1) * 16 + 4 * (lane & 3);
-
-    load_tile(t_begin);
-    for (int t0 = t_begin; t0 < t_end; t0 += kTile) {
-        // The block is one wavefront: LDS accesses of a wave complete in
-        // issue order, so a wave-level scheduling barrier is all the ordering
-        // needed (a workgroup barrier would also drain the prefetch below).
-        store_tile();
-        __builtin_amdgcn_wave_barrier();
-        if (t0 + kTile < t_end) load_tile(t0 + kTile);
-
-        f32x16 s = f32x16{};
-#pragma unroll
-        for (int dc = 0; dc < D / 16; ++dc) {
-            const u32x4 a = *reinterpret_cast<const u32x4*>(ldsK + l32 * RS + dc * 16 + hi * 8);
-            s = Ops::mma(as_vec8<Vec>(a), as_vec8<Vec>(qreg[dc]), s);
-        }
-        float y[16];
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int t = t0 + (v >> 2) * 8 + hi * 4 + (v & 3);
-            const float w = sp2_weight<false>(__builtin_fmaf(s[v], p.scale, -0.5f));
-            y[v] = t < t_end ? w : 0.f;
-            ssum += y[v];
-        }
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-            u32x4 pw;
-            pw.x = pack2<T>(y[8 * c + 0], y[8 * c + 1]);
-            pw.y = pack2<T>(y[8 * c + 2], y[8 * c + 3]);
-            pw.z = pack2<T>(y[8 * c + 4], y[8 * c + 5]);
-            pw.w = pack2<T>(y[8 * c + 6], y[8 * c + 7]);
-            const Vec bop = as_vec8<Vec>(pw);
+        const float stot = ssum + __shfl_xor(ssum, 32);
+        if (l32 < p.G) {
+            const int hq = hk * p.G + l32;
+            const int64_t slot = (static_cast<int64_t>(b) * p.Hq + hq) * p.n_slots + slot_k;
+            float* wo = p.ws_o + slot * D;
 #pragma unroll
             for (int dt = 0; dt < D / 32; ++dt) {
-                const T* base = ldsV + (16 * c) * RSV + dt * 32 + v_tr_off;
-                const uint2 lo = lds_read_tr16(base);
-                const uint2 hi8 = lds_read_tr16(base + 8 * RSV);
-                const u32x4 aw{lo.x, lo.y, hi8.x, hi8.y};
-                oacc[dt] = Ops::mma(as_vec8<Vec>(aw), bop, oacc[dt]);
-            }
-        }
-        __builtin_amdgcn_wave_barrier();
-    }
-
-    const float stot = ssum + __shfl_xor(ssum, 32);
-    if (l32 < p.G) {
-        const int hq = hk * p.G + l32;
-        const int64_t slot = (static_cast<int64_t>(b) * p.Hq + hq) * p.n_splits + split;
-        float* wo = p.ws_o + slot * D;
 #pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt) {
-#pragma unroll
-            for (int vg = 0; vg < 4; ++vg) {
-                const int d0 = dt * 32 + vg * 8 + hi * 4;
-                *reinterpret_cast<float4*>(wo + d0) =
-                    float4{oacc[dt][vg * 4 + 0], oacc[dt][vg * 4 + 1], oacc[dt][vg * 4 + 2], oacc[dt][vg * 4 + 3]};
+                for (int vg = 0; vg < 4; ++vg) {
+                    const int d0 = dt * 32 + vg * 8 + hi * 4;
+                    *reinterpret_cast<float4*>(wo + d0) = float4{oacc[dt][vg * 4 + 0], oacc[dt][vg * 4 + 1],
+                                                                 oacc[dt][vg * 4 + 2], oacc[dt][vg * 4 + 3]};
+                }
             }
+            if (hi == 0) p.ws_s[slot] = stot;
         }
-        if (hi == 0) p.ws_s[slot] = stot;
+        x = piece_end;
     }
 }
 
-// Sum the split partials of one (b, query head) in split order, then divide.
+// Sum the piece partials of one (b, query head) in slot order, then divide
+// (an empty context gives 0 / eps = 0).
 template <int D>
 __global__ __launch_bounds__(D) void paged_merge_kernel(PagedParams p) {
     const int bh = blockIdx.x;
     const int b = bh / p.Hq;
     const int hq = bh - b * p.Hq;
+    const int hk = hq / p.G;
     const int d = threadIdx.x;
-    const int ctx = min(max(p.ctx[b], 0), p.max_pages * p.P);
-    const int n_valid = (ctx + kSplitTok - 1) / kSplitTok;
-    const int64_t slot0 = static_cast<int64_t>(bh) * p.n_splits;
+    const int Tt = p.plan[p.B];
+    const int Ne = p.plan[p.B + 1];
+    const int seg0 = p.plan[b];
+    const int n_b = (p.plan[b + 1] - seg0) / p.Hkv;
     float o = 0.f, s = 0.f;
-    for (int i = 0; i < n_valid; ++i) {
-        o += p.ws_o[(slot0 + i) * D + d];
-        s += p.ws_s[slot0 + i];
+    if (n_b > 0) {
+        const int first = seg0 + hk * n_b, last = first + n_b - 1;
+        const int w0 = static_cast<int>((static_cast<int64_t>(first + 1) * Ne - 1) / Tt);
+        const int w1 = static_cast<int>((static_cast<int64_t>(last + 1) * Ne - 1) / Tt);
+        const int64_t slot0 = static_cast<int64_t>(bh) * p.n_slots;
+        for (int i = 0; i <= w1 - w0; ++i) {
+            o += p.ws_o[(slot0 + i) * D + d];
+            s += p.ws_s[slot0 + i];
+        }
     }
     p.out[b * p.os[0] + hq * p.os[1] + d * p.os[2]] = static_cast<bf16>(o / (s + kEps));
 }
 
+// Waves of paged_partial_kernel<T, D, U> resident on the device at once (the
+// persistent grid), per device.
+template <typename T, int D, bool U>
+int resident_waves() {
+    static int cache[16] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) dev = 0;
+    const int slot = dev < 16 ? dev : 15;
+    if (cache[slot] == 0) {
+        int cus = 0, per_cu = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_partial_kernel<T, D, U>, 64, 0) !=
+                hipSuccess ||
+            per_cu <= 0)
+            per_cu = 1;
+        cache[slot] = cus * per_cu;
+    }
+    return cache[slot];
+}
+
 template <typename T, int D>
-int launch_paged(const PagedParams& prm, hipStream_t st) {
-    const unsigned units = static_cast<unsigned>(prm.B) * prm.Hkv * prm.n_splits;
-    if (prm.P * (D / 8) >= 64)
-        paged_partial_kernel<T, D, true><<<units, 64, 0, st>>>(prm);
+int launch_paged(PagedParams prm, hipStream_t st) {
+    const bool uniform = prm.P * (D / 8) >= 64;
+    prm.n_waves = uniform ? resident_waves<T, D, true>() : resident_waves<T, D, false>();
+    paged_plan_kernel<<<1, 256, 0, st>>>(prm);
+    if (uniform)
+        paged_partial_kernel<T, D, true><<<prm.n_waves, 64, 0, st>>>(prm);
     else
-        paged_partial_kernel<T, D, false><<<units, 64, 0, st>>>(prm);
+        paged_partial_kernel<T, D, false><<<prm.n_waves, 64, 0, st>>>(prm);
     paged_merge_kernel<D><<<static_cast<unsigned>(prm.B) * prm.Hq, D, 0, st>>>(prm);
     return status_from_launch();
 }
 
-int64_t splits_for(int max_pages, int page_size) {
+// Partial slots per (sequence, query head): a segment of c tokens meets at
+// most ceil(c / kSplitTok) + 1 waves.
+int64_t slots_for(int max_pages, int page_size) {
     const int64_t toks = static_cast<int64_t>(max_pages) * page_size;
-    return toks <= 0 ? 1 : (toks + kSplitTok - 1) / kSplitTok;
+    return (toks <= 0 ? 1 : (toks + kSplitTok - 1) / kSplitTok) + 1;
 }
+
+// Workspace layout: plan (B + 2 int32, padded to 16 bytes), then the O and S
+// partials (fp32).
+int64_t plan_bytes(int B) { return ((static_cast<int64_t>(B) + 2) * 4 + 15) / 16 * 16; }
 
 }  // namespace
 }  // namespace sa
 
 extern "C" int64_t sa_paged_decode_workspace_size(int B, int Hq, int D, int max_pages, int page_size) {
     if (B <= 0 || Hq <= 0 || D <= 0 || max_pages < 0 || page_size <= 0) return 0;
-    const int64_t slots = static_cast<int64_t>(B) * Hq * sa::splits_for(max_pages, page_size);
-    return slots * (D + 1) * static_cast<int64_t>(sizeof(float));
+    const int64_t slots = static_cast<int64_t>(B) * Hq * sa::slots_for(max_pages, page_size);
+    return sa::plan_bytes(B) + slots * (D + 1) * static_cast<int64_t>(sizeof(float));
 }
 
 extern "C" int sa_paged_decode(const void* q, const void* k_cache, const void* v_cache, void* out,
@@ -283,9 +395,10 @@ extern "C" int sa_paged_decode(const void* q, const void* k_cache, const void* v
     prm.out = static_cast<bf16*>(out);
     prm.table = block_table;
     prm.ctx = context_lens;
-    prm.n_splits = static_cast<int>(splits_for(max_pages, page_size));
-    prm.ws_o = workspace;
-    prm.ws_s = workspace + static_cast<int64_t>(B) * Hq * prm.n_splits * D;
+    prm.n_slots = static_cast<int>(slots_for(max_pages, page_size));
+    prm.plan = reinterpret_cast<int*>(workspace);
+    prm.ws_o = workspace + plan_bytes(B) / 4;
+    prm.ws_s = prm.ws_o + static_cast<int64_t>(B) * Hq * prm.n_slots * D;
     for (int i = 0; i < 4; ++i) {
         prm.qs[i] = q_strides[i];
         prm.ks[i] = kv_strides[i];

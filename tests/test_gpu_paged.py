@@ -77,6 +77,51 @@ def test_paged_variable_context_lengths():
     assert bool((out[4] == 0).all())  # empty context -> 0 / eps = 0 (reference: o_acc / 1e-12)
 
 
+@pytest.mark.parametrize("D,BS,hq,hkv", [(64, 16, 4, 1), (128, 8, 8, 2)])
+def test_paged_many_skewed_sequences(D, BS, hq, hkv):
+    # 300 sequences (more than one 256-wide plan chunk and 64-lane search
+    # chunk), lengths skewed with empty ones: waves' tile ranges cross many
+    # sequence and head boundaries.
+    g = _g(D + BS)
+    B = 300
+    lens = torch.randint(0, 700, (B,), generator=g)
+    lens[::7] = 0
+    lens[5] = 4000
+    lens[-1] = 1
+    table, n_pages = paging.random_paged_layout(lens.tolist(), BS, generator=g)
+    kc = torch.randn(n_pages, hkv, BS, D, generator=g).to(torch.bfloat16)
+    vc = torch.randn(n_pages, hkv, BS, D, generator=g).to(torch.bfloat16)
+    q = torch.randn(B, hq, 1, D, generator=g).to(torch.bfloat16)
+    out = run(q, kc, vc, table, lens.to(torch.int32), BS)
+    ref = eager.paged_decode_eager(q.double(), kc.double(), vc.double(), table, lens.to(torch.int32))
+    assert bool(torch.isfinite(out).all())
+    assert rel_err(out, ref) <= 1e-2
+    empty = (lens == 0).nonzero().flatten()
+    assert bool((out[empty] == 0).all())
+
+
+@pytest.mark.parametrize("D,BS", [(128, 16), (128, 64), (64, 8), (32, 8), (32, 32)])
+def test_paged_ignores_cache_past_context(D, BS):
+    # Cache slots past each sequence's length (the tail of its last page,
+    # and whole pages past it) hold NaN: the output must not see them.
+    lens = [1, 15, 16, 17, 100, 511, 513, 700]
+    T = max(lens)
+    q, k, v = case(len(lens), 8, 2, T, D, seed=D + BS)
+    kc, vc, table, lens_t = paging.build_paged_cache(k, v, page_size=BS, shuffle=True, generator=_g(7),
+                                                     context_lens=lens)
+    ref = eager.paged_decode_eager(q.double(), kc.double(), vc.double(), table, lens_t)
+    kg, vg = kc.clone(), vc.clone()
+    for b, n in enumerate(lens):
+        for blk in range(table.shape[1]):
+            valid = max(0, min(BS, n - blk * BS))
+            phys = int(table[b, blk])
+            kg[phys, :, valid:] = float("nan")
+            vg[phys, :, valid:] = float("nan")
+    out = run(q, kg, vg, table, lens_t, BS)
+    assert bool(torch.isfinite(out).all())
+    assert rel_err(out, ref) <= 1e-2
+
+
 @pytest.mark.parametrize("BS", [8, 16, 32, 64])
 def test_paged_block_sizes_agree(BS):
     q, k, v = case(2, 4, 4, 128, 32, seed=5)
