@@ -197,7 +197,9 @@ int sa_flash_rope_fwd(const void* q, const void* k, const void* v,
                       int dtype, sa_stream_t stream);
 
 /*
- * Bytes of fp32 workspace sa_paged_decode needs for these sizes.
+ * Bytes of workspace sa_paged_decode needs for these sizes: a plan of B + 2
+ * int32 (padded to 16 bytes), then fp32 partials [B, Hq, n_slots, D] and
+ * [B, Hq, n_slots] with n_slots = ceil(max_pages * page_size / 512) + 1.
  */
 int64_t sa_paged_decode_workspace_size(int B, int Hq, int D, int max_pages,
                                        int page_size);
@@ -216,7 +218,8 @@ int64_t sa_paged_decode_workspace_size(int B, int Hq, int D, int max_pages,
  * out[b,h] = sum_{t<ctx_b} y_t V_t / (sum_t y_t + 1e-12) with
  * K_t = k_cache[block_table[b, t/P], h/(Hq/Hkv), t%P].  dtype (q and cache):
  * SA_BF16 or SA_F16.  D in {32, 64, 128}; page_size in {8,16,32,64}.
- * workspace: fp32, at least sa_paged_decode_workspace_size() bytes.
+ * workspace: at least sa_paged_decode_workspace_size() bytes, 16-byte
+ * aligned, no initialisation needed (a plan kernel writes it).
  * Replaces sp2norm_paged_attention (kernels.py:2776-2829) and its kernel
  * _sp2norm_paged_attention_kernel (:2681-2773).
  */
