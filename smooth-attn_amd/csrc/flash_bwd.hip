@@ -45,6 +45,7 @@ constexpr int kBwdBQ = 128;   // query rows per dQ block (32 per wave)
 constexpr int kBwdKT = 64;    // keys per staged tile in the dQ kernel
 constexpr int kBwdBK = 128;   // key rows per dK/dV block (32 per wave)
 constexpr int kBwdQT = 64;    // query rows per staged tile in the dK/dV kernel
+constexpr int kBwdXcdSlots = 64;  // blocks one XCD runs at once (32 CUs x 2)
 
 struct BwdParams {
     const void* q;
@@ -161,13 +162,13 @@ __global__ __launch_bounds__(kBwdThreads, 2) void flash_bwd_dq_kernel(BwdParams 
     const int l32 = lane & 31;
 
     const int nqb = (p.T + kBwdBQ - 1) / kBwdBQ;
-    const int BH = p.B * p.Hq;
-    const int id = blockIdx.x;
-    const int qb = nqb - 1 - id / BH;  // heaviest (latest) query blocks first
-    const int bh = id % BH;
-    const int b = bh / p.Hq;
-    const int hq = bh - b * p.Hq;
-    const int hk = hq / p.G;
+    int step, unit, sub;
+    grouped_block(blockIdx.x, p.B * p.Hkv, p.G, nqb, kBwdXcdSlots, step, unit, sub);
+    const int qb = nqb - 1 - step;  // heaviest (latest) query blocks first
+    const int b = unit / p.Hkv;
+    const int hk = unit - b * p.Hkv;
+    const int hq = hk * p.G + sub;
+    const int bh = b * p.Hq + hq;
     const int T_ = p.T;
 
     const T* qp = static_cast<const T*>(p.q) + b * p.qs[0] + hq * p.qs[1];
@@ -222,22 +223,22 @@ __global__ __launch_bounds__(kBwdThreads, 2) void flash_bwd_dq_kernel(BwdParams 
                           T_ - 1 - k0, lds + (2 * buf + 1) * Tl::BYTES, wave, lane);
     };
 
-    issue_tile(kv_begin, 0);
-    wait_vmem();
-    __syncthreads();
-    for (int j = kv_begin; j < kv_end; ++j) {
-        const int buf = (j - kv_begin) & 1;
-        const bool has_next = j + 1 < kv_end;
-        if (has_next) issue_tile(j + 1, buf ^ 1);
+    // One key tile for the wave's 32 query rows.  MASK: some row of the
+    // wave has keys of the tile outside its causal window (or past a
+    // window edge); halves no row sees are skipped.
+    auto tile_step = [&](auto mask_tag, int j, int buf) {
+        constexpr bool MASK = decltype(mask_tag)::value;
         const int k0 = j * kBwdKT;
         const unsigned char* Kb = lds + (2 * buf) * Tl::BYTES;
         const unsigned char* Vb = lds + (2 * buf + 1) * Tl::BYTES;
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
             const int kh0 = k0 + kt * 32;
-            // the wave's rows see some key of this half
-            const bool act = (kh0 <= wq0 + 31) && !(W > 0 && kh0 + 31 <= wq0 - W);
-            if (!act) continue;
+            if constexpr (MASK) {
+                // the wave's rows see some key of this half
+                const bool act = (kh0 <= wq0 + 31) && !(W > 0 && kh0 + 31 <= wq0 - W);
+                if (!act) continue;
+            }
             f32x16 s = f32x16{}, dp = f32x16{};
             const int r = kt * 32 + l32;
 #pragma unroll
@@ -248,16 +249,20 @@ __global__ __launch_bounds__(kBwdThreads, 2) void flash_bwd_dq_kernel(BwdParams 
                 s = Ops::mma(as_vec8<Vec>(ka), as_vec8<Vec>(qreg[dc]), s);
                 dp = Ops::mma(as_vec8<Vec>(va), as_vec8<Vec>(doreg[dc]), dp);
             }
-        // C layout: column = query l32, rows = keys kh0 + (v/4)*8 + 4 hi + v%4.
+            // C layout: column = query l32, rows = keys kh0 + (v/4)*8 + 4 hi + v%4.
             const int dbase = qi - kh0 - hi * 4;
             float ds[16];
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 float y, rr;
                 weight_and_rr<EXACT>(s[v], sc, y, rr);
-                const int cv = (v >> 2) * 8 + (v & 3);
                 const float g = (dp[v] - dl) * y * rr;
-                ds[v] = static_cast<unsigned>(dbase - cv) < weff ? g : 0.f;
+                if constexpr (MASK) {
+                    const int cv = (v >> 2) * 8 + (v & 3);
+                    ds[v] = static_cast<unsigned>(dbase - cv) < weff ? g : 0.f;
+                } else {
+                    ds[v] = g;
+                }
             }
 #pragma unroll
             for (int ch = 0; ch < 2; ++ch) {
@@ -270,13 +275,34 @@ __global__ __launch_bounds__(kBwdThreads, 2) void flash_bwd_dq_kernel(BwdParams 
                 const int c = 2 * kt + ch;  // 16-key chunk of the tile
 #pragma unroll
                 for (int dt = 0; dt < D / 32; ++dt)
-                    acc[dt] = Ops::mma(tr_operand<Vec, Tl>(Kb + 16 * c * Tl::ROWB, lane, dt), bop,
-                                       acc[dt]);
+                    acc[dt] = Ops::mma(tr_operand<Vec, Tl>(Kb + 16 * c * Tl::ROWB, lane, dt), bop, acc[dt]);
             }
         }
+    };
+    auto run_tile = [&](auto mask_tag, int j) {
+        const int buf = (j - kv_begin) & 1;
+        const bool has_next = j + 1 < kv_end;
+        if (has_next) issue_tile(j + 1, buf ^ 1);
+        tile_step(mask_tag, j, buf);
         wait_vmem();
         __syncthreads();
-    }
+    };
+
+    issue_tile(kv_begin, 0);
+    wait_vmem();
+    __syncthreads();
+    // Interior tiles [ja, jb): every row of the wave sees every key (jb: the
+    // tiles ending at or before the wave's first row; ja: the first tile past
+    // the window edge of its last row).  Separate loops per kind keep the
+    // accumulators in fixed registers.
+    int ja = kv_begin;
+    if (W > 0 && wq0 + 31 - W >= 0) ja = max(ja, (wq0 + 31 - W) / kBwdKT + 1);
+    ja = min(ja, kv_end);
+    const int jb = max(ja, min((wq0 + 1) / kBwdKT, kv_end));
+    int j = kv_begin;
+    for (; j < ja; ++j) run_tile(std::true_type{}, j);
+    for (; j < jb; ++j) run_tile(std::false_type{}, j);
+    for (; j < kv_end; ++j) run_tile(std::true_type{}, j);
 
     // dS was kept without its per-row factor 2 scale / R_i (applied here).
     if (qi < T_) {
@@ -314,12 +340,12 @@ __global__ __launch_bounds__(kBwdThreads, SA_BWD_DKDV_MINB) void flash_bwd_dkdv_
     const int hi = lane >> 5;
     const int l32 = lane & 31;
 
-    const int BHk = p.B * p.Hkv;
-    const int id = blockIdx.x;
-    const int kb = id / BHk;  // earliest key blocks see the most queries: first
-    const int bhk = id % BHk;
-    const int b = bhk / p.Hkv;
-    const int hk = bhk - b * p.Hkv;
+    const int nkb = (p.T + kBwdBK - 1) / kBwdBK;
+    int kb, unit, sub;
+    // earliest key blocks see the most queries: first
+    grouped_block(blockIdx.x, p.B * p.Hkv, 1, nkb, kBwdXcdSlots, kb, unit, sub);
+    const int b = unit / p.Hkv;
+    const int hk = unit - b * p.Hkv;
     const int T_ = p.T;
 
     const T* kp = static_cast<const T*>(p.k) + b * p.ks[0] + hk * p.ks[1];
@@ -381,16 +407,17 @@ __global__ __launch_bounds__(kBwdThreads, SA_BWD_DKDV_MINB) void flash_bwd_dkdv_
         if (tid < 2 * kBwdQT) ldr[buf][tid / kBwdQT][tid & (kBwdQT - 1)] = rst;
     };
 
-    issue_tile(0, 0);
-    store_rs(0);
-    wait_vmem();
-    __syncthreads();
-    for (int it = 0; it < n_it; ++it) {
-        const int buf = it & 1;
-        const bool has_next = it + 1 < n_it;
-        if (has_next) issue_tile(it + 1, buf ^ 1);
+    // One query tile (iteration it: head g = it / nq, tile qt_begin + it % nq)
+    // for the wave's 32 keys.  Masks are applied (a wave-uniform branch
+    // around them) only when some (query, key) pair of the tile is outside
+    // the causal window, past a window edge or past T; halves no query of
+    // which sees a key of the wave are skipped.  (One loop with the branch
+    // inside keeps the 128 accumulator registers in place; separate loops
+    // per tile kind made the compiler spill them.)
+    auto tile_step = [&](int it, int buf) {
         const int g = it / nq;
         const int q0 = (qt_begin + (it - g * nq)) * kBwdQT;
+        const bool interior = q0 >= wk0 + 31 && q0 + kBwdQT <= T_ && !(W > 0 && q0 + kBwdQT - 1 - wk0 >= W);
         const unsigned char* Qb = lds + (2 * buf) * Tl::BYTES;
         const unsigned char* Ob = lds + (2 * buf + 1) * Tl::BYTES;
 #pragma unroll
@@ -425,11 +452,18 @@ __global__ __launch_bounds__(kBwdThreads, SA_BWD_DKDV_MINB) void flash_bwd_dkdv_
                     const int v = vg * 4 + e;
                     float y, rr;
                     weight_and_rr<EXACT>(s[v], sc, y, rr);
-                    const int cv = vg * 8 + e;
-                    const bool ok = (static_cast<unsigned>(dbase + cv) < weff) && (cv < qlim);
                     const float yi = y * irv[e];
-                    pv[v] = ok ? yi : 0.f;
-                    ds[v] = ok ? (dp[v] - dlv[e]) * yi * rr : 0.f;
+                    pv[v] = yi;
+                    ds[v] = (dp[v] - dlv[e]) * yi * rr;
+                }
+            }
+            if (!interior) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int cv = (v >> 2) * 8 + (v & 3);
+                    const bool ok = (static_cast<unsigned>(dbase + cv) < weff) && (cv < qlim);
+                    pv[v] = ok ? pv[v] : 0.f;
+                    ds[v] = ok ? ds[v] : 0.f;
                 }
             }
 #pragma unroll
@@ -454,6 +488,16 @@ __global__ __launch_bounds__(kBwdThreads, SA_BWD_DKDV_MINB) void flash_bwd_dkdv_
                 }
             }
         }
+    };
+    issue_tile(0, 0);
+    store_rs(0);
+    wait_vmem();
+    __syncthreads();
+    for (int it = 0; it < n_it; ++it) {
+        const int buf = it & 1;
+        const bool has_next = it + 1 < n_it;
+        if (has_next) issue_tile(it + 1, buf ^ 1);
+        tile_step(it, buf);
         if (has_next) store_rs(buf ^ 1);
         wait_vmem();
         __syncthreads();

@@ -72,6 +72,42 @@ __device__ __forceinline__ V lds_read_tr16_pair(const void* p0, const void* p1) 
     return __builtin_bit_cast(V, ab);
 }
 
+// Block -> (step, unit, sub) for grids of n_steps x n_units x n_sub blocks,
+// where a unit is a KV head ((b, hk) pair), sub a query head sharing it and
+// step the tile position (step 0 runs first: callers map it to their
+// heaviest tiles).  Blocks are dealt to the 8 XCDs round-robin by index.
+// When n_units is a multiple of 8, XCD x gets units x, x+8, ... (each KV
+// head's data is then fetched into one XCD's L2 only), taken a few units at
+// a time: a group holds at least xcd_slots blocks (the blocks one XCD runs
+// at once), with the steps of the group's heads in order and its heads
+// fastest, so the blocks in flight share a handful of K/V (or Q/dO) streams
+// and the group's heavy steps still start early.  Otherwise step-major over
+// all (unit, sub).
+__device__ __forceinline__ void grouped_block(int id, int n_units, int n_sub, int n_steps, int xcd_slots,
+                                              int& step, int& unit, int& sub) {
+    if ((n_units & 7) == 0) {
+        const int x = id & 7;
+        const int j = id >> 3;
+        const int nh = (n_units >> 3) * n_sub;  // (unit, sub) pairs on this XCD
+        const int gu = min(max(1, (xcd_slots + n_sub * n_steps - 1) / (n_sub * n_steps)), n_units >> 3);
+        const int gh = gu * n_sub;  // pairs per group
+        const int grp = j / (gh * n_steps);
+        const int r = j - grp * (gh * n_steps);
+        const int ghs = min(gh, nh - grp * gh);  // pairs in this group (the last may be short)
+        step = r / ghs;
+        const int hl = grp * gh + (r - step * ghs);
+        const int ul = hl / n_sub;
+        unit = ul * 8 + x;
+        sub = hl - ul * n_sub;
+    } else {
+        const int per = n_units * n_sub;
+        step = id / per;
+        const int rest = id - step * per;
+        unit = rest / n_sub;
+        sub = rest - unit * n_sub;
+    }
+}
+
 // squareplus(a)^2 with a = scale * s - 1/2 already folded in:
 //   squareplus(2 s scale - 1) = (2 s scale - 1 + sqrt((2 s scale - 1)^2 + 4)) / 2
 //                             = a + sqrt(a^2 + 1),   a = s scale - 1/2.
