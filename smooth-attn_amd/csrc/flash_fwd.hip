@@ -199,44 +199,16 @@ __device__ __forceinline__ u32x4 tile_load16(const T* p) {
     return *reinterpret_cast<const u32x4*>(p);
 }
 
-// Block -> (query block, batch, query head).  Blocks are dealt to the 8 XCDs
-// round-robin by index.  When B*Hkv is a multiple of 8, XCD x gets the KV
-// heads u = x, x+8, ... together with all G query heads that read them (so
-// each KV head is fetched into one XCD's L2 only).  On each XCD the heads
-// are taken a few KV heads at a time (a group holds at least
-// kBlocksPerXcd blocks, one per CU), heaviest query block first within the
-// group: the blocks in flight then share a handful of K/V streams, and the
-// group's heavy blocks still start early enough not to form a tail.
-// Otherwise heaviest query block first across all heads.
+// Block -> (query block, batch, query head): grouped_block over the KV heads
+// (units) and the query heads sharing each (sub), heaviest query block first;
+// one block per CU, so an XCD runs 32 at once.
 constexpr int kBlocksPerXcd = 32;
 __device__ __forceinline__ void block_coords(const FlashParams& p, int& qb, int& b, int& hq) {
-    const int id = blockIdx.x;
-    const int BHk = p.B * p.Hkv;
-    if ((BHk & 7) == 0) {
-        const int x = id & 7;
-        const int j = id >> 3;
-        const int G = p.G;
-        const int nh = (BHk >> 3) * G;  // query heads per XCD
-        const int gkv = min(max(1, (kBlocksPerXcd + G * p.nqb - 1) / (G * p.nqb)), BHk >> 3);
-        const int gh = gkv * G;  // query heads per group
-        const int grp = j / (gh * p.nqb);
-        const int r = j - grp * (gh * p.nqb);
-        const int ghs = min(gh, nh - grp * gh);  // heads in this group (the last may be short)
-        const int step = r / ghs;
-        const int hl = grp * gh + (r - step * ghs);  // query head on this XCD
-        const int kvl = hl / G;
-        const int u = kvl * 8 + x;  // (b, hk)
-        b = u / p.Hkv;
-        const int hk = u - b * p.Hkv;
-        qb = p.nqb - 1 - step;
-        hq = hk * G + (hl - kvl * G);
-    } else {
-        const int BH = p.B * p.Hq;
-        qb = p.nqb - 1 - id / BH;
-        const int bh = id - (id / BH) * BH;
-        b = bh / p.Hq;
-        hq = bh - b * p.Hq;
-    }
+    int step, unit, sub;
+    grouped_block(blockIdx.x, p.B * p.Hkv, p.G, p.nqb, kBlocksPerXcd, step, unit, sub);
+    qb = p.nqb - 1 - step;
+    b = unit / p.Hkv;
+    hq = (unit - b * p.Hkv) * p.G + sub;
 }
 
 constexpr int kBQ2 = 32 * kWaves * kQT;  // query rows per block
