@@ -252,11 +252,15 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashParams p) {
     const int64_t vrs = p.vs[2] * (V8 ? 1 : 2);
 
     const int q_start = qb * kBQ2;
-    // Query tile qt of wave w: rows q_start + 32 (w + kWaves qt) .. +31, so
-    // the causal work of the waves stays balanced.
+    // Query tile qt of wave w: rows q_start + 32 (slot + kWaves qt) .. +31.
+    // Waves w and w + 4 share a SIMD; with 8 waves the second four take the
+    // row slots in reverse (7, 6, 5, 4), so each SIMD pairs an early-row
+    // wave (idle over more of the block's last, diagonal tiles) with a
+    // late-row one and the SIMDs carry equal work.
     int wq0[kQT];
+    const int slot = (kWaves == 8 && wave >= 4) ? 11 - wave : wave;
 #pragma unroll
-    for (int qt = 0; qt < kQT; ++qt) wq0[qt] = q_start + 32 * (wave + kWaves * qt);
+    for (int qt = 0; qt < kQT; ++qt) wq0[qt] = q_start + 32 * (slot + kWaves * qt);
     const int W = p.window;
     const int n_kv = (T_ + kBKV - 1) / kBKV;
     const int kv_end = min((q_start + kBQ2 + kBKV - 1) / kBKV, n_kv);
