@@ -13,7 +13,8 @@ dy and writes the full dx (2 bytes per element).
 The same JSON line carries the fused-attention figures the metric also names
 (config 3 forward and backward, TFLOP/s over the causal triangle), config 4
 (fp8), config 5 (paged decode), config 2 at L = 1024 / 2048 with its
-row-wise fp32 variant, config 1's shape on the GPU, the roofline of the
+row-wise fp32 variant, config 1's shape on the GPU, the rows built after the
+hot path (RoPE attention, softmax baselines, paged-KV append), the roofline of the
 dominant kernel (from HIP events around each launch), and the CPU
 baselines: the reference's eager CPU path restated in oracle/ (fp32 torch
 on the host cores), timed on a bounded sample of the config 2 workload and
@@ -256,6 +257,98 @@ def bench_paged(torch, iters):
     }
 
 
+def bench_next_rows(torch, iters):
+    """The rows built after the hot path, each timed like the rest (HIP
+    events on the launch stream, average per launch):
+    - RoPE-fused attention forward on config 3's shape (K rotated once by a
+      streaming kernel, Q in registers; the time includes the rotation),
+      and the RoPE + W_o projection variant (RoPE forward plus one fp32-
+      accumulating GEMM O[B*T, H*D] x W_o[H, D, D_model] viewed as
+      [H*D, D_model], D_model = H*D);
+    - row-wise and causal softmax (the comparison baselines) on config 2's
+      largest shapes: causal bf16 [4,16,4096,4096] (reads the triangle,
+      writes the full matrix), row-wise fp32 [64*4096, 4096];
+    - the paged-KV writer on config 5's cache: a 1-token decode append and
+      a 512-token chunk append for all 64 sequences."""
+    import smooth_attn as sa
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(11)
+    out = {}
+
+    def avg_us(fn, n):
+        for _ in range(2):
+            fn()
+        ms = time_events(torch, fn, n)
+        return sum(ms) / len(ms) * 1e3
+
+    B, H, L, D = 4, 32, 4096, 128
+    q, k, v = (torch.randn(B, H, L, D, generator=gen, device=dev).to(torch.bfloat16) for _ in range(3))
+    cos, sin = sa.precompute_rope_cos_sin(D, L, device=dev)
+    us = avg_us(lambda: sa.sp2norm_rope_flash_attention(q, k, v, cos, sin), iters)
+    fl = attn_flops(B, H, L, D)
+    out["rope_attention"] = {"shape": [B, H, L, D], "us": round(us, 1), "tflops": round(fl / us / 1e6, 1),
+                             "frac_bf16_peak": round(fl / us / 1e6 / BF16_PEAK_TFLOPS, 4),
+                             "note": "includes the K rotation (read + write of K)"}
+    d_model = H * D
+    w_o = (torch.randn(H, D, d_model, generator=gen, device=dev) / math.sqrt(H * D)).to(torch.bfloat16)
+    us = avg_us(lambda: sa.sp2norm_rope_flash_attention_proj(q, k, v, w_o, cos, sin), iters)
+    fl_proj = 2 * B * L * (H * D) * d_model
+    out["rope_attention_proj"] = {"shape": [B, H, L, D], "d_model": d_model, "us": round(us, 1),
+                                  "tflops": round((fl + fl_proj) / us / 1e6, 1),
+                                  "frac_bf16_peak": round((fl + fl_proj) / us / 1e6 / BF16_PEAK_TFLOPS, 4),
+                                  "flops": fl + fl_proj}
+    del q, k, v, w_o
+    torch.cuda.empty_cache()
+
+    Bn, Hn, Ln = 4, 16, 4096
+    x = (torch.randn(Bn, Hn, Ln, Ln, generator=gen, device=dev) / math.sqrt(128)).to(torch.bfloat16)
+    y = torch.empty_like(x)
+    us = avg_us(lambda: sa.softmax_causal_triton_out(y, x), iters)
+    nb = Bn * Hn * 2 * (tri(Ln) + Ln * Ln)
+    out["softmax_causal_bf16"] = {"shape": [Bn, Hn, Ln, Ln], "us": round(us, 1), "GBs": round(nb / us / 1e3, 1),
+                                  "frac_hbm_peak": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)}
+    del x, y
+    torch.cuda.empty_cache()
+    xr = torch.randn(Bn * Hn * Ln, Ln, generator=gen, device=dev)
+    yr = torch.empty_like(xr)
+    us = avg_us(lambda: sa.softmax_triton_out(yr, xr), iters)
+    nb = 2 * xr.numel() * 4
+    out["softmax_rowwise_fp32"] = {"shape": list(xr.shape), "us": round(us, 1), "GBs": round(nb / us / 1e3, 1),
+                                   "frac_hbm_peak": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)}
+    del xr, yr
+    torch.cuda.empty_cache()
+
+    Bp, Hkv, P = 64, 8, 16
+    g = torch.Generator().manual_seed(5)
+    lens = torch.randint(512, 16385, (Bp,), generator=g)
+    n_max = 512
+    npg = [(int(c) + n_max + P - 1) // P for c in lens]
+    n_pages = sum(npg)
+    perm = torch.randperm(n_pages, generator=g).to(torch.int32)
+    table = torch.zeros(Bp, max(npg), dtype=torch.int32)
+    pos = 0
+    for i, n in enumerate(npg):
+        table[i, :n] = perm[pos:pos + n]
+        pos += n
+    kc = torch.zeros(n_pages, Hkv, P, D, device=dev, dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    table_d = table.to(dev)
+    lens_d = lens.to(torch.int32).to(dev)
+    for n_new in (1, n_max):
+        kn = torch.randn(Bp, Hkv, n_new, D, generator=gen, device=dev).to(torch.bfloat16)
+        vn = torch.randn(Bp, Hkv, n_new, D, generator=gen, device=dev).to(torch.bfloat16)
+        us = avg_us(lambda: sa.sp2norm_paged_kv_append(kc, vc, kn, vn, table_d, lens_d, block_size=P), iters)
+        nb = 2 * 2 * kn.numel() * 2  # K and V rows, read once and written once
+        out[f"paged_append_{n_new}"] = {"seqs": Bp, "n_new": n_new, "us": round(us, 2),
+                                        "GBs": round(nb / us / 1e3, 1),
+                                        "frac_hbm_peak": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)}
+        del kn, vn
+    del kc, vc
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_norm_sizes(torch, sa, iters):
     """Config 2 at the other lengths (causal bf16, L = 1024, 2048), its
     row-wise fp32 variant (x, dy fp32 [64 L, L], L = 1024, 2048, 4096) and
@@ -402,7 +495,7 @@ def main():
     log("bench: causal norm fwd+bwd [4,16,4096,4096] bf16")
     norm = bench_norm(torch, sa, args.steps, args.warmup)
     log(f"bench: norm {norm['ms_per_step']:.3f} ms/step, fwd {norm['fwd_us']:.1f} us, bwd {norm['bwd_us']:.1f} us")
-    attn = fp8 = paged = sizes = None
+    attn = fp8 = paged = sizes = nxt = None
     if not args.no_extra:
         log("bench: fused attention config 3")
         attn = bench_attention(torch, sa, max(args.steps, 10))
@@ -416,6 +509,9 @@ def main():
         log("bench: config 2 other lengths, row-wise fp32, config 1 shape")
         sizes = bench_norm_sizes(torch, sa, max(args.steps, 10))
         log(f"bench: sizes {sizes}")
+        log("bench: RoPE attention, softmax baselines, paged-KV append")
+        nxt = bench_next_rows(torch, max(args.steps, 10))
+        log(f"bench: next rows {nxt}")
     cpu = None
     if not args.no_cpu:
         log("bench: cpu baseline")
@@ -463,6 +559,7 @@ def main():
         "fp8_attention": fp8,
         "paged_decode": paged,
         "norm_other_sizes": sizes,
+        "next_rows": nxt,
     }
     print(json.dumps(line), flush=True)
 
