@@ -108,31 +108,51 @@ __device__ __forceinline__ Vec tr_operand(const unsigned char* p, int lane, int 
 }
 
 typedef __attribute__((address_space(3))) void bwd_lds_void_t;
-typedef __attribute__((address_space(1))) void bwd_glb_void_t;
 
-// One 16-byte global -> LDS load per lane at lds_base + 16 * lane (wave-uniform base).
-__device__ __forceinline__ void dma16(const void* g, void* lds_base) {
-    __builtin_amdgcn_global_load_lds((bwd_glb_void_t*)(g), (bwd_lds_void_t*)(lds_base), 16, 0, 0);
+// Buffer resource over the nbytes bytes from base (raw, no stride): loads at
+// or past nbytes return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t bwd_rsrc(const void* base, int nbytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, nbytes, 0x00020000);
+}
+
+// One 16-byte buffer -> LDS load per lane: lane i writes bytes [16 i, 16 i + 16)
+// after lds_base (wave-uniform), read from byte voff of the resource.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, int voff, void* lds_base) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (bwd_lds_void_t*)(lds_base), 16, voff, 0, 0, 0);
+}
+
+// p, computed from wave-uniform values, as a scalar.
+__device__ __forceinline__ const unsigned char* bwd_uniform_ptr(const unsigned char* p) {
+    const uint64_t u = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
+    return reinterpret_cast<const unsigned char*>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
 // s_waitcnt vmcnt(0): this wave's direct-to-LDS loads have landed.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-// Issue the DMA loads of one [64][D] tile: rows row0 .. row0 + 63 of the
-// matrix at `base` (row stride rsb bytes), rows past `rmax` (relative)
-// clamped, into the swizzled LDS tile at `dst`.
+// Byte offset (from the tile's first row, row stride rsb) of the source of
+// this lane's DMA load i of a swizzled [64][D] tile: LDS slot s = (4 i +
+// wave) * 64 + lane holds row s / CPR, logical chunk (s % CPR) ^ f(row).
 template <int D>
-__device__ __forceinline__ void issue_swz_tile(const unsigned char* base, int rsb, int rmax, unsigned char* dst,
-                                               int wave, int lane) {
+__device__ __forceinline__ int swz_src_off(int i, int wave, int lane, int rsb) {
     using Tl = SwzTile<D>;
+    const int sl = (i * 4 + wave) * 64 + lane;
+    const int row = sl / Tl::CPR;
+    return row * rsb + (((sl - row * Tl::CPR) ^ Tl::f(row)) << 4);
+}
+
+// Issue the DMA loads of one [64][D] tile whose first row is at `base`
+// (wave-uniform; row stride rsb bytes) into the swizzled LDS tile at `dst`;
+// rows at or past `nrows` read as zeros.  off[i]: swz_src_off(i, ...).
+template <int D>
+__device__ __forceinline__ void issue_swz_tile(const unsigned char* base, int rsb, int nrows, unsigned char* dst,
+                                               int wave, const int (&off)[SwzTile<D>::NI]) {
+    using Tl = SwzTile<D>;
+    const __amdgpu_buffer_rsrc_t rs = bwd_rsrc(base, nrows * rsb);
 #pragma unroll
-    for (int i = 0; i < Tl::NI; ++i) {
-        const int sbase = (i * 4 + wave) * 64;
-        const int sl = sbase + lane;
-        const int row = sl / Tl::CPR;
-        const int c = (sl - row * Tl::CPR) ^ Tl::f(row);
-        dma16(base + (min(row, rmax) * rsb + c * 16), dst + sbase * 16);
-    }
+    for (int i = 0; i < Tl::NI; ++i) dma16(rs, off[i], dst + (i * 4 + wave) * 64 * 16);
 }
 
 template <bool EXACT>
@@ -172,8 +192,10 @@ __global__ __launch_bounds__(kBwdThreads, 2) void flash_bwd_dq_kernel(BwdParams 
     const int T_ = p.T;
 
     const T* qp = static_cast<const T*>(p.q) + b * p.qs[0] + hq * p.qs[1];
-    const T* kp = static_cast<const T*>(p.k) + b * p.ks[0] + hk * p.ks[1];
-    const T* vp = static_cast<const T*>(p.v) + b * p.vs[0] + hk * p.vs[1];
+    const unsigned char* kp =
+        bwd_uniform_ptr(reinterpret_cast<const unsigned char*>(static_cast<const T*>(p.k) + b * p.ks[0] + hk * p.ks[1]));
+    const unsigned char* vp =
+        bwd_uniform_ptr(reinterpret_cast<const unsigned char*>(static_cast<const T*>(p.v) + b * p.vs[0] + hk * p.vs[1]));
     const T* op = static_cast<const T*>(p.o) + b * p.os[0] + hq * p.os[1];
     const T* dop = static_cast<const T*>(p.dout) + b * p.dos[0] + hq * p.dos[1];
     T* dqp = static_cast<T*>(p.dq) + b * p.dqs[0] + hq * p.dqs[1];
@@ -215,12 +237,20 @@ __global__ __launch_bounds__(kBwdThreads, 2) void flash_bwd_dq_kernel(BwdParams 
     const float sc = p.scale;
 
     const int ksb = static_cast<int>(p.ks[2] * 2), vsb = static_cast<int>(p.vs[2] * 2);  // row strides (bytes)
+    int koff[Tl::NI], voff[Tl::NI];
+#pragma unroll
+    for (int i = 0; i < Tl::NI; ++i) {
+        koff[i] = swz_src_off<D>(i, wave, lane, ksb);
+        voff[i] = swz_src_off<D>(i, wave, lane, vsb);
+    }
+    // Keys past T read as zeros; they only meet masked weights (or rows
+    // past T, whose dQ is not written).
     auto issue_tile = [&](int j, int buf) {
         const int k0 = j * kBwdKT;
-        issue_swz_tile<D>(reinterpret_cast<const unsigned char*>(kp) + static_cast<int64_t>(k0) * ksb, ksb,
-                          T_ - 1 - k0, lds + (2 * buf) * Tl::BYTES, wave, lane);
-        issue_swz_tile<D>(reinterpret_cast<const unsigned char*>(vp) + static_cast<int64_t>(k0) * vsb, vsb,
-                          T_ - 1 - k0, lds + (2 * buf + 1) * Tl::BYTES, wave, lane);
+        const int nrows = min(T_ - k0, kBwdKT);
+        issue_swz_tile<D>(kp + static_cast<int64_t>(k0) * ksb, ksb, nrows, lds + (2 * buf) * Tl::BYTES, wave, koff);
+        issue_swz_tile<D>(vp + static_cast<int64_t>(k0) * vsb, vsb, nrows, lds + (2 * buf + 1) * Tl::BYTES, wave,
+                          voff);
     };
 
     // One key tile for the wave's 32 query rows.  MASK: some row of the
@@ -384,19 +414,25 @@ __global__ __launch_bounds__(kBwdThreads, SA_BWD_DKDV_MINB) void flash_bwd_dkdv_
 
     const int qsb = static_cast<int>(p.qs[2] * 2), dsb = static_cast<int>(p.dos[2] * 2);  // row strides (bytes)
     float rst = 0.f;
+    // Queries past T read as zeros; their weights are masked.
     auto issue_tile = [&](int it, int buf) {
         const int g = it / nq;
         const int qt = qt_begin + (it - g * nq);
         const int hq = hk * p.G + g;
-        const unsigned char* qp = reinterpret_cast<const unsigned char*>(static_cast<const T*>(p.q) + b * p.qs[0] +
-                                                                          hq * p.qs[1]);
-        const unsigned char* dop = reinterpret_cast<const unsigned char*>(static_cast<const T*>(p.dout) +
-                                                                           b * p.dos[0] + hq * p.dos[1]);
+        const unsigned char* qp = bwd_uniform_ptr(
+            reinterpret_cast<const unsigned char*>(static_cast<const T*>(p.q) + b * p.qs[0] + hq * p.qs[1]));
+        const unsigned char* dop = bwd_uniform_ptr(
+            reinterpret_cast<const unsigned char*>(static_cast<const T*>(p.dout) + b * p.dos[0] + hq * p.dos[1]));
         const int q0 = qt * kBwdQT;
-        issue_swz_tile<D>(qp + static_cast<int64_t>(q0) * qsb, qsb, T_ - 1 - q0, lds + (2 * buf) * Tl::BYTES, wave,
-                          lane);
-        issue_swz_tile<D>(dop + static_cast<int64_t>(q0) * dsb, dsb, T_ - 1 - q0, lds + (2 * buf + 1) * Tl::BYTES,
-                          wave, lane);
+        const int nrows = min(T_ - q0, kBwdQT);
+        int off[Tl::NI];
+#pragma unroll
+        for (int i = 0; i < Tl::NI; ++i) off[i] = swz_src_off<D>(i, wave, lane, qsb);
+        issue_swz_tile<D>(qp + static_cast<int64_t>(q0) * qsb, qsb, nrows, lds + (2 * buf) * Tl::BYTES, wave, off);
+#pragma unroll
+        for (int i = 0; i < Tl::NI; ++i) off[i] = swz_src_off<D>(i, wave, lane, dsb);
+        issue_swz_tile<D>(dop + static_cast<int64_t>(q0) * dsb, dsb, nrows, lds + (2 * buf + 1) * Tl::BYTES, wave,
+                          off);
         if (tid < 2 * kBwdQT) {
             const int r = tid & (kBwdQT - 1);
             const int64_t idx = (static_cast<int64_t>(b) * p.Hq + hq) * T_ + min(q0 + r, T_ - 1);
