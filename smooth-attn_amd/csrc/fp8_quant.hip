@@ -4,7 +4,9 @@
 // Three launches on one stream: zero the amax word, reduce amax with one
 // atomicMax per block (non-negative floats order like their bit patterns),
 // then quantise.  x / scale is a true division so the codes match torch's
-// fp32 division followed by the round-to-nearest-even e4m3fn cast.
+// fp32 division followed by the round-to-nearest-even e4m3fn cast.  Both
+// passes read 16 bytes per lane and step when x is 16-byte aligned (the
+// remainder, and unaligned inputs, element by element).
 #include "common.hpp"
 
 namespace sa {
@@ -24,12 +26,21 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 
 template <typename T>
-__global__ __launch_bounds__(kQThreads) void amax_kernel(const T* __restrict__ x, int64_t n, uint32_t* amax_bits) {
+__global__ __launch_bounds__(kQThreads) void amax_kernel(const T* __restrict__ x, int64_t n, uint32_t* amax_bits,
+                                                         int vec) {
+    constexpr int NV = 16 / sizeof(T);  // elements per 16-byte load
     __shared__ float part[kQThreads / 64];
     float m = 0.f;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kQThreads;
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kQThreads + threadIdx.x; i < n; i += stride)
-        m = fmaxf(m, fabsf(ld(x, i)));
+    const int64_t tid0 = static_cast<int64_t>(blockIdx.x) * kQThreads + threadIdx.x;
+    const int64_t nv = vec ? n / NV : 0;
+    for (int64_t i = tid0; i < nv; i += stride) {
+        uint32_t w[4];
+        load_words(x + i * NV, w);
+#pragma unroll
+        for (int e = 0; e < NV; ++e) m = fmaxf(m, fabsf(elem<T>(w, e)));
+    }
+    for (int64_t i = nv * NV + tid0; i < n; i += stride) m = fmaxf(m, fabsf(ld(x, i)));
     m = wave_max(m);
     if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = m;
     __syncthreads();
@@ -50,15 +61,47 @@ __device__ __forceinline__ uint32_t to_e4m3(float v) {
     return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(v, v, 0, false)) & 0xFFu;
 }
 
+// Four clamped values -> one word of e4m3fn codes (element e in byte e).
+__device__ __forceinline__ uint32_t pack_e4m3(float v0, float v1, float v2, float v3) {
+    const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(v0, v1, 0, false);
+    return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(v2, v3, lo, true));
+}
+
 template <typename T>
 __global__ __launch_bounds__(kQThreads) void quant_kernel(const T* __restrict__ x, uint8_t* __restrict__ x8, int64_t n,
-                                                          const uint32_t* amax_bits, float* scale_out) {
+                                                          const uint32_t* amax_bits, float* scale_out, int vec) {
+    constexpr int NV = 16 / sizeof(T);  // elements per 16-byte load
     const float scale = quant_scale(amax_bits);
     if (blockIdx.x == 0 && threadIdx.x == 0) scale_out[0] = scale;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kQThreads;
+    const int64_t tid0 = static_cast<int64_t>(blockIdx.x) * kQThreads + threadIdx.x;
+    if (vec) {
+        // NV elements per thread and step: one 16-byte load, NV / 4 word stores
+        const int64_t nv = n / NV;
+        for (int64_t i = tid0; i < nv; i += stride) {
+            uint32_t w[4];
+            load_words(x + i * NV, w);
+            float v[NV];
+#pragma unroll
+            for (int e = 0; e < NV; ++e) v[e] = fminf(fmaxf(elem<T>(w, e) / scale, -448.f), 448.f);
+            if constexpr (NV == 8) {
+                *reinterpret_cast<uint2*>(x8 + i * NV) =
+                    uint2{pack_e4m3(v[0], v[1], v[2], v[3]), pack_e4m3(v[4], v[5], v[6], v[7])};
+            } else {
+                *reinterpret_cast<uint32_t*>(x8 + i * NV) = pack_e4m3(v[0], v[1], v[2], v[3]);
+            }
+        }
+        if (blockIdx.x == 0) {
+            for (int64_t i = nv * NV + threadIdx.x; i < n; i += kQThreads) {
+                const float v = fminf(fmaxf(ld(x, i) / scale, -448.f), 448.f);
+                x8[i] = static_cast<uint8_t>(to_e4m3(v));
+            }
+        }
+        return;
+    }
     // four elements per thread and step, one 32-bit store
     const int64_t n4 = n / 4;
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kQThreads + threadIdx.x; i < n4; i += stride) {
+    for (int64_t i = tid0; i < n4; i += stride) {
         uint32_t word = 0;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -79,11 +122,15 @@ template <typename T>
 int launch_quant(const void* x, void* x8, int64_t n, float* amax_ws, float* scale_out, hipStream_t st) {
     uint32_t* ab = reinterpret_cast<uint32_t*>(amax_ws);
     fill_zero_u32<<<1, 1, 0, st>>>(ab);
-    const int64_t want = (n + kQThreads * 8 - 1) / (kQThreads * 8);
+    // 16-byte steps need x 16-byte aligned and x8 aligned to the step's
+    // output (8 or 4 bytes; the entry point requires 4)
+    constexpr int NV = 16 / sizeof(T);
+    const int vec = aligned16(x) && (reinterpret_cast<uintptr_t>(x8) % NV) == 0 ? 1 : 0;
+    const int64_t want = (n + kQThreads * 4 * NV - 1) / (kQThreads * 4 * NV);
     const unsigned blocks = static_cast<unsigned>(want < 1 ? 1 : (want > 4096 ? 4096 : want));
-    amax_kernel<T><<<blocks, kQThreads, 0, st>>>(static_cast<const T*>(x), n, ab);
+    amax_kernel<T><<<blocks, kQThreads, 0, st>>>(static_cast<const T*>(x), n, ab, vec);
     quant_kernel<T><<<blocks, kQThreads, 0, st>>>(static_cast<const T*>(x), static_cast<uint8_t*>(x8), n, ab,
-                                                  scale_out);
+                                                  scale_out, vec);
     return status_from_launch();
 }
 

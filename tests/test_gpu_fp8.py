@@ -47,6 +47,20 @@ def test_quantize_bit_exact(dtype, n):
     assert torch.equal(x8b.cpu().view(torch.uint8), ref8.view(torch.uint8))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_quantize_unaligned_input(dtype):
+    # a view starting one element into its storage: not 16-byte aligned, so
+    # the element-by-element path runs; codes must match all the same
+    g = _g(9)
+    base = (torch.randn(70001, generator=g) * 5).to(dtype).to(DEV)
+    x = base[1:]
+    assert x.data_ptr() % 16 != 0
+    x8, scale = kernels._quantize_to_fp8_device(x)
+    ref8, ref_scale = eager.quantize_to_fp8(x.cpu())
+    assert float(scale) == float(ref_scale)
+    assert torch.equal(x8.view(torch.uint8).cpu(), ref8.view(torch.uint8))
+
+
 def test_quantize_zero_and_shape():
     x8, scale = kernels._quantize_to_fp8_device(torch.zeros(3, 5, device=DEV, dtype=torch.bfloat16))
     assert x8.shape == (3, 5) and float(scale) == pytest.approx(1e-12)
