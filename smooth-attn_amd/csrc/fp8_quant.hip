@@ -5,14 +5,22 @@
 // atomicMax per block (non-negative floats order like their bit patterns),
 // then quantise.  x / scale is a true division so the codes match torch's
 // fp32 division followed by the round-to-nearest-even e4m3fn cast.  Both
-// passes read 16 bytes per lane and step when x is 16-byte aligned (the
-// remainder, and unaligned inputs, element by element).
+// passes read 16 bytes per lane and load when x is 16-byte aligned (the
+// remainder, and unaligned inputs, element by element), several loads in
+// flight per lane.
 #include "common.hpp"
 
 namespace sa {
 namespace {
 
 constexpr int kQThreads = 256;
+// The amax pass ends in one same-address atomicMax per block; those
+// serialise, so the pass runs on at most kAmaxBlocks blocks (one per CU)
+// with kAmaxUnroll loads in flight per lane (measured on config 4's Q,
+// 67M bf16: 4096 blocks 95 us, 512 blocks 64 us, 256 blocks x 8 loads 62 us
+// for amax + quantise together).
+constexpr unsigned kAmaxBlocks = 256;
+constexpr int kAmaxUnroll = 8;
 
 __global__ void fill_zero_u32(uint32_t* p) { p[0] = 0u; }
 
@@ -34,7 +42,20 @@ __global__ __launch_bounds__(kQThreads) void amax_kernel(const T* __restrict__ x
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kQThreads;
     const int64_t tid0 = static_cast<int64_t>(blockIdx.x) * kQThreads + threadIdx.x;
     const int64_t nv = vec ? n / NV : 0;
-    for (int64_t i = tid0; i < nv; i += stride) {
+    int64_t i = tid0;
+    // kAmaxUnroll independent 16-byte loads in flight per lane: the grid is
+    // small (see launch_quant), so each lane must keep several loads going
+    constexpr int U = kAmaxUnroll;
+    for (; i + (U - 1) * stride < nv; i += U * stride) {
+        uint32_t w[U][4];
+#pragma unroll
+        for (int u = 0; u < U; ++u) load_words(x + (i + u * stride) * NV, w[u]);
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int e = 0; e < NV; ++e) m = fmaxf(m, fabsf(elem<T>(w[u], e)));
+    }
+    for (; i < nv; i += stride) {
         uint32_t w[4];
         load_words(x + i * NV, w);
 #pragma unroll
@@ -78,18 +99,29 @@ __global__ __launch_bounds__(kQThreads) void quant_kernel(const T* __restrict__ 
     if (vec) {
         // NV elements per thread and step: one 16-byte load, NV / 4 word stores
         const int64_t nv = n / NV;
-        for (int64_t i = tid0; i < nv; i += stride) {
-            uint32_t w[4];
-            load_words(x + i * NV, w);
+        auto emit = [&](int64_t j, const uint32_t* w) {
             float v[NV];
 #pragma unroll
             for (int e = 0; e < NV; ++e) v[e] = fminf(fmaxf(elem<T>(w, e) / scale, -448.f), 448.f);
             if constexpr (NV == 8) {
-                *reinterpret_cast<uint2*>(x8 + i * NV) =
+                *reinterpret_cast<uint2*>(x8 + j * NV) =
                     uint2{pack_e4m3(v[0], v[1], v[2], v[3]), pack_e4m3(v[4], v[5], v[6], v[7])};
             } else {
-                *reinterpret_cast<uint32_t*>(x8 + i * NV) = pack_e4m3(v[0], v[1], v[2], v[3]);
+                *reinterpret_cast<uint32_t*>(x8 + j * NV) = pack_e4m3(v[0], v[1], v[2], v[3]);
             }
+        };
+        int64_t i = tid0;
+        for (; i + stride < nv; i += 2 * stride) {  // two loads in flight per lane
+            uint32_t w0[4], w1[4];
+            load_words(x + i * NV, w0);
+            load_words(x + (i + stride) * NV, w1);
+            emit(i, w0);
+            emit(i + stride, w1);
+        }
+        for (; i < nv; i += stride) {
+            uint32_t w[4];
+            load_words(x + i * NV, w);
+            emit(i, w);
         }
         if (blockIdx.x == 0) {
             for (int64_t i = nv * NV + threadIdx.x; i < n; i += kQThreads) {
@@ -128,7 +160,8 @@ int launch_quant(const void* x, void* x8, int64_t n, float* amax_ws, float* scal
     const int vec = aligned16(x) && (reinterpret_cast<uintptr_t>(x8) % NV) == 0 ? 1 : 0;
     const int64_t want = (n + kQThreads * 4 * NV - 1) / (kQThreads * 4 * NV);
     const unsigned blocks = static_cast<unsigned>(want < 1 ? 1 : (want > 4096 ? 4096 : want));
-    amax_kernel<T><<<blocks, kQThreads, 0, st>>>(static_cast<const T*>(x), n, ab, vec);
+    const unsigned ablocks = blocks > kAmaxBlocks ? kAmaxBlocks : blocks;
+    amax_kernel<T><<<ablocks, kQThreads, 0, st>>>(static_cast<const T*>(x), n, ab, vec);
     quant_kernel<T><<<blocks, kQThreads, 0, st>>>(static_cast<const T*>(x), static_cast<uint8_t*>(x8), n, ab,
                                                   scale_out, vec);
     return status_from_launch();

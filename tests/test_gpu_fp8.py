@@ -33,7 +33,7 @@ def rel_err(got, ref):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize("n", [1, 7, 4096, 100003])
+@pytest.mark.parametrize("n", [1, 7, 4096, 100003, 5000011])
 def test_quantize_bit_exact(dtype, n):
     g = _g(n)
     x = torch.randn(n, generator=g) * torch.exp(torch.randn(n, generator=g) * 3)  # wide dynamic range
@@ -57,6 +57,20 @@ def test_quantize_unaligned_input(dtype):
     assert x.data_ptr() % 16 != 0
     x8, scale = kernels._quantize_to_fp8_device(x)
     ref8, ref_scale = eager.quantize_to_fp8(x.cpu())
+    assert float(scale) == float(ref_scale)
+    assert torch.equal(x8.view(torch.uint8).cpu(), ref8.view(torch.uint8))
+
+
+@pytest.mark.parametrize("pos", [0, 3_000_000, 4_194_303, 4_500_000, 5_000_010])
+def test_quantize_amax_spike_anywhere(pos):
+    # one outlier sets the scale wherever it sits: in the amax pass's
+    # unrolled loads, its one-load remainder loop or the element tail
+    g = _g(pos)
+    x = (torch.randn(5_000_011, generator=g)).to(torch.bfloat16)
+    x[pos] = -300.0
+    x8, scale = kernels._quantize_to_fp8_device(x.to(DEV))
+    ref8, ref_scale = eager.quantize_to_fp8(x)
+    assert float(ref_scale) == pytest.approx(300.0 / 448.0)
     assert float(scale) == float(ref_scale)
     assert torch.equal(x8.view(torch.uint8).cpu(), ref8.view(torch.uint8))
 
