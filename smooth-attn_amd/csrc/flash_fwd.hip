@@ -216,7 +216,7 @@ constexpr int kBQ2 = 32 * kWaves * kQT;  // query rows per block
 // One block per CU: with one query tile per wave, 8 waves (2 per SIMD, 256
 // VGPRs per lane); with two, 4 waves (1 per SIMD, 512 registers per lane,
 // the O accumulators in AGPRs).
-template <typename T, int D, bool QK8, bool V8, bool EXACT, bool ROPE>
+template <typename T, int D, bool QK8, bool V8, bool EXACT, bool ROPE, bool FOLD = false>
 __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashParams p) {
     using Gm = Geom<T, D, QK8, V8>;
     using Ops = MfmaOps<T>;
@@ -436,10 +436,19 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashParams p) {
     struct STiles {
         f32x16 v[kQT];
     };
+    // FOLD: every S^T chain starts from c0 = -1/(2 sc) instead of 0, so the
+    // accumulator holds s' = s - 1/(2 sc) and a = sc s'.  Then
+    // (a + sqrt(a^2 + 1))^2 = sc^2 (s' + sqrt(s'^2 + 1/sc^2))^2: the weights
+    // are computed scaled by 1/sc^2 (one FMA per score fewer), which cancels
+    // between P V and the row sum (rescaled at the end).
+    const float c0 = -0.5f / sc, c2 = 1.f / (sc * sc);
+    f32x16 sinit;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) sinit[v] = FOLD ? c0 : 0.f;
     auto s_tile = [&](const KFrag (&kf)[Gm::NQC]) {
         STiles s;
 #pragma unroll
-        for (int qt = 0; qt < kQT; ++qt) s.v[qt] = f32x16{};
+        for (int qt = 0; qt < kQT; ++qt) s.v[qt] = FOLD ? sinit : f32x16{};
 #pragma unroll
         for (int dc = 0; dc < Gm::NQC; ++dc) {
 #pragma unroll
@@ -466,7 +475,13 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashParams p) {
         float y[16];
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-            float w = sp2_weight<EXACT>(__builtin_fmaf(s[v], sc, -0.5f));
+            float w;
+            if constexpr (FOLD) {
+                const float wf = s[v] + fast_sqrt(__builtin_fmaf(s[v], s[v], c2));
+                w = wf * wf;
+            } else {
+                w = sp2_weight<EXACT>(__builtin_fmaf(s[v], sc, -0.5f));
+            }
             if constexpr (MASK) {
                 const int cv = (v >> 2) * 8 + (v & 3);
                 w = static_cast<unsigned>(dbase - cv) < weff ? w : 0.f;
@@ -590,8 +605,10 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashParams p) {
     for (int qt = 0; qt < kQT; ++qt) {
         // Row sums: lanes l and l^32 hold the two key halves of one query column.
         const float part = (ssum[qt][0] + ssum[qt][1]) + (ssum[qt][2] + ssum[qt][3]);
-        const float stot = part + __shfl_xor(part, 32) + kEps;
-        const float inv = vsc / stot;
+        const float both = part + __shfl_xor(part, 32);
+        // FOLD: the sums and P V carry the factor 1/sc^2
+        const float stot = FOLD ? __builtin_fmaf(both, sc * sc, kEps) : both + kEps;
+        const float inv = FOLD ? vsc * (sc * sc) / stot : vsc / stot;
         const int qi = wq0[qt] + l32;
         if (qi < T_) {
             T* orow = op + qi * p.os[2];
@@ -611,14 +628,32 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashParams p) {
     }
 }
 
+// The folded weights (FOLD above) for bf16 P only: fp16 P would overflow
+// 65504 sooner by the factor 1/sc^2.  The scale must be positive and
+// moderate so that -1/(2 sc), 1/sc^2 and the scaled sums stay well inside
+// fp32; the fp8 path's scale is only known on the device and is not folded.
+// D = 128 only: the 16 registers holding the chains' start value cost the
+// D = 32 and 64 kernels a wave per SIMD (config 3, D = 128: 767 -> 752 us).
+template <typename T, bool QK8, int D>
+constexpr bool kCanFold = std::is_same_v<T, bf16> && !QK8 && D == 128;
+
+bool fold_scale_ok(float scale) { return scale >= 0x1p-20f && scale <= 0x1p20f; }
+
 template <typename T, int D, bool QK8, bool V8>
 int launch_flash(const FlashParams& prm, int exact, hipStream_t st) {
     const dim3 grid(static_cast<unsigned>(prm.nqb) * prm.B * prm.Hq);
     const dim3 block(kThreads);
-    if (exact)
+    if (exact) {
         flash_fwd_kernel<T, D, QK8, V8, true, false><<<grid, block, 0, st>>>(prm);
-    else
-        flash_fwd_kernel<T, D, QK8, V8, false, false><<<grid, block, 0, st>>>(prm);
+        return status_from_launch();
+    }
+    if constexpr (kCanFold<T, QK8, D>) {
+        if (fold_scale_ok(prm.scale)) {
+            flash_fwd_kernel<T, D, QK8, V8, false, false, true><<<grid, block, 0, st>>>(prm);
+            return status_from_launch();
+        }
+    }
+    flash_fwd_kernel<T, D, QK8, V8, false, false><<<grid, block, 0, st>>>(prm);
     return status_from_launch();
 }
 
@@ -638,6 +673,12 @@ int launch_rope(FlashParams prm, T* k_rot, hipStream_t st) {
     prm.ks[2] = D;
     prm.ks[3] = 1;
     const dim3 grid(static_cast<unsigned>(prm.nqb) * prm.B * prm.Hq);
+    if constexpr (kCanFold<T, false, D>) {
+        if (fold_scale_ok(prm.scale)) {
+            flash_fwd_kernel<T, D, false, false, false, true, true><<<grid, dim3(kThreads), 0, st>>>(prm);
+            return status_from_launch();
+        }
+    }
     flash_fwd_kernel<T, D, false, false, false, true><<<grid, dim3(kThreads), 0, st>>>(prm);
     return status_from_launch();
 }

@@ -68,6 +68,21 @@ def test_forward_gqa_window(hq, hkv, window):
     check_forward(*qkv(1, hq, hkv, 256, 64, torch.bfloat16, seed=hq * 10 + hkv + window), window=window)
 
 
+@pytest.mark.parametrize("scale", [0.02, 0.3, 1.7, 2.0 ** -21, -0.05])
+def test_forward_scales_d128(scale):
+    # D = 128 bf16 computes the weights scaled by 1/scale^2 (start value
+    # -1/(2 scale) on the score accumulators) for 2^-20 <= scale <= 2^20 and
+    # the plain form otherwise (the last two); outputs and row sums must match
+    # the oracle either way
+    q, k, v = qkv(2, 4, 2, 200, 128, torch.bfloat16, seed=int(abs(scale) * 1000) + 11)
+    o, rs = kernels._sp2norm_flash_fwd(q.to(DEV), k.to(DEV), v.to(DEV), scale, 2, 0)
+    ref, ref_rs = eager.flash_attention_eager(q.double(), k.double(), v.double(), scale=scale,
+                                              return_row_sums=True)
+    assert bool(torch.isfinite(o).all())
+    assert rel_err(o, ref) <= 1e-2
+    assert rel_err(rs, ref_rs) <= 1e-5
+
+
 def test_forward_exact_math():
     check_forward(*qkv(2, 4, 4, 256, 32, torch.bfloat16, seed=5), exact=True)
 
