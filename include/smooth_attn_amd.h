@@ -97,6 +97,45 @@ int sa_softmax_fwd(const void* x, void* y, int64_t n_rows, int64_t n_cols,
                    int64_t x_row_stride, int64_t y_row_stride, int dtype,
                    int causal, sa_stream_t stream);
 
+/* Row kernel variants (sa_launch_info.variant). */
+enum {
+    SA_ROW_SCALAR = 0, /* element loads (unaligned rows or n_cols % vec != 0) */
+    SA_ROW_VEC = 1,    /* one wave per row, 16-byte loads */
+    SA_ROW_SPLIT = 2   /* several waves per row, 16-byte loads */
+};
+
+/* The launch a row entry point makes for given arguments, and the compiled
+ * kernel's resources (queried from the HIP runtime on the current device). */
+typedef struct sa_launch_info {
+    int variant;          /* SA_ROW_* */
+    int grid_x;           /* blocks launched */
+    int block_threads;    /* threads per block (64 per wave) */
+    int rows_per_block;
+    int waves_per_row;
+    int elems_per_load;   /* elements per lane load: 16 bytes / element, or 1 */
+    int row_pass_elems;   /* columns one pass over a row covers (power of 2) */
+    int n_vgprs;          /* registers per lane of the compiled kernel */
+    int shared_mem_bytes; /* static LDS per block */
+    int blocks_per_cu;    /* resident blocks per CU (occupancy) */
+} sa_launch_info;
+
+/*
+ * Describe, without launching, the kernel sa_norm_fwd (resp. sa_softmax_fwd)
+ * runs for these arguments (x, y are only inspected for 16-byte alignment).
+ * Returns a status as the launchers do.  Backs the launch metadata
+ * (block_size, num_warps, num_programs, n_regs, shared_mem, occupancy) of
+ * return_meta=True (kernels.py:287-317, :1154-1172), which the reference
+ * reads from the compiled Triton kernel.
+ */
+int sa_norm_fwd_launch_info(const void* x, const void* y, int64_t n_rows,
+                            int64_t n_cols, int64_t x_row_stride,
+                            int64_t y_row_stride, int dtype, int power,
+                            sa_launch_info* info);
+int sa_softmax_fwd_launch_info(const void* x, const void* y, int64_t n_rows,
+                               int64_t n_cols, int64_t x_row_stride,
+                               int64_t y_row_stride, int dtype,
+                               sa_launch_info* info);
+
 /*
  * Fused causal squareplus attention forward (bf16 or fp16 q/k/v/o):
  *   O_i = sum_{j<=i, i-j<W} y_ij V_j / (sum_j y_ij + 1e-12),

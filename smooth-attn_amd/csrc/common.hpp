@@ -146,4 +146,41 @@ inline int status_from_launch() {
     return e == hipSuccess ? 0 : static_cast<int>(e);
 }
 
+// A planned row-kernel launch: the kernel (host stub address), its grid and
+// block, and how rows map onto waves.  The row entry points launch exactly
+// the plan their *_launch_info query describes.
+struct RowLaunch {
+    const void* fn = nullptr;
+    dim3 grid, block;
+    int variant = SA_ROW_SCALAR;
+    int rows_per_block = 1, waves_per_row = 1, elems_per_load = 1, row_pass_elems = 64;
+};
+
+inline int launch_row(const RowLaunch& L, void** args, hipStream_t st) {
+    const hipError_t e = hipLaunchKernel(L.fn, L.grid, L.block, args, 0, st);
+    return e == hipSuccess ? status_from_launch() : static_cast<int>(e);
+}
+
+// *info from a plan plus the compiled kernel's registers, static LDS and
+// occupancy on the current device.
+inline int describe_row_launch(const RowLaunch& L, sa_launch_info* info) {
+    hipFuncAttributes a{};
+    hipError_t e = hipFuncGetAttributes(&a, L.fn);
+    if (e != hipSuccess) return static_cast<int>(e);
+    int nb = 0;
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, L.fn, static_cast<int>(L.block.x), 0);
+    if (e != hipSuccess) return static_cast<int>(e);
+    info->variant = L.variant;
+    info->grid_x = static_cast<int>(L.grid.x);
+    info->block_threads = static_cast<int>(L.block.x);
+    info->rows_per_block = L.rows_per_block;
+    info->waves_per_row = L.waves_per_row;
+    info->elems_per_load = L.elems_per_load;
+    info->row_pass_elems = L.row_pass_elems;
+    info->n_vgprs = a.numRegs;
+    info->shared_mem_bytes = static_cast<int>(a.sharedSizeBytes);
+    info->blocks_per_cu = nb;
+    return 0;
+}
+
 }  // namespace sa

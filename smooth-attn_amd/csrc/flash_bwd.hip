@@ -224,6 +224,9 @@ __global__ __launch_bounds__(kBwdThreads, 2) void flash_bwd_dq_kernel(BwdParams 
     const int64_t rbase = static_cast<int64_t>(bh) * T_;
     if (qi < T_ && hi == 0) p.delta[rbase + qi] = dl;
     const float inv_r = 1.f / p.rs[rbase + qrow];
+    f32x16 ndl;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) ndl[v] = -dl;
 
     f32x16 acc[D / 32];
 #pragma unroll
@@ -269,7 +272,9 @@ __global__ __launch_bounds__(kBwdThreads, 2) void flash_bwd_dq_kernel(BwdParams 
                 const bool act = (kh0 <= wq0 + 31) && !(W > 0 && kh0 + 31 <= wq0 - W);
                 if (!act) continue;
             }
-            f32x16 s = f32x16{}, dp = f32x16{};
+            // the dP^T chain starts at -delta (this lane's query), so it ends
+            // holding dP - delta
+            f32x16 s = f32x16{}, dp = ndl;
             const int r = kt * 32 + l32;
 #pragma unroll
             for (int dc = 0; dc < D / 16; ++dc) {
@@ -286,7 +291,7 @@ __global__ __launch_bounds__(kBwdThreads, 2) void flash_bwd_dq_kernel(BwdParams 
             for (int v = 0; v < 16; ++v) {
                 float y, rr;
                 weight_and_rr<EXACT>(s[v], sc, y, rr);
-                const float g = (dp[v] - dl) * y * rr;
+                const float g = dp[v] * y * rr;
                 if constexpr (MASK) {
                     const int cv = (v >> 2) * 8 + (v & 3);
                     ds[v] = static_cast<unsigned>(dbase - cv) < weff ? g : 0.f;
@@ -362,7 +367,7 @@ __global__ __launch_bounds__(kBwdThreads, SA_BWD_DKDV_MINB) void flash_bwd_dkdv_
     using Tl = SwzTile<D>;
     static_assert(kBwdQT == 64, "query tiles are 64 rows");
     __shared__ __attribute__((aligned(1024))) unsigned char lds[2 * 2 * Tl::BYTES];  // [buf][Q, dO]
-    __shared__ __attribute__((aligned(16))) float ldr[2][2][kBwdQT];   // [buf][1/R, delta]
+    __shared__ __attribute__((aligned(16))) float ldr[2][2][kBwdQT];   // [buf][1/R, -delta]
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -436,7 +441,7 @@ __global__ __launch_bounds__(kBwdThreads, SA_BWD_DKDV_MINB) void flash_bwd_dkdv_
         if (tid < 2 * kBwdQT) {
             const int r = tid & (kBwdQT - 1);
             const int64_t idx = (static_cast<int64_t>(b) * p.Hq + hq) * T_ + min(q0 + r, T_ - 1);
-            rst = tid < kBwdQT ? 1.f / p.rs[idx] : p.delta[idx];
+            rst = tid < kBwdQT ? 1.f / p.rs[idx] : -p.delta[idx];
         }
     };
     auto store_rs = [&](int buf) {
@@ -462,7 +467,17 @@ __global__ __launch_bounds__(kBwdThreads, SA_BWD_DKDV_MINB) void flash_bwd_dkdv_
             // some query of this half sees some key of the wave
             const bool act = (qh0 + 31 >= wk0) && !(W > 0 && qh0 - (wk0 + 31) >= W) && qh0 < T_;
             if (!act) continue;
-            f32x16 s = f32x16{}, dp = f32x16{};
+            // the dP chain starts at -delta of its query rows (C layout, read
+            // from the staged -delta), so it ends holding dP - delta
+            f32x16 s = f32x16{}, dp;
+#pragma unroll
+            for (int vg = 0; vg < 4; ++vg) {
+                const float4 nd = *reinterpret_cast<const float4*>(&ldr[buf][1][qh * 32 + vg * 8 + hi * 4]);
+                dp[vg * 4 + 0] = nd.x;
+                dp[vg * 4 + 1] = nd.y;
+                dp[vg * 4 + 2] = nd.z;
+                dp[vg * 4 + 3] = nd.w;
+            }
             const int r = qh * 32 + l32;
 #pragma unroll
             for (int dc = 0; dc < D / 16; ++dc) {
@@ -480,9 +495,7 @@ __global__ __launch_bounds__(kBwdThreads, SA_BWD_DKDV_MINB) void flash_bwd_dkdv_
             for (int vg = 0; vg < 4; ++vg) {
                 const int roff = qh * 32 + vg * 8 + hi * 4;
                 const float4 ir = *reinterpret_cast<const float4*>(&ldr[buf][0][roff]);
-                const float4 dl = *reinterpret_cast<const float4*>(&ldr[buf][1][roff]);
                 const float irv[4] = {ir.x, ir.y, ir.z, ir.w};
-                const float dlv[4] = {dl.x, dl.y, dl.z, dl.w};
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int v = vg * 4 + e;
@@ -490,7 +503,7 @@ __global__ __launch_bounds__(kBwdThreads, SA_BWD_DKDV_MINB) void flash_bwd_dkdv_
                     weight_and_rr<EXACT>(s[v], sc, y, rr);
                     const float yi = y * irv[e];
                     pv[v] = yi;
-                    ds[v] = (dp[v] - dlv[e]) * yi * rr;
+                    ds[v] = dp[v] * yi * rr;
                 }
             }
             if (!interior) {

@@ -486,32 +486,43 @@ int chunks_for(int n_cols, int vec) {
 
 float eps_for_power(int power) { return kEps * static_cast<float>(1 << power); }
 
+// The forward launch for these arguments: element kernel for unaligned rows
+// (or n_cols not a multiple of the vector width), else one wave per row, or
+// split_for(NCH) waves per row for long rows.
 template <typename T, int POWER>
-int launch_fwd_t(const void* x, void* y, int64_t n_rows, int n_cols, int64_t xs, int64_t ys,
-                 int causal, float alpha, float theta, hipStream_t st) {
+int plan_fwd_t(const void* x, const void* y, int64_t n_rows, int n_cols, int64_t xs, int64_t ys, RowLaunch& L) {
     constexpr int VEC = 16 / sizeof(T);
-    const dim3 grid(static_cast<unsigned>((n_rows + kWavesPerBlock - 1) / kWavesPerBlock));
-    const dim3 block(64 * kWavesPerBlock);
-    const float nat = -alpha * theta;
-    const float eps = eps_for_power(POWER);
-    const T* xp = static_cast<const T*>(x);
-    T* yp = static_cast<T*>(y);
+    L.grid = dim3(static_cast<unsigned>((n_rows + kWavesPerBlock - 1) / kWavesPerBlock));
+    L.block = dim3(64 * kWavesPerBlock);
+    L.rows_per_block = kWavesPerBlock;
+    L.waves_per_row = 1;
     const bool vec_ok = (n_cols % VEC == 0) && (xs % VEC == 0) && (ys % VEC == 0) && aligned16(x) && aligned16(y);
     if (!vec_ok) {
-        norm_fwd_scalar<T, POWER><<<grid, block, 0, st>>>(xp, yp, n_rows, n_cols, xs, ys, causal, alpha, nat, eps);
-        return status_from_launch();
+        L.fn = reinterpret_cast<const void*>(&norm_fwd_scalar<T, POWER>);
+        L.variant = SA_ROW_SCALAR;
+        L.elems_per_load = 1;
+        L.row_pass_elems = 64;
+        return 0;
     }
-    switch (chunks_for(n_cols, VEC)) {
-#define SA_FWD_CASE(N)                                                                                  \
-    case N:                                                                                             \
-        if constexpr (split_for(N) > 1)                                                                 \
-            norm_fwd_split<T, N, POWER, split_for(N)><<<split_grid<split_for(N)>(n_rows),              \
-                                                            64 * split_block_waves<split_for(N)>(), 0, st>>>( \
-                    xp, yp, n_rows, n_cols, xs, ys, causal, alpha, nat, eps);                           \
-        else                                                                                            \
-            norm_fwd_vec<T, N, POWER><<<grid, block, 0, st>>>(xp, yp, n_rows, n_cols, xs, ys, causal, alpha, \
-                                                              nat, eps);                                \
-        break;
+    const int nch = chunks_for(n_cols, VEC);
+    L.elems_per_load = VEC;
+    L.row_pass_elems = nch * 64 * VEC;
+    switch (nch) {
+#define SA_FWD_CASE(N)                                                                        \
+    case N:                                                                                   \
+        if constexpr (split_for(N) > 1) {                                                     \
+            constexpr int R = split_for(N);                                                   \
+            L.fn = reinterpret_cast<const void*>(&norm_fwd_split<T, N, POWER, R>);            \
+            L.grid = split_grid<R>(n_rows);                                                   \
+            L.block = dim3(64 * split_block_waves<R>());                                      \
+            L.rows_per_block = split_block_waves<R>() / R;                                    \
+            L.waves_per_row = R;                                                              \
+            L.variant = SA_ROW_SPLIT;                                                         \
+        } else {                                                                              \
+            L.fn = reinterpret_cast<const void*>(&norm_fwd_vec<T, N, POWER>);                 \
+            L.variant = SA_ROW_VEC;                                                           \
+        }                                                                                     \
+        return 0;
         SA_FWD_CASE(1)
         SA_FWD_CASE(2)
         SA_FWD_CASE(4)
@@ -522,7 +533,21 @@ int launch_fwd_t(const void* x, void* y, int64_t n_rows, int n_cols, int64_t xs,
         default:
             return SA_ERR_UNSUPPORTED;
     }
-    return status_from_launch();
+}
+
+template <typename T, int POWER>
+int launch_fwd_t(const void* x, void* y, int64_t n_rows, int n_cols, int64_t xs, int64_t ys,
+                 int causal, float alpha, float theta, hipStream_t st) {
+    RowLaunch L;
+    const int pst = plan_fwd_t<T, POWER>(x, y, n_rows, n_cols, xs, ys, L);
+    if (pst != 0) return pst;
+    // every forward kernel takes (x, y, n_rows, n_cols, xs, ys, causal, alpha, -alpha theta, eps)
+    const T* xp = static_cast<const T*>(x);
+    T* yp = static_cast<T*>(y);
+    float nat = -alpha * theta;
+    float eps = eps_for_power(POWER);
+    void* args[] = {&xp, &yp, &n_rows, &n_cols, &xs, &ys, &causal, &alpha, &nat, &eps};
+    return launch_row(L, args, st);
 }
 
 template <typename T>
@@ -616,6 +641,34 @@ extern "C" int sa_norm_fwd(const void* x, void* y, int64_t n_rows, int64_t n_col
         case SA_BF16: return launch_fwd_p<bf16>(x, y, n_rows, nc, x_row_stride, y_row_stride, causal, alpha, theta, power, st);
         default: return SA_ERR_BAD_DTYPE;
     }
+}
+
+extern "C" int sa_norm_fwd_launch_info(const void* x, const void* y, int64_t n_rows, int64_t n_cols,
+                                       int64_t x_row_stride, int64_t y_row_stride, int dtype, int power,
+                                       sa_launch_info* info) {
+    using namespace sa;
+    if (info == nullptr) return SA_ERR_NULL_POINTER;
+    if (n_rows < 0 || n_cols <= 0 || n_cols > kMaxCols) return SA_ERR_BAD_SHAPE;
+    if (x_row_stride < n_cols || y_row_stride < n_cols) return SA_ERR_BAD_STRIDE;
+    const int nc = static_cast<int>(n_cols);
+    RowLaunch L;
+    int st = SA_ERR_BAD_FAMILY;
+#define SA_PLAN(TT)                                                                                      \
+    switch (power) {                                                                                     \
+        case 1: st = plan_fwd_t<TT, 1>(x, y, n_rows, nc, x_row_stride, y_row_stride, L); break;           \
+        case 2: st = plan_fwd_t<TT, 2>(x, y, n_rows, nc, x_row_stride, y_row_stride, L); break;           \
+        case 3: st = plan_fwd_t<TT, 3>(x, y, n_rows, nc, x_row_stride, y_row_stride, L); break;           \
+        default: break;                                                                                  \
+    }
+    switch (dtype) {
+        case SA_F32: SA_PLAN(float) break;
+        case SA_F16: SA_PLAN(f16) break;
+        case SA_BF16: SA_PLAN(bf16) break;
+        default: return SA_ERR_BAD_DTYPE;
+    }
+#undef SA_PLAN
+    if (st != 0) return st;
+    return describe_row_launch(L, info);
 }
 
 extern "C" int sa_norm_bwd(const void* x, const void* dy, void* dx, int64_t n_rows, int64_t n_cols,

@@ -106,25 +106,30 @@ __global__ __launch_bounds__(256) void softmax_fwd_scalar(const T* __restrict__ 
 constexpr int kSmMaxCols = 8192;
 
 template <typename T>
-int launch_softmax(const void* x, void* y, int64_t n_rows, int n_cols, int64_t xs, int64_t ys, int causal,
-                   hipStream_t st) {
+int plan_softmax(const void* x, const void* y, int64_t n_rows, int n_cols, int64_t xs, int64_t ys, RowLaunch& L) {
     constexpr int VEC = 16 / sizeof(T);
-    const dim3 grid(static_cast<unsigned>((n_rows + kSmWavesPerBlock - 1) / kSmWavesPerBlock));
-    const dim3 block(64 * kSmWavesPerBlock);
-    const T* xp = static_cast<const T*>(x);
-    T* yp = static_cast<T*>(y);
+    L.grid = dim3(static_cast<unsigned>((n_rows + kSmWavesPerBlock - 1) / kSmWavesPerBlock));
+    L.block = dim3(64 * kSmWavesPerBlock);
+    L.rows_per_block = kSmWavesPerBlock;
+    L.waves_per_row = 1;
     const bool vec_ok = (n_cols % VEC == 0) && (xs % VEC == 0) && (ys % VEC == 0) && aligned16(x) && aligned16(y);
     if (!vec_ok) {
-        softmax_fwd_scalar<T><<<grid, block, 0, st>>>(xp, yp, n_rows, n_cols, xs, ys, causal);
-        return status_from_launch();
+        L.fn = reinterpret_cast<const void*>(&softmax_fwd_scalar<T>);
+        L.variant = SA_ROW_SCALAR;
+        L.elems_per_load = 1;
+        L.row_pass_elems = 64;
+        return 0;
     }
     int need = (n_cols + 64 * VEC - 1) / (64 * VEC), nch = 1;
     while (nch < need) nch *= 2;
+    L.variant = SA_ROW_VEC;
+    L.elems_per_load = VEC;
+    L.row_pass_elems = nch * 64 * VEC;
     switch (nch) {
-#define SA_SM_CASE(N)                                                                          \
-    case N:                                                                                    \
-        softmax_fwd_vec<T, N><<<grid, block, 0, st>>>(xp, yp, n_rows, n_cols, xs, ys, causal); \
-        break;
+#define SA_SM_CASE(N)                                                     \
+    case N:                                                               \
+        L.fn = reinterpret_cast<const void*>(&softmax_fwd_vec<T, N>);     \
+        return 0;
         SA_SM_CASE(1)
         SA_SM_CASE(2)
         SA_SM_CASE(4)
@@ -135,7 +140,19 @@ int launch_softmax(const void* x, void* y, int64_t n_rows, int n_cols, int64_t x
         default:
             return SA_ERR_UNSUPPORTED;
     }
-    return status_from_launch();
+}
+
+template <typename T>
+int launch_softmax(const void* x, void* y, int64_t n_rows, int n_cols, int64_t xs, int64_t ys, int causal,
+                   hipStream_t st) {
+    RowLaunch L;
+    const int pst = plan_softmax<T>(x, y, n_rows, n_cols, xs, ys, L);
+    if (pst != 0) return pst;
+    // both kernels take (x, y, n_rows, n_cols, xs, ys, causal)
+    const T* xp = static_cast<const T*>(x);
+    T* yp = static_cast<T*>(y);
+    void* args[] = {&xp, &yp, &n_rows, &n_cols, &xs, &ys, &causal};
+    return launch_row(L, args, st);
 }
 
 }  // namespace
@@ -156,4 +173,24 @@ extern "C" int sa_softmax_fwd(const void* x, void* y, int64_t n_rows, int64_t n_
         case SA_BF16: return launch_softmax<bf16>(x, y, n_rows, nc, x_row_stride, y_row_stride, causal, st);
         default: return SA_ERR_BAD_DTYPE;
     }
+}
+
+extern "C" int sa_softmax_fwd_launch_info(const void* x, const void* y, int64_t n_rows, int64_t n_cols,
+                                          int64_t x_row_stride, int64_t y_row_stride, int dtype,
+                                          sa_launch_info* info) {
+    using namespace sa;
+    if (info == nullptr) return SA_ERR_NULL_POINTER;
+    if (n_rows < 0 || n_cols <= 0 || n_cols > kSmMaxCols) return SA_ERR_BAD_SHAPE;
+    if (x_row_stride < n_cols || y_row_stride < n_cols) return SA_ERR_BAD_STRIDE;
+    const int nc = static_cast<int>(n_cols);
+    RowLaunch L;
+    int st;
+    switch (dtype) {
+        case SA_F32: st = plan_softmax<float>(x, y, n_rows, nc, x_row_stride, y_row_stride, L); break;
+        case SA_F16: st = plan_softmax<f16>(x, y, n_rows, nc, x_row_stride, y_row_stride, L); break;
+        case SA_BF16: st = plan_softmax<bf16>(x, y, n_rows, nc, x_row_stride, y_row_stride, L); break;
+        default: return SA_ERR_BAD_DTYPE;
+    }
+    if (st != 0) return st;
+    return describe_row_launch(L, info);
 }

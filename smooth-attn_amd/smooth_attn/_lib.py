@@ -21,6 +21,17 @@ SA_F32, SA_F16, SA_BF16, SA_FP8_E4M3FN = 0, 1, 2, 3
 
 _I64P = POINTER(c_int64)
 
+
+class LaunchInfo(ctypes.Structure):
+    """``sa_launch_info`` of include/smooth_attn_amd.h."""
+
+    _fields_ = [(name, c_int) for name in (
+        "variant", "grid_x", "block_threads", "rows_per_block", "waves_per_row", "elems_per_load",
+        "row_pass_elems", "n_vgprs", "shared_mem_bytes", "blocks_per_cu")]
+
+
+ROW_VARIANTS = {0: "scalar", 1: "vec", 2: "split"}
+
 # name -> (restype, argtypes); mirrors include/smooth_attn_amd.h.
 SIGNATURES = {
     "sa_status_string": (ctypes.c_char_p, [c_int]),
@@ -29,6 +40,10 @@ SIGNATURES = {
     "sa_norm_bwd": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64,
                             c_int, c_int, c_int, c_float, c_float, c_int, c_void_p]),
     "sa_softmax_fwd": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int, c_int, c_void_p]),
+    "sa_norm_fwd_launch_info": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int, c_int,
+                                        POINTER(LaunchInfo)]),
+    "sa_softmax_fwd_launch_info": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int,
+                                           POINTER(LaunchInfo)]),
     "sa_flash_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int,
                              c_int, _I64P, _I64P, _I64P, _I64P, c_float, c_int, c_int, c_int, c_void_p]),
     "sa_flash_bwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,

@@ -8,6 +8,7 @@ Citations are ``path:line`` into the reference.
 """
 from __future__ import annotations
 
+import ctypes
 import math
 from dataclasses import dataclass
 
@@ -161,23 +162,53 @@ def _is_winner_family(family):
     return family.cache_key == DEFAULT_FAMILY.cache_key
 
 
-def _row_launch_meta(variant, n_rows, n_cols, dtype):
-    vec = 16 // torch.empty((), dtype=dtype).element_size()
-    chunks = 1
-    while chunks * 64 * vec < n_cols:
-        chunks *= 2
-    return {
-        "variant": variant,
-        "block_size": chunks * 64 * vec,
-        "num_warps": 4,
-        "num_stages": 1,
-        "num_programs": (n_rows + 3) // 4,
-        "rows_per_wave": 1,
-        "occupancy": None,
-        "n_regs": None,
-        "shared_mem": 0,
-        "time_us": None,
-    }
+_LAUNCH_META_CACHE = {}
+
+
+def _row_launch_meta(variant, kind, x2d, y2d, rerun, power=2):
+    """Launch metadata of a row entry point — the keys of kernels.py:310-317
+    and :423-427.  Everything but ``time_us`` describes the kernel the call
+    just ran (``sa_*_launch_info``: variant, grid, registers, static LDS,
+    resident blocks per CU); ``time_us`` is the median of a few re-runs of
+    the same call, measured on the first request per shape and cached, as the
+    reference's autotuner measures its candidates on first use."""
+    n_rows, n_cols = x2d.shape
+    key = (kind, power, x2d.dtype, n_rows, n_cols, x2d.stride(0), y2d.stride(0),
+           x2d.data_ptr() % 16 == 0 and y2d.data_ptr() % 16 == 0, x2d.device.index)
+    meta = _LAUNCH_META_CACHE.get(key)
+    if meta is None:
+        if n_rows == 0 or n_cols == 0:
+            meta = {"block_size": 0, "num_warps": 0, "num_stages": 1, "num_programs": 0, "rows_per_program": 0,
+                    "waves_per_row": 0, "kernel": None, "occupancy": None, "n_regs": None, "shared_mem": 0,
+                    "time_us": None}
+        else:
+            lib = _lib.load()
+            info = _lib.LaunchInfo()
+            with torch.cuda.device(x2d.device):
+                if kind == "norm":
+                    st = lib.sa_norm_fwd_launch_info(x2d.data_ptr(), y2d.data_ptr(), n_rows, n_cols, x2d.stride(0),
+                                                     y2d.stride(0), _DTYPE_CODE[x2d.dtype], int(power),
+                                                     ctypes.byref(info))
+                else:
+                    st = lib.sa_softmax_fwd_launch_info(x2d.data_ptr(), y2d.data_ptr(), n_rows, n_cols,
+                                                        x2d.stride(0), y2d.stride(0), _DTYPE_CODE[x2d.dtype],
+                                                        ctypes.byref(info))
+            _lib.check(st, f"sa_{kind}_fwd_launch_info")
+            meta = {
+                "block_size": info.row_pass_elems,
+                "num_warps": info.block_threads // 64,
+                "num_stages": 1,
+                "num_programs": info.grid_x,
+                "rows_per_program": info.rows_per_block,
+                "waves_per_row": info.waves_per_row,
+                "kernel": _lib.ROW_VARIANTS.get(info.variant, str(info.variant)),
+                "occupancy": info.blocks_per_cu,
+                "n_regs": info.n_vgprs,
+                "shared_mem": info.shared_mem_bytes,
+                "time_us": _median_cuda_us(rerun, warmup=2, iters=5),
+            }
+        _LAUNCH_META_CACHE[key] = meta
+    return {"variant": variant, **meta}
 
 
 # ---------------------------------------------------------------------------
@@ -217,7 +248,8 @@ def softplus_norm_triton(x, alpha=DEFAULT_FAMILY.alpha, theta=DEFAULT_FAMILY.the
     out = torch.empty_like(x_row)
     _norm_fwd_2d(x_row, out, family, causal=False)
     if return_meta:
-        return out, _row_launch_meta("softplus_norm", *x_row.shape, x_row.dtype)
+        return out, _row_launch_meta("softplus_norm", "norm", x_row, out,
+                                     lambda: _norm_fwd_2d(x_row, out, family, causal=False), family.power)
     return out
 
 
@@ -230,7 +262,9 @@ def softplus_norm_triton_out(out, x, alpha=DEFAULT_FAMILY.alpha, theta=DEFAULT_F
     _norm_fwd_2d(x_row, kernel_out, family, causal=False)
     result = _finalize_output(kernel_out, user_out)
     if return_meta:
-        return result, _row_launch_meta("softplus_norm", *x_row.shape, x_row.dtype)
+        return result, _row_launch_meta("softplus_norm", "norm", x_row, kernel_out,
+                                        lambda: _norm_fwd_2d(x_row, kernel_out, family, causal=False),
+                                        family.power)
     return result
 
 
@@ -257,7 +291,8 @@ def softplus_norm_causal_triton_out(out, x, alpha=DEFAULT_FAMILY.alpha, theta=DE
     result = _finalize_output(kernel_out, user_out)
     if return_meta:
         variant = "squareplus_winner" if _is_winner_family(family) else "softplus_norm_causal"
-        return result, _row_launch_meta(variant, x2d.shape[0], seq_len, x2d.dtype)
+        return result, _row_launch_meta(variant, "norm", x2d, o2d,
+                                        lambda: _norm_fwd_2d(x2d, o2d, family, causal=True), family.power)
     return result
 
 
@@ -401,7 +436,7 @@ def softmax_triton(x, return_meta=False):
     out = torch.empty_like(x_row)
     _softmax_2d(x_row, out, causal=False)
     if return_meta:
-        return out, _row_launch_meta("softmax", *x_row.shape, x_row.dtype)
+        return out, _row_launch_meta("softmax", "softmax", x_row, out, lambda: _softmax_2d(x_row, out, causal=False))
     return out
 
 
@@ -412,7 +447,8 @@ def softmax_triton_out(out, x, return_meta=False):
     _softmax_2d(x_row, kernel_out, causal=False)
     result = _finalize_output(kernel_out, user_out)
     if return_meta:
-        return result, _row_launch_meta("softmax", *x_row.shape, x_row.dtype)
+        return result, _row_launch_meta("softmax", "softmax", x_row, kernel_out,
+                                        lambda: _softmax_2d(x_row, kernel_out, causal=False))
     return result
 
 
@@ -423,10 +459,12 @@ def softmax_causal_triton_out(out, x, return_meta=False):
     kernel_out, user_out = _prepare_output(out, x_attn)
     seq_len = x_attn.shape[-1]
     x2d = x_attn.view(-1, seq_len)
-    _softmax_2d(x2d, kernel_out.view(-1, seq_len), causal=True)
+    o2d = kernel_out.view(-1, seq_len)
+    _softmax_2d(x2d, o2d, causal=True)
     result = _finalize_output(kernel_out, user_out)
     if return_meta:
-        return result, _row_launch_meta("softmax_causal", x2d.shape[0], seq_len, x2d.dtype)
+        return result, _row_launch_meta("softmax_causal", "softmax", x2d, o2d,
+                                        lambda: _softmax_2d(x2d, o2d, causal=True))
     return result
 
 

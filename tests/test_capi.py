@@ -1,5 +1,6 @@
 """The C-ABI library loads and exports every entry point the header declares —
 CPU only (no kernel launch; sa_status_string is host code)."""
+import ctypes
 import re
 from pathlib import Path
 
@@ -37,3 +38,27 @@ def test_status_strings():
     assert b"dtype" in lib.sa_status_string(-3)
     with pytest.raises(RuntimeError, match="dtype"):
         _lib.check(-3, "probe")
+
+
+def test_launch_info_struct_matches_header():
+    # field names and order of sa_launch_info, all int
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    body = re.search(r"typedef struct sa_launch_info \{(.*?)\} sa_launch_info;", text, flags=re.S).group(1)
+    fields = re.findall(r"int\s+(\w+)\s*;", body)
+    assert fields == [name for name, _ in _lib.LaunchInfo._fields_]
+    assert len(re.findall(r";", body)) == len(fields)
+    assert _lib.LaunchInfo().__sizeof__() >= 4 * len(fields)
+
+
+def test_launch_info_argument_errors():
+    # rejected before any HIP call, so these run without a GPU
+    lib = _lib.load()
+    info = _lib.LaunchInfo()
+    assert lib.sa_norm_fwd_launch_info(None, None, 4, 64, 64, 64, _lib.SA_BF16, 2, None) == -1
+    assert lib.sa_norm_fwd_launch_info(None, None, 4, 0, 64, 64, _lib.SA_BF16, 2, ctypes.byref(info)) == -2
+    assert lib.sa_norm_fwd_launch_info(None, None, 4, 9000, 9000, 9000, _lib.SA_BF16, 2, ctypes.byref(info)) == -2
+    assert lib.sa_norm_fwd_launch_info(None, None, 4, 64, 32, 64, _lib.SA_BF16, 2, ctypes.byref(info)) == -5
+    assert lib.sa_norm_fwd_launch_info(None, None, 4, 64, 64, 64, 7, 2, ctypes.byref(info)) == -3
+    assert lib.sa_norm_fwd_launch_info(None, None, 4, 64, 64, 64, _lib.SA_BF16, 4, ctypes.byref(info)) == -4
+    assert lib.sa_softmax_fwd_launch_info(None, None, 4, 64, 64, 64, _lib.SA_F32, None) == -1
+    assert lib.sa_softmax_fwd_launch_info(None, None, 4, 64, 64, 64, 7, ctypes.byref(info)) == -3

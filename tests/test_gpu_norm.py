@@ -178,3 +178,34 @@ def test_full_size_config2_properties(L):
     for b, h in [(0, 0), (3, 15)]:
         ref = eager.softplus_norm_backward(x[b, h].cpu().double(), dy[b, h].cpu().double(), causal=True)
         assert rel_err(dx[b, h, rows], ref[rows]) <= 1e-2
+
+
+@pytest.mark.parametrize("dtype,L,kernel,waves", [
+    (torch.bfloat16, 4096, "split", 4),   # 8 chunks of 512 -> 4 waves per row
+    (torch.bfloat16, 1024, "vec", 1),
+    (torch.bfloat16, 100, "scalar", 1),   # 100 % 8 != 0: element loads
+    (torch.float32, 2048, "split", 4),
+])
+def test_launch_meta_describes_the_kernel(dtype, L, kernel, waves):
+    # return_meta carries the reference's keys (kernels.py:310-317, :423-427),
+    # filled from the launch this call made and the compiled kernel
+    B, H = 1, 2
+    x = _randn((B, H, L, L), dtype, seed=L + 5).to(DEV)
+    y, meta = smooth_attn.softplus_norm_causal_triton(x, return_meta=True)
+    for key in ["variant", "block_size", "num_warps", "num_stages", "num_programs", "occupancy", "n_regs",
+                "shared_mem", "time_us"]:
+        assert key in meta
+    assert meta["variant"] == "squareplus_winner"
+    assert meta["kernel"] == kernel and meta["waves_per_row"] == waves
+    rows = B * H * L
+    assert meta["num_programs"] == -(-rows // meta["rows_per_program"])
+    assert meta["num_warps"] * 64 >= 64 * waves
+    assert meta["block_size"] >= (L if kernel != "scalar" else 64)
+    assert 0 < meta["n_regs"] <= 512 and meta["occupancy"] >= 1
+    assert (meta["shared_mem"] > 0) == (kernel == "split")  # split rows combine partial sums in LDS
+    assert meta["time_us"] > 0
+    # cached per shape: the same dict values on a second call
+    _, meta2 = smooth_attn.softplus_norm_causal_triton(x, return_meta=True)
+    assert meta2 == meta
+    ref = eager.softplus_norm_causal_eager(x[:1, :1].cpu().double())
+    assert rel_err(y[:1, :1], ref) <= REL_TOL[dtype]
