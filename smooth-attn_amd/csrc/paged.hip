@@ -375,6 +375,11 @@ extern "C" int sa_paged_decode(const void* q, const void* k_cache, const void* v
     if (D != 32 && D != 64 && D != 128) return SA_ERR_UNSUPPORTED;
     if (B == 0) return 0;
     if (n_pages == 0) max_pages = 0;  // no cache: every context is empty
+    // The plan keeps token positions, tile counts and their prefix sums over
+    // (sequence, KV head) in 32-bit ints.
+    const int64_t max_ctx = static_cast<int64_t>(max_pages) * page_size;
+    if (max_ctx > INT32_MAX / 2 || static_cast<int64_t>(B) * Hkv * ((max_ctx + kTile - 1) / kTile) > INT32_MAX / 2)
+        return SA_ERR_UNSUPPORTED;
     if (!q || !k_cache || !v_cache || !out || !block_table || !context_lens || !q_strides || !kv_strides ||
         !vv_strides || !o_strides || !workspace)
         return SA_ERR_NULL_POINTER;

@@ -62,3 +62,16 @@ def test_launch_info_argument_errors():
     assert lib.sa_norm_fwd_launch_info(None, None, 4, 64, 64, 64, _lib.SA_BF16, 4, ctypes.byref(info)) == -4
     assert lib.sa_softmax_fwd_launch_info(None, None, 4, 64, 64, 64, _lib.SA_F32, None) == -1
     assert lib.sa_softmax_fwd_launch_info(None, None, 4, 64, 64, 64, 7, ctypes.byref(info)) == -3
+
+
+def test_paged_decode_rejects_plans_past_int32():
+    # B * Hkv * ceil(max context / 32) tiles must fit the plan's 32-bit
+    # prefix sums; rejected before any HIP call, so this runs without a GPU
+    lib = _lib.load()
+    strides = (ctypes.c_int64 * 4)(128 * 32, 128, 128, 1)
+    kv = (ctypes.c_int64 * 4)(8 * 16 * 128, 16 * 128, 128, 1)
+    o = (ctypes.c_int64 * 3)(32 * 128, 128, 1)
+    dummy = ctypes.c_void_p(16)
+    st = lib.sa_paged_decode(dummy, dummy, dummy, dummy, dummy, dummy, 4096, 32, 8, 128, 16, 1 << 20, 1 << 20,
+                             strides, kv, kv, o, 1 << 20, 0.1, _lib.SA_BF16, dummy, 1 << 62, None)
+    assert st == -6  # SA_ERR_UNSUPPORTED
