@@ -145,14 +145,25 @@ __device__ __forceinline__ int swz_src_off(int i, int wave, int lane, int rsb) {
 
 // Issue the DMA loads of one [64][D] tile whose first row is at `base`
 // (wave-uniform; row stride rsb bytes) into the swizzled LDS tile at `dst`;
-// rows at or past `nrows` read as zeros.  off[i]: swz_src_off(i, ...).
+// rows at or past `nrows` read as zeros.  lane_off: swz_src_off(0, ...).
+// Load i covers rows 256/CPR further down than load i - 1 with the same
+// swizzle (f depends on row bits that i does not change), so
+// swz_src_off(i) = i * (256 / CPR) * rsb + swz_src_off(0): each load gets a
+// scalar resource starting i * (256 / CPR) rows in (with the byte count
+// shortened to match, so the zero fill past nrows is unchanged) and one
+// per-lane offset serves them all.
 template <int D>
 __device__ __forceinline__ void issue_swz_tile(const unsigned char* base, int rsb, int nrows, unsigned char* dst,
-                                               int wave, const int (&off)[SwzTile<D>::NI]) {
+                                               int wave, int lane_off) {
     using Tl = SwzTile<D>;
-    const __amdgpu_buffer_rsrc_t rs = bwd_rsrc(base, nrows * rsb);
+    constexpr int kRowsPerLoad = 256 / Tl::CPR;
+    const int nbytes = nrows * rsb;
 #pragma unroll
-    for (int i = 0; i < Tl::NI; ++i) dma16(rs, off[i], dst + (i * 4 + wave) * 64 * 16);
+    for (int i = 0; i < Tl::NI; ++i) {
+        const int skip = i * kRowsPerLoad * rsb;
+        const __amdgpu_buffer_rsrc_t rs = bwd_rsrc(base + skip, max(nbytes - skip, 0));
+        dma16(rs, lane_off, dst + (i * 4 + wave) * 64 * 16);
+    }
 }
 
 template <bool EXACT>
@@ -240,12 +251,7 @@ __global__ __launch_bounds__(kBwdThreads, 2) void flash_bwd_dq_kernel(BwdParams 
     const float sc = p.scale;
 
     const int ksb = static_cast<int>(p.ks[2] * 2), vsb = static_cast<int>(p.vs[2] * 2);  // row strides (bytes)
-    int koff[Tl::NI], voff[Tl::NI];
-#pragma unroll
-    for (int i = 0; i < Tl::NI; ++i) {
-        koff[i] = swz_src_off<D>(i, wave, lane, ksb);
-        voff[i] = swz_src_off<D>(i, wave, lane, vsb);
-    }
+    const int koff = swz_src_off<D>(0, wave, lane, ksb), voff = swz_src_off<D>(0, wave, lane, vsb);
     // Keys past T read as zeros; they only meet masked weights (or rows
     // past T, whose dQ is not written).
     auto issue_tile = [&](int j, int buf) {
@@ -418,6 +424,7 @@ __global__ __launch_bounds__(kBwdThreads, SA_BWD_DKDV_MINB) void flash_bwd_dkdv_
     const float sc = p.scale;
 
     const int qsb = static_cast<int>(p.qs[2] * 2), dsb = static_cast<int>(p.dos[2] * 2);  // row strides (bytes)
+    const int qoff = swz_src_off<D>(0, wave, lane, qsb), dooff = swz_src_off<D>(0, wave, lane, dsb);
     float rst = 0.f;
     // Queries past T read as zeros; their weights are masked.
     auto issue_tile = [&](int it, int buf) {
@@ -430,14 +437,9 @@ __global__ __launch_bounds__(kBwdThreads, SA_BWD_DKDV_MINB) void flash_bwd_dkdv_
             reinterpret_cast<const unsigned char*>(static_cast<const T*>(p.dout) + b * p.dos[0] + hq * p.dos[1]));
         const int q0 = qt * kBwdQT;
         const int nrows = min(T_ - q0, kBwdQT);
-        int off[Tl::NI];
-#pragma unroll
-        for (int i = 0; i < Tl::NI; ++i) off[i] = swz_src_off<D>(i, wave, lane, qsb);
-        issue_swz_tile<D>(qp + static_cast<int64_t>(q0) * qsb, qsb, nrows, lds + (2 * buf) * Tl::BYTES, wave, off);
-#pragma unroll
-        for (int i = 0; i < Tl::NI; ++i) off[i] = swz_src_off<D>(i, wave, lane, dsb);
+        issue_swz_tile<D>(qp + static_cast<int64_t>(q0) * qsb, qsb, nrows, lds + (2 * buf) * Tl::BYTES, wave, qoff);
         issue_swz_tile<D>(dop + static_cast<int64_t>(q0) * dsb, dsb, nrows, lds + (2 * buf + 1) * Tl::BYTES, wave,
-                          off);
+                          dooff);
         if (tid < 2 * kBwdQT) {
             const int r = tid & (kBwdQT - 1);
             const int64_t idx = (static_cast<int64_t>(b) * p.Hq + hq) * T_ + min(q0 + r, T_ - 1);
