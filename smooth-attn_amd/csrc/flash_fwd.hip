@@ -332,40 +332,49 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashParams p) {
     // Slot s of a tile is written by wave (s / 64) % kWaves, instruction
     // s / kThreads.
     u32x4 vst[V8 ? Gm::VNL : 1];
-    // Per-lane byte offsets of the DMA loads inside a tile, fixed for the
-    // whole walk: each load is a per-tile scalar resource (the tile's first
-    // row, sized to the rows before T, so rows past T read as zeros: they
-    // only meet masked weights) plus this offset.
-    int koff[Gm::KNI], voff[Gm::VNI];
-#pragma unroll
-    for (int i = 0; i < Gm::KNI; ++i) {
-        const int sl = (i * kWaves + wave) * 64 + lane;
-        const int row = min(sl / Gm::KCPR, kBKV - 1);
-        koff[i] = row * static_cast<int>(krs) + ((sl - row * Gm::KCPR) ^ Gm::swz_k(row)) * 16;
-    }
-#pragma unroll
-    for (int i = 0; i < Gm::VNI; ++i) {
-        const int sl = (i * kWaves + wave) * 64 + lane;
-        const int row = min(sl / Gm::VCPRL, kBKV - 1);
-        voff[i] = row * static_cast<int>(vrs) + ((sl - row * Gm::VCPRL) ^ Gm::swz_v(row)) * 16;
+    // Per-lane byte offset of the DMA loads inside a tile, fixed for the
+    // whole walk.  Load i of a tile covers kKRows (kVRows) rows further down
+    // than load i - 1 with the same chunk swizzle (where a lane has several
+    // loads, the swizzle reads only row bits that i does not change), so
+    // one offset serves every load; load i gets its own scalar resource
+    // starting i * kKRows rows into the tile, sized to the rows before T, so
+    // rows past T read as zeros (they only meet masked weights).
+    constexpr int kKRows = kThreads / Gm::KCPR, kVRows = kThreads / Gm::VCPRL;
+    static_assert(Gm::KNI == 1 || (kThreads % Gm::KCPR == 0 && (kKRows / Gm::KRPW) % Gm::KCPR == 0),
+                  "K loads of a lane must share one swizzled offset");
+    static_assert(V8 || Gm::VNI == 1 || (kThreads % Gm::VCPRL == 0 && (kVRows / Gm::VRPW) % (Gm::VCPRL / 4) == 0),
+                  "V loads of a lane must share one swizzled offset");
+    int koff, voff;
+    {
+        const int sl = wave * 64 + lane;
+        const int krow = min(sl / Gm::KCPR, kBKV - 1);
+        koff = krow * static_cast<int>(krs) + ((sl - krow * Gm::KCPR) ^ Gm::swz_k(krow)) * 16;
+        const int vrow = min(sl / Gm::VCPRL, kBKV - 1);
+        voff = vrow * static_cast<int>(vrs) + ((sl - vrow * Gm::VCPRL) ^ Gm::swz_v(vrow)) * 16;
     }
     auto issue_tile = [&](int j, int buf) {
         const int k0 = j * kBKV;
         const int nrows = min(T_ - k0, kBKV);  // rows of this tile before T
-        const __amdgpu_buffer_rsrc_t krs_ = tile_rsrc(kp + static_cast<int64_t>(k0) * krs, nrows * static_cast<int>(krs));
+        const int kbytes = nrows * static_cast<int>(krs);
 #pragma unroll
         for (int i = 0; i < Gm::KNI; ++i) {
             const int sbase = (i * kWaves + wave) * 64;
-            if ((kBKV * Gm::KCPR) % kThreads == 0 || sbase < kBKV * Gm::KCPR)
-                dma16(krs_, koff[i], ldsK + buf * Gm::KT + sbase * 16);
+            if ((kBKV * Gm::KCPR) % kThreads == 0 || sbase < kBKV * Gm::KCPR) {
+                const int skip = i * kKRows * static_cast<int>(krs);
+                dma16(tile_rsrc(kp + static_cast<int64_t>(k0) * krs + skip, max(kbytes - skip, 0)), koff,
+                      ldsK + buf * Gm::KT + sbase * 16);
+            }
         }
         if constexpr (!V8) {
-            const __amdgpu_buffer_rsrc_t vrs_ = tile_rsrc(vp + static_cast<int64_t>(k0) * vrs, nrows * static_cast<int>(vrs));
+            const int vbytes = nrows * static_cast<int>(vrs);
 #pragma unroll
             for (int i = 0; i < Gm::VNI; ++i) {
                 const int sbase = (i * kWaves + wave) * 64;
-                if ((kBKV * Gm::VCPRL) % kThreads == 0 || sbase < kBKV * Gm::VCPRL)
-                    dma16(vrs_, voff[i], ldsVb + buf * Gm::VT + sbase * 16);
+                if ((kBKV * Gm::VCPRL) % kThreads == 0 || sbase < kBKV * Gm::VCPRL) {
+                    const int skip = i * kVRows * static_cast<int>(vrs);
+                    dma16(tile_rsrc(vp + static_cast<int64_t>(k0) * vrs + skip, max(vbytes - skip, 0)), voff,
+                          ldsVb + buf * Gm::VT + sbase * 16);
+                }
             }
         } else {
 #pragma unroll
