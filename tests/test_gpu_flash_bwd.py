@@ -143,3 +143,18 @@ def test_full_size_config3_sampled():
     refs = eager.flash_attention_bwd(*(t[sl].cpu().double() for t in (q, k, v, o, do)))
     for got, ref in zip((dq, dk, dv), refs):
         assert rel_err(got[sl], ref) <= TOL
+
+
+@pytest.mark.parametrize("scale", [0.02, 0.3, 1.7, 2.0 ** -21, -0.05])
+def test_backward_scales(scale):
+    # scales other than 1/sqrt(D), including tiny and negative ones:
+    # gradients must match the oracle
+    q, k, v, do = inputs(1, 4, 2, 150, 64, torch.bfloat16, seed=int(abs(scale) * 1000) + 21)
+    qd, kd, vd, dod = (t.to(DEV) for t in (q, k, v, do))
+    o, rs = kernels._sp2norm_flash_fwd(qd, kd, vd, scale, 2, 0)
+    grads = kernels._sp2norm_flash_bwd(qd, kd, vd, o, dod, rs, scale, 2, 0)
+    refs = eager.flash_attention_bwd(q.double(), k.double(), v.double(), o.cpu().double(), do.double(),
+                                     scale=scale)
+    for name, got, ref in zip(("dq", "dk", "dv"), grads, refs):
+        assert bool(torch.isfinite(got).all()), name
+        assert rel_err(got, ref) <= TOL, f"{name}: rel err {rel_err(got, ref):.3e}"
