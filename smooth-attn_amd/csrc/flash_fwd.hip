@@ -121,9 +121,10 @@ __device__ __forceinline__ const unsigned char* uniform_ptr(const unsigned char*
 // s_waitcnt vmcnt(0): this wave's direct-to-LDS loads have landed.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-__device__ __forceinline__ f32x16 mma_fp8(i32x8 a, i32x8 b, f32x16 c) {
-    // e4m3 x e4m3, unit block scales (E8M0 127 = 2^0)
-    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+// e4m3 x e4m3 with block scales 2^(ea-127) and 2^(eb-127) (E8M0; 127 =
+// 2^0): D = 2^(ea+eb-254) sum a b + C, the power of two applied exactly.
+__device__ __forceinline__ f32x16 mma_fp8(i32x8 a, i32x8 b, f32x16 c, int ea, int eb) {
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, ea, 0, eb);
 }
 
 // Widen 16 e4m3fn values (one 16-byte word) to 16 bf16 / f16 values (two words).
@@ -445,12 +446,34 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashParams p) {
     struct STiles {
         f32x16 v[kQT];
     };
-    // FOLD: every S^T chain starts from c0 = -1/(2 sc) instead of 0, so the
-    // accumulator holds s' = s - 1/(2 sc) and a = sc s'.  Then
-    // (a + sqrt(a^2 + 1))^2 = sc^2 (s' + sqrt(s'^2 + 1/sc^2))^2: the weights
-    // are computed scaled by 1/sc^2 (one FMA per score fewer), which cancels
-    // between P V and the row sum (rescaled at the end).
-    const float c0 = -0.5f / sc, c2 = 1.f / (sc * sc);
+    // FOLD: every S^T chain starts from c0 = -1/(2 fs) instead of 0, so the
+    // accumulator holds s' = s - 1/(2 fs) and a = fs s'.  Then
+    // (a + sqrt(a^2 + 1))^2 = fs^2 (s' + sqrt(s'^2 + 1/fs^2))^2: the weights
+    // are computed scaled by 1/fs^2 (one FMA per score fewer), which cancels
+    // between P V and the row sum (rescaled at the end).  16-bit Q/K: fs = sc
+    // (the host folds only moderate positive scales).  fp8 Q/K: the MFMA
+    // block scales apply 2^k of sc = fs 2^k exactly (k split over the two
+    // E8M0 exponents, each within +-127), leaving fs in [1, 2) for any
+    // positive sc.
+    float fs = sc;
+    int e8a = 127, e8b = 127;
+    if constexpr (QK8 && FOLD) {
+        if (sc > 0.f) {
+            int e;
+            fs = 2.f * frexpf(sc, &e);  // sc = fs 2^(e-1)
+            const int k = e - 1;
+            const int ka = max(-127, min(127, k));
+            e8a = 127 + ka;
+            e8b = 127 + (k - ka);
+        } else {
+            // q_scale k_scale scale underflowed to 0: scores 2^-254 s (zero
+            // for every e4m3 product), a = -1/2, as sc s - 1/2 gives
+            fs = 1.f;
+            e8a = 0;
+            e8b = 0;
+        }
+    }
+    const float c0 = -0.5f / fs, c2 = 1.f / (fs * fs);
     f32x16 sinit;
 #pragma unroll
     for (int v = 0; v < 16; ++v) sinit[v] = FOLD ? c0 : 0.f;
@@ -466,7 +489,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashParams p) {
                     const i32x8 bv{(int)qreg[qt][dc][0].x, (int)qreg[qt][dc][0].y, (int)qreg[qt][dc][0].z,
                                    (int)qreg[qt][dc][0].w, (int)qreg[qt][dc][1].x, (int)qreg[qt][dc][1].y,
                                    (int)qreg[qt][dc][1].z, (int)qreg[qt][dc][1].w};
-                    s.v[qt] = mma_fp8(kf[dc], bv, s.v[qt]);
+                    s.v[qt] = mma_fp8(kf[dc], bv, s.v[qt], e8a, e8b);
                 } else {
                     s.v[qt] = Ops::mma(kf[dc], as_vec8<Vec>(qreg[qt][dc][0]), s.v[qt]);
                 }
@@ -615,9 +638,9 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashParams p) {
         // Row sums: lanes l and l^32 hold the two key halves of one query column.
         const float part = (ssum[qt][0] + ssum[qt][1]) + (ssum[qt][2] + ssum[qt][3]);
         const float both = part + __shfl_xor(part, 32);
-        // FOLD: the sums and P V carry the factor 1/sc^2
-        const float stot = FOLD ? __builtin_fmaf(both, sc * sc, kEps) : both + kEps;
-        const float inv = FOLD ? vsc * (sc * sc) / stot : vsc / stot;
+        // FOLD: the sums and P V carry the factor 1/fs^2
+        const float stot = FOLD ? __builtin_fmaf(both, fs * fs, kEps) : both + kEps;
+        const float inv = FOLD ? vsc * (fs * fs) / stot : vsc / stot;
         const int qi = wq0[qt] + l32;
         if (qi < T_) {
             T* orow = op + qi * p.os[2];
@@ -644,9 +667,15 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashParams p) {
 // D = 128 only: the 16 registers holding the chains' start value cost the
 // D = 32 and 64 kernels a wave per SIMD (config 3, D = 128: 767 -> 752 us).
 template <typename T, bool QK8, int D>
-constexpr bool kCanFold = std::is_same_v<T, bf16> && !QK8 && D == 128;
+constexpr bool kCanFold = std::is_same_v<T, bf16> && D == 128;
 
-bool fold_scale_ok(float scale) { return scale >= 0x1p-20f && scale <= 0x1p20f; }
+// 16-bit Q/K fold relative to the scale itself; fp8 Q/K fold relative to
+// its mantissa (any positive scale: q_scale and k_scale are positive).
+template <bool QK8>
+bool fold_scale_ok(float scale) {
+    if constexpr (QK8) return scale > 0.f && scale <= 3.0e38f;
+    return scale >= 0x1p-20f && scale <= 0x1p20f;
+}
 
 template <typename T, int D, bool QK8, bool V8>
 int launch_flash(const FlashParams& prm, int exact, hipStream_t st) {
@@ -657,7 +686,7 @@ int launch_flash(const FlashParams& prm, int exact, hipStream_t st) {
         return status_from_launch();
     }
     if constexpr (kCanFold<T, QK8, D>) {
-        if (fold_scale_ok(prm.scale)) {
+        if (fold_scale_ok<QK8>(prm.scale)) {
             flash_fwd_kernel<T, D, QK8, V8, false, false, true><<<grid, block, 0, st>>>(prm);
             return status_from_launch();
         }
@@ -683,7 +712,7 @@ int launch_rope(FlashParams prm, T* k_rot, hipStream_t st) {
     prm.ks[3] = 1;
     const dim3 grid(static_cast<unsigned>(prm.nqb) * prm.B * prm.Hq);
     if constexpr (kCanFold<T, false, D>) {
-        if (fold_scale_ok(prm.scale)) {
+        if (fold_scale_ok<false>(prm.scale)) {
             flash_fwd_kernel<T, D, false, false, false, true, true><<<grid, dim3(kThreads), 0, st>>>(prm);
             return status_from_launch();
         }

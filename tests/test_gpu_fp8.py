@@ -167,3 +167,34 @@ def test_fp8_config4_sampled():
         ref = eager.fp8_flash_attention_eager(q8[b:b + 1, h:h + 1].cpu(), k8[b:b + 1, hk:hk + 1].cpu(),
                                               v[b:b + 1, hk:hk + 1].cpu(), qs.cpu(), ks.cpu(), 1.0, 1 / math.sqrt(D))
         assert rel_err(o[b:b + 1, h:h + 1], ref) <= 1e-2
+
+
+@pytest.mark.parametrize("qmag,kmag,attn_scale", [
+    (1e-8, 1e-8, None),     # score scale ~2^-70: folded through the MFMA block exponents
+    (1e6, 1e5, None),       # ~2^+19 (scores ~1e12: far larger ones overflow y = (2a)^2 in fp32 either way)
+    (1.0, 1.0, -0.05),      # negative scale: plain form
+    (1e-6, 1e-6, 1e-30),    # q_scale k_scale scale underflows to 0 in fp32: all scores 0
+])
+@pytest.mark.parametrize("v_fp8", [True, False])
+def test_fp8_forward_score_scale_range(qmag, kmag, attn_scale, v_fp8):
+    q, k, v = _fp8_case(1, 4, 2, 160, 128, seed=int(abs(math.log10(qmag))) + 7)
+    q = (q.float() * qmag).to(torch.bfloat16)
+    k = (k.float() * kmag).to(torch.bfloat16)
+    q8, qs = eager.quantize_to_fp8(q)
+    k8, ks = eager.quantize_to_fp8(k)
+    if v_fp8:
+        vv, vs = eager.quantize_to_fp8(v)
+    else:
+        vv, vs = v, torch.tensor(1.0)
+    scale = attn_scale if attn_scale is not None else 1 / math.sqrt(128)
+    o, rs = kernels._sp2norm_fp8_flash_fwd(q8.to(DEV), k8.to(DEV), vv.to(DEV), float(qs), float(ks),
+                                           float(vs) if v_fp8 else None, scale, 2)
+    sc32 = torch.tensor(scale, dtype=torch.float32) * qs.float() * ks.float()  # the kernel's fp32 product
+    ref, ref_rs = eager.fp8_flash_attention_eager(q8, k8, vv, qs, ks, vs, scale, return_row_sums=True)
+    if float(sc32) == 0.0:
+        # the reference's fp32 product underflows the same way: every score
+        # is 0, so each row averages its visible values
+        ref, ref_rs = eager.fp8_flash_attention_eager(q8, k8, vv, qs, ks, vs, 0.0, return_row_sums=True)
+    assert bool(torch.isfinite(o).all())
+    assert rel_err(o, ref) <= 1e-2
+    assert rel_err(rs, ref_rs) <= 1e-4
