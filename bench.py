@@ -277,10 +277,13 @@ def bench_next_rows(torch, iters):
     out = {}
 
     def avg_us(fn, n):
-        for _ in range(2):
+        # median of per-call event times after a few warmup calls (first
+        # calls grow torch's allocator pools and pick library GEMM kernels),
+        # as the reference's _median_cuda_us (kernels.py:322-336)
+        for _ in range(5):
             fn()
-        ms = time_events(torch, fn, n)
-        return sum(ms) / len(ms) * 1e3
+        ms = sorted(time_events(torch, fn, n))
+        return ms[len(ms) // 2] * 1e3
 
     B, H, L, D = 4, 32, 4096, 128
     q, k, v = (torch.randn(B, H, L, D, generator=gen, device=dev).to(torch.bfloat16) for _ in range(3))

@@ -97,6 +97,18 @@ int sa_softmax_fwd(const void* x, void* y, int64_t n_rows, int64_t n_cols,
                    int64_t x_row_stride, int64_t y_row_stride, int dtype,
                    int causal, sa_stream_t stream);
 
+/*
+ * dst[c][r] = src[r][c] for a rows x cols matrix of 16-bit elements (bf16
+ * or fp16; element row strides, multiples of 8, both pointers 16-byte
+ * aligned).  Lays out the RoPE projection's W_o as [D_model, Hq*D] so the
+ * projection runs as the faster GEMM form O (W_o^T)^T.  No counterpart in
+ * the reference, whose projection kernel reads W_o per head
+ * (kernels.py:2373-2426).
+ */
+int sa_transpose16(const void* src, void* dst, int64_t rows, int64_t cols,
+                   int64_t src_row_stride, int64_t dst_row_stride,
+                   sa_stream_t stream);
+
 /* Row kernel variants (sa_launch_info.variant). */
 enum {
     SA_ROW_SCALAR = 0, /* element loads (unaligned rows or n_cols % vec != 0) */

@@ -40,6 +40,7 @@ SIGNATURES = {
     "sa_norm_bwd": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64,
                             c_int, c_int, c_int, c_float, c_float, c_int, c_void_p]),
     "sa_softmax_fwd": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int, c_int, c_void_p]),
+    "sa_transpose16": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p]),
     "sa_norm_fwd_launch_info": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int, c_int,
                                         POINTER(LaunchInfo)]),
     "sa_softmax_fwd_launch_info": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int,

@@ -696,7 +696,25 @@ def sp2norm_rope_flash_attention_proj(q, k, v, w_o, cos, sin, *, scale=None, win
     o_bthd = torch.empty(B, T, H_q, D, device=q.device, dtype=q.dtype)
     _sp2norm_rope_flash_fwd(q, k, v, cos, sin, scale, H_q // H_kv, window_size, o=o_bthd.transpose(1, 2))
     w = w_o.to(q.dtype).reshape(H_q * D, D_model)
-    return torch.matmul(o_bthd.view(B * T, H_q * D), w).view(B, T, D_model)
+    # W_o^T contiguous: the GEMM then takes its faster layout (F.linear form)
+    w_t = _transpose16(w)
+    return F.linear(o_bthd.view(B * T, H_q * D), w_t).view(B, T, D_model)
+
+
+def _transpose16(x):
+    """Contiguous transpose of a 2-D bf16/fp16 CUDA matrix by sa_transpose16."""
+    assert x.ndim == 2 and x.dtype in (torch.bfloat16, torch.float16)
+    if x.stride(1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
+        x = x.contiguous()
+    rows, cols = x.shape
+    out = torch.empty(cols, rows, device=x.device, dtype=x.dtype)
+    if out.stride(0) % 8:  # rows not a multiple of 8: fall back to a torch copy of the view
+        return x.t().contiguous()
+    lib = _lib.load()
+    with torch.cuda.device(x.device):
+        st = lib.sa_transpose16(x.data_ptr(), out.data_ptr(), rows, cols, x.stride(0), out.stride(0), _stream(x))
+    _lib.check(st, "sa_transpose16")
+    return out
 
 
 # ---------------------------------------------------------------------------

@@ -75,3 +75,14 @@ def test_paged_decode_rejects_plans_past_int32():
     st = lib.sa_paged_decode(dummy, dummy, dummy, dummy, dummy, dummy, 4096, 32, 8, 128, 16, 1 << 20, 1 << 20,
                              strides, kv, kv, o, 1 << 20, 0.1, _lib.SA_BF16, dummy, 1 << 62, None)
     assert st == -6  # SA_ERR_UNSUPPORTED
+
+
+def test_transpose16_argument_errors():
+    lib = _lib.load()
+    d = ctypes.c_void_p(16)
+    assert lib.sa_transpose16(None, d, 8, 8, 8, 8, None) == -1
+    assert lib.sa_transpose16(d, d, -1, 8, 8, 8, None) == -2
+    assert lib.sa_transpose16(d, d, 8, 16, 8, 8, None) == -5   # source stride below cols
+    assert lib.sa_transpose16(d, d, 8, 8, 12, 8, None) == -5   # stride not a multiple of 8
+    assert lib.sa_transpose16(ctypes.c_void_p(18), d, 8, 8, 8, 8, None) == -5  # unaligned
+    assert lib.sa_transpose16(d, d, 0, 8, 8, 8, None) == 0

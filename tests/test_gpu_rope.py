@@ -115,3 +115,18 @@ def test_rope_proj_matches_oracle(B, H, Hkv, T, D, M, window):
     out2 = smooth_attn.sp2norm_rope_flash_attention_proj(q.to(DEV), k.to(DEV), v.to(DEV), w_o.to(DEV), cos, sin,
                                                          window_size=window)
     assert torch.equal(out, out2)
+
+
+@pytest.mark.parametrize("rows,cols", [(4096, 4096), (64, 128), (72, 200), (8, 8), (1000, 16), (136, 4104)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_transpose16_bit_exact(rows, cols, dtype):
+    # the projection's weight transpose: full 64x64 tiles and ragged edges
+    g = torch.Generator().manual_seed(rows * 7 + cols)
+    x = torch.randn(rows, cols, generator=g).to(dtype).to(DEV)
+    y = kernels._transpose16(x)
+    assert y.shape == (cols, rows) and y.is_contiguous()
+    assert torch.equal(y.cpu(), x.cpu().t())
+    # a strided source (a column slice of a wider matrix)
+    wide = torch.randn(rows, cols + 16, generator=g).to(dtype).to(DEV)
+    ys = kernels._transpose16(wide[:, 8:8 + cols])
+    assert torch.equal(ys.cpu(), wide[:, 8:8 + cols].cpu().t())
