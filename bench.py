@@ -3,7 +3,7 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
 
 A step is one forward + backward pass of the causal squareplus
-normalisation over BASELINE config 2 at L=4096 (x = randn/sqrt(128) and
+normalisation over config 2 at L=4096 (x = randn/sqrt(128) and
 dy = randn, bf16 [4,16,4096,4096], family alpha=2, theta=0.5, p=2), run
 through the public autograd API.  ``value`` is algorithmic HBM bytes per
 step / step time.  Algorithmic bytes: the forward reads the causal triangle

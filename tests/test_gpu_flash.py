@@ -129,7 +129,7 @@ def test_identical_values_and_single_key_rows():
 
 
 def test_full_size_config3_sampled():
-    """BASELINE config 3 at full size [4,32,4096,128] bf16: whole-output
+    """config 3 at full size [4,32,4096,128] bf16: whole-output
     properties, oracle parity on two sampled heads."""
     B, H, T, D = 4, 32, 4096, 128
     gen = torch.Generator(device=DEV).manual_seed(3)

@@ -128,7 +128,7 @@ def test_backward_strided_rows():
 
 
 def test_full_size_config3_sampled():
-    """BASELINE config 3 at full size [4,32,4096,128] bf16: finite gradients
+    """config 3 at full size [4,32,4096,128] bf16: finite gradients
     everywhere, oracle parity on one sampled head."""
     B, H, T, D = 4, 32, 4096, 128
     gen = torch.Generator(device=DEV).manual_seed(3)

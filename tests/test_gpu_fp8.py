@@ -145,13 +145,13 @@ def test_fp8_entry_point_gqa_window_bounds():
     out = smooth_attn.sp2norm_fp8_flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), window_size=64)
     ref = eager.flash_attention_eager(q.double(), k.double(), v.double(), window_size=64)
     assert float((out.double().cpu() - ref).abs().max()) < 0.3
-    # bf16 V variant (BASELINE config 4 keeps V in bf16)
+    # bf16 V variant (config 4 keeps V in bf16)
     out2 = smooth_attn.sp2norm_fp8_flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), window_size=64, quantize_v=False)
     assert float((out2.double().cpu() - ref).abs().max()) < 0.3
 
 
 def test_fp8_config4_sampled():
-    """BASELINE config 4 at full size: Q [2,32,8192,128], K/V [2,8,8192,128],
+    """config 4 at full size: Q [2,32,8192,128], K/V [2,8,8192,128],
     Q/K e4m3fn, V bf16; sampled heads against the oracle on the same codes."""
     B, Hq, Hkv, T, D = 2, 32, 8, 8192, 128
     gen = torch.Generator(device=DEV).manual_seed(4)

@@ -1,6 +1,6 @@
 """Parity of the HIP normalisation kernels with the CPU oracle (GPU).
 
-Tolerances: relative error max|HIP - oracle| /
+Tolerances (the path's stated bars): relative error max|HIP - oracle| /
 max|oracle| <= 1e-2 for bf16/fp16 outputs and <= 1e-5 for fp32 outputs,
 against the float64 oracle on the same seeded inputs; causal zeros exact.
 The reference's own test tolerances (tests/test_training_api.py:36-78: atol
@@ -158,7 +158,7 @@ def test_empty_and_limits():
 
 @pytest.mark.parametrize("L", [2048, 4096])
 def test_full_size_config2_properties(L):
-    """BASELINE config 2 at full size [4,16,L,L]: size-independent properties
+    """config 2 at full size [4,16,L,L]: size-independent properties
     on the whole output, oracle parity on sampled rows."""
     B, H = 4, 16
     gen = torch.Generator(device=DEV).manual_seed(L)

@@ -152,7 +152,7 @@ def test_paged_long_context():
 
 
 def test_paged_config5():
-    """64 sequences, ctx ~ U[512, 16384], Hq 32 / Hkv 8,
+    """config 5: 64 sequences, ctx ~ U[512, 16384], Hq 32 / Hkv 8,
     D 128, page 16, block table a seeded permutation of all pages."""
     g = _g(5)
     B, Hq, Hkv, D, P = 64, 32, 8, 128, 16
