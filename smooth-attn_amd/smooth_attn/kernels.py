@@ -173,7 +173,8 @@ def _row_launch_meta(variant, kind, x2d, y2d, rerun, power=2):
     the same call, measured on the first request per shape and cached, as the
     reference's autotuner measures its candidates on first use."""
     n_rows, n_cols = x2d.shape
-    key = (kind, power, x2d.dtype, n_rows, n_cols, x2d.stride(0), y2d.stride(0),
+    # the variant names the mode (row-wise or causal): same launch, other time
+    key = (variant, kind, power, x2d.dtype, n_rows, n_cols, x2d.stride(0), y2d.stride(0),
            x2d.data_ptr() % 16 == 0 and y2d.data_ptr() % 16 == 0, x2d.device.index)
     meta = _LAUNCH_META_CACHE.get(key)
     if meta is None:
@@ -815,6 +816,22 @@ def sp2norm_fp8_flash_attention(q, k, v, *, scale=None, window_size=0, quantize_
 # ---------------------------------------------------------------------------
 # Paged decode.
 # ---------------------------------------------------------------------------
+def _check_paging_args(B, D, k_cache, v_cache, block_table, context_lens):
+    """The kernels read B block-table rows and B context lengths, and cache
+    rows of D elements: reject shorter arrays here rather than read past them
+    on the device (the reference does not check these)."""
+    if k_cache.ndim != 4 or v_cache.shape != k_cache.shape or k_cache.shape[3] != D:
+        raise ValueError(f"k/v caches must both be [n_pages, H_kv, block_size, {D}], got "
+                         f"{tuple(k_cache.shape)} / {tuple(v_cache.shape)}")
+    if block_table.ndim != 2 or block_table.shape[0] < B:
+        raise ValueError(f"block_table must be [B={B}, max_pages], got {tuple(block_table.shape)}")
+    if context_lens.numel() < B:
+        raise ValueError(f"context_lens must hold B={B} lengths, got {context_lens.numel()}")
+    for t in (block_table, context_lens):
+        if t.dtype.is_floating_point or t.dtype.is_complex or t.device != k_cache.device:
+            raise ValueError("block_table and context_lens must be integer tensors on the caches' device")
+
+
 def sp2norm_paged_attention(q, k_cache, v_cache, block_table, context_lens, *, scale=None, block_size=16):
     """Paged single-token decode — kernels.py:2776-2829 (output bf16 [B, Hq, D])."""
     assert q.ndim == 4 and q.shape[2] == 1, "Decode: q must be [B, H, 1, D]"
@@ -827,6 +844,7 @@ def sp2norm_paged_attention(q, k_cache, v_cache, block_table, context_lens, *, s
         scale = 1.0 / math.sqrt(D)
     if q.dtype not in (torch.bfloat16, torch.float16) or k_cache.dtype != q.dtype or v_cache.dtype != q.dtype:
         raise ValueError("paged decode expects bf16 or fp16 q and caches of one dtype")
+    _check_paging_args(B, D, k_cache, v_cache, block_table, context_lens)
     q = _flash_operand(q)
     k_cache = _flash_operand(k_cache)
     v_cache = _flash_operand(v_cache)
@@ -864,6 +882,7 @@ def sp2norm_paged_kv_append(k_cache, v_cache, k_new, v_new, block_table, context
     assert k_cache.shape[2] == block_size
     if k_cache.dtype not in (torch.bfloat16, torch.float16) or v_cache.dtype != k_cache.dtype:
         raise ValueError("paged caches must be bf16 or fp16 of one dtype")
+    _check_paging_args(B, D, k_cache, v_cache, block_table, context_lens)
     for t in (k_cache, v_cache):
         if t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:-1]) or t.data_ptr() % 16:
             raise ValueError("paged caches need 16-byte aligned rows with unit stride along D")

@@ -140,3 +140,26 @@ def test_softmax_entry_points_validate_before_launch():
         smooth_attn.softmax_triton(torch.zeros(2, 2))  # not a device tensor
     with pytest.raises(ValueError):
         smooth_attn.softmax_causal_triton(torch.zeros(2, 3))
+
+
+def test_paged_entry_points_reject_short_tables_before_launch():
+    # the kernels read B block-table rows, B context lengths and D-wide cache
+    # rows: shorter arrays are refused on the host, before any device call
+    B, Hq, Hkv, P, D = 3, 4, 2, 16, 32
+    q = torch.zeros(B, Hq, 1, D, dtype=torch.bfloat16)
+    kc = torch.zeros(6, Hkv, P, D, dtype=torch.bfloat16)
+    table = torch.zeros(B, 2, dtype=torch.int32)
+    lens = torch.full((B,), 5, dtype=torch.int32)
+    bad = [
+        (kc, table[:2], lens),                         # block table shorter than B
+        (kc, table, lens[:2]),                         # fewer context lengths than B
+        (kc[..., :16].contiguous(), table, lens),      # cache rows narrower than D
+        (kc, table.float(), lens),                     # floating-point block table
+    ]
+    for cache, tab, ctx in bad:
+        with pytest.raises(ValueError):
+            smooth_attn.sp2norm_paged_attention(q, cache, cache, tab, ctx, block_size=P)
+    new = torch.zeros(B, Hkv, 1, D, dtype=torch.bfloat16)
+    for cache, tab, ctx in bad[:2] + bad[3:]:
+        with pytest.raises(ValueError):
+            smooth_attn.sp2norm_paged_kv_append(cache, cache, new, new, tab, ctx, block_size=P)
