@@ -166,3 +166,20 @@ def test_paged_config5():
     ref = eager.paged_decode_eager(q[sel].double(), kc.double(), vc.double(), table[sel], lens[sel])
     assert rel_err(out[sel], ref) <= 1e-2
     assert bool(torch.isfinite(out).all())
+
+
+def test_index_tensors_on_another_device_are_refused():
+    # a host block table or context array would be dereferenced by the
+    # kernel as a device pointer: the entry points refuse it before launching
+    B, Hq, Hkv, P, D = 2, 4, 2, 16, 64
+    q = torch.randn(B, Hq, 1, D, generator=_g(31)).bfloat16().to(DEV)
+    kc = torch.zeros(4, Hkv, P, D, dtype=torch.bfloat16, device=DEV)
+    table = torch.arange(2 * B, dtype=torch.int32).view(B, 2)
+    lens = torch.full((B,), 20, dtype=torch.int32)
+    for tab, ctx in ((table, lens.to(DEV)), (table.to(DEV), lens)):
+        with pytest.raises(ValueError):
+            smooth_attn.sp2norm_paged_attention(q, kc, kc, tab, ctx, block_size=P)
+        with pytest.raises(ValueError):
+            smooth_attn.sp2norm_paged_kv_append(kc, kc, kc[:B, :, :1], kc[:B, :, :1], tab, ctx, block_size=P)
+    out = smooth_attn.sp2norm_paged_attention(q, kc, kc, table.to(DEV), lens.to(DEV), block_size=P)
+    assert out.shape == (B, Hq, D) and bool((out == 0).all())  # zero V rows
