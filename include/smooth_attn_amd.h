@@ -250,7 +250,10 @@ int sa_flash_rope_fwd(const void* q, const void* k, const void* v,
 /*
  * Bytes of workspace sa_paged_decode needs for these sizes: a plan of B + 2
  * int32 (padded to 16 bytes), then fp32 partials [B, Hq, n_slots, D] and
- * [B, Hq, n_slots] with n_slots = ceil(max_pages * page_size / 512) + 1.
+ * [B, Hq, n_slots] with n_slots = ceil(max_pages * page_size / (32 m)) + 1,
+ * m = clamp(B * ceil(Hq / 8) * ceil(max_pages * page_size / 32) / 2048, 1,
+ * 16), a floor on the 32-token tiles each wave takes (smaller batches spread
+ * over more waves).
  */
 int64_t sa_paged_decode_workspace_size(int B, int Hq, int D, int max_pages,
                                        int page_size);

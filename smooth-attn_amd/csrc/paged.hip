@@ -24,13 +24,16 @@
 // k = its wave minus the wave that owns the segment's first tile; a merge
 // kernel sums the slots in order (squareplus needs no running maximum, so
 // merging is a plain sum) and divides once.
+#include <algorithm>
+
 #include "flash_common.hpp"
 
 namespace sa {
 namespace {
 
-constexpr int kSplitTok = 512;  // minimum tokens per wave (bounds the pieces per segment)
 constexpr int kTile = 32;       // tokens per MFMA tile
+constexpr int kSplitTok = 512;  // largest minimum of tokens per wave (bounds the pieces per segment)
+constexpr int kTargetWaves = 2048;  // about the partial kernel's resident waves (256 CUs x 8)
 constexpr int kWinPages = 64;   // page ids held per wave at a time (one per lane)
 
 struct PagedParams {
@@ -46,6 +49,7 @@ struct PagedParams {
     int64_t qs[4], ks[4], vs[4], os[3];
     int64_t bt_stride;
     int B, Hq, Hkv, G, P, logP, max_pages, n_pages, n_slots, n_waves;
+    int per;  // minimum tiles per active wave
     float scale;
 };
 
@@ -56,9 +60,9 @@ __device__ __forceinline__ int ctx_of(const PagedParams& p, int b) {
 
 // Plan: plan[b] = sum_{b' < b} Hkv * ceil(ctx_b' / 32) for b <= B (plan[B] =
 // Tt, the tiles of all (sequence, KV head) segments), plan[B + 1] = Ne, the
-// waves that get work: every wave's range holds at least kSplitTok / kTile
-// tiles (so a segment of c tokens is cut into at most ceil(c / kSplitTok) + 1
-// pieces), and at most n_waves waves run.  One block.
+// waves that get work: every wave's range holds at least `per` tiles (so a
+// segment of c tokens is cut into at most ceil(c / (32 per)) + 1 pieces),
+// and at most n_waves waves run.  One block.
 __global__ __launch_bounds__(256) void paged_plan_kernel(PagedParams p) {
     __shared__ int part[256];
     const int tid = threadIdx.x;
@@ -81,8 +85,7 @@ __global__ __launch_bounds__(256) void paged_plan_kernel(PagedParams p) {
     }
     if (tid == 0) {
         p.plan[p.B] = carry;
-        const int per = kSplitTok / kTile;
-        p.plan[p.B + 1] = carry == 0 ? 0 : max(1, min(p.n_waves, carry / per));
+        p.plan[p.B + 1] = carry == 0 ? 0 : max(1, min(p.n_waves, carry / p.per));
     }
 }
 
@@ -332,7 +335,12 @@ int resident_waves() {
 template <typename T, int D>
 int launch_paged(PagedParams prm, hipStream_t st) {
     const bool uniform = prm.P * (D / 8) >= 64;
-    prm.n_waves = uniform ? resident_waves<T, D, true>() : resident_waves<T, D, false>();
+    const int resident = uniform ? resident_waves<T, D, true>() : resident_waves<T, D, false>();
+    // The plan gives work to at most Tt / per waves, and Tt is at most
+    // B * Hkv * ceil(max_pages * P / kTile): no more waves are launched.
+    const int64_t max_tiles = static_cast<int64_t>(prm.B) * prm.Hkv *
+                              ((static_cast<int64_t>(prm.max_pages) * prm.P + kTile - 1) / kTile);
+    prm.n_waves = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(resident, max_tiles / prm.per)));
     paged_plan_kernel<<<1, 256, 0, st>>>(prm);
     if (uniform)
         paged_partial_kernel<T, D, true><<<prm.n_waves, 64, 0, st>>>(prm);
@@ -342,11 +350,28 @@ int launch_paged(PagedParams prm, hipStream_t st) {
     return status_from_launch();
 }
 
-// Partial slots per (sequence, query head): a segment of c tokens meets at
-// most ceil(c / kSplitTok) + 1 waves.
-int64_t slots_for(int max_pages, int page_size) {
+// Minimum tiles per active wave: kSplitTok / kTile (few pieces, few
+// partials to merge) when the work fills the device, down to 1 for small
+// batches, so that their tiles spread over up to kTargetWaves waves instead
+// of queueing on a few: clamp(n_segments * max_tiles / kTargetWaves, 1, 16).
+int split_for(int64_t segments, int max_pages, int page_size) {
     const int64_t toks = static_cast<int64_t>(max_pages) * page_size;
-    return (toks <= 0 ? 1 : (toks + kSplitTok - 1) / kSplitTok) + 1;
+    const int64_t ub = segments * ((toks + kTile - 1) / kTile);
+    return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(kSplitTok / kTile, ub / kTargetWaves)));
+}
+// The workspace is sized for the split with B * ceil(Hq / 8) segments (KV
+// groups of up to 8 query heads); the launch takes the larger of that and
+// the split its B * Hkv segments give, so its partial slots always fit.
+int split_floor(int B, int Hq, int max_pages, int page_size) {
+    return split_for(static_cast<int64_t>(B) * ((Hq + 7) / 8), max_pages, page_size);
+}
+
+// Partial slots per (sequence, query head): a segment of c tokens meets at
+// most ceil(c / (kTile per)) + 1 waves.
+int64_t slots_for(int max_pages, int page_size, int per) {
+    const int64_t toks = static_cast<int64_t>(max_pages) * page_size;
+    const int64_t span = static_cast<int64_t>(per) * kTile;
+    return (toks <= 0 ? 1 : (toks + span - 1) / span) + 1;
 }
 
 // Workspace layout: plan (B + 2 int32, padded to 16 bytes), then the O and S
@@ -358,7 +383,8 @@ int64_t plan_bytes(int B) { return ((static_cast<int64_t>(B) + 2) * 4 + 15) / 16
 
 extern "C" int64_t sa_paged_decode_workspace_size(int B, int Hq, int D, int max_pages, int page_size) {
     if (B <= 0 || Hq <= 0 || D <= 0 || max_pages < 0 || page_size <= 0) return 0;
-    const int64_t slots = static_cast<int64_t>(B) * Hq * sa::slots_for(max_pages, page_size);
+    const int64_t slots = static_cast<int64_t>(B) * Hq *
+                          sa::slots_for(max_pages, page_size, sa::split_floor(B, Hq, max_pages, page_size));
     return sa::plan_bytes(B) + slots * (D + 1) * static_cast<int64_t>(sizeof(float));
 }
 
@@ -400,7 +426,9 @@ extern "C" int sa_paged_decode(const void* q, const void* k_cache, const void* v
     prm.out = static_cast<bf16*>(out);
     prm.table = block_table;
     prm.ctx = context_lens;
-    prm.n_slots = static_cast<int>(slots_for(max_pages, page_size));
+    prm.per = std::max(split_floor(B, Hq, max_pages, page_size),
+                       split_for(static_cast<int64_t>(B) * Hkv, max_pages, page_size));
+    prm.n_slots = static_cast<int>(slots_for(max_pages, page_size, prm.per));
     prm.plan = reinterpret_cast<int*>(workspace);
     prm.ws_o = workspace + plan_bytes(B) / 4;
     prm.ws_s = prm.ws_o + static_cast<int64_t>(B) * Hq * prm.n_slots * D;

@@ -86,3 +86,30 @@ def test_transpose16_argument_errors():
     assert lib.sa_transpose16(d, d, 8, 8, 12, 8, None) == -5   # stride not a multiple of 8
     assert lib.sa_transpose16(ctypes.c_void_p(18), d, 8, 8, 8, 8, None) == -5  # unaligned
     assert lib.sa_transpose16(d, d, 0, 8, 8, 8, None) == 0
+
+
+def test_paged_workspace_sizes():
+    # plan (B + 2 int32, padded to 16 bytes) + fp32 partials [B, Hq, n_slots, D + 1];
+    # n_slots = ceil(max_pages * P / (32 m)) + 1 with the tile floor
+    # m = clamp(B * ceil(Hq / 8) * ceil(max_pages * P / 32) / 2048, 1, 16)
+    lib = _lib.load()
+
+    def expect(B, Hq, D, max_pages, P):
+        tiles = -(-max_pages * P // 32)
+        m = max(1, min(16, B * -(-Hq // 8) * tiles // 2048))
+        slots = -(-max_pages * P // (32 * m)) + 1
+        return ((B + 2) * 4 + 15) // 16 * 16 + B * Hq * slots * (D + 1) * 4, m, slots
+
+    cases = {  # shape -> (m, n_slots)
+        (64, 32, 128, 1024, 16): (16, 33),  # config 5: the full split, as for large batches
+        (4, 8, 128, 16, 16): (1, 9),        # 4 short sequences: one tile per wave
+        (16, 32, 128, 128, 16): (2, 33),    # 16 x 2K tokens, Hq 32
+        (0, 8, 128, 16, 16): None,          # empty batch: nothing to size
+    }
+    for (B, Hq, D, mp, P), ms in cases.items():
+        got = lib.sa_paged_decode_workspace_size(B, Hq, D, mp, P)
+        if ms is None:
+            assert got == 0
+            continue
+        want, m, slots = expect(B, Hq, D, mp, P)
+        assert (m, slots) == ms and got == want
