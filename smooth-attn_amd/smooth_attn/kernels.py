@@ -8,6 +8,7 @@ Citations are ``path:line`` into the reference.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import math
 from dataclasses import dataclass
@@ -155,7 +156,20 @@ def _check_row_length(n_cols):
 
 
 def _stream(t):
-    return torch.cuda.current_stream(t.device).cuda_stream
+    """The current HIP stream of t's device as a raw handle (without building
+    a torch Stream object on every launch)."""
+    return torch._C._cuda_getCurrentRawStream(t.device.index)
+
+
+_NO_GUARD = contextlib.nullcontext()
+
+
+def _device_of(t):
+    """Context that makes t's device current for the launch: a no-op when it
+    already is (the common case), else torch.cuda.device."""
+    if t.device.index == torch._C._cuda_getDevice():
+        return _NO_GUARD
+    return torch.cuda.device(t.device)
 
 
 def _is_winner_family(family):
@@ -185,7 +199,7 @@ def _row_launch_meta(variant, kind, x2d, y2d, rerun, power=2):
         else:
             lib = _lib.load()
             info = _lib.LaunchInfo()
-            with torch.cuda.device(x2d.device):
+            with _device_of(x2d):
                 if kind == "norm":
                     st = lib.sa_norm_fwd_launch_info(x2d.data_ptr(), y2d.data_ptr(), n_rows, n_cols, x2d.stride(0),
                                                      y2d.stride(0), _DTYPE_CODE[x2d.dtype], int(power),
@@ -219,7 +233,7 @@ def _norm_fwd_2d(x2d, out2d, family, causal):
     n_rows, n_cols = x2d.shape
     _check_row_length(n_cols)
     lib = _lib.load()
-    with torch.cuda.device(x2d.device):
+    with _device_of(x2d):
         st = lib.sa_norm_fwd(
             x2d.data_ptr(), out2d.data_ptr(), n_rows, n_cols, x2d.stride(0), out2d.stride(0),
             _DTYPE_CODE[x2d.dtype], 1 if causal else 0, float(family.alpha), float(family.theta),
@@ -232,7 +246,7 @@ def _norm_bwd_2d(x2d, g2d, dx2d, family, causal):
     n_rows, n_cols = x2d.shape
     _check_row_length(n_cols)
     lib = _lib.load()
-    with torch.cuda.device(x2d.device):
+    with _device_of(x2d):
         st = lib.sa_norm_bwd(
             x2d.data_ptr(), g2d.data_ptr(), dx2d.data_ptr(), n_rows, n_cols, x2d.stride(0),
             g2d.stride(0), dx2d.stride(0), _DTYPE_CODE[x2d.dtype], _DTYPE_CODE[g2d.dtype],
@@ -425,7 +439,7 @@ def _softmax_2d(x2d, out2d, causal):
     n_rows, n_cols = x2d.shape
     _check_row_length(n_cols)
     lib = _lib.load()
-    with torch.cuda.device(x2d.device):
+    with _device_of(x2d):
         st = lib.sa_softmax_fwd(x2d.data_ptr(), out2d.data_ptr(), n_rows, n_cols, x2d.stride(0), out2d.stride(0),
                                 _DTYPE_CODE[x2d.dtype], 1 if causal else 0, _stream(x2d))
     _lib.check(st, "sa_softmax_fwd")
@@ -541,7 +555,7 @@ def _sp2norm_flash_fwd(q, k, v, scale, n_kv_groups=1, window_size=0, use_fast_sq
         o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     row_sums = torch.empty(B, H_q, T, device=q.device, dtype=torch.float32)
     lib = _lib.load()
-    with torch.cuda.device(q.device):
+    with _device_of(q):
         st = lib.sa_flash_fwd(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), row_sums.data_ptr(),
             B, H_q, H_kv, T, D, _lib.strides(q), _lib.strides(k), _lib.strides(v), _lib.strides(o),
@@ -563,7 +577,7 @@ def _sp2norm_flash_bwd(q, k, v, o, do, row_sums, scale, n_kv_groups=1, window_si
     delta = torch.empty(B, H_q, T, device=q.device, dtype=torch.float32)
     rs = row_sums.contiguous()
     lib = _lib.load()
-    with torch.cuda.device(q.device):
+    with _device_of(q):
         st = lib.sa_flash_bwd(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(), rs.data_ptr(),
             dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr(), B, H_q, H_kv, T, D,
@@ -648,7 +662,7 @@ def _sp2norm_rope_flash_fwd(q, k, v, cos, sin, scale, n_kv_groups=1, window_size
     lib = _lib.load()
     ws = torch.empty(max(int(lib.sa_flash_rope_workspace_size(B, H_kv, T, D)), 16), dtype=torch.uint8,
                      device=q.device)
-    with torch.cuda.device(q.device):
+    with _device_of(q):
         st = lib.sa_flash_rope_fwd(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), cos.data_ptr(), sin.data_ptr(), o.data_ptr(),
             row_sums.data_ptr(), ws.data_ptr(), ws.numel(), B, H_q, H_kv, T, D, _lib.strides(q), _lib.strides(k),
@@ -712,7 +726,7 @@ def _transpose16(x):
     if out.stride(0) % 8:  # rows not a multiple of 8: fall back to a torch copy of the view
         return x.t().contiguous()
     lib = _lib.load()
-    with torch.cuda.device(x.device):
+    with _device_of(x):
         st = lib.sa_transpose16(x.data_ptr(), out.data_ptr(), rows, cols, x.stride(0), out.stride(0), _stream(x))
     _lib.check(st, "sa_transpose16")
     return out
@@ -732,7 +746,7 @@ def _quantize_to_fp8_device(x):
     x8 = torch.empty(xc.shape, dtype=torch.float8_e4m3fn, device=x.device)
     ws = torch.empty(2, dtype=torch.float32, device=x.device)
     lib = _lib.load()
-    with torch.cuda.device(x.device):
+    with _device_of(x):
         st = lib.sa_fp8_quantize(xc.data_ptr(), x8.data_ptr(), xc.numel(), _DTYPE_CODE[xc.dtype],
                                  ws.data_ptr(), ws.data_ptr() + 4, _stream(xc))
     _lib.check(st, "sa_fp8_quantize")
@@ -777,7 +791,7 @@ def _sp2norm_fp8_flash_fwd(q_fp8, k_fp8, v_fp8, q_scale, k_scale, v_scale, attn_
     qs, ks = _scale_tensor(q_scale, dev), _scale_tensor(k_scale, dev)
     vs = _scale_tensor(1.0 if v_scale is None else v_scale, dev)
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _device_of(q8):
         st = lib.sa_flash_fp8_fwd(
             q8.data_ptr(), k8.data_ptr(), v8.data_ptr(), o.data_ptr(), row_sums.data_ptr(), qs.data_ptr(),
             ks.data_ptr(), vs.data_ptr(), B, H_q, H_kv, T, D, _lib.strides(q8), _lib.strides(k8),
@@ -856,7 +870,7 @@ def sp2norm_paged_attention(q, k_cache, v_cache, block_table, context_lens, *, s
     lib = _lib.load()
     ws_bytes = lib.sa_paged_decode_workspace_size(B, H_q, D, max_blocks_per_seq, block_size)
     ws = torch.empty(max(1, (ws_bytes + 3) // 4), dtype=torch.float32, device=q.device)
-    with torch.cuda.device(q.device):
+    with _device_of(q):
         st = lib.sa_paged_decode(
             q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(), block_table.data_ptr(),
             context_lens.data_ptr(), B, H_q, H_kv, D, block_size, max_blocks_per_seq, k_cache.shape[0],
@@ -896,7 +910,7 @@ def sp2norm_paged_kv_append(k_cache, v_cache, k_new, v_new, block_table, context
         block_table = block_table.contiguous()
     context_lens = context_lens.to(torch.int32).contiguous()
     lib = _lib.load()
-    with torch.cuda.device(k_cache.device):
+    with _device_of(k_cache):
         st = lib.sa_paged_kv_append(
             k_new.data_ptr(), v_new.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), block_table.data_ptr(),
             context_lens.data_ptr(), B, H_kv, n_new, D, block_size, block_table.shape[1], k_cache.shape[0],
