@@ -464,12 +464,15 @@ __global__ __launch_bounds__(256) void norm_bwd_scalar(const T* __restrict__ x, 
 // Host dispatch.
 // ---------------------------------------------------------------------------
 constexpr int kMaxCols = 8192;
-// Waves per row for rows of NCH 1 KB chunks: 4 (one row per block) from 8
-// chunks up.  Measured: causal bf16 L=4096 fwd 3-4% and bwd 1-3% faster,
-// row-wise fp32 L=2048 6% faster; for rows of 2-4 chunks (causal bf16
-// L=1024/2048) splitting was 11-17% slower, so those keep one wave per row.
-// (8 waves per row, one chunk per wave at bf16 L=4096, measured 17% slower.)
-constexpr int split_for(int nch) { return nch >= 8 ? 4 : 1; }
+// Waves per row for rows of NCH 1 KB chunks: 4 (one row per block) for 8
+// chunks, 8 from 16 chunks up.  Measured: causal bf16 L=4096 fwd 3-4% and
+// bwd 1-3% faster, row-wise fp32 L=2048 6% faster; for rows of 2-4 chunks
+// (causal bf16 L=1024/2048) splitting was 11-17% slower, so those keep one
+// wave per row.  Two chunks per wave does best: 8 waves per row at bf16
+// L=4096 (one chunk each) was 17% slower, while at fp32 L=4096 (16 chunks)
+// 8 waves beat 4 by 6.7% (fwd 1390 vs 1490 us) and 3.8% (bwd 2129 vs
+// 2212 us).
+constexpr int split_for(int nch) { return nch >= 16 ? 8 : nch >= 8 ? 4 : 1; }
 
 template <int R>
 dim3 split_grid(int64_t n_rows) {

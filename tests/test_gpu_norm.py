@@ -185,6 +185,7 @@ def test_full_size_config2_properties(L):
     (torch.bfloat16, 1024, "vec", 1),
     (torch.bfloat16, 100, "scalar", 1),   # 100 % 8 != 0: element loads
     (torch.float32, 2048, "split", 4),
+    (torch.float32, 4096, "split", 8),    # 16 chunks of 256 -> 8 waves per row
 ])
 def test_launch_meta_describes_the_kernel(dtype, L, kernel, waves):
     # return_meta carries the reference's keys (kernels.py:310-317, :423-427),
