@@ -619,7 +619,7 @@ int launch_bwd_p(const void* x, const void* dy, void* dx, int64_t n_rows, int n_
 }
 
 int check_rows(const void* a, const void* b, int64_t n_rows, int64_t n_cols) {
-    if (n_rows < 0 || n_cols < 0 || n_cols > kMaxCols) return SA_ERR_BAD_SHAPE;
+    if (n_rows < 0 || n_rows > INT32_MAX || n_cols < 0 || n_cols > kMaxCols) return SA_ERR_BAD_SHAPE;
     if (n_rows == 0 || n_cols == 0) return 1;  // nothing to do
     if (a == nullptr || b == nullptr) return SA_ERR_NULL_POINTER;
     return 0;
@@ -651,7 +651,7 @@ extern "C" int sa_norm_fwd_launch_info(const void* x, const void* y, int64_t n_r
                                        sa_launch_info* info) {
     using namespace sa;
     if (info == nullptr) return SA_ERR_NULL_POINTER;
-    if (n_rows < 0 || n_cols <= 0 || n_cols > kMaxCols) return SA_ERR_BAD_SHAPE;
+    if (n_rows < 0 || n_rows > INT32_MAX || n_cols <= 0 || n_cols > kMaxCols) return SA_ERR_BAD_SHAPE;
     if (x_row_stride < n_cols || y_row_stride < n_cols) return SA_ERR_BAD_STRIDE;
     const int nc = static_cast<int>(n_cols);
     RowLaunch L;

@@ -62,6 +62,14 @@ def test_launch_info_argument_errors():
     assert lib.sa_norm_fwd_launch_info(None, None, 4, 64, 64, 64, _lib.SA_BF16, 4, ctypes.byref(info)) == -4
     assert lib.sa_softmax_fwd_launch_info(None, None, 4, 64, 64, 64, _lib.SA_F32, None) == -1
     assert lib.sa_softmax_fwd_launch_info(None, None, 4, 64, 64, 64, 7, ctypes.byref(info)) == -3
+    # 2^31 rows: the one-block-per-row grids would wrap, so the row count is refused
+    big = 1 << 31
+    assert lib.sa_norm_fwd_launch_info(None, None, big, 64, 64, 64, _lib.SA_BF16, 2, ctypes.byref(info)) == -2
+    assert lib.sa_softmax_fwd_launch_info(None, None, big, 64, 64, 64, _lib.SA_F32, ctypes.byref(info)) == -2
+    assert lib.sa_norm_fwd(None, None, big, 64, 64, 64, _lib.SA_BF16, 1, 2.0, 0.5, 2, None) == -2
+    assert lib.sa_norm_bwd(None, None, None, big, 64, 64, 64, 64, _lib.SA_BF16, _lib.SA_BF16, 1, 2.0, 0.5, 2,
+                           None) == -2
+    assert lib.sa_softmax_fwd(None, None, big, 64, 64, 64, _lib.SA_F32, 0, None) == -2
 
 
 def test_paged_decode_rejects_plans_past_int32():

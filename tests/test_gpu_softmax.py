@@ -52,6 +52,21 @@ def test_causal_softmax(dtype, L):
     assert torch.allclose(y.float().sum(-1).cpu(), torch.ones(2, 3, L), atol=atol)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("L", [2048, 4096])
+def test_causal_softmax_long_rows(dtype, L):
+    # rows of 8 or more 1 KB chunks run 4 or 8 waves per row (one row per
+    # block); causal rows leave whole waves without a visible chunk
+    x = torch.randn(1, 1, L, L, generator=torch.Generator().manual_seed(L + 1)).to(dtype)
+    y = smooth_attn.softmax_causal_triton(x.to(DEV))
+    ref = eager.softmax_causal_eager(x.double())
+    assert rel_err(y, ref) <= tol(dtype)
+    upper = torch.triu(torch.ones(L, L, dtype=torch.bool), 1)
+    assert bool((y.cpu()[..., upper] == 0).all())
+    atol = 1e-4 if dtype == torch.float32 else 5e-3
+    assert torch.allclose(y.float().sum(-1).cpu(), torch.ones(1, 1, L), atol=atol)
+
+
 def test_softmax_large_values_and_unaligned_rows():
     # |x| up to 200: exp without the max shift would overflow fp32
     x = torch.linspace(-200, 200, 3 * 77).reshape(3, 77)
