@@ -114,6 +114,23 @@ def _validate_cuda_tensor(x, *, name):
         raise ValueError(f"{name} dtype must be one of {tuple(SUPPORTED_DTYPES.values())}, got {x.dtype}")
 
 
+def _check_same_device(ref_name, ref, **tensors):
+    """Every tensor argument of a fused entry point must be a CUDA tensor on
+    the device of ``ref`` (the kernels dereference them all as device
+    pointers there).  Raised before any launch, with the wording of
+    kernels.py:179-187; ``None`` entries (optional arguments) are skipped."""
+    for name, t in ((ref_name, ref), *tensors.items()):
+        if t is None:
+            continue
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"{name} must be a torch.Tensor")
+        if not t.is_cuda:
+            raise ValueError(f"{name} must be a CUDA tensor")
+        if t.device != ref.device:
+            raise ValueError(f"{name} must live on the same CUDA device as {ref_name} ({ref.device}), "
+                             f"got {t.device}")
+
+
 def _prepare_rowwise_input(x):
     _validate_cuda_tensor(x, name="x")
     if x.ndim != 2:
@@ -325,6 +342,7 @@ def _softplus_norm_causal_backward(x, grad_output, family):
 
     dy may be fp32 or x's dtype; the kernel reads it directly (no upcast pass).
     """
+    _check_same_device("x", x, grad_output=grad_output)
     seq_len = x.shape[-1]
     x2d = x.reshape(-1, seq_len)
     g = grad_output
@@ -340,6 +358,7 @@ def _softplus_norm_causal_backward(x, grad_output, family):
 
 def _softplus_norm_backward(x, grad_output, family):
     """Fused row-wise backward (the reference has only eager autograd, :1332-1346)."""
+    _check_same_device("x", x, grad_output=grad_output)
     g = grad_output if grad_output.dtype in (torch.float32, x.dtype) else grad_output.float()
     g = g.contiguous()
     dx = torch.empty_like(x)
@@ -540,6 +559,7 @@ def _flash_operand(t):
 
 def _sp2norm_flash_fwd(q, k, v, scale, n_kv_groups=1, window_size=0, use_fast_sqrt=True):
     """(o, row_sums) of the fused forward — replaces kernels.py:1912-1931."""
+    _check_same_device("q", q, k=k, v=v)
     B, H_q, T, D = q.shape
     H_kv = k.shape[1]
     if q.dtype not in (torch.bfloat16, torch.float16) or k.dtype != q.dtype or v.dtype != q.dtype:
@@ -567,6 +587,7 @@ def _sp2norm_flash_fwd(q, k, v, scale, n_kv_groups=1, window_size=0, use_fast_sq
 
 def _sp2norm_flash_bwd(q, k, v, o, do, row_sums, scale, n_kv_groups=1, window_size=0, use_fast_sqrt=True):
     """(dq, dk, dv) of the fused attention — replaces kernels.py:1934-1989."""
+    _check_same_device("q", q, k=k, v=v, o=o, do=do, row_sums=row_sums)
     B, H_q, T, D = q.shape
     H_kv = k.shape[1]
     q, k, v, o = _flash_operand(q), _flash_operand(k), _flash_operand(v), _flash_operand(o)
@@ -647,6 +668,7 @@ def _rope_tables(cos, sin, T, D):
 def _sp2norm_rope_flash_fwd(q, k, v, cos, sin, scale, n_kv_groups=1, window_size=0, o=None):
     """(o, row_sums) of the RoPE forward; ``o`` may be a caller view (e.g. of a
     [B, T, Hq, D] buffer) with 16-byte aligned rows."""
+    _check_same_device("q", q, k=k, v=v, cos=cos, sin=sin, o=o)
     B, H_q, T, D = q.shape
     H_kv = k.shape[1]
     if q.dtype not in (torch.bfloat16, torch.float16) or k.dtype != q.dtype or v.dtype != q.dtype:
@@ -705,6 +727,7 @@ def sp2norm_rope_flash_attention_proj(q, k, v, w_o, cos, sin, *, scale=None, win
     assert H_q % H_kv == 0
     assert D % 2 == 0
     assert w_o.shape[0] == H_q and w_o.shape[1] == D
+    _check_same_device("q", q, k=k, v=v, w_o=w_o, cos=cos, sin=sin)
     D_model = w_o.shape[2]
     if scale is None:
         scale = 1.0 / math.sqrt(D)
@@ -719,6 +742,7 @@ def sp2norm_rope_flash_attention_proj(q, k, v, w_o, cos, sin, *, scale=None, win
 def _transpose16(x):
     """Contiguous transpose of a 2-D bf16/fp16 CUDA matrix by sa_transpose16."""
     assert x.ndim == 2 and x.dtype in (torch.bfloat16, torch.float16)
+    _check_same_device("x", x)
     if x.stride(1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
         x = x.contiguous()
     rows, cols = x.shape
@@ -740,6 +764,7 @@ FP8_MAX = 448.0
 
 def _quantize_to_fp8_device(x):
     """(x8, scale) with the scale left on the device (no host sync)."""
+    _check_same_device("x", x)
     if x.dtype not in _DTYPE_CODE:
         raise ValueError(f"cannot quantise dtype {x.dtype}")
     xc = x.detach().contiguous()
@@ -772,6 +797,7 @@ def _sp2norm_fp8_flash_fwd(q_fp8, k_fp8, v_fp8, q_scale, k_scale, v_scale, attn_
     Scales may be Python floats or device scalars.  ``v_fp8`` may also be a
     bf16 tensor, in which case ``v_scale`` is ignored (PV on bf16 V).
     """
+    _check_same_device("q_fp8", q_fp8, k_fp8=k_fp8, v_fp8=v_fp8)
     B, H_q, T, D = q_fp8.shape
     H_kv = k_fp8.shape[1]
     if D not in _FLASH_HEAD_DIMS:
@@ -814,6 +840,7 @@ def sp2norm_fp8_flash_attention(q, k, v, *, scale=None, window_size=0, quantize_
     H_kv = k.shape[1]
     assert k.shape == (B, H_kv, T, D) and v.shape == (B, H_kv, T, D)
     assert H_q % H_kv == 0, f"H_q ({H_q}) must be divisible by H_kv ({H_kv})"
+    _check_same_device("q", q, k=k, v=v)
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     n_kv_groups = H_q // H_kv
@@ -856,6 +883,8 @@ def sp2norm_paged_attention(q, k_cache, v_cache, block_table, context_lens, *, s
     max_blocks_per_seq = block_table.shape[1]
     if scale is None:
         scale = 1.0 / math.sqrt(D)
+    _check_same_device("q", q, k_cache=k_cache, v_cache=v_cache, block_table=block_table,
+                       context_lens=context_lens)
     if q.dtype not in (torch.bfloat16, torch.float16) or k_cache.dtype != q.dtype or v_cache.dtype != q.dtype:
         raise ValueError("paged decode expects bf16 or fp16 q and caches of one dtype")
     _check_paging_args(B, D, k_cache, v_cache, block_table, context_lens)
@@ -894,6 +923,8 @@ def sp2norm_paged_kv_append(k_cache, v_cache, k_new, v_new, block_table, context
     B, H_kv, n_new, D = k_new.shape
     assert k_cache.shape[1] == H_kv and k_cache.shape[3] == D and v_cache.shape == k_cache.shape
     assert k_cache.shape[2] == block_size
+    _check_same_device("k_cache", k_cache, v_cache=v_cache, k_new=k_new, v_new=v_new, block_table=block_table,
+                       context_lens=context_lens)
     if k_cache.dtype not in (torch.bfloat16, torch.float16) or v_cache.dtype != k_cache.dtype:
         raise ValueError("paged caches must be bf16 or fp16 of one dtype")
     _check_paging_args(B, D, k_cache, v_cache, block_table, context_lens)

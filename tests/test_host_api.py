@@ -156,10 +156,115 @@ def test_paged_entry_points_reject_short_tables_before_launch():
         (kc[..., :16].contiguous(), table, lens),      # cache rows narrower than D
         (kc, table.float(), lens),                     # floating-point block table
     ]
-    for cache, tab, ctx in bad:
+    messages = ["block_table must be", "context_lens must hold", "caches must both be", "integer tensors"]
+    for (cache, tab, ctx), msg in zip(bad, messages):
+        with pytest.raises(ValueError, match=msg):
+            kernels._check_paging_args(B, D, cache, cache, tab, ctx)
+        # the public entry points refuse these host tensors before any launch
         with pytest.raises(ValueError):
             smooth_attn.sp2norm_paged_attention(q, cache, cache, tab, ctx, block_size=P)
     new = torch.zeros(B, Hkv, 1, D, dtype=torch.bfloat16)
     for cache, tab, ctx in bad[:2] + bad[3:]:
         with pytest.raises(ValueError):
             smooth_attn.sp2norm_paged_kv_append(cache, cache, new, new, tab, ctx, block_size=P)
+
+
+class _OnDevice(torch.Tensor):
+    """A host tensor that reports itself as living on a given CUDA device:
+    enough for the host-side device checks, which never dereference it."""
+
+    @staticmethod
+    def make(t, index):
+        out = torch.Tensor._make_subclass(_OnDevice, t)
+        out._index = index
+        return out
+
+    @property
+    def is_cuda(self):
+        return True
+
+    @property
+    def device(self):
+        return torch.device("cuda", getattr(self, "_index", 0))  # views of a cuda:0 tensor
+
+
+@pytest.fixture
+def no_library(monkeypatch):
+    """Any attempt to reach the HIP library fails the test: the device checks
+    must fire before it is loaded."""
+    from smooth_attn import _lib
+
+    def fail():
+        raise AssertionError("the HIP library was reached before the device check")
+
+    monkeypatch.setattr(_lib, "load", fail)
+
+
+def _fused_calls(mk, alt):
+    """(label, call) for every fused entry point, built from the tensor maker
+    ``mk(shape, dtype)`` (the reference device) with ``alt`` applied to the
+    argument under test."""
+    B, Hq, Hkv, T, D, P = 1, 4, 2, 16, 32, 16
+    bf = torch.bfloat16
+    q = mk((B, Hq, T, D), bf)
+    k, v = mk((B, Hkv, T, D), bf), mk((B, Hkv, T, D), bf)
+    o, do = mk((B, Hq, T, D), bf), mk((B, Hq, T, D), bf)
+    rs = mk((B, Hq, T), torch.float32)
+    cos, sin = mk((T, D // 2), torch.float32), mk((T, D // 2), torch.float32)
+    w_o = mk((Hq, D, 64), bf)
+    q8, k8 = mk((B, Hq, T, D), torch.float8_e4m3fn), mk((B, Hkv, T, D), torch.float8_e4m3fn)
+    qd = mk((B, Hq, 1, D), bf)
+    kc, vc = mk((4, Hkv, P, D), bf), mk((4, Hkv, P, D), bf)
+    tab, lens = mk((B, 4), torch.int32), mk((B,), torch.int32)
+    kn = mk((B, Hkv, 2, D), bf)
+    x, g = mk((2, 8, 8), bf), mk((2, 8, 8), bf)
+    fam = FamilyConfig()
+    return [
+        ("flash k", lambda: kernels._sp2norm_flash_fwd(q, alt(k), v, 0.1, 2)),
+        ("flash v", lambda: kernels._sp2norm_flash_fwd(q, k, alt(v), 0.1, 2)),
+        ("public flash", lambda: smooth_attn.sp2norm_flash_attention(q, alt(k), v)),
+        ("flash bwd do", lambda: kernels._sp2norm_flash_bwd(q, k, v, o, alt(do), rs, 0.1, 2)),
+        ("flash bwd row_sums", lambda: kernels._sp2norm_flash_bwd(q, k, v, o, do, alt(rs), 0.1, 2)),
+        ("flash bwd o", lambda: kernels._sp2norm_flash_bwd(q, k, v, alt(o), do, rs, 0.1, 2)),
+        ("rope cos", lambda: smooth_attn.sp2norm_rope_flash_attention(q, k, v, alt(cos), sin)),
+        ("rope sin", lambda: smooth_attn.sp2norm_rope_flash_attention(q, k, v, cos, alt(sin))),
+        ("rope v", lambda: smooth_attn.sp2norm_rope_flash_attention(q, k, alt(v), cos, sin)),
+        ("rope proj w_o", lambda: smooth_attn.sp2norm_rope_flash_attention_proj(q, k, v, alt(w_o), cos, sin)),
+        ("fp8 k8", lambda: kernels._sp2norm_fp8_flash_fwd(q8, alt(k8), v, 1.0, 1.0, None, 0.1, 2)),
+        ("fp8 v", lambda: kernels._sp2norm_fp8_flash_fwd(q8, k8, alt(v), 1.0, 1.0, None, 0.1, 2)),
+        ("fp8 public v", lambda: smooth_attn.sp2norm_fp8_flash_attention(q, k, alt(v))),
+        ("paged k_cache", lambda: smooth_attn.sp2norm_paged_attention(qd, alt(kc), vc, tab, lens)),
+        ("paged v_cache", lambda: smooth_attn.sp2norm_paged_attention(qd, kc, alt(vc), tab, lens)),
+        ("paged table", lambda: smooth_attn.sp2norm_paged_attention(qd, kc, vc, alt(tab), lens)),
+        ("paged lens", lambda: smooth_attn.sp2norm_paged_attention(qd, kc, vc, tab, alt(lens))),
+        ("append k_new", lambda: smooth_attn.sp2norm_paged_kv_append(kc, vc, alt(kn), kn, tab, lens)),
+        ("append table", lambda: smooth_attn.sp2norm_paged_kv_append(kc, vc, kn, kn, alt(tab), lens)),
+        ("norm bwd dy", lambda: kernels._softplus_norm_causal_backward(x, alt(g), fam)),
+        ("rowwise bwd dy", lambda: kernels._softplus_norm_backward(x[0], alt(g[0]), fam)),
+    ]
+
+
+@pytest.mark.parametrize("case", range(21))
+def test_fused_entry_points_refuse_host_tensors(case, no_library):
+    # one argument left on the host while the rest claim cuda:0
+    mk = lambda shape, dtype: _OnDevice.make(torch.zeros(shape, dtype=dtype), 0)
+    label, call = _fused_calls(mk, lambda t: t.as_subclass(torch.Tensor))[case]
+    with pytest.raises(ValueError, match="must be a CUDA tensor"):
+        call()
+
+
+@pytest.mark.parametrize("case", range(21))
+def test_fused_entry_points_refuse_mixed_devices(case, no_library):
+    # one argument on cuda:1 while the rest are on cuda:0
+    mk = lambda shape, dtype: _OnDevice.make(torch.zeros(shape, dtype=dtype), 0)
+    label, call = _fused_calls(mk, lambda t: _OnDevice.make(t.as_subclass(torch.Tensor), 1))[case]
+    with pytest.raises(ValueError, match="same CUDA device"):
+        call()
+
+
+@pytest.mark.parametrize("case", range(21))
+def test_fused_entry_points_refuse_meta_tensors(case, no_library):
+    mk = lambda shape, dtype: torch.empty(shape, dtype=dtype, device="meta")
+    label, call = _fused_calls(mk, lambda t: t)[case]
+    with pytest.raises(ValueError, match="must be a CUDA tensor"):
+        call()
