@@ -56,7 +56,10 @@ const char* sa_status_string(int status);
  *   causal != 0: row r attends to columns j <= (r mod n_cols); the rest of the
  *                row is written as exact zeros.
  * dtype: SA_F32 / SA_F16 / SA_BF16 for both x and y; fp32 arithmetic.
- * n_rows < 2^31, n_cols <= 8192.
+ * n_cols <= 8192.  n_rows * 64 * waves_per_row < 2^32 (one launch's work-item
+ * count), i.e. n_rows < 2^26 for rows of up to four 1 KB chunks (one wave
+ * per row), 2^24 for eight (4 waves) and 2^23 beyond (8 waves); more rows
+ * return SA_ERR_BAD_SHAPE.  sa_norm_fwd_launch_info reports waves_per_row.
  * Replaces the launches of _softplus_norm_fwd (kernels.py:494-531, launched
  * by _launch_row_kernel_out :887-939), _softplus_norm_causal_fwd (:565-604),
  * _winner_squareplus_p2_causal_fwd (:607-637) and the tiered path
@@ -88,7 +91,9 @@ int sa_norm_bwd(const void* x, const void* dy, void* dx, int64_t n_rows,
  * Softmax over each row of a [n_rows, n_cols] matrix (the comparison
  * baseline).  causal != 0: row r sees columns 0 .. r mod n_cols (others are
  * written as 0).  fp32 arithmetic, exp(x - rowmax) / sum.  dtype as
- * sa_norm_fwd; n_rows < 2^31, n_cols <= 8192.
+ * sa_norm_fwd; n_cols <= 8192; n_rows * 64 * waves_per_row < 2^32
+ * (sa_softmax_fwd_launch_info reports waves_per_row: 8 for rows of 16 or
+ * more 1 KB chunks, else 1), else SA_ERR_BAD_SHAPE.
  * Replaces softmax_triton[_out] / softmax_causal_triton[_out]
  * (kernels.py:1233-1325) and the kernels _softmax_fwd (:534-562) and
  * _softmax_causal_fwd (:852-884).

@@ -156,7 +156,15 @@ struct RowLaunch {
     int rows_per_block = 1, waves_per_row = 1, elems_per_load = 1, row_pass_elems = 64;
 };
 
+// A dispatch covers grid.x * block.x work-items, a count the dispatch packet
+// holds in 32 bits: with one block row per 64 * waves_per_row lanes this caps
+// n_rows at 2^26 for one wave per row, 2^24 for 4 and 2^23 for 8.
+inline bool grid_fits(dim3 grid, dim3 block) {
+    return static_cast<uint64_t>(grid.x) * block.x <= static_cast<uint64_t>(UINT32_MAX);
+}
+
 inline int launch_row(const RowLaunch& L, void** args, hipStream_t st) {
+    if (!grid_fits(L.grid, L.block)) return SA_ERR_BAD_SHAPE;
     const hipError_t e = hipLaunchKernel(L.fn, L.grid, L.block, args, 0, st);
     return e == hipSuccess ? status_from_launch() : static_cast<int>(e);
 }
@@ -164,6 +172,7 @@ inline int launch_row(const RowLaunch& L, void** args, hipStream_t st) {
 // *info from a plan plus the compiled kernel's registers, static LDS and
 // occupancy on the current device.
 inline int describe_row_launch(const RowLaunch& L, sa_launch_info* info) {
+    if (!grid_fits(L.grid, L.block)) return SA_ERR_BAD_SHAPE;
     hipFuncAttributes a{};
     hipError_t e = hipFuncGetAttributes(&a, L.fn);
     if (e != hipSuccess) return static_cast<int>(e);

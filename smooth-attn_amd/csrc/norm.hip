@@ -579,6 +579,7 @@ int launch_bwd_t(const void* x, const void* dy, void* dx, int64_t n_rows, int n_
     const bool vec_ok = (n_cols % VEC == 0) && (xs % VEC == 0) && (gs % GVEC == 0) && (dxs % VEC == 0) &&
                         aligned16(x) && aligned16(dy) && aligned16(dx);
     if (!vec_ok) {
+        if (!grid_fits(grid, block)) return SA_ERR_BAD_SHAPE;
         norm_bwd_scalar<T, TG, POWER><<<grid, block, 0, st>>>(xp, gp, dp, n_rows, n_cols, xs, gs, dxs, causal,
                                                               alpha, nat, eps);
         return status_from_launch();
@@ -586,13 +587,16 @@ int launch_bwd_t(const void* x, const void* dy, void* dx, int64_t n_rows, int n_
     switch (chunks_for(n_cols, VEC)) {
 #define SA_BWD_CASE(N)                                                                                   \
     case N:                                                                                              \
-        if constexpr (split_for(N) > 1)                                                                  \
-            norm_bwd_split<T, TG, N, POWER, split_for(N)><<<split_grid<split_for(N)>(n_rows),           \
-                                                                64 * split_block_waves<split_for(N)>(), 0, st>>>( \
+        if constexpr (split_for(N) > 1) {                                                                \
+            const dim3 sg = split_grid<split_for(N)>(n_rows), sb(64 * split_block_waves<split_for(N)>()); \
+            if (!grid_fits(sg, sb)) return SA_ERR_BAD_SHAPE;                                             \
+            norm_bwd_split<T, TG, N, POWER, split_for(N)><<<sg, sb, 0, st>>>(                            \
                     xp, gp, dp, n_rows, n_cols, xs, gs, dxs, causal, alpha, nat, eps);                   \
-        else                                                                                             \
+        } else {                                                                                         \
+            if (!grid_fits(grid, block)) return SA_ERR_BAD_SHAPE;                                        \
             norm_bwd_vec<T, TG, N, POWER><<<grid, block, 0, st>>>(xp, gp, dp, n_rows, n_cols, xs, gs, dxs, \
                                                                   causal, alpha, nat, eps);              \
+        }                                                                                                \
         break;
         SA_BWD_CASE(1)
         SA_BWD_CASE(2)

@@ -72,6 +72,25 @@ def test_launch_info_argument_errors():
     assert lib.sa_softmax_fwd(None, None, big, 64, 64, 64, _lib.SA_F32, 0, None) == -2
 
 
+def test_row_launches_refuse_grids_past_32_bit_work_items():
+    # a dispatch holds grid * block work-items in 32 bits: 2^26 rows of one
+    # wave each, 2^24 rows of 4 waves (bf16 rows of 8 KB), 2^23 of 8 waves
+    # (fp32 rows of 16 KB).  Refused by the plan before any HIP call (the
+    # pointers are 16-byte aligned dummies that nothing dereferences).
+    lib = _lib.load()
+    info = _lib.LaunchInfo()
+    d = ctypes.c_void_p(16)
+    for n_cols, dtype, limit in ((1024, _lib.SA_BF16, 1 << 26), (4096, _lib.SA_BF16, 1 << 24),
+                                 (4096, _lib.SA_F32, 1 << 23)):
+        assert lib.sa_norm_fwd_launch_info(d, d, limit, n_cols, n_cols, n_cols, dtype, 2, ctypes.byref(info)) == -2
+        assert lib.sa_norm_fwd(d, d, limit, n_cols, n_cols, n_cols, dtype, 1, 2.0, 0.5, 2, None) == -2
+        assert lib.sa_norm_bwd(d, d, d, limit, n_cols, n_cols, n_cols, n_cols, dtype, dtype, 1, 2.0, 0.5, 2,
+                               None) == -2
+    assert lib.sa_softmax_fwd_launch_info(d, d, 1 << 23, 4096, 4096, 4096, _lib.SA_F32, ctypes.byref(info)) == -2
+    assert lib.sa_softmax_fwd(d, d, 1 << 23, 4096, 4096, 4096, _lib.SA_F32, 0, None) == -2
+    assert lib.sa_softmax_fwd(d, d, 1 << 26, 256, 256, 256, _lib.SA_F32, 0, None) == -2
+
+
 def test_paged_decode_rejects_plans_past_int32():
     # B * Hkv * ceil(max context / 32) tiles must fit the plan's 32-bit
     # prefix sums; rejected before any HIP call, so this runs without a GPU

@@ -5,7 +5,7 @@ The oracle is the reference's backward formula in float64
 same inputs and the output O of the HIP forward: like the reference's
 backward, the kernels take delta = rowsum(dO * O) from the stored O, whose
 P was rounded to 16 bits.  Tolerance: every gradient
-max|HIP - oracle| / max(max|oracle|, 1e-2) <= 2e-2 (bf16 / fp16 outputs;
+max|HIP - oracle| / max(max|oracle|, 1e-2) <= 1e-2 (bf16 / fp16 outputs;
 P and dS are rounded to the 16-bit type before their products, as in the
 reference).  The public-API cases also meet the reference tests' own bound,
 assert_close(atol=5e-2, rtol=0.1) against autograd of the eager attention
@@ -22,7 +22,7 @@ from smooth_attn import kernels
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
-TOL = 2e-2
+TOL = 1e-2  # measured 2.3e-3 .. 4.9e-3 over the cases here
 
 
 def _g(seed):

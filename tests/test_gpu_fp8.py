@@ -4,7 +4,8 @@ and the fp8 fused forward against the oracle on the same quantised inputs.
 
 Tolerances: quantised codes and scales bit-exact; fp8 attention output
 (bf16) max|HIP - oracle| / max|oracle| <= 1e-2 against the dequantised fp64
-oracle on identical fp8 inputs (row sums <= 1e-4, see below); against unquantised bf16 eager the
+oracle on identical fp8 inputs (fp32 row sums <= 1e-4: the MFMA's fp8 dot
+keeps about 13 bits, shown by a known-answer test below); against unquantised bf16 eager the
 reference's own bounds (tests/test_training_api.py:326-372,
 tests/test_fp8_flash.py:10-102): max < 0.3 (0.4 for the length sweep),
 mean < 0.02.
@@ -81,6 +82,56 @@ def test_quantize_zero_and_shape():
     assert int(x8.view(torch.uint8).count_nonzero()) == 0
 
 
+def _score_from_row_sum(rs):
+    """The score s of a one-key row from its row sum rs = y + 1e-12, where
+    y = squareplus(2 s - 1)^2 = (a + sqrt(a^2 + 1))^2 with a = s - 1/2:
+    sqrt(y) = a + sqrt(a^2 + 1) gives a = (sqrt(y) - 1/sqrt(y)) / 2."""
+    r = (rs.double() - 1e-12).sqrt()
+    return (r - 1 / r) / 2 + 0.5
+
+
+def test_fp8_mfma_dot_precision_known_answer():
+    """Known-answer test of the fp8 QK^T products behind the row-sum bar.
+
+    One query and one key per head (T = 1, D = 128, so the scores come from
+    two 64-term f8f6f4 MFMA blocks, d < 64 and d >= 64, added in fp32).
+    Each head holds one large product q0 k0 = 16 * 16 = 2^8 and one small
+    product 2^(8-m) (powers of two, exact in e4m3fn), either in the large
+    product's block (d = 1) or in the other one (d = 65).  Scores are read
+    back exactly enough from the fp32 row sums (y is monotonic in s).
+
+    Measured: inside one block, a product below 2^-13 of the block's largest
+    is dropped (either sign), while the same product in the other block is
+    kept at fp32 precision.  So each 64-term fp8 dot carries about 13 bits
+    below its largest product (fp8 GEMMs on other vendors' hardware are
+    likewise known to keep about 14), which puts the fp8 path's fp32 row
+    sums 5e-6 .. 3e-5 from the exact-product oracle: their bar is 1e-4."""
+    cases = [(m, pos, sign) for m in (6, 10, 13, 15, 17, 19) for pos in (1, 65) for sign in (1, -1)]
+    H, D = len(cases), 128
+    q = torch.zeros(1, H, 1, D)
+    k = torch.zeros(1, H, 1, D)
+    for h, (m, pos, sign) in enumerate(cases):
+        q[0, h, 0, 0] = k[0, h, 0, 0] = 16.0
+        e = 8 - m
+        e1 = -((-e) // 2)
+        q[0, h, 0, pos] = sign * 2.0 ** e1
+        k[0, h, 0, pos] = 2.0 ** (e - e1)
+    q8, k8 = q.to(torch.float8_e4m3fn), k.to(torch.float8_e4m3fn)
+    assert torch.equal(q8.float(), q) and torch.equal(k8.float(), k)  # exact codes
+    v = torch.ones(1, H, 1, D, dtype=torch.bfloat16)
+    attn_scale = 2.0 ** -8  # scores about 1: y well conditioned
+    _, rs = kernels._sp2norm_fp8_flash_fwd(q8.to(DEV), k8.to(DEV), v.to(DEV), 1.0, 1.0, None, attn_scale, 1)
+    got = _score_from_row_sum(rs.cpu()[0, :, 0]) / attn_scale
+    exact = (q.double() * k.double()).sum(-1)[0, :, 0]
+    for h, (m, pos, sign) in enumerate(cases):
+        small = sign * 2.0 ** (8 - m)
+        # read-back noise is about 1e-5 on a score of 256 (fp32 row sums)
+        if m <= 13 or pos == 65:
+            assert abs(float(got[h] - exact[h])) <= 1e-4, (m, pos, sign, float(got[h] - exact[h]))
+        else:
+            assert abs(float(got[h] - (exact[h] - small))) <= 1e-4, (m, pos, sign, float(got[h] - exact[h]))
+
+
 def _fp8_case(B, Hq, Hkv, T, D, seed, quantize_v=True):
     g = _g(seed)
     q = torch.randn(B, Hq, T, D, generator=g).to(torch.bfloat16)
@@ -106,10 +157,11 @@ def test_fp8_forward_matches_oracle_on_same_codes(D, T, v_fp8):
     ref, ref_rs = eager.fp8_flash_attention_eager(q8, k8, vv, qs, ks, vs, scale, return_row_sums=True)
     assert o.dtype == torch.bfloat16
     assert rel_err(o, ref) <= 1e-2
-    # fp32 row sums: the f8f6f4 MFMA accumulates its 64-term fp8 dot products
-    # with reduced internal precision (observed ~2^-17 relative on scores), so
-    # the bound is 1e-4 rather than the 1e-5 used for bf16 scores.  The
-    # reference's fp8 entry point does not return row sums (kernels.py:2669-2673).
+    # fp32 row sums: each 64-term f8f6f4 MFMA dot keeps about 13 bits below
+    # its largest product (test_fp8_mfma_dot_precision_known_answer), which
+    # puts them 5e-6 .. 3e-5 from the exact-product oracle here, so the bound
+    # is 1e-4 rather than the 1e-5 used for bf16 scores.  The reference's
+    # fp8 entry point does not return row sums (kernels.py:2669-2673).
     assert rel_err(rs, ref_rs) <= 1e-4
 
 

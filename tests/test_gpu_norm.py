@@ -69,7 +69,7 @@ def test_rowwise_forward_matches_oracle(dtype, L):
 @pytest.mark.parametrize("dtype,gdtype", [(torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float32),
                                           (torch.float16, torch.float16), (torch.float32, torch.float32)])
 @pytest.mark.parametrize("L", [5, 32, 256, 1024])
-@pytest.mark.parametrize("fam", FAMILIES[:2], ids=["default", "a1.5t.25p3"])
+@pytest.mark.parametrize("fam", FAMILIES, ids=["default", "a1.5t.25p3", "a.75t-.5p1"])
 def test_causal_backward_matches_oracle(dtype, gdtype, L, fam):
     x = _randn((2, 2, L, L), dtype, seed=3 * L)
     dy = _randn((2, 2, L, L), gdtype, seed=3 * L + 1)
@@ -89,6 +89,122 @@ def test_rowwise_backward_matches_oracle(dtype, L):
     dx = kernels._softplus_norm_backward(x.to(DEV), dy.to(DEV), FamilyConfig())
     ref = eager.softplus_norm_backward(x.double(), dy.double(), causal=False)
     assert rel_err(dx, ref) <= REL_TOL[dtype]
+
+
+# Rows long enough to take the split kernels (several waves per row): 8
+# chunks of 1 KB -> 4 waves, 16 or more -> 8 waves.  fp32 L=2048 (R=4) and
+# L=4096 (R=8) are config 2's row-wise fp32 lengths.
+SPLIT_CASES = [
+    (torch.float32, 2048, 4), (torch.float32, 4096, 8), (torch.float32, 8192, 8),
+    (torch.bfloat16, 4096, 4), (torch.bfloat16, 8192, 8), (torch.float16, 8192, 8),
+]
+SPLIT_IDS = [f"{str(d).split('.')[-1]}-L{L}-R{r}" for d, L, r in SPLIT_CASES]
+
+
+def _check_row_kernel(dtype, L, waves, causal):
+    """The launch metadata names the split kernel with ``waves`` per row."""
+    if causal:
+        _, meta = smooth_attn.softplus_norm_causal_triton(_randn((1, 1, L, L), dtype, seed=L).to(DEV),
+                                                          return_meta=True)
+    else:
+        _, meta = smooth_attn.softplus_norm_triton(_randn((2, L), dtype, seed=L).to(DEV), return_meta=True)
+    assert meta["kernel"] == "split" and meta["waves_per_row"] == waves
+
+
+def _gradient_invariant(x, dy, dx, fam):
+    """Per-row |sum_j dx_j r_j| / (sum_j |dx_j r_j| + alpha p max_j |dy_j|),
+    r_j = sqrt(a_j^2 + 4), a = alpha (x - theta).  Since
+    dx_j = alpha p y_j (dy_j - T) / r_j with T = sum_k dy_k y_k, the sum is
+    alpha p T (1 - sum_j y_j) = O(eps): every row's ratio is rounding noise.
+    The denominator bounds the rounding of the terms and of T (which enters
+    every term coherently).  Computed in fp32 on the device."""
+    r = fam.alpha * (x.float() - fam.theta)
+    r.mul_(r).add_(4.0).sqrt_()
+    r.mul_(dx.float())
+    num = r.sum(-1, dtype=torch.float64).abs()
+    den = r.abs().sum(-1, dtype=torch.float64) + fam.alpha * fam.power * dy.float().abs().amax(-1).double()
+    return float((num / den.clamp(min=1e-30)).max())
+
+
+@pytest.mark.parametrize("dtype,L,waves", SPLIT_CASES, ids=SPLIT_IDS)
+@pytest.mark.parametrize("fam", FAMILIES, ids=["default", "a1.5t.25p3", "a.75t-.5p1"])
+def test_rowwise_split_kernels_match_oracle(dtype, L, waves, fam):
+    """Row-wise forward and backward of the split kernels vs the float64
+    oracle on a few full rows (the row-wise gradient is autograd of
+    softplus_norm_eager, kernels.py:1332-1346)."""
+    _check_row_kernel(dtype, L, waves, causal=False)
+    x = _randn((6, L), dtype, seed=7 * L + fam.power, scale=128 ** -0.5)
+    dy = _randn((6, L), dtype, seed=7 * L + fam.power + 1)
+    y = smooth_attn.softplus_norm_triton(x.to(DEV), family=fam)
+    assert rel_err(y, eager.softplus_norm_eager(x.double(), fam.alpha, fam.theta, fam.power)) <= REL_TOL[dtype]
+    dx = kernels._softplus_norm_backward(x.to(DEV), dy.to(DEV), fam)
+    ref = eager.softplus_norm_backward(x.double(), dy.double(), fam.alpha, fam.theta, fam.power, causal=False)
+    assert rel_err(dx, ref) <= REL_TOL[dtype]
+
+
+# rows across the matrix, including both sides of the 1 KB chunk edges (256
+# fp32 / 512 bf16 columns) and of the waves' chunk ranges
+SAMPLED_CAUSAL_ROWS = [0, 1, 2, 255, 256, 511, 512, 1023, 1024, 2047, 2048, 3000, 4095, 4096, 6000, 8190, 8191]
+
+
+@pytest.mark.parametrize("dtype,L,waves", SPLIT_CASES, ids=SPLIT_IDS)
+@pytest.mark.parametrize("fam", FAMILIES, ids=["default", "a1.5t.25p3", "a.75t-.5p1"])
+def test_causal_split_kernels_match_oracle(dtype, L, waves, fam):
+    """Causal forward and backward of the split kernels on one [L, L] matrix:
+    exact zeros over the whole upper triangle, and oracle parity on sampled
+    rows (causal row i is the row-wise function of its prefix x[i, :i+1])."""
+    _check_row_kernel(dtype, L, waves, causal=True)
+    gen = torch.Generator(device=DEV).manual_seed(L + fam.power)
+    x = (torch.randn(1, 1, L, L, generator=gen, device=DEV) * 128 ** -0.5).to(dtype)
+    dy = torch.randn(1, 1, L, L, generator=gen, device=DEV).to(dtype)
+    y = smooth_attn.softplus_norm_causal_triton(x, family=fam)
+    dx = kernels._softplus_norm_causal_backward(x, dy, fam)
+    up = torch.triu(torch.ones(L, L, dtype=torch.bool, device=DEV), 1)
+    assert int(y[0, 0][up].count_nonzero()) == 0 and int(dx[0, 0][up].count_nonzero()) == 0
+    del up
+    # size-independent properties of every row: sum_j y_j = 1, and the
+    # gradient invariant sum_j dx_j sqrt(a_j^2 + 4) = 0 (masked entries are
+    # exact zeros, so whole rows can be summed)
+    sums = y[0, 0].sum(-1, dtype=torch.float64)
+    assert float((sums - 1).abs().max()) <= (1e-5 if dtype == torch.float32 else 2e-2)
+    assert _gradient_invariant(x[0, 0], dy[0, 0], dx[0, 0], fam) <= REL_TOL[dtype]
+    # one relative error over all sampled rows, as over whole tensors elsewhere
+    # (row 0's exact gradient is O(eps), so a per-row ratio there is noise)
+    rows = [i for i in SAMPLED_CAUSAL_ROWS if i < L]
+    xs, dys = x[0, 0, rows].cpu().double(), dy[0, 0, rows].cpu().double()
+    ref_y = torch.zeros(len(rows), L, dtype=torch.float64)
+    ref_dx = torch.zeros(len(rows), L, dtype=torch.float64)
+    for n, i in enumerate(rows):
+        ref_y[n, :i + 1] = eager.softplus_norm_eager(xs[n, :i + 1], fam.alpha, fam.theta, fam.power)
+        ref_dx[n, :i + 1] = eager.softplus_norm_backward(xs[n:n + 1, :i + 1], dys[n:n + 1, :i + 1], fam.alpha,
+                                                         fam.theta, fam.power, causal=False)[0]
+    assert rel_err(y[0, 0, rows], ref_y) <= REL_TOL[dtype]
+    assert rel_err(dx[0, 0, rows], ref_dx) <= REL_TOL[dtype]
+
+
+@pytest.mark.parametrize("L", [2048, 4096])
+def test_full_size_config2_rowwise_fp32(L):
+    """Config 2's row-wise fp32 variant at full size, x = randn/sqrt(128)
+    and dy = randn, fp32 [64 L, L]: properties over the whole output
+    (rows sum to 1; sum_j dx_j sqrt(a_j^2 + 4) = 0 for every row) and the
+    float64 oracle at <= 1e-5 on sampled rows."""
+    fam = FamilyConfig()
+    n = 64 * L
+    gen = torch.Generator(device=DEV).manual_seed(40 + L)
+    x = torch.randn(n, L, generator=gen, device=DEV) / 128 ** 0.5
+    dy = torch.randn(n, L, generator=gen, device=DEV)
+    y = smooth_attn.softplus_norm_triton(x, family=fam)
+    assert float((y.sum(-1, dtype=torch.float64) - 1).abs().max()) <= 1e-5
+    dx = kernels._softplus_norm_backward(x, dy, fam)
+    step = n // 8
+    for lo in range(0, n, step):  # the row invariant in slices (bounded temporaries)
+        sl = slice(lo, lo + step)
+        assert _gradient_invariant(x[sl], dy[sl], dx[sl], fam) <= 1e-5, lo
+    rows = torch.tensor([0, 1, L - 1, L, n // 2 + 3, n - 2, n - 1] +
+                        torch.randint(0, n, (9,), generator=torch.Generator().manual_seed(L)).tolist())
+    xs, dys = x[rows.to(DEV)].cpu().double(), dy[rows.to(DEV)].cpu().double()
+    assert rel_err(y[rows.to(DEV)], eager.softplus_norm_eager(xs)) <= 1e-5
+    assert rel_err(dx[rows.to(DEV)], eager.softplus_norm_backward(xs, dys, causal=False)) <= 1e-5
 
 
 def test_autograd_module_matches_reference_test():

@@ -52,13 +52,17 @@ def test_causal_softmax(dtype, L):
     assert torch.allclose(y.float().sum(-1).cpu(), torch.ones(2, 3, L), atol=atol)
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("L", [2048, 4096])
-def test_causal_softmax_long_rows(dtype, L):
-    # rows of 8 or more 1 KB chunks run 4 or 8 waves per row (one row per
-    # block); causal rows leave whole waves without a visible chunk
+@pytest.mark.parametrize("dtype,L,kernel", [
+    (torch.float32, 2048, "vec"), (torch.bfloat16, 2048, "vec"), (torch.bfloat16, 4096, "vec"),
+    (torch.float32, 4096, "split"), (torch.bfloat16, 8192, "split"), (torch.float16, 8192, "split"),
+])
+def test_causal_softmax_long_rows(dtype, L, kernel):
+    # rows of 16 or more 1 KB chunks (fp32 L >= 4096, 16-bit L = 8192) run 8
+    # waves per row, one row per block; causal rows leave whole waves without
+    # a visible chunk.  Shorter rows keep one wave per row.
     x = torch.randn(1, 1, L, L, generator=torch.Generator().manual_seed(L + 1)).to(dtype)
-    y = smooth_attn.softmax_causal_triton(x.to(DEV))
+    y, meta = smooth_attn.softmax_causal_triton(x.to(DEV), return_meta=True)
+    assert meta["kernel"] == kernel and meta["waves_per_row"] == (8 if kernel == "split" else 1)
     ref = eager.softmax_causal_eager(x.double())
     assert rel_err(y, ref) <= tol(dtype)
     upper = torch.triu(torch.ones(L, L, dtype=torch.bool), 1)
@@ -84,12 +88,21 @@ def test_softmax_large_values_and_unaligned_rows():
 
 
 def test_benchmark_cli_quick(capsys):
-    # kernels.py:3078-3128 with a small sweep: every column runs, errors and sums are reported
+    # the reference's command line (kernels.py:3078-3128) with a small sweep:
+    # every column runs, HIP launches are reported against the HBM roofline,
+    # errors, row sums and the backward check come out right
     smooth_attn.main(["--mode", "all", "--quick", "--dtypes", "fp32,bf16", "--lengths", "64,128",
                       "--warmup", "2", "--iters", "3", "--check-backward"])
     text = capsys.readouterr().out
-    assert "Geo mean fam_hip / F.softmax" in text and "Geo means by dtype" in text
-    assert "softmax_sum=True family_sum=True" in text
-    assert "grad_close=True" in text
+    assert "row-wise fp32" in text and "squareplus family vs torch softmax: geometric mean" in text
+    assert text.count("%") >= 2 * 24  # two HIP columns per row-wise shape report a fraction of peak
+    assert "fp32: squareplus family vs torch softmax" in text and "bf16: squareplus family vs torch softmax" in text
+    assert " NO " not in text and "close: NO" not in text
+    assert text.count("close: yes") == 2
     res = smooth_attn.benchmark_causal_suite(smooth_attn.DEFAULT_FAMILY, [torch.bfloat16], [96], warmup=1, iters=2)
     assert res[0].softmax_sums_ok and res[0].family_sums_ok and res[0].softmax_err < 1e-2
+    assert res[0].family_meta["kernel"] in ("vec", "scalar", "split")
+    rows = smooth_attn.benchmark_rowwise_suite(smooth_attn.DEFAULT_FAMILY, shapes=[(64, 256)], warmup=1, iters=2)
+    assert rows[0].shape == (64, 256) and rows[0].family_us > 0 and rows[0].torch_softmax_us > 0
+    grads = smooth_attn.validate_causal_backward(smooth_attn.DEFAULT_FAMILY, [torch.float32], seq_len=32)
+    assert grads[0]["grad_close"] and grads[0]["max_abs_grad_err"] < 1e-4

@@ -135,6 +135,24 @@ def test_backward_known_answers():
     assert bool(torch.isfinite(dx2).all())
 
 
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("alpha,theta,power", [(2.0, 0.5, 2), (1.5, 0.25, 3), (0.75, -0.5, 1)])
+def test_backward_row_invariant(causal, alpha, theta, power):
+    # dx_j = alpha p y_j (dy_j - T) / sqrt(a_j^2 + 4) with T = sum_k dy_k y_k,
+    # so sum_j dx_j sqrt(a_j^2 + 4) = alpha p T (1 - sum_j y_j) = O(eps) for
+    # every row (the GPU tests check this over whole full-size outputs); a
+    # dropped or mis-signed T term or a wrong activation derivative breaks it
+    L = 40
+    x = torch.randn(5, L, L, generator=_g(13), dtype=DTYPE)
+    dy = torch.randn(5, L, L, generator=_g(14), dtype=DTYPE)
+    dx = eager.softplus_norm_backward(x, dy, alpha, theta, power, causal=causal)
+    a = alpha * (x - theta)
+    inv = (dx * torch.sqrt(a * a + 4.0)).sum(-1)
+    assert float(inv.abs().max()) < 1e-9  # alpha p |T| eps / S, S as small as 1e-2 here
+    # and it is not vacuous: the terms themselves are O(1)
+    assert float((dx * torch.sqrt(a * a + 4.0)).abs().sum(-1).min()) > (1e-3 if not causal else 0.0)
+
+
 # ---------------------------------------------------------------------------
 # Attention
 # ---------------------------------------------------------------------------
