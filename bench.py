@@ -8,17 +8,21 @@ dy = randn, bf16 [4,16,4096,4096], family alpha=2, theta=0.5, p=2), run
 through the public autograd API.  ``value`` is algorithmic HBM bytes per
 step / step time.  Algorithmic bytes: the forward reads the causal triangle
 of x and writes the full output; the backward reads the triangle of x and
-dy and writes the full dx (2 bytes per element).
+dy and writes the full dx (2 bytes per element).  HIP events around the
+forward and backward launches inside the timed steps give the per-launch
+durations behind ``roofline``.
 
-The same JSON line carries the fused-attention figures the metric also names
-(config 3 forward and backward, TFLOP/s over the causal triangle), config 4
-(fp8), config 5 (paged decode), config 2 at L = 1024 / 2048 with its
-row-wise fp32 variant, config 1's shape on the GPU, the rows built after the
-hot path (RoPE attention, softmax baselines, paged-KV append), the roofline of the
-dominant kernel (from HIP events around each launch), and the CPU
-baselines: the reference's eager CPU path restated in oracle/ (fp32 torch
-on the host cores), timed on a bounded sample of the config 2 workload and
-on config 1 at full shape.
+Every other figure follows one protocol: the median of 100 launches, each
+timed by its own HIP event pair on the launch stream and preceded by a read
+of 512 MiB of unrelated memory (which evicts the inputs from L2 and the
+256 MB Infinity Cache), after 20 warm-up launches.  The line carries the
+fused-attention figures the metric also names (config 3 forward and
+backward, TFLOP/s over the causal triangle), config 4 (fp8), config 5
+(paged decode), config 2 at L = 1024 / 2048 with its row-wise fp32 variant,
+config 1's shape on the GPU, the rows built after the hot path (RoPE
+attention, softmax baselines, paged-KV append), and the CPU baselines: the
+reference's eager CPU path restated in oracle/ (fp32 torch on the host
+cores), each on a bounded, stated sample of its config.
 """
 from __future__ import annotations
 
@@ -87,7 +91,50 @@ def time_events(torch, fn, iters):
     return [a.elapsed_time(b) for a, b in evs]
 
 
+FLUSH_BYTES = 512 << 20
+KERNEL_ITERS = 100
+KERNEL_WARMUP = 20
+_flush_buf = None
+
+
+def flush_caches(torch):
+    """Read 512 MiB of unrelated memory: evicts earlier data from the 4 MB
+    L2s and the 256 MB Infinity Cache, and (being a read) leaves no dirty
+    lines whose write-back would land in the next timed launch."""
+    global _flush_buf
+    if _flush_buf is None:
+        _flush_buf = torch.ones(FLUSH_BYTES // 4, dtype=torch.float32, device="cuda:0")
+    _flush_buf.sum()
+
+
+def time_kernel(torch, fn, iters=KERNEL_ITERS, warmup=KERNEL_WARMUP, flush=True):
+    """BASELINE protocol for one launch ``fn``: ``warmup`` untimed launches,
+    then ``iters`` launches each bracketed by its own HIP event pair on the
+    current (launch) stream and preceded by a cache flush outside the
+    events.  Returns the median, mean and p10/p90 in microseconds."""
+    for _ in range(warmup):
+        if flush:
+            flush_caches(torch)
+        fn()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
+    for a, b in evs:
+        if flush:
+            flush_caches(torch)
+        a.record(st)
+        fn()
+        b.record(st)
+    torch.cuda.synchronize()
+    us = sorted(a.elapsed_time(b) * 1e3 for a, b in evs)
+    n = len(us)
+    return {"median": us[n // 2], "mean": sum(us) / n, "p10": us[n // 10], "p90": us[(9 * n) // 10], "n": n}
+
+
 def bench_norm(torch, sa, steps, warmup):
+    """Config 2 at L=4096: the per-kernel protocol on the forward and the
+    backward launch, then the timed steps (W untimed, K timed) with HIP
+    events around each launch inside them."""
     from smooth_attn import FamilyConfig, kernels
 
     B, H, L = 4, 16, 4096
@@ -95,33 +142,41 @@ def bench_norm(torch, sa, steps, warmup):
     gen = torch.Generator(device=dev).manual_seed(2)
     x = (torch.randn(B, H, L, L, generator=gen, device=dev) / math.sqrt(128)).to(torch.bfloat16)
     dy = torch.randn(B, H, L, L, generator=gen, device=dev).to(torch.bfloat16)
-    xg = x.detach().requires_grad_(True)
     fam = FamilyConfig()
+    fwd_b, bwd_b = norm_bytes(B, H, L)
 
-    def step():
+    out = torch.empty_like(x)
+    kf = time_kernel(torch, lambda: sa.softplus_norm_causal_triton_out(out, x, family=fam))
+    kb = time_kernel(torch, lambda: kernels._softplus_norm_causal_backward(x, dy, fam))
+    del out
+
+    xg = x.detach().requires_grad_(True)
+    st = torch.cuda.current_stream()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+
+    def step(e=None):
+        if e is not None:
+            e[0].record(st)
         y = sa.softplus_norm_causal(xg, family=fam)
+        if e is not None:
+            e[1].record(st)
         (dx,) = torch.autograd.grad(y, xg, dy)
+        if e is not None:
+            e[2].record(st)
         return dx
 
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(steps):
-        step()
+    for i in range(steps):
+        step(ev[i])
     torch.cuda.synchronize()
     ms_per_step = (time.perf_counter() - t0) * 1e3 / steps
-
-    # Kernel-level timing: HIP events around each launch on the launch stream.
-    out = torch.empty_like(x)
-    n_ev = max(steps, 10)
-    fwd_ms = time_events(torch, lambda: sa.softplus_norm_causal_triton_out(out, x, family=fam), n_ev)
-    bwd_ms = time_events(torch, lambda: kernels._softplus_norm_causal_backward(x, dy, fam), n_ev)
-    fwd_b, bwd_b = norm_bytes(B, H, L)
-    fwd_avg = sum(fwd_ms) / len(fwd_ms)
-    bwd_avg = sum(bwd_ms) / len(bwd_ms)
+    fwd_avg = sum(e[0].elapsed_time(e[1]) for e in ev) / steps  # ms
+    bwd_avg = sum(e[1].elapsed_time(e[2]) for e in ev) / steps
     sample = x[0, 0].cpu(), dy[0, 0].cpu()
-    del x, dy, xg, out
+    del x, dy, xg
     torch.cuda.empty_cache()
     return {
         "shape": [B, H, L, L],
@@ -133,11 +188,18 @@ def bench_norm(torch, sa, steps, warmup):
         "bwd_us": bwd_avg * 1e3,
         "fwd_gbs": fwd_b / (fwd_avg * 1e-3) / 1e9,
         "bwd_gbs": bwd_b / (bwd_avg * 1e-3) / 1e9,
+        "kernel_fwd": kf,
+        "kernel_bwd": kb,
         "sample": sample,
     }
 
 
-def bench_attention(torch, sa, iters):
+def _rounded(d, nd=2):
+    return {k: (round(v, nd) if isinstance(v, float) else v) for k, v in d.items()}
+
+
+def bench_attention(torch, sa):
+    """Config 3: forward and backward of the fused bf16 attention."""
     from smooth_attn import kernels
 
     B, H, L, D = 4, 32, 4096, 128
@@ -147,14 +209,7 @@ def bench_attention(torch, sa, iters):
     k = torch.randn(B, H, L, D, generator=gen, device=dev).to(torch.bfloat16)
     v = torch.randn(B, H, L, D, generator=gen, device=dev).to(torch.bfloat16)
     scale = 1.0 / math.sqrt(D)
-    try:
-        kernels._sp2norm_flash_fwd(q, k, v, scale)
-    except RuntimeError as exc:
-        return {"status": f"not built: {exc}"}
-    for _ in range(3):
-        kernels._sp2norm_flash_fwd(q, k, v, scale)
-    ms = time_events(torch, lambda: kernels._sp2norm_flash_fwd(q, k, v, scale), iters)
-    avg = sum(ms) / len(ms)
+    kf = time_kernel(torch, lambda: kernels._sp2norm_flash_fwd(q, k, v, scale))
     flops = attn_flops(B, H, L, D)
     # Backward (dQ + delta kernel, then dK/dV kernel) on the forward's o and
     # row sums with a seeded upstream gradient.  FLOPs counted as 2.5 x the
@@ -162,29 +217,32 @@ def bench_attention(torch, sa, iters):
     # two-kernel scheme executes 3.5 x (S and dP are recomputed in both).
     do = torch.randn(B, H, L, D, generator=gen, device=dev).to(torch.bfloat16)
     o, rs = kernels._sp2norm_flash_fwd(q, k, v, scale)
-    bwd = lambda: kernels._sp2norm_flash_bwd(q, k, v, o, do, rs, scale)
-    for _ in range(2):
-        bwd()
-    bms = time_events(torch, bwd, iters)
-    bavg = sum(bms) / len(bms)
+    kb = time_kernel(torch, lambda: kernels._sp2norm_flash_bwd(q, k, v, o, do, rs, scale))
     bflops = 2.5 * flops
+    us, bus = kf["median"], kb["median"]
+    sample = q[0, :4].cpu(), k[0, :4].cpu(), v[0, :4].cpu()
+    del q, k, v, do, o, rs
+    torch.cuda.empty_cache()
     return {
         "config": "config3 fused causal attention fwd bf16 [4,32,4096,128]",
-        "us": avg * 1e3,
-        "tflops": flops / (avg * 1e-3) / 1e12,
-        "frac_bf16_peak": flops / (avg * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+        "us": round(us, 2),
+        "tflops": round(flops / us / 1e6, 1),
+        "frac_bf16_peak": round(flops / us / 1e6 / BF16_PEAK_TFLOPS, 4),
         "flops": flops,
-        "bwd_us": bavg * 1e3,
-        "bwd_tflops": bflops / (bavg * 1e-3) / 1e12,
-        "bwd_frac_bf16_peak": bflops / (bavg * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+        "fwd_times_us": _rounded(kf),
+        "bwd_us": round(bus, 2),
+        "bwd_tflops": round(bflops / bus / 1e6, 1),
+        "bwd_frac_bf16_peak": round(bflops / bus / 1e6 / BF16_PEAK_TFLOPS, 4),
         "bwd_flops": bflops,
-    }
+        "bwd_times_us": _rounded(kb),
+    }, sample
 
 
-def bench_fp8(torch, iters):
+def bench_fp8(torch):
     """Config 4: fp8 e4m3fn Q/K (per-tensor scales), bf16 V, GQA 32/8, L=8192.
     Kernel-only timing on pre-quantised inputs (as tests/bench_fp8_kernel.py
     times the reference), plus the full entry point with device quantisation."""
+    import smooth_attn
     from smooth_attn import kernels
 
     B, Hq, Hkv, L, D = 2, 32, 8, 8192, 128
@@ -196,34 +254,32 @@ def bench_fp8(torch, iters):
     q8, qs = kernels._quantize_to_fp8_device(q)
     k8, ks = kernels._quantize_to_fp8_device(k)
     scale = 1.0 / math.sqrt(D)
-    fn = lambda: kernels._sp2norm_fp8_flash_fwd(q8, k8, v, qs, ks, None, scale, Hq // Hkv)
-    for _ in range(3):
-        fn()
-    ms = time_events(torch, fn, iters)
-    avg = sum(ms) / len(ms)
-    full = time_events(torch, lambda: __import__("smooth_attn").sp2norm_fp8_flash_attention(
-        q, k, v, quantize_v=False), max(3, iters // 3))
+    kt = time_kernel(torch, lambda: kernels._sp2norm_fp8_flash_fwd(q8, k8, v, qs, ks, None, scale, Hq // Hkv))
+    full = time_kernel(torch, lambda: smooth_attn.sp2norm_fp8_flash_attention(q, k, v, quantize_v=False),
+                       iters=30, warmup=5)
     qk_flops = 2 * B * Hq * D * tri(L)
     ideal_us = qk_flops / (FP8_PEAK_TFLOPS * 1e12) * 1e6 + qk_flops / (BF16_PEAK_TFLOPS * 1e12) * 1e6
+    us = kt["median"]
+    sample = (q8[0, 0].cpu(), k8[0, 0].cpu(), v[0, 0].cpu(), float(qs), float(ks))
+    del q, k, v, q8, k8
+    torch.cuda.empty_cache()
     return {
         "config": "config4 fp8 e4m3fn QK^T + bf16 PV, GQA 32/8, [2,32|8,8192,128]",
-        "us": avg * 1e3,
-        "tflops_total": 2 * qk_flops / (avg * 1e-3) / 1e12,
-        "frac_of_mfma_roofline": ideal_us / (avg * 1e3),
-        "ideal_us": ideal_us,
-        "entry_point_us_incl_quantisation": sum(full) / len(full) * 1e3,
-    }
+        "us": round(us, 2),
+        "tflops_total": round(2 * qk_flops / us / 1e6, 1),
+        "frac_of_mfma_roofline": round(ideal_us / us, 4),
+        "ideal_us": round(ideal_us, 2),
+        "times_us": _rounded(kt),
+        "entry_point_us_incl_quantisation": round(full["median"], 2),
+    }, sample
 
 
-def bench_paged(torch, iters):
-    """Config 5: 64 sequences, ctx ~ U[512, 16384] (seeded), Hq 32 / Hkv 8,
-    D 128, page 16, block table a seeded permutation of all pages."""
-    import smooth_attn as sa
-
-    B, Hq, Hkv, D, P = 64, 32, 8, 128, 16
+def config5_inputs(torch):
+    """Config 5's seeded layout: 64 sequences, ctx ~ U[512, 16384], page 16,
+    the block table a seeded permutation of all pages handed out in order."""
+    B, P = 64, 16
     g = torch.Generator().manual_seed(5)
     lens = torch.randint(512, 16385, (B,), generator=g)
-    # serving-style table: a seeded permutation of all pages, handed out in order
     npg_seq = [(int(c) + P - 1) // P for c in lens]
     n_pages = sum(npg_seq)
     perm = torch.randperm(n_pages, generator=g).to(torch.int32)
@@ -232,6 +288,22 @@ def bench_paged(torch, iters):
     for i, n in enumerate(npg_seq):
         table[i, :n] = perm[pos:pos + n]
         pos += n
+    return lens, table, n_pages
+
+
+def paged_bytes(lens, P=16, B=64, Hq=32, D=128):
+    tot = int(lens.sum())
+    npg = sum((int(c) + P - 1) // P for c in lens)
+    return 4096 * tot + 4 * npg + B * Hq * D * 2 * 2 + 4 * B
+
+
+def bench_paged(torch):
+    """Config 5: 64 sequences, ctx ~ U[512, 16384] (seeded), Hq 32 / Hkv 8,
+    D 128, page 16, block table a seeded permutation of all pages."""
+    import smooth_attn as sa
+
+    B, Hq, Hkv, D, P = 64, 32, 8, 128, 16
+    lens, table, n_pages = config5_inputs(torch)
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev).manual_seed(5)
     kc = torch.randn(n_pages, Hkv, P, D, generator=gen, device=dev).to(torch.bfloat16)
@@ -239,27 +311,25 @@ def bench_paged(torch, iters):
     q = torch.randn(B, Hq, 1, D, generator=gen, device=dev).to(torch.bfloat16)
     table_d = table.to(dev)
     lens_d = lens.to(torch.int32).to(dev)
-    fn = lambda: sa.sp2norm_paged_attention(q, kc, vc, table_d, lens_d, block_size=P)
-    for _ in range(3):
-        fn()
-    ms = time_events(torch, fn, iters)
-    avg = sum(ms) / len(ms)
-    tot = int(lens.sum())
-    npg = sum((int(c) + P - 1) // P for c in lens)
-    nbytes = 4096 * tot + 4 * npg + B * Hq * D * 2 * 2 + 4 * B
-    return {
+    kt = time_kernel(torch, lambda: sa.sp2norm_paged_attention(q, kc, vc, table_d, lens_d, block_size=P))
+    nbytes = paged_bytes(lens)
+    us = kt["median"]
+    # the CPU leg gathers its sequences' pages from these device caches
+    sample = (q.cpu(), kc, vc, table, lens)
+    res = {
         "config": "config5 paged decode, 64 seqs ctx~U[512,16384], Hq32/Hkv8, D128, page16",
-        "us": avg * 1e3,
+        "us": round(us, 2),
         "bytes": nbytes,
-        "gbs": nbytes / (avg * 1e-3) / 1e9,
-        "frac_hbm_peak": nbytes / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS,
-        "sum_ctx": tot,
+        "gbs": round(nbytes / us / 1e3, 1),
+        "frac_hbm_peak": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+        "times_us": _rounded(kt),
+        "sum_ctx": int(lens.sum()),
     }
+    return res, sample
 
 
-def bench_next_rows(torch, iters):
-    """The rows built after the hot path, each timed like the rest (HIP
-    events on the launch stream, average per launch):
+def bench_next_rows(torch):
+    """The rows built after the hot path, each timed by the same protocol:
     - RoPE-fused attention forward on config 3's shape (K rotated once by a
       streaming kernel, Q in registers; the time includes the rotation),
       and the RoPE + W_o projection variant (RoPE forward plus one fp32-
@@ -276,26 +346,20 @@ def bench_next_rows(torch, iters):
     gen = torch.Generator(device=dev).manual_seed(11)
     out = {}
 
-    def avg_us(fn, n):
-        # median of per-call event times after a few warmup calls (first
-        # calls grow torch's allocator pools and pick library GEMM kernels),
-        # as the reference's _median_cuda_us (kernels.py:322-336)
-        for _ in range(5):
-            fn()
-        ms = sorted(time_events(torch, fn, n))
-        return ms[len(ms) // 2] * 1e3
+    def med(fn, **kw):
+        return time_kernel(torch, fn, **kw)["median"]
 
     B, H, L, D = 4, 32, 4096, 128
     q, k, v = (torch.randn(B, H, L, D, generator=gen, device=dev).to(torch.bfloat16) for _ in range(3))
     cos, sin = sa.precompute_rope_cos_sin(D, L, device=dev)
-    us = avg_us(lambda: sa.sp2norm_rope_flash_attention(q, k, v, cos, sin), iters)
+    us = med(lambda: sa.sp2norm_rope_flash_attention(q, k, v, cos, sin))
     fl = attn_flops(B, H, L, D)
     out["rope_attention"] = {"shape": [B, H, L, D], "us": round(us, 1), "tflops": round(fl / us / 1e6, 1),
                              "frac_bf16_peak": round(fl / us / 1e6 / BF16_PEAK_TFLOPS, 4),
                              "note": "includes the K rotation (read + write of K)"}
     d_model = H * D
     w_o = (torch.randn(H, D, d_model, generator=gen, device=dev) / math.sqrt(H * D)).to(torch.bfloat16)
-    us = avg_us(lambda: sa.sp2norm_rope_flash_attention_proj(q, k, v, w_o, cos, sin), iters)
+    us = med(lambda: sa.sp2norm_rope_flash_attention_proj(q, k, v, w_o, cos, sin))
     fl_proj = 2 * B * L * (H * D) * d_model
     out["rope_attention_proj"] = {"shape": [B, H, L, D], "d_model": d_model, "us": round(us, 1),
                                   "tflops": round((fl + fl_proj) / us / 1e6, 1),
@@ -307,7 +371,7 @@ def bench_next_rows(torch, iters):
     Bn, Hn, Ln = 4, 16, 4096
     x = (torch.randn(Bn, Hn, Ln, Ln, generator=gen, device=dev) / math.sqrt(128)).to(torch.bfloat16)
     y = torch.empty_like(x)
-    us = avg_us(lambda: sa.softmax_causal_triton_out(y, x), iters)
+    us = med(lambda: sa.softmax_causal_triton_out(y, x))
     nb = Bn * Hn * 2 * (tri(Ln) + Ln * Ln)
     out["softmax_causal_bf16"] = {"shape": [Bn, Hn, Ln, Ln], "us": round(us, 1), "GBs": round(nb / us / 1e3, 1),
                                   "frac_hbm_peak": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)}
@@ -315,7 +379,7 @@ def bench_next_rows(torch, iters):
     torch.cuda.empty_cache()
     xr = torch.randn(Bn * Hn * Ln, Ln, generator=gen, device=dev)
     yr = torch.empty_like(xr)
-    us = avg_us(lambda: sa.softmax_triton_out(yr, xr), iters)
+    us = med(lambda: sa.softmax_triton_out(yr, xr))
     nb = 2 * xr.numel() * 4
     out["softmax_rowwise_fp32"] = {"shape": list(xr.shape), "us": round(us, 1), "GBs": round(nb / us / 1e3, 1),
                                    "frac_hbm_peak": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)}
@@ -341,7 +405,7 @@ def bench_next_rows(torch, iters):
     for n_new in (1, n_max):
         kn = torch.randn(Bp, Hkv, n_new, D, generator=gen, device=dev).to(torch.bfloat16)
         vn = torch.randn(Bp, Hkv, n_new, D, generator=gen, device=dev).to(torch.bfloat16)
-        us = avg_us(lambda: sa.sp2norm_paged_kv_append(kc, vc, kn, vn, table_d, lens_d, block_size=P), iters)
+        us = med(lambda: sa.sp2norm_paged_kv_append(kc, vc, kn, vn, table_d, lens_d, block_size=P))
         nb = 2 * 2 * kn.numel() * 2  # K and V rows, read once and written once
         out[f"paged_append_{n_new}"] = {"seqs": Bp, "n_new": n_new, "us": round(us, 2),
                                         "GBs": round(nb / us / 1e3, 1),
@@ -352,10 +416,11 @@ def bench_next_rows(torch, iters):
     return out
 
 
-def bench_norm_sizes(torch, sa, iters):
+def bench_norm_sizes(torch, sa):
     """Config 2 at the other lengths (causal bf16, L = 1024, 2048), its
     row-wise fp32 variant (x, dy fp32 [64 L, L], L = 1024, 2048, 4096) and
-    config 1's shape on the GPU: kernel times from HIP events."""
+    config 1's shape on the GPU: per-kernel medians (caches flushed before
+    every launch, so the 128 MiB inputs at L = 1024 come from HBM)."""
     from smooth_attn import FamilyConfig, kernels
 
     fam = FamilyConfig()
@@ -366,10 +431,9 @@ def bench_norm_sizes(torch, sa, iters):
         x = (torch.randn(4, 16, L, L, generator=gen, device=dev) / math.sqrt(128)).to(torch.bfloat16)
         dy = torch.randn(4, 16, L, L, generator=gen, device=dev).to(torch.bfloat16)
         y = torch.empty_like(x)
-        f = time_events(torch, lambda: sa.softplus_norm_causal_triton_out(y, x, family=fam), iters)
-        b = time_events(torch, lambda: kernels._softplus_norm_causal_backward(x, dy, fam), iters)
+        fus = time_kernel(torch, lambda: sa.softplus_norm_causal_triton_out(y, x, family=fam))["median"]
+        bus = time_kernel(torch, lambda: kernels._softplus_norm_causal_backward(x, dy, fam))["median"]
         fb, bb = norm_bytes(4, 16, L)
-        fus, bus = 1e3 * sum(f) / len(f), 1e3 * sum(b) / len(b)
         out["causal_bf16"].append({"L": L, "fwd_us": round(fus, 2), "bwd_us": round(bus, 2),
                                    "GBs": round((fb + bb) / ((fus + bus) * 1e-6) / 1e9, 1),
                                    "frac_hbm_peak": round((fb + bb) / ((fus + bus) * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
@@ -380,10 +444,9 @@ def bench_norm_sizes(torch, sa, iters):
         dy = torch.randn(64 * L, L, generator=gen, device=dev)
         y = torch.empty_like(x)
         dx = torch.empty_like(x)
-        f = time_events(torch, lambda: sa.softplus_norm_triton_out(y, x, family=fam), iters)
-        b = time_events(torch, lambda: kernels._norm_bwd_2d(x, dy, dx, fam, causal=False), iters)
+        fus = time_kernel(torch, lambda: sa.softplus_norm_triton_out(y, x, family=fam))["median"]
+        bus = time_kernel(torch, lambda: kernels._norm_bwd_2d(x, dy, dx, fam, causal=False))["median"]
         fb, bb = 64 * 8 * L * L, 64 * 12 * L * L
-        fus, bus = 1e3 * sum(f) / len(f), 1e3 * sum(b) / len(b)
         out["rowwise_fp32"].append({"L": L, "fwd_us": round(fus, 2), "bwd_us": round(bus, 2),
                                     "GBs": round((fb + bb) / ((fus + bus) * 1e-6) / 1e9, 1),
                                     "frac_hbm_peak": round((fb + bb) / ((fus + bus) * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
@@ -392,42 +455,69 @@ def bench_norm_sizes(torch, sa, iters):
     gen = torch.Generator(device=dev).manual_seed(1)
     x1 = torch.randn(2, 8, 512, 512, generator=gen, device=dev).to(torch.bfloat16)
     y1 = torch.empty_like(x1)
-    t1 = time_events(torch, lambda: sa.softplus_norm_causal_triton_out(y1, x1, family=fam), iters)
+    us1 = time_kernel(torch, lambda: sa.softplus_norm_causal_triton_out(y1, x1, family=fam))["median"]
     b1 = 16 * (2 * tri(512) + 2 * 512 * 512)
-    us1 = 1e3 * sum(t1) / len(t1)
     out["config1_gpu_fwd"] = {"shape": [2, 8, 512, 512], "us": round(us1, 2), "bytes": b1,
                               "GBs": round(b1 / (us1 * 1e-6) / 1e9, 1)}
     return out
 
 
+# ---------------------------------------------------------------------------
+# CPU baselines: the reference's eager CPU path, restated in oracle/ (fp32
+# torch), on the host cores of the GPU box.
+# ---------------------------------------------------------------------------
+def cpu_threads(torch):
+    """Threads for the CPU legs: the cores this process may run on
+    (sched_getaffinity), capped by OMP_NUM_THREADS when the environment sets
+    it (the GPU box grants one GPU's job 16 threads and sets it so).
+    Returns the thread count used and a description of the host."""
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = os.cpu_count() or 1
+    n = affinity
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    torch.set_num_threads(n)
+    return n, {"os_cpu_count": os.cpu_count(), "affinity_cpus": affinity, "omp_num_threads": env,
+               "torch_threads": torch.get_num_threads(), "cpu_model": cpu_model()}
+
+
+def _median_wall(fn, budget_s, max_runs=5):
+    """Median wall time (s) of fn after one warm-up run: at most max_runs
+    runs, fewer when the budget is spent (at least one)."""
+    fn()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < max_runs and (not times or time.perf_counter() - t_start < budget_s):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
 def cpu_config1(torch, budget_s=10.0):
     """Config 1: the reference's CPU eager forward at full shape
-    ([2,8,512,512] bf16), the oracle restatement, median of <= 7 runs."""
+    ([2,8,512,512] bf16), the oracle restatement."""
     from oracle import eager
 
     x = torch.randn(2, 8, 512, 512, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
-    eager.softplus_norm_causal_cpu_path(x)
-    times = []
-    t_start = time.perf_counter()
-    while len(times) < 7 and (time.perf_counter() - t_start) < budget_s:
-        t0 = time.perf_counter()
-        eager.softplus_norm_causal_cpu_path(x)
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    med = times[len(times) // 2]
+    med, n = _median_wall(lambda: eager.softplus_norm_causal_cpu_path(x), budget_s, max_runs=7)
     b1 = 16 * (2 * tri(512) + 2 * 512 * 512)
-    return {"shape": [2, 8, 512, 512], "ms": round(med * 1e3, 3), "GBs": round(b1 / med / 1e9, 3),
+    return {"shape": [2, 8, 512, 512], "ms": round(med * 1e3, 3), "GBs": round(b1 / med / 1e9, 3), "runs": n,
             "threads": torch.get_num_threads()}
 
 
-def cpu_baseline(torch, sample, budget_s=20.0):
-    """The reference's eager CPU path (oracle restatement, fp32 torch) on one
-    [L, L] matrix of the benchmark input: forward + autograd backward."""
+def cpu_baseline(torch, sample, threads, budget_s=20.0):
+    """Config 2: the reference's eager CPU path (oracle restatement, fp32
+    torch) on one [L, L] matrix of the benchmark input: forward + autograd
+    backward."""
     from oracle import eager
 
     x, dy = sample
     L = x.shape[-1]
-    threads = torch.get_num_threads()
 
     def run():
         xr = x.detach().clone().requires_grad_(True)
@@ -435,25 +525,65 @@ def cpu_baseline(torch, sample, budget_s=20.0):
         y.backward(dy)
         return xr.grad
 
-    run()
-    times = []
-    t_start = time.perf_counter()
-    while len(times) < 5 and (time.perf_counter() - t_start) < budget_s:
-        t0 = time.perf_counter()
-        run()
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    med = times[len(times) // 2]
+    med, n = _median_wall(run, budget_s)
     fwd_b, bwd_b = norm_bytes(1, 1, L)
     return {
-        "value": (fwd_b + bwd_b) / med / 1e9,
+        "value": round((fwd_b + bwd_b) / med / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"1 of 64 [{L},{L}] bf16 matrices of the same input, eager fp32 fwd + autograd bwd, "
-                  f"median of {len(times)} runs ({med * 1e3:.0f} ms each), host '{cpu_model()}', "
-                  f"torch threads {threads}",
+        "sample": f"1 of the 64 [{L},{L}] bf16 matrices of the benchmark input, eager fp32 fwd + autograd bwd, "
+                  f"median of {n} runs ({med * 1e3:.0f} ms each); throughput per matrix, which is the "
+                  f"whole-config rate since the 64 matrices are independent",
     }
+
+
+def cpu_attention(torch, sample, threads, budget_s=20.0):
+    """Config 3 on the CPU: the restated sp2norm_flash_attention_eager
+    (kernels.py:2053-2084) in fp32 on four (b, h) heads of the benchmark's
+    inputs (it runs one head at a time); TFLOP/s over the causal triangle,
+    as for the GPU figure."""
+    from oracle import eager
+
+    q, k, v = (t.float()[None] for t in sample)
+    H, L, D = q.shape[1], q.shape[-2], q.shape[-1]
+    med, n = _median_wall(lambda: eager.flash_attention_eager(q, k, v), budget_s, max_runs=3)
+    fl = attn_flops(1, H, L, D)
+    return {"value": round(fl / med / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"{H} of the 128 (b, h) heads of config 3, eager fp32, median of {n} runs "
+                      f"({med * 1e3:.0f} ms each; the full config would take about {128 / H * med:.0f} s)"}
+
+
+def cpu_fp8(torch, sample, threads, budget_s=20.0):
+    """Config 4 on the CPU: the restated eager attention in fp32 on the
+    dequantised Q/K codes of one query head (and its KV head), bf16 V."""
+    from oracle import eager
+
+    q8, k8, v, qs, ks = sample
+    qd, kd = (q8.float() * qs)[None, None], (k8.float() * ks)[None, None]
+    vd = v.float()[None, None]
+    L, D = qd.shape[-2], qd.shape[-1]
+    med, n = _median_wall(lambda: eager.flash_attention_eager(qd, kd, vd), budget_s, max_runs=3)
+    fl = 2 * 2 * D * tri(L)
+    return {"value": round(fl / med / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"1 of the 64 query heads of config 4 on dequantised fp8 Q/K, eager fp32, median of {n} "
+                      f"runs ({med * 1e3:.0f} ms each; about {64 * med:.0f} s for the full config)"}
+
+
+def cpu_paged(torch, sample, threads, budget_s=30.0):
+    """Config 5 on the CPU: the restated decode reference
+    (tests/test_paged_long_context.py:39-65, oracle.eager.paged_decode_eager)
+    over all 64 sequences, gathering pages through the same block table;
+    GB/s over the config's algorithmic bytes."""
+    from oracle import eager
+
+    q, kc, vc, table, lens = sample
+    kh, vh = kc.cpu(), vc.cpu()
+    med, n = _median_wall(lambda: eager.paged_decode_eager(q, kh, vh, table, lens), budget_s, max_runs=3)
+    nbytes = paged_bytes(lens)
+    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"the whole config (64 sequences, {int(lens.sum())} context tokens), eager fp32 page "
+                      f"gather + decode, median of {n} runs ({med * 1e3:.0f} ms each)"}
 
 
 def copy_calibration(torch, nbytes=1 << 30):
@@ -470,6 +600,34 @@ def copy_calibration(torch, nbytes=1 << 30):
     torch.cuda.empty_cache()
 
 
+def profile_attention(torch, reps=3):
+    """The workload of the attention counter profiles: config 3's forward
+    and backward and config 4's fp8 forward, ``reps`` launches each on the
+    bench's inputs, nothing else timed."""
+    from smooth_attn import kernels
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(3)
+    B, H, L, D = 4, 32, 4096, 128
+    q, k, v, do = (torch.randn(B, H, L, D, generator=gen, device=dev).to(torch.bfloat16) for _ in range(4))
+    scale = 1.0 / math.sqrt(D)
+    for _ in range(reps):
+        o, rs = kernels._sp2norm_flash_fwd(q, k, v, scale)
+    for _ in range(reps):
+        kernels._sp2norm_flash_bwd(q, k, v, o, do, rs, scale)
+    del q, k, v, do, o, rs
+    B, Hq, Hkv, L = 2, 32, 8, 8192
+    q = torch.randn(B, Hq, L, D, generator=gen, device=dev).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, L, D, generator=gen, device=dev).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, L, D, generator=gen, device=dev).to(torch.bfloat16)
+    q8, qs = kernels._quantize_to_fp8_device(q)
+    k8, ks = kernels._quantize_to_fp8_device(k)
+    for _ in range(reps):
+        kernels._sp2norm_fp8_flash_fwd(q8, k8, v, qs, ks, None, scale, Hq // Hkv)
+    torch.cuda.synchronize()
+    log(f"bench: profile workload done ({reps} launches each of flash fwd, flash bwd, fp8 fwd)")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -482,6 +640,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run three plain 1 GiB device copies (reference point for HBM counters)")
+    ap.add_argument("--profile-attention", action="store_true",
+                    help="only launch the attention kernels of configs 3 and 4 a few times (counter profiles)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the smooth-attn hot path has no multi-GPU component "
@@ -496,35 +656,50 @@ def main():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(1)
 
+    if args.profile_attention:
+        profile_attention(torch)
+        return
     if args.copy_calibration:
         copy_calibration(torch)
     log("bench: causal norm fwd+bwd [4,16,4096,4096] bf16")
     norm = bench_norm(torch, sa, args.steps, args.warmup)
     log(f"bench: norm {norm['ms_per_step']:.3f} ms/step, fwd {norm['fwd_us']:.1f} us, bwd {norm['bwd_us']:.1f} us")
     attn = fp8 = paged = sizes = nxt = None
+    samples = {}
     if not args.no_extra:
         log("bench: fused attention config 3")
-        attn = bench_attention(torch, sa, max(args.steps, 10))
+        attn, samples["attn"] = bench_attention(torch, sa)
         log(f"bench: attention {attn}")
         log("bench: fp8 attention config 4")
-        fp8 = bench_fp8(torch, max(args.steps, 10))
+        fp8, samples["fp8"] = bench_fp8(torch)
         log(f"bench: fp8 {fp8}")
         log("bench: paged decode config 5")
-        paged = bench_paged(torch, max(args.steps, 20))
+        paged, samples["paged"] = bench_paged(torch)
         log(f"bench: paged {paged}")
         log("bench: config 2 other lengths, row-wise fp32, config 1 shape")
-        sizes = bench_norm_sizes(torch, sa, max(args.steps, 10))
+        sizes = bench_norm_sizes(torch, sa)
         log(f"bench: sizes {sizes}")
         log("bench: RoPE attention, softmax baselines, paged-KV append")
-        nxt = bench_next_rows(torch, max(args.steps, 10))
+        nxt = bench_next_rows(torch)
         log(f"bench: next rows {nxt}")
-    cpu = None
+    cpu = host = None
     if not args.no_cpu:
-        log("bench: cpu baseline")
-        cpu = cpu_baseline(torch, norm["sample"])
-        log(f"bench: cpu {cpu['value']:.3f} GB/s")
+        threads, host = cpu_threads(torch)
+        log(f"bench: cpu baselines on {threads} threads ({host})")
+        cpu = cpu_baseline(torch, norm["sample"], threads)
+        log(f"bench: cpu config 2 {cpu['value']} GB/s")
         if sizes is not None:
             sizes["config1_cpu_eager_fwd"] = cpu_config1(torch)
+        if attn is not None:
+            attn["cpu_baseline"] = cpu_attention(torch, samples["attn"], threads)
+            log(f"bench: cpu config 3 {attn['cpu_baseline']}")
+        if fp8 is not None:
+            fp8["cpu_baseline"] = cpu_fp8(torch, samples["fp8"], threads)
+            log(f"bench: cpu config 4 {fp8['cpu_baseline']}")
+        if paged is not None:
+            paged["cpu_baseline"] = cpu_paged(torch, samples["paged"], threads)
+            log(f"bench: cpu config 5 {paged['cpu_baseline']}")
+        cpu["host"] = host
 
     dominant = "bwd" if norm["bwd_us"] >= norm["fwd_us"] else "fwd"
     achieved = norm[f"{dominant}_gbs"]
@@ -549,6 +724,11 @@ def main():
             "fwd_GBs": round(norm["fwd_gbs"], 1),
             "bwd_GBs": round(norm["bwd_gbs"], 1),
             "frac_hbm_peak_step": round(norm["gbs"] / HBM_PEAK_GBS, 4),
+            "kernel_fwd_us": _rounded(norm["kernel_fwd"]),
+            "kernel_bwd_us": _rounded(norm["kernel_bwd"]),
+            "kernel_fwd_bwd_frac_hbm_peak": round(
+                (norm["fwd_bytes"] + norm["bwd_bytes"]) /
+                ((norm["kernel_fwd"]["median"] + norm["kernel_bwd"]["median"]) * 1e3) / HBM_PEAK_GBS, 4),
             "compute_dtype": "f32",
         },
         "roofline": {
