@@ -2,8 +2,9 @@
  * smooth_attn_amd.h — C ABI of the MI355X (gfx950) smooth-attn hot path.
  *
  * Plain pointers, sizes and element strides; no torch types.  Every entry
- * point is asynchronous on the given HIP stream, allocates nothing, and
- * returns a status:
+ * point is asynchronous on the given HIP stream, allocates nothing (device
+ * memory beyond the arguments is a caller workspace, or for
+ * sa_paged_decode_noalloc a fixed module-scope array), and returns a status:
  *      0            success
  *     < 0           invalid argument (see sa_status_string)
  *     > 0           a hipError_t from the launch
@@ -291,6 +292,38 @@ int sa_paged_decode(const void* q, const void* k_cache, const void* v_cache,
                     int64_t bt_stride, float scale, int dtype,
                     float* workspace, int64_t workspace_bytes,
                     sa_stream_t stream);
+
+/* Device memory sa_paged_decode_noalloc keeps per device for its plan and
+ * partials (64 MiB). */
+#define SA_PAGED_NOALLOC_SCRATCH_BYTES (64LL << 20)
+
+/*
+ * sa_paged_decode without a workspace argument: allocates nothing and takes
+ * no caller memory beyond its inputs and output, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  No counterpart in the reference.  The plan and
+ * the partials live in a module-scope device array of
+ * SA_PAGED_NOALLOC_SCRATCH_BYTES that every device using the library holds
+ * until the process ends; its address is looked up on the first call on a
+ * device.  When sa_paged_decode's partials would not fit, the split is
+ * coarsened (more 32-token tiles per wave, fewer partials); when even two
+ * partials per (sequence, query head) do not fit (B * Hq * 2 * (D + 1) * 4
+ * bytes plus the plan over 64 MiB) it returns SA_ERR_WORKSPACE.  Nothing in
+ * the array needs to start at zero (the plan kernel writes what the other
+ * kernels read).  Calls that overlap on one device (other streams, other
+ * host threads) share the array and race: serialise them.  Arguments and
+ * result as sa_paged_decode.
+ */
+int sa_paged_decode_noalloc(const void* q, const void* k_cache,
+                            const void* v_cache, void* out,
+                            const int32_t* block_table,
+                            const int32_t* context_lens, int B, int Hq,
+                            int Hkv, int D, int page_size, int max_pages,
+                            int n_pages, const int64_t* q_strides,
+                            const int64_t* kv_strides,
+                            const int64_t* vv_strides,
+                            const int64_t* o_strides, int64_t bt_stride,
+                            float scale, int dtype, sa_stream_t stream);
 
 /*
  * Paged-KV cache writer (the step before sa_paged_decode): for sequence b

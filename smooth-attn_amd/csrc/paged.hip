@@ -25,6 +25,8 @@
 // kernel sums the slots in order (squareplus needs no running maximum, so
 // merging is a plain sum) and divides once.
 #include <algorithm>
+#include <atomic>
+#include <mutex>
 
 #include "flash_common.hpp"
 
@@ -378,28 +380,30 @@ int64_t slots_for(int max_pages, int page_size, int per) {
 // partials (fp32).
 int64_t plan_bytes(int B) { return ((static_cast<int64_t>(B) + 2) * 4 + 15) / 16 * 16; }
 
-}  // namespace
-}  // namespace sa
-
-extern "C" int64_t sa_paged_decode_workspace_size(int B, int Hq, int D, int max_pages, int page_size) {
-    if (B <= 0 || Hq <= 0 || D <= 0 || max_pages < 0 || page_size <= 0) return 0;
-    const int64_t slots = static_cast<int64_t>(B) * Hq *
-                          sa::slots_for(max_pages, page_size, sa::split_floor(B, Hq, max_pages, page_size));
-    return sa::plan_bytes(B) + slots * (D + 1) * static_cast<int64_t>(sizeof(float));
+int64_t workspace_bytes_for(int B, int Hq, int D, int max_pages, int page_size, int per) {
+    const int64_t slots = static_cast<int64_t>(B) * Hq * slots_for(max_pages, page_size, per);
+    return plan_bytes(B) + slots * (D + 1) * static_cast<int64_t>(sizeof(float));
 }
 
-extern "C" int sa_paged_decode(const void* q, const void* k_cache, const void* v_cache, void* out,
-                               const int32_t* block_table, const int32_t* context_lens, int B, int Hq, int Hkv,
-                               int D, int page_size, int max_pages, int n_pages, const int64_t* q_strides,
-                               const int64_t* kv_strides, const int64_t* vv_strides, const int64_t* o_strides,
-                               int64_t bt_stride, float scale, int dtype, float* workspace, int64_t workspace_bytes,
-                               sa_stream_t stream) {
-    using namespace sa;
+// The minimum tiles per active wave a launch uses: the workspace is sized
+// for split_floor, and the launch takes the larger split its B * Hkv
+// segments give (so its slots always fit).
+int launch_per(int B, int Hq, int Hkv, int max_pages, int page_size) {
+    return std::max(split_floor(B, Hq, max_pages, page_size),
+                    split_for(static_cast<int64_t>(B) * Hkv, max_pages, page_size));
+}
+
+// Argument checks shared by both decode entry points (0 = launch, 1 =
+// nothing to do, < 0 = status).  max_pages becomes 0 when there are no pages.
+int validate_paged(const void* q, const void* k_cache, const void* v_cache, const void* out,
+                   const int32_t* block_table, const int32_t* context_lens, int B, int Hq, int Hkv, int D,
+                   int page_size, int& max_pages, int n_pages, const int64_t* q_strides,
+                   const int64_t* kv_strides, const int64_t* vv_strides, const int64_t* o_strides, int dtype) {
     if (B < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || max_pages < 0 || n_pages < 0) return SA_ERR_BAD_SHAPE;
     if (Hq / Hkv > 32) return SA_ERR_UNSUPPORTED;  // query heads per KV head fill one 32-wide MFMA column block
     if (page_size != 8 && page_size != 16 && page_size != 32 && page_size != 64) return SA_ERR_UNSUPPORTED;
     if (D != 32 && D != 64 && D != 128) return SA_ERR_UNSUPPORTED;
-    if (B == 0) return 0;
+    if (B == 0) return 1;
     if (n_pages == 0) max_pages = 0;  // no cache: every context is empty
     // The plan keeps token positions, tile counts and their prefix sums over
     // (sequence, KV head) in 32-bit ints.
@@ -407,9 +411,8 @@ extern "C" int sa_paged_decode(const void* q, const void* k_cache, const void* v
     if (max_ctx > INT32_MAX / 2 || static_cast<int64_t>(B) * Hkv * ((max_ctx + kTile - 1) / kTile) > INT32_MAX / 2)
         return SA_ERR_UNSUPPORTED;
     if (!q || !k_cache || !v_cache || !out || !block_table || !context_lens || !q_strides || !kv_strides ||
-        !vv_strides || !o_strides || !workspace)
+        !vv_strides || !o_strides)
         return SA_ERR_NULL_POINTER;
-    if (workspace_bytes < sa_paged_decode_workspace_size(B, Hq, D, max_pages, page_size)) return SA_ERR_WORKSPACE;
     const auto ok16 = [](const int64_t* s, int n) {
         for (int i = 0; i < n - 1; ++i)
             if (s[i] % 8 != 0) return false;
@@ -419,6 +422,16 @@ extern "C" int sa_paged_decode(const void* q, const void* k_cache, const void* v
         !aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache))
         return SA_ERR_BAD_STRIDE;
     if (dtype != SA_BF16 && dtype != SA_F16) return SA_ERR_BAD_DTYPE;
+    return 0;
+}
+
+// Plan, partial and merge launches with the workspace at `ws` (laid out for
+// `per` minimum tiles per wave).
+int run_paged(const void* q, const void* k_cache, const void* v_cache, void* out, const int32_t* block_table,
+              const int32_t* context_lens, int B, int Hq, int Hkv, int D, int page_size, int max_pages,
+              int n_pages, const int64_t* q_strides, const int64_t* kv_strides, const int64_t* vv_strides,
+              const int64_t* o_strides, int64_t bt_stride, float scale, int dtype, float* ws, int per,
+              hipStream_t st) {
     PagedParams prm{};
     prm.q = q;
     prm.k = k_cache;
@@ -426,11 +439,10 @@ extern "C" int sa_paged_decode(const void* q, const void* k_cache, const void* v
     prm.out = static_cast<bf16*>(out);
     prm.table = block_table;
     prm.ctx = context_lens;
-    prm.per = std::max(split_floor(B, Hq, max_pages, page_size),
-                       split_for(static_cast<int64_t>(B) * Hkv, max_pages, page_size));
-    prm.n_slots = static_cast<int>(slots_for(max_pages, page_size, prm.per));
-    prm.plan = reinterpret_cast<int*>(workspace);
-    prm.ws_o = workspace + plan_bytes(B) / 4;
+    prm.per = per;
+    prm.n_slots = static_cast<int>(slots_for(max_pages, page_size, per));
+    prm.plan = reinterpret_cast<int*>(ws);
+    prm.ws_o = ws + plan_bytes(B) / 4;
     prm.ws_s = prm.ws_o + static_cast<int64_t>(B) * Hq * prm.n_slots * D;
     for (int i = 0; i < 4; ++i) {
         prm.qs[i] = q_strides[i];
@@ -448,7 +460,6 @@ extern "C" int sa_paged_decode(const void* q, const void* k_cache, const void* v
     prm.max_pages = max_pages;
     prm.n_pages = n_pages;
     prm.scale = scale;
-    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     if (dtype == SA_BF16) {
         switch (D) {
             case 32: return launch_paged<bf16, 32>(prm, st);
@@ -461,4 +472,99 @@ extern "C" int sa_paged_decode(const void* q, const void* k_cache, const void* v
         case 64: return launch_paged<f16, 64>(prm, st);
         default: return launch_paged<f16, 128>(prm, st);
     }
+}
+
+}  // namespace
+}  // namespace sa
+
+extern "C" int64_t sa_paged_decode_workspace_size(int B, int Hq, int D, int max_pages, int page_size) {
+    if (B <= 0 || Hq <= 0 || D <= 0 || max_pages < 0 || page_size <= 0) return 0;
+    return sa::workspace_bytes_for(B, Hq, D, max_pages, page_size, sa::split_floor(B, Hq, max_pages, page_size));
+}
+
+extern "C" int sa_paged_decode(const void* q, const void* k_cache, const void* v_cache, void* out,
+                               const int32_t* block_table, const int32_t* context_lens, int B, int Hq, int Hkv,
+                               int D, int page_size, int max_pages, int n_pages, const int64_t* q_strides,
+                               const int64_t* kv_strides, const int64_t* vv_strides, const int64_t* o_strides,
+                               int64_t bt_stride, float scale, int dtype, float* workspace, int64_t workspace_bytes,
+                               sa_stream_t stream) {
+    using namespace sa;
+    const int chk = validate_paged(q, k_cache, v_cache, out, block_table, context_lens, B, Hq, Hkv, D, page_size,
+                                   max_pages, n_pages, q_strides, kv_strides, vv_strides, o_strides, dtype);
+    if (chk != 0) return chk > 0 ? 0 : chk;
+    if (!workspace) return SA_ERR_NULL_POINTER;
+    if (workspace_bytes < sa_paged_decode_workspace_size(B, Hq, D, max_pages, page_size)) return SA_ERR_WORKSPACE;
+    return run_paged(q, k_cache, v_cache, out, block_table, context_lens, B, Hq, Hkv, D, page_size, max_pages,
+                     n_pages, q_strides, kv_strides, vv_strides, o_strides, bt_stride, scale, dtype, workspace,
+                     launch_per(B, Hq, Hkv, max_pages, page_size), reinterpret_cast<hipStream_t>(stream));
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free decode.  The plan and partials live in `scratch`, a
+// module-scope device array: each device that loads this library holds its
+// own copy (SA_PAGED_NOALLOC_SCRATCH_BYTES) until the process ends.  In host
+// code the array's name is only a host-side stand-in, so its device address
+// is looked up once per device with hipGetSymbolAddress (with that device
+// current) and that address is what the kernels receive.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) float scratch[SA_PAGED_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
+namespace sa {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::atomic<float*> g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// The current device's copy of `scratch` (0 = ok, else a status).
+int scratch_of_current_device(float** out) {
+    int dev = -1;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return static_cast<int>(e);
+    if (dev < 0 || dev >= kMaxDevices) return SA_ERR_UNSUPPORTED;
+    float* p = g_scratch[dev].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        p = g_scratch[dev].load(std::memory_order_relaxed);
+        if (p == nullptr) {
+            void* addr = nullptr;
+            const hipError_t es = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+            if (es != hipSuccess) return static_cast<int>(es);
+            if (addr == nullptr) return SA_ERR_WORKSPACE;
+            p = static_cast<float*>(addr);
+            g_scratch[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return 0;
+}
+
+}  // namespace
+}  // namespace sa
+
+extern "C" int sa_paged_decode_noalloc(const void* q, const void* k_cache, const void* v_cache, void* out,
+                                       const int32_t* block_table, const int32_t* context_lens, int B, int Hq,
+                                       int Hkv, int D, int page_size, int max_pages, int n_pages,
+                                       const int64_t* q_strides, const int64_t* kv_strides,
+                                       const int64_t* vv_strides, const int64_t* o_strides, int64_t bt_stride,
+                                       float scale, int dtype, sa_stream_t stream) {
+    using namespace sa;
+    const int chk = validate_paged(q, k_cache, v_cache, out, block_table, context_lens, B, Hq, Hkv, D, page_size,
+                                   max_pages, n_pages, q_strides, kv_strides, vv_strides, o_strides, dtype);
+    if (chk != 0) return chk > 0 ? 0 : chk;
+    // The workspace launch's split, or a coarser one (more tiles per wave,
+    // fewer partial slots) when its partials would not fit the scratch: the
+    // plan honours any per, which only caps how many waves share the work.
+    int per = launch_per(B, Hq, Hkv, max_pages, page_size);
+    constexpr int64_t cap = SA_PAGED_NOALLOC_SCRATCH_BYTES;
+    while (workspace_bytes_for(B, Hq, D, max_pages, page_size, per) > cap &&
+           slots_for(max_pages, page_size, per) > 2)
+        per *= 2;
+    if (workspace_bytes_for(B, Hq, D, max_pages, page_size, per) > cap) return SA_ERR_WORKSPACE;
+    float* ws = nullptr;
+    const int sst = scratch_of_current_device(&ws);
+    if (sst != 0) return sst;
+    return run_paged(q, k_cache, v_cache, out, block_table, context_lens, B, Hq, Hkv, D, page_size, max_pages,
+                     n_pages, q_strides, kv_strides, vv_strides, o_strides, bt_stride, scale, dtype, ws, per,
+                     reinterpret_cast<hipStream_t>(stream));
 }

@@ -7,17 +7,18 @@ build command.
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from ctypes import POINTER, c_float, c_int, c_int32, c_int64, c_void_p
 from pathlib import Path
-
-import os
 
 # SMOOTH_ATTN_LIB selects an alternate build of the same library (tuning runs).
 LIB_PATH = Path(os.environ.get("SMOOTH_ATTN_LIB") or Path(__file__).resolve().parent / "libsmooth_attn_amd.so")
 
 # Element-type codes (SA_F32 ... in the header).
 SA_F32, SA_F16, SA_BF16, SA_FP8_E4M3FN = 0, 1, 2, 3
+# SA_PAGED_NOALLOC_SCRATCH_BYTES: the fixed scratch of sa_paged_decode_noalloc.
+PAGED_NOALLOC_SCRATCH_BYTES = 64 << 20
 
 _I64P = POINTER(c_int64)
 
@@ -62,6 +63,9 @@ SIGNATURES = {
     "sa_paged_decode": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
                                 c_int, c_int, c_int, c_int, c_int, _I64P, _I64P, _I64P, _I64P, c_int64, c_float,
                                 c_int, c_void_p, c_int64, c_void_p]),
+    "sa_paged_decode_noalloc": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
+                                        c_int, c_int, c_int, c_int, c_int, _I64P, _I64P, _I64P, _I64P, c_int64,
+                                        c_float, c_int, c_void_p]),
     "sa_paged_kv_append": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
                                    c_int, c_int, c_int, c_int, c_int, _I64P, _I64P, _I64P, c_int64, c_int,
                                    c_void_p]),

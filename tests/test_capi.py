@@ -140,3 +140,26 @@ def test_paged_workspace_sizes():
             continue
         want, m, slots = expect(B, Hq, D, mp, P)
         assert (m, slots) == ms and got == want
+
+
+def test_paged_decode_noalloc_refuses_what_its_scratch_cannot_hold():
+    # two partials per (sequence, query head) are the least any split needs:
+    # 4096 x 32 x 2 x 129 fp32 = 135 MB > SA_PAGED_NOALLOC_SCRATCH_BYTES, so
+    # the call returns SA_ERR_WORKSPACE before any HIP call (dummy pointers)
+    lib = _lib.load()
+    q = (ctypes.c_int64 * 4)(32 * 128, 128, 128, 1)
+    kv = (ctypes.c_int64 * 4)(8 * 16 * 128, 16 * 128, 128, 1)
+    o = (ctypes.c_int64 * 3)(32 * 128, 128, 1)
+    d = ctypes.c_void_p(256)
+    args = (d, d, d, d, d, d, 4096, 32, 8, 128, 16, 4, 1 << 14, q, kv, kv, o, 4, 0.1, _lib.SA_BF16, None)
+    assert lib.sa_paged_decode_noalloc(*args) == -7
+    assert _lib.PAGED_NOALLOC_SCRATCH_BYTES == 64 << 20
+    header = HEADER.read_text()
+    assert "#define SA_PAGED_NOALLOC_SCRATCH_BYTES (64LL << 20)" in header
+    # argument errors as the workspace entry point
+    bad = list(args)
+    bad[10] = 12  # page size not a power of two in {8, 16, 32, 64}
+    assert lib.sa_paged_decode_noalloc(*bad) == -6
+    bad = list(args)
+    bad[0] = None
+    assert lib.sa_paged_decode_noalloc(*bad) == -1
