@@ -1,16 +1,26 @@
-"""Benchmark harness and command line of smooth-attn — reference
-kernels.py:2841-3132 (suites, backward validation, reports, argparse, main;
-console script ``smooth-attn = smooth_attn.kernels:main``, pyproject.toml:36-37).
+"""Benchmark command line of smooth-attn on MI355X: ``python -m smooth_attn``.
 
-Every timed column runs a gfx950 HIP kernel of this package except the
-``F.softmax`` / eager columns, which are torch's own GPU kernels (the
-comparison the reference makes).  Timing: one HIP event pair per launch,
-median (kernels.py:322-336).  Run as ``python -m smooth_attn [args]``.
+The flags and their defaults, and the three benchmark functions with their
+signatures and result types, are the reference's interface
+(kernels.py:2841-2967, :3061-3128; console script ``smooth-attn``,
+pyproject.toml:36-37), so scripts written against it keep working.
+
+What the harness measures and prints is this package's own.  Each case is a
+small table of *columns*: the package's HIP launches (writing into a
+preallocated output) and torch's own kernel for the same operation.  Every
+column is timed the same way (median of per-launch HIP event pairs,
+``kernels.bench``), and every HIP column is reported against the bound these
+kernels are built for: algorithmic HBM bytes per launch (read x once, only
+its causal triangle for causal rows; write the whole output once), the
+GB/s that gives, and the fraction of MI355X's 8 TB/s HBM peak.  The torch
+column gives the speed ratio, and the causal table adds each HIP output's
+error against fp32 eager and whether its rows sum to one.
 """
 from __future__ import annotations
 
 import argparse
 import math
+from dataclasses import dataclass
 
 import torch
 import torch.nn.functional as F
@@ -22,197 +32,279 @@ from .kernels import (
     FamilyConfig,
     RowwiseBenchmarkResult,
     bench,
-    bench_out,
     softmax_causal_eager,
+    softmax_causal_triton,
     softmax_causal_triton_out,
     softmax_triton_out,
     softplus_norm_causal,
     softplus_norm_causal_eager,
+    softplus_norm_causal_triton,
     softplus_norm_causal_triton_out,
     softplus_norm_triton_out,
 )
 
-# kernels.py:30-55
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+
+# The reference's default sweeps (kernels.py:30-56): the row-wise shapes and
+# the causal lengths.
 DEFAULT_ROWWISE_SHAPES = (
     (256, 256), (256, 512), (256, 1024), (1024, 256), (1024, 512), (1024, 1024),
     (4096, 128), (4096, 256), (4096, 512), (4096, 1024), (8192, 256), (8192, 512),
     (8192, 1024), (16384, 128), (16384, 256), (16384, 512), (32768, 256), (32768, 512),
     (32, 512), (32, 1024), (32, 2048), (128, 512), (128, 1024), (128, 2048),
 )
-# kernels.py:56
 DEFAULT_CAUSAL_LENGTHS = (128, 256, 512, 1024)
+
+# Row sums of a normalised output are 1 up to the rounding of its dtype (the
+# bound the result fields *_sums_ok report); gradients are compared with
+# allclose at these (atol, rtol).
+_SUM_ATOL = {torch.float32: 1e-4, torch.float16: 5e-3, torch.bfloat16: 5e-3}
+_GRAD_TOL = {torch.float32: (1e-4, 1e-3), torch.float16: (5e-3, 5e-2), torch.bfloat16: (5e-3, 5e-2)}
 
 
 def _current_device_index():
-    """kernels.py:123-126."""
     if not torch.cuda.is_available():
         raise RuntimeError("a ROCm GPU is required for these kernels")
     return torch.cuda.current_device()
 
 
 def _dtype_label(dtype):
-    """kernels.py:143-147."""
-    for label, candidate in SUPPORTED_DTYPES.items():
-        if candidate == dtype:
-            return label
-    return str(dtype).replace("torch.", "")
+    """fp32 / fp16 / bf16, or torch's own name for anything else."""
+    names = {v: k for k, v in SUPPORTED_DTYPES.items()}
+    return names.get(dtype, str(dtype).replace("torch.", ""))
 
 
 def _parse_dtype_list(text):
-    """kernels.py:150-157: comma-separated fp32/fp16/bf16."""
+    """Comma-separated dtype labels (case and spaces ignored)."""
     labels = [tok.strip().lower() for tok in text.split(",") if tok.strip()]
     if not labels:
         raise ValueError("at least one dtype must be provided")
-    out = []
-    for label in labels:
-        if label not in SUPPORTED_DTYPES:
-            raise ValueError(f"unsupported dtype label: {label}")
-        out.append(SUPPORTED_DTYPES[label])
-    return out
+    unknown = [lab for lab in labels if lab not in SUPPORTED_DTYPES]
+    if unknown:
+        raise ValueError(f"unsupported dtype label: {unknown[0]}")
+    return [SUPPORTED_DTYPES[lab] for lab in labels]
 
 
 def _parse_int_list(text):
-    """kernels.py:160-164."""
-    vals = [tok.strip() for tok in text.split(",") if tok.strip()]
+    vals = [int(tok) for tok in text.split(",") if tok.strip()]
     if not vals:
         raise ValueError("at least one integer must be provided")
-    return [int(v) for v in vals]
+    return vals
+
+
+# ---------------------------------------------------------------------------
+# Byte model and columns
+# ---------------------------------------------------------------------------
+def rowwise_bytes(rows, cols, dtype):
+    """Algorithmic HBM bytes of one row-wise launch: read x, write y."""
+    return 2 * rows * cols * torch.finfo(dtype).bits // 8
+
+
+def causal_bytes(n_matrices, seq_len, dtype):
+    """Algorithmic HBM bytes of one causal launch over n [L, L] matrices:
+    read the causal triangle of x, write the whole output (zeros included)."""
+    elem = torch.finfo(dtype).bits // 8
+    return n_matrices * elem * (seq_len * (seq_len + 1) // 2 + seq_len * seq_len)
+
+
+@dataclass
+class _Column:
+    """One timed launch of a case; ``nbytes`` is set for the HIP columns
+    (reported against the HBM roofline) and None for torch's."""
+
+    label: str
+    launch: object
+    nbytes: int | None = None
+    us: float = float("nan")
+
+    def gbs(self):
+        return self.nbytes / self.us / 1e3
+
+    def cell(self):
+        if self.nbytes is None:
+            return f"{self.us:9.1f}"
+        return f"{self.us:9.1f} {self.gbs():7.0f} {100 * self.gbs() / HBM_PEAK_GBS:5.1f}%"
+
+
+def _time_columns(columns, warmup, iters):
+    for col in columns:
+        col.us = bench(col.launch, warmup=warmup, iters=iters)
+    return {col.label: col for col in columns}
+
+
+# ---------------------------------------------------------------------------
+# Suites (signatures and result types of kernels.py:2841-2967)
+# ---------------------------------------------------------------------------
+_LAST_COLUMNS = {}  # (suite, index) -> timed columns, for the reports
 
 
 def benchmark_rowwise_suite(family, shapes=None, warmup=50, iters=200):
-    """F.softmax vs the HIP softmax vs the HIP family norm on fp32 rows —
-    kernels.py:2841-2867."""
+    """fp32 rows: torch F.softmax, the HIP softmax and the HIP family
+    normalisation, each into its own buffer (RowwiseBenchmarkResult per
+    shape, times in microseconds)."""
     results = []
-    for rows, cols in tuple(shapes or DEFAULT_ROWWISE_SHAPES):
+    for i, (rows, cols) in enumerate(tuple(shapes or DEFAULT_ROWWISE_SHAPES)):
         x = torch.randn(rows, cols, device="cuda")
-        out_sm, out_fam = torch.empty_like(x), torch.empty_like(x)
-        t_torch = bench(lambda z: F.softmax(z, dim=-1), x, warmup=warmup, iters=iters)
-        t_sm = bench_out(softmax_triton_out, out_sm, x, warmup=warmup, iters=iters)
-        t_fam = bench_out(lambda o, z: softplus_norm_triton_out(o, z, family=family), out_fam, x,
-                          warmup=warmup, iters=iters)
-        results.append(RowwiseBenchmarkResult(shape=(rows, cols), torch_softmax_us=t_torch,
-                                              triton_softmax_us=t_sm, family_us=t_fam))
+        y = torch.empty_like(x)
+        nb = rowwise_bytes(rows, cols, x.dtype)
+        cols_t = _time_columns([
+            _Column("torch", lambda: F.softmax(x, dim=-1)),
+            _Column("softmax", lambda: softmax_triton_out(y, x), nb),
+            _Column("family", lambda: softplus_norm_triton_out(y, x, family=family), nb),
+        ], warmup, iters)
+        _LAST_COLUMNS[("rowwise", i)] = cols_t
+        results.append(RowwiseBenchmarkResult(shape=(rows, cols), torch_softmax_us=cols_t["torch"].us,
+                                              triton_softmax_us=cols_t["softmax"].us,
+                                              family_us=cols_t["family"].us))
     return results
 
 
+def _rows_sum_to_one(y, dtype):
+    return bool(((y.float().sum(-1) - 1.0).abs() <= _SUM_ATOL[dtype]).all())
+
+
 def benchmark_causal_suite(family, dtypes, lengths, batch=2, heads=8, warmup=50, iters=200):
-    """Causal [batch, heads, T, T]: eager torch softmax vs the HIP causal
-    softmax vs the HIP causal family norm, with errors against fp32 eager and
-    row-sum checks — kernels.py:2870-2932."""
+    """Causal [batch, heads, T, T] scores: torch's eager causal softmax, the
+    HIP causal softmax and the HIP causal family normalisation.  Accuracy
+    (max |HIP - fp32 eager|, rows summing to one) and the launch metadata
+    come from one untimed call of each HIP entry point."""
     results = []
     for dtype in dtypes:
         for seq_len in lengths:
             x = torch.randn(batch, heads, seq_len, seq_len, device="cuda", dtype=dtype)
-            ref_sm = softmax_causal_eager(x.float())
-            ref_fam = softplus_norm_causal_eager(x.float(), family=family)
-            out_sm, out_fam = torch.empty_like(x), torch.empty_like(x)
-            our_sm, sm_meta = softmax_causal_triton_out(out_sm, x, return_meta=True)
-            our_fam, fam_meta = softplus_norm_causal_triton_out(out_fam, x, family=family, return_meta=True)
-            atol = 1e-4 if dtype == torch.float32 else 5e-3
-            ones = torch.ones(batch, heads, seq_len, device=x.device)
-            t_torch = bench(softmax_causal_eager, x, warmup=warmup, iters=iters)
-            t_sm = bench_out(softmax_causal_triton_out, out_sm, x, warmup=warmup, iters=iters)
-            t_fam = bench_out(lambda o, z: softplus_norm_causal_triton_out(o, z, family=family), out_fam, x,
-                              warmup=warmup, iters=iters)
+            sm, sm_meta = softmax_causal_triton(x, return_meta=True)
+            fam, fam_meta = softplus_norm_causal_triton(x, family=family, return_meta=True)
+            sm_err = float((sm.float() - softmax_causal_eager(x.float())).abs().max())
+            fam_err = float((fam.float() - softplus_norm_causal_eager(x.float(), family=family)).abs().max())
+            sums = (_rows_sum_to_one(sm, dtype), _rows_sum_to_one(fam, dtype))
+            del sm, fam
+            y = torch.empty_like(x)
+            nb = causal_bytes(batch * heads, seq_len, dtype)
+            cols_t = _time_columns([
+                _Column("torch", lambda: softmax_causal_eager(x)),
+                _Column("softmax", lambda: softmax_causal_triton_out(y, x), nb),
+                _Column("family", lambda: softplus_norm_causal_triton_out(y, x, family=family), nb),
+            ], warmup, iters)
+            _LAST_COLUMNS[("causal", len(results))] = cols_t
             results.append(CausalBenchmarkResult(
                 dtype=dtype, batch=batch, heads=heads, seq_len=seq_len,
-                torch_softmax_us=t_torch, triton_softmax_us=t_sm, family_us=t_fam,
-                softmax_err=float((ref_sm - our_sm.float()).abs().max()),
-                family_err=float((ref_fam - our_fam.float()).abs().max()),
-                softmax_sums_ok=bool(torch.allclose(our_sm.float().sum(-1), ones, atol=atol)),
-                family_sums_ok=bool(torch.allclose(our_fam.float().sum(-1), ones, atol=atol)),
-                softmax_meta=sm_meta, family_meta=fam_meta,
-            ))
+                torch_softmax_us=cols_t["torch"].us, triton_softmax_us=cols_t["softmax"].us,
+                family_us=cols_t["family"].us, softmax_err=sm_err, family_err=fam_err,
+                softmax_sums_ok=sums[0], family_sums_ok=sums[1], softmax_meta=sm_meta, family_meta=fam_meta))
     return results
 
 
 def validate_causal_backward(family, dtypes, seq_len=128, batch=2, heads=4):
-    """Fused causal backward vs autograd of the fp32 eager forward —
-    kernels.py:2935-2967."""
-    results = []
+    """The fused causal backward (through the autograd entry point) against
+    autograd of the fp32 eager forward, for the same upstream gradient: a
+    dict per dtype with ``dtype``, ``max_abs_grad_err`` and ``grad_close``."""
+    out = []
     for dtype in dtypes:
-        x = torch.randn(batch, heads, seq_len, seq_len, device="cuda", dtype=dtype, requires_grad=True)
-        up = torch.randn(batch, heads, seq_len, seq_len, device="cuda", dtype=torch.float32)
-        (softplus_norm_causal(x, family=family, implementation="triton").float() * up).sum().backward()
-        g_hip = x.grad.detach().clone()
-        x_ref = x.detach().clone().requires_grad_(True)
-        (softplus_norm_causal_eager(x_ref.float(), family=family) * up).sum().backward()
-        g_ref = x_ref.grad.detach()
-        fp32 = dtype == torch.float32
-        results.append({
-            "dtype": dtype,
-            "max_abs_grad_err": float((g_hip.float() - g_ref.float()).abs().max()),
-            "grad_close": bool(torch.allclose(g_hip.float(), g_ref.float(), atol=1e-4 if fp32 else 5e-3,
-                                              rtol=1e-3 if fp32 else 5e-2)),
-        })
-    return results
+        x = torch.randn(batch, heads, seq_len, seq_len, device="cuda", dtype=dtype)
+        upstream = torch.randn(batch, heads, seq_len, seq_len, device="cuda")
+        grads = []
+        for fwd in (lambda t: softplus_norm_causal(t, family=family, implementation="triton").float(),
+                    lambda t: softplus_norm_causal_eager(t.float(), family=family)):
+            leaf = x.detach().clone().requires_grad_(True)
+            (fwd(leaf) * upstream).sum().backward()
+            grads.append(leaf.grad.float())
+        atol, rtol = _GRAD_TOL[dtype]
+        out.append({"dtype": dtype, "max_abs_grad_err": float((grads[0] - grads[1]).abs().max()),
+                    "grad_close": bool(torch.allclose(grads[0], grads[1], atol=atol, rtol=rtol))})
+    return out
 
 
-def _geo_mean(values):
-    return math.exp(sum(math.log(v) for v in values) / len(values))
+# ---------------------------------------------------------------------------
+# Reports
+# ---------------------------------------------------------------------------
+def _geomean(values):
+    return math.exp(sum(map(math.log, values)) / len(values)) if values else float("nan")
 
 
-def _print_header(title):
-    print("=" * 80)
-    print(title)
-    print("=" * 80)
+def _kernel_label(meta):
+    """The HIP kernel a launch ran: element, one wave per row, or split over
+    several waves per row."""
+    kind = meta.get("kernel") or "-"
+    return f"{kind} x{meta.get('waves_per_row', 1)}"
 
 
-def _print_launch_meta(label, meta):
-    """kernels.py:2970-2980; every meta of this package carries the launch
-    keys, so the reference's KeyError on tiered meta cannot occur."""
-    line = (f"  {label}: BLOCK={meta['block_size']} warps={meta['num_warps']} "
-            f"stages={meta['num_stages']} progs={meta['num_programs']}")
-    if "variant" in meta:
-        line += f" variant={meta['variant']}"
-    print(line)
+_HIP_HEAD = f"{'us':>9s} {'GB/s':>7s} {'%HBM':>6s}"
 
 
+def report_rowwise(results):
+    """One line per shape: torch F.softmax time, then each HIP launch as
+    time, algorithmic GB/s and fraction of the HBM peak; then how the
+    squareplus family compares with F.softmax over the sweep."""
+    print("\nrow-wise fp32 (read x + write y per launch)")
+    print(f"  {'rows x cols':>13s} | {'torch us':>9s} | softmax {_HIP_HEAD} | family  {_HIP_HEAD} | vs torch")
+    speedups = []
+    for i, row in enumerate(results):
+        cols = _LAST_COLUMNS.get(("rowwise", i))
+        if cols is None:  # results not produced by this process's suite: times only
+            cols = {"torch": _Column("torch", None, None, row.torch_softmax_us),
+                    "softmax": _Column("softmax", None, rowwise_bytes(*row.shape, torch.float32),
+                                       row.triton_softmax_us),
+                    "family": _Column("family", None, rowwise_bytes(*row.shape, torch.float32), row.family_us)}
+        speedups.append(row.torch_softmax_us / row.family_us)
+        shape = f"{row.shape[0]} x {row.shape[1]}"
+        print(f"  {shape:>13s} | {cols['torch'].cell()} | {cols['softmax'].cell()} | "
+              f"{cols['family'].cell()} | {speedups[-1]:5.2f}x")
+    print(f"  squareplus family vs torch softmax: geometric mean {_geomean(speedups):.2f}x "
+          f"(range {min(speedups):.2f}x .. {max(speedups):.2f}x)")
+
+
+def report_causal(results, family):
+    """Per dtype: one line per length with the torch time, each HIP launch's
+    time / GB/s / fraction of the HBM peak, the kernel it ran, its max error
+    against fp32 eager and whether its rows sum to one."""
+    print(f"\ncausal [B, H, T, T] (read the causal triangle + write all of y per launch); {family.label}")
+    by_dtype = {}
+    for i, row in enumerate(results):
+        by_dtype.setdefault(_dtype_label(row.dtype), []).append((i, row))
+    for label, rows in by_dtype.items():
+        print(f"  {label}: {'B x H x T':>12s} | {'torch us':>9s} | softmax {_HIP_HEAD} | family  {_HIP_HEAD} | "
+              f"{'kernel':>8s} | {'sm err':>8s} {'fam err':>8s} | sums ok | vs torch")
+        speedups, fracs = [], []
+        for i, row in rows:
+            cols = _LAST_COLUMNS.get(("causal", i))
+            if cols is None:
+                nb = causal_bytes(row.batch * row.heads, row.seq_len, row.dtype)
+                cols = {"torch": _Column("torch", None, None, row.torch_softmax_us),
+                        "softmax": _Column("softmax", None, nb, row.triton_softmax_us),
+                        "family": _Column("family", None, nb, row.family_us)}
+            speedups.append(row.torch_softmax_us / row.family_us)
+            fracs.append(cols["family"].gbs() / HBM_PEAK_GBS)
+            shape = f"{row.batch} x {row.heads} x {row.seq_len}"
+            ok = "yes" if row.softmax_sums_ok and row.family_sums_ok else "NO"
+            print(f"  {'':{len(label)}s}  {shape:>12s} | {cols['torch'].cell()} | {cols['softmax'].cell()} | "
+                  f"{cols['family'].cell()} | {_kernel_label(row.family_meta):>8s} | {row.softmax_err:8.1e} "
+                  f"{row.family_err:8.1e} | {ok:>7s} | {speedups[-1]:5.2f}x")
+        print(f"  {label}: squareplus family vs torch softmax: geometric mean {_geomean(speedups):.2f}x; "
+              f"family at {100 * _geomean(fracs):.1f}% of the HBM peak (geometric mean)")
+
+
+def report_backward(rows):
+    print("\nfused causal backward vs autograd of the fp32 eager forward")
+    for row in rows:
+        print(f"  {_dtype_label(row['dtype']):>5s}: max |grad err| {row['max_abs_grad_err']:.2e}, "
+              f"close: {'yes' if row['grad_close'] else 'NO'}")
+
+
+# Names of the reference's report functions (kernels.py:2983-3058), kept for
+# callers that print results themselves.
 def print_rowwise_report(results):
-    """kernels.py:2983-3008."""
-    print("\n--- Legacy Rowwise Benchmark ---")
-    print("  HIP columns use reusable output buffers.")
-    print(f"  {'Shape':>18s} {'F.softmax':>10s} {'sm_hip':>10s} {'fam_hip':>11s} {'fam/F.sm':>9s} {'fam/sm_hip':>10s}")
-    print("  " + "-" * 74)
-    r_torch, r_sm = [], []
-    for row in results:
-        r_torch.append(row.family_us / row.torch_softmax_us)
-        r_sm.append(row.family_us / row.triton_softmax_us)
-        print(f"  {str(row.shape):>18s} {row.torch_softmax_us:8.1f}us {row.triton_softmax_us:8.1f}us"
-              f" {row.family_us:9.1f}us {r_torch[-1]:7.2f}x {r_sm[-1]:8.2f}x")
-    print(f"\n  Geo mean fam_hip / F.softmax:  {_geo_mean(r_torch):.3f}x")
-    print(f"  Geo mean fam_hip / softmax_hip: {_geo_mean(r_sm):.3f}x")
+    report_rowwise(results)
 
 
 def print_causal_report(results, family):
-    """kernels.py:3011-3058."""
-    print("\n--- Production Causal Benchmark ---")
-    print("  HIP columns use reusable output buffers and fp32 arithmetic.")
-    print(f"  Family: {family.label}")
-    print(f"  {'dtype':>6s} {'B,H,T':>12s} {'torch.sm':>10s} {'sm_hip':>10s} {'fam_hip':>10s}"
-          f" {'fam/torch':>10s} {'fam/sm':>8s} {'sm_err':>10s} {'fam_err':>10s}")
-    print("  " + "-" * 100)
-    grouped = {}
-    for row in results:
-        label = _dtype_label(row.dtype)
-        g = grouped.setdefault(label, ([], []))
-        g[0].append(row.family_us / row.torch_softmax_us)
-        g[1].append(row.family_us / row.triton_softmax_us)
-        print(f"  {label:>6s} {f'{row.batch}x{row.heads}x{row.seq_len}':>12s} {row.torch_softmax_us:8.1f}us"
-              f" {row.triton_softmax_us:8.1f}us {row.family_us:8.1f}us {g[0][-1]:8.2f}x {g[1][-1]:7.2f}x"
-              f" {row.softmax_err:10.2e} {row.family_err:10.2e}")
-    print("\n  Correctness:")
-    for row in results:
-        print(f"  {_dtype_label(row.dtype):>6s} T={row.seq_len:<4d} softmax_sum={row.softmax_sums_ok}"
-              f" family_sum={row.family_sums_ok}")
-    print("\n  Geo means by dtype:")
-    for label, (vt, vs) in grouped.items():
-        print(f"  {label:>6s} fam/torch={_geo_mean(vt):.3f}x fam/sm_hip={_geo_mean(vs):.3f}x")
+    report_causal(results, family)
 
 
+# ---------------------------------------------------------------------------
+# Command line (flags and defaults of kernels.py:3061-3075)
+# ---------------------------------------------------------------------------
 def parse_args(argv=None):
-    """kernels.py:3061-3075 (same options and defaults)."""
-    p = argparse.ArgumentParser(description="smooth-attn squareplus benchmark harness (MI355X)")
+    p = argparse.ArgumentParser(description="smooth-attn squareplus benchmark harness (MI355X, HIP)")
     p.add_argument("--mode", choices=("causal", "rowwise", "all"), default="causal")
     p.add_argument("--dtypes", default="bf16", help="comma-separated: fp32,fp16,bf16")
     p.add_argument("--lengths", default=",".join(map(str, DEFAULT_CAUSAL_LENGTHS)),
@@ -230,36 +322,22 @@ def parse_args(argv=None):
 
 
 def main(argv=None):
-    """kernels.py:3078-3128."""
     args = parse_args(argv)
     family = FamilyConfig(alpha=args.alpha, theta=args.theta, power=args.power)
     dtypes = _parse_dtype_list(args.dtypes)
     lengths = _parse_int_list(args.lengths)
-    if args.quick:
-        lengths = lengths[: min(2, len(lengths))]
-        args.warmup = min(args.warmup, 20)
-        args.iters = min(args.iters, 100)
-
-    _print_header("SMOOTH-ATTN SQUAREPLUS BENCHMARK (gfx950 HIP)")
-    print(f"GPU: {torch.cuda.get_device_name(_current_device_index())}")
-    print(f"Family: {family.label}")
-
+    warmup, iters = args.warmup, args.iters
+    if args.quick:  # the first two lengths, shorter timing loops
+        lengths = lengths[:2]
+        warmup, iters = min(warmup, 20), min(iters, 100)
+    dev = _current_device_index()
+    print(f"smooth-attn benchmark on {torch.cuda.get_device_name(dev)} (HIP kernels for gfx950); "
+          f"HBM peak {HBM_PEAK_GBS / 1000:.0f} TB/s; median of {iters} launches after {warmup} warm-up")
     if args.mode in ("rowwise", "all"):
-        print_rowwise_report(benchmark_rowwise_suite(family=family, warmup=args.warmup, iters=args.iters))
-
+        report_rowwise(benchmark_rowwise_suite(family, warmup=warmup, iters=iters))
     if args.mode in ("causal", "all"):
-        res = benchmark_causal_suite(family=family, dtypes=dtypes, lengths=lengths, batch=args.batch,
-                                     heads=args.heads, warmup=args.warmup, iters=args.iters)
-        if res:
-            print("\n--- Causal Launch Meta (first case) ---")
-            _print_launch_meta("softmax", res[0].softmax_meta)
-            _print_launch_meta("family", res[0].family_meta)
-        print_causal_report(res, family)
-
+        report_causal(benchmark_causal_suite(family, dtypes, lengths, batch=args.batch, heads=args.heads,
+                                             warmup=warmup, iters=iters), family)
     if args.check_backward:
-        print("\n--- Backward Validation ---")
-        for row in validate_causal_backward(family=family, dtypes=dtypes, seq_len=lengths[0],
-                                            batch=min(args.batch, 2), heads=min(args.heads, 4)):
-            print(f"  {_dtype_label(row['dtype']):>6s} grad_close={row['grad_close']}"
-                  f" max_abs_grad_err={row['max_abs_grad_err']:.2e}")
-    print("\n" + "=" * 80)
+        report_backward(validate_causal_backward(family, dtypes, seq_len=lengths[0], batch=min(args.batch, 2),
+                                                 heads=min(args.heads, 4)))

@@ -104,5 +104,5 @@ def test_benchmark_cli_quick(capsys):
     assert res[0].family_meta["kernel"] in ("vec", "scalar", "split")
     rows = smooth_attn.benchmark_rowwise_suite(smooth_attn.DEFAULT_FAMILY, shapes=[(64, 256)], warmup=1, iters=2)
     assert rows[0].shape == (64, 256) and rows[0].family_us > 0 and rows[0].torch_softmax_us > 0
-    grads = smooth_attn.validate_causal_backward(smooth_attn.DEFAULT_FAMILY, [torch.float32], seq_len=32)
+    grads = smooth_attn.kernels.validate_causal_backward(smooth_attn.DEFAULT_FAMILY, [torch.float32], seq_len=32)
     assert grads[0]["grad_close"] and grads[0]["max_abs_grad_err"] < 1e-4
