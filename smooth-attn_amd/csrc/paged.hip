@@ -401,7 +401,9 @@ int validate_paged(const void* q, const void* k_cache, const void* v_cache, cons
                    const int64_t* kv_strides, const int64_t* vv_strides, const int64_t* o_strides, int dtype) {
     if (B < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || max_pages < 0 || n_pages < 0) return SA_ERR_BAD_SHAPE;
     if (Hq / Hkv > 32) return SA_ERR_UNSUPPORTED;  // query heads per KV head fill one 32-wide MFMA column block
-    if (page_size != 8 && page_size != 16 && page_size != 32 && page_size != 64) return SA_ERR_UNSUPPORTED;
+    // any power of two: a tile of 32 tokens spans 32 / P pages (P < 32) or
+    // lies in one page; a window of 64 page ids always covers whole tiles
+    if (page_size <= 0 || (page_size & (page_size - 1)) != 0 || page_size > (1 << 20)) return SA_ERR_UNSUPPORTED;
     if (D != 32 && D != 64 && D != 128) return SA_ERR_UNSUPPORTED;
     if (B == 0) return 1;
     if (n_pages == 0) max_pages = 0;  // no cache: every context is empty

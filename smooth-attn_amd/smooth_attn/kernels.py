@@ -557,18 +557,42 @@ def _flash_operand(t):
     return t if ok else t.clone(memory_format=torch.contiguous_format)
 
 
+def _kernel_head_dim(D):
+    """The head dim the kernels run for a head dim D: D itself for 32, 64 and
+    128, else the next of those (inputs zero-padded, outputs sliced: zero
+    columns add nothing to q.k, and the padded columns of O, dQ, dK, dV are
+    dropped).  The reference takes any power of two through next_pow2
+    (kernels.py:1918); head dims above 128 are not supported here."""
+    if D in _FLASH_HEAD_DIMS:
+        return D
+    if D < 1 or D > _FLASH_HEAD_DIMS[-1]:
+        raise ValueError(f"fused attention supports head dims 1..{_FLASH_HEAD_DIMS[-1]}, got {D}")
+    return next(d for d in _FLASH_HEAD_DIMS if d >= D)
+
+
+def _pad_head_dim(t, Dk):
+    return t if t.shape[-1] == Dk else F.pad(t, (0, Dk - t.shape[-1]))
+
+
+def _check_flash_dtypes(q, k, v):
+    if q.dtype not in (torch.bfloat16, torch.float16) or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError(f"fused attention expects bf16 or fp16 q/k/v of one dtype, got "
+                         f"{q.dtype}/{k.dtype}/{v.dtype}")
+
+
 def _sp2norm_flash_fwd(q, k, v, scale, n_kv_groups=1, window_size=0, use_fast_sqrt=True):
     """(o, row_sums) of the fused forward — replaces kernels.py:1912-1931."""
     _check_same_device("q", q, k=k, v=v)
     B, H_q, T, D = q.shape
     H_kv = k.shape[1]
-    if q.dtype not in (torch.bfloat16, torch.float16) or k.dtype != q.dtype or v.dtype != q.dtype:
-        raise ValueError(f"fused attention expects bf16 or fp16 q/k/v of one dtype, got "
-                         f"{q.dtype}/{k.dtype}/{v.dtype}")
-    if D not in _FLASH_HEAD_DIMS:
-        raise ValueError(f"fused attention supports head dims {_FLASH_HEAD_DIMS}, got {D}")
+    _check_flash_dtypes(q, k, v)
     if H_kv * n_kv_groups != H_q:
         raise ValueError("n_kv_groups must equal H_q // H_kv")
+    Dk = _kernel_head_dim(D)
+    if Dk != D:
+        o, row_sums = _sp2norm_flash_fwd(_pad_head_dim(q, Dk), _pad_head_dim(k, Dk), _pad_head_dim(v, Dk), scale,
+                                         n_kv_groups, window_size, use_fast_sqrt)
+        return o[..., :D].contiguous(), row_sums
     q, k, v = _flash_operand(q), _flash_operand(k), _flash_operand(v)
     o = torch.empty_like(q)
     if o.stride(-1) != 1:
@@ -590,6 +614,12 @@ def _sp2norm_flash_bwd(q, k, v, o, do, row_sums, scale, n_kv_groups=1, window_si
     _check_same_device("q", q, k=k, v=v, o=o, do=do, row_sums=row_sums)
     B, H_q, T, D = q.shape
     H_kv = k.shape[1]
+    _check_flash_dtypes(q, k, v)
+    Dk = _kernel_head_dim(D)
+    if Dk != D:
+        pad = [_pad_head_dim(t, Dk) for t in (q, k, v, o, do.to(q.dtype))]
+        dq, dk, dv = _sp2norm_flash_bwd(*pad, row_sums, scale, n_kv_groups, window_size, use_fast_sqrt)
+        return dq[..., :D].contiguous(), dk[..., :D].contiguous(), dv[..., :D].contiguous()
     q, k, v, o = _flash_operand(q), _flash_operand(k), _flash_operand(v), _flash_operand(o)
     do = _flash_operand(do.to(q.dtype))
     dq = torch.empty_like(q)
@@ -674,8 +704,8 @@ def _sp2norm_rope_flash_fwd(q, k, v, cos, sin, scale, n_kv_groups=1, window_size
     if q.dtype not in (torch.bfloat16, torch.float16) or k.dtype != q.dtype or v.dtype != q.dtype:
         raise ValueError(f"RoPE attention expects bf16 or fp16 q/k/v of one dtype, got "
                          f"{q.dtype}/{k.dtype}/{v.dtype}")
-    if D not in _FLASH_HEAD_DIMS:
-        raise ValueError(f"fused attention supports head dims {_FLASH_HEAD_DIMS}, got {D}")
+    if D not in _FLASH_HEAD_DIMS:  # rotate-half pairs d with d + D/2: no padding of the head dim
+        raise ValueError(f"RoPE attention supports head dims {_FLASH_HEAD_DIMS}, got {D}")
     q, k, v = _flash_operand(q), _flash_operand(k), _flash_operand(v)
     cos, sin = _rope_tables(cos, sin, T, D)
     if o is None:
@@ -800,10 +830,16 @@ def _sp2norm_fp8_flash_fwd(q_fp8, k_fp8, v_fp8, q_scale, k_scale, v_scale, attn_
     _check_same_device("q_fp8", q_fp8, k_fp8=k_fp8, v_fp8=v_fp8)
     B, H_q, T, D = q_fp8.shape
     H_kv = k_fp8.shape[1]
-    if D not in _FLASH_HEAD_DIMS:
-        raise ValueError(f"fused attention supports head dims {_FLASH_HEAD_DIMS}, got {D}")
     if q_fp8.dtype != torch.float8_e4m3fn or k_fp8.dtype != torch.float8_e4m3fn:
         raise ValueError("q and k must be float8_e4m3fn")
+    Dk = _kernel_head_dim(D)
+    if Dk != D:
+        # zero codes pad the head dim exactly (F.pad works on the bytes)
+        pad8 = lambda t: _pad_head_dim(t.view(torch.uint8), Dk).view(t.dtype) if t.dtype == torch.float8_e4m3fn \
+            else _pad_head_dim(t, Dk)
+        o, row_sums = _sp2norm_fp8_flash_fwd(pad8(q_fp8), pad8(k_fp8), pad8(v_fp8), q_scale, k_scale, v_scale,
+                                             attn_scale, n_kv_groups, window_size)
+        return o[..., :D].contiguous(), row_sums
     if v_fp8.dtype == torch.float8_e4m3fn:
         v_code = _lib.SA_FP8_E4M3FN
     elif v_fp8.dtype == torch.bfloat16:
@@ -880,6 +916,10 @@ def sp2norm_paged_attention(q, k_cache, v_cache, block_table, context_lens, *, s
     H_kv = k_cache.shape[1]
     assert H_q % H_kv == 0
     assert k_cache.shape[2] == block_size and v_cache.shape[2] == block_size
+    if block_size < 1 or block_size & (block_size - 1):
+        # the reference rounds BLOCK_SIZE up to a power of two and then
+        # addresses the pages wrongly (kernels.py:2815, :2737-2743)
+        raise ValueError(f"block_size must be a power of two, got {block_size}")
     max_blocks_per_seq = block_table.shape[1]
     if scale is None:
         scale = 1.0 / math.sqrt(D)

@@ -143,3 +143,15 @@ def test_full_size_config3_sampled():
                                                   v[b:b + 1, h:h + 1].cpu().double(), return_row_sums=True)
         assert rel_err(o[b:b + 1, h:h + 1], ref) <= 1e-2
         assert rel_err(rs[b:b + 1, h:h + 1], ref_rs) <= 1e-5
+
+
+@pytest.mark.parametrize("D", [8, 16, 48, 96])
+@pytest.mark.parametrize("T", [1, 100, 300])
+def test_forward_head_dims_below_128(D, T):
+    # any head dim up to 128 (the reference takes powers of two through
+    # next_pow2, kernels.py:1918): run zero-padded to 32 / 64 / 128
+    q, k, v = qkv(1, 4, 2, T, D, torch.bfloat16, seed=D + T)
+    o, _ = check_forward(q, k, v)
+    assert o.is_contiguous() and o.shape == (1, 4, T, D)
+    out = smooth_attn.sp2norm_flash_attention(q.to(DEV), k.to(DEV), v.to(DEV))
+    assert torch.equal(out, o)

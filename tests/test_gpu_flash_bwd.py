@@ -158,3 +158,11 @@ def test_backward_scales(scale):
     for name, got, ref in zip(("dq", "dk", "dv"), grads, refs):
         assert bool(torch.isfinite(got).all()), name
         assert rel_err(got, ref) <= TOL, f"{name}: rel err {rel_err(got, ref):.3e}"
+
+
+@pytest.mark.parametrize("D", [16, 48, 96])
+def test_backward_head_dims_below_128(D):
+    # head dims other than 32 / 64 / 128 run zero-padded; the padded columns
+    # of dQ, dK, dV are dropped
+    grads, _ = check_backward(*inputs(1, 4, 2, 200, D, torch.bfloat16, seed=D))
+    assert all(g.is_contiguous() and g.shape[-1] == D for g in grads)

@@ -250,3 +250,17 @@ def test_fp8_forward_score_scale_range(qmag, kmag, attn_scale, v_fp8):
     assert bool(torch.isfinite(o).all())
     assert rel_err(o, ref) <= 1e-2
     assert rel_err(rs, ref_rs) <= 1e-4
+
+
+@pytest.mark.parametrize("D", [16, 80])
+def test_fp8_forward_head_dims_below_128(D):
+    # zero fp8 codes pad the head dim to 32 / 128 for the kernel
+    q, k, v = _fp8_case(1, 4, 2, 130, D, seed=D)
+    q8, qs = eager.quantize_to_fp8(q)
+    k8, ks = eager.quantize_to_fp8(k)
+    scale = 1 / math.sqrt(D)
+    o, rs = kernels._sp2norm_fp8_flash_fwd(q8.to(DEV), k8.to(DEV), v.to(DEV), float(qs), float(ks), None, scale, 2)
+    ref, ref_rs = eager.fp8_flash_attention_eager(q8, k8, v, qs, ks, torch.tensor(1.0), scale, return_row_sums=True)
+    assert o.shape == (1, 4, 130, D) and o.is_contiguous()
+    assert rel_err(o, ref) <= 1e-2
+    assert rel_err(rs, ref_rs) <= 1e-4

@@ -100,7 +100,8 @@ def test_paged_many_skewed_sequences(D, BS, hq, hkv):
     assert bool((out[empty] == 0).all())
 
 
-@pytest.mark.parametrize("D,BS", [(128, 16), (128, 64), (64, 8), (32, 8), (32, 32)])
+@pytest.mark.parametrize("D,BS", [(128, 16), (128, 64), (64, 8), (32, 8), (32, 32), (128, 1), (64, 2), (32, 4),
+                                  (128, 128), (64, 256)])
 def test_paged_ignores_cache_past_context(D, BS):
     # Cache slots past each sequence's length (the tail of its last page,
     # and whole pages past it) hold NaN: the output must not see them.
@@ -122,8 +123,11 @@ def test_paged_ignores_cache_past_context(D, BS):
     assert rel_err(out, ref) <= 1e-2
 
 
-@pytest.mark.parametrize("BS", [8, 16, 32, 64])
+@pytest.mark.parametrize("BS", [1, 2, 4, 8, 16, 32, 64, 128, 256, 1024])
 def test_paged_block_sizes_agree(BS):
+    # every power-of-two page size (the reference's BLOCK_SIZE = next_pow2,
+    # kernels.py:2815): pages smaller than a load instruction's tokens take
+    # per-lane page lookups, larger ones hold whole 32-token tiles
     q, k, v = case(2, 4, 4, 128, 32, seed=5)
     kc, vc, table, lens = paging.build_paged_cache(k, v, page_size=BS, shuffle=True, generator=_g(BS))
     out = run(q, kc, vc, table, lens, BS)
