@@ -10,7 +10,9 @@ extern "C" const char* sa_status_string(int status) {
         case SA_ERR_BAD_FAMILY: return "power must be 1, 2 or 3";
         case SA_ERR_BAD_STRIDE: return "unsupported stride or alignment";
         case SA_ERR_UNSUPPORTED: return "unsupported configuration";
-        case SA_ERR_WORKSPACE: return "workspace too small";
+        case SA_ERR_WORKSPACE:
+            return "workspace too small (sa_paged_decode_noalloc: the call needs more than its fixed "
+                   "SA_PAGED_NOALLOC_SCRATCH_BYTES of scratch)";
         default:
             if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));
             return "unknown error";

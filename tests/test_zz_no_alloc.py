@@ -104,3 +104,16 @@ def test_noalloc_coarsens_the_split_when_the_partials_do_not_fit():
     got = decode_noalloc(*dev, 16)
     torch.cuda.synchronize()
     assert torch.equal(got, smooth_attn.sp2norm_paged_attention(*dev, block_size=16))
+
+
+@pytest.mark.parametrize("P,D,dtype", [(1, 64, torch.float16), (128, 32, torch.bfloat16), (4, 128, torch.bfloat16)])
+def test_noalloc_page_sizes_and_head_dims(P, D, dtype):
+    # the allocation-free call on the page sizes and head dims the workspace
+    # entry point takes, against it (same split: bit-identical) and the oracle
+    cpu, dev = make_case(6, 16, 4, D, P, 900, seed=10 + P, dtype=dtype)
+    got = decode_noalloc(*dev, P)
+    want = smooth_attn.sp2norm_paged_attention(*dev, block_size=P)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    ref = eager.paged_decode_eager(*(t.double() if t.is_floating_point() else t for t in cpu))
+    assert rel_err(got, ref) <= 1e-2
