@@ -42,6 +42,7 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2516.6
 FP8_PEAK_TFLOPS = 5033.2
+FP32_PEAK_TFLOPS = 157.3  # dense fp32 MFMA
 # HBM bytes per launch of the causal-norm kernels on this workload, measured
 # with rocprofv3 FETCH_SIZE and WRITE_SIZE passes over this script
 # (--copy-calibration) and scaled by what the same counters read for a plain
@@ -330,6 +331,8 @@ def bench_paged(torch):
 
 def bench_next_rows(torch):
     """The rows built after the hot path, each timed by the same protocol:
+    - fp32 fused attention forward and backward on config 3's shape (fp32
+      MFMA, against the 157.3 TFLOP/s dense fp32 peak);
     - RoPE-fused attention forward on config 3's shape (K rotated once by a
       streaming kernel, Q in registers; the time includes the rotation),
       and the RoPE + W_o projection variant (RoPE forward plus one fp32-
@@ -366,6 +369,17 @@ def bench_next_rows(torch):
                                   "frac_bf16_peak": round((fl + fl_proj) / us / 1e6 / BF16_PEAK_TFLOPS, 4),
                                   "flops": fl + fl_proj}
     del q, k, v, w_o
+    torch.cuda.empty_cache()
+
+    q, k, v, do = (torch.randn(B, H, L, D, generator=gen, device=dev) for _ in range(4))
+    o, rs = sa.kernels._sp2norm_flash_fwd(q, k, v, 1 / math.sqrt(D))
+    us_f = med(lambda: sa.kernels._sp2norm_flash_fwd(q, k, v, 1 / math.sqrt(D)))
+    us_b = med(lambda: sa.kernels._sp2norm_flash_bwd(q, k, v, o, do, rs, 1 / math.sqrt(D)))
+    out["attention_fp32"] = {"shape": [B, H, L, D], "fwd_us": round(us_f, 1), "bwd_us": round(us_b, 1),
+                             "fwd_tflops": round(fl / us_f / 1e6, 1), "bwd_tflops": round(2.5 * fl / us_b / 1e6, 1),
+                             "fwd_frac_fp32_peak": round(fl / us_f / 1e6 / FP32_PEAK_TFLOPS, 4),
+                             "bwd_frac_fp32_peak": round(2.5 * fl / us_b / 1e6 / FP32_PEAK_TFLOPS, 4)}
+    del q, k, v, do, o, rs
     torch.cuda.empty_cache()
 
     Bn, Hn, Ln = 4, 16, 4096

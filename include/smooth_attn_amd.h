@@ -155,12 +155,16 @@ int sa_softmax_fwd_launch_info(const void* x, const void* y, int64_t n_rows,
                                sa_launch_info* info);
 
 /*
- * Fused causal squareplus attention forward (bf16 or fp16 q/k/v/o):
+ * Fused causal squareplus attention forward (bf16, fp16 or fp32 q/k/v/o,
+ * dtype SA_BF16 / SA_F16 / SA_F32; fp32 runs on the fp32 MFMA with P kept in
+ * fp32):
  *   O_i = sum_{j<=i, i-j<W} y_ij V_j / (sum_j y_ij + 1e-12),
  *   y = squareplus(2 s - 1)^2,  s = scale * q_i . k_j
  * q,o: [B, Hq, T, D]; k,v: [B, Hkv, T, D]; Hq % Hkv == 0 (query head h reads
- * KV head h / (Hq/Hkv)).  *_strides are element strides for (b, h, t, d) and
- * the d stride must be 1 (K and V row strides at most 16 MiB).  row_sums (nullable): fp32 [B, Hq, T] contiguous,
+ * KV head h / (Hq/Hkv)).  *_strides are element strides for (b, h, t, d):
+ * the d stride must be 1, the others multiples of 16 bytes (8 elements of a
+ * 16-bit type, 4 of fp32), base pointers 16-byte aligned, and for bf16/fp16
+ * K and V row strides at most 16 MiB.  row_sums (nullable): fp32 [B, Hq, T] contiguous,
  * receives sum_j y_ij + 1e-12.  window_size 0 = full causal.  D in {32, 64,
  * 128}.  exact_math != 0 selects a correctly rounded sqrt.
  * Replaces _sp2norm_flash_fwd (kernels.py:1912-1931) and its kernel

@@ -1,0 +1,564 @@
+// fp32 fused causal squareplus attention, forward and backward, on the fp32
+// MFMA of gfx950 (v_mfma_f32_32x32x2_f32: exact fp32 products, fp32 sums).
+//
+// Same mathematics as the 16-bit kernels (flash_fwd.hip, flash_bwd.hip),
+// with P and dS kept in fp32 (the reference keeps P in the input dtype,
+// kernels.py:1621, and for fp32 inputs its dots run at Triton's TF32
+// default).  Layout of v_mfma_f32_32x32x2_f32 (checked on the device): A
+// (32 x 2) lane l holds row l % 32 and k = l / 32; B (2 x 32) lane l holds
+// k = l / 32 and column l % 32; C (32 x 32) lane l holds column l % 32 and
+// rows 8 (v / 4) + 4 (l / 32) + v % 4, v = 0..15.
+//
+// Contraction order.  For S^T = K Q^T the k index of MFMA i pairs d = i (k
+// = 0) with d = i + D/2 (k = 1), so a lane's D/2 operands of Q (or K) are one
+// contiguous half-row.  For products with P or dS as the B operand (O^T +=
+// V^T P^T, dQ^T += K^T dS^T, dV^T += dO^T P, dK^T += Q^T dS) MFMA j takes the
+// lane's own C element v = j: k = 0 is row 8 (j / 4) + j % 4 and k = 1 that
+// row + 4, so the A operand's four consecutive rows for j = 4m .. 4m + 3 come
+// from one 16-byte read of a transposed [D][rows] LDS tile.
+//
+// Work decomposition: blocks of 4 waves, 32 rows per wave (queries in the
+// forward and dQ, keys in dK/dV), tiles of 32 rows staged in LDS (row-major
+// [32][D + 4] and, where the transposed operand is needed, [D][36]); the
+// next tile's global loads are in flight while the current one is used.
+#include "flash_f32.hpp"
+
+namespace sa {
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kFW = 4;             // waves per block
+constexpr int kFT = 32;            // rows per staged tile
+constexpr int kFRows = 32 * kFW;   // rows a block owns
+constexpr int kTP = kFT + 4;       // pitch (floats) of a transposed [D][kFT] tile
+
+__device__ __forceinline__ f32x16 mma32(float a, float b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+struct F32Params {
+    const float* q;
+    const float* k;
+    const float* v;
+    const float* o;     // backward input
+    const float* dout;  // backward input
+    const float* rs;    // backward input: forward row sums [B, Hq, T]
+    float* out;         // forward output
+    float* row_sums;    // forward output (nullable)
+    float* dq;
+    float* dk;
+    float* dv;
+    float* delta;  // [B, Hq, T]
+    int64_t qs[4], ks[4], vs[4], os[4], dos[4], dqs[4], dks[4], dvs[4];
+    int B, Hq, Hkv, T, G, window;
+    float scale;
+};
+
+// One [kFT][D] fp32 tile (rows r0.., clamped to T - 1) held in registers
+// between its global loads and its LDS stores.
+template <int D>
+struct TileRegs {
+    static constexpr int PER = kFT * D / 4 / (64 * kFW);  // float4 per thread
+    float4 v[PER];
+    __device__ __forceinline__ void load(const float* base, int64_t rstride, int r0, int T, int tid) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int idx = tid + 64 * kFW * i;
+            const int r = idx / (D / 4);
+            const int c = (idx - r * (D / 4)) * 4;
+            v[i] = *reinterpret_cast<const float4*>(base + static_cast<int64_t>(min(r0 + r, T - 1)) * rstride + c);
+        }
+    }
+    // row-major [kFT][D + 4] (nullable) and transposed [D][kTP] (nullable)
+    __device__ __forceinline__ void store(float* row, float* tr, int tid) const {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int idx = tid + 64 * kFW * i;
+            const int r = idx / (D / 4);
+            const int c = (idx - r * (D / 4)) * 4;
+            if (row != nullptr) *reinterpret_cast<float4*>(row + r * (D + 4) + c) = v[i];
+            if (tr != nullptr) {
+                tr[(c + 0) * kTP + r] = v[i].x;
+                tr[(c + 1) * kTP + r] = v[i].y;
+                tr[(c + 2) * kTP + r] = v[i].z;
+                tr[(c + 3) * kTP + r] = v[i].w;
+            }
+        }
+    }
+};
+
+// y = squareplus(2 s scale - 1)^2 = (a + r)^2 with a = s scale - 1/2,
+// r = sqrt(a^2 + 1); rr = 1 / r.
+template <bool EXACT>
+__device__ __forceinline__ void weight_rr(float s, float sc, float& y, float& rr) {
+    const float a = __builtin_fmaf(s, sc, -0.5f);
+    const float u = __builtin_fmaf(a, a, 1.f);
+    float r;
+    if constexpr (EXACT) {
+        r = __builtin_sqrtf(u);
+        rr = 1.f / r;
+    } else {
+        rr = fast_rsqrt(u);
+        r = u * rr;
+    }
+    const float sp = a + r;
+    y = sp * sp;
+}
+
+// A lane's half row: x[i] = row[i + hi D/2], i < D/2.
+template <int D>
+__device__ __forceinline__ void load_half_row(const float* row, int hi, float (&x)[D / 2]) {
+#pragma unroll
+    for (int i4 = 0; i4 < D / 8; ++i4) {
+        const float4 t = *reinterpret_cast<const float4*>(row + hi * (D / 2) + 4 * i4);
+        x[4 * i4 + 0] = t.x;
+        x[4 * i4 + 1] = t.y;
+        x[4 * i4 + 2] = t.z;
+        x[4 * i4 + 3] = t.w;
+    }
+}
+
+// C (32 x 32) += A B^T over D, A rows from a row-major [kFT][D + 4] LDS
+// tile (row l32), B rows from a lane's half-row registers.
+template <int D>
+__device__ __forceinline__ f32x16 mma_rows(const float* lds_rows, int l32, int hi, const float (&b)[D / 2],
+                                           f32x16 c) {
+    const float* ar = lds_rows + l32 * (D + 4) + hi * (D / 2);
+#pragma unroll
+    for (int i4 = 0; i4 < D / 8; ++i4) {
+        const float4 a = *reinterpret_cast<const float4*>(ar + 4 * i4);
+        c = mma32(a.x, b[4 * i4 + 0], c);
+        c = mma32(a.y, b[4 * i4 + 1], c);
+        c = mma32(a.z, b[4 * i4 + 2], c);
+        c = mma32(a.w, b[4 * i4 + 3], c);
+    }
+    return c;
+}
+
+// acc[dt] (rows d = 32 dt + ..) += A^T(d, r) X(r, col) over the tile's 32
+// rows r, A^T read from a transposed [D][kTP] LDS tile and X the lane's own
+// 16 C-layout values x[v] (row 8 (v / 4) + 4 hi + v % 4).
+template <int D>
+__device__ __forceinline__ void mma_cols(const float* lds_tr, int l32, int hi, const float (&x)[16],
+                                         f32x16 (&acc)[D / 32]) {
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+        const float* ar = lds_tr + (dt * 32 + l32) * kTP + 4 * hi;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const float4 a = *reinterpret_cast<const float4*>(ar + 8 * m);
+            acc[dt] = mma32(a.x, x[4 * m + 0], acc[dt]);
+            acc[dt] = mma32(a.y, x[4 * m + 1], acc[dt]);
+            acc[dt] = mma32(a.z, x[4 * m + 2], acc[dt]);
+            acc[dt] = mma32(a.w, x[4 * m + 3], acc[dt]);
+        }
+    }
+}
+
+// Write a lane's C-layout rows of acc (column = its row index of the output,
+// d = 32 dt + 8 m + 4 hi .. +3) times f as 16-byte stores.
+template <int D>
+__device__ __forceinline__ void store_cols(float* row, int hi, const f32x16 (&acc)[D / 32], float f) {
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const float4 w{acc[dt][4 * m + 0] * f, acc[dt][4 * m + 1] * f, acc[dt][4 * m + 2] * f,
+                           acc[dt][4 * m + 3] * f};
+            *reinterpret_cast<float4*>(row + dt * 32 + 8 * m + 4 * hi) = w;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Forward
+// ---------------------------------------------------------------------------
+// Every kernel here is held to two waves per SIMD.  Left to itself the
+// compiler gives the D = 128 forward 258 registers and one wave (config 3's
+// shape in fp32: 7.7 ms vs 5.0 ms), the D = 64 dK/dV kernel 290 registers
+// (10.1 vs 8.2 ms for the backward); the D = 128 backward kernels spill at two
+// waves and are still faster (21.4 vs 22.0 ms).
+template <int D, bool EXACT>
+__global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(2, 8))) void flash_fwd_f32_kernel(F32Params p) {
+    __shared__ __attribute__((aligned(16))) float ldsK[kFT * (D + 4)];
+    __shared__ __attribute__((aligned(16))) float ldsVt[D * kTP];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int hi = lane >> 5;
+    const int l32 = lane & 31;
+    const int T_ = p.T;
+    const int nqb = (T_ + kFRows - 1) / kFRows;
+    const int per = p.B * p.Hq;
+    const int step = blockIdx.x / per;  // heaviest (latest) query blocks first
+    const int rest = blockIdx.x - step * per;
+    const int qb = nqb - 1 - step;
+    const int b = rest / p.Hq;
+    const int hq = rest - b * p.Hq;
+    const int hk = hq / p.G;
+    const float* kp = p.k + b * p.ks[0] + hk * p.ks[1];
+    const float* vp = p.v + b * p.vs[0] + hk * p.vs[1];
+
+    const int q0 = qb * kFRows + 32 * wave;
+    const int qi = q0 + l32;
+    const int qrow = min(qi, T_ - 1);
+    float qv[D / 2];
+    load_half_row<D>(p.q + b * p.qs[0] + hq * p.qs[1] + qrow * p.qs[2], hi, qv);
+
+    f32x16 oacc[D / 32];
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) oacc[dt] = f32x16{};
+    float ssum = 0.f;
+    const int W = p.window;
+    const unsigned weff = W > 0 ? static_cast<unsigned>(W) : 0x7FFFFFFFu;
+    const int n_kv = (T_ + kFT - 1) / kFT;
+    const int kv_end = min((qb * kFRows + kFRows + kFT - 1) / kFT, n_kv);
+    const int kv_begin = W > 0 ? max(0, qb * kFRows - W + 1) / kFT : 0;
+    const float sc = p.scale;
+
+    TileRegs<D> kreg, vreg;
+    kreg.load(kp, p.ks[2], kv_begin * kFT, T_, tid);
+    vreg.load(vp, p.vs[2], kv_begin * kFT, T_, tid);
+    for (int t = kv_begin; t < kv_end; ++t) {
+        __syncthreads();  // every wave is done with tile t - 1
+        kreg.store(ldsK, nullptr, tid);
+        vreg.store(nullptr, ldsVt, tid);
+        __syncthreads();
+        if (t + 1 < kv_end) {
+            kreg.load(kp, p.ks[2], (t + 1) * kFT, T_, tid);
+            vreg.load(vp, p.vs[2], (t + 1) * kFT, T_, tid);
+        }
+        const int k0 = t * kFT;
+        const bool active = k0 <= q0 + 31 && !(W > 0 && q0 - (k0 + 31) >= W);
+        if (!active) continue;
+        const f32x16 s = mma_rows<D>(ldsK, l32, hi, qv, f32x16{});  // S^T: rows keys, column query
+        float pv[16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int key = k0 + 8 * (v >> 2) + 4 * hi + (v & 3);
+            float y, rr;
+            weight_rr<EXACT>(s[v], sc, y, rr);
+            y = static_cast<unsigned>(qi - key) < weff ? y : 0.f;
+            pv[v] = y;
+            ssum += y;
+        }
+        mma_cols<D>(ldsVt, l32, hi, pv, oacc);  // O^T += V^T P^T
+    }
+
+    const float tot = ssum + __shfl_xor(ssum, 32) + kEps;
+    if (qi < T_) {
+        store_cols<D>(p.out + b * p.os[0] + hq * p.os[1] + qi * p.os[2], hi, oacc, 1.f / tot);
+        if (hi == 0 && p.row_sums != nullptr) p.row_sums[(static_cast<int64_t>(b) * p.Hq + hq) * T_ + qi] = tot;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Backward: dQ (and delta)
+// ---------------------------------------------------------------------------
+template <int D, bool EXACT>
+__global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(2, 8))) void flash_bwd_dq_f32_kernel(F32Params p) {
+    __shared__ __attribute__((aligned(16))) float ldsK[kFT * (D + 4)];
+    __shared__ __attribute__((aligned(16))) float ldsKt[D * kTP];
+    __shared__ __attribute__((aligned(16))) float ldsV[kFT * (D + 4)];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int hi = lane >> 5;
+    const int l32 = lane & 31;
+    const int T_ = p.T;
+    const int nqb = (T_ + kFRows - 1) / kFRows;
+    const int per = p.B * p.Hq;
+    const int step = blockIdx.x / per;
+    const int rest = blockIdx.x - step * per;
+    const int qb = nqb - 1 - step;
+    const int b = rest / p.Hq;
+    const int hq = rest - b * p.Hq;
+    const int hk = hq / p.G;
+    const float* kp = p.k + b * p.ks[0] + hk * p.ks[1];
+    const float* vp = p.v + b * p.vs[0] + hk * p.vs[1];
+
+    const int q0 = qb * kFRows + 32 * wave;
+    const int qi = q0 + l32;
+    const int qrow = min(qi, T_ - 1);
+    float qv[D / 2], dov[D / 2];
+    load_half_row<D>(p.q + b * p.qs[0] + hq * p.qs[1] + qrow * p.qs[2], hi, qv);
+    load_half_row<D>(p.dout + b * p.dos[0] + hq * p.dos[1] + qrow * p.dos[2], hi, dov);
+    // delta = rowsum(dO * O) of this lane's query (lanes l and l ^ 32 hold the halves)
+    float dpart = 0.f;
+    {
+        const float* orow = p.o + b * p.os[0] + hq * p.os[1] + qrow * p.os[2] + hi * (D / 2);
+#pragma unroll
+        for (int i4 = 0; i4 < D / 8; ++i4) {
+            const float4 ov = *reinterpret_cast<const float4*>(orow + 4 * i4);
+            dpart = __builtin_fmaf(dov[4 * i4 + 0], ov.x, dpart);
+            dpart = __builtin_fmaf(dov[4 * i4 + 1], ov.y, dpart);
+            dpart = __builtin_fmaf(dov[4 * i4 + 2], ov.z, dpart);
+            dpart = __builtin_fmaf(dov[4 * i4 + 3], ov.w, dpart);
+        }
+    }
+    const float dl = dpart + __shfl_xor(dpart, 32);
+    const int64_t rbase = (static_cast<int64_t>(b) * p.Hq + hq) * T_;
+    if (qi < T_ && hi == 0) p.delta[rbase + qi] = dl;
+    const float inv_r = 1.f / p.rs[rbase + qrow];
+
+    f32x16 acc[D / 32];
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) acc[dt] = f32x16{};
+    f32x16 ndl;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) ndl[v] = -dl;
+    const int W = p.window;
+    const unsigned weff = W > 0 ? static_cast<unsigned>(W) : 0x7FFFFFFFu;
+    const int n_kv = (T_ + kFT - 1) / kFT;
+    const int kv_end = min((qb * kFRows + kFRows + kFT - 1) / kFT, n_kv);
+    const int kv_begin = W > 0 ? max(0, qb * kFRows - W + 1) / kFT : 0;
+    const float sc = p.scale;
+
+    TileRegs<D> kreg, vreg;
+    kreg.load(kp, p.ks[2], kv_begin * kFT, T_, tid);
+    vreg.load(vp, p.vs[2], kv_begin * kFT, T_, tid);
+    for (int t = kv_begin; t < kv_end; ++t) {
+        __syncthreads();
+        kreg.store(ldsK, ldsKt, tid);
+        vreg.store(ldsV, nullptr, tid);
+        __syncthreads();
+        if (t + 1 < kv_end) {
+            kreg.load(kp, p.ks[2], (t + 1) * kFT, T_, tid);
+            vreg.load(vp, p.vs[2], (t + 1) * kFT, T_, tid);
+        }
+        const int k0 = t * kFT;
+        const bool active = k0 <= q0 + 31 && !(W > 0 && q0 - (k0 + 31) >= W);
+        if (!active) continue;
+        const f32x16 s = mma_rows<D>(ldsK, l32, hi, qv, f32x16{});  // S^T
+        const f32x16 dp = mma_rows<D>(ldsV, l32, hi, dov, ndl);     // dP^T - delta
+        float ds[16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int key = k0 + 8 * (v >> 2) + 4 * hi + (v & 3);
+            float y, rr;
+            weight_rr<EXACT>(s[v], sc, y, rr);
+            ds[v] = static_cast<unsigned>(qi - key) < weff ? dp[v] * y * rr : 0.f;
+        }
+        mma_cols<D>(ldsKt, l32, hi, ds, acc);  // dQ^T += K^T dS^T
+    }
+    // dS carried without its per-row factor 2 scale / R
+    if (qi < T_) store_cols<D>(p.dq + b * p.dqs[0] + hq * p.dqs[1] + qi * p.dqs[2], hi, acc, 2.f * sc * inv_r);
+}
+
+// ---------------------------------------------------------------------------
+// Backward: dK, dV
+// ---------------------------------------------------------------------------
+template <int D, bool EXACT>
+__global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(2, 8))) void flash_bwd_dkdv_f32_kernel(F32Params p) {
+    __shared__ __attribute__((aligned(16))) float ldsQ[kFT * (D + 4)];
+    __shared__ __attribute__((aligned(16))) float ldsQt[D * kTP];
+    __shared__ __attribute__((aligned(16))) float ldsO[kFT * (D + 4)];
+    __shared__ __attribute__((aligned(16))) float ldsOt[D * kTP];
+    __shared__ __attribute__((aligned(16))) float ldr[2][kFT];  // [1/R, -delta] of the tile's rows
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int hi = lane >> 5;
+    const int l32 = lane & 31;
+    const int T_ = p.T;
+    const int nkb = (T_ + kFRows - 1) / kFRows;
+    const int per = p.B * p.Hkv;
+    const int kb = blockIdx.x / per;  // earliest key blocks (most queries) first
+    const int rest = blockIdx.x - kb * per;
+    const int b = rest / p.Hkv;
+    const int hk = rest - b * p.Hkv;
+    (void)nkb;
+
+    const int k_start = kb * kFRows;
+    const int wk0 = k_start + 32 * wave;
+    const int kj = wk0 + l32;
+    const int krow = min(kj, T_ - 1);
+    float kv[D / 2], vv[D / 2];
+    load_half_row<D>(p.k + b * p.ks[0] + hk * p.ks[1] + krow * p.ks[2], hi, kv);
+    load_half_row<D>(p.v + b * p.vs[0] + hk * p.vs[1] + krow * p.vs[2], hi, vv);
+
+    f32x16 dkacc[D / 32], dvacc[D / 32];
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+        dkacc[dt] = f32x16{};
+        dvacc[dt] = f32x16{};
+    }
+    const int W = p.window;
+    const unsigned weff = W > 0 ? static_cast<unsigned>(W) : 0x7FFFFFFFu;
+    const int n_qt = (T_ + kFT - 1) / kFT;
+    const int qt_begin = k_start / kFT;
+    const int qt_end = W > 0 ? min(n_qt, (k_start + kFRows - 1 + W - 1) / kFT + 1) : n_qt;
+    const int nq = qt_end - qt_begin;  // >= 1 (k_start < T)
+    const int n_it = p.G * nq;
+    const float sc = p.scale;
+
+    TileRegs<D> qreg, oreg;
+    float rst = 0.f;
+    auto fetch = [&](int it) {
+        const int g = it / nq;
+        const int q0 = (qt_begin + it - g * nq) * kFT;
+        const int hq = hk * p.G + g;
+        qreg.load(p.q + b * p.qs[0] + hq * p.qs[1], p.qs[2], q0, T_, tid);
+        oreg.load(p.dout + b * p.dos[0] + hq * p.dos[1], p.dos[2], q0, T_, tid);
+        if (tid < 2 * kFT) {
+            const int64_t idx = (static_cast<int64_t>(b) * p.Hq + hq) * T_ + min(q0 + (tid & (kFT - 1)), T_ - 1);
+            rst = tid < kFT ? 1.f / p.rs[idx] : -p.delta[idx];
+        }
+    };
+    fetch(0);
+    for (int it = 0; it < n_it; ++it) {
+        __syncthreads();
+        qreg.store(ldsQ, ldsQt, tid);
+        oreg.store(ldsO, ldsOt, tid);
+        if (tid < 2 * kFT) ldr[tid / kFT][tid & (kFT - 1)] = rst;
+        __syncthreads();
+        const int g = it / nq;
+        const int q0 = (qt_begin + it - g * nq) * kFT;
+        if (it + 1 < n_it) fetch(it + 1);
+        // some query of the tile sees some key of the wave
+        const bool active = q0 + 31 >= wk0 && !(W > 0 && q0 - (wk0 + 31) >= W) && q0 < T_;
+        if (!active) continue;
+        const f32x16 s = mma_rows<D>(ldsQ, l32, hi, kv, f32x16{});  // S: rows queries, column key
+        f32x16 dp;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) dp[v] = ldr[1][8 * (v >> 2) + 4 * hi + (v & 3)];
+        dp = mma_rows<D>(ldsO, l32, hi, vv, dp);  // dP - delta
+        float pw[16], ds[16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int r = 8 * (v >> 2) + 4 * hi + (v & 3);
+            const int q = q0 + r;
+            float y, rr;
+            weight_rr<EXACT>(s[v], sc, y, rr);
+            const float yi = y * ldr[0][r];
+            const bool ok = static_cast<unsigned>(q - kj) < weff && q < T_;
+            pw[v] = ok ? yi : 0.f;
+            ds[v] = ok ? dp[v] * yi * rr : 0.f;
+        }
+        mma_cols<D>(ldsOt, l32, hi, pw, dvacc);  // dV^T += dO^T P
+        mma_cols<D>(ldsQt, l32, hi, ds, dkacc);  // dK^T += Q^T dS
+    }
+    if (kj < T_) {
+        store_cols<D>(p.dk + b * p.dks[0] + hk * p.dks[1] + kj * p.dks[2], hi, dkacc, 2.f * sc);
+        store_cols<D>(p.dv + b * p.dvs[0] + hk * p.dvs[1] + kj * p.dvs[2], hi, dvacc, 1.f);
+    }
+}
+
+// fp32 tensors: (b, h, t) strides multiples of 4 elements (16-byte rows), d stride 1.
+bool f32_strides_ok(const int64_t* s) { return s[3] == 1 && s[0] % 4 == 0 && s[1] % 4 == 0 && s[2] % 4 == 0; }
+
+int check_common(int B, int Hq, int Hkv, int T, int D, int window_size) {
+    if (B < 0 || Hq <= 0 || Hkv <= 0 || T < 0 || Hq % Hkv != 0 || window_size < 0) return SA_ERR_BAD_SHAPE;
+    if (D != 32 && D != 64 && D != 128) return SA_ERR_UNSUPPORTED;
+    return 0;
+}
+
+template <int D>
+int launch_fwd_f32_d(const F32Params& prm, int exact, hipStream_t st) {
+    const int64_t nblk = static_cast<int64_t>((prm.T + kFRows - 1) / kFRows) * prm.B * prm.Hq;
+    if (nblk * 64 * kFW >= (int64_t(1) << 32)) return SA_ERR_BAD_SHAPE;
+    const dim3 grid(static_cast<unsigned>(nblk));
+    if (exact)
+        flash_fwd_f32_kernel<D, true><<<grid, 64 * kFW, 0, st>>>(prm);
+    else
+        flash_fwd_f32_kernel<D, false><<<grid, 64 * kFW, 0, st>>>(prm);
+    return status_from_launch();
+}
+
+template <int D>
+int launch_bwd_f32_d(const F32Params& prm, int exact, hipStream_t st) {
+    const int64_t nq = static_cast<int64_t>((prm.T + kFRows - 1) / kFRows) * prm.B * prm.Hq;
+    if (nq * 64 * kFW >= (int64_t(1) << 32)) return SA_ERR_BAD_SHAPE;
+    const int64_t nk = nq / prm.G;
+    const dim3 gq(static_cast<unsigned>(nq)), gk(static_cast<unsigned>(nk));
+    if (exact) {
+        flash_bwd_dq_f32_kernel<D, true><<<gq, 64 * kFW, 0, st>>>(prm);
+        flash_bwd_dkdv_f32_kernel<D, true><<<gk, 64 * kFW, 0, st>>>(prm);
+    } else {
+        flash_bwd_dq_f32_kernel<D, false><<<gq, 64 * kFW, 0, st>>>(prm);
+        flash_bwd_dkdv_f32_kernel<D, false><<<gk, 64 * kFW, 0, st>>>(prm);
+    }
+    return status_from_launch();
+}
+
+}  // namespace
+
+int flash_fwd_f32(const void* q, const void* k, const void* v, void* o, float* row_sums, int B, int Hq, int Hkv,
+                  int T, int D, const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                  const int64_t* o_strides, float scale, int window_size, int exact_math, hipStream_t st) {
+    const int chk = check_common(B, Hq, Hkv, T, D, window_size);
+    if (chk != 0) return chk;
+    if (!q || !k || !v || !o || !q_strides || !k_strides || !v_strides || !o_strides) return SA_ERR_NULL_POINTER;
+    if (!f32_strides_ok(q_strides) || !f32_strides_ok(k_strides) || !f32_strides_ok(v_strides) ||
+        !f32_strides_ok(o_strides) || !aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
+        return SA_ERR_BAD_STRIDE;
+    if (B == 0 || T == 0) return 0;
+    F32Params prm{};
+    prm.q = static_cast<const float*>(q);
+    prm.k = static_cast<const float*>(k);
+    prm.v = static_cast<const float*>(v);
+    prm.out = static_cast<float*>(o);
+    prm.row_sums = row_sums;
+    for (int i = 0; i < 4; ++i) {
+        prm.qs[i] = q_strides[i];
+        prm.ks[i] = k_strides[i];
+        prm.vs[i] = v_strides[i];
+        prm.os[i] = o_strides[i];
+    }
+    prm.B = B;
+    prm.Hq = Hq;
+    prm.Hkv = Hkv;
+    prm.T = T;
+    prm.G = Hq / Hkv;
+    prm.window = window_size;
+    prm.scale = scale;
+    switch (D) {
+        case 32: return launch_fwd_f32_d<32>(prm, exact_math, st);
+        case 64: return launch_fwd_f32_d<64>(prm, exact_math, st);
+        default: return launch_fwd_f32_d<128>(prm, exact_math, st);
+    }
+}
+
+int flash_bwd_f32(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                  const float* row_sums, void* dq, void* dk, void* dv, float* delta_ws, int B, int Hq, int Hkv,
+                  int T, int D, const int64_t* const strides[8], float scale, int window_size, int exact_math,
+                  hipStream_t st) {
+    const int chk = check_common(B, Hq, Hkv, T, D, window_size);
+    if (chk != 0) return chk;
+    if (!q || !k || !v || !o || !dout || !row_sums || !dq || !dk || !dv || !delta_ws) return SA_ERR_NULL_POINTER;
+    const void* ptrs[8] = {q, k, v, o, dout, dq, dk, dv};
+    for (int i = 0; i < 8; ++i) {
+        if (!strides[i]) return SA_ERR_NULL_POINTER;
+        if (!f32_strides_ok(strides[i]) || !aligned16(ptrs[i])) return SA_ERR_BAD_STRIDE;
+    }
+    if (B == 0 || T == 0) return 0;
+    F32Params prm{};
+    prm.q = static_cast<const float*>(q);
+    prm.k = static_cast<const float*>(k);
+    prm.v = static_cast<const float*>(v);
+    prm.o = static_cast<const float*>(o);
+    prm.dout = static_cast<const float*>(dout);
+    prm.rs = row_sums;
+    prm.dq = static_cast<float*>(dq);
+    prm.dk = static_cast<float*>(dk);
+    prm.dv = static_cast<float*>(dv);
+    prm.delta = delta_ws;
+    int64_t* dst[8] = {prm.qs, prm.ks, prm.vs, prm.os, prm.dos, prm.dqs, prm.dks, prm.dvs};
+    for (int i = 0; i < 8; ++i)
+        for (int j = 0; j < 4; ++j) dst[i][j] = strides[i][j];
+    prm.B = B;
+    prm.Hq = Hq;
+    prm.Hkv = Hkv;
+    prm.T = T;
+    prm.G = Hq / Hkv;
+    prm.window = window_size;
+    prm.scale = scale;
+    switch (D) {
+        case 32: return launch_bwd_f32_d<32>(prm, exact_math, st);
+        case 64: return launch_bwd_f32_d<64>(prm, exact_math, st);
+        default: return launch_bwd_f32_d<128>(prm, exact_math, st);
+    }
+}
+
+}  // namespace sa

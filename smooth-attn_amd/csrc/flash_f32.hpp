@@ -1,0 +1,20 @@
+// fp32 fused attention (forward and backward) on the fp32 MFMA, reached from
+// sa_flash_fwd / sa_flash_bwd when dtype is SA_F32.
+#pragma once
+
+#include "common.hpp"
+
+namespace sa {
+
+// Validates and launches the fp32 forward (same contract as sa_flash_fwd).
+int flash_fwd_f32(const void* q, const void* k, const void* v, void* o, float* row_sums, int B, int Hq, int Hkv,
+                  int T, int D, const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                  const int64_t* o_strides, float scale, int window_size, int exact_math, hipStream_t st);
+
+// Validates and launches the fp32 backward (same contract as sa_flash_bwd).
+int flash_bwd_f32(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                  const float* row_sums, void* dq, void* dk, void* dv, float* delta_ws, int B, int Hq, int Hkv,
+                  int T, int D, const int64_t* const strides[8], float scale, int window_size, int exact_math,
+                  hipStream_t st);
+
+}  // namespace sa

@@ -26,6 +26,7 @@
 #include <type_traits>
 
 #include "flash_common.hpp"
+#include "flash_f32.hpp"
 
 namespace sa {
 namespace {
@@ -783,6 +784,9 @@ extern "C" int sa_flash_fwd(const void* q, const void* k, const void* v, void* o
                             const int64_t* v_strides, const int64_t* o_strides, float scale, int window_size,
                             int exact_math, int dtype, sa_stream_t stream) {
     using namespace sa;
+    if (dtype == SA_F32)
+        return flash_fwd_f32(q, k, v, o, row_sums, B, Hq, Hkv, T, D, q_strides, k_strides, v_strides, o_strides,
+                             scale, window_size, exact_math, reinterpret_cast<hipStream_t>(stream));
     if (dtype != SA_BF16 && dtype != SA_F16) return SA_ERR_BAD_DTYPE;
     FlashParams prm{};
     const int st = fill_params(prm, q, k, v, o, row_sums, B, Hq, Hkv, T, D, q_strides, k_strides, v_strides,

@@ -538,7 +538,7 @@ def sp2norm_flash_attention_eager(q, k, v, *, scale=None, window_size=0):
 
 
 # ---------------------------------------------------------------------------
-# Fused attention (bf16 / fp16 MFMA).
+# Fused attention (bf16 / fp16 / fp32 MFMA).
 # ---------------------------------------------------------------------------
 _FLASH_HEAD_DIMS = (32, 64, 128)
 
@@ -575,8 +575,10 @@ def _pad_head_dim(t, Dk):
 
 
 def _check_flash_dtypes(q, k, v):
-    if q.dtype not in (torch.bfloat16, torch.float16) or k.dtype != q.dtype or v.dtype != q.dtype:
-        raise ValueError(f"fused attention expects bf16 or fp16 q/k/v of one dtype, got "
+    """bf16 / fp16 run on the 16-bit MFMA kernels, fp32 on the fp32-MFMA ones
+    (products exact in fp32, P and dS kept in fp32)."""
+    if q.dtype not in (torch.bfloat16, torch.float16, torch.float32) or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError(f"fused attention expects bf16, fp16 or fp32 q/k/v of one dtype, got "
                          f"{q.dtype}/{k.dtype}/{v.dtype}")
 
 

@@ -272,19 +272,22 @@ def test_fused_entry_points_refuse_meta_tensors(case, no_library):
 
 def test_head_dims_and_page_sizes_checked_before_launch(no_library):
     # fused attention: any head dim up to 128 (zero-padded to 32 / 64 / 128
-    # for the kernels); above 128 and fp32 q/k/v are refused with a clear
-    # error; paged decode: power-of-two page sizes only
+    # for the kernels); above 128, fp64 and mixed dtypes are refused with a
+    # clear error; paged decode: power-of-two page sizes only
     mk = lambda shape, dtype: _OnDevice.make(torch.zeros(shape, dtype=dtype), 0)
     for D in (160, 256):
         q = mk((1, 2, 8, D), torch.bfloat16)
         with pytest.raises(ValueError, match="head dims 1..128"):
             kernels._sp2norm_flash_fwd(q, q, q, 0.1)
     assert [kernels._kernel_head_dim(d) for d in (1, 16, 32, 33, 64, 96, 128)] == [32, 32, 32, 64, 64, 128, 128]
-    q = mk((1, 2, 8, 64), torch.float32)
-    with pytest.raises(ValueError, match="bf16 or fp16"):
+    q = mk((1, 2, 8, 64), torch.float64)
+    with pytest.raises(ValueError, match="bf16, fp16 or fp32"):
         kernels._sp2norm_flash_fwd(q, q, q, 0.1)
-    with pytest.raises(ValueError, match="bf16 or fp16"):
+    with pytest.raises(ValueError, match="bf16, fp16 or fp32"):
         kernels._sp2norm_flash_bwd(q, q, q, q, q, mk((1, 2, 8), torch.float32), 0.1)
+    q32, k16 = mk((1, 2, 8, 64), torch.float32), mk((1, 2, 8, 64), torch.bfloat16)
+    with pytest.raises(ValueError, match="of one dtype"):
+        kernels._sp2norm_flash_fwd(q32, k16, k16, 0.1)
     qd = torch.zeros(2, 4, 1, 32, dtype=torch.bfloat16)
     kc = torch.zeros(4, 2, 12, 32, dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="power of two"):
