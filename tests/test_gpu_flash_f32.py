@@ -1,0 +1,174 @@
+"""Parity of the fp32 fused attention (forward and backward on the fp32 MFMA)
+with the float64 CPU oracle (GPU).
+
+fp32 q/k/v run on v_mfma_f32_32x32x2_f32: products exact in fp32, sums in
+fp32, P and dS kept in fp32.  Tolerance 1e-5: every output and gradient
+max|HIP - oracle| / max(max|oracle|, 1e-2) <= 1e-5.  Where a true gradient
+vanishes (every query sees one key: T = 1 or window 1, so dQ = dK = 0) the
+HIP result is the fp32 rounding of dP - delta, and those gradients are held
+to max|HIP| <= 1e-5 instead (inputs of unit scale).  The
+reference runs fp32 inputs through Triton's default TF32 dots
+(kernels.py:1582-1631, tl.dot without input_precision), so its own fp32
+results carry ~1e-3 relative error; these kernels are held to fp32
+accuracy instead.  Backward oracle: the reference's formula
+(oracle.eager.flash_attention_bwd, pinned against autograd) fed the HIP
+forward's O, as in the 16-bit tests.
+"""
+import math
+
+import pytest
+import torch
+
+import smooth_attn
+from oracle import eager
+from smooth_attn import kernels
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = 1e-5
+F32 = torch.float32
+
+
+def _g(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def rel_err(got, ref, floor=1e-30):
+    got = got.detach().double().cpu()
+    ref = ref.detach().double().cpu()
+    return float((got - ref).abs().max() / max(float(ref.abs().max()), floor))
+
+
+def inputs(B, Hq, Hkv, T, D, seed, layout="bhtd"):
+    g = _g(seed)
+    if layout == "bthd":  # [B,T,H,D].transpose(1,2): non-contiguous, as in the reference tests
+        q = torch.randn(B, T, Hq, D, generator=g).transpose(1, 2)
+        k = torch.randn(B, T, Hkv, D, generator=g).transpose(1, 2)
+        v = torch.randn(B, T, Hkv, D, generator=g).transpose(1, 2)
+        do = torch.randn(B, T, Hq, D, generator=g).transpose(1, 2)
+    else:
+        q = torch.randn(B, Hq, T, D, generator=g)
+        k = torch.randn(B, Hkv, T, D, generator=g)
+        v = torch.randn(B, Hkv, T, D, generator=g)
+        do = torch.randn(B, Hq, T, D, generator=g)
+    return q, k, v, do
+
+
+def check_forward(q, k, v, window=0, exact=False, scale=None):
+    D = q.shape[-1]
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    o, rs = kernels._sp2norm_flash_fwd(q.to(DEV), k.to(DEV), v.to(DEV), scale, q.shape[1] // k.shape[1], window,
+                                       use_fast_sqrt=not exact)
+    ref, ref_rs = eager.flash_attention_eager(q.double(), k.double(), v.double(), scale=scale, window_size=window,
+                                              return_row_sums=True)
+    assert o.dtype == F32 and o.shape == q.shape
+    assert bool(torch.isfinite(o).all())
+    err = rel_err(o, ref)
+    assert err <= TOL, f"o: rel err {err:.3e}"
+    assert rel_err(rs, ref_rs) <= TOL
+    return o, rs
+
+
+def check_backward(q, k, v, do, window=0, exact=False, scale=None):
+    vanishing = q.shape[2] == 1 or window == 1  # one visible key per query: dQ = dK = 0
+    D = q.shape[-1]
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    G = q.shape[1] // k.shape[1]
+    qd, kd, vd, dod = (t.to(DEV) for t in (q, k, v, do))
+    o, rs = kernels._sp2norm_flash_fwd(qd, kd, vd, scale, G, window, use_fast_sqrt=not exact)
+    grads = kernels._sp2norm_flash_bwd(qd, kd, vd, o, dod, rs, scale, G, window, use_fast_sqrt=not exact)
+    refs = eager.flash_attention_bwd(q.double(), k.double(), v.double(), o.cpu().double(), do.double(),
+                                     scale=scale, window_size=window)
+    for name, got, ref, src in zip(("dq", "dk", "dv"), grads, refs, (q, k, v)):
+        assert got.shape == src.shape and got.dtype == F32, name
+        assert bool(torch.isfinite(got).all()), name
+        if vanishing and name != "dv":
+            assert float(ref.abs().max()) <= TOL and float(got.abs().max()) <= TOL, name
+            continue
+        err = rel_err(got, ref, floor=1e-2)
+        assert err <= TOL, f"{name}: rel err {err:.3e}"
+    return grads
+
+
+@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("T", [1, 17, 64, 100, 128, 200, 512])
+def test_forward_matches_oracle(D, T):
+    q, k, v, _ = inputs(2, 2, 2, T, D, seed=D * 1000 + T)
+    check_forward(q, k, v)
+
+
+@pytest.mark.parametrize("hq,hkv,window", [(4, 1, 0), (4, 2, 7), (8, 2, 64), (4, 4, 1), (6, 3, 300)])
+def test_forward_gqa_window(hq, hkv, window):
+    q, k, v, _ = inputs(1, hq, hkv, 300, 64, seed=hq * 100 + window)
+    check_forward(q, k, v, window=window)
+
+
+def test_forward_exact_math_and_layouts():
+    q, k, v, _ = inputs(2, 4, 2, 257, 128, seed=5, layout="bthd")
+    check_forward(q, k, v, exact=True)
+    check_forward(q, k, v, window=33)
+
+
+@pytest.mark.parametrize("scale", [0.01, 0.5, 2.0])
+def test_forward_scales(scale):
+    q, k, v, _ = inputs(1, 2, 1, 200, 64, seed=int(scale * 100))
+    check_forward(q, k, v, scale=scale)
+
+
+@pytest.mark.parametrize("D", [1, 8, 48, 96])
+def test_forward_head_dims_below_128(D):
+    q, k, v, _ = inputs(1, 4, 2, 150, D, seed=D)
+    o, _ = check_forward(q, k, v)
+    assert o.is_contiguous() and o.shape == (1, 4, 150, D)
+
+
+def test_forward_long_sequence_sampled():
+    # T = 2048 with D = 128: fp32 accumulation over up to 2048 keys still meets 1e-5
+    q, k, v, _ = inputs(1, 2, 1, 2048, 128, seed=11)
+    o, rs = kernels._sp2norm_flash_fwd(q.to(DEV), k.to(DEV), v.to(DEV), 1 / math.sqrt(128), 2)
+    ref, ref_rs = eager.flash_attention_eager(q.double(), k.double(), v.double(), return_row_sums=True)
+    assert rel_err(o, ref) <= TOL and rel_err(rs, ref_rs) <= TOL
+
+
+@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("T", [1, 17, 64, 100, 128, 200, 300])
+def test_backward_matches_oracle(D, T):
+    q, k, v, do = inputs(2, 2, 2, T, D, seed=D * 1000 + T + 1)
+    check_backward(q, k, v, do)
+
+
+@pytest.mark.parametrize("hq,hkv,window", [(4, 1, 0), (4, 2, 7), (8, 2, 64), (6, 3, 300)])
+def test_backward_gqa_window(hq, hkv, window):
+    q, k, v, do = inputs(1, hq, hkv, 300, 64, seed=hq * 100 + window + 1)
+    check_backward(q, k, v, do, window=window)
+
+
+def test_backward_exact_math_layouts_and_head_dims():
+    q, k, v, do = inputs(2, 4, 2, 257, 128, seed=6, layout="bthd")
+    check_backward(q, k, v, do, exact=True)
+    for D in (8, 48, 96):
+        q, k, v, do = inputs(1, 2, 1, 130, D, seed=D)
+        check_backward(q, k, v, do, window=50)
+
+
+def test_backward_window_one_is_identity():
+    # window 1: each query sees only its own key, O = V, dV = dO summed over
+    # the GQA group, dQ = dK = 0 up to rounding
+    q, k, v, do = inputs(1, 4, 2, 100, 64, seed=3)
+    o, _ = check_forward(q, k, v, window=1)
+    assert torch.allclose(o.cpu(), v.repeat_interleave(2, dim=1), rtol=1e-6, atol=1e-6)
+    dq, dk, dv = check_backward(q, k, v, do, window=1)
+    assert torch.allclose(dv.cpu(), do.view(1, 2, 2, 100, 64).sum(2), rtol=1e-5, atol=1e-5)
+
+
+def test_public_autograd_fp32():
+    q, k, v, do = inputs(2, 4, 2, 160, 64, seed=9)
+    qd, kd, vd = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
+    out = smooth_attn.sp2norm_flash_attention(qd, kd, vd, window_size=40)
+    out.backward(do.to(DEV))
+    qr, kr, vr = (t.double().requires_grad_(True) for t in (q, k, v))
+    ref = eager.flash_attention_eager(qr, kr, vr, window_size=40)
+    ref.backward(do.double())
+    assert out.dtype == F32 and rel_err(out, ref) <= TOL
+    for got, want in ((qd.grad, qr.grad), (kd.grad, kr.grad), (vd.grad, vr.grad)):
+        assert rel_err(got, want, floor=1e-2) <= TOL
