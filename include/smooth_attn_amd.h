@@ -166,7 +166,7 @@ int sa_softmax_fwd_launch_info(const void* x, const void* y, int64_t n_rows,
  * 16-bit type, 4 of fp32), base pointers 16-byte aligned, and for bf16/fp16
  * K and V row strides at most 16 MiB.  row_sums (nullable): fp32 [B, Hq, T] contiguous,
  * receives sum_j y_ij + 1e-12.  window_size 0 = full causal.  D in {32, 64,
- * 128}.  exact_math != 0 selects a correctly rounded sqrt.
+ * 128, 256}.  exact_math != 0 selects a correctly rounded sqrt.
  * Replaces _sp2norm_flash_fwd (kernels.py:1912-1931) and its kernel
  * _sp2norm_flash_fwd_with_rowsum_kernel (:1536-1631).
  */
@@ -214,7 +214,7 @@ int sa_fp8_quantize(const void* x, void* x8, int64_t n, int dtype,
  * ignored, may be NULL, for bf16 v).  Scores = (q8 . k8) * q_s * k_s *
  * attn_scale on fp8 MFMA; y rounded to bf16 and multiplied with v (as bf16)
  * on bf16 MFMA, times v_s.  o: bf16 [B, Hq, T, D]; row_sums nullable.
- * Layout rules as sa_flash_fwd.
+ * Layout rules as sa_flash_fwd; D in {32, 64, 128}.
  * Replaces _sp2norm_fp8_flash_fwd (kernels.py:2604-2627) and its kernel
  * _sp2norm_fp8_flash_fwd_kernel (:2498-2589).
  */

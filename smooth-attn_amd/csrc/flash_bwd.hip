@@ -30,6 +30,7 @@
 // buffered, one barrier per tile), as in the forward.
 #include "flash_common.hpp"
 #include "flash_f32.hpp"
+#include "flash_wide.hpp"
 
 namespace sa {
 namespace {
@@ -622,6 +623,12 @@ extern "C" int sa_flash_bwd(const void* q, const void* k, const void* v, const v
                              window_size, exact_math, reinterpret_cast<hipStream_t>(stream));
     }
     if (dtype != SA_BF16 && dtype != SA_F16) return SA_ERR_BAD_DTYPE;
+    if (D == 256) {
+        const int64_t* const all[8] = {q_strides,  k_strides,  v_strides,  o_strides,
+                                       do_strides, dq_strides, dk_strides, dv_strides};
+        return flash_bwd_wide(q, k, v, o, dout, row_sums, dq, dk, dv, delta_ws, B, Hq, Hkv, T, D, all, scale,
+                              window_size, exact_math, dtype, reinterpret_cast<hipStream_t>(stream));
+    }
     if (B < 0 || Hq <= 0 || Hkv <= 0 || T < 0 || Hq % Hkv != 0 || window_size < 0) return SA_ERR_BAD_SHAPE;
     if (!q || !k || !v || !o || !dout || !row_sums || !dq || !dk || !dv || !delta_ws) return SA_ERR_NULL_POINTER;
     if (!q_strides || !k_strides || !v_strides || !o_strides || !do_strides || !dq_strides || !dk_strides ||

@@ -180,7 +180,7 @@ __device__ __forceinline__ void store_cols(float* row, int hi, const f32x16 (&ac
 // (10.1 vs 8.2 ms for the backward); the D = 128 backward kernels spill at two
 // waves and are still faster (21.4 vs 22.0 ms).
 template <int D, bool EXACT>
-__global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(2, 8))) void flash_fwd_f32_kernel(F32Params p) {
+__global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 128 ? 1 : 2, 8))) void flash_fwd_f32_kernel(F32Params p) {
     __shared__ __attribute__((aligned(16))) float ldsK[kFT * (D + 4)];
     __shared__ __attribute__((aligned(16))) float ldsVt[D * kTP];
     const int tid = threadIdx.x;
@@ -257,7 +257,7 @@ __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(2, 8))
 // Backward: dQ (and delta)
 // ---------------------------------------------------------------------------
 template <int D, bool EXACT>
-__global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(2, 8))) void flash_bwd_dq_f32_kernel(F32Params p) {
+__global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 128 ? 1 : 2, 8))) void flash_bwd_dq_f32_kernel(F32Params p) {
     __shared__ __attribute__((aligned(16))) float ldsK[kFT * (D + 4)];
     __shared__ __attribute__((aligned(16))) float ldsKt[D * kTP];
     __shared__ __attribute__((aligned(16))) float ldsV[kFT * (D + 4)];
@@ -350,7 +350,7 @@ __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(2, 8))
 // Backward: dK, dV
 // ---------------------------------------------------------------------------
 template <int D, bool EXACT>
-__global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(2, 8))) void flash_bwd_dkdv_f32_kernel(F32Params p) {
+__global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 128 ? 1 : 2, 8))) void flash_bwd_dkdv_f32_kernel(F32Params p) {
     __shared__ __attribute__((aligned(16))) float ldsQ[kFT * (D + 4)];
     __shared__ __attribute__((aligned(16))) float ldsQt[D * kTP];
     __shared__ __attribute__((aligned(16))) float ldsO[kFT * (D + 4)];
@@ -450,7 +450,7 @@ bool f32_strides_ok(const int64_t* s) { return s[3] == 1 && s[0] % 4 == 0 && s[1
 
 int check_common(int B, int Hq, int Hkv, int T, int D, int window_size) {
     if (B < 0 || Hq <= 0 || Hkv <= 0 || T < 0 || Hq % Hkv != 0 || window_size < 0) return SA_ERR_BAD_SHAPE;
-    if (D != 32 && D != 64 && D != 128) return SA_ERR_UNSUPPORTED;
+    if (D != 32 && D != 64 && D != 128 && D != 256) return SA_ERR_UNSUPPORTED;
     return 0;
 }
 
@@ -516,7 +516,8 @@ int flash_fwd_f32(const void* q, const void* k, const void* v, void* o, float* r
     switch (D) {
         case 32: return launch_fwd_f32_d<32>(prm, exact_math, st);
         case 64: return launch_fwd_f32_d<64>(prm, exact_math, st);
-        default: return launch_fwd_f32_d<128>(prm, exact_math, st);
+        case 128: return launch_fwd_f32_d<128>(prm, exact_math, st);
+        default: return launch_fwd_f32_d<256>(prm, exact_math, st);
     }
 }
 
@@ -557,7 +558,8 @@ int flash_bwd_f32(const void* q, const void* k, const void* v, const void* o, co
     switch (D) {
         case 32: return launch_bwd_f32_d<32>(prm, exact_math, st);
         case 64: return launch_bwd_f32_d<64>(prm, exact_math, st);
-        default: return launch_bwd_f32_d<128>(prm, exact_math, st);
+        case 128: return launch_bwd_f32_d<128>(prm, exact_math, st);
+        default: return launch_bwd_f32_d<256>(prm, exact_math, st);
     }
 }
 

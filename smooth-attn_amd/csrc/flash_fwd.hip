@@ -27,6 +27,7 @@
 
 #include "flash_common.hpp"
 #include "flash_f32.hpp"
+#include "flash_wide.hpp"
 
 namespace sa {
 namespace {
@@ -788,6 +789,9 @@ extern "C" int sa_flash_fwd(const void* q, const void* k, const void* v, void* o
         return flash_fwd_f32(q, k, v, o, row_sums, B, Hq, Hkv, T, D, q_strides, k_strides, v_strides, o_strides,
                              scale, window_size, exact_math, reinterpret_cast<hipStream_t>(stream));
     if (dtype != SA_BF16 && dtype != SA_F16) return SA_ERR_BAD_DTYPE;
+    if (D == 256)
+        return flash_fwd_wide(q, k, v, o, row_sums, B, Hq, Hkv, T, D, q_strides, k_strides, v_strides, o_strides,
+                              scale, window_size, exact_math, dtype, reinterpret_cast<hipStream_t>(stream));
     FlashParams prm{};
     const int st = fill_params(prm, q, k, v, o, row_sums, B, Hq, Hkv, T, D, q_strides, k_strides, v_strides,
                                o_strides, scale, window_size, 2, 2);

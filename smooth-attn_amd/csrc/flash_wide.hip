@@ -1,0 +1,595 @@
+// 16-bit (bf16 / fp16) fused causal squareplus attention at head dim 256,
+// forward and backward, on v_mfma_f32_32x32x16_{bf16,f16}.  Head dims
+// 129..255 reach it zero-padded.
+//
+// Same mathematics and rounding points as the D <= 128 kernels
+// (flash_fwd.hip, flash_bwd.hip; reference kernels.py:1536-1631 and
+// :1667-1909): fp32 scores and weights, P and dS rounded to the input type
+// before their products, fp32 accumulation, row sums of the fp32 weights.
+// At D = 256 the O accumulators alone take 128 registers per lane, so these
+// kernels run one wave per SIMD with the accumulators in AGPRs and a simpler
+// structure than the D <= 128 ones: blocks of 4 waves x 32 rows, 32-row tiles
+// staged through registers into LDS (the next tile's loads in flight during
+// the current tile's MFMAs), two barriers per tile.  dK and dV are separate
+// kernels: together they would need 256 accumulator registers plus 128 for
+// the K and V operands and spill.
+//
+// Operands (the 32x32x16 layout and the transposing LDS read are described
+// in flash_common.hpp).  For contractions over D, chunk c of a lane's operand
+// is elements 16c + 8 (l / 32) .. +7 of its row: Q, dO (forward, dQ) or K, V
+// (dK, dV) stay in registers, the other side is a 16-byte read of a
+// row-major LDS tile.  For contractions over keys (or queries) the B operand
+// is the lane's own 16 C-layout values v = 8j .. 8j + 7, whose k slots are
+// rows 16j + 8 (i / 4) + 4 (l / 32) + i % 4 of the tile (i = 0..7), so the A
+// operand is a pair of transposing reads of a row-major tile (4 rows each).
+// The two read patterns want different row pitches to be free of bank
+// conflicts (16 rows x 16 bytes: a pitch of 4 banks mod 64; the transposing
+// read's 4 rows x 32 bytes per 16 lanes: 16 banks), so a tile read both ways
+// is stored twice, at pitch D + 8 and D + 32 elements.
+#include "flash_common.hpp"
+#include "flash_wide.hpp"
+
+namespace sa {
+namespace {
+
+constexpr int kWW = 4;            // waves per block
+constexpr int kWT = 32;           // rows per staged tile
+constexpr int kWRows = 32 * kWW;  // rows a block owns
+
+template <int D>
+struct WPitch {
+    static constexpr int ROW = D + 8;   // row reads: 16 rows x 16 bytes, conflict-free
+    static constexpr int TR = D + 32;   // transposing reads: 4 rows x 32 bytes per 16 lanes
+};
+
+template <typename E>
+struct WideParams {
+    const E* q;
+    const E* k;
+    const E* v;
+    const E* o;     // backward input
+    const E* dout;  // backward input
+    const float* rs;  // backward input: forward row sums [B, Hq, T]
+    E* out;           // forward output
+    float* row_sums;  // forward output (nullable)
+    E* dq;
+    E* dk;
+    E* dv;
+    float* delta;  // [B, Hq, T]
+    int64_t qs[4], ks[4], vs[4], os[4], dos[4], dqs[4], dks[4], dvs[4];
+    int B, Hq, Hkv, T, G, window;
+    float scale;
+};
+
+// One [kWT][D] tile (rows r0.., clamped to T - 1) held in registers between
+// its global loads and its LDS stores; a thread unit is one 16-byte chunk.
+template <typename T, int D>
+struct WTile {
+    static constexpr int CPR = D / 8;                  // 16-byte chunks per row
+    static constexpr int PER = kWT * CPR / (64 * kWW);  // chunks per thread
+    u32x4 x[PER];
+    __device__ __forceinline__ void load(const T* base, int64_t rstride, int r0, int T_, int tid) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int idx = tid + 64 * kWW * i;
+            const int r = idx / CPR;
+            const int c = idx - r * CPR;
+            x[i] = *reinterpret_cast<const u32x4*>(base + static_cast<int64_t>(min(r0 + r, T_ - 1)) * rstride +
+                                                   8 * c);
+        }
+    }
+    // row-major copies at pitch WPitch::ROW (nullable) and WPitch::TR (nullable)
+    __device__ __forceinline__ void store(T* rows, T* trs, int tid) const {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int idx = tid + 64 * kWW * i;
+            const int r = idx / CPR;
+            const int c = idx - r * CPR;
+            if (rows != nullptr) *reinterpret_cast<u32x4*>(rows + r * WPitch<D>::ROW + 8 * c) = x[i];
+            if (trs != nullptr) *reinterpret_cast<u32x4*>(trs + r * WPitch<D>::TR + 8 * c) = x[i];
+        }
+    }
+};
+
+// y = squareplus(2 s scale - 1)^2 = (a + r)^2, a = s scale - 1/2,
+// r = sqrt(a^2 + 1); rr = 1 / r.
+template <bool EXACT>
+__device__ __forceinline__ void weight_rr16(float s, float sc, float& y, float& rr) {
+    const float a = __builtin_fmaf(s, sc, -0.5f);
+    const float u = __builtin_fmaf(a, a, 1.f);
+    float r;
+    if constexpr (EXACT) {
+        r = __builtin_sqrtf(u);
+        rr = 1.f / r;
+    } else {
+        rr = fast_rsqrt(u);
+        r = u * rr;
+    }
+    const float sp = a + r;
+    y = sp * sp;
+}
+
+// A lane's D / 16 operand chunks of one row: x[c] = row[16c + 8 hi .. +7].
+template <int D, typename T>
+__device__ __forceinline__ void load_frags(const T* row, int hi, u32x4 (&x)[D / 16]) {
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) x[c] = *reinterpret_cast<const u32x4*>(row + 16 * c + 8 * hi);
+}
+
+// C += A B^T over D: A rows from a row-major LDS tile at pitch ROW (row
+// l32), B from a lane's register chunks.
+template <typename T, int D>
+__device__ __forceinline__ f32x16 mma_rows16(const T* lds_rows, int l32, int hi, const u32x4 (&b)[D / 16],
+                                             f32x16 c) {
+    using V8 = typename MfmaOps<T>::vec8;
+    const T* ar = lds_rows + l32 * WPitch<D>::ROW + 8 * hi;
+#pragma unroll
+    for (int i = 0; i < D / 16; ++i)
+        c = MfmaOps<T>::mma(as_vec8<V8>(*reinterpret_cast<const u32x4*>(ar + 16 * i)), as_vec8<V8>(b[i]), c);
+    return c;
+}
+
+// Pack a lane's 16 C-layout values as the two B operands over the tile rows.
+template <typename T>
+__device__ __forceinline__ void pack_b(const float (&x)[16], u32x4 (&w)[2]) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+        w[j] = u32x4{pack2<T>(x[8 * j + 0], x[8 * j + 1]), pack2<T>(x[8 * j + 2], x[8 * j + 3]),
+                     pack2<T>(x[8 * j + 4], x[8 * j + 5]), pack2<T>(x[8 * j + 6], x[8 * j + 7])};
+}
+
+// acc[dt] (rows d = 32 dt + ..) += A^T(d, r) X(r, col) over the tile's 32
+// rows r: A^T by transposing reads of a row-major tile at pitch TR (lane
+// supplies row 4 (l / 32) + (l % 16) / 4, column 32 dt + 16 ((l / 16) % 2) +
+// 4 (l % 4); the 16 lanes of its group receive column 32 dt + l % 32 of rows
+// +0..3), X the packed B operands.
+template <typename T, int D>
+__device__ __forceinline__ void mma_cols16(const T* lds_tr, int lane, const u32x4 (&x)[2],
+                                           f32x16 (&acc)[D / 32]) {
+    using V8 = typename MfmaOps<T>::vec8;
+    constexpr int P = WPitch<D>::TR;
+    const T* base = lds_tr + (4 * (lane >> 5) + ((lane & 15) >> 2)) * P + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const T* p0 = base + 16 * j * P + 32 * dt;
+            acc[dt] = MfmaOps<T>::mma(lds_read_tr16_pair<V8>(p0, p0 + 8 * P), as_vec8<V8>(x[j]), acc[dt]);
+        }
+    }
+}
+
+// Write a lane's C-layout rows of acc (d = 32 dt + 8 m + 4 hi .. +3) times f
+// into its output row as 8-byte stores.
+template <typename T, int D>
+__device__ __forceinline__ void store_cols16(T* row, int hi, const f32x16 (&acc)[D / 32], float f) {
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const uint2 w{pack2<T>(acc[dt][4 * m + 0] * f, acc[dt][4 * m + 1] * f),
+                          pack2<T>(acc[dt][4 * m + 2] * f, acc[dt][4 * m + 3] * f)};
+            *reinterpret_cast<uint2*>(row + dt * 32 + 8 * m + 4 * hi) = w;
+        }
+    }
+}
+
+// Query blocks of kWRows rows, heaviest (latest) first, over (b, hq).
+struct QBlock {
+    int qb, b, hq;
+    __device__ __forceinline__ QBlock(int id, int T_, int B, int Hq) {
+        const int nqb = (T_ + kWRows - 1) / kWRows;
+        const int per = B * Hq;
+        const int step = id / per;
+        const int rest = id - step * per;
+        qb = nqb - 1 - step;
+        b = rest / Hq;
+        hq = rest - b * Hq;
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Forward
+// ---------------------------------------------------------------------------
+template <typename T, int D, bool EXACT>
+__global__ __launch_bounds__(64 * kWW) void flash_fwd_wide_kernel(WideParams<T> p) {
+    __shared__ __attribute__((aligned(16))) T ldsK[kWT * WPitch<D>::ROW];
+    __shared__ __attribute__((aligned(16))) T ldsV[kWT * WPitch<D>::TR];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int hi = lane >> 5;
+    const int l32 = lane & 31;
+    const int T_ = p.T;
+    const QBlock blk(blockIdx.x, T_, p.B, p.Hq);
+    const int qb = blk.qb, b = blk.b, hq = blk.hq;
+    const int hk = hq / p.G;
+    const T* kp = p.k + b * p.ks[0] + hk * p.ks[1];
+    const T* vp = p.v + b * p.vs[0] + hk * p.vs[1];
+
+    const int q0 = qb * kWRows + 32 * wave;
+    const int qi = q0 + l32;
+    const int qrow = min(qi, T_ - 1);
+    u32x4 qf[D / 16];
+    load_frags<D>(p.q + b * p.qs[0] + hq * p.qs[1] + qrow * p.qs[2], hi, qf);
+
+    f32x16 oacc[D / 32];
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) oacc[dt] = f32x16{};
+    float ssum = 0.f;
+    const int W = p.window;
+    const unsigned weff = W > 0 ? static_cast<unsigned>(W) : 0x7FFFFFFFu;
+    const int n_kv = (T_ + kWT - 1) / kWT;
+    const int kv_end = min((qb * kWRows + kWRows + kWT - 1) / kWT, n_kv);
+    const int kv_begin = W > 0 ? max(0, qb * kWRows - W + 1) / kWT : 0;
+    const float sc = p.scale;
+
+    WTile<T, D> kreg, vreg;
+    kreg.load(kp, p.ks[2], kv_begin * kWT, T_, tid);
+    vreg.load(vp, p.vs[2], kv_begin * kWT, T_, tid);
+    for (int t = kv_begin; t < kv_end; ++t) {
+        __syncthreads();  // every wave is done with tile t - 1
+        kreg.store(ldsK, nullptr, tid);
+        vreg.store(nullptr, ldsV, tid);
+        __syncthreads();
+        if (t + 1 < kv_end) {
+            kreg.load(kp, p.ks[2], (t + 1) * kWT, T_, tid);
+            vreg.load(vp, p.vs[2], (t + 1) * kWT, T_, tid);
+        }
+        const int k0 = t * kWT;
+        const bool active = k0 <= q0 + 31 && !(W > 0 && q0 - (k0 + 31) >= W);
+        if (!active) continue;
+        const f32x16 s = mma_rows16<T, D>(ldsK, l32, hi, qf, f32x16{});  // S^T: rows keys, column query
+        float y[16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int key = k0 + 8 * (v >> 2) + 4 * hi + (v & 3);
+            float w, rr;
+            weight_rr16<EXACT>(s[v], sc, w, rr);
+            y[v] = static_cast<unsigned>(qi - key) < weff ? w : 0.f;
+            ssum += y[v];
+        }
+        u32x4 pw[2];
+        pack_b<T>(y, pw);
+        mma_cols16<T, D>(ldsV, lane, pw, oacc);  // O^T += V^T P^T
+    }
+
+    const float tot = ssum + __shfl_xor(ssum, 32) + kEps;
+    if (qi < T_) {
+        store_cols16<T, D>(p.out + b * p.os[0] + hq * p.os[1] + qi * p.os[2], hi, oacc, 1.f / tot);
+        if (hi == 0 && p.row_sums != nullptr) p.row_sums[(static_cast<int64_t>(b) * p.Hq + hq) * T_ + qi] = tot;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Backward: dQ (and delta)
+// ---------------------------------------------------------------------------
+template <typename T, int D, bool EXACT>
+__global__ __launch_bounds__(64 * kWW) void flash_bwd_dq_wide_kernel(WideParams<T> p) {
+    __shared__ __attribute__((aligned(16))) T ldsK[kWT * WPitch<D>::ROW];
+    __shared__ __attribute__((aligned(16))) T ldsKt[kWT * WPitch<D>::TR];
+    __shared__ __attribute__((aligned(16))) T ldsV[kWT * WPitch<D>::ROW];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int hi = lane >> 5;
+    const int l32 = lane & 31;
+    const int T_ = p.T;
+    const QBlock blk(blockIdx.x, T_, p.B, p.Hq);
+    const int qb = blk.qb, b = blk.b, hq = blk.hq;
+    const int hk = hq / p.G;
+    const T* kp = p.k + b * p.ks[0] + hk * p.ks[1];
+    const T* vp = p.v + b * p.vs[0] + hk * p.vs[1];
+
+    const int q0 = qb * kWRows + 32 * wave;
+    const int qi = q0 + l32;
+    const int qrow = min(qi, T_ - 1);
+    u32x4 qf[D / 16], df[D / 16];
+    load_frags<D>(p.q + b * p.qs[0] + hq * p.qs[1] + qrow * p.qs[2], hi, qf);
+    load_frags<D>(p.dout + b * p.dos[0] + hq * p.dos[1] + qrow * p.dos[2], hi, df);
+    // delta = rowsum(dO * O) of this lane's query (lanes l and l ^ 32 hold the halves)
+    float dpart = 0.f;
+    {
+        const T* orow = p.o + b * p.os[0] + hq * p.os[1] + qrow * p.os[2];
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c) {
+            const u32x4 ov = *reinterpret_cast<const u32x4*>(orow + 16 * c + 8 * hi);
+            const uint32_t ow[4] = {ov[0], ov[1], ov[2], ov[3]};
+            const uint32_t dw[4] = {df[c][0], df[c][1], df[c][2], df[c][3]};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) dpart = __builtin_fmaf(elem<T>(dw, e), elem<T>(ow, e), dpart);
+        }
+    }
+    const float dl = dpart + __shfl_xor(dpart, 32);
+    const int64_t rbase = (static_cast<int64_t>(b) * p.Hq + hq) * T_;
+    if (qi < T_ && hi == 0) p.delta[rbase + qi] = dl;
+    const float inv_r = 1.f / p.rs[rbase + qrow];
+
+    f32x16 acc[D / 32];
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) acc[dt] = f32x16{};
+    f32x16 ndl;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) ndl[v] = -dl;
+    const int W = p.window;
+    const unsigned weff = W > 0 ? static_cast<unsigned>(W) : 0x7FFFFFFFu;
+    const int n_kv = (T_ + kWT - 1) / kWT;
+    const int kv_end = min((qb * kWRows + kWRows + kWT - 1) / kWT, n_kv);
+    const int kv_begin = W > 0 ? max(0, qb * kWRows - W + 1) / kWT : 0;
+    const float sc = p.scale;
+
+    WTile<T, D> kreg, vreg;
+    kreg.load(kp, p.ks[2], kv_begin * kWT, T_, tid);
+    vreg.load(vp, p.vs[2], kv_begin * kWT, T_, tid);
+    for (int t = kv_begin; t < kv_end; ++t) {
+        __syncthreads();
+        kreg.store(ldsK, ldsKt, tid);
+        vreg.store(ldsV, nullptr, tid);
+        __syncthreads();
+        if (t + 1 < kv_end) {
+            kreg.load(kp, p.ks[2], (t + 1) * kWT, T_, tid);
+            vreg.load(vp, p.vs[2], (t + 1) * kWT, T_, tid);
+        }
+        const int k0 = t * kWT;
+        const bool active = k0 <= q0 + 31 && !(W > 0 && q0 - (k0 + 31) >= W);
+        if (!active) continue;
+        const f32x16 s = mma_rows16<T, D>(ldsK, l32, hi, qf, f32x16{});  // S^T
+        const f32x16 dp = mma_rows16<T, D>(ldsV, l32, hi, df, ndl);     // dP^T - delta
+        float ds[16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int key = k0 + 8 * (v >> 2) + 4 * hi + (v & 3);
+            float y, rr;
+            weight_rr16<EXACT>(s[v], sc, y, rr);
+            ds[v] = static_cast<unsigned>(qi - key) < weff ? dp[v] * y * rr : 0.f;
+        }
+        u32x4 dsw[2];
+        pack_b<T>(ds, dsw);
+        mma_cols16<T, D>(ldsKt, lane, dsw, acc);  // dQ^T += K^T dS^T
+    }
+    // dS carried without its per-row factor 2 scale / R
+    if (qi < T_)
+        store_cols16<T, D>(p.dq + b * p.dqs[0] + hq * p.dqs[1] + qi * p.dqs[2], hi, acc, 2.f * sc * inv_r);
+}
+
+// ---------------------------------------------------------------------------
+// Backward: dV (DK = false) or dK (DK = true) of a block of 128 keys, walking
+// every query head of the GQA group and every 32-row query tile that sees
+// them.  dV needs only S (P = y / R); dK needs S and dP (dS).
+// ---------------------------------------------------------------------------
+template <typename T, int D, bool EXACT, bool DK>
+__global__ __launch_bounds__(64 * kWW) void flash_bwd_kv_wide_kernel(WideParams<T> p) {
+    // Q rows (S = Q K^T), and for dK: Q^T (dK^T += Q^T dS) and dO rows
+    // (dP = dO V^T); for dV: dO^T (dV^T += dO^T P).
+    __shared__ __attribute__((aligned(16))) T ldsQ[kWT * WPitch<D>::ROW];
+    __shared__ __attribute__((aligned(16))) T ldsTr[kWT * WPitch<D>::TR];
+    __shared__ __attribute__((aligned(16))) T ldsO[DK ? kWT * WPitch<D>::ROW : 8];
+    __shared__ __attribute__((aligned(16))) float ldr[2][kWT];  // [1/R, -delta] of the tile's rows
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int hi = lane >> 5;
+    const int l32 = lane & 31;
+    const int T_ = p.T;
+    const int per = p.B * p.Hkv;
+    const int kb = blockIdx.x / per;  // earliest key blocks (most queries) first
+    const int rest = blockIdx.x - kb * per;
+    const int b = rest / p.Hkv;
+    const int hk = rest - b * p.Hkv;
+
+    const int k_start = kb * kWRows;
+    const int wk0 = k_start + 32 * wave;
+    const int kj = wk0 + l32;
+    const int krow = min(kj, T_ - 1);
+    u32x4 kf[D / 16], vf[DK ? D / 16 : 1];
+    load_frags<D>(p.k + b * p.ks[0] + hk * p.ks[1] + krow * p.ks[2], hi, kf);
+    if constexpr (DK) load_frags<D>(p.v + b * p.vs[0] + hk * p.vs[1] + krow * p.vs[2], hi, vf);
+
+    f32x16 acc[D / 32];
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) acc[dt] = f32x16{};
+    const int W = p.window;
+    const unsigned weff = W > 0 ? static_cast<unsigned>(W) : 0x7FFFFFFFu;
+    const int n_qt = (T_ + kWT - 1) / kWT;
+    const int qt_begin = k_start / kWT;
+    const int qt_end = W > 0 ? min(n_qt, (k_start + kWRows - 1 + W - 1) / kWT + 1) : n_qt;
+    const int nq = qt_end - qt_begin;  // >= 1 (k_start < T)
+    const int n_it = p.G * nq;
+    const float sc = p.scale;
+
+    WTile<T, D> qreg, oreg;
+    float rst = 0.f;
+    auto fetch = [&](int it) {
+        const int g = it / nq;
+        const int q0 = (qt_begin + it - g * nq) * kWT;
+        const int hq = hk * p.G + g;
+        qreg.load(p.q + b * p.qs[0] + hq * p.qs[1], p.qs[2], q0, T_, tid);
+        oreg.load(p.dout + b * p.dos[0] + hq * p.dos[1], p.dos[2], q0, T_, tid);
+        if (tid < 2 * kWT) {
+            const int64_t idx = (static_cast<int64_t>(b) * p.Hq + hq) * T_ + min(q0 + (tid & (kWT - 1)), T_ - 1);
+            rst = tid < kWT ? 1.f / p.rs[idx] : -p.delta[idx];
+        }
+    };
+    fetch(0);
+    for (int it = 0; it < n_it; ++it) {
+        __syncthreads();
+        if constexpr (DK) {
+            qreg.store(ldsQ, ldsTr, tid);
+            oreg.store(ldsO, nullptr, tid);
+        } else {
+            qreg.store(ldsQ, nullptr, tid);
+            oreg.store(nullptr, ldsTr, tid);
+        }
+        if (tid < 2 * kWT) ldr[tid / kWT][tid & (kWT - 1)] = rst;
+        __syncthreads();
+        const int g = it / nq;
+        const int q0 = (qt_begin + it - g * nq) * kWT;
+        if (it + 1 < n_it) fetch(it + 1);
+        // some query of the tile sees some key of the wave
+        const bool active = q0 + 31 >= wk0 && !(W > 0 && q0 - (wk0 + 31) >= W);
+        if (!active) continue;
+        const f32x16 s = mma_rows16<T, D>(ldsQ, l32, hi, kf, f32x16{});  // S: rows queries, column key
+        f32x16 dp;
+        if constexpr (DK) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) dp[v] = ldr[1][8 * (v >> 2) + 4 * hi + (v & 3)];
+            dp = mma_rows16<T, D>(ldsO, l32, hi, vf, dp);  // dP - delta
+        }
+        float x[16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int r = 8 * (v >> 2) + 4 * hi + (v & 3);
+            const int q = q0 + r;
+            float y, rr;
+            weight_rr16<EXACT>(s[v], sc, y, rr);
+            const float yi = y * ldr[0][r];
+            const bool ok = static_cast<unsigned>(q - kj) < weff && q < T_;
+            if constexpr (DK) x[v] = ok ? dp[v] * yi * rr : 0.f;  // dS
+            else x[v] = ok ? yi : 0.f;                             // P
+        }
+        u32x4 xw[2];
+        pack_b<T>(x, xw);
+        mma_cols16<T, D>(ldsTr, lane, xw, acc);  // dK^T += Q^T dS, or dV^T += dO^T P
+    }
+    if (kj < T_) {
+        if constexpr (DK) store_cols16<T, D>(p.dk + b * p.dks[0] + hk * p.dks[1] + kj * p.dks[2], hi, acc, 2.f * sc);
+        else store_cols16<T, D>(p.dv + b * p.dvs[0] + hk * p.dvs[1] + kj * p.dvs[2], hi, acc, 1.f);
+    }
+}
+
+// 16-bit tensors: (b, h, t) strides multiples of 8 elements (16-byte rows), d stride 1.
+bool wide_strides_ok(const int64_t* s) { return s[3] == 1 && s[0] % 8 == 0 && s[1] % 8 == 0 && s[2] % 8 == 0; }
+
+int check_wide(int B, int Hq, int Hkv, int T, int D, int window_size, int dtype) {
+    if (dtype != SA_BF16 && dtype != SA_F16) return SA_ERR_BAD_DTYPE;
+    if (B < 0 || Hq <= 0 || Hkv <= 0 || T < 0 || Hq % Hkv != 0 || window_size < 0) return SA_ERR_BAD_SHAPE;
+    if (D != 256) return SA_ERR_UNSUPPORTED;
+    return 0;
+}
+
+template <typename T>
+int launch_fwd_wide(const WideParams<T>& prm, int exact, hipStream_t st) {
+    const int64_t nblk = static_cast<int64_t>((prm.T + kWRows - 1) / kWRows) * prm.B * prm.Hq;
+    if (nblk * 64 * kWW >= (int64_t(1) << 32)) return SA_ERR_BAD_SHAPE;
+    const dim3 grid(static_cast<unsigned>(nblk));
+    if (exact)
+        flash_fwd_wide_kernel<T, 256, true><<<grid, 64 * kWW, 0, st>>>(prm);
+    else
+        flash_fwd_wide_kernel<T, 256, false><<<grid, 64 * kWW, 0, st>>>(prm);
+    return status_from_launch();
+}
+
+template <typename T>
+int launch_bwd_wide(const WideParams<T>& prm, int exact, hipStream_t st) {
+    const int64_t nq = static_cast<int64_t>((prm.T + kWRows - 1) / kWRows) * prm.B * prm.Hq;
+    if (nq * 64 * kWW >= (int64_t(1) << 32)) return SA_ERR_BAD_SHAPE;
+    const int64_t nk = nq / prm.G;
+    const dim3 gq(static_cast<unsigned>(nq)), gk(static_cast<unsigned>(nk));
+    if (exact) {
+        flash_bwd_dq_wide_kernel<T, 256, true><<<gq, 64 * kWW, 0, st>>>(prm);
+        flash_bwd_kv_wide_kernel<T, 256, true, false><<<gk, 64 * kWW, 0, st>>>(prm);
+        flash_bwd_kv_wide_kernel<T, 256, true, true><<<gk, 64 * kWW, 0, st>>>(prm);
+    } else {
+        flash_bwd_dq_wide_kernel<T, 256, false><<<gq, 64 * kWW, 0, st>>>(prm);
+        flash_bwd_kv_wide_kernel<T, 256, false, false><<<gk, 64 * kWW, 0, st>>>(prm);
+        flash_bwd_kv_wide_kernel<T, 256, false, true><<<gk, 64 * kWW, 0, st>>>(prm);
+    }
+    return status_from_launch();
+}
+
+template <typename T>
+int run_fwd_wide(const void* q, const void* k, const void* v, void* o, float* row_sums, int B, int Hq, int Hkv,
+                 int T_, const int64_t* qs, const int64_t* ks, const int64_t* vs, const int64_t* os, float scale,
+                 int window_size, int exact_math, hipStream_t st) {
+    WideParams<T> prm{};
+    prm.q = static_cast<const T*>(q);
+    prm.k = static_cast<const T*>(k);
+    prm.v = static_cast<const T*>(v);
+    prm.out = static_cast<T*>(o);
+    prm.row_sums = row_sums;
+    for (int i = 0; i < 4; ++i) {
+        prm.qs[i] = qs[i];
+        prm.ks[i] = ks[i];
+        prm.vs[i] = vs[i];
+        prm.os[i] = os[i];
+    }
+    prm.B = B;
+    prm.Hq = Hq;
+    prm.Hkv = Hkv;
+    prm.T = T_;
+    prm.G = Hq / Hkv;
+    prm.window = window_size;
+    prm.scale = scale;
+    return launch_fwd_wide<T>(prm, exact_math, st);
+}
+
+template <typename T>
+int run_bwd_wide(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                 const float* row_sums, void* dq, void* dk, void* dv, float* delta_ws, int B, int Hq, int Hkv,
+                 int T_, const int64_t* const strides[8], float scale, int window_size, int exact_math,
+                 hipStream_t st) {
+    WideParams<T> prm{};
+    prm.q = static_cast<const T*>(q);
+    prm.k = static_cast<const T*>(k);
+    prm.v = static_cast<const T*>(v);
+    prm.o = static_cast<const T*>(o);
+    prm.dout = static_cast<const T*>(dout);
+    prm.rs = row_sums;
+    prm.dq = static_cast<T*>(dq);
+    prm.dk = static_cast<T*>(dk);
+    prm.dv = static_cast<T*>(dv);
+    prm.delta = delta_ws;
+    int64_t* dst[8] = {prm.qs, prm.ks, prm.vs, prm.os, prm.dos, prm.dqs, prm.dks, prm.dvs};
+    for (int i = 0; i < 8; ++i)
+        for (int j = 0; j < 4; ++j) dst[i][j] = strides[i][j];
+    prm.B = B;
+    prm.Hq = Hq;
+    prm.Hkv = Hkv;
+    prm.T = T_;
+    prm.G = Hq / Hkv;
+    prm.window = window_size;
+    prm.scale = scale;
+    return launch_bwd_wide<T>(prm, exact_math, st);
+}
+
+}  // namespace
+
+int flash_fwd_wide(const void* q, const void* k, const void* v, void* o, float* row_sums, int B, int Hq, int Hkv,
+                   int T, int D, const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                   const int64_t* o_strides, float scale, int window_size, int exact_math, int dtype,
+                   hipStream_t st) {
+    const int chk = check_wide(B, Hq, Hkv, T, D, window_size, dtype);
+    if (chk != 0) return chk;
+    if (!q || !k || !v || !o || !q_strides || !k_strides || !v_strides || !o_strides) return SA_ERR_NULL_POINTER;
+    if (!wide_strides_ok(q_strides) || !wide_strides_ok(k_strides) || !wide_strides_ok(v_strides) ||
+        !wide_strides_ok(o_strides) || !aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
+        return SA_ERR_BAD_STRIDE;
+    if (B == 0 || T == 0) return 0;
+    if (dtype == SA_BF16)
+        return run_fwd_wide<bf16>(q, k, v, o, row_sums, B, Hq, Hkv, T, q_strides, k_strides, v_strides, o_strides,
+                                  scale, window_size, exact_math, st);
+    return run_fwd_wide<f16>(q, k, v, o, row_sums, B, Hq, Hkv, T, q_strides, k_strides, v_strides, o_strides,
+                             scale, window_size, exact_math, st);
+}
+
+int flash_bwd_wide(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                   const float* row_sums, void* dq, void* dk, void* dv, float* delta_ws, int B, int Hq, int Hkv,
+                   int T, int D, const int64_t* const strides[8], float scale, int window_size, int exact_math,
+                   int dtype, hipStream_t st) {
+    const int chk = check_wide(B, Hq, Hkv, T, D, window_size, dtype);
+    if (chk != 0) return chk;
+    if (!q || !k || !v || !o || !dout || !row_sums || !dq || !dk || !dv || !delta_ws) return SA_ERR_NULL_POINTER;
+    const void* ptrs[8] = {q, k, v, o, dout, dq, dk, dv};
+    for (int i = 0; i < 8; ++i) {
+        if (!strides[i]) return SA_ERR_NULL_POINTER;
+        if (!wide_strides_ok(strides[i]) || !aligned16(ptrs[i])) return SA_ERR_BAD_STRIDE;
+    }
+    if (B == 0 || T == 0) return 0;
+    if (dtype == SA_BF16)
+        return run_bwd_wide<bf16>(q, k, v, o, dout, row_sums, dq, dk, dv, delta_ws, B, Hq, Hkv, T, strides, scale,
+                                  window_size, exact_math, st);
+    return run_bwd_wide<f16>(q, k, v, o, dout, row_sums, dq, dk, dv, delta_ws, B, Hq, Hkv, T, strides, scale,
+                             window_size, exact_math, st);
+}
+
+}  // namespace sa

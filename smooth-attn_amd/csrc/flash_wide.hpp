@@ -1,0 +1,21 @@
+// 16-bit fused attention at head dim 256, reached from sa_flash_fwd /
+// sa_flash_bwd when D is 256 and dtype SA_BF16 or SA_F16.
+#pragma once
+
+#include "common.hpp"
+
+namespace sa {
+
+// Validates and launches the D = 256 forward (same contract as sa_flash_fwd).
+int flash_fwd_wide(const void* q, const void* k, const void* v, void* o, float* row_sums, int B, int Hq, int Hkv,
+                   int T, int D, const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                   const int64_t* o_strides, float scale, int window_size, int exact_math, int dtype,
+                   hipStream_t st);
+
+// Validates and launches the D = 256 backward (same contract as sa_flash_bwd).
+int flash_bwd_wide(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                   const float* row_sums, void* dq, void* dk, void* dv, float* delta_ws, int B, int Hq, int Hkv,
+                   int T, int D, const int64_t* const strides[8], float scale, int window_size, int exact_math,
+                   int dtype, hipStream_t st);
+
+}  // namespace sa

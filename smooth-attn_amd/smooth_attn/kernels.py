@@ -557,17 +557,22 @@ def _flash_operand(t):
     return t if ok else t.clone(memory_format=torch.contiguous_format)
 
 
-def _kernel_head_dim(D):
-    """The head dim the kernels run for a head dim D: D itself for 32, 64 and
-    128, else the next of those (inputs zero-padded, outputs sliced: zero
-    columns add nothing to q.k, and the padded columns of O, dQ, dK, dV are
-    dropped).  The reference takes any power of two through next_pow2
-    (kernels.py:1918); head dims above 128 are not supported here."""
-    if D in _FLASH_HEAD_DIMS:
+# Head dims the fused-attention kernels are built for, per input dtype.
+_FLASH_KERNEL_DIMS = {dt: (32, 64, 128, 256) for dt in (torch.bfloat16, torch.float16, torch.float32)}
+
+
+def _kernel_head_dim(D, dtype=None):
+    """The head dim the kernels run for a head dim D: D itself where a kernel
+    exists for it, else the next one up (inputs zero-padded, outputs sliced:
+    zero columns add nothing to q.k, and the padded columns of O, dQ, dK, dV
+    are dropped).  The reference takes any power of two through next_pow2
+    (kernels.py:1918)."""
+    dims = _FLASH_KERNEL_DIMS.get(dtype, _FLASH_HEAD_DIMS)
+    if D in dims:
         return D
-    if D < 1 or D > _FLASH_HEAD_DIMS[-1]:
-        raise ValueError(f"fused attention supports head dims 1..{_FLASH_HEAD_DIMS[-1]}, got {D}")
-    return next(d for d in _FLASH_HEAD_DIMS if d >= D)
+    if D < 1 or D > dims[-1]:
+        raise ValueError(f"fused attention supports head dims 1..{dims[-1]}, got {D}")
+    return next(d for d in dims if d >= D)
 
 
 def _pad_head_dim(t, Dk):
@@ -590,7 +595,7 @@ def _sp2norm_flash_fwd(q, k, v, scale, n_kv_groups=1, window_size=0, use_fast_sq
     _check_flash_dtypes(q, k, v)
     if H_kv * n_kv_groups != H_q:
         raise ValueError("n_kv_groups must equal H_q // H_kv")
-    Dk = _kernel_head_dim(D)
+    Dk = _kernel_head_dim(D, q.dtype)
     if Dk != D:
         o, row_sums = _sp2norm_flash_fwd(_pad_head_dim(q, Dk), _pad_head_dim(k, Dk), _pad_head_dim(v, Dk), scale,
                                          n_kv_groups, window_size, use_fast_sqrt)
@@ -617,7 +622,7 @@ def _sp2norm_flash_bwd(q, k, v, o, do, row_sums, scale, n_kv_groups=1, window_si
     B, H_q, T, D = q.shape
     H_kv = k.shape[1]
     _check_flash_dtypes(q, k, v)
-    Dk = _kernel_head_dim(D)
+    Dk = _kernel_head_dim(D, q.dtype)
     if Dk != D:
         pad = [_pad_head_dim(t, Dk) for t in (q, k, v, o, do.to(q.dtype))]
         dq, dk, dv = _sp2norm_flash_bwd(*pad, row_sums, scale, n_kv_groups, window_size, use_fast_sqrt)

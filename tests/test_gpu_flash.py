@@ -155,3 +155,28 @@ def test_forward_head_dims_below_128(D, T):
     assert o.is_contiguous() and o.shape == (1, 4, T, D)
     out = smooth_attn.sp2norm_flash_attention(q.to(DEV), k.to(DEV), v.to(DEV))
     assert torch.equal(out, o)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("T", [1, 17, 100, 128, 300])
+def test_forward_head_dim_256(dtype, T):
+    # D = 256 runs its own kernels (one wave per SIMD, O accumulators in AGPRs)
+    q, k, v = qkv(2, 4, 2, T, 256, dtype, seed=T + 256)
+    check_forward(q, k, v)
+    check_forward(q, k, v, window=45)
+
+
+@pytest.mark.parametrize("D", [160, 200])
+def test_forward_head_dims_above_128(D):
+    # head dims 129..255 run zero-padded to 256
+    q, k, v = qkv(1, 4, 4, 150, D, torch.bfloat16, seed=D)
+    o, _ = check_forward(q, k, v, exact=True)
+    assert o.is_contiguous() and o.shape == (1, 4, 150, D)
+
+
+def test_forward_head_dim_256_layouts():
+    q, k, v = qkv(2, 8, 2, 257, 256, torch.bfloat16, seed=7, layout="bthd")
+    check_forward(q, k, v)
+    out = smooth_attn.sp2norm_flash_attention(q.to(DEV), k.to(DEV), v.to(DEV))
+    o, _ = kernels._sp2norm_flash_fwd(q.to(DEV), k.to(DEV), v.to(DEV), 1 / 16, 4)
+    assert torch.equal(out, o)

@@ -166,3 +166,28 @@ def test_backward_head_dims_below_128(D):
     # of dQ, dK, dV are dropped
     grads, _ = check_backward(*inputs(1, 4, 2, 200, D, torch.bfloat16, seed=D))
     assert all(g.is_contiguous() and g.shape[-1] == D for g in grads)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("T", [1, 17, 100, 300])
+def test_backward_head_dim_256(dtype, T):
+    # D = 256 runs its own kernels; head dims 129..255 reach them zero-padded
+    check_backward(*inputs(2, 4, 2, T, 256, dtype, seed=T + 256))
+    check_backward(*inputs(1, 4, 1, T, 256, dtype, seed=T + 257), window=33)
+
+
+@pytest.mark.parametrize("D", [160, 200])
+def test_backward_head_dims_above_128(D):
+    grads, _ = check_backward(*inputs(1, 4, 2, 130, D, torch.bfloat16, seed=D), exact=True)
+    assert all(g.is_contiguous() and g.shape[-1] == D for g in grads)
+
+
+def test_backward_head_dim_256_public_api():
+    q, k, v, do = inputs(2, 8, 2, 200, 256, torch.bfloat16, seed=3, layout="bthd")
+    qd, kd, vd = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
+    out = smooth_attn.sp2norm_flash_attention(qd, kd, vd, window_size=70)
+    out.backward(do.to(DEV))
+    refs = eager.flash_attention_bwd(q.double(), k.double(), v.double(), out.detach().cpu().double(), do.double(),
+                                     window_size=70)
+    for got, ref in zip((qd.grad, kd.grad, vd.grad), refs):
+        assert rel_err(got, ref) <= TOL

@@ -172,3 +172,13 @@ def test_public_autograd_fp32():
     assert out.dtype == F32 and rel_err(out, ref) <= TOL
     for got, want in ((qd.grad, qr.grad), (kd.grad, kr.grad), (vd.grad, vr.grad)):
         assert rel_err(got, want, floor=1e-2) <= TOL
+
+
+@pytest.mark.parametrize("D", [160, 256])
+@pytest.mark.parametrize("T", [1, 100, 300])
+def test_head_dims_above_128(D, T):
+    # fp32 runs head dims up to 256 (D = 256 kernels, smaller ones zero-padded)
+    q, k, v, do = inputs(1, 4, 2, T, D, seed=D + T)
+    check_forward(q, k, v)
+    check_forward(q, k, v, window=37)
+    check_backward(q, k, v, do)
