@@ -7,25 +7,24 @@
 // :1667-1909): fp32 scores and weights, P and dS rounded to the input type
 // before their products, fp32 accumulation, row sums of the fp32 weights.
 // At D = 256 the O accumulators alone take 128 registers per lane, so these
-// kernels run one wave per SIMD with the accumulators in AGPRs and a simpler
-// structure than the D <= 128 ones: blocks of 4 waves x 32 rows, 32-row tiles
-// staged through registers into LDS (the next tile's loads in flight during
-// the current tile's MFMAs), two barriers per tile.  dK and dV are separate
-// kernels: together they would need 256 accumulator registers plus 128 for
-// the K and V operands and spill.
+// kernels run one wave per SIMD with the accumulators in AGPRs: blocks of 4
+// waves x 32 rows, 32-row tiles loaded straight into a ring of LDS stages
+// (the next tile in flight while the current one is used), one barrier per
+// tile.  With one wave per SIMD any overlap of MFMA and VALU work has to
+// come from within the wave: the forward is software-pipelined over tiles
+// (S^T of tile t + 1 issued among the VALU instructions that turn tile t's
+// scores into weights), and every MFMA group's LDS operands are read before
+// its first MFMA.  dK and dV are separate kernels: together they would need
+// 256 accumulator registers plus 128 for the K and V operands and spill.
 //
 // Operands (the 32x32x16 layout and the transposing LDS read are described
 // in flash_common.hpp).  For contractions over D, chunk c of a lane's operand
 // is elements 16c + 8 (l / 32) .. +7 of its row: Q, dO (forward, dQ) or K, V
-// (dK, dV) stay in registers, the other side is a 16-byte read of a
-// row-major LDS tile.  For contractions over keys (or queries) the B operand
-// is the lane's own 16 C-layout values v = 8j .. 8j + 7, whose k slots are
-// rows 16j + 8 (i / 4) + 4 (l / 32) + i % 4 of the tile (i = 0..7), so the A
-// operand is a pair of transposing reads of a row-major tile (4 rows each).
-// The two read patterns want different row pitches to be free of bank
-// conflicts (16 rows x 16 bytes: a pitch of 4 banks mod 64; the transposing
-// read's 4 rows x 32 bytes per 16 lanes: 16 banks), so a tile read both ways
-// is stored twice, at pitch D + 8 and D + 32 elements.
+// (dK, dV) stay in registers, the other side is a 16-byte read of an LDS
+// tile.  For contractions over keys (or queries) the B operand is the lane's
+// own 16 C-layout values v = 8j .. 8j + 7, whose k slots are rows
+// 16j + 8 (i / 4) + 4 (l / 32) + i % 4 of the tile (i = 0..7), so the A
+// operand is a pair of transposing reads (4 rows each).
 #include "flash_common.hpp"
 #include "flash_wide.hpp"
 
@@ -36,10 +35,68 @@ constexpr int kWW = 4;            // waves per block
 constexpr int kWT = 32;           // rows per staged tile
 constexpr int kWRows = 32 * kWW;  // rows a block owns
 
-template <int D>
-struct WPitch {
-    static constexpr int ROW = D + 8;   // row reads: 16 rows x 16 bytes, conflict-free
-    static constexpr int TR = D + 32;   // transposing reads: 4 rows x 32 bytes per 16 lanes
+// LDS tiles are unpadded [kWT][D] rows of 16-byte chunks filled by direct
+// global -> LDS loads (lane i of a wave writes bytes [16 i, 16 i + 16) after
+// the wave's base, so one instruction fills 1 KB).  The LDS serves a 16-byte
+// read 16 lanes per cycle and an 8-byte transposing read 32 lanes per cycle,
+// conflict-free when the lanes of a cycle cover 256 distinct bytes modulo
+// 256.  Rows are 512 bytes (a multiple of 256), so logical chunk c of row r
+// is stored at chunk c ^ swz(r):
+//  * ROW layout (row reads: 16 rows at one logical chunk): swz = r mod 16
+//    gives the 16 rows 16 distinct 16-byte slots;
+//  * TR layout (transposing reads: 4 consecutive rows x 64 bytes per 32
+//    lanes): swz = 4 (r mod 4) moves the rows' 64-byte groups to 4 distinct
+//    64-byte slots.
+// A tile read both ways is loaded twice, once per layout.
+template <bool TR>
+__device__ __forceinline__ int wswz(int r) {
+    return TR ? 4 * (r & 3) : (r & 15);
+}
+
+typedef __attribute__((address_space(3))) void wide_lds_void_t;
+
+// One 16-byte buffer -> LDS load per lane: lane i writes bytes [16 i, 16 i + 16)
+// after lds_base (wave-uniform), read from byte voff of the resource.
+__device__ __forceinline__ void wide_dma16(__amdgpu_buffer_rsrc_t rs, int voff, void* lds_base) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (wide_lds_void_t*)(lds_base), 16, voff, 0, 0, 0);
+}
+
+// s_waitcnt vmcnt(0): this wave's direct-to-LDS loads have landed.
+__device__ __forceinline__ void wide_wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Loads of kWT-row tiles of a [T, D] 16-bit matrix (row stride rstride
+// elements) into LDS in layout TR: each wave issues kWT * D * 2 / 1024 / kWW
+// instructions of 1 KB.  The per-lane byte offsets depend only on the layout
+// and the row stride, so they are computed once; each tile then takes a
+// buffer resource at its first row whose size ends at row T - 1 (rows past
+// it read as zeros).
+template <typename T, int D, bool TR>
+struct WideLoader {
+    static constexpr int CPR = D / 8;                // 16-byte chunks per row
+    static constexpr int NI = kWT * CPR / 64 / kWW;  // instructions per wave
+    int voff[NI];
+    int lds_off[NI];  // wave-uniform element offset of each instruction's 1 KB
+    int64_t row_bytes;
+    __device__ __forceinline__ WideLoader(int64_t rstride, int wave, int lane) : row_bytes(rstride * 2) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int base_slot = __builtin_amdgcn_readfirstlane((wave * NI + i) * 64);
+            const int slot = base_slot + lane;
+            const int r = slot / CPR;
+            const int lc = (slot - r * CPR) ^ wswz<TR>(r);
+            voff[i] = static_cast<int>(r * row_bytes) + 16 * lc;
+            lds_off[i] = base_slot * 8;
+        }
+    }
+    // rows r0 .. r0 + kWT - 1 of the matrix at base into lds
+    __device__ __forceinline__ void issue(const T* base, int r0, int T_, T* lds) const {
+        const int rows = min(kWT, T_ - r0);
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<T*>(base + static_cast<int64_t>(r0) * (row_bytes / 2)), 0, static_cast<int>(rows * row_bytes),
+            0x00020000);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) wide_dma16(rs, voff[i], lds + lds_off[i]);
+    }
 };
 
 template <typename E>
@@ -59,36 +116,6 @@ struct WideParams {
     int64_t qs[4], ks[4], vs[4], os[4], dos[4], dqs[4], dks[4], dvs[4];
     int B, Hq, Hkv, T, G, window;
     float scale;
-};
-
-// One [kWT][D] tile (rows r0.., clamped to T - 1) held in registers between
-// its global loads and its LDS stores; a thread unit is one 16-byte chunk.
-template <typename T, int D>
-struct WTile {
-    static constexpr int CPR = D / 8;                  // 16-byte chunks per row
-    static constexpr int PER = kWT * CPR / (64 * kWW);  // chunks per thread
-    u32x4 x[PER];
-    __device__ __forceinline__ void load(const T* base, int64_t rstride, int r0, int T_, int tid) {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int idx = tid + 64 * kWW * i;
-            const int r = idx / CPR;
-            const int c = idx - r * CPR;
-            x[i] = *reinterpret_cast<const u32x4*>(base + static_cast<int64_t>(min(r0 + r, T_ - 1)) * rstride +
-                                                   8 * c);
-        }
-    }
-    // row-major copies at pitch WPitch::ROW (nullable) and WPitch::TR (nullable)
-    __device__ __forceinline__ void store(T* rows, T* trs, int tid) const {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int idx = tid + 64 * kWW * i;
-            const int r = idx / CPR;
-            const int c = idx - r * CPR;
-            if (rows != nullptr) *reinterpret_cast<u32x4*>(rows + r * WPitch<D>::ROW + 8 * c) = x[i];
-            if (trs != nullptr) *reinterpret_cast<u32x4*>(trs + r * WPitch<D>::TR + 8 * c) = x[i];
-        }
-    }
 };
 
 // y = squareplus(2 s scale - 1)^2 = (a + r)^2, a = s scale - 1/2,
@@ -116,16 +143,21 @@ __device__ __forceinline__ void load_frags(const T* row, int hi, u32x4 (&x)[D / 
     for (int c = 0; c < D / 16; ++c) x[c] = *reinterpret_cast<const u32x4*>(row + 16 * c + 8 * hi);
 }
 
-// C += A B^T over D: A rows from a row-major LDS tile at pitch ROW (row
-// l32), B from a lane's register chunks.
+// C += A B^T over D: A rows from a ROW-layout LDS tile (row l32), B from a
+// lane's register chunks.  All reads are issued before the first MFMA, so
+// their latency is paid once per call rather than once per MFMA.
 template <typename T, int D>
 __device__ __forceinline__ f32x16 mma_rows16(const T* lds_rows, int l32, int hi, const u32x4 (&b)[D / 16],
                                              f32x16 c) {
     using V8 = typename MfmaOps<T>::vec8;
-    const T* ar = lds_rows + l32 * WPitch<D>::ROW + 8 * hi;
+    const T* ar = lds_rows + l32 * D;
+    const int sw = wswz<false>(l32);
+    u32x4 a[D / 16];
 #pragma unroll
-    for (int i = 0; i < D / 16; ++i)
-        c = MfmaOps<T>::mma(as_vec8<V8>(*reinterpret_cast<const u32x4*>(ar + 16 * i)), as_vec8<V8>(b[i]), c);
+    for (int i = 0; i < D / 16; ++i) a[i] = *reinterpret_cast<const u32x4*>(ar + 8 * ((2 * i + hi) ^ sw));
+    __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
+#pragma unroll
+    for (int i = 0; i < D / 16; ++i) c = MfmaOps<T>::mma(as_vec8<V8>(a[i]), as_vec8<V8>(b[i]), c);
     return c;
 }
 
@@ -138,26 +170,39 @@ __device__ __forceinline__ void pack_b(const float (&x)[16], u32x4 (&w)[2]) {
                      pack2<T>(x[8 * j + 4], x[8 * j + 5]), pack2<T>(x[8 * j + 6], x[8 * j + 7])};
 }
 
-// acc[dt] (rows d = 32 dt + ..) += A^T(d, r) X(r, col) over the tile's 32
-// rows r: A^T by transposing reads of a row-major tile at pitch TR (lane
-// supplies row 4 (l / 32) + (l % 16) / 4, column 32 dt + 16 ((l / 16) % 2) +
-// 4 (l % 4); the 16 lanes of its group receive column 32 dt + l % 32 of rows
-// +0..3), X the packed B operands.
+// A^T operands of acc[dt] (rows d = 32 dt + ..) += A^T(d, r) X(r, col) over
+// a tile's 32 rows r: transposing reads of a TR-layout tile (lane supplies
+// row 4 (l / 32) + (l % 16) / 4, column 32 dt + 16 ((l / 16) % 2) + 4 (l % 4);
+// the 16 lanes of its group receive column 32 dt + l % 32 of rows +0..3).
+// Read before the B operands exist, so the reads overlap the work that
+// produces them.
 template <typename T, int D>
-__device__ __forceinline__ void mma_cols16(const T* lds_tr, int lane, const u32x4 (&x)[2],
-                                           f32x16 (&acc)[D / 32]) {
+struct ColOperands {
     using V8 = typename MfmaOps<T>::vec8;
-    constexpr int P = WPitch<D>::TR;
-    const T* base = lds_tr + (4 * (lane >> 5) + ((lane & 15) >> 2)) * P + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    V8 a[D / 32][2];
+    __device__ __forceinline__ void read(const T* lds_tr, int lane) {
+        const int r = 4 * (lane >> 5) + ((lane & 15) >> 2);
+        const int sw = wswz<true>(r);  // the same for rows r + 8, r + 16, r + 24
+        const T* base = lds_tr + r * D + 4 * (lane & 1);
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) {
+        for (int dt = 0; dt < D / 32; ++dt) {
+            const int chunk = (4 * dt + 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1)) ^ sw;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const T* p0 = base + 16 * j * P + 32 * dt;
-            acc[dt] = MfmaOps<T>::mma(lds_read_tr16_pair<V8>(p0, p0 + 8 * P), as_vec8<V8>(x[j]), acc[dt]);
+            for (int j = 0; j < 2; ++j) {
+                const T* p0 = base + 16 * j * D + 8 * chunk;
+                a[dt][j] = lds_read_tr16_pair<V8>(p0, p0 + 8 * D);
+            }
         }
+        __builtin_amdgcn_sched_barrier(0);  // issue the reads here, ahead of the caller's VALU work
     }
-}
+    // acc[dt] += A^T X, X the packed B operands
+    __device__ __forceinline__ void mma(const u32x4 (&x)[2], f32x16 (&acc)[D / 32]) const {
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) acc[dt] = MfmaOps<T>::mma(a[dt][j], as_vec8<V8>(x[j]), acc[dt]);
+    }
+};
 
 // Write a lane's C-layout rows of acc (d = 32 dt + 8 m + 4 hi .. +3) times f
 // into its output row as 8-byte stores.
@@ -193,8 +238,8 @@ struct QBlock {
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool EXACT>
 __global__ __launch_bounds__(64 * kWW) void flash_fwd_wide_kernel(WideParams<T> p) {
-    __shared__ __attribute__((aligned(16))) T ldsK[kWT * WPitch<D>::ROW];
-    __shared__ __attribute__((aligned(16))) T ldsV[kWT * WPitch<D>::TR];
+    __shared__ __attribute__((aligned(16))) T ldsK[3][kWT * D];  // ROW layout
+    __shared__ __attribute__((aligned(16))) T ldsV[3][kWT * D];  // TR layout
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -224,22 +269,46 @@ __global__ __launch_bounds__(64 * kWW) void flash_fwd_wide_kernel(WideParams<T> 
     const int kv_begin = W > 0 ? max(0, qb * kWRows - W + 1) / kWT : 0;
     const float sc = p.scale;
 
-    WTile<T, D> kreg, vreg;
-    kreg.load(kp, p.ks[2], kv_begin * kWT, T_, tid);
-    vreg.load(vp, p.vs[2], kv_begin * kWT, T_, tid);
+    // Three LDS stages and a software pipeline over tiles: while the S^T
+    // MFMAs of tile t + 1 run, the VALU turns tile t's scores into weights
+    // (the MFMAs and the VALU instructions interleaved in the wave's stream),
+    // then P V of tile t; tile t + 2 loads meanwhile.  One wave per SIMD, so
+    // this overlap has to come from within the wave.
+    const WideLoader<T, D, false> kld(p.ks[2], wave, lane);
+    const WideLoader<T, D, true> vld(p.vs[2], wave, lane);
+    kld.issue(kp, kv_begin * kWT, T_, ldsK[0]);
+    vld.issue(vp, kv_begin * kWT, T_, ldsV[0]);
+    if (kv_begin + 1 < kv_end) {
+        kld.issue(kp, (kv_begin + 1) * kWT, T_, ldsK[1]);
+        vld.issue(vp, (kv_begin + 1) * kWT, T_, ldsV[1]);
+    }
+    wide_wait_vmem();
+    __syncthreads();
+    f32x16 s_next = mma_rows16<T, D>(ldsK[0], l32, hi, qf, f32x16{});  // S^T of the first tile
+    int st = 0;
     for (int t = kv_begin; t < kv_end; ++t) {
-        __syncthreads();  // every wave is done with tile t - 1
-        kreg.store(ldsK, nullptr, tid);
-        vreg.store(nullptr, ldsV, tid);
-        __syncthreads();
-        if (t + 1 < kv_end) {
-            kreg.load(kp, p.ks[2], (t + 1) * kWT, T_, tid);
-            vreg.load(vp, p.vs[2], (t + 1) * kWT, T_, tid);
+        const int st1 = st == 2 ? 0 : st + 1;
+        const int st2 = st1 == 2 ? 0 : st1 + 1;
+        if (t + 2 < kv_end) {  // stage st2 held tile t - 1, released by the barrier ending tile t - 1
+            kld.issue(kp, (t + 2) * kWT, T_, ldsK[st2]);
+            vld.issue(vp, (t + 2) * kWT, T_, ldsV[st2]);
         }
         const int k0 = t * kWT;
-        const bool active = k0 <= q0 + 31 && !(W > 0 && q0 - (k0 + 31) >= W);
-        if (!active) continue;
-        const f32x16 s = mma_rows16<T, D>(ldsK, l32, hi, qf, f32x16{});  // S^T: rows keys, column query
+        const f32x16 s = s_next;
+        // operands: K of tile t + 1 (the last tile re-reads its own, result unused), V of tile t
+        const T* kn = ldsK[t + 1 < kv_end ? st1 : st] + l32 * D;
+        const int sw = wswz<false>(l32);
+        u32x4 ka[D / 16];
+#pragma unroll
+        for (int i = 0; i < D / 16; ++i) ka[i] = *reinterpret_cast<const u32x4*>(kn + 8 * ((2 * i + hi) ^ sw));
+        ColOperands<T, D> vt;
+        vt.read(ldsV[st], lane);
+        // S^T of tile t + 1 ...
+        using V8 = typename MfmaOps<T>::vec8;
+        s_next = f32x16{};
+#pragma unroll
+        for (int i = 0; i < D / 16; ++i) s_next = MfmaOps<T>::mma(as_vec8<V8>(ka[i]), as_vec8<V8>(qf[i]), s_next);
+        // ... interleaved with the weights of tile t
         float y[16];
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
@@ -251,7 +320,16 @@ __global__ __launch_bounds__(64 * kWW) void flash_fwd_wide_kernel(WideParams<T> 
         }
         u32x4 pw[2];
         pack_b<T>(y, pw);
-        mma_cols16<T, D>(ldsV, lane, pw, oacc);  // O^T += V^T P^T
+#pragma unroll
+        for (int i = 0; i < D / 16; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x402, 10, 0);  // then VALU / transcendental
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        vt.mma(pw, oacc);  // O^T += V^T P^T of tile t
+        wide_wait_vmem();
+        __syncthreads();  // tile t + 2 landed; every wave is done with stage st
+        st = st1;
     }
 
     const float tot = ssum + __shfl_xor(ssum, 32) + kEps;
@@ -266,9 +344,9 @@ __global__ __launch_bounds__(64 * kWW) void flash_fwd_wide_kernel(WideParams<T> 
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool EXACT>
 __global__ __launch_bounds__(64 * kWW) void flash_bwd_dq_wide_kernel(WideParams<T> p) {
-    __shared__ __attribute__((aligned(16))) T ldsK[kWT * WPitch<D>::ROW];
-    __shared__ __attribute__((aligned(16))) T ldsKt[kWT * WPitch<D>::TR];
-    __shared__ __attribute__((aligned(16))) T ldsV[kWT * WPitch<D>::ROW];
+    __shared__ __attribute__((aligned(16))) T ldsK[2][kWT * D];   // ROW layout
+    __shared__ __attribute__((aligned(16))) T ldsKt[2][kWT * D];  // TR layout
+    __shared__ __attribute__((aligned(16))) T ldsV[2][kWT * D];   // ROW layout
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -318,34 +396,40 @@ __global__ __launch_bounds__(64 * kWW) void flash_bwd_dq_wide_kernel(WideParams<
     const int kv_begin = W > 0 ? max(0, qb * kWRows - W + 1) / kWT : 0;
     const float sc = p.scale;
 
-    WTile<T, D> kreg, vreg;
-    kreg.load(kp, p.ks[2], kv_begin * kWT, T_, tid);
-    vreg.load(vp, p.vs[2], kv_begin * kWT, T_, tid);
+    const WideLoader<T, D, false> kld(p.ks[2], wave, lane);
+    const WideLoader<T, D, true> ktld(p.ks[2], wave, lane);
+    const WideLoader<T, D, false> vld(p.vs[2], wave, lane);
+    auto issue = [&](int t, int buf) {
+        kld.issue(kp, t * kWT, T_, ldsK[buf]);
+        ktld.issue(kp, t * kWT, T_, ldsKt[buf]);
+        vld.issue(vp, t * kWT, T_, ldsV[buf]);
+    };
+    issue(kv_begin, 0);
+    wide_wait_vmem();
+    __syncthreads();
     for (int t = kv_begin; t < kv_end; ++t) {
-        __syncthreads();
-        kreg.store(ldsK, ldsKt, tid);
-        vreg.store(ldsV, nullptr, tid);
-        __syncthreads();
-        if (t + 1 < kv_end) {
-            kreg.load(kp, p.ks[2], (t + 1) * kWT, T_, tid);
-            vreg.load(vp, p.vs[2], (t + 1) * kWT, T_, tid);
-        }
+        const int buf = (t - kv_begin) & 1;
+        if (t + 1 < kv_end) issue(t + 1, buf ^ 1);  // released by the barrier ending tile t - 1
         const int k0 = t * kWT;
-        const bool active = k0 <= q0 + 31 && !(W > 0 && q0 - (k0 + 31) >= W);
-        if (!active) continue;
-        const f32x16 s = mma_rows16<T, D>(ldsK, l32, hi, qf, f32x16{});  // S^T
-        const f32x16 dp = mma_rows16<T, D>(ldsV, l32, hi, df, ndl);     // dP^T - delta
-        float ds[16];
+        {
+            const f32x16 s = mma_rows16<T, D>(ldsK[buf], l32, hi, qf, f32x16{});  // S^T
+            const f32x16 dp = mma_rows16<T, D>(ldsV[buf], l32, hi, df, ndl);     // dP^T - delta
+            ColOperands<T, D> kt;
+            kt.read(ldsKt[buf], lane);
+            float ds[16];
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int key = k0 + 8 * (v >> 2) + 4 * hi + (v & 3);
-            float y, rr;
-            weight_rr16<EXACT>(s[v], sc, y, rr);
-            ds[v] = static_cast<unsigned>(qi - key) < weff ? dp[v] * y * rr : 0.f;
+            for (int v = 0; v < 16; ++v) {
+                const int key = k0 + 8 * (v >> 2) + 4 * hi + (v & 3);
+                float y, rr;
+                weight_rr16<EXACT>(s[v], sc, y, rr);
+                ds[v] = static_cast<unsigned>(qi - key) < weff ? dp[v] * y * rr : 0.f;
+            }
+            u32x4 dsw[2];
+            pack_b<T>(ds, dsw);
+            kt.mma(dsw, acc);  // dQ^T += K^T dS^T
         }
-        u32x4 dsw[2];
-        pack_b<T>(ds, dsw);
-        mma_cols16<T, D>(ldsKt, lane, dsw, acc);  // dQ^T += K^T dS^T
+        wide_wait_vmem();
+        __syncthreads();  // tile t + 1 landed; every wave is done with stage buf
     }
     // dS carried without its per-row factor 2 scale / R
     if (qi < T_)
@@ -361,10 +445,10 @@ template <typename T, int D, bool EXACT, bool DK>
 __global__ __launch_bounds__(64 * kWW) void flash_bwd_kv_wide_kernel(WideParams<T> p) {
     // Q rows (S = Q K^T), and for dK: Q^T (dK^T += Q^T dS) and dO rows
     // (dP = dO V^T); for dV: dO^T (dV^T += dO^T P).
-    __shared__ __attribute__((aligned(16))) T ldsQ[kWT * WPitch<D>::ROW];
-    __shared__ __attribute__((aligned(16))) T ldsTr[kWT * WPitch<D>::TR];
-    __shared__ __attribute__((aligned(16))) T ldsO[DK ? kWT * WPitch<D>::ROW : 8];
-    __shared__ __attribute__((aligned(16))) float ldr[2][kWT];  // [1/R, -delta] of the tile's rows
+    __shared__ __attribute__((aligned(16))) T ldsQ[2][kWT * D];               // ROW layout
+    __shared__ __attribute__((aligned(16))) T ldsTr[2][kWT * D];              // TR layout
+    __shared__ __attribute__((aligned(16))) T ldsO[2][DK ? kWT * D : 8];      // ROW layout
+    __shared__ __attribute__((aligned(16))) float ldr[2][2][kWT];  // [stage][1/R, -delta] of the tile's rows
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -397,59 +481,83 @@ __global__ __launch_bounds__(64 * kWW) void flash_bwd_kv_wide_kernel(WideParams<
     const int n_it = p.G * nq;
     const float sc = p.scale;
 
-    WTile<T, D> qreg, oreg;
-    float rst = 0.f;
-    auto fetch = [&](int it) {
+    // Query tile it: (group head g, rows q0 ..); its 1/R and -delta values go
+    // through a register one iteration ahead of their LDS store.
+    auto tile_of = [&](int it, int& hq, int& q0) {
         const int g = it / nq;
-        const int q0 = (qt_begin + it - g * nq) * kWT;
-        const int hq = hk * p.G + g;
-        qreg.load(p.q + b * p.qs[0] + hq * p.qs[1], p.qs[2], q0, T_, tid);
-        oreg.load(p.dout + b * p.dos[0] + hq * p.dos[1], p.dos[2], q0, T_, tid);
-        if (tid < 2 * kWT) {
-            const int64_t idx = (static_cast<int64_t>(b) * p.Hq + hq) * T_ + min(q0 + (tid & (kWT - 1)), T_ - 1);
-            rst = tid < kWT ? 1.f / p.rs[idx] : -p.delta[idx];
+        q0 = (qt_begin + it - g * nq) * kWT;
+        hq = hk * p.G + g;
+    };
+    const WideLoader<T, D, false> qld(p.qs[2], wave, lane);
+    const WideLoader<T, D, true> trld(DK ? p.qs[2] : p.dos[2], wave, lane);
+    const WideLoader<T, D, false> old(p.dos[2], wave, lane);
+    auto issue = [&](int it, int buf) {
+        int hq, q0;
+        tile_of(it, hq, q0);
+        const T* qp = p.q + b * p.qs[0] + hq * p.qs[1];
+        const T* op = p.dout + b * p.dos[0] + hq * p.dos[1];
+        qld.issue(qp, q0, T_, ldsQ[buf]);
+        if constexpr (DK) {
+            trld.issue(qp, q0, T_, ldsTr[buf]);
+            old.issue(op, q0, T_, ldsO[buf]);
+        } else {
+            trld.issue(op, q0, T_, ldsTr[buf]);
         }
     };
-    fetch(0);
+    auto row_value = [&](int it) {
+        int hq, q0;
+        tile_of(it, hq, q0);
+        const int64_t idx = (static_cast<int64_t>(b) * p.Hq + hq) * T_ + min(q0 + (tid & (kWT - 1)), T_ - 1);
+        return tid < kWT ? 1.f / p.rs[idx] : -p.delta[idx];
+    };
+    float rnext = 0.f;
+    issue(0, 0);
+    if (tid < 2 * kWT) {
+        ldr[0][tid / kWT][tid & (kWT - 1)] = row_value(0);
+        if (n_it > 1) rnext = row_value(1);
+    }
+    wide_wait_vmem();
+    __syncthreads();
     for (int it = 0; it < n_it; ++it) {
-        __syncthreads();
-        if constexpr (DK) {
-            qreg.store(ldsQ, ldsTr, tid);
-            oreg.store(ldsO, nullptr, tid);
-        } else {
-            qreg.store(ldsQ, nullptr, tid);
-            oreg.store(nullptr, ldsTr, tid);
+        const int buf = it & 1;
+        if (it + 1 < n_it) {  // stage buf ^ 1 was released by the barrier ending iteration it - 1
+            issue(it + 1, buf ^ 1);
+            if (tid < 2 * kWT) {
+                ldr[buf ^ 1][tid / kWT][tid & (kWT - 1)] = rnext;
+                if (it + 2 < n_it) rnext = row_value(it + 2);
+            }
         }
-        if (tid < 2 * kWT) ldr[tid / kWT][tid & (kWT - 1)] = rst;
-        __syncthreads();
-        const int g = it / nq;
-        const int q0 = (qt_begin + it - g * nq) * kWT;
-        if (it + 1 < n_it) fetch(it + 1);
+        int hq, q0;
+        tile_of(it, hq, q0);
         // some query of the tile sees some key of the wave
-        const bool active = q0 + 31 >= wk0 && !(W > 0 && q0 - (wk0 + 31) >= W);
-        if (!active) continue;
-        const f32x16 s = mma_rows16<T, D>(ldsQ, l32, hi, kf, f32x16{});  // S: rows queries, column key
-        f32x16 dp;
-        if constexpr (DK) {
+        {
+            const f32x16 s = mma_rows16<T, D>(ldsQ[buf], l32, hi, kf, f32x16{});  // S: rows queries, column key
+            f32x16 dp;
+            if constexpr (DK) {
 #pragma unroll
-            for (int v = 0; v < 16; ++v) dp[v] = ldr[1][8 * (v >> 2) + 4 * hi + (v & 3)];
-            dp = mma_rows16<T, D>(ldsO, l32, hi, vf, dp);  // dP - delta
-        }
-        float x[16];
+                for (int v = 0; v < 16; ++v) dp[v] = ldr[buf][1][8 * (v >> 2) + 4 * hi + (v & 3)];
+                dp = mma_rows16<T, D>(ldsO[buf], l32, hi, vf, dp);  // dP - delta
+            }
+            ColOperands<T, D> at;
+            at.read(ldsTr[buf], lane);
+            float x[16];
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int r = 8 * (v >> 2) + 4 * hi + (v & 3);
-            const int q = q0 + r;
-            float y, rr;
-            weight_rr16<EXACT>(s[v], sc, y, rr);
-            const float yi = y * ldr[0][r];
-            const bool ok = static_cast<unsigned>(q - kj) < weff && q < T_;
-            if constexpr (DK) x[v] = ok ? dp[v] * yi * rr : 0.f;  // dS
-            else x[v] = ok ? yi : 0.f;                             // P
+            for (int v = 0; v < 16; ++v) {
+                const int r = 8 * (v >> 2) + 4 * hi + (v & 3);
+                const int q = q0 + r;
+                float y, rr;
+                weight_rr16<EXACT>(s[v], sc, y, rr);
+                const float yi = y * ldr[buf][0][r];
+                const bool ok = static_cast<unsigned>(q - kj) < weff && q < T_;
+                if constexpr (DK) x[v] = ok ? dp[v] * yi * rr : 0.f;  // dS
+                else x[v] = ok ? yi : 0.f;                             // P
+            }
+            u32x4 xw[2];
+            pack_b<T>(x, xw);
+            at.mma(xw, acc);  // dK^T += Q^T dS, or dV^T += dO^T P
         }
-        u32x4 xw[2];
-        pack_b<T>(x, xw);
-        mma_cols16<T, D>(ldsTr, lane, xw, acc);  // dK^T += Q^T dS, or dV^T += dO^T P
+        wide_wait_vmem();
+        __syncthreads();  // tile it + 1 landed; every wave is done with stage buf
     }
     if (kj < T_) {
         if constexpr (DK) store_cols16<T, D>(p.dk + b * p.dks[0] + hk * p.dks[1] + kj * p.dks[2], hi, acc, 2.f * sc);
@@ -457,8 +565,12 @@ __global__ __launch_bounds__(64 * kWW) void flash_bwd_kv_wide_kernel(WideParams<
     }
 }
 
-// 16-bit tensors: (b, h, t) strides multiples of 8 elements (16-byte rows), d stride 1.
-bool wide_strides_ok(const int64_t* s) { return s[3] == 1 && s[0] % 8 == 0 && s[1] % 8 == 0 && s[2] % 8 == 0; }
+// 16-bit tensors: (b, h, t) strides multiples of 8 elements (16-byte rows),
+// d stride 1, and a tile's rows within 32-bit byte offsets of its first row.
+bool wide_strides_ok(const int64_t* s) {
+    return s[3] == 1 && s[0] % 8 == 0 && s[1] % 8 == 0 && s[2] % 8 == 0 && s[2] >= 0 &&
+           s[2] * 2 * kWT < (int64_t(1) << 31);
+}
 
 int check_wide(int B, int Hq, int Hkv, int T, int D, int window_size, int dtype) {
     if (dtype != SA_BF16 && dtype != SA_F16) return SA_ERR_BAD_DTYPE;
