@@ -281,8 +281,9 @@ int64_t sa_paged_decode_workspace_size(int B, int Hq, int D, int max_pages,
  *   out: bf16 [B, Hq, D] (strides o_strides)
  * out[b,h] = sum_{t<ctx_b} y_t V_t / (sum_t y_t + 1e-12) with
  * K_t = k_cache[block_table[b, t/P], h/(Hq/Hkv), t%P].  dtype (q and cache):
- * SA_BF16 or SA_F16.  D in {32, 64, 128}; page_size a power of two (at
- * most 2^20).
+ * SA_BF16 or SA_F16.  D a multiple of 8 in 8..256 (kernels for 32, 64, 128
+ * and 256; smaller D read only their own columns); page_size a power of two
+ * (at most 2^20).
  * workspace: at least sa_paged_decode_workspace_size() bytes, 16-byte
  * aligned, no initialisation needed (a plan kernel writes it).
  * Replaces sp2norm_paged_attention (kernels.py:2776-2829) and its kernel

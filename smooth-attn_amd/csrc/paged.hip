@@ -51,6 +51,7 @@ struct PagedParams {
     int64_t qs[4], ks[4], vs[4], os[3];
     int64_t bt_stride;
     int B, Hq, Hkv, G, P, logP, max_pages, n_pages, n_slots, n_waves;
+    int D;    // head dim (a multiple of 8, at most the kernel's DP)
     int per;  // minimum tiles per active wave
     float scale;
 };
@@ -91,6 +92,10 @@ __global__ __launch_bounds__(256) void paged_plan_kernel(PagedParams p) {
     }
 }
 
+// The kernels run a padded head dim D (32, 64, 128 or 256); head dims
+// p.D < D (multiples of 8) load only their p.D / 8 chunks per row and leave
+// zeros in the rest of the LDS rows and Q registers, which add nothing to
+// the scores, and write only p.D output columns.
 // UNIFORM: every load instruction's tokens lie in one page (64 / (D/8)
 // tokens per instruction divide the page size), so the page base is
 // wave-uniform and comes from v_readlane of the window's page-id register.
@@ -162,7 +167,7 @@ __global__ __launch_bounds__(64) void paged_partial_kernel(PagedParams p) {
             const T* qrow = static_cast<const T*>(p.q) + b * p.qs[0] + (hk * p.G + (live ? l32 : 0)) * p.qs[1];
 #pragma unroll
             for (int dc = 0; dc < D / 16; ++dc)
-                qreg[dc] = live ? load16(qrow + dc * 16 + hi * 8) : u32x4{0u, 0u, 0u, 0u};
+                qreg[dc] = live && dc * 16 + hi * 8 < p.D ? load16(qrow + dc * 16 + hi * 8) : u32x4{0u, 0u, 0u, 0u};
         }
 
         f32x16 oacc[D / 32];
@@ -185,6 +190,7 @@ __global__ __launch_bounds__(64) void paged_partial_kernel(PagedParams p) {
             // c = 64 i + l of the tile (token c / CPT, columns 8 (c % CPT) .. +7).
             const int lane_tok = lane / CPT;
             const int lane_col = (lane % CPT) * 8;
+            const bool col_live = lane_col < p.D;  // columns past the head dim stay zero
             u32x4 kbuf[NC], vbuf[NC];
             auto load_tile = [&](int t0) {
 #pragma unroll
@@ -203,7 +209,7 @@ __global__ __launch_bounds__(64) void paged_partial_kernel(PagedParams p) {
                         koff = phys * p.ks[0] + (t & pmask) * p.ks[2];
                         voff = phys * p.vs[0] + (t & pmask) * p.vs[2];
                     }
-                    if (t < we) {
+                    if (t < we && col_live) {
                         kbuf[i] = load16(kc + koff + lane_col);
                         vbuf[i] = load16(vc + voff + lane_col);
                     } else {
@@ -270,14 +276,15 @@ __global__ __launch_bounds__(64) void paged_partial_kernel(PagedParams p) {
         if (l32 < p.G) {
             const int hq = hk * p.G + l32;
             const int64_t slot = (static_cast<int64_t>(b) * p.Hq + hq) * p.n_slots + slot_k;
-            float* wo = p.ws_o + slot * D;
+            float* wo = p.ws_o + slot * p.D;
 #pragma unroll
             for (int dt = 0; dt < D / 32; ++dt) {
 #pragma unroll
                 for (int vg = 0; vg < 4; ++vg) {
                     const int d0 = dt * 32 + vg * 8 + hi * 4;
-                    *reinterpret_cast<float4*>(wo + d0) = float4{oacc[dt][vg * 4 + 0], oacc[dt][vg * 4 + 1],
-                                                                 oacc[dt][vg * 4 + 2], oacc[dt][vg * 4 + 3]};
+                    if (d0 < p.D)  // p.D is a multiple of 8: groups of 4 are wholly in or out
+                        *reinterpret_cast<float4*>(wo + d0) = float4{oacc[dt][vg * 4 + 0], oacc[dt][vg * 4 + 1],
+                                                                     oacc[dt][vg * 4 + 2], oacc[dt][vg * 4 + 3]};
                 }
             }
             if (hi == 0) p.ws_s[slot] = stot;
@@ -306,7 +313,7 @@ __global__ __launch_bounds__(D) void paged_merge_kernel(PagedParams p) {
         const int w1 = static_cast<int>((static_cast<int64_t>(last + 1) * Ne - 1) / Tt);
         const int64_t slot0 = static_cast<int64_t>(bh) * p.n_slots;
         for (int i = 0; i <= w1 - w0; ++i) {
-            o += p.ws_o[(slot0 + i) * D + d];
+            o += p.ws_o[(slot0 + i) * p.D + d];
             s += p.ws_s[slot0 + i];
         }
     }
@@ -348,7 +355,7 @@ int launch_paged(PagedParams prm, hipStream_t st) {
         paged_partial_kernel<T, D, true><<<prm.n_waves, 64, 0, st>>>(prm);
     else
         paged_partial_kernel<T, D, false><<<prm.n_waves, 64, 0, st>>>(prm);
-    paged_merge_kernel<D><<<static_cast<unsigned>(prm.B) * prm.Hq, D, 0, st>>>(prm);
+    paged_merge_kernel<D><<<static_cast<unsigned>(prm.B) * prm.Hq, prm.D, 0, st>>>(prm);
     return status_from_launch();
 }
 
@@ -404,7 +411,7 @@ int validate_paged(const void* q, const void* k_cache, const void* v_cache, cons
     // any power of two: a tile of 32 tokens spans 32 / P pages (P < 32) or
     // lies in one page; a window of 64 page ids always covers whole tiles
     if (page_size <= 0 || (page_size & (page_size - 1)) != 0 || page_size > (1 << 20)) return SA_ERR_UNSUPPORTED;
-    if (D != 32 && D != 64 && D != 128) return SA_ERR_UNSUPPORTED;
+    if (D < 8 || D > 256 || D % 8 != 0) return SA_ERR_UNSUPPORTED;
     if (B == 0) return 1;
     if (n_pages == 0) max_pages = 0;  // no cache: every context is empty
     // The plan keeps token positions, tile counts and their prefix sums over
@@ -446,6 +453,7 @@ int run_paged(const void* q, const void* k_cache, const void* v_cache, void* out
     prm.plan = reinterpret_cast<int*>(ws);
     prm.ws_o = ws + plan_bytes(B) / 4;
     prm.ws_s = prm.ws_o + static_cast<int64_t>(B) * Hq * prm.n_slots * D;
+    prm.D = D;
     for (int i = 0; i < 4; ++i) {
         prm.qs[i] = q_strides[i];
         prm.ks[i] = kv_strides[i];
@@ -462,17 +470,20 @@ int run_paged(const void* q, const void* k_cache, const void* v_cache, void* out
     prm.max_pages = max_pages;
     prm.n_pages = n_pages;
     prm.scale = scale;
+    const int dp = D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 256;  // padded head dim of the kernels
     if (dtype == SA_BF16) {
-        switch (D) {
+        switch (dp) {
             case 32: return launch_paged<bf16, 32>(prm, st);
             case 64: return launch_paged<bf16, 64>(prm, st);
-            default: return launch_paged<bf16, 128>(prm, st);
+            case 128: return launch_paged<bf16, 128>(prm, st);
+            default: return launch_paged<bf16, 256>(prm, st);
         }
     }
-    switch (D) {
+    switch (dp) {
         case 32: return launch_paged<f16, 32>(prm, st);
         case 64: return launch_paged<f16, 64>(prm, st);
-        default: return launch_paged<f16, 128>(prm, st);
+        case 128: return launch_paged<f16, 128>(prm, st);
+        default: return launch_paged<f16, 256>(prm, st);
     }
 }
 

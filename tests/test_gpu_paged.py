@@ -187,3 +187,32 @@ def test_index_tensors_on_another_device_are_refused():
             smooth_attn.sp2norm_paged_kv_append(kc, kc, kc[:B, :, :1], kc[:B, :, :1], tab, ctx, block_size=P)
     out = smooth_attn.sp2norm_paged_attention(q, kc, kc, table.to(DEV), lens.to(DEV), block_size=P)
     assert out.shape == (B, Hq, D) and bool((out == 0).all())  # zero V rows
+
+
+@pytest.mark.parametrize("D", [8, 16, 24, 48, 80, 96, 136, 160, 200, 256])
+@pytest.mark.parametrize("BS", [1, 16, 64])
+def test_paged_head_dims(D, BS):
+    # any head dim that is a multiple of 8 up to 256 (the reference takes any
+    # D through next_pow2, kernels.py:2815): kernels for 32 / 64 / 128 / 256,
+    # smaller head dims load only their own columns
+    q, k, v = case(3, 8, 2, 333, D, seed=D + BS)
+    kc, vc, table, lens = paging.build_paged_cache(k, v, page_size=BS, shuffle=True, generator=_g(D))
+    lens = torch.tensor([333, 1, 170], dtype=torch.int32)
+    out = run(q, kc, vc, table, lens, BS)
+    ref = eager.paged_decode_eager(q.double(), kc.double(), vc.double(), table, lens)
+    assert out.shape == (3, 8, D)
+    assert rel_err(out, ref) <= 1e-2
+
+
+def test_paged_head_dim_256_config5_like():
+    # 64 sequences of up to 2K tokens at D = 256, GQA 16 / 4
+    g = _g(256)
+    B, Hq, Hkv, D, BS = 16, 16, 4, 256, 16
+    lens = torch.randint(1, 2049, (B,), generator=g, dtype=torch.int32)
+    q = torch.randn(B, Hq, 1, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, int(lens.max()), D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, int(lens.max()), D, generator=g).to(torch.bfloat16)
+    kc, vc, table, _ = paging.build_paged_cache(k, v, page_size=BS, shuffle=True, generator=_g(3))
+    out = run(q, kc, vc, table, lens, BS)
+    ref = eager.paged_decode_eager(q.double(), kc.double(), vc.double(), table, lens)
+    assert rel_err(out, ref) <= 1e-2
