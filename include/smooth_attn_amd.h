@@ -227,6 +227,22 @@ int sa_flash_fp8_fwd(const void* q8, const void* k8, const void* v, void* o,
                      int window_size, int v_dtype, sa_stream_t stream);
 
 /*
+ * Rotate-half RoPE of a [B, H, T, D] 16-bit tensor x (element strides
+ * x_strides, d stride 1, the others multiples of 8) into the contiguous
+ * [B, H, T, D] buffer out: for each pair (d, d + D/2) of row t,
+ * a' = a cos - b sin, b' = b cos + a sin in fp32 with cos/sin = fp32
+ * contiguous [T, D/2] tables, rounded to the input type.  D a multiple of
+ * 16.  RoPE attention at head dims other than 32, 64 and 128 is this
+ * rotation of Q and K followed by sa_flash_fwd.
+ * Replaces the rotation step of _sp2norm_rope_flash_fwd_kernel
+ * (kernels.py:2104-2224), which the reference runs only inside the fused
+ * kernel.
+ */
+int sa_rope_rotate(const void* x, void* out, const float* cos_table,
+                   const float* sin_table, int B, int H, int T, int D,
+                   const int64_t* x_strides, int dtype, sa_stream_t stream);
+
+/*
  * Bytes of workspace sa_flash_rope_fwd needs (the rotated K, contiguous
  * [B, Hkv, T, D] of the 16-bit type).  -1 for negative sizes.
  */

@@ -195,6 +195,40 @@ __global__ __launch_bounds__(256) void rope_rotate_rows(const T* __restrict__ k,
     *reinterpret_cast<u32x4*>(dst + D / 2) = bb;
 }
 
+// The same rotation for any head dim D that is a multiple of 16 (pairs of
+// 16-byte chunks (d, d + D/2)), from strided rows into a contiguous
+// [B, H, T, D] buffer: the first pass of RoPE attention at head dims the
+// fused Q rotation does not cover.
+template <typename T>
+__global__ __launch_bounds__(256) void rope_rotate_any(const T* __restrict__ x, T* __restrict__ out,
+                                                       const float* __restrict__ cs, const float* __restrict__ sn,
+                                                       int H, int T_, int D, int64_t s0, int64_t s1, int64_t s2,
+                                                       int64_t n_pairs) {
+    const int ppr = D / 16;  // chunk pairs per row
+    const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (gid >= n_pairs) return;
+    const int64_t row = gid / ppr;
+    const int c = static_cast<int>(gid - row * ppr);
+    const int64_t bh = row / T_;
+    const int t = static_cast<int>(row - bh * T_);
+    const int b = static_cast<int>(bh / H);
+    const int h = static_cast<int>(bh - static_cast<int64_t>(b) * H);
+    const T* src = x + b * s0 + h * s1 + t * s2 + c * 8;
+    u32x4 a = load16(src);
+    u32x4 bb = load16(src + D / 2);
+    float cv[8], sv[8];
+    const float* cr = cs + static_cast<int64_t>(t) * (D / 2) + c * 8;
+    const float* sr = sn + static_cast<int64_t>(t) * (D / 2) + c * 8;
+    *reinterpret_cast<float4*>(cv) = *reinterpret_cast<const float4*>(cr);
+    *reinterpret_cast<float4*>(cv + 4) = *reinterpret_cast<const float4*>(cr + 4);
+    *reinterpret_cast<float4*>(sv) = *reinterpret_cast<const float4*>(sr);
+    *reinterpret_cast<float4*>(sv + 4) = *reinterpret_cast<const float4*>(sr + 4);
+    rope_rotate8<T>(a, bb, cv, sv);
+    T* dst = out + row * D + c * 8;
+    *reinterpret_cast<u32x4*>(dst) = a;
+    *reinterpret_cast<u32x4*>(dst + D / 2) = bb;
+}
+
 // K/V tile loads: every tile is read by all query blocks of its head, so
 // these loads are cached (a nontemporal load would stream past L2).
 template <typename T>
@@ -823,6 +857,30 @@ extern "C" int sa_flash_fp8_fwd(const void* q8, const void* k8, const void* v, v
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     if (v8) return launch_flash_d<bf16, true, true>(prm, D, 0, s);
     return launch_flash_d<bf16, true, false>(prm, D, 0, s);
+}
+
+extern "C" int sa_rope_rotate(const void* x, void* out, const float* cos_table, const float* sin_table, int B,
+                              int H, int T, int D, const int64_t* x_strides, int dtype, sa_stream_t stream) {
+    using namespace sa;
+    if (dtype != SA_BF16 && dtype != SA_F16) return SA_ERR_BAD_DTYPE;
+    if (B < 0 || H < 0 || T < 0 || D <= 0 || D % 16 != 0) return SA_ERR_BAD_SHAPE;
+    if (!x || !out || !cos_table || !sin_table || !x_strides) return SA_ERR_NULL_POINTER;
+    const int64_t* s = x_strides;
+    if (s[3] != 1 || s[0] % 8 || s[1] % 8 || s[2] % 8 || !aligned16(x) || !aligned16(out) || !aligned16(cos_table) ||
+        !aligned16(sin_table))
+        return SA_ERR_BAD_STRIDE;
+    const int64_t n_pairs = static_cast<int64_t>(B) * H * T * (D / 16);
+    if (n_pairs == 0) return 0;
+    if ((n_pairs + 255) / 256 > INT32_MAX) return SA_ERR_BAD_SHAPE;
+    const dim3 grid(static_cast<unsigned>((n_pairs + 255) / 256));
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (dtype == SA_BF16)
+        rope_rotate_any<bf16><<<grid, 256, 0, st>>>(static_cast<const bf16*>(x), static_cast<bf16*>(out), cos_table,
+                                                    sin_table, H, T, D, s[0], s[1], s[2], n_pairs);
+    else
+        rope_rotate_any<f16><<<grid, 256, 0, st>>>(static_cast<const f16*>(x), static_cast<f16*>(out), cos_table,
+                                                   sin_table, H, T, D, s[0], s[1], s[2], n_pairs);
+    return status_from_launch();
 }
 
 extern "C" int64_t sa_flash_rope_workspace_size(int B, int Hkv, int T, int D) {

@@ -56,6 +56,8 @@ SIGNATURES = {
                                  c_void_p, c_int, c_int, c_int, c_int, c_int, _I64P, _I64P, _I64P, _I64P,
                                  c_float, c_int, c_int, c_void_p]),
     "sa_flash_rope_workspace_size": (c_int64, [c_int, c_int, c_int, c_int]),
+    "sa_rope_rotate": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, _I64P, c_int,
+                               c_void_p]),
     "sa_flash_rope_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                   c_void_p, c_int64, c_int, c_int, c_int, c_int, c_int, _I64P, _I64P, _I64P,
                                   _I64P, c_float, c_int, c_int, c_void_p]),

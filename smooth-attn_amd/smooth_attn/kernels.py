@@ -702,19 +702,44 @@ def _rope_tables(cos, sin, T, D):
     return fix(cos), fix(sin)
 
 
+def _rope_rotate(x, cos, sin):
+    """Rotate-half RoPE of a [B, H, T, D] 16-bit tensor into a new contiguous
+    tensor (sa_rope_rotate)."""
+    B, H, T, D = x.shape
+    x = _flash_operand(x)
+    out = torch.empty(B, H, T, D, device=x.device, dtype=x.dtype)
+    lib = _lib.load()
+    with _device_of(x):
+        st = lib.sa_rope_rotate(x.data_ptr(), out.data_ptr(), cos.data_ptr(), sin.data_ptr(), B, H, T, D,
+                                _lib.strides(x), _DTYPE_CODE[x.dtype], _stream(x))
+    _lib.check(st, "sa_rope_rotate")
+    return out
+
+
 def _sp2norm_rope_flash_fwd(q, k, v, cos, sin, scale, n_kv_groups=1, window_size=0, o=None):
     """(o, row_sums) of the RoPE forward; ``o`` may be a caller view (e.g. of a
-    [B, T, Hq, D] buffer) with 16-byte aligned rows."""
+    [B, T, Hq, D] buffer) with 16-byte aligned rows.  Head dims 32, 64 and
+    128 rotate Q in registers inside the fused kernel (K once into a
+    workspace); other head dims that are multiples of 16, up to 256, rotate
+    Q and K by sa_rope_rotate and run the plain fused forward (head dims
+    other than 32 / 64 / 128 / 256 zero-padded after the rotation)."""
     _check_same_device("q", q, k=k, v=v, cos=cos, sin=sin, o=o)
     B, H_q, T, D = q.shape
     H_kv = k.shape[1]
     if q.dtype not in (torch.bfloat16, torch.float16) or k.dtype != q.dtype or v.dtype != q.dtype:
         raise ValueError(f"RoPE attention expects bf16 or fp16 q/k/v of one dtype, got "
                          f"{q.dtype}/{k.dtype}/{v.dtype}")
-    if D not in _FLASH_HEAD_DIMS:  # rotate-half pairs d with d + D/2: no padding of the head dim
-        raise ValueError(f"RoPE attention supports head dims {_FLASH_HEAD_DIMS}, got {D}")
-    q, k, v = _flash_operand(q), _flash_operand(k), _flash_operand(v)
+    if D % 16 or not 16 <= D <= 256:  # rotate-half pairs 16-byte chunks d, d + D/2
+        raise ValueError(f"RoPE attention supports head dims that are multiples of 16 in 16..256, got {D}")
     cos, sin = _rope_tables(cos, sin, T, D)
+    if D not in _FLASH_HEAD_DIMS:
+        o_full, row_sums = _sp2norm_flash_fwd(_rope_rotate(q, cos, sin), _rope_rotate(k, cos, sin), v, scale,
+                                              n_kv_groups, window_size)
+        if o is None:
+            return o_full, row_sums
+        o.copy_(o_full)
+        return o, row_sums
+    q, k, v = _flash_operand(q), _flash_operand(k), _flash_operand(v)
     if o is None:
         o = torch.empty_like(q)
     row_sums = torch.empty(B, H_q, T, device=q.device, dtype=torch.float32)

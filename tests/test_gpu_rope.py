@@ -130,3 +130,37 @@ def test_transpose16_bit_exact(rows, cols, dtype):
     wide = torch.randn(rows, cols + 16, generator=g).to(dtype).to(DEV)
     ys = kernels._transpose16(wide[:, 8:8 + cols])
     assert torch.equal(ys.cpu(), wide[:, 8:8 + cols].cpu().t())
+
+
+@pytest.mark.parametrize("D", [16, 48, 80, 96, 160, 256])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_rope_other_head_dims(D, dtype):
+    # head dims other than 32 / 64 / 128: Q and K rotated by sa_rope_rotate,
+    # then the plain fused forward (D = 256 kernels, others zero-padded)
+    check_rope(*inputs(2, 4, 2, 150, D, dtype, seed=D), window=0)
+    check_rope(*inputs(1, 4, 4, 200, D, dtype, seed=D + 1, layout="bthd"), window=50)
+
+
+def test_rope_rotate_matches_oracle():
+    # sa_rope_rotate against the oracle's rotation, both in fp32 and rounded
+    # to bf16 once: the kernel may fuse a product into an FMA, so a value can
+    # round to the neighbouring bf16 number, never further
+    for D in (16, 64, 256):
+        x = torch.randn(2, 3, 70, D, generator=_g(D)).to(torch.bfloat16)
+        cos, sin = smooth_attn.precompute_rope_cos_sin(D, 70, device=DEV)
+        got = kernels._rope_rotate(x.to(DEV), cos, sin).cpu().float()
+        want = eager.apply_rope(x.float(), cos.cpu(), sin.cpu())
+        ulp = torch.ldexp(torch.ones_like(want), torch.frexp(want.abs().clamp(min=1e-30))[1] - 8)
+        assert bool(((got - want).abs() <= ulp).all()), D
+        assert float((got == want.to(torch.bfloat16).float()).float().mean()) > 0.99, D
+
+
+def test_rope_proj_head_dim_256():
+    B, H, Hkv, T, D, M = 1, 4, 2, 96, 256, 384
+    q, k, v = inputs(B, H, Hkv, T, D, torch.bfloat16, seed=77)
+    w_o = (torch.randn(H, D, M, generator=_g(78)) * 0.02).to(torch.bfloat16)
+    cos, sin = smooth_attn.precompute_rope_cos_sin(D, T, device=DEV)
+    out = smooth_attn.sp2norm_rope_flash_attention_proj(q.to(DEV), k.to(DEV), v.to(DEV), w_o.to(DEV), cos, sin)
+    ref = eager.rope_proj_eager(q.double(), k.double(), v.double(), w_o.double(), cos.cpu(), sin.cpu())
+    assert out.shape == (B, T, M)
+    assert rel_err(out, ref) <= 1e-2
