@@ -214,7 +214,8 @@ int sa_fp8_quantize(const void* x, void* x8, int64_t n, int dtype,
  * ignored, may be NULL, for bf16 v).  Scores = (q8 . k8) * q_s * k_s *
  * attn_scale on fp8 MFMA; y rounded to bf16 and multiplied with v (as bf16)
  * on bf16 MFMA, times v_s.  o: bf16 [B, Hq, T, D]; row_sums nullable.
- * Layout rules as sa_flash_fwd; D in {32, 64, 128}.
+ * Layout rules as sa_flash_fwd; D in {32, 64, 128} (the Python wrapper runs
+ * head dims 129..256 on sa_flash_fwd with the fp8 codes widened to bf16).
  * Replaces _sp2norm_fp8_flash_fwd (kernels.py:2604-2627) and its kernel
  * _sp2norm_fp8_flash_fwd_kernel (:2498-2589).
  */

@@ -864,6 +864,12 @@ def _sp2norm_fp8_flash_fwd(q_fp8, k_fp8, v_fp8, q_scale, k_scale, v_scale, attn_
     H_kv = k_fp8.shape[1]
     if q_fp8.dtype != torch.float8_e4m3fn or k_fp8.dtype != torch.float8_e4m3fn:
         raise ValueError("q and k must be float8_e4m3fn")
+    if v_fp8.dtype not in (torch.float8_e4m3fn, torch.bfloat16):
+        raise ValueError("v must be float8_e4m3fn or bfloat16")
+    if D < 1 or D > 256:
+        raise ValueError(f"fused attention supports head dims 1..256, got {D}")
+    if D > 128:
+        return _fp8_wide_fwd(q_fp8, k_fp8, v_fp8, q_scale, k_scale, v_scale, attn_scale, n_kv_groups, window_size)
     Dk = _kernel_head_dim(D)
     if Dk != D:
         # zero codes pad the head dim exactly (F.pad works on the bytes)
@@ -872,12 +878,7 @@ def _sp2norm_fp8_flash_fwd(q_fp8, k_fp8, v_fp8, q_scale, k_scale, v_scale, attn_
         o, row_sums = _sp2norm_fp8_flash_fwd(pad8(q_fp8), pad8(k_fp8), pad8(v_fp8), q_scale, k_scale, v_scale,
                                              attn_scale, n_kv_groups, window_size)
         return o[..., :D].contiguous(), row_sums
-    if v_fp8.dtype == torch.float8_e4m3fn:
-        v_code = _lib.SA_FP8_E4M3FN
-    elif v_fp8.dtype == torch.bfloat16:
-        v_code = _lib.SA_BF16
-    else:
-        raise ValueError("v must be float8_e4m3fn or bfloat16")
+    v_code = _lib.SA_FP8_E4M3FN if v_fp8.dtype == torch.float8_e4m3fn else _lib.SA_BF16
     dev = q_fp8.device
     q8, k8, v8 = _flash_operand(q_fp8), _flash_operand(k_fp8), _flash_operand(v_fp8)
     o = torch.empty(B, H_q, T, D, device=dev, dtype=torch.bfloat16)
@@ -892,6 +893,24 @@ def _sp2norm_fp8_flash_fwd(q_fp8, k_fp8, v_fp8, q_scale, k_scale, v_scale, attn_
             _lib.strides(v8), _lib.strides(o), float(attn_scale), int(window_size), v_code, _stream(q8),
         )
     _lib.check(st, "sa_flash_fp8_fwd")
+    return o, row_sums
+
+
+def _fp8_wide_fwd(q8, k8, v8, q_scale, k_scale, v_scale, attn_scale, n_kv_groups, window_size):
+    """fp8 attention at head dims 129..256: the e4m3fn codes are widened to
+    bf16 (exact: every e4m3fn value is a bf16 value), the bf16 head-dim-256
+    kernels run with the dequantisation folded into the score scale
+    (q_s * k_s * attn_scale), and fp8 V's scale multiplies the output.  The
+    scales are read on the host here (one synchronisation, as the
+    reference's entry point makes three)."""
+    qs = float(q_scale.reshape(-1)[0]) if isinstance(q_scale, torch.Tensor) else float(q_scale)
+    ks = float(k_scale.reshape(-1)[0]) if isinstance(k_scale, torch.Tensor) else float(k_scale)
+    s_eff = float(attn_scale) * qs * ks
+    o, row_sums = _sp2norm_flash_fwd(q8.to(torch.bfloat16), k8.to(torch.bfloat16), v8.to(torch.bfloat16), s_eff,
+                                     n_kv_groups, window_size)
+    if v8.dtype == torch.float8_e4m3fn and v_scale is not None:
+        vs = float(v_scale.reshape(-1)[0]) if isinstance(v_scale, torch.Tensor) else float(v_scale)
+        o = (o.float() * vs).to(torch.bfloat16)
     return o, row_sums
 
 

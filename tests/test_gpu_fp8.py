@@ -264,3 +264,28 @@ def test_fp8_forward_head_dims_below_128(D):
     assert o.shape == (1, 4, 130, D) and o.is_contiguous()
     assert rel_err(o, ref) <= 1e-2
     assert rel_err(rs, ref_rs) <= 1e-4
+
+
+@pytest.mark.parametrize("D", [160, 256])
+@pytest.mark.parametrize("v_fp8", [True, False])
+def test_fp8_forward_head_dims_above_128(D, v_fp8):
+    # head dims 129..256: codes widened to bf16 (exact) on the D = 256 bf16
+    # kernels, so the scores are exact-product fp32 sums and the row sums
+    # meet 1e-5; with fp8 V the output is rounded once more after v_scale
+    q, k, v = _fp8_case(1, 4, 2, 150, D, seed=D + v_fp8)
+    q8, qs = eager.quantize_to_fp8(q)
+    k8, ks = eager.quantize_to_fp8(k)
+    if v_fp8:
+        vv, vs = eager.quantize_to_fp8(v)
+    else:
+        vv, vs = v, torch.tensor(1.0)
+    scale = 1 / math.sqrt(D)
+    o, rs = kernels._sp2norm_fp8_flash_fwd(q8.to(DEV), k8.to(DEV), vv.to(DEV), qs.to(DEV), ks.to(DEV),
+                                           vs.to(DEV) if v_fp8 else None, scale, 2, 40)
+    ref, ref_rs = eager.fp8_flash_attention_eager(q8, k8, vv, qs, ks, vs, scale, window_size=40,
+                                                  return_row_sums=True)
+    assert o.shape == (1, 4, 150, D) and o.dtype == torch.bfloat16
+    assert rel_err(o, ref) <= 1e-2
+    assert rel_err(rs, ref_rs) <= 1e-5
+    out = smooth_attn.sp2norm_fp8_flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), quantize_v=v_fp8)
+    assert out.shape == (1, 4, 150, D) and not out.isnan().any()

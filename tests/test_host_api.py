@@ -271,8 +271,8 @@ def test_fused_entry_points_refuse_meta_tensors(case, no_library):
 
 
 def test_head_dims_and_page_sizes_checked_before_launch(no_library):
-    # fused attention: any head dim up to 256 (zero-padded to 32 / 64 / 128 /
-    # 256 for the kernels), the fp8 path up to 128; larger head dims, fp64 and
+    # fused attention, fp8 included: any head dim up to 256 (zero-padded to
+    # 32 / 64 / 128 / 256 for the kernels); larger head dims, fp64 and
     # mixed dtypes are refused with a clear error; paged decode: power-of-two
     # page sizes only
     mk = lambda shape, dtype: _OnDevice.make(torch.zeros(shape, dtype=dtype), 0)
@@ -283,8 +283,8 @@ def test_head_dims_and_page_sizes_checked_before_launch(no_library):
                 kernels._sp2norm_flash_fwd(q, q, q, 0.1)
             with pytest.raises(ValueError, match="head dims 1..256"):
                 kernels._sp2norm_flash_bwd(q, q, q, q, q, mk((1, 2, 8), torch.float32), 0.1)
-    q8 = mk((1, 2, 8, 160), torch.float8_e4m3fn)
-    with pytest.raises(ValueError, match="head dims 1..128"):
+    q8 = mk((1, 2, 8, 264), torch.float8_e4m3fn)
+    with pytest.raises(ValueError, match="head dims 1..256"):
         kernels._sp2norm_fp8_flash_fwd(q8, q8, q8, 1.0, 1.0, 1.0, 0.1)
     dims = (1, 16, 32, 33, 64, 96, 128, 129, 200, 256)
     assert [kernels._kernel_head_dim(d, torch.bfloat16) for d in dims] == [32, 32, 32, 64, 64, 128, 128, 256, 256, 256]
