@@ -333,6 +333,9 @@ def bench_next_rows(torch):
     """The rows built after the hot path, each timed by the same protocol:
     - fp32 fused attention forward and backward on config 3's shape (fp32
       MFMA, against the 157.3 TFLOP/s dense fp32 peak);
+    - bf16 attention forward and backward at head dim 256, [4,16,4096,256]
+      (config 3's FLOPs), and paged decode at head dim 256 on config 5's
+      layout with Hq 16 / Hkv 4 (config 5's bytes);
     - RoPE-fused attention forward on config 3's shape (K rotated once by a
       streaming kernel, Q in registers; the time includes the rotation),
       and the RoPE + W_o projection variant (RoPE forward plus one fp32-
@@ -380,6 +383,32 @@ def bench_next_rows(torch):
                              "fwd_frac_fp32_peak": round(fl / us_f / 1e6 / FP32_PEAK_TFLOPS, 4),
                              "bwd_frac_fp32_peak": round(2.5 * fl / us_b / 1e6 / FP32_PEAK_TFLOPS, 4)}
     del q, k, v, do, o, rs
+    torch.cuda.empty_cache()
+
+    # head dim 256 (its own one-wave-per-SIMD kernels): [4,16,4096,256] has config 3's FLOPs
+    q, k, v, do = (torch.randn(4, 16, L, 256, generator=gen, device=dev).to(torch.bfloat16) for _ in range(4))
+    o, rs = sa.kernels._sp2norm_flash_fwd(q, k, v, 1 / 16)
+    us_f = med(lambda: sa.kernels._sp2norm_flash_fwd(q, k, v, 1 / 16))
+    us_b = med(lambda: sa.kernels._sp2norm_flash_bwd(q, k, v, o, do, rs, 1 / 16))
+    fl256 = attn_flops(4, 16, L, 256)
+    out["attention_d256"] = {"shape": [4, 16, L, 256], "fwd_us": round(us_f, 1), "bwd_us": round(us_b, 1),
+                             "fwd_frac_bf16_peak": round(fl256 / us_f / 1e6 / BF16_PEAK_TFLOPS, 4),
+                             "bwd_frac_bf16_peak": round(2.5 * fl256 / us_b / 1e6 / BF16_PEAK_TFLOPS, 4)}
+    del q, k, v, do, o, rs
+    torch.cuda.empty_cache()
+
+    # paged decode at head dim 256 on config 5's layout with Hq 16 / Hkv 4
+    # (the same 4 KB of K and V per token as config 5)
+    lens, table, n_pages = config5_inputs(torch)
+    kc = torch.randn(n_pages, 4, 16, 256, generator=gen, device=dev).to(torch.bfloat16)
+    vc = torch.randn(n_pages, 4, 16, 256, generator=gen, device=dev).to(torch.bfloat16)
+    qd = torch.randn(64, 16, 1, 256, generator=gen, device=dev).to(torch.bfloat16)
+    table_d, lens_d = table.to(dev), lens.to(torch.int32).to(dev)
+    us = med(lambda: sa.sp2norm_paged_attention(qd, kc, vc, table_d, lens_d))
+    nb = paged_bytes(lens, Hq=16, D=256)
+    out["paged_decode_d256"] = {"us": round(us, 1), "GBs": round(nb / us / 1e3, 1),
+                                "frac_hbm_peak": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)}
+    del kc, vc, qd
     torch.cuda.empty_cache()
 
     Bn, Hn, Ln = 4, 16, 4096
