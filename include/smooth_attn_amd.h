@@ -228,8 +228,9 @@ int sa_flash_fp8_fwd(const void* q8, const void* k8, const void* v, void* o,
                      int window_size, int v_dtype, sa_stream_t stream);
 
 /*
- * Rotate-half RoPE of a [B, H, T, D] 16-bit tensor x (element strides
- * x_strides, d stride 1, the others multiples of 8) into the contiguous
+ * Rotate-half RoPE of a [B, H, T, D] tensor x (dtype SA_BF16, SA_F16 or
+ * SA_F32; element strides x_strides, d stride 1, the others multiples of 16
+ * bytes) into the contiguous
  * [B, H, T, D] buffer out: for each pair (d, d + D/2) of row t,
  * a' = a cos - b sin, b' = b cos + a sin in fp32 with cos/sin = fp32
  * contiguous [T, D/2] tables, rounded to the input type.  D a multiple of

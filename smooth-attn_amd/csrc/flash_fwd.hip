@@ -214,8 +214,6 @@ __global__ __launch_bounds__(256) void rope_rotate_any(const T* __restrict__ x, 
     const int b = static_cast<int>(bh / H);
     const int h = static_cast<int>(bh - static_cast<int64_t>(b) * H);
     const T* src = x + b * s0 + h * s1 + t * s2 + c * 8;
-    u32x4 a = load16(src);
-    u32x4 bb = load16(src + D / 2);
     float cv[8], sv[8];
     const float* cr = cs + static_cast<int64_t>(t) * (D / 2) + c * 8;
     const float* sr = sn + static_cast<int64_t>(t) * (D / 2) + c * 8;
@@ -223,10 +221,32 @@ __global__ __launch_bounds__(256) void rope_rotate_any(const T* __restrict__ x, 
     *reinterpret_cast<float4*>(cv + 4) = *reinterpret_cast<const float4*>(cr + 4);
     *reinterpret_cast<float4*>(sv) = *reinterpret_cast<const float4*>(sr);
     *reinterpret_cast<float4*>(sv + 4) = *reinterpret_cast<const float4*>(sr + 4);
-    rope_rotate8<T>(a, bb, cv, sv);
     T* dst = out + row * D + c * 8;
-    *reinterpret_cast<u32x4*>(dst) = a;
-    *reinterpret_cast<u32x4*>(dst + D / 2) = bb;
+    if constexpr (std::is_same_v<T, float>) {  // 8 fp32 elements: two 16-byte loads per half
+        float a[8], bb[8];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            *reinterpret_cast<float4*>(a + 4 * j) = *reinterpret_cast<const float4*>(src + 4 * j);
+            *reinterpret_cast<float4*>(bb + 4 * j) = *reinterpret_cast<const float4*>(src + D / 2 + 4 * j);
+        }
+        float ra[8], rb[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            ra[e] = a[e] * cv[e] - bb[e] * sv[e];
+            rb[e] = bb[e] * cv[e] + a[e] * sv[e];
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            *reinterpret_cast<float4*>(dst + 4 * j) = *reinterpret_cast<const float4*>(ra + 4 * j);
+            *reinterpret_cast<float4*>(dst + D / 2 + 4 * j) = *reinterpret_cast<const float4*>(rb + 4 * j);
+        }
+    } else {
+        u32x4 a = load16(src);
+        u32x4 bb = load16(src + D / 2);
+        rope_rotate8<T>(a, bb, cv, sv);
+        *reinterpret_cast<u32x4*>(dst) = a;
+        *reinterpret_cast<u32x4*>(dst + D / 2) = bb;
+    }
 }
 
 // K/V tile loads: every tile is read by all query blocks of its head, so
@@ -862,19 +882,23 @@ extern "C" int sa_flash_fp8_fwd(const void* q8, const void* k8, const void* v, v
 extern "C" int sa_rope_rotate(const void* x, void* out, const float* cos_table, const float* sin_table, int B,
                               int H, int T, int D, const int64_t* x_strides, int dtype, sa_stream_t stream) {
     using namespace sa;
-    if (dtype != SA_BF16 && dtype != SA_F16) return SA_ERR_BAD_DTYPE;
+    if (dtype != SA_BF16 && dtype != SA_F16 && dtype != SA_F32) return SA_ERR_BAD_DTYPE;
     if (B < 0 || H < 0 || T < 0 || D <= 0 || D % 16 != 0) return SA_ERR_BAD_SHAPE;
     if (!x || !out || !cos_table || !sin_table || !x_strides) return SA_ERR_NULL_POINTER;
     const int64_t* s = x_strides;
-    if (s[3] != 1 || s[0] % 8 || s[1] % 8 || s[2] % 8 || !aligned16(x) || !aligned16(out) || !aligned16(cos_table) ||
-        !aligned16(sin_table))
+    const int64_t q16 = dtype == SA_F32 ? 4 : 8;  // elements per 16 bytes
+    if (s[3] != 1 || s[0] % q16 || s[1] % q16 || s[2] % q16 || !aligned16(x) || !aligned16(out) ||
+        !aligned16(cos_table) || !aligned16(sin_table))
         return SA_ERR_BAD_STRIDE;
     const int64_t n_pairs = static_cast<int64_t>(B) * H * T * (D / 16);
     if (n_pairs == 0) return 0;
     if ((n_pairs + 255) / 256 > INT32_MAX) return SA_ERR_BAD_SHAPE;
     const dim3 grid(static_cast<unsigned>((n_pairs + 255) / 256));
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    if (dtype == SA_BF16)
+    if (dtype == SA_F32)
+        rope_rotate_any<float><<<grid, 256, 0, st>>>(static_cast<const float*>(x), static_cast<float*>(out),
+                                                     cos_table, sin_table, H, T, D, s[0], s[1], s[2], n_pairs);
+    else if (dtype == SA_BF16)
         rope_rotate_any<bf16><<<grid, 256, 0, st>>>(static_cast<const bf16*>(x), static_cast<bf16*>(out), cos_table,
                                                     sin_table, H, T, D, s[0], s[1], s[2], n_pairs);
     else

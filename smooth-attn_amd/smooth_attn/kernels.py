@@ -718,21 +718,22 @@ def _rope_rotate(x, cos, sin):
 
 def _sp2norm_rope_flash_fwd(q, k, v, cos, sin, scale, n_kv_groups=1, window_size=0, o=None):
     """(o, row_sums) of the RoPE forward; ``o`` may be a caller view (e.g. of a
-    [B, T, Hq, D] buffer) with 16-byte aligned rows.  Head dims 32, 64 and
-    128 rotate Q in registers inside the fused kernel (K once into a
-    workspace); other head dims that are multiples of 16, up to 256, rotate
-    Q and K by sa_rope_rotate and run the plain fused forward (head dims
-    other than 32 / 64 / 128 / 256 zero-padded after the rotation)."""
+    [B, T, Hq, D] buffer) with 16-byte aligned rows.  16-bit head dims 32,
+    64 and 128 rotate Q in registers inside the fused kernel (K once into a
+    workspace); fp32, and other head dims that are multiples of 16 up to
+    256, rotate Q and K by sa_rope_rotate and run the plain fused forward
+    (head dims other than 32 / 64 / 128 / 256 zero-padded after the
+    rotation)."""
     _check_same_device("q", q, k=k, v=v, cos=cos, sin=sin, o=o)
     B, H_q, T, D = q.shape
     H_kv = k.shape[1]
-    if q.dtype not in (torch.bfloat16, torch.float16) or k.dtype != q.dtype or v.dtype != q.dtype:
-        raise ValueError(f"RoPE attention expects bf16 or fp16 q/k/v of one dtype, got "
+    if q.dtype not in (torch.bfloat16, torch.float16, torch.float32) or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError(f"RoPE attention expects bf16, fp16 or fp32 q/k/v of one dtype, got "
                          f"{q.dtype}/{k.dtype}/{v.dtype}")
-    if D % 16 or not 16 <= D <= 256:  # rotate-half pairs 16-byte chunks d, d + D/2
+    if D % 16 or not 16 <= D <= 256:  # rotate-half pairs 8-element chunks d, d + D/2
         raise ValueError(f"RoPE attention supports head dims that are multiples of 16 in 16..256, got {D}")
     cos, sin = _rope_tables(cos, sin, T, D)
-    if D not in _FLASH_HEAD_DIMS:
+    if D not in _FLASH_HEAD_DIMS or q.dtype == torch.float32:
         o_full, row_sums = _sp2norm_flash_fwd(_rope_rotate(q, cos, sin), _rope_rotate(k, cos, sin), v, scale,
                                               n_kv_groups, window_size)
         if o is None:
@@ -796,6 +797,8 @@ def sp2norm_rope_flash_attention_proj(q, k, v, w_o, cos, sin, *, scale=None, win
     o_bthd = torch.empty(B, T, H_q, D, device=q.device, dtype=q.dtype)
     _sp2norm_rope_flash_fwd(q, k, v, cos, sin, scale, H_q // H_kv, window_size, o=o_bthd.transpose(1, 2))
     w = w_o.to(q.dtype).reshape(H_q * D, D_model)
+    if q.dtype == torch.float32:
+        return torch.matmul(o_bthd.view(B * T, H_q * D), w).view(B, T, D_model)
     # W_o^T contiguous: the GEMM then takes its faster layout (F.linear form)
     w_t = _transpose16(w)
     return F.linear(o_bthd.view(B * T, H_q * D), w_t).view(B, T, D_model)

@@ -164,3 +164,22 @@ def test_rope_proj_head_dim_256():
     ref = eager.rope_proj_eager(q.double(), k.double(), v.double(), w_o.double(), cos.cpu(), sin.cpu())
     assert out.shape == (B, T, M)
     assert rel_err(out, ref) <= 1e-2
+
+
+@pytest.mark.parametrize("D", [32, 128, 256])
+def test_rope_fp32(D):
+    # fp32 q/k/v: rotation in fp32 (sa_rope_rotate), then the fp32-MFMA
+    # attention; fp32 output held to 1e-5 against the float64 oracle
+    q, k, v = inputs(1, 4, 2, 130, D, torch.float32, seed=D + 5)
+    T = q.shape[2]
+    cos, sin = smooth_attn.precompute_rope_cos_sin(D, T, device=DEV)
+    out = smooth_attn.sp2norm_rope_flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), cos, sin, window_size=60)
+    ref = eager.rope_flash_attention_eager(q.double(), k.double(), v.double(), cos.cpu(), sin.cpu(),
+                                           window_size=60, round_to=None)
+    assert out.dtype == torch.float32 and out.shape == q.shape
+    assert rel_err(out, ref) <= 1e-5
+    w_o = torch.randn(4, D, 96, generator=_g(D)) * 0.05
+    proj = smooth_attn.sp2norm_rope_flash_attention_proj(q.to(DEV), k.to(DEV), v.to(DEV), w_o.to(DEV), cos, sin)
+    ref_p = eager.rope_proj_eager(q.double(), k.double(), v.double(), w_o.double(), cos.cpu(), sin.cpu(),
+                                  round_to=None)
+    assert proj.dtype == torch.float32 and rel_err(proj, ref_p) <= 1e-5
