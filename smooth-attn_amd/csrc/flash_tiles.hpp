@@ -93,6 +93,13 @@ __device__ __forceinline__ void weight_rr16(float s, float sc, float& y, float& 
     y = sp * sp;
 }
 
+// x where c holds, +0 where not, as a bitwise AND: the value is always
+// computed, so the compiler cannot turn the choice into a branch around the
+// computation (a divergent branch per score, which it does for a select).
+__device__ __forceinline__ float keep_if(bool c, float x) {
+    return __uint_as_float(__float_as_uint(x) & (0u - static_cast<uint32_t>(c)));
+}
+
 // A lane's D / 16 operand chunks of one row: x[c] = row[16c + 8 hi .. +7].
 template <int D, typename T>
 __device__ __forceinline__ void load_frags(const T* row, int hi, u32x4 (&x)[D / 16]) {

@@ -146,7 +146,7 @@ __global__ __launch_bounds__(64 * kWW) void flash_fwd_wide_kernel(WideParams<T> 
             const int key = k0 + 8 * (v >> 2) + 4 * hi + (v & 3);
             float w, rr;
             weight_rr16<EXACT>(s[v], sc, w, rr);
-            y[v] = static_cast<unsigned>(qi - key) < weff ? w : 0.f;
+            y[v] = keep_if(static_cast<unsigned>(qi - key) < weff, w);
             ssum += y[v];
         }
         u32x4 pw[2];
@@ -253,7 +253,7 @@ __global__ __launch_bounds__(64 * kWW) void flash_bwd_dq_wide_kernel(WideParams<
                 const int key = k0 + 8 * (v >> 2) + 4 * hi + (v & 3);
                 float y, rr;
                 weight_rr16<EXACT>(s[v], sc, y, rr);
-                ds[v] = static_cast<unsigned>(qi - key) < weff ? dp[v] * y * rr : 0.f;
+                ds[v] = keep_if(static_cast<unsigned>(qi - key) < weff, dp[v] * y * rr);
             }
             u32x4 dsw[2];
             pack_b<T>(ds, dsw);
@@ -335,38 +335,42 @@ __global__ __launch_bounds__(64 * kWW) void flash_bwd_kv_wide_kernel(WideParams<
             trld.issue(op, q0, T_, ldsTr[buf]);
         }
     };
+    // Lane l of every wave loads row l % 32's 1/R (l < 32) or -delta; the
+    // four waves store the same values, so no branch divides the loop.
     auto row_value = [&](int it) {
         int hq, q0;
         tile_of(it, hq, q0);
-        const int64_t idx = (static_cast<int64_t>(b) * p.Hq + hq) * T_ + min(q0 + (tid & (kWT - 1)), T_ - 1);
-        return tid < kWT ? 1.f / p.rs[idx] : -p.delta[idx];
+        const int64_t idx = (static_cast<int64_t>(b) * p.Hq + hq) * T_ + min(q0 + (lane & (kWT - 1)), T_ - 1);
+        const float rinv = 1.f / p.rs[idx], nd = -p.delta[idx];
+        return keep_if(lane < kWT, rinv) + keep_if(lane >= kWT, nd);
     };
-    float rnext = 0.f;
     issue(0, 0);
-    if (tid < 2 * kWT) {
-        ldr[0][tid / kWT][tid & (kWT - 1)] = row_value(0);
-        if (n_it > 1) rnext = row_value(1);
-    }
+    ldr[0][lane / kWT][lane & (kWT - 1)] = row_value(0);
+    float rnext = row_value(min(1, n_it - 1));
     wide_wait_vmem();
     __syncthreads();
     for (int it = 0; it < n_it; ++it) {
         const int buf = it & 1;
-        if (it + 1 < n_it) {  // stage buf ^ 1 was released by the barrier ending iteration it - 1
-            issue(it + 1, buf ^ 1);
-            if (tid < 2 * kWT) {
-                ldr[buf ^ 1][tid / kWT][tid & (kWT - 1)] = rnext;
-                if (it + 2 < n_it) rnext = row_value(it + 2);
-            }
-        }
+        // stage buf ^ 1 was released by the barrier ending iteration it - 1;
+        // the last iteration reloads its own tile there (unused)
+        issue(min(it + 1, n_it - 1), buf ^ 1);
+        ldr[buf ^ 1][lane / kWT][lane & (kWT - 1)] = rnext;
+        rnext = row_value(min(it + 2, n_it - 1));
         int hq, q0;
         tile_of(it, hq, q0);
-        // some query of the tile sees some key of the wave
         {
             const f32x16 s = mma_rows16<T, D>(ldsQ[buf], l32, hi, kf, f32x16{});  // S: rows queries, column key
+            // this lane's rows r = 8 m + 4 hi .. +3 of 1/R and -delta
+            float ir[16], nd[16];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                *reinterpret_cast<float4*>(ir + 4 * m) = *reinterpret_cast<const float4*>(&ldr[buf][0][8 * m + 4 * hi]);
+                *reinterpret_cast<float4*>(nd + 4 * m) = *reinterpret_cast<const float4*>(&ldr[buf][1][8 * m + 4 * hi]);
+            }
             f32x16 dp;
             if constexpr (DK) {
 #pragma unroll
-                for (int v = 0; v < 16; ++v) dp[v] = ldr[buf][1][8 * (v >> 2) + 4 * hi + (v & 3)];
+                for (int v = 0; v < 16; ++v) dp[v] = nd[v];
                 dp = mma_rows16<T, D>(ldsO[buf], l32, hi, vf, dp);  // dP - delta
             }
             ColOperands<T, D> at;
@@ -378,10 +382,10 @@ __global__ __launch_bounds__(64 * kWW) void flash_bwd_kv_wide_kernel(WideParams<
                 const int q = q0 + r;
                 float y, rr;
                 weight_rr16<EXACT>(s[v], sc, y, rr);
-                const float yi = y * ldr[buf][0][r];
+                const float yi = y * ir[v];
                 const bool ok = static_cast<unsigned>(q - kj) < weff && q < T_;
-                if constexpr (DK) x[v] = ok ? dp[v] * yi * rr : 0.f;  // dS
-                else x[v] = ok ? yi : 0.f;                             // P
+                if constexpr (DK) x[v] = keep_if(ok, dp[v] * yi * rr);  // dS
+                else x[v] = keep_if(ok, yi);                            // P
             }
             u32x4 xw[2];
             pack_b<T>(x, xw);
