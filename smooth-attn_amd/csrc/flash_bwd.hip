@@ -442,14 +442,16 @@ __global__ __launch_bounds__(kBwdThreads, SA_BWD_DKDV_MINB) void flash_bwd_dkdv_
         issue_swz_tile<D>(qp + static_cast<int64_t>(q0) * qsb, qsb, nrows, lds + (2 * buf) * Tl::BYTES, wave, qoff);
         issue_swz_tile<D>(dop + static_cast<int64_t>(q0) * dsb, dsb, nrows, lds + (2 * buf + 1) * Tl::BYTES, wave,
                           dooff);
+        // the raw row sum or delta, turned into 1/R or -delta only when it is
+        // stored an iteration later, so this load's latency is not waited for here
         if (tid < 2 * kBwdQT) {
             const int r = tid & (kBwdQT - 1);
             const int64_t idx = (static_cast<int64_t>(b) * p.Hq + hq) * T_ + min(q0 + r, T_ - 1);
-            rst = tid < kBwdQT ? 1.f / p.rs[idx] : -p.delta[idx];
+            rst = (tid < kBwdQT ? p.rs : p.delta)[idx];
         }
     };
     auto store_rs = [&](int buf) {
-        if (tid < 2 * kBwdQT) ldr[buf][tid / kBwdQT][tid & (kBwdQT - 1)] = rst;
+        if (tid < 2 * kBwdQT) ldr[buf][tid / kBwdQT][tid & (kBwdQT - 1)] = tid < kBwdQT ? 1.f / rst : -rst;
     };
 
     // One query tile (iteration it: head g = it / nq, tile qt_begin + it % nq)

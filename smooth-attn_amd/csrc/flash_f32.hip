@@ -401,9 +401,10 @@ __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 12
         const int hq = hk * p.G + g;
         qreg.load(p.q + b * p.qs[0] + hq * p.qs[1], p.qs[2], q0, T_, tid);
         oreg.load(p.dout + b * p.dos[0] + hq * p.dos[1], p.dos[2], q0, T_, tid);
+        // raw row sum or delta; 1/R or -delta is formed where it is stored
         if (tid < 2 * kFT) {
             const int64_t idx = (static_cast<int64_t>(b) * p.Hq + hq) * T_ + min(q0 + (tid & (kFT - 1)), T_ - 1);
-            rst = tid < kFT ? 1.f / p.rs[idx] : -p.delta[idx];
+            rst = (tid < kFT ? p.rs : p.delta)[idx];
         }
     };
     fetch(0);
@@ -411,7 +412,7 @@ __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 12
         __syncthreads();
         qreg.store(ldsQ, ldsQt, tid);
         oreg.store(ldsO, ldsOt, tid);
-        if (tid < 2 * kFT) ldr[tid / kFT][tid & (kFT - 1)] = rst;
+        if (tid < 2 * kFT) ldr[tid / kFT][tid & (kFT - 1)] = tid < kFT ? 1.f / rst : -rst;
         __syncthreads();
         const int g = it / nq;
         const int q0 = (qt_begin + it - g * nq) * kFT;

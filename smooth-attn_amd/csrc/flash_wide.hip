@@ -335,17 +335,21 @@ __global__ __launch_bounds__(64 * kWW) void flash_bwd_kv_wide_kernel(WideParams<
             trld.issue(op, q0, T_, ldsTr[buf]);
         }
     };
-    // Lane l of every wave loads row l % 32's 1/R (l < 32) or -delta; the
-    // four waves store the same values, so no branch divides the loop.
+    // Lane l of every wave loads row l % 32's row sum (l < 32) or delta (the
+    // four waves store the same values, so no branch divides the loop); the
+    // raw value becomes 1/R or -delta only when it is stored an iteration
+    // later, so the load's latency is not waited for where it is issued.
     auto row_value = [&](int it) {
         int hq, q0;
         tile_of(it, hq, q0);
         const int64_t idx = (static_cast<int64_t>(b) * p.Hq + hq) * T_ + min(q0 + (lane & (kWT - 1)), T_ - 1);
-        const float rinv = 1.f / p.rs[idx], nd = -p.delta[idx];
-        return keep_if(lane < kWT, rinv) + keep_if(lane >= kWT, nd);
+        return (lane < kWT ? p.rs : p.delta)[idx];
+    };
+    auto staged = [&](float raw) {
+        return lane < kWT ? 1.f / raw : -raw;
     };
     issue(0, 0);
-    ldr[0][lane / kWT][lane & (kWT - 1)] = row_value(0);
+    ldr[0][lane / kWT][lane & (kWT - 1)] = staged(row_value(0));
     float rnext = row_value(min(1, n_it - 1));
     wide_wait_vmem();
     __syncthreads();
@@ -354,7 +358,7 @@ __global__ __launch_bounds__(64 * kWW) void flash_bwd_kv_wide_kernel(WideParams<
         // stage buf ^ 1 was released by the barrier ending iteration it - 1;
         // the last iteration reloads its own tile there (unused)
         issue(min(it + 1, n_it - 1), buf ^ 1);
-        ldr[buf ^ 1][lane / kWT][lane & (kWT - 1)] = rnext;
+        ldr[buf ^ 1][lane / kWT][lane & (kWT - 1)] = staged(rnext);
         rnext = row_value(min(it + 2, n_it - 1));
         int hq, q0;
         tile_of(it, hq, q0);
