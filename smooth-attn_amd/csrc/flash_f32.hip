@@ -22,6 +22,7 @@
 // [32][D + 4] and, where the transposed operand is needed, [D][36]); the
 // next tile's global loads are in flight while the current one is used.
 #include "flash_f32.hpp"
+#include "flash_tiles.hpp"
 
 namespace sa {
 namespace {
@@ -174,6 +175,14 @@ __device__ __forceinline__ void store_cols(float* row, int hi, const f32x16 (&ac
 // ---------------------------------------------------------------------------
 // Forward
 // ---------------------------------------------------------------------------
+// Tiles that none of a wave's rows sees are skipped at D <= 128; at D = 256
+// (one wave per SIMD, accumulators in AGPRs) the branch made the compiler
+// move every accumulator between AGPRs and VGPRs each tile, so there the
+// masks zero those tiles instead (backward 39.1 -> 31.0 ms on
+// [4,16,4096,256]; at D = 128 skipping is faster, 21.3 vs 24.0 ms).
+template <int D>
+constexpr bool kSkipIdle = D <= 128;
+
 // Every kernel here is held to two waves per SIMD.  Left to itself the
 // compiler gives the D = 128 forward 258 registers and one wave (config 3's
 // shape in fp32: 7.7 ms vs 5.0 ms), the D = 64 dK/dV kernel 290 registers
@@ -231,7 +240,7 @@ __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 12
         }
         const int k0 = t * kFT;
         const bool active = k0 <= q0 + 31 && !(W > 0 && q0 - (k0 + 31) >= W);
-        if (!active) continue;
+        if (kSkipIdle<D> && !active) continue;
         const f32x16 s = mma_rows<D>(ldsK, l32, hi, qv, f32x16{});  // S^T: rows keys, column query
         float pv[16];
 #pragma unroll
@@ -239,7 +248,7 @@ __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 12
             const int key = k0 + 8 * (v >> 2) + 4 * hi + (v & 3);
             float y, rr;
             weight_rr<EXACT>(s[v], sc, y, rr);
-            y = static_cast<unsigned>(qi - key) < weff ? y : 0.f;
+            y = keep_if(static_cast<unsigned>(qi - key) < weff, y);
             pv[v] = y;
             ssum += y;
         }
@@ -329,7 +338,7 @@ __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 12
         }
         const int k0 = t * kFT;
         const bool active = k0 <= q0 + 31 && !(W > 0 && q0 - (k0 + 31) >= W);
-        if (!active) continue;
+        if (kSkipIdle<D> && !active) continue;
         const f32x16 s = mma_rows<D>(ldsK, l32, hi, qv, f32x16{});  // S^T
         const f32x16 dp = mma_rows<D>(ldsV, l32, hi, dov, ndl);     // dP^T - delta
         float ds[16];
@@ -338,7 +347,7 @@ __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 12
             const int key = k0 + 8 * (v >> 2) + 4 * hi + (v & 3);
             float y, rr;
             weight_rr<EXACT>(s[v], sc, y, rr);
-            ds[v] = static_cast<unsigned>(qi - key) < weff ? dp[v] * y * rr : 0.f;
+            ds[v] = keep_if(static_cast<unsigned>(qi - key) < weff, dp[v] * y * rr);
         }
         mma_cols<D>(ldsKt, l32, hi, ds, acc);  // dQ^T += K^T dS^T
     }
@@ -419,7 +428,7 @@ __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 12
         if (it + 1 < n_it) fetch(it + 1);
         // some query of the tile sees some key of the wave
         const bool active = q0 + 31 >= wk0 && !(W > 0 && q0 - (wk0 + 31) >= W) && q0 < T_;
-        if (!active) continue;
+        if (kSkipIdle<D> && !active) continue;
         const f32x16 s = mma_rows<D>(ldsQ, l32, hi, kv, f32x16{});  // S: rows queries, column key
         f32x16 dp;
 #pragma unroll
@@ -434,8 +443,8 @@ __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 12
             weight_rr<EXACT>(s[v], sc, y, rr);
             const float yi = y * ldr[0][r];
             const bool ok = static_cast<unsigned>(q - kj) < weff && q < T_;
-            pw[v] = ok ? yi : 0.f;
-            ds[v] = ok ? dp[v] * yi * rr : 0.f;
+            pw[v] = keep_if(ok, yi);
+            ds[v] = keep_if(ok, dp[v] * yi * rr);
         }
         mma_cols<D>(ldsOt, l32, hi, pw, dvacc);  // dV^T += dO^T P
         mma_cols<D>(ldsQt, l32, hi, ds, dkacc);  // dK^T += Q^T dS
