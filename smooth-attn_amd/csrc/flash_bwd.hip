@@ -29,6 +29,7 @@
 // Tiles go straight from global memory into LDS (global_load_lds, double
 // buffered, one barrier per tile), as in the forward.
 #include "flash_common.hpp"
+#include "flash_tiles.hpp"
 #include "flash_f32.hpp"
 #include "flash_wide.hpp"
 
@@ -302,7 +303,7 @@ __global__ __launch_bounds__(kBwdThreads, 2) void flash_bwd_dq_kernel(BwdParams 
                 const float g = dp[v] * y * rr;
                 if constexpr (MASK) {
                     const int cv = (v >> 2) * 8 + (v & 3);
-                    ds[v] = static_cast<unsigned>(dbase - cv) < weff ? g : 0.f;
+                    ds[v] = keep_if(static_cast<unsigned>(dbase - cv) < weff, g);
                 } else {
                     ds[v] = g;
                 }
@@ -517,8 +518,8 @@ __global__ __launch_bounds__(kBwdThreads, SA_BWD_DKDV_MINB) void flash_bwd_dkdv_
                 for (int v = 0; v < 16; ++v) {
                     const int cv = (v >> 2) * 8 + (v & 3);
                     const bool ok = (static_cast<unsigned>(dbase + cv) < weff) && (cv < qlim);
-                    pv[v] = ok ? pv[v] : 0.f;
-                    ds[v] = ok ? ds[v] : 0.f;
+                    pv[v] = keep_if(ok, pv[v]);
+                    ds[v] = keep_if(ok, ds[v]);
                 }
             }
 #pragma unroll

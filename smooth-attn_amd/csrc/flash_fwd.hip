@@ -26,6 +26,7 @@
 #include <type_traits>
 
 #include "flash_common.hpp"
+#include "flash_tiles.hpp"
 #include "flash_f32.hpp"
 #include "flash_wide.hpp"
 
@@ -572,7 +573,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashParams p) {
             }
             if constexpr (MASK) {
                 const int cv = (v >> 2) * 8 + (v & 3);
-                w = static_cast<unsigned>(dbase - cv) < weff ? w : 0.f;
+                w = keep_if(static_cast<unsigned>(dbase - cv) < weff, w);
             }
             y[v] = w;
             ssum[qt][v & 3] += w;
