@@ -202,3 +202,18 @@ def test_paged_decode_head_dims():
         assert lib.sa_paged_decode(dummy, dummy, dummy, dummy, dummy, dummy, 0, 8, 2, D, 16, 4, 8,
                                    s4, s4, s4, o, 4, 0.1, _lib.SA_BF16, dummy, 1 << 30, None) == 0
         assert lib.sa_paged_decode_workspace_size(2, 8, D, 4, 16) > 0
+
+
+def test_rope_rotate_argument_errors():
+    # checked before any HIP call: dtype, D a multiple of 16, null pointers,
+    # 16-byte strides and alignment; B = 0 launches nothing
+    lib = _lib.load()
+    d = ctypes.c_void_p(16)
+    s = (ctypes.c_int64 * 4)(4 * 64 * 64, 64 * 64, 64, 1)
+    assert lib.sa_rope_rotate(d, d, d, d, 1, 4, 64, 64, s, 7, None) == -3
+    assert lib.sa_rope_rotate(d, d, d, d, 1, 4, 64, 40, s, _lib.SA_BF16, None) == -2
+    assert lib.sa_rope_rotate(None, d, d, d, 1, 4, 64, 64, s, _lib.SA_BF16, None) == -1
+    odd = (ctypes.c_int64 * 4)(4 * 64 * 68, 64 * 68, 68, 1)  # rows 136 bytes apart (bf16)
+    assert lib.sa_rope_rotate(d, d, d, d, 1, 4, 64, 64, odd, _lib.SA_BF16, None) == -5
+    assert lib.sa_rope_rotate(ctypes.c_void_p(24), d, d, d, 1, 4, 64, 64, s, _lib.SA_BF16, None) == -5
+    assert lib.sa_rope_rotate(d, d, d, d, 0, 4, 64, 64, s, _lib.SA_BF16, None) == 0
