@@ -11,10 +11,10 @@
 // waves x 32 rows, 32-row tiles loaded straight into a ring of LDS stages
 // (the next tile in flight while the current one is used), one barrier per
 // tile.  With one wave per SIMD any overlap of MFMA and VALU work has to
-// come from within the wave: the forward is software-pipelined over tiles
-// (S^T of tile t + 1 issued among the VALU instructions that turn tile t's
-// scores into weights), and every MFMA group's LDS operands are read before
-// its first MFMA.  dK and dV are separate kernels: together they would need
+// come from within the wave: the forward and dQ are software-pipelined over
+// tiles (S^T of tile t + 1 issued among the VALU instructions that turn tile
+// t's scores into weights; three LDS stages), and every MFMA group's LDS
+// operands are read before its first MFMA.  dK and dV are separate kernels: together they would need
 // 256 accumulator registers plus 128 for the K and V operands and spill.
 //
 // Operands (the 32x32x16 layout and the transposing LDS read are described
@@ -175,9 +175,9 @@ __global__ __launch_bounds__(64 * kWW) void flash_fwd_wide_kernel(WideParams<T> 
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool EXACT>
 __global__ __launch_bounds__(64 * kWW) void flash_bwd_dq_wide_kernel(WideParams<T> p) {
-    __shared__ __attribute__((aligned(16))) T ldsK[2][kWT * D];   // ROW layout
-    __shared__ __attribute__((aligned(16))) T ldsKt[2][kWT * D];  // TR layout
-    __shared__ __attribute__((aligned(16))) T ldsV[2][kWT * D];   // ROW layout
+    __shared__ __attribute__((aligned(16))) T ldsK[3][kWT * D];   // ROW layout
+    __shared__ __attribute__((aligned(16))) T ldsKt[3][kWT * D];  // TR layout
+    __shared__ __attribute__((aligned(16))) T ldsV[3][kWT * D];   // ROW layout
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -227,6 +227,10 @@ __global__ __launch_bounds__(64 * kWW) void flash_bwd_dq_wide_kernel(WideParams<
     const int kv_begin = W > 0 ? max(0, qb * kWRows - W + 1) / kWT : 0;
     const float sc = p.scale;
 
+    // Three LDS stages and a software pipeline over key tiles, as in the
+    // forward: S^T of tile t + 1 is issued among the VALU instructions that
+    // turn tile t's scores into weights; then dP^T of tile t, dS, and
+    // dQ^T += K^T dS^T; tile t + 2 loads meanwhile.
     const WideLoader<T, D, false> kld(p.ks[2], wave, lane);
     const WideLoader<T, D, true> ktld(p.ks[2], wave, lane);
     const WideLoader<T, D, false> vld(p.vs[2], wave, lane);
@@ -235,32 +239,60 @@ __global__ __launch_bounds__(64 * kWW) void flash_bwd_dq_wide_kernel(WideParams<
         ktld.issue(kp, t * kWT, T_, ldsKt[buf]);
         vld.issue(vp, t * kWT, T_, ldsV[buf]);
     };
+    using V8 = typename MfmaOps<T>::vec8;
+    const int sw = wswz<false>(l32);
     issue(kv_begin, 0);
+    if (kv_begin + 1 < kv_end) issue(kv_begin + 1, 1);
     wide_wait_vmem();
     __syncthreads();
+    f32x16 s_nx = mma_rows16<T, D>(ldsK[0], l32, hi, qf, f32x16{});  // S^T of the first tile
+    int st = 0;
     for (int t = kv_begin; t < kv_end; ++t) {
-        const int buf = (t - kv_begin) & 1;
-        if (t + 1 < kv_end) issue(t + 1, buf ^ 1);  // released by the barrier ending tile t - 1
+        const int st1 = st == 2 ? 0 : st + 1;
+        const int st2 = st1 == 2 ? 0 : st1 + 1;
+        if (t + 2 < kv_end) issue(t + 2, st2);  // stage st2 held tile t - 1, released by the barrier ending t - 1
         const int k0 = t * kWT;
+        const f32x16 s = s_nx;
+        // S^T of tile t + 1 (the last tile re-reads its own, result unused)
+        // with the weights of tile t: g = y / r
         {
-            const f32x16 s = mma_rows16<T, D>(ldsK[buf], l32, hi, qf, f32x16{});  // S^T
-            const f32x16 dp = mma_rows16<T, D>(ldsV[buf], l32, hi, df, ndl);     // dP^T - delta
-            ColOperands<T, D> kt;
-            kt.read(ldsKt[buf], lane);
-            float ds[16];
+            const T* kr = ldsK[t + 1 < kv_end ? st1 : st] + l32 * D;
+            u32x4 ka[D / 16];
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int key = k0 + 8 * (v >> 2) + 4 * hi + (v & 3);
-                float y, rr;
-                weight_rr16<EXACT>(s[v], sc, y, rr);
-                ds[v] = keep_if(static_cast<unsigned>(qi - key) < weff, dp[v] * y * rr);
-            }
-            u32x4 dsw[2];
-            pack_b<T>(ds, dsw);
-            kt.mma(dsw, acc);  // dQ^T += K^T dS^T
+            for (int i = 0; i < D / 16; ++i) ka[i] = *reinterpret_cast<const u32x4*>(kr + 8 * ((2 * i + hi) ^ sw));
+            __builtin_amdgcn_sched_barrier(0);
+            s_nx = f32x16{};
+#pragma unroll
+            for (int i = 0; i < D / 16; ++i) s_nx = MfmaOps<T>::mma(as_vec8<V8>(ka[i]), as_vec8<V8>(qf[i]), s_nx);
         }
+        float g[16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            float y, rr;
+            weight_rr16<EXACT>(s[v], sc, y, rr);
+            g[v] = y * rr;
+        }
+#pragma unroll
+        for (int i = 0; i < D / 16; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x402, 6, 0);  // then VALU / transcendental
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        const f32x16 dp = mma_rows16<T, D>(ldsV[st], l32, hi, df, ndl);  // dP^T - delta of tile t
+        ColOperands<T, D> kt;
+        kt.read(ldsKt[st], lane);
+        float ds[16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int key = k0 + 8 * (v >> 2) + 4 * hi + (v & 3);
+            ds[v] = keep_if(static_cast<unsigned>(qi - key) < weff, dp[v] * g[v]);
+        }
+        u32x4 dsw[2];
+        pack_b<T>(ds, dsw);
+        kt.mma(dsw, acc);  // dQ^T += K^T dS^T of tile t
         wide_wait_vmem();
-        __syncthreads();  // tile t + 1 landed; every wave is done with stage buf
+        __syncthreads();  // tile t + 2 landed; every wave is done with stage st
+        st = st1;
     }
     // dS carried without its per-row factor 2 scale / R
     if (qi < T_)
