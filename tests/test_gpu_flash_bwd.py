@@ -191,3 +191,24 @@ def test_backward_head_dim_256_public_api():
                                      window_size=70)
     for got, ref in zip((qd.grad, kd.grad, vd.grad), refs):
         assert rel_err(got, ref) <= TOL
+
+
+def test_full_size_head_dim_256_sampled():
+    """head dim 256 at the bench shape [4,16,4096,256] bf16 (the one-wave-per-SIMD
+    kernels over 128 query / key blocks per head): finite outputs and
+    gradients everywhere, oracle parity on one sampled head."""
+    B, H, T, D = 4, 16, 4096, 256
+    gen = torch.Generator(device=DEV).manual_seed(7)
+    q, k, v, do = (torch.randn(B, H, T, D, generator=gen, device=DEV).to(torch.bfloat16) for _ in range(4))
+    scale = 1 / math.sqrt(D)
+    o, rs = kernels._sp2norm_flash_fwd(q, k, v, scale)
+    dq, dk, dv = kernels._sp2norm_flash_bwd(q, k, v, o, do, rs, scale)
+    for t in (o, dq, dk, dv):
+        assert bool(torch.isfinite(t).all())
+    b, h = 3, 11
+    sl = (slice(b, b + 1), slice(h, h + 1))
+    ref, ref_rs = eager.flash_attention_eager(*(t[sl].cpu().double() for t in (q, k, v)), return_row_sums=True)
+    assert rel_err(o[sl], ref) <= 1e-2 and rel_err(rs[sl], ref_rs) <= 1e-5
+    refs = eager.flash_attention_bwd(*(t[sl].cpu().double() for t in (q, k, v, o, do)))
+    for got, want in zip((dq, dk, dv), refs):
+        assert rel_err(got[sl], want) <= TOL
