@@ -132,6 +132,26 @@ def time_kernel(torch, fn, iters=KERNEL_ITERS, warmup=KERNEL_WARMUP, flush=True)
     return {"median": us[n // 2], "mean": sum(us) / n, "p10": us[n // 10], "p90": us[(9 * n) // 10], "n": n}
 
 
+def time_rotating(torch, fns, iters=KERNEL_ITERS, warmup=KERNEL_WARMUP):
+    """Back-to-back launches cycling over ``fns`` (closures over separate
+    input/output copies, so each launch's inputs were last touched
+    len(fns) - 1 launches earlier and, with at least 3 copies larger than
+    the 256 MB Infinity Cache together, come from HBM), ``iters`` of them
+    between one HIP event pair: the average per launch, without the fixed
+    cost of an event pair per launch.  Returns microseconds."""
+    for i in range(warmup):
+        fns[i % len(fns)]()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(st)
+    for i in range(iters):
+        fns[i % len(fns)]()
+    b.record(st)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e3 / iters
+
+
 def bench_norm(torch, sa, steps, warmup):
     """Config 2 at L=4096: the per-kernel protocol on the forward and the
     backward launch, then the timed steps (W untimed, K timed) with HIP
@@ -468,7 +488,7 @@ def bench_norm_sizes(torch, sa):
 
     fam = FamilyConfig()
     dev = torch.device("cuda:0")
-    out = {"causal_bf16": [], "rowwise_fp32": []}
+    out = {"causal_bf16": [], "causal_bf16_rotating": [], "rowwise_fp32": []}
     for L in (1024, 2048):
         gen = torch.Generator(device=dev).manual_seed(20 + L)
         x = (torch.randn(4, 16, L, L, generator=gen, device=dev) / math.sqrt(128)).to(torch.bfloat16)
@@ -480,7 +500,21 @@ def bench_norm_sizes(torch, sa):
         out["causal_bf16"].append({"L": L, "fwd_us": round(fus, 2), "bwd_us": round(bus, 2),
                                    "GBs": round((fb + bb) / ((fus + bus) * 1e-6) / 1e9, 1),
                                    "frac_hbm_peak": round((fb + bb) / ((fus + bus) * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
-        del x, dy, y
+        # The same kernels back to back over 4 copies of x, dy, y and dx
+        # (4 x 512 MiB at L = 1024).
+        copies = [(x, dy, y, torch.empty_like(x))] + [
+            (torch.randn_like(x), torch.randn_like(dy), torch.empty_like(x), torch.empty_like(x)) for _ in range(3)]
+        fr = time_rotating(torch, [lambda c=c: sa.softplus_norm_causal_triton_out(c[2], c[0], family=fam)
+                                   for c in copies])
+        br = time_rotating(torch, [lambda c=c: kernels._norm_bwd_2d(c[0].view(-1, L), c[1].view(-1, L),
+                                                                    c[3].view(-1, L), fam, causal=True)
+                                   for c in copies])
+        out["causal_bf16_rotating"].append({
+            "L": L, "fwd_us": round(fr, 2), "bwd_us": round(br, 2),
+            "GBs": round((fb + bb) / ((fr + br) * 1e-6) / 1e9, 1),
+            "frac_hbm_peak": round((fb + bb) / ((fr + br) * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "protocol": "100 back-to-back launches over 4 input/output copies, one event pair"})
+        del x, dy, y, copies
     for L in (1024, 2048, 4096):
         gen = torch.Generator(device=dev).manual_seed(30 + L)
         x = torch.randn(64 * L, L, generator=gen, device=dev) / math.sqrt(128)
