@@ -40,6 +40,14 @@ __device__ __forceinline__ void wide_dma16(__amdgpu_buffer_rsrc_t rs, int voff, 
 // s_waitcnt vmcnt(0): this wave's direct-to-LDS loads have landed.
 __device__ __forceinline__ void wide_wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// p, computed from wave-uniform values, as a scalar (buffer resources are built from it).
+__device__ __forceinline__ const unsigned char* wide_uniform_ptr(const unsigned char* p) {
+    const uint64_t u = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
+    return reinterpret_cast<const unsigned char*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 // Loads of kWT-row tiles of a [T, D] 16-bit matrix (row stride rstride
 // elements) into LDS in layout TR: each wave issues kWT * D * 2 / 1024 / kWW
 // instructions of 1 KB.  The per-lane byte offsets depend only on the layout

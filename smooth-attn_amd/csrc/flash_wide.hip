@@ -6,25 +6,31 @@
 // (flash_fwd.hip, flash_bwd.hip; reference kernels.py:1536-1631 and
 // :1667-1909): fp32 scores and weights, P and dS rounded to the input type
 // before their products, fp32 accumulation, row sums of the fp32 weights.
-// At D = 256 the O accumulators alone take 128 registers per lane, so these
-// kernels run one wave per SIMD with the accumulators in AGPRs: blocks of 4
-// waves x 32 rows, 32-row tiles loaded straight into a ring of LDS stages
-// (the next tile in flight while the current one is used), one barrier per
-// tile.  With one wave per SIMD any overlap of MFMA and VALU work has to
-// come from within the wave: the forward and dQ are software-pipelined over
-// tiles (S^T of tile t + 1 issued among the VALU instructions that turn tile
-// t's scores into weights; three LDS stages), and every MFMA group's LDS
-// operands are read before its first MFMA.  dK and dV are separate kernels: together they would need
-// 256 accumulator registers plus 128 for the K and V operands and spill.
+// The forward gives each wave 16 query rows on the 16x16x32 MFMA, which
+// halves its accumulators and lets a block of 8 waves run two per SIMD (see
+// the forward's comment).  The backward kernels keep 32 rows per wave on the
+// 32x32x16 MFMA: their accumulators (dQ, or dK / dV) take 128 registers per
+// lane, so they run one wave per SIMD with the accumulators in AGPRs: blocks
+// of 4 waves x 32 rows, 32-row tiles loaded straight into a ring of LDS
+// stages (the next tile in flight while the current one is used), one barrier
+// per tile.  With one wave per SIMD any overlap of MFMA and VALU work has to
+// come from within the wave: dQ is software-pipelined over tiles (S^T of
+// tile t + 1 issued among the VALU instructions that turn tile t's scores
+// into weights; three LDS stages), and every MFMA group's LDS operands are
+// read before its first MFMA.  dK and dV are separate kernels: together they
+// would need 256 accumulator registers plus 128 for the K and V operands and
+// spill.
 //
-// Operands (the 32x32x16 layout and the transposing LDS read are described
-// in flash_common.hpp).  For contractions over D, chunk c of a lane's operand
-// is elements 16c + 8 (l / 32) .. +7 of its row: Q, dO (forward, dQ) or K, V
+// Backward operands (the 32x32x16 layout and the transposing LDS read are
+// described in flash_common.hpp).  For contractions over D, chunk c of a lane's
+// operand is elements 16c + 8 (l / 32) .. +7 of its row: Q, dO (dQ) or K, V
 // (dK, dV) stay in registers, the other side is a 16-byte read of an LDS
 // tile.  For contractions over keys (or queries) the B operand is the lane's
 // own 16 C-layout values v = 8j .. 8j + 7, whose k slots are rows
 // 16j + 8 (i / 4) + 4 (l / 32) + i % 4 of the tile (i = 0..7), so the A
 // operand is a pair of transposing reads (4 rows each).
+#include <type_traits>
+
 #include "flash_tiles.hpp"
 #include "flash_wide.hpp"
 
@@ -65,108 +71,247 @@ struct QBlock {
 };
 
 // ---------------------------------------------------------------------------
-// Forward
+// Forward: 16 query rows per wave on v_mfma_f32_16x16x32_{bf16,f16}
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool EXACT>
-__global__ __launch_bounds__(64 * kWW) void flash_fwd_wide_kernel(WideParams<T> p) {
-    __shared__ __attribute__((aligned(16))) T ldsK[3][kWT * D];  // ROW layout
-    __shared__ __attribute__((aligned(16))) T ldsV[3][kWT * D];  // TR layout
+// With 32 rows per wave the O accumulators of D = 256 fill a wave's share of
+// the register file at one wave per SIMD; 16 rows per wave halve them (O^T
+// is 16 tiles of 16 x 16, 64 registers), so a block of 8 waves runs two per
+// SIMD.  Per 64-key tile a wave runs S^T = K Q^T (4 key subtiles x 8 k
+// steps) and O^T += V^T P^T (16 d tiles x 2 key steps) on the 16x16x32 MFMA:
+// A lane l holds row l % 16, k = 8 (l / 16) .. +7; B column l % 16, the
+// same k; C column l % 16, rows 4 (l / 16) .. +3.  The S^T accumulators of
+// key subtiles 2j and 2j + 1 (keys 4 g + e and 16 + 4 g + e, g = l / 16)
+// are the B operand P^T of key step j as they stand; the matching V^T A
+// operand comes from two transposing reads of the row-major V tile (lane
+// supplies row 4 g + (l % 16) / 4, and that + 16, columns 16 dt + 4 (l % 4):
+// inside its 16-lane group lane i then receives d = 16 dt + i of keys 4 g + j
+// and 16 + 4 g + j).  K and V tiles go straight from global memory into a
+// 2-stage LDS ring (2 x 64 KB); K rows store logical chunk c at c ^ (r & 15)
+// (16-byte row reads, 16 rows per cycle), V rows at c ^ 2 (r & 7)
+// (transposing reads, 8 rows x 32 bytes per cycle): both conflict-free.
+constexpr int kFW = 8;             // waves per block
+constexpr int kFRows = 16 * kFW;   // query rows per block (= kWRows)
+constexpr int kFKT = 64;           // keys per tile
+static_assert(kFRows == kWRows, "forward and backward share the query block size");
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+template <typename T>
+struct Mfma16;
+template <>
+struct Mfma16<bf16> {
+    static __device__ __forceinline__ f32x4 mma(bf16x8 a, bf16x8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+};
+template <>
+struct Mfma16<f16> {
+    static __device__ __forceinline__ f32x4 mma(f16x8 a, f16x8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+};
+
+// FOLD (bf16, moderate positive scales): the S^T chains start at
+// c0 = -1/(2 scale), so they hold s' = s - 1/(2 scale) and
+// (a + sqrt(a^2 + 1))^2 = scale^2 (s' + sqrt(s'^2 + 1/scale^2))^2: the
+// weights carry 1/scale^2 (one FMA per score fewer), cancelled between P V
+// and the row sum.
+template <typename T, int D, bool EXACT, bool FOLD>
+__global__ __launch_bounds__(64 * kFW) void flash_fwd_wide_kernel(WideParams<T> p) {
+    using V8 = typename MfmaOps<T>::vec8;
+    constexpr int ROWB = D * 2;          // bytes per K / V row
+    constexpr int TB = kFKT * ROWB;      // bytes per tile
+    constexpr int CPR = ROWB / 16;       // 16-byte chunks per row
+    constexpr int NI = TB / 1024 / kFW;  // DMA instructions per wave per tensor and tile
+    constexpr int RPI = 64 * kFW / CPR;  // rows one round of kFW instructions covers
+    constexpr int NKS = kFKT / 16;       // 16-key S^T subtiles per tile
+    static_assert(NI == 1 || RPI % 16 == 0, "one swizzled offset per lane");
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[2 * 2 * TB];  // [stage][K, V]
+
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int hi = lane >> 5;
-    const int l32 = lane & 31;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4;
+    const int i16 = lane & 15;
     const int T_ = p.T;
-    const QBlock blk(blockIdx.x, T_, p.B, p.Hq);
-    const int qb = blk.qb, b = blk.b, hq = blk.hq;
-    const int hk = hq / p.G;
-    const T* kp = p.k + b * p.ks[0] + hk * p.ks[1];
-    const T* vp = p.v + b * p.vs[0] + hk * p.vs[1];
+    const int nqb = (T_ + kFRows - 1) / kFRows;
+    int step, unit, sub;
+    grouped_block(blockIdx.x, p.B * p.Hkv, p.G, nqb, 32, step, unit, sub);  // heaviest query blocks first
+    const int qb = nqb - 1 - step;
+    const int b = unit / p.Hkv;
+    const int hk = unit - b * p.Hkv;
+    const int hq = hk * p.G + sub;
 
-    const int q0 = qb * kWRows + 32 * wave;
-    const int qi = q0 + l32;
+    const unsigned char* kp = wide_uniform_ptr(reinterpret_cast<const unsigned char*>(p.k + b * p.ks[0] + hk * p.ks[1]));
+    const unsigned char* vp = wide_uniform_ptr(reinterpret_cast<const unsigned char*>(p.v + b * p.vs[0] + hk * p.vs[1]));
+    const int64_t krs = p.ks[2] * 2, vrs = p.vs[2] * 2;
+
+    // waves w and w + 4 share a SIMD: the second four take the row slots in
+    // reverse, so each SIMD pairs an early-row wave with a late-row one
+    const int q_start = qb * kFRows;
+    const int slot = wave >= 4 ? 11 - wave : wave;
+    const int q0w = q_start + 16 * slot;
+    const int qi = q0w + i16;
     const int qrow = min(qi, T_ - 1);
-    u32x4 qf[D / 16];
-    load_frags<D>(p.q + b * p.qs[0] + hq * p.qs[1] + qrow * p.qs[2], hi, qf);
-
-    f32x16 oacc[D / 32];
+    // Q^T as the B operand of S^T: k step ks holds d = 32 ks + 8 g .. +7 of query qi
+    u32x4 qf[D / 32];
+    {
+        const T* qr = p.q + b * p.qs[0] + hq * p.qs[1] + qrow * p.qs[2];
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) oacc[dt] = f32x16{};
-    float ssum = 0.f;
+        for (int ks = 0; ks < D / 32; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qr + 32 * ks + 8 * g);
+    }
+
     const int W = p.window;
     const unsigned weff = W > 0 ? static_cast<unsigned>(W) : 0x7FFFFFFFu;
-    const int n_kv = (T_ + kWT - 1) / kWT;
-    const int kv_end = min((qb * kWRows + kWRows + kWT - 1) / kWT, n_kv);
-    const int kv_begin = W > 0 ? max(0, qb * kWRows - W + 1) / kWT : 0;
+    const int n_kv = (T_ + kFKT - 1) / kFKT;
+    const int kv_end = min((q_start + kFRows + kFKT - 1) / kFKT, n_kv);
+    const int kv_begin = W > 0 ? max(0, q_start - W + 1) / kFKT : 0;
     const float sc = p.scale;
 
-    // Three LDS stages and a software pipeline over tiles: while the S^T
-    // MFMAs of tile t + 1 run, the VALU turns tile t's scores into weights
-    // (the MFMAs and the VALU instructions interleaved in the wave's stream),
-    // then P V of tile t; tile t + 2 loads meanwhile.  One wave per SIMD, so
-    // this overlap has to come from within the wave.
-    const WideLoader<T, D, false> kld(p.ks[2], wave, lane);
-    const WideLoader<T, D, true> vld(p.vs[2], wave, lane);
-    kld.issue(kp, kv_begin * kWT, T_, ldsK[0]);
-    vld.issue(vp, kv_begin * kWT, T_, ldsV[0]);
-    if (kv_begin + 1 < kv_end) {
-        kld.issue(kp, (kv_begin + 1) * kWT, T_, ldsK[1]);
-        vld.issue(vp, (kv_begin + 1) * kWT, T_, ldsV[1]);
-    }
+    // DMA: slot s = (kFW i + wave) * 64 + lane of a tile holds row s / CPR,
+    // physical chunk s % CPR; rows past T read as zeros (they meet only masked
+    // weights).
+    const int drow = (wave * 64 + lane) / CPR;
+    const int pch = (wave * 64 + lane) % CPR;
+    const int koff = drow * static_cast<int>(krs) + ((pch ^ (drow & 15)) << 4);
+    const int voff = drow * static_cast<int>(vrs) + ((pch ^ (2 * (drow & 7))) << 4);
+    auto issue = [&](int t) {
+        const int k0 = t * kFKT;
+        const int nrows = min(T_ - k0, kFKT);
+        unsigned char* lk = lds + ((t - kv_begin) & 1) * 2 * TB;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int skip = i * RPI;
+            wide_dma16(__builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(kp + (k0 + skip) * krs), 0,
+                                                         max((nrows - skip) * static_cast<int>(krs), 0), 0x00020000),
+                       koff, lk + (i * kFW + wave) * 1024);
+            wide_dma16(__builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(vp + (k0 + skip) * vrs), 0,
+                                                         max((nrows - skip) * static_cast<int>(vrs), 0), 0x00020000),
+                       voff, lk + TB + (i * kFW + wave) * 1024);
+        }
+    };
+
+    const int vr = 4 * g + (i16 >> 2);
+    const int vbase = vr * ROWB + (((lane & 3) >> 1) << 4) + 8 * (lane & 1);
+    const int vsw = vr & 7;
+    f32x4 oacc[D / 16];
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) oacc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float ssum0 = 0.f, ssum1 = 0.f;
+    const float c0 = -0.5f / sc, c2 = 1.f / (sc * sc);
+
+    auto tile = [&](auto mask_tag, int t) {
+        constexpr bool MASK = decltype(mask_tag)::value;
+        const int k0 = t * kFKT;
+        const unsigned char* Kb = lds + ((t - kv_begin) & 1) * 2 * TB;
+        const unsigned char* Vb = Kb + TB;
+        f32x4 s[NKS];
+#pragma unroll
+        for (int kst = 0; kst < NKS; ++kst) {
+            u32x4 ka[D / 32];
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks)
+                ka[ks] = *reinterpret_cast<const u32x4*>(Kb + (16 * kst + i16) * ROWB + (((4 * ks + g) ^ i16) << 4));
+            s[kst] = FOLD ? f32x4{c0, c0, c0, c0} : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks) s[kst] = Mfma16<T>::mma(as_vec8<V8>(ka[ks]), as_vec8<V8>(qf[ks]), s[kst]);
+        }
+        // lane: query qi, keys k0 + 16 kst + 4 g + e
+        const int dbase = qi - k0 - 4 * g;
+        float y[4 * NKS];
+#pragma unroll
+        for (int kst = 0; kst < NKS; ++kst) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float w;
+                if constexpr (FOLD) {
+                    const float wf = s[kst][e] + fast_sqrt(__builtin_fmaf(s[kst][e], s[kst][e], c2));
+                    w = wf * wf;
+                } else {
+                    w = sp2_weight<EXACT>(__builtin_fmaf(s[kst][e], sc, -0.5f));
+                }
+                if constexpr (MASK) w = keep_if(static_cast<unsigned>(dbase - 16 * kst - e) < weff, w);
+                y[4 * kst + e] = w;
+                if (e & 1) ssum1 += w;
+                else ssum0 += w;
+            }
+        }
+#pragma unroll
+        for (int kk = 0; kk < kFKT / 32; ++kk) {
+            const float* yk = y + 8 * kk;
+            const u32x4 pw{pack2<T>(yk[0], yk[1]), pack2<T>(yk[2], yk[3]), pack2<T>(yk[4], yk[5]),
+                           pack2<T>(yk[6], yk[7])};
+            const V8 bop = as_vec8<V8>(pw);
+#pragma unroll
+            for (int dt = 0; dt < D / 16; ++dt) {
+                const unsigned char* p0 = Vb + 32 * kk * ROWB + vbase + ((dt ^ vsw) << 5);
+                oacc[dt] = Mfma16<T>::mma(lds_read_tr16_pair<V8>(p0, p0 + 16 * ROWB), bop, oacc[dt]);
+            }
+        }
+    };
+
+    // Iteration t requests tile t + 1 into the stage of tile t - 1 (free since
+    // the barrier that ended t - 1), runs tile t, then waits for t + 1 and
+    // publishes it.  Waves run only the tiles their rows see (masks only where
+    // some pair is outside the causal window or past a window edge) but take
+    // every barrier.
+    issue(kv_begin);
     wide_wait_vmem();
     __syncthreads();
-    f32x16 s_next = mma_rows16<T, D>(ldsK[0], l32, hi, qf, f32x16{});  // S^T of the first tile
-    int st = 0;
-    for (int t = kv_begin; t < kv_end; ++t) {
-        const int st1 = st == 2 ? 0 : st + 1;
-        const int st2 = st1 == 2 ? 0 : st1 + 1;
-        if (t + 2 < kv_end) {  // stage st2 held tile t - 1, released by the barrier ending tile t - 1
-            kld.issue(kp, (t + 2) * kWT, T_, ldsK[st2]);
-            vld.issue(vp, (t + 2) * kWT, T_, ldsV[st2]);
+    auto begin_t = [&](int t) {
+        if (t + 1 < kv_end) issue(t + 1);
+    };
+    auto end_t = [&](int t) {
+        if (t + 1 < kv_end) {
+            wide_wait_vmem();
+            __syncthreads();
         }
-        const int k0 = t * kWT;
-        const f32x16 s = s_next;
-        // operands: K of tile t + 1 (the last tile re-reads its own, result unused), V of tile t
-        const T* kn = ldsK[t + 1 < kv_end ? st1 : st] + l32 * D;
-        const int sw = wswz<false>(l32);
-        u32x4 ka[D / 16];
-#pragma unroll
-        for (int i = 0; i < D / 16; ++i) ka[i] = *reinterpret_cast<const u32x4*>(kn + 8 * ((2 * i + hi) ^ sw));
-        ColOperands<T, D> vt;
-        vt.read(ldsV[st], lane);
-        // S^T of tile t + 1 ...
-        using V8 = typename MfmaOps<T>::vec8;
-        s_next = f32x16{};
-#pragma unroll
-        for (int i = 0; i < D / 16; ++i) s_next = MfmaOps<T>::mma(as_vec8<V8>(ka[i]), as_vec8<V8>(qf[i]), s_next);
-        // ... interleaved with the weights of tile t
-        float y[16];
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int key = k0 + 8 * (v >> 2) + 4 * hi + (v & 3);
-            float w, rr;
-            weight_rr16<EXACT>(s[v], sc, w, rr);
-            y[v] = keep_if(static_cast<unsigned>(qi - key) < weff, w);
-            ssum += y[v];
-        }
-        u32x4 pw[2];
-        pack_b<T>(y, pw);
-#pragma unroll
-        for (int i = 0; i < D / 16; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
-            __builtin_amdgcn_sched_group_barrier(0x402, 10, 0);  // then VALU / transcendental
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        vt.mma(pw, oacc);  // O^T += V^T P^T of tile t
-        wide_wait_vmem();
-        __syncthreads();  // tile t + 2 landed; every wave is done with stage st
-        st = st1;
+    };
+    const int wf = q0w, wl = q0w + 15;  // the wave's query rows
+    int t_first = kv_begin;
+    if (W > 0 && wf - W + 1 > 0) t_first = max(t_first, (wf - W + 1) / kFKT);
+    const int t_last = wf < T_ ? min(wl / kFKT, kv_end - 1) : t_first - 1;
+    int ja = t_first;
+    if (W > 0 && wl - W >= 0) ja = max(ja, (wl - W) / kFKT + 1);
+    const int jb = (wf + 1) / kFKT;
+    int t = kv_begin;
+    for (; t < t_first; ++t) {
+        begin_t(t);
+        end_t(t);
+    }
+    for (; t <= t_last && t < ja; ++t) {
+        begin_t(t);
+        tile(std::true_type{}, t);
+        end_t(t);
+    }
+    for (; t <= t_last && t < jb; ++t) {
+        begin_t(t);
+        tile(std::false_type{}, t);
+        end_t(t);
+    }
+    for (; t <= t_last; ++t) {
+        begin_t(t);
+        tile(std::true_type{}, t);
+        end_t(t);
+    }
+    for (; t < kv_end; ++t) {
+        begin_t(t);
+        end_t(t);
     }
 
-    const float tot = ssum + __shfl_xor(ssum, 32) + kEps;
+    // row sums: lanes i16, i16 + 16, + 32, + 48 hold the four key groups of query qi
+    float part = ssum0 + ssum1;
+    part += __shfl_xor(part, 16);
+    part += __shfl_xor(part, 32);
+    const float tot = FOLD ? __builtin_fmaf(part, sc * sc, kEps) : part + kEps;
+    const float inv = FOLD ? (sc * sc) / tot : 1.f / tot;
     if (qi < T_) {
-        store_cols16<T, D>(p.out + b * p.os[0] + hq * p.os[1] + qi * p.os[2], hi, oacc, 1.f / tot);
-        if (hi == 0 && p.row_sums != nullptr) p.row_sums[(static_cast<int64_t>(b) * p.Hq + hq) * T_ + qi] = tot;
+        T* orow = p.out + b * p.os[0] + hq * p.os[1] + qi * p.os[2];
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt) {
+            const uint2 w{pack2<T>(oacc[dt][0] * inv, oacc[dt][1] * inv), pack2<T>(oacc[dt][2] * inv, oacc[dt][3] * inv)};
+            *reinterpret_cast<uint2*>(orow + 16 * dt + 4 * g) = w;
+        }
+        if (g == 0 && p.row_sums != nullptr) p.row_sums[(static_cast<int64_t>(b) * p.Hq + hq) * T_ + qi] = tot;
     }
 }
 
@@ -452,13 +597,21 @@ int check_wide(int B, int Hq, int Hkv, int T, int D, int window_size, int dtype)
 
 template <typename T>
 int launch_fwd_wide(const WideParams<T>& prm, int exact, hipStream_t st) {
-    const int64_t nblk = static_cast<int64_t>((prm.T + kWRows - 1) / kWRows) * prm.B * prm.Hq;
-    if (nblk * 64 * kWW >= (int64_t(1) << 32)) return SA_ERR_BAD_SHAPE;
+    const int64_t nblk = static_cast<int64_t>((prm.T + kFRows - 1) / kFRows) * prm.B * prm.Hq;
+    if (nblk * 64 * kFW >= (int64_t(1) << 32)) return SA_ERR_BAD_SHAPE;
     const dim3 grid(static_cast<unsigned>(nblk));
-    if (exact)
-        flash_fwd_wide_kernel<T, 256, true><<<grid, 64 * kWW, 0, st>>>(prm);
-    else
-        flash_fwd_wide_kernel<T, 256, false><<<grid, 64 * kWW, 0, st>>>(prm);
+    if (exact) {
+        flash_fwd_wide_kernel<T, 256, true, false><<<grid, 64 * kFW, 0, st>>>(prm);
+        return status_from_launch();
+    }
+    // folded weights for bf16 P only (fp16 P would overflow sooner by 1/scale^2)
+    if constexpr (std::is_same_v<T, bf16>) {
+        if (prm.scale >= 0x1p-20f && prm.scale <= 0x1p20f) {
+            flash_fwd_wide_kernel<T, 256, false, true><<<grid, 64 * kFW, 0, st>>>(prm);
+            return status_from_launch();
+        }
+    }
+    flash_fwd_wide_kernel<T, 256, false, false><<<grid, 64 * kFW, 0, st>>>(prm);
     return status_from_launch();
 }
 
@@ -546,6 +699,9 @@ int flash_fwd_wide(const void* q, const void* k, const void* v, void* o, float* 
     if (!q || !k || !v || !o || !q_strides || !k_strides || !v_strides || !o_strides) return SA_ERR_NULL_POINTER;
     if (!wide_strides_ok(q_strides) || !wide_strides_ok(k_strides) || !wide_strides_ok(v_strides) ||
         !wide_strides_ok(o_strides) || !aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
+        return SA_ERR_BAD_STRIDE;
+    // the forward's K / V tiles are kFKT rows: byte offsets within one stay 32-bit
+    if (k_strides[2] * 2 * kFKT >= (int64_t(1) << 31) || v_strides[2] * 2 * kFKT >= (int64_t(1) << 31))
         return SA_ERR_BAD_STRIDE;
     if (B == 0 || T == 0) return 0;
     if (dtype == SA_BF16)
