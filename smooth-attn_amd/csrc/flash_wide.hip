@@ -6,25 +6,21 @@
 // (flash_fwd.hip, flash_bwd.hip; reference kernels.py:1536-1631 and
 // :1667-1909): fp32 scores and weights, P and dS rounded to the input type
 // before their products, fp32 accumulation, row sums of the fp32 weights.
-// The forward gives each wave 16 query rows on the 16x16x32 MFMA, which
-// halves its accumulators and lets a block of 8 waves run two per SIMD (see
-// the forward's comment).  The backward kernels keep 32 rows per wave on the
-// 32x32x16 MFMA: their accumulators (dQ, or dK / dV) take 128 registers per
+// The forward and dQ give each wave 16 query rows on the 16x16x32 MFMA,
+// which halves their accumulators and lets a block of 8 waves run two per
+// SIMD (see the forward's comment).  The dK and dV kernels keep 32 key rows
+// per wave on the 32x32x16 MFMA: their accumulators take 128 registers per
 // lane, so they run one wave per SIMD with the accumulators in AGPRs: blocks
 // of 4 waves x 32 rows, 32-row tiles loaded straight into a ring of LDS
 // stages (the next tile in flight while the current one is used), one barrier
-// per tile.  With one wave per SIMD any overlap of MFMA and VALU work has to
-// come from within the wave: dQ is software-pipelined over tiles (S^T of
-// tile t + 1 issued among the VALU instructions that turn tile t's scores
-// into weights; three LDS stages), and every MFMA group's LDS operands are
-// read before its first MFMA.  dK and dV are separate kernels: together they
-// would need 256 accumulator registers plus 128 for the K and V operands and
-// spill.
+// per tile, every MFMA group's LDS operands read before its first MFMA.  dK
+// and dV are separate kernels: together they would need 256 accumulator
+// registers plus 128 for the K and V operands and spill.
 //
-// Backward operands (the 32x32x16 layout and the transposing LDS read are
+// dK / dV operands (the 32x32x16 layout and the transposing LDS read are
 // described in flash_common.hpp).  For contractions over D, chunk c of a lane's
-// operand is elements 16c + 8 (l / 32) .. +7 of its row: Q, dO (dQ) or K, V
-// (dK, dV) stay in registers, the other side is a 16-byte read of an LDS
+// operand is elements 16c + 8 (l / 32) .. +7 of its row: K, V stay in
+// registers, the other side is a 16-byte read of an LDS
 // tile.  For contractions over keys (or queries) the B operand is the lane's
 // own 16 C-layout values v = 8j .. 8j + 7, whose k slots are rows
 // 16j + 8 (i / 4) + 4 (l / 32) + i % 4 of the tile (i = 0..7), so the A
@@ -56,19 +52,6 @@ struct WideParams {
     float scale;
 };
 
-// Query blocks of kWRows rows, heaviest (latest) first, over (b, hq).
-struct QBlock {
-    int qb, b, hq;
-    __device__ __forceinline__ QBlock(int id, int T_, int B, int Hq) {
-        const int nqb = (T_ + kWRows - 1) / kWRows;
-        const int per = B * Hq;
-        const int step = id / per;
-        const int rest = id - step * per;
-        qb = nqb - 1 - step;
-        b = rest / Hq;
-        hq = rest - b * Hq;
-    }
-};
 
 // ---------------------------------------------------------------------------
 // Forward: 16 query rows per wave on v_mfma_f32_16x16x32_{bf16,f16}
@@ -316,132 +299,216 @@ __global__ __launch_bounds__(64 * kFW) void flash_fwd_wide_kernel(WideParams<T> 
 }
 
 // ---------------------------------------------------------------------------
-// Backward: dQ (and delta)
+// Backward: dQ (and delta), 16 query rows per wave on the 16x16x32 MFMA
 // ---------------------------------------------------------------------------
+// As the forward: 8 waves x 16 rows, two waves per SIMD, 64-key tiles in a
+// 2-stage LDS ring.  Per tile: S^T = K Q^T and dP^T = V dO^T (dP^T chains
+// start at -delta of the lane's query), dS on the VALU, then
+// dQ^T += K^T dS^T with K^T from transposing reads of the K tile.  The K tile
+// is read both ways, so it stores logical chunk c of row r at c ^ fk(r),
+// fk(r) = 2 (r & 7) | ((r >> 3) & 1): injective on 16 consecutive rows (row
+// reads) and, on bits 1-3, on 8 consecutive rows while keeping 32-byte units
+// together (transposing reads); V rows use c ^ (r & 15).
+__device__ __forceinline__ int fk_swz(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
+
 template <typename T, int D, bool EXACT>
-__global__ __launch_bounds__(64 * kWW) void flash_bwd_dq_wide_kernel(WideParams<T> p) {
-    __shared__ __attribute__((aligned(16))) T ldsK[3][kWT * D];   // ROW layout
-    __shared__ __attribute__((aligned(16))) T ldsKt[3][kWT * D];  // TR layout
-    __shared__ __attribute__((aligned(16))) T ldsV[3][kWT * D];   // ROW layout
+__global__ __launch_bounds__(64 * kFW) void flash_bwd_dq_wide_kernel(WideParams<T> p) {
+    using V8 = typename MfmaOps<T>::vec8;
+    constexpr int ROWB = D * 2;
+    constexpr int TB = kFKT * ROWB;
+    constexpr int CPR = ROWB / 16;
+    constexpr int NI = TB / 1024 / kFW;
+    constexpr int RPI = 64 * kFW / CPR;
+    constexpr int NKS = kFKT / 16;
+    static_assert(NI == 1 || RPI % 16 == 0, "one swizzled offset per lane");
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[2 * 2 * TB];  // [stage][K, V]
+
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int hi = lane >> 5;
-    const int l32 = lane & 31;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4;
+    const int i16 = lane & 15;
     const int T_ = p.T;
-    const QBlock blk(blockIdx.x, T_, p.B, p.Hq);
-    const int qb = blk.qb, b = blk.b, hq = blk.hq;
-    const int hk = hq / p.G;
-    const T* kp = p.k + b * p.ks[0] + hk * p.ks[1];
-    const T* vp = p.v + b * p.vs[0] + hk * p.vs[1];
+    const int nqb = (T_ + kFRows - 1) / kFRows;
+    int step, unit, sub;
+    grouped_block(blockIdx.x, p.B * p.Hkv, p.G, nqb, 32, step, unit, sub);
+    const int qb = nqb - 1 - step;
+    const int b = unit / p.Hkv;
+    const int hk = unit - b * p.Hkv;
+    const int hq = hk * p.G + sub;
+    const unsigned char* kp = wide_uniform_ptr(reinterpret_cast<const unsigned char*>(p.k + b * p.ks[0] + hk * p.ks[1]));
+    const unsigned char* vp = wide_uniform_ptr(reinterpret_cast<const unsigned char*>(p.v + b * p.vs[0] + hk * p.vs[1]));
+    const int64_t krs = p.ks[2] * 2, vrs = p.vs[2] * 2;
 
-    const int q0 = qb * kWRows + 32 * wave;
-    const int qi = q0 + l32;
+    const int q_start = qb * kFRows;
+    const int slot = wave >= 4 ? 11 - wave : wave;
+    const int q0w = q_start + 16 * slot;
+    const int qi = q0w + i16;
     const int qrow = min(qi, T_ - 1);
-    u32x4 qf[D / 16], df[D / 16];
-    load_frags<D>(p.q + b * p.qs[0] + hq * p.qs[1] + qrow * p.qs[2], hi, qf);
-    load_frags<D>(p.dout + b * p.dos[0] + hq * p.dos[1] + qrow * p.dos[2], hi, df);
-    // delta = rowsum(dO * O) of this lane's query (lanes l and l ^ 32 hold the halves)
+    // Q^T and dO^T as B operands: k step ks holds d = 32 ks + 8 g .. +7 of query qi;
+    // delta = dO . O of that query (lanes i16 + 16 g share it)
+    u32x4 qf[D / 32], df[D / 32];
     float dpart = 0.f;
     {
-        const T* orow = p.o + b * p.os[0] + hq * p.os[1] + qrow * p.os[2];
+        const T* qr = p.q + b * p.qs[0] + hq * p.qs[1] + qrow * p.qs[2];
+        const T* dr = p.dout + b * p.dos[0] + hq * p.dos[1] + qrow * p.dos[2];
+        const T* orw = p.o + b * p.os[0] + hq * p.os[1] + qrow * p.os[2];
 #pragma unroll
-        for (int c = 0; c < D / 16; ++c) {
-            const u32x4 ov = *reinterpret_cast<const u32x4*>(orow + 16 * c + 8 * hi);
+        for (int ks = 0; ks < D / 32; ++ks) {
+            qf[ks] = *reinterpret_cast<const u32x4*>(qr + 32 * ks + 8 * g);
+            df[ks] = *reinterpret_cast<const u32x4*>(dr + 32 * ks + 8 * g);
+            const u32x4 ov = *reinterpret_cast<const u32x4*>(orw + 32 * ks + 8 * g);
             const uint32_t ow[4] = {ov[0], ov[1], ov[2], ov[3]};
-            const uint32_t dw[4] = {df[c][0], df[c][1], df[c][2], df[c][3]};
+            const uint32_t dw[4] = {df[ks][0], df[ks][1], df[ks][2], df[ks][3]};
 #pragma unroll
             for (int e = 0; e < 8; ++e) dpart = __builtin_fmaf(elem<T>(dw, e), elem<T>(ow, e), dpart);
         }
     }
+    dpart += __shfl_xor(dpart, 16);
     const float dl = dpart + __shfl_xor(dpart, 32);
     const int64_t rbase = (static_cast<int64_t>(b) * p.Hq + hq) * T_;
-    if (qi < T_ && hi == 0) p.delta[rbase + qi] = dl;
+    if (qi < T_ && g == 0) p.delta[rbase + qi] = dl;
     const float inv_r = 1.f / p.rs[rbase + qrow];
 
-    f32x16 acc[D / 32];
-#pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) acc[dt] = f32x16{};
-    f32x16 ndl;
-#pragma unroll
-    for (int v = 0; v < 16; ++v) ndl[v] = -dl;
     const int W = p.window;
     const unsigned weff = W > 0 ? static_cast<unsigned>(W) : 0x7FFFFFFFu;
-    const int n_kv = (T_ + kWT - 1) / kWT;
-    const int kv_end = min((qb * kWRows + kWRows + kWT - 1) / kWT, n_kv);
-    const int kv_begin = W > 0 ? max(0, qb * kWRows - W + 1) / kWT : 0;
+    const int n_kv = (T_ + kFKT - 1) / kFKT;
+    const int kv_end = min((q_start + kFRows + kFKT - 1) / kFKT, n_kv);
+    const int kv_begin = W > 0 ? max(0, q_start - W + 1) / kFKT : 0;
     const float sc = p.scale;
 
-    // Three LDS stages and a software pipeline over key tiles, as in the
-    // forward: S^T of tile t + 1 is issued among the VALU instructions that
-    // turn tile t's scores into weights; then dP^T of tile t, dS, and
-    // dQ^T += K^T dS^T; tile t + 2 loads meanwhile.
-    const WideLoader<T, D, false> kld(p.ks[2], wave, lane);
-    const WideLoader<T, D, true> ktld(p.ks[2], wave, lane);
-    const WideLoader<T, D, false> vld(p.vs[2], wave, lane);
-    auto issue = [&](int t, int buf) {
-        kld.issue(kp, t * kWT, T_, ldsK[buf]);
-        ktld.issue(kp, t * kWT, T_, ldsKt[buf]);
-        vld.issue(vp, t * kWT, T_, ldsV[buf]);
+    const int drow = (wave * 64 + lane) / CPR;
+    const int pch = (wave * 64 + lane) % CPR;
+    const int koff = drow * static_cast<int>(krs) + ((pch ^ fk_swz(drow)) << 4);
+    const int voff = drow * static_cast<int>(vrs) + ((pch ^ (drow & 15)) << 4);
+    auto issue = [&](int t) {
+        const int k0 = t * kFKT;
+        const int nrows = min(T_ - k0, kFKT);
+        unsigned char* lk = lds + ((t - kv_begin) & 1) * 2 * TB;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int skip = i * RPI;
+            wide_dma16(__builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(kp + (k0 + skip) * krs), 0,
+                                                         max((nrows - skip) * static_cast<int>(krs), 0), 0x00020000),
+                       koff, lk + (i * kFW + wave) * 1024);
+            wide_dma16(__builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(vp + (k0 + skip) * vrs), 0,
+                                                         max((nrows - skip) * static_cast<int>(vrs), 0), 0x00020000),
+                       voff, lk + TB + (i * kFW + wave) * 1024);
+        }
     };
-    using V8 = typename MfmaOps<T>::vec8;
-    const int sw = wswz<false>(l32);
-    issue(kv_begin, 0);
-    if (kv_begin + 1 < kv_end) issue(kv_begin + 1, 1);
+
+    // K^T operand (16 d x 32 keys) by two transposing reads, as V^T in the forward
+    const int vr = 4 * g + (i16 >> 2);
+    const int fv = fk_swz(vr);
+    const int ktbase = vr * ROWB + (((((lane & 3) >> 1) ^ (fv & 1))) << 4) + 8 * (lane & 1);
+    const int ktsw = fv >> 1;
+    const int fki = fk_swz(i16);
+    f32x4 acc[D / 16];
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const f32x4 ndl{-dl, -dl, -dl, -dl};
+
+    auto tile = [&](auto mask_tag, int t) {
+        constexpr bool MASK = decltype(mask_tag)::value;
+        const int k0 = t * kFKT;
+        const unsigned char* Kb = lds + ((t - kv_begin) & 1) * 2 * TB;
+        const unsigned char* Vb = Kb + TB;
+        f32x4 s[NKS], dp[NKS];
+#pragma unroll
+        for (int kst = 0; kst < NKS; ++kst) {
+            u32x4 op[D / 32];
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks)
+                op[ks] = *reinterpret_cast<const u32x4*>(Kb + (16 * kst + i16) * ROWB + (((4 * ks + g) ^ fki) << 4));
+            s[kst] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks) s[kst] = Mfma16<T>::mma(as_vec8<V8>(op[ks]), as_vec8<V8>(qf[ks]), s[kst]);
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks)
+                op[ks] = *reinterpret_cast<const u32x4*>(Vb + (16 * kst + i16) * ROWB + (((4 * ks + g) ^ i16) << 4));
+            dp[kst] = ndl;
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks) dp[kst] = Mfma16<T>::mma(as_vec8<V8>(op[ks]), as_vec8<V8>(df[ks]), dp[kst]);
+        }
+        const int dbase = qi - k0 - 4 * g;
+        float ds[4 * NKS];
+#pragma unroll
+        for (int kst = 0; kst < NKS; ++kst) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float y, rr;
+                weight_rr16<EXACT>(s[kst][e], sc, y, rr);
+                const float x = dp[kst][e] * y * rr;
+                ds[4 * kst + e] = MASK ? keep_if(static_cast<unsigned>(dbase - 16 * kst - e) < weff, x) : x;
+            }
+        }
+#pragma unroll
+        for (int kk = 0; kk < kFKT / 32; ++kk) {
+            const float* xk = ds + 8 * kk;
+            const u32x4 pw{pack2<T>(xk[0], xk[1]), pack2<T>(xk[2], xk[3]), pack2<T>(xk[4], xk[5]),
+                           pack2<T>(xk[6], xk[7])};
+            const V8 bop = as_vec8<V8>(pw);
+#pragma unroll
+            for (int dt = 0; dt < D / 16; ++dt) {
+                const unsigned char* p0 = Kb + 32 * kk * ROWB + ktbase + ((dt ^ ktsw) << 5);
+                acc[dt] = Mfma16<T>::mma(lds_read_tr16_pair<V8>(p0, p0 + 16 * ROWB), bop, acc[dt]);
+            }
+        }
+    };
+
+    issue(kv_begin);
     wide_wait_vmem();
     __syncthreads();
-    f32x16 s_nx = mma_rows16<T, D>(ldsK[0], l32, hi, qf, f32x16{});  // S^T of the first tile
-    int st = 0;
-    for (int t = kv_begin; t < kv_end; ++t) {
-        const int st1 = st == 2 ? 0 : st + 1;
-        const int st2 = st1 == 2 ? 0 : st1 + 1;
-        if (t + 2 < kv_end) issue(t + 2, st2);  // stage st2 held tile t - 1, released by the barrier ending t - 1
-        const int k0 = t * kWT;
-        const f32x16 s = s_nx;
-        // S^T of tile t + 1 (the last tile re-reads its own, result unused)
-        // with the weights of tile t: g = y / r
-        {
-            const T* kr = ldsK[t + 1 < kv_end ? st1 : st] + l32 * D;
-            u32x4 ka[D / 16];
-#pragma unroll
-            for (int i = 0; i < D / 16; ++i) ka[i] = *reinterpret_cast<const u32x4*>(kr + 8 * ((2 * i + hi) ^ sw));
-            __builtin_amdgcn_sched_barrier(0);
-            s_nx = f32x16{};
-#pragma unroll
-            for (int i = 0; i < D / 16; ++i) s_nx = MfmaOps<T>::mma(as_vec8<V8>(ka[i]), as_vec8<V8>(qf[i]), s_nx);
+    auto begin_t = [&](int t) {
+        if (t + 1 < kv_end) issue(t + 1);
+    };
+    auto end_t = [&](int t) {
+        if (t + 1 < kv_end) {
+            wide_wait_vmem();
+            __syncthreads();
         }
-        float g[16];
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            float y, rr;
-            weight_rr16<EXACT>(s[v], sc, y, rr);
-            g[v] = y * rr;
-        }
-#pragma unroll
-        for (int i = 0; i < D / 16; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-            __builtin_amdgcn_sched_group_barrier(0x402, 6, 0);  // then VALU / transcendental
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        const f32x16 dp = mma_rows16<T, D>(ldsV[st], l32, hi, df, ndl);  // dP^T - delta of tile t
-        ColOperands<T, D> kt;
-        kt.read(ldsKt[st], lane);
-        float ds[16];
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int key = k0 + 8 * (v >> 2) + 4 * hi + (v & 3);
-            ds[v] = keep_if(static_cast<unsigned>(qi - key) < weff, dp[v] * g[v]);
-        }
-        u32x4 dsw[2];
-        pack_b<T>(ds, dsw);
-        kt.mma(dsw, acc);  // dQ^T += K^T dS^T of tile t
-        wide_wait_vmem();
-        __syncthreads();  // tile t + 2 landed; every wave is done with stage st
-        st = st1;
+    };
+    const int wf = q0w, wl = q0w + 15;
+    int t_first = kv_begin;
+    if (W > 0 && wf - W + 1 > 0) t_first = max(t_first, (wf - W + 1) / kFKT);
+    const int t_last = wf < T_ ? min(wl / kFKT, kv_end - 1) : t_first - 1;
+    int ja = t_first;
+    if (W > 0 && wl - W >= 0) ja = max(ja, (wl - W) / kFKT + 1);
+    const int jb = (wf + 1) / kFKT;
+    int t = kv_begin;
+    for (; t < t_first; ++t) {
+        begin_t(t);
+        end_t(t);
+    }
+    for (; t <= t_last && t < ja; ++t) {
+        begin_t(t);
+        tile(std::true_type{}, t);
+        end_t(t);
+    }
+    for (; t <= t_last && t < jb; ++t) {
+        begin_t(t);
+        tile(std::false_type{}, t);
+        end_t(t);
+    }
+    for (; t <= t_last; ++t) {
+        begin_t(t);
+        tile(std::true_type{}, t);
+        end_t(t);
+    }
+    for (; t < kv_end; ++t) {
+        begin_t(t);
+        end_t(t);
     }
     // dS carried without its per-row factor 2 scale / R
-    if (qi < T_)
-        store_cols16<T, D>(p.dq + b * p.dqs[0] + hq * p.dqs[1] + qi * p.dqs[2], hi, acc, 2.f * sc * inv_r);
+    if (qi < T_) {
+        const float f = 2.f * sc * inv_r;
+        T* row = p.dq + b * p.dqs[0] + hq * p.dqs[1] + qi * p.dqs[2];
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt) {
+            const uint2 w{pack2<T>(acc[dt][0] * f, acc[dt][1] * f), pack2<T>(acc[dt][2] * f, acc[dt][3] * f)};
+            *reinterpret_cast<uint2*>(row + 16 * dt + 4 * g) = w;
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -618,15 +685,15 @@ int launch_fwd_wide(const WideParams<T>& prm, int exact, hipStream_t st) {
 template <typename T>
 int launch_bwd_wide(const WideParams<T>& prm, int exact, hipStream_t st) {
     const int64_t nq = static_cast<int64_t>((prm.T + kWRows - 1) / kWRows) * prm.B * prm.Hq;
-    if (nq * 64 * kWW >= (int64_t(1) << 32)) return SA_ERR_BAD_SHAPE;
+    if (nq * 64 * kFW >= (int64_t(1) << 32)) return SA_ERR_BAD_SHAPE;  // dQ blocks of kFW waves
     const int64_t nk = nq / prm.G;
     const dim3 gq(static_cast<unsigned>(nq)), gk(static_cast<unsigned>(nk));
     if (exact) {
-        flash_bwd_dq_wide_kernel<T, 256, true><<<gq, 64 * kWW, 0, st>>>(prm);
+        flash_bwd_dq_wide_kernel<T, 256, true><<<gq, 64 * kFW, 0, st>>>(prm);
         flash_bwd_kv_wide_kernel<T, 256, true, false><<<gk, 64 * kWW, 0, st>>>(prm);
         flash_bwd_kv_wide_kernel<T, 256, true, true><<<gk, 64 * kWW, 0, st>>>(prm);
     } else {
-        flash_bwd_dq_wide_kernel<T, 256, false><<<gq, 64 * kWW, 0, st>>>(prm);
+        flash_bwd_dq_wide_kernel<T, 256, false><<<gq, 64 * kFW, 0, st>>>(prm);
         flash_bwd_kv_wide_kernel<T, 256, false, false><<<gk, 64 * kWW, 0, st>>>(prm);
         flash_bwd_kv_wide_kernel<T, 256, false, true><<<gk, 64 * kWW, 0, st>>>(prm);
     }
