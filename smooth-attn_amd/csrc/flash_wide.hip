@@ -6,25 +6,29 @@
 // (flash_fwd.hip, flash_bwd.hip; reference kernels.py:1536-1631 and
 // :1667-1909): fp32 scores and weights, P and dS rounded to the input type
 // before their products, fp32 accumulation, row sums of the fp32 weights.
-// The forward and dQ give each wave 16 query rows on the 16x16x32 MFMA,
-// which halves their accumulators and lets a block of 8 waves run two per
-// SIMD (see the forward's comment).  The dK and dV kernels keep 32 key rows
-// per wave on the 32x32x16 MFMA: their accumulators take 128 registers per
-// lane, so they run one wave per SIMD with the accumulators in AGPRs: blocks
-// of 4 waves x 32 rows, 32-row tiles loaded straight into a ring of LDS
-// stages (the next tile in flight while the current one is used), one barrier
-// per tile, every MFMA group's LDS operands read before its first MFMA.  dK
-// and dV are separate kernels: together they would need 256 accumulator
-// registers plus 128 for the K and V operands and spill.
 //
-// dK / dV operands (the 32x32x16 layout and the transposing LDS read are
-// described in flash_common.hpp).  For contractions over D, chunk c of a lane's
-// operand is elements 16c + 8 (l / 32) .. +7 of its row: K, V stay in
-// registers, the other side is a 16-byte read of an LDS
-// tile.  For contractions over keys (or queries) the B operand is the lane's
-// own 16 C-layout values v = 8j .. 8j + 7, whose k slots are rows
-// 16j + 8 (i / 4) + 4 (l / 32) + i % 4 of the tile (i = 0..7), so the A
-// operand is a pair of transposing reads (4 rows each).
+// Every kernel here gives a wave 16 rows (queries for the forward and dQ,
+// keys for dK and dV) on v_mfma_f32_16x16x32: at D = 256 the accumulators of
+// 16 rows (16 tiles of 16 x 16, 64 registers per lane) leave room for two
+// waves per SIMD, where 32 rows on the 32x32x16 MFMA would need one wave per
+// SIMD.  Blocks of 8 waves own 128 rows and walk 64-row tiles of the other
+// side through a 2-stage LDS ring (2 x 64 KB) filled by direct-to-LDS loads,
+// one barrier per tile.  dK and dV are separate kernels (both accumulators
+// plus the K and V operands would not fit two waves per SIMD).
+//
+// 16x16x32 operands: A lane l holds row l % 16, k = 8 (l / 16) .. +7; B column
+// l % 16, the same k; C column l % 16, rows 4 (l / 16) .. +3.  For
+// contractions over D one side stays in registers and the other is a 16-byte
+// row read of an LDS tile.  For contractions over the tile's rows, the C
+// values of 16-row subtiles 2j and 2j + 1 (rows 4 (l / 16) + e and
+// 16 + 4 (l / 16) + e) are the B operand of step j as they stand, and the A
+// operand comes from two transposing reads of the row-major tile (lane
+// supplies row 4 (l / 16) + (l % 16) / 4, and that + 16, columns 16 dt +
+// 4 (l % 4): inside its 16-lane group lane i then receives column 16 dt + i of
+// those rows).  LDS rows are 512 bytes; logical 16-byte chunk c of row r is
+// stored at c ^ swz(r): r & 15 for row reads (16 rows per cycle), 2 (r & 7)
+// for transposing reads (8 rows x 32 bytes per cycle), and for tiles read
+// both ways fk_swz(r) = 2 (r & 7) | ((r >> 3) & 1), which serves both.
 #include <type_traits>
 
 #include "flash_tiles.hpp"
@@ -73,9 +77,8 @@ struct WideParams {
 // (16-byte row reads, 16 rows per cycle), V rows at c ^ 2 (r & 7)
 // (transposing reads, 8 rows x 32 bytes per cycle): both conflict-free.
 constexpr int kFW = 8;             // waves per block
-constexpr int kFRows = 16 * kFW;   // query rows per block (= kWRows)
-constexpr int kFKT = 64;           // keys per tile
-static_assert(kFRows == kWRows, "forward and backward share the query block size");
+constexpr int kFRows = 16 * kFW;   // query (key) rows per block
+constexpr int kFKT = 64;           // rows per staged tile
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 template <typename T>
@@ -512,139 +515,215 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_dq_wide_kernel(WideParams<
 }
 
 // ---------------------------------------------------------------------------
-// Backward: dV (DK = false) or dK (DK = true) of a block of 128 keys, walking
-// every query head of the GQA group and every 32-row query tile that sees
-// them.  dV needs only S (P = y / R); dK needs S and dP (dS).
+// Backward: dV (DK = false) or dK (DK = true), 16 key rows per wave on the
+// 16x16x32 MFMA: 8 waves x 16 keys (128 keys per block), two waves per SIMD,
+// 64-query tiles of every query head of the GQA group in a 2-stage LDS ring.
+// S = Q K^T (Q rows from LDS, K in registers) leaves lane l with key
+// l % 16 and queries 4 (l / 16) + e of each 16-query subtile: as they stand,
+// P (or dS) of subtiles 2j, 2j + 1 are the B operand of dV^T += dO^T P (dK^T
+// += Q^T dS) over query step j, with dO^T (Q^T) from transposing reads.  The
+// Q tile of dK is read both ways (shared swizzle fk_swz), the other tiles one
+// way (row reads: c ^ (r & 15); transposing reads: c ^ 2 (r & 7)).
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool EXACT, bool DK>
-__global__ __launch_bounds__(64 * kWW) void flash_bwd_kv_wide_kernel(WideParams<T> p) {
-    // Q rows (S = Q K^T), and for dK: Q^T (dK^T += Q^T dS) and dO rows
-    // (dP = dO V^T); for dV: dO^T (dV^T += dO^T P).
-    __shared__ __attribute__((aligned(16))) T ldsQ[2][kWT * D];               // ROW layout
-    __shared__ __attribute__((aligned(16))) T ldsTr[2][kWT * D];              // TR layout
-    __shared__ __attribute__((aligned(16))) T ldsO[2][DK ? kWT * D : 8];      // ROW layout
-    __shared__ __attribute__((aligned(16))) float ldr[2][2][kWT];  // [stage][1/R, -delta] of the tile's rows
+__global__ __launch_bounds__(64 * kFW) void flash_bwd_kv_wide_kernel(WideParams<T> p) {
+    using V8 = typename MfmaOps<T>::vec8;
+    constexpr int ROWB = D * 2;
+    constexpr int TB = kFKT * ROWB;     // bytes per 64-row query tile
+    constexpr int CPR = ROWB / 16;
+    constexpr int NI = TB / 1024 / kFW;
+    constexpr int RPI = 64 * kFW / CPR;
+    constexpr int NQS = kFKT / 16;      // 16-query subtiles per tile
+    static_assert(NI == 1 || RPI % 16 == 0, "one swizzled offset per lane");
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[2 * 2 * TB];  // [stage][Q, dO]
+    __shared__ __attribute__((aligned(16))) float ldr[2][2][kFKT];            // [stage][1/R, -delta]
+
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int hi = lane >> 5;
-    const int l32 = lane & 31;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4;
+    const int i16 = lane & 15;
     const int T_ = p.T;
     const int per = p.B * p.Hkv;
     const int kb = blockIdx.x / per;  // earliest key blocks (most queries) first
     const int rest = blockIdx.x - kb * per;
     const int b = rest / p.Hkv;
     const int hk = rest - b * p.Hkv;
-
-    const int k_start = kb * kWRows;
-    const int wk0 = k_start + 32 * wave;
-    const int kj = wk0 + l32;
+    const int k_start = kb * kFRows;
+    const int wk0 = k_start + 16 * wave;
+    const int kj = wk0 + i16;
     const int krow = min(kj, T_ - 1);
-    u32x4 kf[D / 16], vf[DK ? D / 16 : 1];
-    load_frags<D>(p.k + b * p.ks[0] + hk * p.ks[1] + krow * p.ks[2], hi, kf);
-    if constexpr (DK) load_frags<D>(p.v + b * p.vs[0] + hk * p.vs[1] + krow * p.vs[2], hi, vf);
 
-    f32x16 acc[D / 32];
+    // K (and V) as B operands: k step ks holds d = 32 ks + 8 g .. +7 of key kj
+    u32x4 kf[D / 32], vf[DK ? D / 32 : 1];
+    {
+        const T* kr = p.k + b * p.ks[0] + hk * p.ks[1] + krow * p.ks[2];
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) acc[dt] = f32x16{};
+        for (int ks = 0; ks < D / 32; ++ks) kf[ks] = *reinterpret_cast<const u32x4*>(kr + 32 * ks + 8 * g);
+        if constexpr (DK) {
+            const T* vr_ = p.v + b * p.vs[0] + hk * p.vs[1] + krow * p.vs[2];
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks) vf[ks] = *reinterpret_cast<const u32x4*>(vr_ + 32 * ks + 8 * g);
+        }
+    }
+    f32x4 acc[D / 16];
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
     const int W = p.window;
     const unsigned weff = W > 0 ? static_cast<unsigned>(W) : 0x7FFFFFFFu;
-    const int n_qt = (T_ + kWT - 1) / kWT;
-    const int qt_begin = k_start / kWT;
-    const int qt_end = W > 0 ? min(n_qt, (k_start + kWRows - 1 + W - 1) / kWT + 1) : n_qt;
+    const int n_qt = (T_ + kFKT - 1) / kFKT;
+    const int qt_begin = k_start / kFKT;
+    const int qt_end = W > 0 ? min(n_qt, (k_start + kFRows - 1 + W - 1) / kFKT + 1) : n_qt;
     const int nq = qt_end - qt_begin;  // >= 1 (k_start < T)
     const int n_it = p.G * nq;
     const float sc = p.scale;
 
-    // Query tile it: (group head g, rows q0 ..); its 1/R and -delta values go
-    // through a register one iteration ahead of their LDS store.
+    // DMA of the Q and dO rows of a query tile; Q stores chunk c of row r at
+    // c ^ qswz(r), dO at c ^ oswz(r)
+    auto qswz = [](int r) { return DK ? fk_swz(r) : (r & 15); };
+    auto oswz = [](int r) { return DK ? (r & 15) : 2 * (r & 7); };
+    const int drow = (wave * 64 + lane) / CPR;
+    const int pch = (wave * 64 + lane) % CPR;
+    const int64_t qrs = p.qs[2] * 2, ors = p.dos[2] * 2;
+    const int qoff = drow * static_cast<int>(qrs) + ((pch ^ qswz(drow)) << 4);
+    const int ooff = drow * static_cast<int>(ors) + ((pch ^ oswz(drow)) << 4);
     auto tile_of = [&](int it, int& hq, int& q0) {
-        const int g = it / nq;
-        q0 = (qt_begin + it - g * nq) * kWT;
-        hq = hk * p.G + g;
+        const int gg = it / nq;
+        q0 = (qt_begin + it - gg * nq) * kFKT;
+        hq = hk * p.G + gg;
     };
-    const WideLoader<T, D, false> qld(p.qs[2], wave, lane);
-    const WideLoader<T, D, true> trld(DK ? p.qs[2] : p.dos[2], wave, lane);
-    const WideLoader<T, D, false> old(p.dos[2], wave, lane);
-    auto issue = [&](int it, int buf) {
+    auto issue = [&](int it) {
         int hq, q0;
         tile_of(it, hq, q0);
-        const T* qp = p.q + b * p.qs[0] + hq * p.qs[1];
-        const T* op = p.dout + b * p.dos[0] + hq * p.dos[1];
-        qld.issue(qp, q0, T_, ldsQ[buf]);
-        if constexpr (DK) {
-            trld.issue(qp, q0, T_, ldsTr[buf]);
-            old.issue(op, q0, T_, ldsO[buf]);
-        } else {
-            trld.issue(op, q0, T_, ldsTr[buf]);
+        const unsigned char* qp = wide_uniform_ptr(reinterpret_cast<const unsigned char*>(p.q + b * p.qs[0] + hq * p.qs[1]));
+        const unsigned char* op = wide_uniform_ptr(reinterpret_cast<const unsigned char*>(p.dout + b * p.dos[0] + hq * p.dos[1]));
+        const int nrows = min(T_ - q0, kFKT);
+        unsigned char* lq = lds + (it & 1) * 2 * TB;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int skip = i * RPI;
+            wide_dma16(__builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(qp + (q0 + skip) * qrs), 0,
+                                                         max((nrows - skip) * static_cast<int>(qrs), 0), 0x00020000),
+                       qoff, lq + (i * kFW + wave) * 1024);
+            wide_dma16(__builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(op + (q0 + skip) * ors), 0,
+                                                         max((nrows - skip) * static_cast<int>(ors), 0), 0x00020000),
+                       ooff, lq + TB + (i * kFW + wave) * 1024);
         }
     };
-    // Lane l of every wave loads row l % 32's row sum (l < 32) or delta (the
-    // four waves store the same values, so no branch divides the loop); the
-    // raw value becomes 1/R or -delta only when it is stored an iteration
-    // later, so the load's latency is not waited for where it is issued.
+    // threads 0..63 load the tile's row sums (staged as 1/R), 64..127 its
+    // delta (staged as -delta); the raw value is stored an iteration later
     auto row_value = [&](int it) {
         int hq, q0;
         tile_of(it, hq, q0);
-        const int64_t idx = (static_cast<int64_t>(b) * p.Hq + hq) * T_ + min(q0 + (lane & (kWT - 1)), T_ - 1);
-        return (lane < kWT ? p.rs : p.delta)[idx];
+        const int64_t idx = (static_cast<int64_t>(b) * p.Hq + hq) * T_ + min(q0 + (tid & (kFKT - 1)), T_ - 1);
+        return tid < kFKT ? p.rs[idx] : (tid < 2 * kFKT ? p.delta[idx] : 0.f);
     };
-    auto staged = [&](float raw) {
-        return lane < kWT ? 1.f / raw : -raw;
+    auto store_rv = [&](int st, float raw) {
+        if (tid < 2 * kFKT) ldr[st][tid / kFKT][tid & (kFKT - 1)] = tid < kFKT ? 1.f / raw : -raw;
     };
-    issue(0, 0);
-    ldr[0][lane / kWT][lane & (kWT - 1)] = staged(row_value(0));
-    float rnext = row_value(min(1, n_it - 1));
+
+    // transposing reads of the tile the accumulators contract over (dK: Q,
+    // dV: dO): lane supplies row 4 g + i16 / 4 (+ 16), columns 16 dt + 4 (lane & 3)
+    const int vr = 4 * g + (i16 >> 2);
+    const int tsw = DK ? fk_swz(vr) : 2 * (vr & 7);
+    const int trbase = vr * ROWB + (((((lane & 3) >> 1) ^ (tsw & 1))) << 4) + 8 * (lane & 1);
+    const int trsw = tsw >> 1;
+    const int qsi = qswz(i16), osi = oswz(i16);
+
+    auto tile = [&](auto mask_tag, int it) {
+        constexpr bool MASK = decltype(mask_tag)::value;
+        int hq, q0;
+        tile_of(it, hq, q0);
+        (void)hq;
+        const int st = it & 1;
+        const unsigned char* Qb = lds + st * 2 * TB;
+        const unsigned char* Ob = Qb + TB;
+        float x[4 * NQS];
+#pragma unroll
+        for (int qst = 0; qst < NQS; ++qst) {
+            u32x4 a[D / 32];
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks)
+                a[ks] = *reinterpret_cast<const u32x4*>(Qb + (16 * qst + i16) * ROWB + (((4 * ks + g) ^ qsi) << 4));
+            f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks) s = Mfma16<T>::mma(as_vec8<V8>(a[ks]), as_vec8<V8>(kf[ks]), s);
+            // lane: key kj, queries q0 + 16 qst + 4 g + e
+            const float4 ir = *reinterpret_cast<const float4*>(&ldr[st][0][16 * qst + 4 * g]);
+            const float irv[4] = {ir.x, ir.y, ir.z, ir.w};
+            f32x4 dp;
+            if constexpr (DK) {
+                const float4 nd = *reinterpret_cast<const float4*>(&ldr[st][1][16 * qst + 4 * g]);
+                dp = f32x4{nd.x, nd.y, nd.z, nd.w};
+#pragma unroll
+                for (int ks = 0; ks < D / 32; ++ks)
+                    a[ks] = *reinterpret_cast<const u32x4*>(Ob + (16 * qst + i16) * ROWB + (((4 * ks + g) ^ osi) << 4));
+#pragma unroll
+                for (int ks = 0; ks < D / 32; ++ks) dp = Mfma16<T>::mma(as_vec8<V8>(a[ks]), as_vec8<V8>(vf[ks]), dp);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float y, rr;
+                weight_rr16<EXACT>(s[e], sc, y, rr);
+                const float yi = y * irv[e];
+                float v;
+                if constexpr (DK) v = dp[e] * yi * rr;  // dS (without 2 scale)
+                else v = yi;                            // P
+                if constexpr (MASK) {
+                    const int q = q0 + 16 * qst + 4 * g + e;
+                    v = keep_if(static_cast<unsigned>(q - kj) < weff && q < T_, v);
+                }
+                x[4 * qst + e] = v;
+            }
+        }
+        const unsigned char* Tb = DK ? Qb : Ob;
+#pragma unroll
+        for (int kk = 0; kk < kFKT / 32; ++kk) {
+            const float* xk = x + 8 * kk;
+            const u32x4 pw{pack2<T>(xk[0], xk[1]), pack2<T>(xk[2], xk[3]), pack2<T>(xk[4], xk[5]),
+                           pack2<T>(xk[6], xk[7])};
+            const V8 bop = as_vec8<V8>(pw);
+#pragma unroll
+            for (int dt = 0; dt < D / 16; ++dt) {
+                const unsigned char* p0 = Tb + 32 * kk * ROWB + trbase + ((dt ^ trsw) << 5);
+                acc[dt] = Mfma16<T>::mma(lds_read_tr16_pair<V8>(p0, p0 + 16 * ROWB), bop, acc[dt]);
+            }
+        }
+    };
+
+    issue(0);
+    store_rv(0, row_value(0));
     wide_wait_vmem();
     __syncthreads();
     for (int it = 0; it < n_it; ++it) {
-        const int buf = it & 1;
-        // stage buf ^ 1 was released by the barrier ending iteration it - 1;
-        // the last iteration reloads its own tile there (unused)
-        issue(min(it + 1, n_it - 1), buf ^ 1);
-        ldr[buf ^ 1][lane / kWT][lane & (kWT - 1)] = staged(rnext);
-        rnext = row_value(min(it + 2, n_it - 1));
+        const bool more = it + 1 < n_it;
+        float rnext = 0.f;
+        if (more) {
+            issue(it + 1);  // into the stage of it - 1, free since the barrier that ended it - 1
+            rnext = row_value(it + 1);
+        }
         int hq, q0;
         tile_of(it, hq, q0);
-        {
-            const f32x16 s = mma_rows16<T, D>(ldsQ[buf], l32, hi, kf, f32x16{});  // S: rows queries, column key
-            // this lane's rows r = 8 m + 4 hi .. +3 of 1/R and -delta
-            float ir[16], nd[16];
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                *reinterpret_cast<float4*>(ir + 4 * m) = *reinterpret_cast<const float4*>(&ldr[buf][0][8 * m + 4 * hi]);
-                *reinterpret_cast<float4*>(nd + 4 * m) = *reinterpret_cast<const float4*>(&ldr[buf][1][8 * m + 4 * hi]);
-            }
-            f32x16 dp;
-            if constexpr (DK) {
-#pragma unroll
-                for (int v = 0; v < 16; ++v) dp[v] = nd[v];
-                dp = mma_rows16<T, D>(ldsO[buf], l32, hi, vf, dp);  // dP - delta
-            }
-            ColOperands<T, D> at;
-            at.read(ldsTr[buf], lane);
-            float x[16];
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int r = 8 * (v >> 2) + 4 * hi + (v & 3);
-                const int q = q0 + r;
-                float y, rr;
-                weight_rr16<EXACT>(s[v], sc, y, rr);
-                const float yi = y * ir[v];
-                const bool ok = static_cast<unsigned>(q - kj) < weff && q < T_;
-                if constexpr (DK) x[v] = keep_if(ok, dp[v] * yi * rr);  // dS
-                else x[v] = keep_if(ok, yi);                            // P
-            }
-            u32x4 xw[2];
-            pack_b<T>(x, xw);
-            at.mma(xw, acc);  // dK^T += Q^T dS, or dV^T += dO^T P
+        // wave-uniform: some (query, key) pair of the tile is visible; all are
+        const bool active = q0 + kFKT - 1 >= wk0 && q0 < T_ && !(W > 0 && q0 - (wk0 + 15) >= W);
+        const bool interior = q0 >= wk0 + 15 && q0 + kFKT <= T_ && !(W > 0 && q0 + kFKT - 1 - wk0 >= W);
+        if (interior) tile(std::false_type{}, it);
+        else if (active) tile(std::true_type{}, it);
+        if (more) {
+            store_rv((it + 1) & 1, rnext);
+            wide_wait_vmem();
+            __syncthreads();
         }
-        wide_wait_vmem();
-        __syncthreads();  // tile it + 1 landed; every wave is done with stage buf
     }
     if (kj < T_) {
-        if constexpr (DK) store_cols16<T, D>(p.dk + b * p.dks[0] + hk * p.dks[1] + kj * p.dks[2], hi, acc, 2.f * sc);
-        else store_cols16<T, D>(p.dv + b * p.dvs[0] + hk * p.dvs[1] + kj * p.dvs[2], hi, acc, 1.f);
+        T* row = DK ? p.dk + b * p.dks[0] + hk * p.dks[1] + kj * p.dks[2] : p.dv + b * p.dvs[0] + hk * p.dvs[1] + kj * p.dvs[2];
+        const float f = DK ? 2.f * sc : 1.f;
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt) {
+            const uint2 w{pack2<T>(acc[dt][0] * f, acc[dt][1] * f), pack2<T>(acc[dt][2] * f, acc[dt][3] * f)};
+            *reinterpret_cast<uint2*>(row + 16 * dt + 4 * g) = w;
+        }
     }
 }
 
@@ -652,7 +731,7 @@ __global__ __launch_bounds__(64 * kWW) void flash_bwd_kv_wide_kernel(WideParams<
 // d stride 1, and a tile's rows within 32-bit byte offsets of its first row.
 bool wide_strides_ok(const int64_t* s) {
     return s[3] == 1 && s[0] % 8 == 0 && s[1] % 8 == 0 && s[2] % 8 == 0 && s[2] >= 0 &&
-           s[2] * 2 * kWT < (int64_t(1) << 31);
+           s[2] * 2 * kFKT < (int64_t(1) << 31);
 }
 
 int check_wide(int B, int Hq, int Hkv, int T, int D, int window_size, int dtype) {
@@ -684,18 +763,18 @@ int launch_fwd_wide(const WideParams<T>& prm, int exact, hipStream_t st) {
 
 template <typename T>
 int launch_bwd_wide(const WideParams<T>& prm, int exact, hipStream_t st) {
-    const int64_t nq = static_cast<int64_t>((prm.T + kWRows - 1) / kWRows) * prm.B * prm.Hq;
+    const int64_t nq = static_cast<int64_t>((prm.T + kFRows - 1) / kFRows) * prm.B * prm.Hq;
     if (nq * 64 * kFW >= (int64_t(1) << 32)) return SA_ERR_BAD_SHAPE;  // dQ blocks of kFW waves
     const int64_t nk = nq / prm.G;
     const dim3 gq(static_cast<unsigned>(nq)), gk(static_cast<unsigned>(nk));
     if (exact) {
         flash_bwd_dq_wide_kernel<T, 256, true><<<gq, 64 * kFW, 0, st>>>(prm);
-        flash_bwd_kv_wide_kernel<T, 256, true, false><<<gk, 64 * kWW, 0, st>>>(prm);
-        flash_bwd_kv_wide_kernel<T, 256, true, true><<<gk, 64 * kWW, 0, st>>>(prm);
+        flash_bwd_kv_wide_kernel<T, 256, true, false><<<gk, 64 * kFW, 0, st>>>(prm);
+        flash_bwd_kv_wide_kernel<T, 256, true, true><<<gk, 64 * kFW, 0, st>>>(prm);
     } else {
         flash_bwd_dq_wide_kernel<T, 256, false><<<gq, 64 * kFW, 0, st>>>(prm);
-        flash_bwd_kv_wide_kernel<T, 256, false, false><<<gk, 64 * kWW, 0, st>>>(prm);
-        flash_bwd_kv_wide_kernel<T, 256, false, true><<<gk, 64 * kWW, 0, st>>>(prm);
+        flash_bwd_kv_wide_kernel<T, 256, false, false><<<gk, 64 * kFW, 0, st>>>(prm);
+        flash_bwd_kv_wide_kernel<T, 256, false, true><<<gk, 64 * kFW, 0, st>>>(prm);
     }
     return status_from_launch();
 }
@@ -766,9 +845,6 @@ int flash_fwd_wide(const void* q, const void* k, const void* v, void* o, float* 
     if (!q || !k || !v || !o || !q_strides || !k_strides || !v_strides || !o_strides) return SA_ERR_NULL_POINTER;
     if (!wide_strides_ok(q_strides) || !wide_strides_ok(k_strides) || !wide_strides_ok(v_strides) ||
         !wide_strides_ok(o_strides) || !aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
-        return SA_ERR_BAD_STRIDE;
-    // the forward's K / V tiles are kFKT rows: byte offsets within one stay 32-bit
-    if (k_strides[2] * 2 * kFKT >= (int64_t(1) << 31) || v_strides[2] * 2 * kFKT >= (int64_t(1) << 31))
         return SA_ERR_BAD_STRIDE;
     if (B == 0 || T == 0) return 0;
     if (dtype == SA_BF16)
