@@ -41,9 +41,7 @@ constexpr int kBwdThreads = 256;
 // lane and the compiler keeps every MFMA in the VGPR form (with one block per
 // CU it moves the accumulators through AGPRs, which costs more than the few
 // dK/dV registers that now spill).
-#ifndef SA_BWD_DKDV_MINB
-#define SA_BWD_DKDV_MINB 2
-#endif
+constexpr int kBwdDkdvMinBlocks = 2;
 constexpr int kBwdBQ = 128;   // query rows per dQ block (32 per wave)
 constexpr int kBwdKT = 64;    // keys per staged tile in the dQ kernel
 constexpr int kBwdBK = 128;   // key rows per dK/dV block (32 per wave)
@@ -370,7 +368,7 @@ __global__ __launch_bounds__(kBwdThreads, 2) void flash_bwd_dq_kernel(BwdParams 
 // dK, dV
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool EXACT>
-__global__ __launch_bounds__(kBwdThreads, SA_BWD_DKDV_MINB) void flash_bwd_dkdv_kernel(BwdParams p) {
+__global__ __launch_bounds__(kBwdThreads, kBwdDkdvMinBlocks) void flash_bwd_dkdv_kernel(BwdParams p) {
     using Ops = MfmaOps<T>;
     using Vec = typename Ops::vec8;
     using Tl = SwzTile<D>;

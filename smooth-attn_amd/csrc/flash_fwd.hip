@@ -33,14 +33,12 @@
 namespace sa {
 namespace {
 
-#ifndef SA_FLASH_BKV
-#define SA_FLASH_BKV 64
-#endif
-constexpr int kBKV = SA_FLASH_BKV;  // keys per tile (a multiple of 32)
-#ifndef SA_FLASH_QT
-#define SA_FLASH_QT 1
-#endif
-constexpr int kQT = SA_FLASH_QT;       // 32-row query tiles per wave
+// Block shape: 64-key tiles, one 32-row query tile per wave, 8 waves (the
+// code also takes other multiples of 32 keys and two query tiles per wave;
+// 32- and 96-key tiles, 4-wave blocks and two query tiles per wave measured
+// slower on config 3).
+constexpr int kBKV = 64;              // keys per tile (a multiple of 32)
+constexpr int kQT = 1;                // 32-row query tiles per wave
 constexpr int kWaves = 8 / kQT;       // waves per block (256 query rows)
 constexpr int kThreads = 64 * kWaves;
 constexpr int kStages = 3;    // LDS ring of K/V tiles
