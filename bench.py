@@ -488,7 +488,7 @@ def bench_norm_sizes(torch, sa):
 
     fam = FamilyConfig()
     dev = torch.device("cuda:0")
-    out = {"causal_bf16": [], "causal_bf16_rotating": [], "rowwise_fp32": []}
+    out = {"causal_bf16": [], "rowwise_fp32": []}
     for L in (1024, 2048):
         gen = torch.Generator(device=dev).manual_seed(20 + L)
         x = (torch.randn(4, 16, L, L, generator=gen, device=dev) / math.sqrt(128)).to(torch.bfloat16)
@@ -500,21 +500,7 @@ def bench_norm_sizes(torch, sa):
         out["causal_bf16"].append({"L": L, "fwd_us": round(fus, 2), "bwd_us": round(bus, 2),
                                    "GBs": round((fb + bb) / ((fus + bus) * 1e-6) / 1e9, 1),
                                    "frac_hbm_peak": round((fb + bb) / ((fus + bus) * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
-        # The same kernels back to back over 4 copies of x, dy, y and dx
-        # (4 x 512 MiB at L = 1024).
-        copies = [(x, dy, y, torch.empty_like(x))] + [
-            (torch.randn_like(x), torch.randn_like(dy), torch.empty_like(x), torch.empty_like(x)) for _ in range(3)]
-        fr = time_rotating(torch, [lambda c=c: sa.softplus_norm_causal_triton_out(c[2], c[0], family=fam)
-                                   for c in copies])
-        br = time_rotating(torch, [lambda c=c: kernels._norm_bwd_2d(c[0].view(-1, L), c[1].view(-1, L),
-                                                                    c[3].view(-1, L), fam, causal=True)
-                                   for c in copies])
-        out["causal_bf16_rotating"].append({
-            "L": L, "fwd_us": round(fr, 2), "bwd_us": round(br, 2),
-            "GBs": round((fb + bb) / ((fr + br) * 1e-6) / 1e9, 1),
-            "frac_hbm_peak": round((fb + bb) / ((fr + br) * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-            "protocol": "100 back-to-back launches over 4 input/output copies, one event pair"})
-        del x, dy, y, copies
+        del x, dy, y
     for L in (1024, 2048, 4096):
         gen = torch.Generator(device=dev).manual_seed(30 + L)
         x = torch.randn(64 * L, L, generator=gen, device=dev) / math.sqrt(128)
@@ -536,6 +522,39 @@ def bench_norm_sizes(torch, sa):
     b1 = 16 * (2 * tri(512) + 2 * 512 * 512)
     out["config1_gpu_fwd"] = {"shape": [2, 8, 512, 512], "us": round(us1, 2), "bytes": b1,
                               "GBs": round(b1 / (us1 * 1e-6) / 1e9, 1)}
+    return out
+
+
+def bench_norm_rotating(torch, sa):
+    """Config 2 at L = 1024 and 2048 (causal bf16), the same kernels as
+    ``norm_other_sizes.causal_bf16`` timed back to back over 4 copies of x,
+    dy, y and dx (4 x 512 MiB at L = 1024, so each launch's inputs come from
+    HBM), 100 launches between one event pair.  Runs after the other GPU
+    legs, whose allocations it would otherwise reshuffle."""
+    from smooth_attn import FamilyConfig, kernels
+
+    fam = FamilyConfig()
+    dev = torch.device("cuda:0")
+    out = []
+    for L in (1024, 2048):
+        gen = torch.Generator(device=dev).manual_seed(20 + L)
+        copies = []
+        for _ in range(4):
+            x = (torch.randn(4, 16, L, L, generator=gen, device=dev) / math.sqrt(128)).to(torch.bfloat16)
+            dy = torch.randn(4, 16, L, L, generator=gen, device=dev).to(torch.bfloat16)
+            copies.append((x, dy, torch.empty_like(x), torch.empty_like(x)))
+        fr = time_rotating(torch, [lambda c=c: sa.softplus_norm_causal_triton_out(c[2], c[0], family=fam)
+                                   for c in copies])
+        br = time_rotating(torch, [lambda c=c: kernels._norm_bwd_2d(c[0].view(-1, L), c[1].view(-1, L),
+                                                                    c[3].view(-1, L), fam, causal=True)
+                                   for c in copies])
+        fb, bb = norm_bytes(4, 16, L)
+        out.append({"L": L, "fwd_us": round(fr, 2), "bwd_us": round(br, 2),
+                    "GBs": round((fb + bb) / ((fr + br) * 1e-6) / 1e9, 1),
+                    "frac_hbm_peak": round((fb + bb) / ((fr + br) * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                    "protocol": "100 back-to-back launches over 4 input/output copies, one event pair"})
+        del copies
+    torch.cuda.empty_cache()
     return out
 
 
@@ -759,6 +778,9 @@ def main():
         log("bench: RoPE attention, softmax baselines, paged-KV append")
         nxt = bench_next_rows(torch)
         log(f"bench: next rows {nxt}")
+        log("bench: config 2 at L = 1024 / 2048 back to back over rotating copies")
+        sizes["causal_bf16_rotating"] = bench_norm_rotating(torch, sa)
+        log(f"bench: rotating {sizes['causal_bf16_rotating']}")
     cpu = host = None
     if not args.no_cpu:
         threads, host = cpu_threads(torch)
