@@ -529,8 +529,9 @@ def bench_norm_rotating(torch, sa):
     """Config 2 at L = 1024 and 2048 (causal bf16), the same kernels as
     ``norm_other_sizes.causal_bf16`` timed back to back over 4 copies of x,
     dy, y and dx (4 x 512 MiB at L = 1024, so each launch's inputs come from
-    HBM), 100 launches between one event pair.  Runs after the other GPU
-    legs, whose allocations it would otherwise reshuffle."""
+    HBM): 100 launches between one event pair after 100 warm-up launches, the
+    median of three such runs.  Runs after the other GPU legs, whose
+    allocations it would otherwise reshuffle."""
     from smooth_attn import FamilyConfig, kernels
 
     fam = FamilyConfig()
@@ -543,16 +544,18 @@ def bench_norm_rotating(torch, sa):
             x = (torch.randn(4, 16, L, L, generator=gen, device=dev) / math.sqrt(128)).to(torch.bfloat16)
             dy = torch.randn(4, 16, L, L, generator=gen, device=dev).to(torch.bfloat16)
             copies.append((x, dy, torch.empty_like(x), torch.empty_like(x)))
-        fr = time_rotating(torch, [lambda c=c: sa.softplus_norm_causal_triton_out(c[2], c[0], family=fam)
-                                   for c in copies])
-        br = time_rotating(torch, [lambda c=c: kernels._norm_bwd_2d(c[0].view(-1, L), c[1].view(-1, L),
-                                                                    c[3].view(-1, L), fam, causal=True)
-                                   for c in copies])
+        fwd_fns = [lambda c=c: sa.softplus_norm_causal_triton_out(c[2], c[0], family=fam) for c in copies]
+        bwd_fns = [lambda c=c: kernels._norm_bwd_2d(c[0].view(-1, L), c[1].view(-1, L), c[3].view(-1, L), fam,
+                                                    causal=True) for c in copies]
+        # median of three timed runs of 100 launches, each after 100 warm-up launches
+        fr = sorted(time_rotating(torch, fwd_fns, warmup=100) for _ in range(3))[1]
+        br = sorted(time_rotating(torch, bwd_fns, warmup=100) for _ in range(3))[1]
         fb, bb = norm_bytes(4, 16, L)
         out.append({"L": L, "fwd_us": round(fr, 2), "bwd_us": round(br, 2),
                     "GBs": round((fb + bb) / ((fr + br) * 1e-6) / 1e9, 1),
                     "frac_hbm_peak": round((fb + bb) / ((fr + br) * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                    "protocol": "100 back-to-back launches over 4 input/output copies, one event pair"})
+                    "protocol": "100 back-to-back launches over 4 input/output copies between one event pair, "
+                                "after 100 warm-up launches; median of 3"})
         del copies
     torch.cuda.empty_cache()
     return out
