@@ -165,7 +165,9 @@ int sa_softmax_fwd_launch_info(const void* x, const void* y, int64_t n_rows,
  * the d stride must be 1, the others multiples of 16 bytes (8 elements of a
  * 16-bit type, 4 of fp32), base pointers 16-byte aligned, and for bf16/fp16
  * K and V row strides at most 16 MiB.  row_sums (nullable): fp32 [B, Hq, T] contiguous,
- * receives sum_j y_ij + 1e-12.  window_size 0 = full causal.  D in {32, 64,
+ * receives sum_j y_ij + 1e-12.  window_size 0 = full causal.  D: bf16 /
+ * fp16 any multiple of 8 in 8..256 (kernels built for 32, 64, 128 and 256
+ * read only the first D columns and store only those), fp32 one of {32, 64,
  * 128, 256}.  exact_math != 0 selects a correctly rounded sqrt.
  * Replaces _sp2norm_flash_fwd (kernels.py:1912-1931) and its kernel
  * _sp2norm_flash_fwd_with_rowsum_kernel (:1536-1631).

@@ -61,11 +61,25 @@ struct BwdParams {
     float* delta;  // [B, Hq, T] workspace (contiguous)
     int64_t qs[4], ks[4], vs[4], os[4], dos[4], dqs[4], dks[4], dvs[4];
     int B, Hq, Hkv, T, G, window;
+    int dr;  // head dim of the tensors (<= D, a multiple of 8; columns past it read as zero, are not stored)
     float scale;
 };
 
+// DMA offset past every tile's buffer resource (at most 64 rows of 2^24
+// bytes): the lane's 16 bytes load as zeros.
+constexpr int kPastTile = 0x7FFFFFF0;
+
 // Plain (cached) 16-byte global load: tiles here are re-read by many blocks.
 __device__ __forceinline__ u32x4 ldg16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+// Columns d0 .. d0 + 7 of a row; PART (head dim dr below the kernel's D):
+// zeros where they lie past dr (the load then reads column 0).
+template <bool PART, typename T>
+__device__ __forceinline__ u32x4 ldg16_cols(const T* row, int d0, int dr) {
+    if constexpr (!PART) return ldg16(row + d0);
+    const u32x4 v = ldg16(row + (d0 < dr ? d0 : 0));
+    return d0 < dr ? v : u32x4{0u, 0u, 0u, 0u};
+}
 
 // Staged tiles are unpadded [64 rows][D] of the 16-bit type, filled by direct
 // global->LDS loads (one 1 KB span of consecutive 16-byte chunks per wave
@@ -135,13 +149,16 @@ __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70)
 
 // Byte offset (from the tile's first row, row stride rsb) of the source of
 // this lane's DMA load i of a swizzled [64][D] tile: LDS slot s = (4 i +
-// wave) * 64 + lane holds row s / CPR, logical chunk (s % CPR) ^ f(row).
-template <int D>
-__device__ __forceinline__ int swz_src_off(int i, int wave, int lane, int rsb) {
+// wave) * 64 + lane holds row s / CPR, logical chunk (s % CPR) ^ f(row);
+// PART: chunks past the head dim dr take kPastTile (zeros).
+template <int D, bool PART>
+__device__ __forceinline__ int swz_src_off(int i, int wave, int lane, int rsb, int dr) {
     using Tl = SwzTile<D>;
     const int sl = (i * 4 + wave) * 64 + lane;
     const int row = sl / Tl::CPR;
-    return row * rsb + (((sl - row * Tl::CPR) ^ Tl::f(row)) << 4);
+    const int c = (sl - row * Tl::CPR) ^ Tl::f(row);
+    if constexpr (!PART) return row * rsb + (c << 4);
+    return 8 * c < dr ? row * rsb + (c << 4) : kPastTile;
 }
 
 // Issue the DMA loads of one [64][D] tile whose first row is at `base`
@@ -180,7 +197,9 @@ __device__ __forceinline__ void weight_and_rr(float s, float sc, float& y, float
 // ---------------------------------------------------------------------------
 // dQ (and delta)
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool EXACT>
+// PART: the tensors' head dim p.dr is below D (its columns past p.dr read as
+// zeros and are not stored); the kernels with PART false serve dr == D.
+template <typename T, int D, bool EXACT, bool PART>
 __global__ __launch_bounds__(kBwdThreads, 2) void flash_bwd_dq_kernel(BwdParams p) {
     using Ops = MfmaOps<T>;
     using Vec = typename Ops::vec8;
@@ -224,9 +243,9 @@ __global__ __launch_bounds__(kBwdThreads, 2) void flash_bwd_dq_kernel(BwdParams 
 #pragma unroll
     for (int dc = 0; dc < D / 16; ++dc) {
         const int d0 = dc * 16 + hi * 8;
-        qreg[dc] = ldg16(qp + qrow * p.qs[2] + d0);
-        doreg[dc] = ldg16(dop + qrow * p.dos[2] + d0);
-        const u32x4 ov = ldg16(op + qrow * p.os[2] + d0);
+        qreg[dc] = ldg16_cols<PART>(qp + qrow * p.qs[2], d0, p.dr);
+        doreg[dc] = ldg16_cols<PART>(dop + qrow * p.dos[2], d0, p.dr);
+        const u32x4 ov = ldg16_cols<PART>(op + qrow * p.os[2], d0, p.dr);
         const uint32_t dw[4] = {doreg[dc].x, doreg[dc].y, doreg[dc].z, doreg[dc].w};
         const uint32_t ow[4] = {ov.x, ov.y, ov.z, ov.w};
 #pragma unroll
@@ -252,7 +271,8 @@ __global__ __launch_bounds__(kBwdThreads, 2) void flash_bwd_dq_kernel(BwdParams 
     const float sc = p.scale;
 
     const int ksb = static_cast<int>(p.ks[2] * 2), vsb = static_cast<int>(p.vs[2] * 2);  // row strides (bytes)
-    const int koff = swz_src_off<D>(0, wave, lane, ksb), voff = swz_src_off<D>(0, wave, lane, vsb);
+    const int koff = swz_src_off<D, PART>(0, wave, lane, ksb, p.dr);
+    const int voff = swz_src_off<D, PART>(0, wave, lane, vsb, p.dr);
     // Keys past T read as zeros; they only meet masked weights (or rows
     // past T, whose dQ is not written).
     auto issue_tile = [&](int j, int buf) {
@@ -358,7 +378,7 @@ __global__ __launch_bounds__(kBwdThreads, 2) void flash_bwd_dq_kernel(BwdParams 
                 uint2 w;
                 w.x = pack2<T>(acc[dt][vg * 4 + 0] * f, acc[dt][vg * 4 + 1] * f);
                 w.y = pack2<T>(acc[dt][vg * 4 + 2] * f, acc[dt][vg * 4 + 3] * f);
-                *reinterpret_cast<uint2*>(row + d0) = w;
+                if (!PART || d0 < p.dr) *reinterpret_cast<uint2*>(row + d0) = w;
             }
         }
     }
@@ -367,7 +387,7 @@ __global__ __launch_bounds__(kBwdThreads, 2) void flash_bwd_dq_kernel(BwdParams 
 // ---------------------------------------------------------------------------
 // dK, dV
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool EXACT>
+template <typename T, int D, bool EXACT, bool PART>
 __global__ __launch_bounds__(kBwdThreads, kBwdDkdvMinBlocks) void flash_bwd_dkdv_kernel(BwdParams p) {
     using Ops = MfmaOps<T>;
     using Vec = typename Ops::vec8;
@@ -404,8 +424,8 @@ __global__ __launch_bounds__(kBwdThreads, kBwdDkdvMinBlocks) void flash_bwd_dkdv
     u32x4 kreg[D / 16], vreg[D / 16];
 #pragma unroll
     for (int dc = 0; dc < D / 16; ++dc) {
-        kreg[dc] = ldg16(kp + krow * p.ks[2] + dc * 16 + hi * 8);
-        vreg[dc] = ldg16(vp + krow * p.vs[2] + dc * 16 + hi * 8);
+        kreg[dc] = ldg16_cols<PART>(kp + krow * p.ks[2], dc * 16 + hi * 8, p.dr);
+        vreg[dc] = ldg16_cols<PART>(vp + krow * p.vs[2], dc * 16 + hi * 8, p.dr);
     }
 
     f32x16 dkacc[D / 32], dvacc[D / 32];
@@ -425,7 +445,8 @@ __global__ __launch_bounds__(kBwdThreads, kBwdDkdvMinBlocks) void flash_bwd_dkdv
     const float sc = p.scale;
 
     const int qsb = static_cast<int>(p.qs[2] * 2), dsb = static_cast<int>(p.dos[2] * 2);  // row strides (bytes)
-    const int qoff = swz_src_off<D>(0, wave, lane, qsb), dooff = swz_src_off<D>(0, wave, lane, dsb);
+    const int qoff = swz_src_off<D, PART>(0, wave, lane, qsb, p.dr);
+    const int dooff = swz_src_off<D, PART>(0, wave, lane, dsb, p.dr);
     float rst = 0.f;
     // Queries past T read as zeros; their weights are masked.
     auto issue_tile = [&](int it, int buf) {
@@ -572,36 +593,45 @@ __global__ __launch_bounds__(kBwdThreads, kBwdDkdvMinBlocks) void flash_bwd_dkdv
                 wk.y = pack2<T>(dkacc[dt][vg * 4 + 2] * f, dkacc[dt][vg * 4 + 3] * f);
                 wv.x = pack2<T>(dvacc[dt][vg * 4 + 0], dvacc[dt][vg * 4 + 1]);
                 wv.y = pack2<T>(dvacc[dt][vg * 4 + 2], dvacc[dt][vg * 4 + 3]);
-                *reinterpret_cast<uint2*>(krw + d0) = wk;
-                *reinterpret_cast<uint2*>(vrw + d0) = wv;
+                if (!PART || d0 < p.dr) {
+                    *reinterpret_cast<uint2*>(krw + d0) = wk;
+                    *reinterpret_cast<uint2*>(vrw + d0) = wv;
+                }
             }
         }
     }
 }
 
-template <typename T, int D>
-int launch_bwd(const BwdParams& prm, int exact, hipStream_t st) {
+template <typename T, int D, bool PART>
+int launch_bwd_part(const BwdParams& prm, int exact, hipStream_t st) {
     const unsigned nqb = static_cast<unsigned>((prm.T + kBwdBQ - 1) / kBwdBQ);
     const unsigned nkb = static_cast<unsigned>((prm.T + kBwdBK - 1) / kBwdBK);
     const dim3 gq(nqb * prm.B * prm.Hq), gk(nkb * prm.B * prm.Hkv), blk(kBwdThreads);
     if (exact) {
-        flash_bwd_dq_kernel<T, D, true><<<gq, blk, 0, st>>>(prm);
-        flash_bwd_dkdv_kernel<T, D, true><<<gk, blk, 0, st>>>(prm);
+        flash_bwd_dq_kernel<T, D, true, PART><<<gq, blk, 0, st>>>(prm);
+        flash_bwd_dkdv_kernel<T, D, true, PART><<<gk, blk, 0, st>>>(prm);
     } else {
-        flash_bwd_dq_kernel<T, D, false><<<gq, blk, 0, st>>>(prm);
-        flash_bwd_dkdv_kernel<T, D, false><<<gk, blk, 0, st>>>(prm);
+        flash_bwd_dq_kernel<T, D, false, PART><<<gq, blk, 0, st>>>(prm);
+        flash_bwd_dkdv_kernel<T, D, false, PART><<<gk, blk, 0, st>>>(prm);
     }
     return status_from_launch();
 }
 
+// The masked kernels (PART) only where the head dim is below D: the masks
+// cost the dK/dV kernel registers, and at D = 128 spills in its tile loop.
+template <typename T, int D>
+int launch_bwd(const BwdParams& prm, int exact, hipStream_t st) {
+    if (prm.dr == D) return launch_bwd_part<T, D, false>(prm, exact, st);
+    return launch_bwd_part<T, D, true>(prm, exact, st);
+}
+
+// Head dims 8..128 (multiples of 8) run on the kernels for the next of 32,
+// 64, 128 with the columns past prm.dr masked.
 template <typename T>
-int launch_bwd_d(const BwdParams& prm, int D, int exact, hipStream_t st) {
-    switch (D) {
-        case 32: return launch_bwd<T, 32>(prm, exact, st);
-        case 64: return launch_bwd<T, 64>(prm, exact, st);
-        case 128: return launch_bwd<T, 128>(prm, exact, st);
-        default: return SA_ERR_UNSUPPORTED;
-    }
+int launch_bwd_d(const BwdParams& prm, int exact, hipStream_t st) {
+    if (prm.dr <= 32) return launch_bwd<T, 32>(prm, exact, st);
+    if (prm.dr <= 64) return launch_bwd<T, 64>(prm, exact, st);
+    return launch_bwd<T, 128>(prm, exact, st);
 }
 
 // (b, h, t) strides keep every row 16-byte aligned; d stride 1.
@@ -624,7 +654,7 @@ extern "C" int sa_flash_bwd(const void* q, const void* k, const void* v, const v
                              window_size, exact_math, reinterpret_cast<hipStream_t>(stream));
     }
     if (dtype != SA_BF16 && dtype != SA_F16) return SA_ERR_BAD_DTYPE;
-    if (D == 256) {
+    if (D > 128) {
         const int64_t* const all[8] = {q_strides,  k_strides,  v_strides,  o_strides,
                                        do_strides, dq_strides, dk_strides, dv_strides};
         return flash_bwd_wide(q, k, v, o, dout, row_sums, dq, dk, dv, delta_ws, B, Hq, Hkv, T, D, all, scale,
@@ -635,7 +665,7 @@ extern "C" int sa_flash_bwd(const void* q, const void* k, const void* v, const v
     if (!q_strides || !k_strides || !v_strides || !o_strides || !do_strides || !dq_strides || !dk_strides ||
         !dv_strides)
         return SA_ERR_NULL_POINTER;
-    if (D != 32 && D != 64 && D != 128) return SA_ERR_UNSUPPORTED;
+    if (D < 8 || D % 8 != 0) return SA_ERR_UNSUPPORTED;
     const int64_t* all[8] = {q_strides, k_strides, v_strides, o_strides, do_strides, dq_strides, dk_strides, dv_strides};
     for (const int64_t* s : all)
         if (!bwd_strides_ok(s)) return SA_ERR_BAD_STRIDE;
@@ -673,9 +703,10 @@ extern "C" int sa_flash_bwd(const void* q, const void* k, const void* v, const v
     prm.T = T;
     prm.G = Hq / Hkv;
     prm.window = window_size;
+    prm.dr = D;
     prm.scale = scale;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int ex = exact_math ? 1 : 0;
-    if (dtype == SA_BF16) return launch_bwd_d<bf16>(prm, D, ex, s);
-    return launch_bwd_d<f16>(prm, D, ex, s);
+    if (dtype == SA_BF16) return launch_bwd_d<bf16>(prm, ex, s);
+    return launch_bwd_d<f16>(prm, ex, s);
 }

@@ -56,8 +56,13 @@ struct FlashParams {
     const float* rope_sin;
     int64_t qs[4], ks[4], vs[4], os[4];
     int B, Hq, Hkv, T, G, window, nqb;
+    int dr;  // head dim of the tensors (<= D, a multiple of 8; columns past it read as zero, are not stored)
     float scale;
 };
+
+// DMA offset past every tile's buffer resource (at most 64 rows of 2^24
+// bytes): the lane's 16 bytes load as zeros.
+constexpr int kPastTile = 0x7FFFFFF0;
 
 // T: 16-bit type of P V (and of q/k/v unless fp8).  QK8: q, k are e4m3fn.
 // V8: v is e4m3fn.
@@ -344,7 +349,10 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashParams p) {
                     qreg[qt][dc][w] = d0 + 16 * w < D ? raw : u32x4{0u, 0u, 0u, 0u};
                 }
             } else {
-                qreg[qt][dc][0] = load16(qp + qrow * qrs + (dc * 16 + hi * 8) * 2);
+                // columns past the head dim (dr < D) read column 0 and are zeroed
+                const int d0 = dc * 16 + hi * 8;
+                const u32x4 raw = load16(qp + qrow * qrs + (d0 < p.dr ? d0 : 0) * 2);
+                qreg[qt][dc][0] = d0 < p.dr ? raw : u32x4{0u, 0u, 0u, 0u};
             }
         }
         if constexpr (ROPE && !QK8) {
@@ -394,7 +402,8 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashParams p) {
     // loads, the swizzle reads only row bits that i does not change), so
     // one offset serves every load; load i gets its own scalar resource
     // starting i * kKRows rows into the tile, sized to the rows before T, so
-    // rows past T read as zeros (they only meet masked weights).
+    // rows past T read as zeros (they only meet masked weights).  Lanes
+    // whose logical chunk lies past the head dim dr take kPastTile (zeros).
     constexpr int kKRows = kThreads / Gm::KCPR, kVRows = kThreads / Gm::VCPRL;
     static_assert(Gm::KNI == 1 || (kThreads % Gm::KCPR == 0 && (kKRows / Gm::KRPW) % Gm::KCPR == 0),
                   "K loads of a lane must share one swizzled offset");
@@ -404,9 +413,11 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashParams p) {
     {
         const int sl = wave * 64 + lane;
         const int krow = min(sl / Gm::KCPR, kBKV - 1);
-        koff = krow * static_cast<int>(krs) + ((sl - krow * Gm::KCPR) ^ Gm::swz_k(krow)) * 16;
+        const int kch = (sl - krow * Gm::KCPR) ^ Gm::swz_k(krow);
+        koff = kch * (16 / Gm::QKB) < p.dr ? krow * static_cast<int>(krs) + kch * 16 : kPastTile;
         const int vrow = min(sl / Gm::VCPRL, kBKV - 1);
-        voff = vrow * static_cast<int>(vrs) + ((sl - vrow * Gm::VCPRL) ^ Gm::swz_v(vrow)) * 16;
+        const int vch = (sl - vrow * Gm::VCPRL) ^ Gm::swz_v(vrow);
+        voff = vch * 8 < p.dr ? vrow * static_cast<int>(vrs) + vch * 16 : kPastTile;
     }
     auto issue_tile = [&](int j, int buf) {
         const int k0 = j * kBKV;
@@ -707,7 +718,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashParams p) {
                     uint2 w;
                     w.x = pack2<T>(oacc[qt][dt][vg * 4 + 0] * inv, oacc[qt][dt][vg * 4 + 1] * inv);
                     w.y = pack2<T>(oacc[qt][dt][vg * 4 + 2] * inv, oacc[qt][dt][vg * 4 + 3] * inv);
-                    *reinterpret_cast<uint2*>(orow + d0) = w;
+                    if (d0 < p.dr) *reinterpret_cast<uint2*>(orow + d0) = w;
                 }
             }
             if (hi == 0 && p.row_sums != nullptr) p.row_sums[static_cast<int64_t>(bh) * T_ + qi] = stot;
@@ -776,14 +787,13 @@ int launch_rope(FlashParams prm, T* k_rot, hipStream_t st) {
     return status_from_launch();
 }
 
+// Head dims 8..128 (multiples of 8) run on the kernel for the next of 32,
+// 64, 128 with the columns past prm.dr masked.
 template <typename T, bool QK8, bool V8>
-int launch_flash_d(const FlashParams& prm, int D, int exact, hipStream_t st) {
-    switch (D) {
-        case 32: return launch_flash<T, 32, QK8, V8>(prm, exact, st);
-        case 64: return launch_flash<T, 64, QK8, V8>(prm, exact, st);
-        case 128: return launch_flash<T, 128, QK8, V8>(prm, exact, st);
-        default: return SA_ERR_UNSUPPORTED;
-    }
+int launch_flash_d(const FlashParams& prm, int exact, hipStream_t st) {
+    if (prm.dr <= 32) return launch_flash<T, 32, QK8, V8>(prm, exact, st);
+    if (prm.dr <= 64) return launch_flash<T, 64, QK8, V8>(prm, exact, st);
+    return launch_flash<T, 128, QK8, V8>(prm, exact, st);
 }
 
 // Largest K / V row stride (bytes) the tile loads address with 32-bit offsets.
@@ -801,7 +811,7 @@ int fill_params(FlashParams& prm, const void* q, const void* k, const void* v, v
                 int v_bytes) {
     if (B < 0 || Hq <= 0 || Hkv <= 0 || T < 0 || Hq % Hkv != 0 || window_size < 0) return SA_ERR_BAD_SHAPE;
     if (!q || !k || !v || !o || !q_strides || !k_strides || !v_strides || !o_strides) return SA_ERR_NULL_POINTER;
-    if (D != 32 && D != 64 && D != 128) return SA_ERR_UNSUPPORTED;
+    if (D < 8 || D > 128 || D % 8 != 0) return SA_ERR_UNSUPPORTED;
     if (!strides_ok(q_strides, qk_bytes) || !strides_ok(k_strides, qk_bytes) || !strides_ok(v_strides, v_bytes) ||
         !strides_ok(o_strides, 2) || !aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
         return SA_ERR_BAD_STRIDE;
@@ -826,6 +836,7 @@ int fill_params(FlashParams& prm, const void* q, const void* k, const void* v, v
     prm.G = Hq / Hkv;
     prm.window = window_size;
     prm.nqb = (T + kBQ2 - 1) / kBQ2;
+    prm.dr = D;
     prm.scale = scale;
     return 0;
 }
@@ -842,7 +853,7 @@ extern "C" int sa_flash_fwd(const void* q, const void* k, const void* v, void* o
         return flash_fwd_f32(q, k, v, o, row_sums, B, Hq, Hkv, T, D, q_strides, k_strides, v_strides, o_strides,
                              scale, window_size, exact_math, reinterpret_cast<hipStream_t>(stream));
     if (dtype != SA_BF16 && dtype != SA_F16) return SA_ERR_BAD_DTYPE;
-    if (D == 256)
+    if (D > 128)
         return flash_fwd_wide(q, k, v, o, row_sums, B, Hq, Hkv, T, D, q_strides, k_strides, v_strides, o_strides,
                               scale, window_size, exact_math, dtype, reinterpret_cast<hipStream_t>(stream));
     FlashParams prm{};
@@ -852,8 +863,8 @@ extern "C" int sa_flash_fwd(const void* q, const void* k, const void* v, void* o
     if (B == 0 || T == 0) return 0;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int ex = exact_math ? 1 : 0;
-    if (dtype == SA_BF16) return launch_flash_d<bf16, false, false>(prm, D, ex, s);
-    return launch_flash_d<f16, false, false>(prm, D, ex, s);
+    if (dtype == SA_BF16) return launch_flash_d<bf16, false, false>(prm, ex, s);
+    return launch_flash_d<f16, false, false>(prm, ex, s);
 }
 
 extern "C" int sa_flash_fp8_fwd(const void* q8, const void* k8, const void* v, void* o, float* row_sums,
@@ -869,13 +880,14 @@ extern "C" int sa_flash_fp8_fwd(const void* q8, const void* k8, const void* v, v
     const int st = fill_params(prm, q8, k8, v, o, row_sums, B, Hq, Hkv, T, D, q_strides, k_strides, v_strides,
                                o_strides, attn_scale, window_size, 1, v8 ? 1 : 2);
     if (st != 0) return st;
+    if (D != 32 && D != 64 && D != 128) return SA_ERR_UNSUPPORTED;  // fp8 kernels: native head dims only
     if (B == 0 || T == 0) return 0;
     prm.q_scale = q_scale;
     prm.k_scale = k_scale;
     prm.v_scale = v_scale;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    if (v8) return launch_flash_d<bf16, true, true>(prm, D, 0, s);
-    return launch_flash_d<bf16, true, false>(prm, D, 0, s);
+    if (v8) return launch_flash_d<bf16, true, true>(prm, 0, s);
+    return launch_flash_d<bf16, true, false>(prm, 0, s);
 }
 
 extern "C" int sa_rope_rotate(const void* x, void* out, const float* cos_table, const float* sin_table, int B,
@@ -924,6 +936,7 @@ extern "C" int sa_flash_rope_fwd(const void* q, const void* k, const void* v, co
     const int st = fill_params(prm, q, k, v, o, row_sums, B, Hq, Hkv, T, D, q_strides, k_strides, v_strides,
                                o_strides, scale, window_size, 2, 2);
     if (st != 0) return st;
+    if (D != 32 && D != 64 && D != 128) return SA_ERR_UNSUPPORTED;  // fused RoPE: native head dims only
     if (B == 0 || T == 0) return 0;
     if (ws_bytes < sa_flash_rope_workspace_size(B, Hkv, T, D)) return SA_ERR_WORKSPACE;
     if (!aligned16(cos_table) || !aligned16(sin_table) || !aligned16(k_rot_ws)) return SA_ERR_BAD_STRIDE;

@@ -53,8 +53,30 @@ struct WideParams {
     float* delta;  // [B, Hq, T]
     int64_t qs[4], ks[4], vs[4], os[4], dos[4], dqs[4], dks[4], dvs[4];
     int B, Hq, Hkv, T, G, window;
+    int dr;  // head dim of the tensors (<= 256, a multiple of 8; columns past it read as zero, are not stored)
     float scale;
 };
+
+// DMA offset past every tile's buffer resource (64 rows, under 2^31 bytes):
+// the lane's 16 bytes load as zeros.
+constexpr int kPastTile = 0x7FFFFFF0;
+
+// 16 bytes of columns d0 .. d0 + 7 of a row; PART (head dim dr below the
+// kernel's D): zeros where they lie past dr (the load then reads column 0).
+template <bool PART, typename T>
+__device__ __forceinline__ u32x4 wide_cols(const T* row, int d0, int dr) {
+    if constexpr (!PART) return *reinterpret_cast<const u32x4*>(row + d0);
+    const u32x4 v = *reinterpret_cast<const u32x4*>(row + (d0 < dr ? d0 : 0));
+    return d0 < dr ? v : u32x4{0u, 0u, 0u, 0u};
+}
+
+// Byte offset of a DMA lane's source: row drow, logical chunk c (8 columns);
+// PART: chunks past the head dim dr take kPastTile.
+template <bool PART>
+__device__ __forceinline__ int wide_src_off(int drow, int c, int64_t rs, int dr) {
+    if constexpr (!PART) return drow * static_cast<int>(rs) + (c << 4);
+    return 8 * c < dr ? drow * static_cast<int>(rs) + (c << 4) : kPastTile;
+}
 
 
 // ---------------------------------------------------------------------------
@@ -143,7 +165,7 @@ __global__ __launch_bounds__(64 * kFW) void flash_fwd_wide_kernel(WideParams<T> 
     {
         const T* qr = p.q + b * p.qs[0] + hq * p.qs[1] + qrow * p.qs[2];
 #pragma unroll
-        for (int ks = 0; ks < D / 32; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qr + 32 * ks + 8 * g);
+        for (int ks = 0; ks < D / 32; ++ks) qf[ks] = wide_cols<true>(qr, 32 * ks + 8 * g, p.dr);
     }
 
     const int W = p.window;
@@ -155,11 +177,11 @@ __global__ __launch_bounds__(64 * kFW) void flash_fwd_wide_kernel(WideParams<T> 
 
     // DMA: slot s = (kFW i + wave) * 64 + lane of a tile holds row s / CPR,
     // physical chunk s % CPR; rows past T read as zeros (they meet only masked
-    // weights).
+    // weights), and so do columns past the head dim.
     const int drow = (wave * 64 + lane) / CPR;
     const int pch = (wave * 64 + lane) % CPR;
-    const int koff = drow * static_cast<int>(krs) + ((pch ^ (drow & 15)) << 4);
-    const int voff = drow * static_cast<int>(vrs) + ((pch ^ (2 * (drow & 7))) << 4);
+    const int koff = wide_src_off<true>(drow, pch ^ (drow & 15), krs, p.dr);
+    const int voff = wide_src_off<true>(drow, pch ^ (2 * (drow & 7)), vrs, p.dr);
     auto issue = [&](int t) {
         const int k0 = t * kFKT;
         const int nrows = min(T_ - k0, kFKT);
@@ -295,7 +317,7 @@ __global__ __launch_bounds__(64 * kFW) void flash_fwd_wide_kernel(WideParams<T> 
 #pragma unroll
         for (int dt = 0; dt < D / 16; ++dt) {
             const uint2 w{pack2<T>(oacc[dt][0] * inv, oacc[dt][1] * inv), pack2<T>(oacc[dt][2] * inv, oacc[dt][3] * inv)};
-            *reinterpret_cast<uint2*>(orow + 16 * dt + 4 * g) = w;
+            if (16 * dt + 4 * g < p.dr) *reinterpret_cast<uint2*>(orow + 16 * dt + 4 * g) = w;
         }
         if (g == 0 && p.row_sums != nullptr) p.row_sums[(static_cast<int64_t>(b) * p.Hq + hq) * T_ + qi] = tot;
     }
@@ -314,7 +336,9 @@ __global__ __launch_bounds__(64 * kFW) void flash_fwd_wide_kernel(WideParams<T> 
 // together (transposing reads); V rows use c ^ (r & 15).
 __device__ __forceinline__ int fk_swz(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
 
-template <typename T, int D, bool EXACT>
+// PART: the tensors' head dim p.dr is below D (columns past it read as zeros
+// and are not stored); the kernels with PART false serve dr == D.
+template <typename T, int D, bool EXACT, bool PART>
 __global__ __launch_bounds__(64 * kFW) void flash_bwd_dq_wide_kernel(WideParams<T> p) {
     using V8 = typename MfmaOps<T>::vec8;
     constexpr int ROWB = D * 2;
@@ -358,9 +382,9 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_dq_wide_kernel(WideParams<
         const T* orw = p.o + b * p.os[0] + hq * p.os[1] + qrow * p.os[2];
 #pragma unroll
         for (int ks = 0; ks < D / 32; ++ks) {
-            qf[ks] = *reinterpret_cast<const u32x4*>(qr + 32 * ks + 8 * g);
-            df[ks] = *reinterpret_cast<const u32x4*>(dr + 32 * ks + 8 * g);
-            const u32x4 ov = *reinterpret_cast<const u32x4*>(orw + 32 * ks + 8 * g);
+            qf[ks] = wide_cols<PART>(qr, 32 * ks + 8 * g, p.dr);
+            df[ks] = wide_cols<PART>(dr, 32 * ks + 8 * g, p.dr);
+            const u32x4 ov = wide_cols<PART>(orw, 32 * ks + 8 * g, p.dr);
             const uint32_t ow[4] = {ov[0], ov[1], ov[2], ov[3]};
             const uint32_t dw[4] = {df[ks][0], df[ks][1], df[ks][2], df[ks][3]};
 #pragma unroll
@@ -382,8 +406,8 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_dq_wide_kernel(WideParams<
 
     const int drow = (wave * 64 + lane) / CPR;
     const int pch = (wave * 64 + lane) % CPR;
-    const int koff = drow * static_cast<int>(krs) + ((pch ^ fk_swz(drow)) << 4);
-    const int voff = drow * static_cast<int>(vrs) + ((pch ^ (drow & 15)) << 4);
+    const int koff = wide_src_off<PART>(drow, pch ^ fk_swz(drow), krs, p.dr);
+    const int voff = wide_src_off<PART>(drow, pch ^ (drow & 15), vrs, p.dr);
     auto issue = [&](int t) {
         const int k0 = t * kFKT;
         const int nrows = min(T_ - k0, kFKT);
@@ -509,7 +533,7 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_dq_wide_kernel(WideParams<
 #pragma unroll
         for (int dt = 0; dt < D / 16; ++dt) {
             const uint2 w{pack2<T>(acc[dt][0] * f, acc[dt][1] * f), pack2<T>(acc[dt][2] * f, acc[dt][3] * f)};
-            *reinterpret_cast<uint2*>(row + 16 * dt + 4 * g) = w;
+            if (!PART || 16 * dt + 4 * g < p.dr) *reinterpret_cast<uint2*>(row + 16 * dt + 4 * g) = w;
         }
     }
 }
@@ -525,7 +549,7 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_dq_wide_kernel(WideParams<
 // Q tile of dK is read both ways (shared swizzle fk_swz), the other tiles one
 // way (row reads: c ^ (r & 15); transposing reads: c ^ 2 (r & 7)).
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool EXACT, bool DK>
+template <typename T, int D, bool EXACT, bool DK, bool PART>
 __global__ __launch_bounds__(64 * kFW) void flash_bwd_kv_wide_kernel(WideParams<T> p) {
     using V8 = typename MfmaOps<T>::vec8;
     constexpr int ROWB = D * 2;
@@ -559,11 +583,11 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_kv_wide_kernel(WideParams<
     {
         const T* kr = p.k + b * p.ks[0] + hk * p.ks[1] + krow * p.ks[2];
 #pragma unroll
-        for (int ks = 0; ks < D / 32; ++ks) kf[ks] = *reinterpret_cast<const u32x4*>(kr + 32 * ks + 8 * g);
+        for (int ks = 0; ks < D / 32; ++ks) kf[ks] = wide_cols<PART>(kr, 32 * ks + 8 * g, p.dr);
         if constexpr (DK) {
             const T* vr_ = p.v + b * p.vs[0] + hk * p.vs[1] + krow * p.vs[2];
 #pragma unroll
-            for (int ks = 0; ks < D / 32; ++ks) vf[ks] = *reinterpret_cast<const u32x4*>(vr_ + 32 * ks + 8 * g);
+            for (int ks = 0; ks < D / 32; ++ks) vf[ks] = wide_cols<PART>(vr_, 32 * ks + 8 * g, p.dr);
         }
     }
     f32x4 acc[D / 16];
@@ -586,8 +610,8 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_kv_wide_kernel(WideParams<
     const int drow = (wave * 64 + lane) / CPR;
     const int pch = (wave * 64 + lane) % CPR;
     const int64_t qrs = p.qs[2] * 2, ors = p.dos[2] * 2;
-    const int qoff = drow * static_cast<int>(qrs) + ((pch ^ qswz(drow)) << 4);
-    const int ooff = drow * static_cast<int>(ors) + ((pch ^ oswz(drow)) << 4);
+    const int qoff = wide_src_off<PART>(drow, pch ^ qswz(drow), qrs, p.dr);
+    const int ooff = wide_src_off<PART>(drow, pch ^ oswz(drow), ors, p.dr);
     auto tile_of = [&](int it, int& hq, int& q0) {
         const int gg = it / nq;
         q0 = (qt_begin + it - gg * nq) * kFKT;
@@ -722,7 +746,7 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_kv_wide_kernel(WideParams<
 #pragma unroll
         for (int dt = 0; dt < D / 16; ++dt) {
             const uint2 w{pack2<T>(acc[dt][0] * f, acc[dt][1] * f), pack2<T>(acc[dt][2] * f, acc[dt][3] * f)};
-            *reinterpret_cast<uint2*>(row + 16 * dt + 4 * g) = w;
+            if (!PART || 16 * dt + 4 * g < p.dr) *reinterpret_cast<uint2*>(row + 16 * dt + 4 * g) = w;
         }
     }
 }
@@ -737,7 +761,7 @@ bool wide_strides_ok(const int64_t* s) {
 int check_wide(int B, int Hq, int Hkv, int T, int D, int window_size, int dtype) {
     if (dtype != SA_BF16 && dtype != SA_F16) return SA_ERR_BAD_DTYPE;
     if (B < 0 || Hq <= 0 || Hkv <= 0 || T < 0 || Hq % Hkv != 0 || window_size < 0) return SA_ERR_BAD_SHAPE;
-    if (D != 256) return SA_ERR_UNSUPPORTED;
+    if (D <= 128 || D > 256 || D % 8 != 0) return SA_ERR_UNSUPPORTED;
     return 0;
 }
 
@@ -761,27 +785,35 @@ int launch_fwd_wide(const WideParams<T>& prm, int exact, hipStream_t st) {
     return status_from_launch();
 }
 
-template <typename T>
-int launch_bwd_wide(const WideParams<T>& prm, int exact, hipStream_t st) {
+template <typename T, bool PART>
+int launch_bwd_wide_part(const WideParams<T>& prm, int exact, hipStream_t st) {
     const int64_t nq = static_cast<int64_t>((prm.T + kFRows - 1) / kFRows) * prm.B * prm.Hq;
     if (nq * 64 * kFW >= (int64_t(1) << 32)) return SA_ERR_BAD_SHAPE;  // dQ blocks of kFW waves
     const int64_t nk = nq / prm.G;
     const dim3 gq(static_cast<unsigned>(nq)), gk(static_cast<unsigned>(nk));
     if (exact) {
-        flash_bwd_dq_wide_kernel<T, 256, true><<<gq, 64 * kFW, 0, st>>>(prm);
-        flash_bwd_kv_wide_kernel<T, 256, true, false><<<gk, 64 * kFW, 0, st>>>(prm);
-        flash_bwd_kv_wide_kernel<T, 256, true, true><<<gk, 64 * kFW, 0, st>>>(prm);
+        flash_bwd_dq_wide_kernel<T, 256, true, PART><<<gq, 64 * kFW, 0, st>>>(prm);
+        flash_bwd_kv_wide_kernel<T, 256, true, false, PART><<<gk, 64 * kFW, 0, st>>>(prm);
+        flash_bwd_kv_wide_kernel<T, 256, true, true, PART><<<gk, 64 * kFW, 0, st>>>(prm);
     } else {
-        flash_bwd_dq_wide_kernel<T, 256, false><<<gq, 64 * kFW, 0, st>>>(prm);
-        flash_bwd_kv_wide_kernel<T, 256, false, false><<<gk, 64 * kFW, 0, st>>>(prm);
-        flash_bwd_kv_wide_kernel<T, 256, false, true><<<gk, 64 * kFW, 0, st>>>(prm);
+        flash_bwd_dq_wide_kernel<T, 256, false, PART><<<gq, 64 * kFW, 0, st>>>(prm);
+        flash_bwd_kv_wide_kernel<T, 256, false, false, PART><<<gk, 64 * kFW, 0, st>>>(prm);
+        flash_bwd_kv_wide_kernel<T, 256, false, true, PART><<<gk, 64 * kFW, 0, st>>>(prm);
     }
     return status_from_launch();
 }
 
+// The masked kernels (PART) only for head dims below 256: the masks cost the
+// dK kernel registers (spills in its tile loop).
+template <typename T>
+int launch_bwd_wide(const WideParams<T>& prm, int exact, hipStream_t st) {
+    if (prm.dr == 256) return launch_bwd_wide_part<T, false>(prm, exact, st);
+    return launch_bwd_wide_part<T, true>(prm, exact, st);
+}
+
 template <typename T>
 int run_fwd_wide(const void* q, const void* k, const void* v, void* o, float* row_sums, int B, int Hq, int Hkv,
-                 int T_, const int64_t* qs, const int64_t* ks, const int64_t* vs, const int64_t* os, float scale,
+                 int T_, int D, const int64_t* qs, const int64_t* ks, const int64_t* vs, const int64_t* os, float scale,
                  int window_size, int exact_math, hipStream_t st) {
     WideParams<T> prm{};
     prm.q = static_cast<const T*>(q);
@@ -801,6 +833,7 @@ int run_fwd_wide(const void* q, const void* k, const void* v, void* o, float* ro
     prm.T = T_;
     prm.G = Hq / Hkv;
     prm.window = window_size;
+    prm.dr = D;
     prm.scale = scale;
     return launch_fwd_wide<T>(prm, exact_math, st);
 }
@@ -808,7 +841,7 @@ int run_fwd_wide(const void* q, const void* k, const void* v, void* o, float* ro
 template <typename T>
 int run_bwd_wide(const void* q, const void* k, const void* v, const void* o, const void* dout,
                  const float* row_sums, void* dq, void* dk, void* dv, float* delta_ws, int B, int Hq, int Hkv,
-                 int T_, const int64_t* const strides[8], float scale, int window_size, int exact_math,
+                 int T_, int D, const int64_t* const strides[8], float scale, int window_size, int exact_math,
                  hipStream_t st) {
     WideParams<T> prm{};
     prm.q = static_cast<const T*>(q);
@@ -830,6 +863,7 @@ int run_bwd_wide(const void* q, const void* k, const void* v, const void* o, con
     prm.T = T_;
     prm.G = Hq / Hkv;
     prm.window = window_size;
+    prm.dr = D;
     prm.scale = scale;
     return launch_bwd_wide<T>(prm, exact_math, st);
 }
@@ -848,9 +882,9 @@ int flash_fwd_wide(const void* q, const void* k, const void* v, void* o, float* 
         return SA_ERR_BAD_STRIDE;
     if (B == 0 || T == 0) return 0;
     if (dtype == SA_BF16)
-        return run_fwd_wide<bf16>(q, k, v, o, row_sums, B, Hq, Hkv, T, q_strides, k_strides, v_strides, o_strides,
+        return run_fwd_wide<bf16>(q, k, v, o, row_sums, B, Hq, Hkv, T, D, q_strides, k_strides, v_strides, o_strides,
                                   scale, window_size, exact_math, st);
-    return run_fwd_wide<f16>(q, k, v, o, row_sums, B, Hq, Hkv, T, q_strides, k_strides, v_strides, o_strides,
+    return run_fwd_wide<f16>(q, k, v, o, row_sums, B, Hq, Hkv, T, D, q_strides, k_strides, v_strides, o_strides,
                              scale, window_size, exact_math, st);
 }
 
@@ -868,9 +902,9 @@ int flash_bwd_wide(const void* q, const void* k, const void* v, const void* o, c
     }
     if (B == 0 || T == 0) return 0;
     if (dtype == SA_BF16)
-        return run_bwd_wide<bf16>(q, k, v, o, dout, row_sums, dq, dk, dv, delta_ws, B, Hq, Hkv, T, strides, scale,
+        return run_bwd_wide<bf16>(q, k, v, o, dout, row_sums, dq, dk, dv, delta_ws, B, Hq, Hkv, T, D, strides, scale,
                                   window_size, exact_math, st);
-    return run_bwd_wide<f16>(q, k, v, o, dout, row_sums, dq, dk, dv, delta_ws, B, Hq, Hkv, T, strides, scale,
+    return run_bwd_wide<f16>(q, k, v, o, dout, row_sums, dq, dk, dv, delta_ws, B, Hq, Hkv, T, D, strides, scale,
                              window_size, exact_math, st);
 }
 

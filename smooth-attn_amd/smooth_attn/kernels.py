@@ -562,16 +562,19 @@ _FLASH_KERNEL_DIMS = {dt: (32, 64, 128, 256) for dt in (torch.bfloat16, torch.fl
 
 
 def _kernel_head_dim(D, dtype=None):
-    """The head dim the kernels run for a head dim D: D itself where a kernel
-    exists for it, else the next one up (inputs zero-padded, outputs sliced:
-    zero columns add nothing to q.k, and the padded columns of O, dQ, dK, dV
-    are dropped).  The reference takes any power of two through next_pow2
-    (kernels.py:1918)."""
+    """The head dim the kernels are called with for a head dim D.  bf16 /
+    fp16: D rounded up to a multiple of 8 (the kernels built for 32, 64, 128
+    and 256 take any such D up to their size, reading only its columns); fp32
+    and fp8: the next of the head dims their kernels are built for.  Where it
+    differs from D, inputs are zero-padded and outputs sliced: zero columns
+    add nothing to q.k, and the padded columns of O, dQ, dK, dV are dropped.
+    The reference takes any power of two through next_pow2 (kernels.py:1918)
+    and masks its loads past D."""
     dims = _FLASH_KERNEL_DIMS.get(dtype, _FLASH_HEAD_DIMS)
-    if D in dims:
-        return D
     if D < 1 or D > dims[-1]:
         raise ValueError(f"fused attention supports head dims 1..{dims[-1]}, got {D}")
+    if dtype in (torch.bfloat16, torch.float16):
+        return -(-D // 8) * 8
     return next(d for d in dims if d >= D)
 
 
@@ -722,7 +725,7 @@ def _sp2norm_rope_flash_fwd(q, k, v, cos, sin, scale, n_kv_groups=1, window_size
     64 and 128 rotate Q in registers inside the fused kernel (K once into a
     workspace); fp32, and other head dims that are multiples of 16 up to
     256, rotate Q and K by sa_rope_rotate and run the plain fused forward
-    (head dims other than 32 / 64 / 128 / 256 zero-padded after the
+    (fp32 head dims other than 32 / 64 / 128 / 256 zero-padded after the
     rotation)."""
     _check_same_device("q", q, k=k, v=v, cos=cos, sin=sin, o=o)
     B, H_q, T, D = q.shape

@@ -217,3 +217,30 @@ def test_rope_rotate_argument_errors():
     assert lib.sa_rope_rotate(d, d, d, d, 1, 4, 64, 64, odd, _lib.SA_BF16, None) == -5
     assert lib.sa_rope_rotate(ctypes.c_void_p(24), d, d, d, 1, 4, 64, 64, s, _lib.SA_BF16, None) == -5
     assert lib.sa_rope_rotate(d, d, d, d, 0, 4, 64, 64, s, _lib.SA_BF16, None) == 0
+
+
+def test_flash_16bit_head_dims():
+    # bf16 / fp16: any multiple of 8 in 8..256 (kernels for 32, 64, 128, 256
+    # read only the first D columns); the fp8 and fused-RoPE kernels take 32,
+    # 64, 128 only.  Every check runs before any launch (B = 0 launches nothing).
+    lib = _lib.load()
+    d = ctypes.c_void_p(256)
+    s = (ctypes.c_int64 * 4)(2 * 64 * 256, 64 * 256, 256, 1)
+    fwd = lambda D, B=0: lib.sa_flash_fwd(d, d, d, d, None, B, 2, 2, 64, D, s, s, s, s, 0.1, 0, 0, _lib.SA_BF16,
+                                          None)
+    bwd = lambda D, B=0: lib.sa_flash_bwd(d, d, d, d, d, d, d, d, d, d, B, 2, 2, 64, D, s, s, s, s, s, s, s, s, 0.1,
+                                          0, 0, _lib.SA_F16, None)
+    for D in (0, 4, 12, 132, 250, 264, 512):
+        assert fwd(D) == -6, D
+        assert bwd(D) == -6, D
+    for D in (8, 24, 40, 96, 128, 136, 200, 248, 256):
+        assert fwd(D) == 0, D
+        assert bwd(D) == 0, D
+    fp8 = lambda D: lib.sa_flash_fp8_fwd(d, d, d, d, None, d, d, d, 0, 2, 2, 64, D, s, s, s, s, 0.1, 0,
+                                         _lib.SA_FP8_E4M3FN, None)
+    rope = lambda D: lib.sa_flash_rope_fwd(d, d, d, d, d, d, None, d, 1 << 20, 0, 2, 2, 64, D, s, s, s, s, 0.1, 0,
+                                           _lib.SA_BF16, None)
+    for D in (48, 96, 256):
+        assert fp8(D) == -6, D
+        assert rope(D) == -6, D
+    assert fp8(64) == 0 and rope(64) == 0

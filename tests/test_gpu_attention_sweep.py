@@ -1,7 +1,7 @@
 """Randomised parity sweep of the fused attention (forward and backward)
 against the float64 oracle, over combinations the fixed cases do not
-enumerate: dtype (bf16, fp16, fp32), head dims 8..256 (padded, native and
-the D = 256 kernels), GQA group sizes, windows, query counts around the
+enumerate: dtype (bf16, fp16, fp32), head dims 8..256 (masked below a
+kernel's size, fp32 padded, and the D = 256 kernels), GQA group sizes, windows, query counts around the
 32/64/128/256-row tile edges, and scales (GPU).
 
 Bars, as in the per-path tests: O and the gradients within 1e-2 (16-bit) or

@@ -149,7 +149,8 @@ def test_full_size_config3_sampled():
 @pytest.mark.parametrize("T", [1, 100, 300])
 def test_forward_head_dims_below_128(D, T):
     # any head dim up to 128 (the reference takes powers of two through
-    # next_pow2, kernels.py:1918): run zero-padded to 32 / 64 / 128
+    # next_pow2, kernels.py:1918): multiples of 8 run on the 32 / 64 / 128
+    # kernels with the columns past D masked
     q, k, v = qkv(1, 4, 2, T, D, torch.bfloat16, seed=D + T)
     o, _ = check_forward(q, k, v)
     assert o.is_contiguous() and o.shape == (1, 4, T, D)
@@ -168,7 +169,7 @@ def test_forward_head_dim_256(dtype, T):
 
 @pytest.mark.parametrize("D", [160, 200])
 def test_forward_head_dims_above_128(D):
-    # head dims 129..255 run zero-padded to 256
+    # head dims 129..255 run on the D = 256 kernels with the columns past D masked
     q, k, v = qkv(1, 4, 4, 150, D, torch.bfloat16, seed=D)
     o, _ = check_forward(q, k, v, exact=True)
     assert o.is_contiguous() and o.shape == (1, 4, 150, D)

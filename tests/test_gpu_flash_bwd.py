@@ -162,8 +162,8 @@ def test_backward_scales(scale):
 
 @pytest.mark.parametrize("D", [16, 48, 96])
 def test_backward_head_dims_below_128(D):
-    # head dims other than 32 / 64 / 128 run zero-padded; the padded columns
-    # of dQ, dK, dV are dropped
+    # head dims other than 32 / 64 / 128 run on the next kernel up with the
+    # columns past D masked (read as zero, not stored)
     grads, _ = check_backward(*inputs(1, 4, 2, 200, D, torch.bfloat16, seed=D))
     assert all(g.is_contiguous() and g.shape[-1] == D for g in grads)
 
@@ -171,7 +171,8 @@ def test_backward_head_dims_below_128(D):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("T", [1, 17, 100, 300])
 def test_backward_head_dim_256(dtype, T):
-    # D = 256 runs its own kernels; head dims 129..255 reach them zero-padded
+    # D = 256 runs its own kernels; head dims 129..255 run on them with the
+    # columns past D masked
     check_backward(*inputs(2, 4, 2, T, 256, dtype, seed=T + 256))
     check_backward(*inputs(1, 4, 1, T, 256, dtype, seed=T + 257), window=33)
 

@@ -136,7 +136,7 @@ def test_transpose16_bit_exact(rows, cols, dtype):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_rope_other_head_dims(D, dtype):
     # head dims other than 32 / 64 / 128: Q and K rotated by sa_rope_rotate,
-    # then the plain fused forward (D = 256 kernels, others zero-padded)
+    # then the plain fused forward (next kernel up, columns past D masked)
     check_rope(*inputs(2, 4, 2, 150, D, dtype, seed=D), window=0)
     check_rope(*inputs(1, 4, 4, 200, D, dtype, seed=D + 1, layout="bthd"), window=50)
 
