@@ -568,8 +568,8 @@ def _kernel_head_dim(D, dtype=None):
     and fp8: the next of the head dims their kernels are built for.  Where it
     differs from D, inputs are zero-padded and outputs sliced: zero columns
     add nothing to q.k, and the padded columns of O, dQ, dK, dV are dropped.
-    The reference takes any power of two through next_pow2 (kernels.py:1918)
-    and masks its loads past D."""
+    The reference computes at next_pow2(D) (kernels.py:1918) without masking
+    the columns past D."""
     dims = _FLASH_KERNEL_DIMS.get(dtype, _FLASH_HEAD_DIMS)
     if D < 1 or D > dims[-1]:
         raise ValueError(f"fused attention supports head dims 1..{dims[-1]}, got {D}")

@@ -3,7 +3,8 @@
 bf16 / fp16 head dims that are multiples of 8 in 8..256 run on the kernels
 built for 32, 64, 128 and 256, which read only the first D columns of every
 row and store only those (the reference computes at D_HEAD = next_pow2(D)
-with masked loads, kernels.py:1918 and :1560-1575).  Here every input is a
+and masks no column, kernels.py:1918 and :1572-1581, so for other head dims
+its loads run past each row).  Here every input is a
 view of a wider tensor whose columns past D hold NaN, so a read of any of
 them would turn the results into NaN, and every output is a view of a wider
 buffer holding a sentinel, which a store past D would change.  The calls go
