@@ -47,6 +47,11 @@ constexpr int kBwdKT = 64;    // keys per staged tile in the dQ kernel
 constexpr int kBwdBK = 128;   // key rows per dK/dV block (32 per wave)
 constexpr int kBwdQT = 64;    // query rows per staged tile in the dK/dV kernel
 constexpr int kBwdXcdSlots = 64;  // blocks one XCD runs at once (32 CUs x 2)
+// D = 128 dK/dV: the first 16-byte chunks of the wave's K and V operands
+// kept in LDS (a slot per lane) instead of registers; see
+// flash_bwd_dkdv_kernel.  4 KB of LDS per chunk and block: with two blocks
+// per CU (80 KB each) three chunks and half of a fourth fit, all from K.
+constexpr int kDkdvLdsK = 3, kDkdvLdsV = 0;
 
 struct BwdParams {
     const void* q;
@@ -393,8 +398,25 @@ __global__ __launch_bounds__(kBwdThreads, kBwdDkdvMinBlocks) void flash_bwd_dkdv
     using Vec = typename Ops::vec8;
     using Tl = SwzTile<D>;
     static_assert(kBwdQT == 64, "query tiles are 64 rows");
-    __shared__ __attribute__((aligned(1024))) unsigned char lds[2 * 2 * Tl::BYTES];  // [buf][Q, dO]
+    // The two ring stages ([Q, dO] each) are separate arrays, and the loop
+    // below is unrolled by two so that each iteration names its stages
+    // statically: the compiler then knows that the current stage's LDS reads
+    // do not touch the stage the next tile's DMA writes, and does not wait
+    // for that DMA before them.
+    __shared__ __attribute__((aligned(1024))) unsigned char lds0[2 * Tl::BYTES];
+    __shared__ __attribute__((aligned(1024))) unsigned char lds1[2 * Tl::BYTES];
     __shared__ __attribute__((aligned(16))) float ldr[2][2][kBwdQT];   // [buf][1/R, -delta]
+    // D = 128: the first NXK (NXV) chunks of the wave's K (V) operands, and
+    // the low half of K chunk NXK, live in LDS and are read again for every
+    // 32-query half.  The 128 accumulators plus all of K and V leave no room
+    // under 256 registers, and a compiler spill instead reloads from scratch
+    // inside the tile loop, where the wait for it (memory loads complete in
+    // order) also waits for the next tile's DMA.  (With fast square roots
+    // this leaves no spill; the exact-sqrt build keeps 12 bytes.)
+    constexpr int NXK = D == 128 ? kDkdvLdsK : 0, NXV = D == 128 ? kDkdvLdsV : 0;
+    __shared__ __attribute__((aligned(16))) u32x4 kvx[NXK + NXV > 0 ? NXK + NXV : 1][4][64];  // [K chunks, V chunks][wave][lane]
+    constexpr bool HALFX = D == 128;
+    __shared__ __attribute__((aligned(16))) uint2 kvh[HALFX ? 4 : 1][64];  // [wave][lane]: low 8 bytes of K chunk NXK
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -427,6 +449,11 @@ __global__ __launch_bounds__(kBwdThreads, kBwdDkdvMinBlocks) void flash_bwd_dkdv
         kreg[dc] = ldg16_cols<PART>(kp + krow * p.ks[2], dc * 16 + hi * 8, p.dr);
         vreg[dc] = ldg16_cols<PART>(vp + krow * p.vs[2], dc * 16 + hi * 8, p.dr);
     }
+#pragma unroll
+    for (int x = 0; x < NXK; ++x) kvx[x][wave][lane] = kreg[x];
+    if constexpr (HALFX) kvh[wave][lane] = uint2{kreg[NXK].x, kreg[NXK].y};
+#pragma unroll
+    for (int x = 0; x < NXV; ++x) kvx[NXK + x][wave][lane] = vreg[x];
 
     f32x16 dkacc[D / 32], dvacc[D / 32];
 #pragma unroll
@@ -449,7 +476,11 @@ __global__ __launch_bounds__(kBwdThreads, kBwdDkdvMinBlocks) void flash_bwd_dkdv
     const int dooff = swz_src_off<D, PART>(0, wave, lane, dsb, p.dr);
     float rst = 0.f;
     // Queries past T read as zeros; their weights are masked.
-    auto issue_tile = [&](int it, int buf) {
+    auto stage_base = [&](auto st) -> unsigned char* {
+        if constexpr (decltype(st)::value == 0) return lds0;
+        else return lds1;
+    };
+    auto issue_tile = [&](int it, auto st) {
         const int g = it / nq;
         const int qt = qt_begin + (it - g * nq);
         const int hq = hk * p.G + g;
@@ -459,15 +490,14 @@ __global__ __launch_bounds__(kBwdThreads, kBwdDkdvMinBlocks) void flash_bwd_dkdv
             reinterpret_cast<const unsigned char*>(static_cast<const T*>(p.dout) + b * p.dos[0] + hq * p.dos[1]));
         const int q0 = qt * kBwdQT;
         const int nrows = min(T_ - q0, kBwdQT);
-        issue_swz_tile<D>(qp + static_cast<int64_t>(q0) * qsb, qsb, nrows, lds + (2 * buf) * Tl::BYTES, wave, qoff);
-        issue_swz_tile<D>(dop + static_cast<int64_t>(q0) * dsb, dsb, nrows, lds + (2 * buf + 1) * Tl::BYTES, wave,
-                          dooff);
+        issue_swz_tile<D>(qp + static_cast<int64_t>(q0) * qsb, qsb, nrows, stage_base(st), wave, qoff);
+        issue_swz_tile<D>(dop + static_cast<int64_t>(q0) * dsb, dsb, nrows, stage_base(st) + Tl::BYTES, wave, dooff);
         // the raw row sum or delta, turned into 1/R or -delta only when it is
         // stored an iteration later, so this load's latency is not waited for here
-        if (tid < 2 * kBwdQT) {
-            const int r = tid & (kBwdQT - 1);
-            const int64_t idx = (static_cast<int64_t>(b) * p.Hq + hq) * T_ + min(q0 + r, T_ - 1);
-            rst = (tid < kBwdQT ? p.rs : p.delta)[idx];
+        // waves 0 and 1 (wave-uniform: the base pointer stays scalar)
+        if (wave < 2) {
+            const float* src = wave == 0 ? p.rs : p.delta;
+            rst = src[(static_cast<int64_t>(b) * p.Hq + hq) * T_ + min(q0 + lane, T_ - 1)];
         }
     };
     auto store_rs = [&](int buf) {
@@ -481,12 +511,13 @@ __global__ __launch_bounds__(kBwdThreads, kBwdDkdvMinBlocks) void flash_bwd_dkdv
     // which sees a key of the wave are skipped.  (One loop with the branch
     // inside keeps the 128 accumulator registers in place; separate loops
     // per tile kind made the compiler spill them.)
-    auto tile_step = [&](int it, int buf) {
+    auto tile_step = [&](int it, auto st) {
+        constexpr int buf = decltype(st)::value;
         const int g = it / nq;
         const int q0 = (qt_begin + (it - g * nq)) * kBwdQT;
         const bool interior = q0 >= wk0 + 31 && q0 + kBwdQT <= T_ && !(W > 0 && q0 + kBwdQT - 1 - wk0 >= W);
-        const unsigned char* Qb = lds + (2 * buf) * Tl::BYTES;
-        const unsigned char* Ob = lds + (2 * buf + 1) * Tl::BYTES;
+        const unsigned char* Qb = stage_base(st);
+        const unsigned char* Ob = stage_base(st) + Tl::BYTES;
 #pragma unroll
         for (int qh = 0; qh < 2; ++qh) {
             const int qh0 = q0 + qh * 32;
@@ -505,13 +536,22 @@ __global__ __launch_bounds__(kBwdThreads, kBwdDkdvMinBlocks) void flash_bwd_dkdv
                 dp[vg * 4 + 3] = nd.w;
             }
             const int r = qh * 32 + l32;
+            // re-read the LDS-held chunks for this half (not kept in registers across halves)
+            if constexpr (NXK + NXV > 0) asm volatile("" ::: "memory");
 #pragma unroll
             for (int dc = 0; dc < D / 16; ++dc) {
                 const int off = Tl::row_off(r, dc * 2 + hi);
                 const u32x4 qa = *reinterpret_cast<const u32x4*>(Qb + off);
                 const u32x4 oa = *reinterpret_cast<const u32x4*>(Ob + off);
-                s = Ops::mma(as_vec8<Vec>(qa), as_vec8<Vec>(kreg[dc]), s);
-                dp = Ops::mma(as_vec8<Vec>(oa), as_vec8<Vec>(vreg[dc]), dp);
+                u32x4 kb = dc < NXK ? kvx[dc < NXK ? dc : 0][wave][lane] : kreg[dc];
+                if (HALFX && dc == NXK) {
+                    const uint2 lo = kvh[wave][lane];
+                    kb.x = lo.x;
+                    kb.y = lo.y;
+                }
+                const u32x4 vb = dc < NXV ? kvx[dc < NXV ? NXK + dc : 0][wave][lane] : vreg[dc];
+                s = Ops::mma(as_vec8<Vec>(qa), as_vec8<Vec>(kb), s);
+                dp = Ops::mma(as_vec8<Vec>(oa), as_vec8<Vec>(vb), dp);
             }
             // C layout: column = key kj, rows = queries qh0 + (v/4)*8 + 4 hi + v%4.
             float pv[16], ds[16];
@@ -564,18 +604,24 @@ __global__ __launch_bounds__(kBwdThreads, kBwdDkdvMinBlocks) void flash_bwd_dkdv
             }
         }
     };
-    issue_tile(0, 0);
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    issue_tile(0, S0{});
     store_rs(0);
     wait_vmem();
     __syncthreads();
-    for (int it = 0; it < n_it; ++it) {
-        const int buf = it & 1;
+    // iteration it reads stage `cur` while the DMA fills stage `nxt` with it + 1
+    auto iteration = [&](int it, auto cur, auto nxt) {
         const bool has_next = it + 1 < n_it;
-        if (has_next) issue_tile(it + 1, buf ^ 1);
-        tile_step(it, buf);
-        if (has_next) store_rs(buf ^ 1);
+        if (has_next) issue_tile(it + 1, nxt);
+        tile_step(it, cur);
+        if (has_next) store_rs(decltype(nxt)::value);
         wait_vmem();
         __syncthreads();
+    };
+    for (int it = 0; it < n_it; it += 2) {
+        iteration(it, S0{}, S1{});
+        if (it + 1 < n_it) iteration(it + 1, S1{}, S0{});
     }
 
     // dS was kept without its factor 2 scale (1/R_i is already in).
