@@ -209,7 +209,12 @@ __global__ __launch_bounds__(kBwdThreads, 2) void flash_bwd_dq_kernel(BwdParams 
     using Ops = MfmaOps<T>;
     using Vec = typename Ops::vec8;
     using Tl = SwzTile<D>;
-    __shared__ __attribute__((aligned(1024))) unsigned char lds[2 * 2 * Tl::BYTES];  // [buf][K, V]
+    // The two ring stages ([K, V] each) are separate arrays and the tile loop
+    // is unrolled by two, so each tile names its stage statically: the
+    // compiler then knows that the current stage's LDS reads cannot touch the
+    // stage the next tile's DMA writes, and does not wait for that DMA first.
+    __shared__ __attribute__((aligned(1024))) unsigned char lds0[2 * Tl::BYTES];
+    __shared__ __attribute__((aligned(1024))) unsigned char lds1[2 * Tl::BYTES];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -280,30 +285,40 @@ __global__ __launch_bounds__(kBwdThreads, 2) void flash_bwd_dq_kernel(BwdParams 
     const int voff = swz_src_off<D, PART>(0, wave, lane, vsb, p.dr);
     // Keys past T read as zeros; they only meet masked weights (or rows
     // past T, whose dQ is not written).
-    auto issue_tile = [&](int j, int buf) {
+    auto stage_base = [&](auto st) -> unsigned char* {
+        if constexpr (decltype(st)::value == 0) return lds0;
+        else return lds1;
+    };
+    auto issue_tile = [&](int j, auto st) {
         const int k0 = j * kBwdKT;
         const int nrows = min(T_ - k0, kBwdKT);
-        issue_swz_tile<D>(kp + static_cast<int64_t>(k0) * ksb, ksb, nrows, lds + (2 * buf) * Tl::BYTES, wave, koff);
-        issue_swz_tile<D>(vp + static_cast<int64_t>(k0) * vsb, vsb, nrows, lds + (2 * buf + 1) * Tl::BYTES, wave,
-                          voff);
+        issue_swz_tile<D>(kp + static_cast<int64_t>(k0) * ksb, ksb, nrows, stage_base(st), wave, koff);
+        issue_swz_tile<D>(vp + static_cast<int64_t>(k0) * vsb, vsb, nrows, stage_base(st) + Tl::BYTES, wave, voff);
     };
 
-    // One key tile for the wave's 32 query rows.  MASK: some row of the
-    // wave has keys of the tile outside its causal window (or past a
-    // window edge); halves no row sees are skipped.
-    auto tile_step = [&](auto mask_tag, int j, int buf) {
-        constexpr bool MASK = decltype(mask_tag)::value;
+    // Interior tiles [ja, jb): every row of the wave sees every key (jb: the
+    // tiles ending at or before the wave's first row; ja: the first tile past
+    // the window edge of its last row).
+    int ja = kv_begin;
+    if (W > 0 && wq0 + 31 - W >= 0) ja = max(ja, (wq0 + 31 - W) / kBwdKT + 1);
+    ja = min(ja, kv_end);
+    const int jb = max(ja, min((wq0 + 1) / kBwdKT, kv_end));
+
+    // One key tile for the wave's 32 query rows.  Masked tiles (some row of
+    // the wave has keys of the tile outside its causal window or past a
+    // window edge; a wave-uniform branch) skip the halves no row sees and
+    // mask the rest.
+    auto tile_step = [&](int j, auto st) {
+        const bool masked = j < ja || j >= jb;
         const int k0 = j * kBwdKT;
-        const unsigned char* Kb = lds + (2 * buf) * Tl::BYTES;
-        const unsigned char* Vb = lds + (2 * buf + 1) * Tl::BYTES;
+        const unsigned char* Kb = stage_base(st);
+        const unsigned char* Vb = stage_base(st) + Tl::BYTES;
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
             const int kh0 = k0 + kt * 32;
-            if constexpr (MASK) {
-                // the wave's rows see some key of this half
-                const bool act = (kh0 <= wq0 + 31) && !(W > 0 && kh0 + 31 <= wq0 - W);
-                if (!act) continue;
-            }
+            // the wave's rows see some key of this half
+            const bool act = (kh0 <= wq0 + 31) && !(W > 0 && kh0 + 31 <= wq0 - W);
+            if (masked && !act) continue;
             // the dP^T chain starts at -delta (this lane's query), so it ends
             // holding dP - delta
             f32x16 s = f32x16{}, dp = ndl;
@@ -323,12 +338,13 @@ __global__ __launch_bounds__(kBwdThreads, 2) void flash_bwd_dq_kernel(BwdParams 
             for (int v = 0; v < 16; ++v) {
                 float y, rr;
                 weight_and_rr<EXACT>(s[v], sc, y, rr);
-                const float g = dp[v] * y * rr;
-                if constexpr (MASK) {
+                ds[v] = dp[v] * y * rr;
+            }
+            if (masked) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
                     const int cv = (v >> 2) * 8 + (v & 3);
-                    ds[v] = keep_if(static_cast<unsigned>(dbase - cv) < weff, g);
-                } else {
-                    ds[v] = g;
+                    ds[v] = keep_if(static_cast<unsigned>(dbase - cv) < weff, ds[v]);
                 }
             }
 #pragma unroll
@@ -346,30 +362,22 @@ __global__ __launch_bounds__(kBwdThreads, 2) void flash_bwd_dq_kernel(BwdParams 
             }
         }
     };
-    auto run_tile = [&](auto mask_tag, int j) {
-        const int buf = (j - kv_begin) & 1;
-        const bool has_next = j + 1 < kv_end;
-        if (has_next) issue_tile(j + 1, buf ^ 1);
-        tile_step(mask_tag, j, buf);
+    // tile j reads stage `cur` while the DMA fills the other with tile j + 1
+    auto run_tile = [&](int j, auto cur) {
+        if (j + 1 < kv_end) issue_tile(j + 1, std::integral_constant<int, 1 - decltype(cur)::value>{});
+        tile_step(j, cur);
         wait_vmem();
         __syncthreads();
     };
-
-    issue_tile(kv_begin, 0);
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    issue_tile(kv_begin, S0{});
     wait_vmem();
     __syncthreads();
-    // Interior tiles [ja, jb): every row of the wave sees every key (jb: the
-    // tiles ending at or before the wave's first row; ja: the first tile past
-    // the window edge of its last row).  Separate loops per kind keep the
-    // accumulators in fixed registers.
-    int ja = kv_begin;
-    if (W > 0 && wq0 + 31 - W >= 0) ja = max(ja, (wq0 + 31 - W) / kBwdKT + 1);
-    ja = min(ja, kv_end);
-    const int jb = max(ja, min((wq0 + 1) / kBwdKT, kv_end));
-    int j = kv_begin;
-    for (; j < ja; ++j) run_tile(std::true_type{}, j);
-    for (; j < jb; ++j) run_tile(std::false_type{}, j);
-    for (; j < kv_end; ++j) run_tile(std::true_type{}, j);
+    for (int j = kv_begin; j < kv_end; j += 2) {
+        run_tile(j, S0{});
+        if (j + 1 < kv_end) run_tile(j + 1, S1{});
+    }
 
     // dS was kept without its per-row factor 2 scale / R_i (applied here).
     if (qi < T_) {
