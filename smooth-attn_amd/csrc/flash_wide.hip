@@ -133,7 +133,16 @@ __global__ __launch_bounds__(64 * kFW) void flash_fwd_wide_kernel(WideParams<T> 
     constexpr int RPI = 64 * kFW / CPR;  // rows one round of kFW instructions covers
     constexpr int NKS = kFKT / 16;       // 16-key S^T subtiles per tile
     static_assert(NI == 1 || RPI % 16 == 0, "one swizzled offset per lane");
-    __shared__ __attribute__((aligned(1024))) unsigned char lds[2 * 2 * TB];  // [stage][K, V]
+    // Two ring stages ([K, V] each) in separate arrays, the tile loop unrolled
+    // by two: each tile names its stage statically, so the compiler knows its
+    // LDS reads cannot touch the stage the next tile's DMA writes and does
+    // not wait for that DMA first.
+    __shared__ __attribute__((aligned(1024))) unsigned char lds0[2 * TB];
+    __shared__ __attribute__((aligned(1024))) unsigned char lds1[2 * TB];
+    auto stage_base = [&](auto st) -> unsigned char* {
+        if constexpr (decltype(st)::value == 0) return lds0;
+        else return lds1;
+    };
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -182,10 +191,10 @@ __global__ __launch_bounds__(64 * kFW) void flash_fwd_wide_kernel(WideParams<T> 
     const int pch = (wave * 64 + lane) % CPR;
     const int koff = wide_src_off<true>(drow, pch ^ (drow & 15), krs, p.dr);
     const int voff = wide_src_off<true>(drow, pch ^ (2 * (drow & 7)), vrs, p.dr);
-    auto issue = [&](int t) {
+    auto issue = [&](int t, auto st) {
         const int k0 = t * kFKT;
         const int nrows = min(T_ - k0, kFKT);
-        unsigned char* lk = lds + ((t - kv_begin) & 1) * 2 * TB;
+        unsigned char* lk = stage_base(st);
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             const int skip = i * RPI;
@@ -207,10 +216,9 @@ __global__ __launch_bounds__(64 * kFW) void flash_fwd_wide_kernel(WideParams<T> 
     float ssum0 = 0.f, ssum1 = 0.f;
     const float c0 = -0.5f / sc, c2 = 1.f / (sc * sc);
 
-    auto tile = [&](auto mask_tag, int t) {
-        constexpr bool MASK = decltype(mask_tag)::value;
+    auto tile = [&](bool masked, int t, auto st) {
         const int k0 = t * kFKT;
-        const unsigned char* Kb = lds + ((t - kv_begin) & 1) * 2 * TB;
+        const unsigned char* Kb = stage_base(st);
         const unsigned char* Vb = Kb + TB;
         f32x4 s[NKS];
 #pragma unroll
@@ -237,11 +245,18 @@ __global__ __launch_bounds__(64 * kFW) void flash_fwd_wide_kernel(WideParams<T> 
                 } else {
                     w = sp2_weight<EXACT>(__builtin_fmaf(s[kst][e], sc, -0.5f));
                 }
-                if constexpr (MASK) w = keep_if(static_cast<unsigned>(dbase - 16 * kst - e) < weff, w);
                 y[4 * kst + e] = w;
-                if (e & 1) ssum1 += w;
-                else ssum0 += w;
             }
+        }
+        if (masked) {
+#pragma unroll
+            for (int i = 0; i < 4 * NKS; ++i)
+                y[i] = keep_if(static_cast<unsigned>(dbase - 16 * (i / 4) - i % 4) < weff, y[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4 * NKS; ++i) {
+            if (i & 1) ssum1 += y[i];
+            else ssum0 += y[i];
         }
 #pragma unroll
         for (int kk = 0; kk < kFKT / 32; ++kk) {
@@ -262,18 +277,11 @@ __global__ __launch_bounds__(64 * kFW) void flash_fwd_wide_kernel(WideParams<T> 
     // publishes it.  Waves run only the tiles their rows see (masks only where
     // some pair is outside the causal window or past a window edge) but take
     // every barrier.
-    issue(kv_begin);
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    issue(kv_begin, S0{});
     wide_wait_vmem();
     __syncthreads();
-    auto begin_t = [&](int t) {
-        if (t + 1 < kv_end) issue(t + 1);
-    };
-    auto end_t = [&](int t) {
-        if (t + 1 < kv_end) {
-            wide_wait_vmem();
-            __syncthreads();
-        }
-    };
     const int wf = q0w, wl = q0w + 15;  // the wave's query rows
     int t_first = kv_begin;
     if (W > 0 && wf - W + 1 > 0) t_first = max(t_first, (wf - W + 1) / kFKT);
@@ -281,29 +289,20 @@ __global__ __launch_bounds__(64 * kFW) void flash_fwd_wide_kernel(WideParams<T> 
     int ja = t_first;
     if (W > 0 && wl - W >= 0) ja = max(ja, (wl - W) / kFKT + 1);
     const int jb = (wf + 1) / kFKT;
-    int t = kv_begin;
-    for (; t < t_first; ++t) {
-        begin_t(t);
-        end_t(t);
-    }
-    for (; t <= t_last && t < ja; ++t) {
-        begin_t(t);
-        tile(std::true_type{}, t);
-        end_t(t);
-    }
-    for (; t <= t_last && t < jb; ++t) {
-        begin_t(t);
-        tile(std::false_type{}, t);
-        end_t(t);
-    }
-    for (; t <= t_last; ++t) {
-        begin_t(t);
-        tile(std::true_type{}, t);
-        end_t(t);
-    }
-    for (; t < kv_end; ++t) {
-        begin_t(t);
-        end_t(t);
+    // Tile t (stage (t - kv_begin) & 1) runs while the DMA fills the other
+    // stage with tile t + 1.  Waves run only the tiles their rows see, masked
+    // outside [ja, jb), but take every barrier.
+    auto run_tile = [&](int t, auto cur) {
+        if (t + 1 < kv_end) issue(t + 1, std::integral_constant<int, 1 - decltype(cur)::value>{});
+        if (t >= t_first && t <= t_last) tile(t < ja || t >= jb, t, cur);
+        if (t + 1 < kv_end) {
+            wide_wait_vmem();
+            __syncthreads();
+        }
+    };
+    for (int t = kv_begin; t < kv_end; t += 2) {
+        run_tile(t, S0{});
+        if (t + 1 < kv_end) run_tile(t + 1, S1{});
     }
 
     // row sums: lanes i16, i16 + 16, + 32, + 48 hold the four key groups of query qi
@@ -348,7 +347,16 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_dq_wide_kernel(WideParams<
     constexpr int RPI = 64 * kFW / CPR;
     constexpr int NKS = kFKT / 16;
     static_assert(NI == 1 || RPI % 16 == 0, "one swizzled offset per lane");
-    __shared__ __attribute__((aligned(1024))) unsigned char lds[2 * 2 * TB];  // [stage][K, V]
+    // Two ring stages ([K, V] each) in separate arrays, the tile loop unrolled
+    // by two: each tile names its stage statically, so the compiler knows its
+    // LDS reads cannot touch the stage the next tile's DMA writes and does
+    // not wait for that DMA first.
+    __shared__ __attribute__((aligned(1024))) unsigned char lds0[2 * TB];
+    __shared__ __attribute__((aligned(1024))) unsigned char lds1[2 * TB];
+    auto stage_base = [&](auto st) -> unsigned char* {
+        if constexpr (decltype(st)::value == 0) return lds0;
+        else return lds1;
+    };
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -408,10 +416,10 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_dq_wide_kernel(WideParams<
     const int pch = (wave * 64 + lane) % CPR;
     const int koff = wide_src_off<PART>(drow, pch ^ fk_swz(drow), krs, p.dr);
     const int voff = wide_src_off<PART>(drow, pch ^ (drow & 15), vrs, p.dr);
-    auto issue = [&](int t) {
+    auto issue = [&](int t, auto st) {
         const int k0 = t * kFKT;
         const int nrows = min(T_ - k0, kFKT);
-        unsigned char* lk = lds + ((t - kv_begin) & 1) * 2 * TB;
+        unsigned char* lk = stage_base(st);
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             const int skip = i * RPI;
@@ -435,10 +443,9 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_dq_wide_kernel(WideParams<
     for (int dt = 0; dt < D / 16; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     const f32x4 ndl{-dl, -dl, -dl, -dl};
 
-    auto tile = [&](auto mask_tag, int t) {
-        constexpr bool MASK = decltype(mask_tag)::value;
+    auto tile = [&](bool masked, int t, auto st) {
         const int k0 = t * kFKT;
-        const unsigned char* Kb = lds + ((t - kv_begin) & 1) * 2 * TB;
+        const unsigned char* Kb = stage_base(st);
         const unsigned char* Vb = Kb + TB;
         f32x4 s[NKS], dp[NKS];
 #pragma unroll
@@ -465,9 +472,13 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_dq_wide_kernel(WideParams<
             for (int e = 0; e < 4; ++e) {
                 float y, rr;
                 weight_rr16<EXACT>(s[kst][e], sc, y, rr);
-                const float x = dp[kst][e] * y * rr;
-                ds[4 * kst + e] = MASK ? keep_if(static_cast<unsigned>(dbase - 16 * kst - e) < weff, x) : x;
+                ds[4 * kst + e] = dp[kst][e] * y * rr;
             }
+        }
+        if (masked) {
+#pragma unroll
+            for (int i = 0; i < 4 * NKS; ++i)
+                ds[i] = keep_if(static_cast<unsigned>(dbase - 16 * (i / 4) - i % 4) < weff, ds[i]);
         }
 #pragma unroll
         for (int kk = 0; kk < kFKT / 32; ++kk) {
@@ -483,18 +494,11 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_dq_wide_kernel(WideParams<
         }
     };
 
-    issue(kv_begin);
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    issue(kv_begin, S0{});
     wide_wait_vmem();
     __syncthreads();
-    auto begin_t = [&](int t) {
-        if (t + 1 < kv_end) issue(t + 1);
-    };
-    auto end_t = [&](int t) {
-        if (t + 1 < kv_end) {
-            wide_wait_vmem();
-            __syncthreads();
-        }
-    };
     const int wf = q0w, wl = q0w + 15;
     int t_first = kv_begin;
     if (W > 0 && wf - W + 1 > 0) t_first = max(t_first, (wf - W + 1) / kFKT);
@@ -502,29 +506,20 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_dq_wide_kernel(WideParams<
     int ja = t_first;
     if (W > 0 && wl - W >= 0) ja = max(ja, (wl - W) / kFKT + 1);
     const int jb = (wf + 1) / kFKT;
-    int t = kv_begin;
-    for (; t < t_first; ++t) {
-        begin_t(t);
-        end_t(t);
-    }
-    for (; t <= t_last && t < ja; ++t) {
-        begin_t(t);
-        tile(std::true_type{}, t);
-        end_t(t);
-    }
-    for (; t <= t_last && t < jb; ++t) {
-        begin_t(t);
-        tile(std::false_type{}, t);
-        end_t(t);
-    }
-    for (; t <= t_last; ++t) {
-        begin_t(t);
-        tile(std::true_type{}, t);
-        end_t(t);
-    }
-    for (; t < kv_end; ++t) {
-        begin_t(t);
-        end_t(t);
+    // Tile t (stage (t - kv_begin) & 1) runs while the DMA fills the other
+    // stage with tile t + 1.  Waves run only the tiles their rows see, masked
+    // outside [ja, jb), but take every barrier.
+    auto run_tile = [&](int t, auto cur) {
+        if (t + 1 < kv_end) issue(t + 1, std::integral_constant<int, 1 - decltype(cur)::value>{});
+        if (t >= t_first && t <= t_last) tile(t < ja || t >= jb, t, cur);
+        if (t + 1 < kv_end) {
+            wide_wait_vmem();
+            __syncthreads();
+        }
+    };
+    for (int t = kv_begin; t < kv_end; t += 2) {
+        run_tile(t, S0{});
+        if (t + 1 < kv_end) run_tile(t + 1, S1{});
     }
     // dS carried without its per-row factor 2 scale / R
     if (qi < T_) {
@@ -559,7 +554,16 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_kv_wide_kernel(WideParams<
     constexpr int RPI = 64 * kFW / CPR;
     constexpr int NQS = kFKT / 16;      // 16-query subtiles per tile
     static_assert(NI == 1 || RPI % 16 == 0, "one swizzled offset per lane");
-    __shared__ __attribute__((aligned(1024))) unsigned char lds[2 * 2 * TB];  // [stage][Q, dO]
+    // Two ring stages ([Q, dO] each) in separate arrays, the tile loop
+    // unrolled by two: each tile names its stage statically, so the compiler
+    // knows its LDS reads cannot touch the stage the next tile's DMA writes
+    // and does not wait for that DMA first.
+    __shared__ __attribute__((aligned(1024))) unsigned char lds0[2 * TB];
+    __shared__ __attribute__((aligned(1024))) unsigned char lds1[2 * TB];
+    auto stage_base = [&](auto st) -> unsigned char* {
+        if constexpr (decltype(st)::value == 0) return lds0;
+        else return lds1;
+    };
     __shared__ __attribute__((aligned(16))) float ldr[2][2][kFKT];            // [stage][1/R, -delta]
 
     const int tid = threadIdx.x;
@@ -617,13 +621,13 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_kv_wide_kernel(WideParams<
         q0 = (qt_begin + it - gg * nq) * kFKT;
         hq = hk * p.G + gg;
     };
-    auto issue = [&](int it) {
+    auto issue = [&](int it, auto st) {
         int hq, q0;
         tile_of(it, hq, q0);
         const unsigned char* qp = wide_uniform_ptr(reinterpret_cast<const unsigned char*>(p.q + b * p.qs[0] + hq * p.qs[1]));
         const unsigned char* op = wide_uniform_ptr(reinterpret_cast<const unsigned char*>(p.dout + b * p.dos[0] + hq * p.dos[1]));
         const int nrows = min(T_ - q0, kFKT);
-        unsigned char* lq = lds + (it & 1) * 2 * TB;
+        unsigned char* lq = stage_base(st);
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             const int skip = i * RPI;
@@ -641,7 +645,10 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_kv_wide_kernel(WideParams<
         int hq, q0;
         tile_of(it, hq, q0);
         const int64_t idx = (static_cast<int64_t>(b) * p.Hq + hq) * T_ + min(q0 + (tid & (kFKT - 1)), T_ - 1);
-        return tid < kFKT ? p.rs[idx] : (tid < 2 * kFKT ? p.delta[idx] : 0.f);
+        // waves 0 and 1 (wave-uniform: the base pointer stays scalar)
+        if (wave == 0) return p.rs[idx];
+        if (wave == 1) return p.delta[idx];
+        return 0.f;
     };
     auto store_rv = [&](int st, float raw) {
         if (tid < 2 * kFKT) ldr[st][tid / kFKT][tid & (kFKT - 1)] = tid < kFKT ? 1.f / raw : -raw;
@@ -655,13 +662,12 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_kv_wide_kernel(WideParams<
     const int trsw = tsw >> 1;
     const int qsi = qswz(i16), osi = oswz(i16);
 
-    auto tile = [&](auto mask_tag, int it) {
-        constexpr bool MASK = decltype(mask_tag)::value;
+    auto tile = [&](bool masked, int it, auto stage) {
+        constexpr int st = decltype(stage)::value;
         int hq, q0;
         tile_of(it, hq, q0);
         (void)hq;
-        const int st = it & 1;
-        const unsigned char* Qb = lds + st * 2 * TB;
+        const unsigned char* Qb = stage_base(stage);
         const unsigned char* Ob = Qb + TB;
         float x[4 * NQS];
 #pragma unroll
@@ -694,11 +700,14 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_kv_wide_kernel(WideParams<
                 float v;
                 if constexpr (DK) v = dp[e] * yi * rr;  // dS (without 2 scale)
                 else v = yi;                            // P
-                if constexpr (MASK) {
-                    const int q = q0 + 16 * qst + 4 * g + e;
-                    v = keep_if(static_cast<unsigned>(q - kj) < weff && q < T_, v);
-                }
                 x[4 * qst + e] = v;
+            }
+        }
+        if (masked) {
+#pragma unroll
+            for (int i = 0; i < 4 * NQS; ++i) {
+                const int q = q0 + 16 * (i / 4) + 4 * g + i % 4;
+                x[i] = keep_if(static_cast<unsigned>(q - kj) < weff && q < T_, x[i]);
             }
         }
         const unsigned char* Tb = DK ? Qb : Ob;
@@ -716,15 +725,19 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_kv_wide_kernel(WideParams<
         }
     };
 
-    issue(0);
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    issue(0, S0{});
     store_rv(0, row_value(0));
     wide_wait_vmem();
     __syncthreads();
-    for (int it = 0; it < n_it; ++it) {
+    // iteration it reads stage it & 1 while the DMA fills the other with it + 1
+    auto step = [&](int it, auto cur) {
+        constexpr int nxt = 1 - decltype(cur)::value;
         const bool more = it + 1 < n_it;
         float rnext = 0.f;
         if (more) {
-            issue(it + 1);  // into the stage of it - 1, free since the barrier that ended it - 1
+            issue(it + 1, std::integral_constant<int, nxt>{});  // free since the barrier that ended it - 1
             rnext = row_value(it + 1);
         }
         int hq, q0;
@@ -732,13 +745,16 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_kv_wide_kernel(WideParams<
         // wave-uniform: some (query, key) pair of the tile is visible; all are
         const bool active = q0 + kFKT - 1 >= wk0 && q0 < T_ && !(W > 0 && q0 - (wk0 + 15) >= W);
         const bool interior = q0 >= wk0 + 15 && q0 + kFKT <= T_ && !(W > 0 && q0 + kFKT - 1 - wk0 >= W);
-        if (interior) tile(std::false_type{}, it);
-        else if (active) tile(std::true_type{}, it);
+        if (active) tile(!interior, it, cur);
         if (more) {
-            store_rv((it + 1) & 1, rnext);
+            store_rv(nxt, rnext);
             wide_wait_vmem();
             __syncthreads();
         }
+    };
+    for (int it = 0; it < n_it; it += 2) {
+        step(it, S0{});
+        if (it + 1 < n_it) step(it + 1, S1{});
     }
     if (kj < T_) {
         T* row = DK ? p.dk + b * p.dks[0] + hk * p.dks[1] + kj * p.dks[2] : p.dv + b * p.dvs[0] + hk * p.dvs[1] + kj * p.dvs[2];
