@@ -20,14 +20,18 @@
 //    MFMA with K, V from LDS, dS^T on the VALU, then dQ^T += K^T dS^T with
 //    K^T read from the same LDS tile by the transposing LDS load.
 //  * flash_bwd_dkdv_kernel: a block of 4 waves owns 128 key rows of one
-//    (batch, KV head); wave w owns keys [32w, 32w+32) and keeps K, V of them
-//    in registers.  It walks every query head of the GQA group and every
+//    (batch, KV head); wave w owns keys [32w, 32w+32) and keeps V and most of
+//    K of them in registers (at D = 128 the first three and a half 16-byte
+//    chunks of K live in LDS, a slot per lane).  It walks every query head of the GQA group and every
 //    query tile of 64 rows that sees its keys: S = Q K^T and dP = dO V^T with
 //    Q, dO from LDS, P and dS on the VALU (their C layout is the B operand of
 //    the next products), then dV^T += dO^T P and dK^T += Q^T dS with dO^T,
 //    Q^T from the transposing LDS load.
 // Tiles go straight from global memory into LDS (global_load_lds, double
-// buffered, one barrier per tile), as in the forward.
+// buffered, one barrier per tile), as in the forward.  The two stages are
+// separate LDS arrays and the tile loops are unrolled by two, so a tile's LDS
+// reads never wait for the DMA filling the other stage (the compiler waits
+// for an in-flight direct-to-LDS load before any read of the same array).
 #include "flash_common.hpp"
 #include "flash_tiles.hpp"
 #include "flash_f32.hpp"

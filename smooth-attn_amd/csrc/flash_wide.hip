@@ -1,6 +1,7 @@
 // 16-bit (bf16 / fp16) fused causal squareplus attention at head dim 256,
-// forward and backward, on v_mfma_f32_32x32x16_{bf16,f16}.  Head dims
-// 129..255 reach it zero-padded.
+// forward and backward, on v_mfma_f32_16x16x32_{bf16,f16}.  Head dims
+// 136..248 (multiples of 8) run on the same kernels with the columns past
+// them read as zeros and not stored.
 //
 // Same mathematics and rounding points as the D <= 128 kernels
 // (flash_fwd.hip, flash_bwd.hip; reference kernels.py:1536-1631 and
@@ -12,9 +13,11 @@
 // 16 rows (16 tiles of 16 x 16, 64 registers per lane) leave room for two
 // waves per SIMD, where 32 rows on the 32x32x16 MFMA would need one wave per
 // SIMD.  Blocks of 8 waves own 128 rows and walk 64-row tiles of the other
-// side through a 2-stage LDS ring (2 x 64 KB) filled by direct-to-LDS loads,
-// one barrier per tile.  dK and dV are separate kernels (both accumulators
-// plus the K and V operands would not fit two waves per SIMD).
+// side through a 2-stage LDS ring (two 64 KB arrays) filled by direct-to-LDS
+// loads, one barrier per tile; the tile loops are unrolled by two so each
+// tile names its stage statically and its LDS reads never wait for the DMA
+// filling the other stage.  dK and dV are separate kernels (both
+// accumulators plus the K and V operands would not fit two waves per SIMD).
 //
 // 16x16x32 operands: A lane l holds row l % 16, k = 8 (l / 16) .. +7; B column
 // l % 16, the same k; C column l % 16, rows 4 (l / 16) .. +3.  For
