@@ -74,10 +74,6 @@ struct BwdParams {
     float scale;
 };
 
-// DMA offset past every tile's buffer resource (at most 64 rows of 2^24
-// bytes): the lane's 16 bytes load as zeros.
-constexpr int kPastTile = 0x7FFFFFF0;
-
 // Plain (cached) 16-byte global load: tiles here are re-read by many blocks.
 __device__ __forceinline__ u32x4 ldg16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 

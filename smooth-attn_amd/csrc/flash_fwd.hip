@@ -60,10 +60,6 @@ struct FlashParams {
     float scale;
 };
 
-// DMA offset past every tile's buffer resource (at most 64 rows of 2^24
-// bytes): the lane's 16 bytes load as zeros.
-constexpr int kPastTile = 0x7FFFFFF0;
-
 // T: 16-bit type of P V (and of q/k/v unless fp8).  QK8: q, k are e4m3fn.
 // V8: v is e4m3fn.
 //

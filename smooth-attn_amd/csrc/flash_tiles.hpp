@@ -14,6 +14,12 @@ __device__ __forceinline__ void wide_dma16(__amdgpu_buffer_rsrc_t rs, int voff, 
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (wide_lds_void_t*)(lds_base), 16, voff, 0, 0, 0);
 }
 
+// Per-lane byte offset past the buffer resource of every tile the attention
+// kernels load (their tiles span at most 64 rows of under 2^25 bytes, so a
+// resource holds at most 2^31 - 1024 bytes): the lane's load returns zeros.
+// Lanes whose 16-byte chunk lies past the tensors' head dim take it.
+constexpr int kPastTile = 0x7FFFFFF0;
+
 // s_waitcnt vmcnt(0): this wave's direct-to-LDS loads have landed.
 __device__ __forceinline__ void wide_wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 

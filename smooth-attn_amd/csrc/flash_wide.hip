@@ -60,10 +60,6 @@ struct WideParams {
     float scale;
 };
 
-// DMA offset past every tile's buffer resource (64 rows, under 2^31 bytes):
-// the lane's 16 bytes load as zeros.
-constexpr int kPastTile = 0x7FFFFFF0;
-
 // 16 bytes of columns d0 .. d0 + 7 of a row; PART (head dim dr below the
 // kernel's D): zeros where they lie past dr (the load then reads column 0).
 template <bool PART, typename T>
