@@ -127,31 +127,6 @@ __device__ __forceinline__ Vec tr_operand(const unsigned char* p, int lane, int 
     return lds_read_tr16_pair<Vec>(p + Tl::tr_off(lane, dt, 0), p + Tl::tr_off(lane, dt, 1));
 }
 
-typedef __attribute__((address_space(3))) void bwd_lds_void_t;
-
-// Buffer resource over the nbytes bytes from base (raw, no stride): loads at
-// or past nbytes return zeros.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t bwd_rsrc(const void* base, int nbytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, nbytes, 0x00020000);
-}
-
-// One 16-byte buffer -> LDS load per lane: lane i writes bytes [16 i, 16 i + 16)
-// after lds_base (wave-uniform), read from byte voff of the resource.
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, int voff, void* lds_base) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (bwd_lds_void_t*)(lds_base), 16, voff, 0, 0, 0);
-}
-
-// p, computed from wave-uniform values, as a scalar.
-__device__ __forceinline__ const unsigned char* bwd_uniform_ptr(const unsigned char* p) {
-    const uint64_t u = reinterpret_cast<uint64_t>(p);
-    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
-    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
-    return reinterpret_cast<const unsigned char*>((static_cast<uint64_t>(hi) << 32) | lo);
-}
-
-// s_waitcnt vmcnt(0): this wave's direct-to-LDS loads have landed.
-__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-
 // Byte offset (from the tile's first row, row stride rsb) of the source of
 // this lane's DMA load i of a swizzled [64][D] tile: LDS slot s = (4 i +
 // wave) * 64 + lane holds row s / CPR, logical chunk (s % CPR) ^ f(row);
@@ -184,8 +159,8 @@ __device__ __forceinline__ void issue_swz_tile(const unsigned char* base, int rs
 #pragma unroll
     for (int i = 0; i < Tl::NI; ++i) {
         const int skip = i * kRowsPerLoad * rsb;
-        const __amdgpu_buffer_rsrc_t rs = bwd_rsrc(base + skip, max(nbytes - skip, 0));
-        dma16(rs, lane_off, dst + (i * 4 + wave) * 64 * 16);
+        const __amdgpu_buffer_rsrc_t rs = tile_rsrc(base + skip, max(nbytes - skip, 0));
+        tile_dma16(rs, lane_off, dst + (i * 4 + wave) * 64 * 16);
     }
 }
 
@@ -234,9 +209,9 @@ __global__ __launch_bounds__(kBwdThreads, 2) void flash_bwd_dq_kernel(BwdParams 
 
     const T* qp = static_cast<const T*>(p.q) + b * p.qs[0] + hq * p.qs[1];
     const unsigned char* kp =
-        bwd_uniform_ptr(reinterpret_cast<const unsigned char*>(static_cast<const T*>(p.k) + b * p.ks[0] + hk * p.ks[1]));
+        tile_uniform_ptr(reinterpret_cast<const unsigned char*>(static_cast<const T*>(p.k) + b * p.ks[0] + hk * p.ks[1]));
     const unsigned char* vp =
-        bwd_uniform_ptr(reinterpret_cast<const unsigned char*>(static_cast<const T*>(p.v) + b * p.vs[0] + hk * p.vs[1]));
+        tile_uniform_ptr(reinterpret_cast<const unsigned char*>(static_cast<const T*>(p.v) + b * p.vs[0] + hk * p.vs[1]));
     const T* op = static_cast<const T*>(p.o) + b * p.os[0] + hq * p.os[1];
     const T* dop = static_cast<const T*>(p.dout) + b * p.dos[0] + hq * p.dos[1];
     T* dqp = static_cast<T*>(p.dq) + b * p.dqs[0] + hq * p.dqs[1];
@@ -366,13 +341,13 @@ __global__ __launch_bounds__(kBwdThreads, 2) void flash_bwd_dq_kernel(BwdParams 
     auto run_tile = [&](int j, auto cur) {
         if (j + 1 < kv_end) issue_tile(j + 1, std::integral_constant<int, 1 - decltype(cur)::value>{});
         tile_step(j, cur);
-        wait_vmem();
+        tile_wait_vmem();
         __syncthreads();
     };
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
     issue_tile(kv_begin, S0{});
-    wait_vmem();
+    tile_wait_vmem();
     __syncthreads();
     for (int j = kv_begin; j < kv_end; j += 2) {
         run_tile(j, S0{});
@@ -492,9 +467,9 @@ __global__ __launch_bounds__(kBwdThreads, kBwdDkdvMinBlocks) void flash_bwd_dkdv
         const int g = it / nq;
         const int qt = qt_begin + (it - g * nq);
         const int hq = hk * p.G + g;
-        const unsigned char* qp = bwd_uniform_ptr(
+        const unsigned char* qp = tile_uniform_ptr(
             reinterpret_cast<const unsigned char*>(static_cast<const T*>(p.q) + b * p.qs[0] + hq * p.qs[1]));
-        const unsigned char* dop = bwd_uniform_ptr(
+        const unsigned char* dop = tile_uniform_ptr(
             reinterpret_cast<const unsigned char*>(static_cast<const T*>(p.dout) + b * p.dos[0] + hq * p.dos[1]));
         const int q0 = qt * kBwdQT;
         const int nrows = min(T_ - q0, kBwdQT);
@@ -616,7 +591,7 @@ __global__ __launch_bounds__(kBwdThreads, kBwdDkdvMinBlocks) void flash_bwd_dkdv
     using S1 = std::integral_constant<int, 1>;
     issue_tile(0, S0{});
     store_rs(0);
-    wait_vmem();
+    tile_wait_vmem();
     __syncthreads();
     // iteration it reads stage `cur` while the DMA fills stage `nxt` with it + 1
     auto iteration = [&](int it, auto cur, auto nxt) {
@@ -624,7 +599,7 @@ __global__ __launch_bounds__(kBwdThreads, kBwdDkdvMinBlocks) void flash_bwd_dkdv
         if (has_next) issue_tile(it + 1, nxt);
         tile_step(it, cur);
         if (has_next) store_rs(decltype(nxt)::value);
-        wait_vmem();
+        tile_wait_vmem();
         __syncthreads();
     };
     for (int it = 0; it < n_it; it += 2) {

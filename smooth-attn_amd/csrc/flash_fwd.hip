@@ -97,32 +97,6 @@ struct Geom {
     static __device__ __forceinline__ int swz_v(int r) { return 4 * ((r / VRPW) & (VCPRL / 4 - 1)); }
 };
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) void glb_void_t;
-
-// Buffer resource over the nbytes bytes from base (raw, no stride): loads at
-// or past nbytes return zeros.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, int nbytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, nbytes, 0x00020000);
-}
-
-// One 16-byte buffer -> LDS load per lane: lane i writes bytes [16 i, 16 i + 16)
-// after lds_base (wave-uniform), read from byte voff of the resource.
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, int voff, void* lds_base) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(lds_base), 16, voff, 0, 0, 0);
-}
-
-// p, computed from wave-uniform values, as a scalar.
-__device__ __forceinline__ const unsigned char* uniform_ptr(const unsigned char* p) {
-    const uint64_t u = reinterpret_cast<uint64_t>(p);
-    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
-    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
-    return reinterpret_cast<const unsigned char*>((static_cast<uint64_t>(hi) << 32) | lo);
-}
-
-// s_waitcnt vmcnt(0): this wave's direct-to-LDS loads have landed.
-__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-
 // e4m3 x e4m3 with block scales 2^(ea-127) and 2^(eb-127) (E8M0; 127 =
 // 2^0): D = 2^(ea+eb-254) sum a b + C, the power of two applied exactly.
 __device__ __forceinline__ f32x16 mma_fp8(i32x8 a, i32x8 b, f32x16 c, int ea, int eb) {
@@ -300,9 +274,9 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashParams p) {
     const unsigned char* qp = static_cast<const unsigned char*>(p.q) + (b * p.qs[0] + hq * p.qs[1]) * Gm::QKB;
     // head bases as scalars (the tile loads build scalar resources from them)
     const unsigned char* kp =
-        uniform_ptr(static_cast<const unsigned char*>(p.k) + (b * p.ks[0] + hk * p.ks[1]) * Gm::QKB);
+        tile_uniform_ptr(static_cast<const unsigned char*>(p.k) + (b * p.ks[0] + hk * p.ks[1]) * Gm::QKB);
     const unsigned char* vp =
-        uniform_ptr(static_cast<const unsigned char*>(p.v) + (b * p.vs[0] + hk * p.vs[1]) * (V8 ? 1 : 2));
+        tile_uniform_ptr(static_cast<const unsigned char*>(p.v) + (b * p.vs[0] + hk * p.vs[1]) * (V8 ? 1 : 2));
     T* op = static_cast<T*>(p.o) + b * p.os[0] + hq * p.os[1];
     const int64_t qrs = p.qs[2] * Gm::QKB;  // row strides in bytes
     const int64_t krs = p.ks[2] * Gm::QKB;
@@ -424,7 +398,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashParams p) {
             const int sbase = (i * kWaves + wave) * 64;
             if ((kBKV * Gm::KCPR) % kThreads == 0 || sbase < kBKV * Gm::KCPR) {
                 const int skip = i * kKRows * static_cast<int>(krs);
-                dma16(tile_rsrc(kp + static_cast<int64_t>(k0) * krs + skip, max(kbytes - skip, 0)), koff,
+                tile_dma16(tile_rsrc(kp + static_cast<int64_t>(k0) * krs + skip, max(kbytes - skip, 0)), koff,
                       ldsK + buf * Gm::KT + sbase * 16);
             }
         }
@@ -435,7 +409,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashParams p) {
                 const int sbase = (i * kWaves + wave) * 64;
                 if ((kBKV * Gm::VCPRL) % kThreads == 0 || sbase < kBKV * Gm::VCPRL) {
                     const int skip = i * kVRows * static_cast<int>(vrs);
-                    dma16(tile_rsrc(vp + static_cast<int64_t>(k0) * vrs + skip, max(vbytes - skip, 0)), voff,
+                    tile_dma16(tile_rsrc(vp + static_cast<int64_t>(k0) * vrs + skip, max(vbytes - skip, 0)), voff,
                           ldsVb + buf * Gm::VT + sbase * 16);
                 }
             }
@@ -622,7 +596,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashParams p) {
     // calls this exactly once per tile of the block, active or not.
     auto boundary = [&](int t) {
         if (t + 1 < kv_end) {
-            wait_vmem();
+            tile_wait_vmem();
             finish_tile(stage_of(t + 1));
             __syncthreads();
             if (t + 2 < kv_end) issue_tile(t + 2, stage_of(t + 2));
@@ -656,7 +630,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashParams p) {
     // Prologue: tile kv_begin staged and published, tile kv_begin + 1 in
     // flight.  kv_begin < kv_end for every block (q_start < T).
     issue_tile(kv_begin, 0);
-    wait_vmem();
+    tile_wait_vmem();
     finish_tile(0);
     __syncthreads();
     if (kv_begin + 1 < kv_end) issue_tile(kv_begin + 1, 1);

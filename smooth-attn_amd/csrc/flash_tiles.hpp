@@ -6,12 +6,18 @@
 
 namespace sa {
 
-typedef __attribute__((address_space(3))) void wide_lds_void_t;
+typedef __attribute__((address_space(3))) void tile_lds_void_t;
+
+// Buffer resource over the nbytes bytes from base (raw, no stride): loads at
+// or past nbytes return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, int nbytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, nbytes, 0x00020000);
+}
 
 // One 16-byte buffer -> LDS load per lane: lane i writes bytes [16 i, 16 i + 16)
 // after lds_base (wave-uniform), read from byte voff of the resource.
-__device__ __forceinline__ void wide_dma16(__amdgpu_buffer_rsrc_t rs, int voff, void* lds_base) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (wide_lds_void_t*)(lds_base), 16, voff, 0, 0, 0);
+__device__ __forceinline__ void tile_dma16(__amdgpu_buffer_rsrc_t rs, int voff, void* lds_base) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (tile_lds_void_t*)(lds_base), 16, voff, 0, 0, 0);
 }
 
 // Per-lane byte offset past the buffer resource of every tile the attention
@@ -21,10 +27,10 @@ __device__ __forceinline__ void wide_dma16(__amdgpu_buffer_rsrc_t rs, int voff, 
 constexpr int kPastTile = 0x7FFFFFF0;
 
 // s_waitcnt vmcnt(0): this wave's direct-to-LDS loads have landed.
-__device__ __forceinline__ void wide_wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+__device__ __forceinline__ void tile_wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // p, computed from wave-uniform values, as a scalar (buffer resources are built from it).
-__device__ __forceinline__ const unsigned char* wide_uniform_ptr(const unsigned char* p) {
+__device__ __forceinline__ const unsigned char* tile_uniform_ptr(const unsigned char* p) {
     const uint64_t u = reinterpret_cast<uint64_t>(p);
     const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
     const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));

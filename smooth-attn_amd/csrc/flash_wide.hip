@@ -157,8 +157,8 @@ __global__ __launch_bounds__(64 * kFW) void flash_fwd_wide_kernel(WideParams<T> 
     const int hk = unit - b * p.Hkv;
     const int hq = hk * p.G + sub;
 
-    const unsigned char* kp = wide_uniform_ptr(reinterpret_cast<const unsigned char*>(p.k + b * p.ks[0] + hk * p.ks[1]));
-    const unsigned char* vp = wide_uniform_ptr(reinterpret_cast<const unsigned char*>(p.v + b * p.vs[0] + hk * p.vs[1]));
+    const unsigned char* kp = tile_uniform_ptr(reinterpret_cast<const unsigned char*>(p.k + b * p.ks[0] + hk * p.ks[1]));
+    const unsigned char* vp = tile_uniform_ptr(reinterpret_cast<const unsigned char*>(p.v + b * p.vs[0] + hk * p.vs[1]));
     const int64_t krs = p.ks[2] * 2, vrs = p.vs[2] * 2;
 
     // waves w and w + 4 share a SIMD: the second four take the row slots in
@@ -197,10 +197,10 @@ __global__ __launch_bounds__(64 * kFW) void flash_fwd_wide_kernel(WideParams<T> 
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             const int skip = i * RPI;
-            wide_dma16(__builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(kp + (k0 + skip) * krs), 0,
+            tile_dma16(__builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(kp + (k0 + skip) * krs), 0,
                                                          max((nrows - skip) * static_cast<int>(krs), 0), 0x00020000),
                        koff, lk + (i * kFW + wave) * 1024);
-            wide_dma16(__builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(vp + (k0 + skip) * vrs), 0,
+            tile_dma16(__builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(vp + (k0 + skip) * vrs), 0,
                                                          max((nrows - skip) * static_cast<int>(vrs), 0), 0x00020000),
                        voff, lk + TB + (i * kFW + wave) * 1024);
         }
@@ -279,7 +279,7 @@ __global__ __launch_bounds__(64 * kFW) void flash_fwd_wide_kernel(WideParams<T> 
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
     issue(kv_begin, S0{});
-    wide_wait_vmem();
+    tile_wait_vmem();
     __syncthreads();
     const int wf = q0w, wl = q0w + 15;  // the wave's query rows
     int t_first = kv_begin;
@@ -295,7 +295,7 @@ __global__ __launch_bounds__(64 * kFW) void flash_fwd_wide_kernel(WideParams<T> 
         if (t + 1 < kv_end) issue(t + 1, std::integral_constant<int, 1 - decltype(cur)::value>{});
         if (t >= t_first && t <= t_last) tile(t < ja || t >= jb, t, cur);
         if (t + 1 < kv_end) {
-            wide_wait_vmem();
+            tile_wait_vmem();
             __syncthreads();
         }
     };
@@ -370,8 +370,8 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_dq_wide_kernel(WideParams<
     const int b = unit / p.Hkv;
     const int hk = unit - b * p.Hkv;
     const int hq = hk * p.G + sub;
-    const unsigned char* kp = wide_uniform_ptr(reinterpret_cast<const unsigned char*>(p.k + b * p.ks[0] + hk * p.ks[1]));
-    const unsigned char* vp = wide_uniform_ptr(reinterpret_cast<const unsigned char*>(p.v + b * p.vs[0] + hk * p.vs[1]));
+    const unsigned char* kp = tile_uniform_ptr(reinterpret_cast<const unsigned char*>(p.k + b * p.ks[0] + hk * p.ks[1]));
+    const unsigned char* vp = tile_uniform_ptr(reinterpret_cast<const unsigned char*>(p.v + b * p.vs[0] + hk * p.vs[1]));
     const int64_t krs = p.ks[2] * 2, vrs = p.vs[2] * 2;
 
     const int q_start = qb * kFRows;
@@ -422,10 +422,10 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_dq_wide_kernel(WideParams<
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             const int skip = i * RPI;
-            wide_dma16(__builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(kp + (k0 + skip) * krs), 0,
+            tile_dma16(__builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(kp + (k0 + skip) * krs), 0,
                                                          max((nrows - skip) * static_cast<int>(krs), 0), 0x00020000),
                        koff, lk + (i * kFW + wave) * 1024);
-            wide_dma16(__builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(vp + (k0 + skip) * vrs), 0,
+            tile_dma16(__builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(vp + (k0 + skip) * vrs), 0,
                                                          max((nrows - skip) * static_cast<int>(vrs), 0), 0x00020000),
                        voff, lk + TB + (i * kFW + wave) * 1024);
         }
@@ -496,7 +496,7 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_dq_wide_kernel(WideParams<
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
     issue(kv_begin, S0{});
-    wide_wait_vmem();
+    tile_wait_vmem();
     __syncthreads();
     const int wf = q0w, wl = q0w + 15;
     int t_first = kv_begin;
@@ -512,7 +512,7 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_dq_wide_kernel(WideParams<
         if (t + 1 < kv_end) issue(t + 1, std::integral_constant<int, 1 - decltype(cur)::value>{});
         if (t >= t_first && t <= t_last) tile(t < ja || t >= jb, t, cur);
         if (t + 1 < kv_end) {
-            wide_wait_vmem();
+            tile_wait_vmem();
             __syncthreads();
         }
     };
@@ -623,17 +623,17 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_kv_wide_kernel(WideParams<
     auto issue = [&](int it, auto st) {
         int hq, q0;
         tile_of(it, hq, q0);
-        const unsigned char* qp = wide_uniform_ptr(reinterpret_cast<const unsigned char*>(p.q + b * p.qs[0] + hq * p.qs[1]));
-        const unsigned char* op = wide_uniform_ptr(reinterpret_cast<const unsigned char*>(p.dout + b * p.dos[0] + hq * p.dos[1]));
+        const unsigned char* qp = tile_uniform_ptr(reinterpret_cast<const unsigned char*>(p.q + b * p.qs[0] + hq * p.qs[1]));
+        const unsigned char* op = tile_uniform_ptr(reinterpret_cast<const unsigned char*>(p.dout + b * p.dos[0] + hq * p.dos[1]));
         const int nrows = min(T_ - q0, kFKT);
         unsigned char* lq = stage_base(st);
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             const int skip = i * RPI;
-            wide_dma16(__builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(qp + (q0 + skip) * qrs), 0,
+            tile_dma16(__builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(qp + (q0 + skip) * qrs), 0,
                                                          max((nrows - skip) * static_cast<int>(qrs), 0), 0x00020000),
                        qoff, lq + (i * kFW + wave) * 1024);
-            wide_dma16(__builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(op + (q0 + skip) * ors), 0,
+            tile_dma16(__builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(op + (q0 + skip) * ors), 0,
                                                          max((nrows - skip) * static_cast<int>(ors), 0), 0x00020000),
                        ooff, lq + TB + (i * kFW + wave) * 1024);
         }
@@ -728,7 +728,7 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_kv_wide_kernel(WideParams<
     using S1 = std::integral_constant<int, 1>;
     issue(0, S0{});
     store_rv(0, row_value(0));
-    wide_wait_vmem();
+    tile_wait_vmem();
     __syncthreads();
     // iteration it reads stage it & 1 while the DMA fills the other with it + 1
     auto step = [&](int it, auto cur) {
@@ -747,7 +747,7 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_kv_wide_kernel(WideParams<
         if (active) tile(!interior, it, cur);
         if (more) {
             store_rv(nxt, rnext);
-            wide_wait_vmem();
+            tile_wait_vmem();
             __syncthreads();
         }
     };
