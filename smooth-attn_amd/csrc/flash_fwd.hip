@@ -700,10 +700,12 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashParams p) {
 // 65504 sooner by the factor 1/sc^2.  The scale must be positive and
 // moderate so that -1/(2 sc), 1/sc^2 and the scaled sums stay well inside
 // fp32; the fp8 path's scale is only known on the device and is not folded.
-// D = 128 only: the 16 registers holding the chains' start value cost the
-// D = 32 and 64 kernels a wave per SIMD (config 3, D = 128: 767 -> 752 us).
+// D = 128 (config 3: 767 -> 752 us) and 16-bit D = 64 ([4,32,4096,64]:
+// 377 -> 363 us): the 16 registers holding the chains' start value take
+// D = 64 from 154 to 189, which leaves it one 8-wave block per CU as before;
+// at D = 32 (108 -> 146) they would halve the resident blocks.
 template <typename T, bool QK8, int D>
-constexpr bool kCanFold = std::is_same_v<T, bf16> && D == 128;
+constexpr bool kCanFold = std::is_same_v<T, bf16> && (D == 128 || (D == 64 && !QK8));
 
 // 16-bit Q/K fold relative to the scale itself; fp8 Q/K fold relative to
 // its mantissa (any positive scale: q_scale and k_scale are positive).
