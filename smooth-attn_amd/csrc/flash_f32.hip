@@ -53,6 +53,7 @@ struct F32Params {
     float* delta;  // [B, Hq, T]
     int64_t qs[4], ks[4], vs[4], os[4], dos[4], dqs[4], dks[4], dvs[4];
     int B, Hq, Hkv, T, G, window;
+    int dr;  // head dim of the tensors (<= D, a multiple of 4; columns past it read as zero, are not stored)
     float scale;
 };
 
@@ -62,13 +63,22 @@ template <int D>
 struct TileRegs {
     static constexpr int PER = kFT * D / 4 / (64 * kFW);  // float4 per thread
     float4 v[PER];
-    __device__ __forceinline__ void load(const float* base, int64_t rstride, int r0, int T, int tid) {
+    // PART: the tensors' head dim dr is below D; columns past it load as zeros
+    // (the load then reads column 0).
+    template <bool PART>
+    __device__ __forceinline__ void load(const float* base, int64_t rstride, int r0, int T, int tid, int dr) {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int idx = tid + 64 * kFW * i;
             const int r = idx / (D / 4);
             const int c = (idx - r * (D / 4)) * 4;
-            v[i] = *reinterpret_cast<const float4*>(base + static_cast<int64_t>(min(r0 + r, T - 1)) * rstride + c);
+            const float* rp = base + static_cast<int64_t>(min(r0 + r, T - 1)) * rstride;
+            if constexpr (PART) {
+                const float4 t = *reinterpret_cast<const float4*>(rp + (c < dr ? c : 0));
+                v[i] = c < dr ? t : float4{0.f, 0.f, 0.f, 0.f};
+            } else {
+                v[i] = *reinterpret_cast<const float4*>(rp + c);
+            }
         }
     }
     // row-major [kFT][D + 4] (nullable) and transposed [D][kTP] (nullable)
@@ -107,12 +117,19 @@ __device__ __forceinline__ void weight_rr(float s, float sc, float& y, float& rr
     y = sp * sp;
 }
 
-// A lane's half row: x[i] = row[i + hi D/2], i < D/2.
-template <int D>
-__device__ __forceinline__ void load_half_row(const float* row, int hi, float (&x)[D / 2]) {
+// A lane's half row: x[i] = row[i + hi D/2], i < D/2 (PART: zero past dr).
+template <int D, bool PART>
+__device__ __forceinline__ void load_half_row(const float* row, int hi, float (&x)[D / 2], int dr) {
 #pragma unroll
     for (int i4 = 0; i4 < D / 8; ++i4) {
-        const float4 t = *reinterpret_cast<const float4*>(row + hi * (D / 2) + 4 * i4);
+        const int c = hi * (D / 2) + 4 * i4;
+        float4 t;
+        if constexpr (PART) {
+            t = *reinterpret_cast<const float4*>(row + (c < dr ? c : 0));
+            if (c >= dr) t = float4{0.f, 0.f, 0.f, 0.f};
+        } else {
+            t = *reinterpret_cast<const float4*>(row + c);
+        }
         x[4 * i4 + 0] = t.x;
         x[4 * i4 + 1] = t.y;
         x[4 * i4 + 2] = t.z;
@@ -158,16 +175,16 @@ __device__ __forceinline__ void mma_cols(const float* lds_tr, int l32, int hi, c
 }
 
 // Write a lane's C-layout rows of acc (column = its row index of the output,
-// d = 32 dt + 8 m + 4 hi .. +3) times f as 16-byte stores.
-template <int D>
-__device__ __forceinline__ void store_cols(float* row, int hi, const f32x16 (&acc)[D / 32], float f) {
+// d = 32 dt + 8 m + 4 hi .. +3) times f as 16-byte stores (PART: only below dr).
+template <int D, bool PART>
+__device__ __forceinline__ void store_cols(float* row, int hi, const f32x16 (&acc)[D / 32], float f, int dr) {
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) {
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
             const float4 w{acc[dt][4 * m + 0] * f, acc[dt][4 * m + 1] * f, acc[dt][4 * m + 2] * f,
                            acc[dt][4 * m + 3] * f};
-            *reinterpret_cast<float4*>(row + dt * 32 + 8 * m + 4 * hi) = w;
+            if (!PART || dt * 32 + 8 * m + 4 * hi < dr) *reinterpret_cast<float4*>(row + dt * 32 + 8 * m + 4 * hi) = w;
         }
     }
 }
@@ -188,8 +205,13 @@ constexpr bool kSkipIdle = D <= 128;
 // shape in fp32: 7.7 ms vs 5.0 ms), the D = 64 dK/dV kernel 290 registers
 // (10.1 vs 8.2 ms for the backward); the D = 128 backward kernels spill at two
 // waves and are still faster (21.4 vs 22.0 ms).
+// The forward runs the masked loads for every head dim (PART below): at D = 64,
+// 128 and 256 that build compiles without the 48-144 B of spills of the
+// unmasked one and is as fast or faster (D = 256: 1945 -> 1539 us on
+// [4,16,2048,256]; D = 64: 2353 -> 2265 us on [4,32,4096,64]).
 template <int D, bool EXACT>
 __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 128 ? 1 : 2, 8))) void flash_fwd_f32_kernel(F32Params p) {
+    constexpr bool PART = true;
     __shared__ __attribute__((aligned(16))) float ldsK[kFT * (D + 4)];
     __shared__ __attribute__((aligned(16))) float ldsVt[D * kTP];
     const int tid = threadIdx.x;
@@ -213,7 +235,7 @@ __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 12
     const int qi = q0 + l32;
     const int qrow = min(qi, T_ - 1);
     float qv[D / 2];
-    load_half_row<D>(p.q + b * p.qs[0] + hq * p.qs[1] + qrow * p.qs[2], hi, qv);
+    load_half_row<D, PART>(p.q + b * p.qs[0] + hq * p.qs[1] + qrow * p.qs[2], hi, qv, p.dr);
 
     f32x16 oacc[D / 32];
 #pragma unroll
@@ -227,16 +249,16 @@ __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 12
     const float sc = p.scale;
 
     TileRegs<D> kreg, vreg;
-    kreg.load(kp, p.ks[2], kv_begin * kFT, T_, tid);
-    vreg.load(vp, p.vs[2], kv_begin * kFT, T_, tid);
+    kreg.template load<PART>(kp, p.ks[2], kv_begin * kFT, T_, tid, p.dr);
+    vreg.template load<PART>(vp, p.vs[2], kv_begin * kFT, T_, tid, p.dr);
     for (int t = kv_begin; t < kv_end; ++t) {
         __syncthreads();  // every wave is done with tile t - 1
         kreg.store(ldsK, nullptr, tid);
         vreg.store(nullptr, ldsVt, tid);
         __syncthreads();
         if (t + 1 < kv_end) {
-            kreg.load(kp, p.ks[2], (t + 1) * kFT, T_, tid);
-            vreg.load(vp, p.vs[2], (t + 1) * kFT, T_, tid);
+            kreg.template load<PART>(kp, p.ks[2], (t + 1) * kFT, T_, tid, p.dr);
+            vreg.template load<PART>(vp, p.vs[2], (t + 1) * kFT, T_, tid, p.dr);
         }
         const int k0 = t * kFT;
         const bool active = k0 <= q0 + 31 && !(W > 0 && q0 - (k0 + 31) >= W);
@@ -257,7 +279,7 @@ __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 12
 
     const float tot = ssum + __shfl_xor(ssum, 32) + kEps;
     if (qi < T_) {
-        store_cols<D>(p.out + b * p.os[0] + hq * p.os[1] + qi * p.os[2], hi, oacc, 1.f / tot);
+        store_cols<D, PART>(p.out + b * p.os[0] + hq * p.os[1] + qi * p.os[2], hi, oacc, 1.f / tot, p.dr);
         if (hi == 0 && p.row_sums != nullptr) p.row_sums[(static_cast<int64_t>(b) * p.Hq + hq) * T_ + qi] = tot;
     }
 }
@@ -265,7 +287,7 @@ __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 12
 // ---------------------------------------------------------------------------
 // Backward: dQ (and delta)
 // ---------------------------------------------------------------------------
-template <int D, bool EXACT>
+template <int D, bool EXACT, bool PART>
 __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 128 ? 1 : 2, 8))) void flash_bwd_dq_f32_kernel(F32Params p) {
     __shared__ __attribute__((aligned(16))) float ldsK[kFT * (D + 4)];
     __shared__ __attribute__((aligned(16))) float ldsKt[D * kTP];
@@ -291,15 +313,18 @@ __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 12
     const int qi = q0 + l32;
     const int qrow = min(qi, T_ - 1);
     float qv[D / 2], dov[D / 2];
-    load_half_row<D>(p.q + b * p.qs[0] + hq * p.qs[1] + qrow * p.qs[2], hi, qv);
-    load_half_row<D>(p.dout + b * p.dos[0] + hq * p.dos[1] + qrow * p.dos[2], hi, dov);
+    load_half_row<D, PART>(p.q + b * p.qs[0] + hq * p.qs[1] + qrow * p.qs[2], hi, qv, p.dr);
+    load_half_row<D, PART>(p.dout + b * p.dos[0] + hq * p.dos[1] + qrow * p.dos[2], hi, dov, p.dr);
     // delta = rowsum(dO * O) of this lane's query (lanes l and l ^ 32 hold the halves)
     float dpart = 0.f;
     {
         const float* orow = p.o + b * p.os[0] + hq * p.os[1] + qrow * p.os[2] + hi * (D / 2);
 #pragma unroll
         for (int i4 = 0; i4 < D / 8; ++i4) {
-            const float4 ov = *reinterpret_cast<const float4*>(orow + 4 * i4);
+            // PART: columns past dr read column 0 and are zeroed
+            const bool in = !PART || hi * (D / 2) + 4 * i4 < p.dr;
+            float4 ov = *reinterpret_cast<const float4*>(orow + (in ? 4 * i4 : -hi * (D / 2)));
+            if (!in) ov = float4{0.f, 0.f, 0.f, 0.f};
             dpart = __builtin_fmaf(dov[4 * i4 + 0], ov.x, dpart);
             dpart = __builtin_fmaf(dov[4 * i4 + 1], ov.y, dpart);
             dpart = __builtin_fmaf(dov[4 * i4 + 2], ov.z, dpart);
@@ -325,16 +350,16 @@ __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 12
     const float sc = p.scale;
 
     TileRegs<D> kreg, vreg;
-    kreg.load(kp, p.ks[2], kv_begin * kFT, T_, tid);
-    vreg.load(vp, p.vs[2], kv_begin * kFT, T_, tid);
+    kreg.template load<PART>(kp, p.ks[2], kv_begin * kFT, T_, tid, p.dr);
+    vreg.template load<PART>(vp, p.vs[2], kv_begin * kFT, T_, tid, p.dr);
     for (int t = kv_begin; t < kv_end; ++t) {
         __syncthreads();
         kreg.store(ldsK, ldsKt, tid);
         vreg.store(ldsV, nullptr, tid);
         __syncthreads();
         if (t + 1 < kv_end) {
-            kreg.load(kp, p.ks[2], (t + 1) * kFT, T_, tid);
-            vreg.load(vp, p.vs[2], (t + 1) * kFT, T_, tid);
+            kreg.template load<PART>(kp, p.ks[2], (t + 1) * kFT, T_, tid, p.dr);
+            vreg.template load<PART>(vp, p.vs[2], (t + 1) * kFT, T_, tid, p.dr);
         }
         const int k0 = t * kFT;
         const bool active = k0 <= q0 + 31 && !(W > 0 && q0 - (k0 + 31) >= W);
@@ -352,13 +377,13 @@ __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 12
         mma_cols<D>(ldsKt, l32, hi, ds, acc);  // dQ^T += K^T dS^T
     }
     // dS carried without its per-row factor 2 scale / R
-    if (qi < T_) store_cols<D>(p.dq + b * p.dqs[0] + hq * p.dqs[1] + qi * p.dqs[2], hi, acc, 2.f * sc * inv_r);
+    if (qi < T_) store_cols<D, PART>(p.dq + b * p.dqs[0] + hq * p.dqs[1] + qi * p.dqs[2], hi, acc, 2.f * sc * inv_r, p.dr);
 }
 
 // ---------------------------------------------------------------------------
 // Backward: dK, dV
 // ---------------------------------------------------------------------------
-template <int D, bool EXACT>
+template <int D, bool EXACT, bool PART>
 __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 128 ? 1 : 2, 8))) void flash_bwd_dkdv_f32_kernel(F32Params p) {
     __shared__ __attribute__((aligned(16))) float ldsQ[kFT * (D + 4)];
     __shared__ __attribute__((aligned(16))) float ldsQt[D * kTP];
@@ -384,8 +409,8 @@ __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 12
     const int kj = wk0 + l32;
     const int krow = min(kj, T_ - 1);
     float kv[D / 2], vv[D / 2];
-    load_half_row<D>(p.k + b * p.ks[0] + hk * p.ks[1] + krow * p.ks[2], hi, kv);
-    load_half_row<D>(p.v + b * p.vs[0] + hk * p.vs[1] + krow * p.vs[2], hi, vv);
+    load_half_row<D, PART>(p.k + b * p.ks[0] + hk * p.ks[1] + krow * p.ks[2], hi, kv, p.dr);
+    load_half_row<D, PART>(p.v + b * p.vs[0] + hk * p.vs[1] + krow * p.vs[2], hi, vv, p.dr);
 
     f32x16 dkacc[D / 32], dvacc[D / 32];
 #pragma unroll
@@ -408,8 +433,8 @@ __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 12
         const int g = it / nq;
         const int q0 = (qt_begin + it - g * nq) * kFT;
         const int hq = hk * p.G + g;
-        qreg.load(p.q + b * p.qs[0] + hq * p.qs[1], p.qs[2], q0, T_, tid);
-        oreg.load(p.dout + b * p.dos[0] + hq * p.dos[1], p.dos[2], q0, T_, tid);
+        qreg.template load<PART>(p.q + b * p.qs[0] + hq * p.qs[1], p.qs[2], q0, T_, tid, p.dr);
+        oreg.template load<PART>(p.dout + b * p.dos[0] + hq * p.dos[1], p.dos[2], q0, T_, tid, p.dr);
         // raw row sum or delta; 1/R or -delta is formed where it is stored
         if (tid < 2 * kFT) {
             const int64_t idx = (static_cast<int64_t>(b) * p.Hq + hq) * T_ + min(q0 + (tid & (kFT - 1)), T_ - 1);
@@ -450,8 +475,8 @@ __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 12
         mma_cols<D>(ldsQt, l32, hi, ds, dkacc);  // dK^T += Q^T dS
     }
     if (kj < T_) {
-        store_cols<D>(p.dk + b * p.dks[0] + hk * p.dks[1] + kj * p.dks[2], hi, dkacc, 2.f * sc);
-        store_cols<D>(p.dv + b * p.dvs[0] + hk * p.dvs[1] + kj * p.dvs[2], hi, dvacc, 1.f);
+        store_cols<D, PART>(p.dk + b * p.dks[0] + hk * p.dks[1] + kj * p.dks[2], hi, dkacc, 2.f * sc, p.dr);
+        store_cols<D, PART>(p.dv + b * p.dvs[0] + hk * p.dvs[1] + kj * p.dvs[2], hi, dvacc, 1.f, p.dr);
     }
 }
 
@@ -460,7 +485,7 @@ bool f32_strides_ok(const int64_t* s) { return s[3] == 1 && s[0] % 4 == 0 && s[1
 
 int check_common(int B, int Hq, int Hkv, int T, int D, int window_size) {
     if (B < 0 || Hq <= 0 || Hkv <= 0 || T < 0 || Hq % Hkv != 0 || window_size < 0) return SA_ERR_BAD_SHAPE;
-    if (D != 32 && D != 64 && D != 128 && D != 256) return SA_ERR_UNSUPPORTED;
+    if (D < 4 || D > 256 || D % 4 != 0) return SA_ERR_UNSUPPORTED;
     return 0;
 }
 
@@ -482,12 +507,22 @@ int launch_bwd_f32_d(const F32Params& prm, int exact, hipStream_t st) {
     if (nq * 64 * kFW >= (int64_t(1) << 32)) return SA_ERR_BAD_SHAPE;
     const int64_t nk = nq / prm.G;
     const dim3 gq(static_cast<unsigned>(nq)), gk(static_cast<unsigned>(nk));
-    if (exact) {
-        flash_bwd_dq_f32_kernel<D, true><<<gq, 64 * kFW, 0, st>>>(prm);
-        flash_bwd_dkdv_f32_kernel<D, true><<<gk, 64 * kFW, 0, st>>>(prm);
+    // Masked builds (PART) except for a full D = 128, whose unmasked build
+    // measured 1% faster; at D = 64 and 256 the masked ones are the faster
+    // even when dr == D (8671 -> 8430 and 8173 -> 7794 us).
+    const bool part = prm.dr != D || D != 128;
+    if (exact && part) {
+        flash_bwd_dq_f32_kernel<D, true, true><<<gq, 64 * kFW, 0, st>>>(prm);
+        flash_bwd_dkdv_f32_kernel<D, true, true><<<gk, 64 * kFW, 0, st>>>(prm);
+    } else if (exact) {
+        flash_bwd_dq_f32_kernel<D, true, false><<<gq, 64 * kFW, 0, st>>>(prm);
+        flash_bwd_dkdv_f32_kernel<D, true, false><<<gk, 64 * kFW, 0, st>>>(prm);
+    } else if (part) {
+        flash_bwd_dq_f32_kernel<D, false, true><<<gq, 64 * kFW, 0, st>>>(prm);
+        flash_bwd_dkdv_f32_kernel<D, false, true><<<gk, 64 * kFW, 0, st>>>(prm);
     } else {
-        flash_bwd_dq_f32_kernel<D, false><<<gq, 64 * kFW, 0, st>>>(prm);
-        flash_bwd_dkdv_f32_kernel<D, false><<<gk, 64 * kFW, 0, st>>>(prm);
+        flash_bwd_dq_f32_kernel<D, false, false><<<gq, 64 * kFW, 0, st>>>(prm);
+        flash_bwd_dkdv_f32_kernel<D, false, false><<<gk, 64 * kFW, 0, st>>>(prm);
     }
     return status_from_launch();
 }
@@ -522,13 +557,13 @@ int flash_fwd_f32(const void* q, const void* k, const void* v, void* o, float* r
     prm.T = T;
     prm.G = Hq / Hkv;
     prm.window = window_size;
+    prm.dr = D;
     prm.scale = scale;
-    switch (D) {
-        case 32: return launch_fwd_f32_d<32>(prm, exact_math, st);
-        case 64: return launch_fwd_f32_d<64>(prm, exact_math, st);
-        case 128: return launch_fwd_f32_d<128>(prm, exact_math, st);
-        default: return launch_fwd_f32_d<256>(prm, exact_math, st);
-    }
+    // head dims 4..256 (multiples of 4) on the kernel for the next of 32, 64, 128, 256
+    if (D <= 32) return launch_fwd_f32_d<32>(prm, exact_math, st);
+    if (D <= 64) return launch_fwd_f32_d<64>(prm, exact_math, st);
+    if (D <= 128) return launch_fwd_f32_d<128>(prm, exact_math, st);
+    return launch_fwd_f32_d<256>(prm, exact_math, st);
 }
 
 int flash_bwd_f32(const void* q, const void* k, const void* v, const void* o, const void* dout,
@@ -564,13 +599,12 @@ int flash_bwd_f32(const void* q, const void* k, const void* v, const void* o, co
     prm.T = T;
     prm.G = Hq / Hkv;
     prm.window = window_size;
+    prm.dr = D;
     prm.scale = scale;
-    switch (D) {
-        case 32: return launch_bwd_f32_d<32>(prm, exact_math, st);
-        case 64: return launch_bwd_f32_d<64>(prm, exact_math, st);
-        case 128: return launch_bwd_f32_d<128>(prm, exact_math, st);
-        default: return launch_bwd_f32_d<256>(prm, exact_math, st);
-    }
+    if (D <= 32) return launch_bwd_f32_d<32>(prm, exact_math, st);
+    if (D <= 64) return launch_bwd_f32_d<64>(prm, exact_math, st);
+    if (D <= 128) return launch_bwd_f32_d<128>(prm, exact_math, st);
+    return launch_bwd_f32_d<256>(prm, exact_math, st);
 }
 
 }  // namespace sa

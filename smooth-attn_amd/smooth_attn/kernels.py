@@ -549,10 +549,11 @@ _MAX_ROW_STRIDE_BYTES = 1 << 24
 
 
 def _flash_operand(t):
-    """The kernels take any (b, h, t) strides that are multiples of 8 elements
+    """The kernels take any (b, h, t) strides that are multiples of 16 bytes
     with a unit stride along D, a 16-byte aligned base and rows at most
     16 MiB apart; anything else is copied to a contiguous tensor first."""
-    ok = (t.stride(-1) == 1 and all(s % 8 == 0 for s in t.stride()[:-1]) and t.data_ptr() % 16 == 0
+    a = 16 // t.element_size()
+    ok = (t.stride(-1) == 1 and all(s % a == 0 for s in t.stride()[:-1]) and t.data_ptr() % 16 == 0
           and t.stride(-2) * t.element_size() <= _MAX_ROW_STRIDE_BYTES)
     return t if ok else t.clone(memory_format=torch.contiguous_format)
 
@@ -563,9 +564,10 @@ _FLASH_KERNEL_DIMS = {dt: (32, 64, 128, 256) for dt in (torch.bfloat16, torch.fl
 
 def _kernel_head_dim(D, dtype=None):
     """The head dim the kernels are called with for a head dim D.  bf16 /
-    fp16: D rounded up to a multiple of 8 (the kernels built for 32, 64, 128
-    and 256 take any such D up to their size, reading only its columns); fp32
-    and fp8: the next of the head dims their kernels are built for.  Where it
+    fp16: D rounded up to a multiple of 8, fp32 to a multiple of 4 (the
+    kernels built for 32, 64, 128 and 256 take any such D up to their size,
+    reading only its columns); fp8: the next of the head dims its kernels
+    are built for.  Where it
     differs from D, inputs are zero-padded and outputs sliced: zero columns
     add nothing to q.k, and the padded columns of O, dQ, dK, dV are dropped.
     The reference computes at next_pow2(D) (kernels.py:1918) without masking
@@ -575,6 +577,8 @@ def _kernel_head_dim(D, dtype=None):
         raise ValueError(f"fused attention supports head dims 1..{dims[-1]}, got {D}")
     if dtype in (torch.bfloat16, torch.float16):
         return -(-D // 8) * 8
+    if dtype == torch.float32:
+        return -(-D // 4) * 4
     return next(d for d in dims if d >= D)
 
 

@@ -272,7 +272,7 @@ def test_fused_entry_points_refuse_meta_tensors(case, no_library):
 
 def test_head_dims_and_page_sizes_checked_before_launch(no_library):
     # fused attention, fp8 included: any head dim up to 256 (16-bit: rounded
-    # up to a multiple of 8; fp32 and fp8: zero-padded to a built size); larger head dims, fp64 and
+    # up to a multiple of 8, fp32 of 4; fp8: zero-padded to a built size); larger head dims, fp64 and
     # mixed dtypes are refused with a clear error; paged decode: power-of-two
     # page sizes only
     mk = lambda shape, dtype: _OnDevice.make(torch.zeros(shape, dtype=dtype), 0)
@@ -289,7 +289,7 @@ def test_head_dims_and_page_sizes_checked_before_launch(no_library):
     dims = (1, 16, 32, 33, 64, 96, 128, 129, 200, 256)
     # 16-bit: multiples of 8 run as they are (columns past D masked in the kernels)
     assert [kernels._kernel_head_dim(d, torch.bfloat16) for d in dims] == [8, 16, 32, 40, 64, 96, 128, 136, 200, 256]
-    assert [kernels._kernel_head_dim(d, torch.float32) for d in dims] == [32, 32, 32, 64, 64, 128, 128, 256, 256, 256]
+    assert [kernels._kernel_head_dim(d, torch.float32) for d in dims] == [4, 16, 32, 36, 64, 96, 128, 132, 200, 256]
     assert [kernels._kernel_head_dim(d) for d in dims[:7]] == [32, 32, 32, 64, 64, 128, 128]
     q = mk((1, 2, 8, 64), torch.float64)
     with pytest.raises(ValueError, match="bf16, fp16 or fp32"):
