@@ -289,6 +289,11 @@ int sa_flash_rope_fwd(const void* q, const void* k, const void* v,
 int64_t sa_paged_decode_workspace_size(int B, int Hq, int D, int max_pages,
                                        int page_size);
 
+/* dtype argument of the paged decode entry points: q's element type in the
+ * low byte, the caches' type plus one in the next (0 there: the caches share
+ * q's type, so a plain SA_BF16 / SA_F16 / SA_F32 means both). */
+#define SA_PAGED_DTYPES(q_type, cache_type) ((q_type) | (((cache_type) + 1) << 8))
+
 /*
  * Paged single-token decode through a block table.
  *   q: [B, Hq, 1, D] (strides q_strides, d stride 1)
@@ -301,10 +306,15 @@ int64_t sa_paged_decode_workspace_size(int B, int Hq, int D, int max_pages,
  * result is then meaningless but no memory outside the cache is read).
  *   out: bf16 [B, Hq, D] (strides o_strides)
  * out[b,h] = sum_{t<ctx_b} y_t V_t / (sum_t y_t + 1e-12) with
- * K_t = k_cache[block_table[b, t/P], h/(Hq/Hkv), t%P].  dtype (q and cache):
- * SA_BF16 or SA_F16.  D a multiple of 8 in 8..256 (kernels for 32, 64, 128
- * and 256; smaller D read only their own columns); page_size a power of two
- * (at most 2^20).
+ * K_t = k_cache[block_table[b, t/P], h/(Hq/Hkv), t%P].  dtype:
+ * SA_PAGED_DTYPES(q type, cache type), or one code for both; supported
+ * pairs: bf16 / bf16, fp16 / fp16, fp32 / fp32, fp32 q over bf16 or fp16
+ * caches (the reference upcasts q, K and V to fp32, kernels.py:2716-2717,
+ * :2746, :2765; mixed pairs and fp32 run their products as bf16
+ * hi + lo splits, about 16 significant bits).  Row strides (element units)
+ * must be 16-byte multiples.  D a multiple of 8 in 8..256 (kernels for 32,
+ * 64, 128 and 256; smaller D read only their own columns); page_size a
+ * power of two (at most 2^20).
  * workspace: at least sa_paged_decode_workspace_size() bytes, 16-byte
  * aligned, no initialisation needed (a plan kernel writes it).
  * Replaces sp2norm_paged_attention (kernels.py:2776-2829) and its kernel
@@ -360,7 +370,9 @@ int sa_paged_decode_noalloc(const void* q, const void* k_cache,
  * k_new, v_new: [B, Hkv, n_new, D] (new_strides, d stride 1); caches as in
  * sa_paged_decode.  Rows whose page index reaches max_pages or whose table
  * entry is outside [0, n_pages) are skipped.  context_lens is not updated
- * (the caller adds n_new).  dtype SA_BF16 or SA_F16; D a multiple of 8.
+ * (the caller adds n_new).  dtype SA_F32, SA_BF16 or SA_F16 (the caches'
+ * type; the rows are copied as bytes); rows of 16-byte multiples (D a
+ * multiple of 4 for fp32, of 8 for 16-bit types).
  * No reference kernel: the reference fills caches with Python loops in its
  * tests (tests/test_paged_attention.py:10-73).
  */

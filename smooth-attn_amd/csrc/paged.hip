@@ -27,6 +27,7 @@
 #include <algorithm>
 #include <atomic>
 #include <mutex>
+#include <type_traits>
 
 #include "flash_common.hpp"
 
@@ -92,15 +93,68 @@ __global__ __launch_bounds__(256) void paged_plan_kernel(PagedParams p) {
     }
 }
 
+// Element types of one decode: q (QE) and both caches (CE).  The MFMAs run
+// on MT: the 16-bit type itself when q and the caches share it, else bf16,
+// with every operand bf16 does not hold exactly split as hi + lo
+// (hi = bf16(x), lo = bf16(x - hi), so hi + lo carries 16 significant bits;
+// fp16 values split exactly).  With a split operand the fp32 weights are
+// split too, and each product becomes the three MFMAs hi*hi + hi*lo + lo*hi:
+// about 2^-16 relative error per product, against the reference's fp32
+// arithmetic (kernels.py:2716-2717, :2746, :2765).
+template <typename QE, typename CE>
+struct PagedTypes {
+    static constexpr bool SAME16 = std::is_same_v<QE, CE> && sizeof(CE) == 2;
+    using MT = std::conditional_t<SAME16, CE, bf16>;
+    static constexpr bool SPLIT_Q = !std::is_same_v<QE, MT>;
+    static constexpr bool SPLIT_C = !std::is_same_v<CE, MT>;
+    static constexpr bool SPLIT_P = !SAME16;
+};
+
+// hi = bf16(a), bf16(b) packed; lo = the same of the remainders.
+__device__ __forceinline__ void split2_bf16(float a, float b, uint32_t& hi, uint32_t& lo) {
+    hi = pack2<bf16>(a, b);
+    lo = pack2<bf16>(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xFFFF0000u));
+}
+
+// 8 elements of E (one or two 16-byte words, as loaded) as 8 MT values, hi
+// and, when SPLIT, lo.
+template <typename E, typename MT, bool SPLIT>
+__device__ __forceinline__ void to_mt8(const u32x4* w, u32x4& h, u32x4& l) {
+    if constexpr (std::is_same_v<E, MT>) {
+        h = w[0];
+        l = u32x4{0u, 0u, 0u, 0u};
+    } else {
+        float f[8];
+        if constexpr (sizeof(E) == 4) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                f[i] = __uint_as_float(w[0][i]);
+                f[4 + i] = __uint_as_float(w[1][i]);
+            }
+        } else {
+            const uint32_t ww[4] = {w[0].x, w[0].y, w[0].z, w[0].w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) f[i] = elem<E>(ww, i);
+        }
+        uint32_t hh[4], ll[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) split2_bf16(f[2 * i], f[2 * i + 1], hh[i], ll[i]);
+        h = u32x4{hh[0], hh[1], hh[2], hh[3]};
+        l = SPLIT ? u32x4{ll[0], ll[1], ll[2], ll[3]} : u32x4{0u, 0u, 0u, 0u};
+    }
+}
+
 // The kernels run a padded head dim D (32, 64, 128 or 256); head dims
-// p.D < D (multiples of 8) load only their p.D / 8 chunks per row and leave
-// zeros in the rest of the LDS rows and Q registers, which add nothing to
-// the scores, and write only p.D output columns.
-// UNIFORM: every load instruction's tokens lie in one page (64 / (D/8)
-// tokens per instruction divide the page size), so the page base is
-// wave-uniform and comes from v_readlane of the window's page-id register.
-template <typename T, int D, bool UNIFORM>
+// p.D < D (multiples of 8) load only their first p.D columns per row and
+// leave zeros in the rest of the LDS rows and Q registers, which add nothing
+// to the scores, and write only p.D output columns.
+// UNIFORM: every load instruction's tokens lie in one page (the tokens per
+// instruction divide the page size), so the page base is wave-uniform and
+// comes from v_readlane of the window's page-id register.
+template <typename QE, typename CE, int D, bool UNIFORM>
 __global__ __launch_bounds__(64) void paged_partial_kernel(PagedParams p) {
+    using Ty = PagedTypes<QE, CE>;
+    using T = typename Ty::MT;
     using Ops = MfmaOps<T>;
     using Vec = typename Ops::vec8;
     // Padded LDS rows.  The LDS has 64 banks of 4 bytes; a 16-byte read is
@@ -112,11 +166,16 @@ __global__ __launch_bounds__(64) void paged_partial_kernel(PagedParams p) {
     // distinct 64-byte slots.
     constexpr int RS = D + 8;                            // K row stride (elements)
     constexpr int RSV = (2 * D) % 256 == 64 ? D : D + 32;  // V row stride (elements)
-    constexpr int CPT = D / 8;             // 16-byte chunks per token row
+    constexpr int EPC = 16 / sizeof(CE);   // cache elements per 16-byte chunk
+    constexpr int CPT = D / EPC;           // 16-byte chunks per token row
     constexpr int TPI = 64 / CPT;          // tokens per load instruction
     constexpr int NC = kTile * CPT / 64;   // chunks per lane per tile and tensor
+    constexpr bool SQ = Ty::SPLIT_Q, SC = Ty::SPLIT_C, SP = Ty::SPLIT_P;
+    // MT tiles; the lo parts of split caches in the second pair
     __shared__ __attribute__((aligned(16))) T ldsK[kTile * RS];
     __shared__ __attribute__((aligned(16))) T ldsV[kTile * RSV];
+    __shared__ __attribute__((aligned(16))) T ldsKl[SC ? kTile * RS : 8];
+    __shared__ __attribute__((aligned(16))) T ldsVl[SC ? kTile * RSV : 8];
 
     const int lane = threadIdx.x;
     const int hi = lane >> 5;
@@ -156,18 +215,28 @@ __global__ __launch_bounds__(64) void paged_partial_kernel(PagedParams p) {
         const int owner0 = static_cast<int>((static_cast<int64_t>(seg_start + 1) * Ne - 1) / Tt);
         const int slot_k = w - owner0;
 
-        const T* kc = static_cast<const T*>(p.k) + hk * p.ks[1];
-        const T* vc = static_cast<const T*>(p.v) + hk * p.vs[1];
+        const CE* kc = static_cast<const CE*>(p.k) + hk * p.ks[1];
+        const CE* vc = static_cast<const CE*>(p.v) + hk * p.vs[1];
         const int32_t* trow = p.table + b * p.bt_stride;
 
-        // Q^T as the B operand: column = query head hk*G + l32 (zero past G).
-        u32x4 qreg[D / 16];
+        // Q^T as the B operand: column = query head hk*G + l32 (zero past G);
+        // qlo holds the lo parts when q is split.
+        u32x4 qreg[D / 16], qlo[SQ ? D / 16 : 1];
         {
             const bool live = l32 < p.G;
-            const T* qrow = static_cast<const T*>(p.q) + b * p.qs[0] + (hk * p.G + (live ? l32 : 0)) * p.qs[1];
+            const QE* qrow = static_cast<const QE*>(p.q) + b * p.qs[0] + (hk * p.G + (live ? l32 : 0)) * p.qs[1];
 #pragma unroll
-            for (int dc = 0; dc < D / 16; ++dc)
-                qreg[dc] = live && dc * 16 + hi * 8 < p.D ? load16(qrow + dc * 16 + hi * 8) : u32x4{0u, 0u, 0u, 0u};
+            for (int dc = 0; dc < D / 16; ++dc) {
+                const int d0 = dc * 16 + hi * 8;
+                u32x4 w[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};
+                if (live && d0 < p.D) {
+                    w[0] = load16(qrow + d0);
+                    if constexpr (sizeof(QE) == 4) w[1] = load16(qrow + d0 + 4);
+                }
+                u32x4 l;
+                to_mt8<QE, T, SQ>(w, qreg[dc], l);
+                if constexpr (SQ) qlo[dc] = l;
+            }
         }
 
         f32x16 oacc[D / 32];
@@ -187,9 +256,10 @@ __global__ __launch_bounds__(64) void paged_partial_kernel(PagedParams p) {
             }
 
             // Coalesced tile loads: instruction i of lane l fetches 16-byte chunk
-            // c = 64 i + l of the tile (token c / CPT, columns 8 (c % CPT) .. +7).
+            // c = 64 i + l of the tile (token c / CPT, columns EPC (c % CPT) ..
+            // + EPC - 1).
             const int lane_tok = lane / CPT;
-            const int lane_col = (lane % CPT) * 8;
+            const int lane_col = (lane % CPT) * EPC;
             const bool col_live = lane_col < p.D;  // columns past the head dim stay zero
             u32x4 kbuf[NC], vbuf[NC];
             auto load_tile = [&](int t0) {
@@ -222,8 +292,33 @@ __global__ __launch_bounds__(64) void paged_partial_kernel(PagedParams p) {
 #pragma unroll
                 for (int i = 0; i < NC; ++i) {
                     const int tok = i * TPI + lane_tok;
-                    *reinterpret_cast<u32x4*>(ldsK + tok * RS + lane_col) = kbuf[i];
-                    *reinterpret_cast<u32x4*>(ldsV + tok * RSV + lane_col) = vbuf[i];
+                    if constexpr (!SC) {
+                        *reinterpret_cast<u32x4*>(ldsK + tok * RS + lane_col) = kbuf[i];
+                        *reinterpret_cast<u32x4*>(ldsV + tok * RSV + lane_col) = vbuf[i];
+                    } else if constexpr (sizeof(CE) == 4) {
+                        // 4 fp32 values -> 4 hi + 4 lo bf16 (8 bytes each)
+                        uint32_t kh[2], kl[2], vh[2], vl[2];
+#pragma unroll
+                        for (int j = 0; j < 2; ++j) {
+                            split2_bf16(__uint_as_float(kbuf[i][2 * j]), __uint_as_float(kbuf[i][2 * j + 1]), kh[j],
+                                        kl[j]);
+                            split2_bf16(__uint_as_float(vbuf[i][2 * j]), __uint_as_float(vbuf[i][2 * j + 1]), vh[j],
+                                        vl[j]);
+                        }
+                        *reinterpret_cast<uint2*>(ldsK + tok * RS + lane_col) = uint2{kh[0], kh[1]};
+                        *reinterpret_cast<uint2*>(ldsKl + tok * RS + lane_col) = uint2{kl[0], kl[1]};
+                        *reinterpret_cast<uint2*>(ldsV + tok * RSV + lane_col) = uint2{vh[0], vh[1]};
+                        *reinterpret_cast<uint2*>(ldsVl + tok * RSV + lane_col) = uint2{vl[0], vl[1]};
+                    } else {
+                        // 8 fp16 values -> 8 hi + 8 lo bf16 (exact)
+                        u32x4 h, l;
+                        to_mt8<CE, T, true>(&kbuf[i], h, l);
+                        *reinterpret_cast<u32x4*>(ldsK + tok * RS + lane_col) = h;
+                        *reinterpret_cast<u32x4*>(ldsKl + tok * RS + lane_col) = l;
+                        to_mt8<CE, T, true>(&vbuf[i], h, l);
+                        *reinterpret_cast<u32x4*>(ldsV + tok * RSV + lane_col) = h;
+                        *reinterpret_cast<u32x4*>(ldsVl + tok * RSV + lane_col) = l;
+                    }
                 }
             };
 
@@ -241,6 +336,11 @@ __global__ __launch_bounds__(64) void paged_partial_kernel(PagedParams p) {
                 for (int dc = 0; dc < D / 16; ++dc) {
                     const u32x4 a = *reinterpret_cast<const u32x4*>(ldsK + l32 * RS + dc * 16 + hi * 8);
                     s = Ops::mma(as_vec8<Vec>(a), as_vec8<Vec>(qreg[dc]), s);
+                    if constexpr (SQ) s = Ops::mma(as_vec8<Vec>(a), as_vec8<Vec>(qlo[dc]), s);
+                    if constexpr (SC) {
+                        const u32x4 al = *reinterpret_cast<const u32x4*>(ldsKl + l32 * RS + dc * 16 + hi * 8);
+                        s = Ops::mma(as_vec8<Vec>(al), as_vec8<Vec>(qreg[dc]), s);
+                    }
                 }
                 float y[16];
 #pragma unroll
@@ -252,11 +352,16 @@ __global__ __launch_bounds__(64) void paged_partial_kernel(PagedParams p) {
                 }
 #pragma unroll
                 for (int c = 0; c < 2; ++c) {
-                    u32x4 pw;
-                    pw.x = pack2<T>(y[8 * c + 0], y[8 * c + 1]);
-                    pw.y = pack2<T>(y[8 * c + 2], y[8 * c + 3]);
-                    pw.z = pack2<T>(y[8 * c + 4], y[8 * c + 5]);
-                    pw.w = pack2<T>(y[8 * c + 6], y[8 * c + 7]);
+                    uint32_t ph[4], plo[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        if constexpr (SP)
+                            split2_bf16(y[8 * c + 2 * j], y[8 * c + 2 * j + 1], ph[j], plo[j]);
+                        else
+                            ph[j] = pack2<T>(y[8 * c + 2 * j], y[8 * c + 2 * j + 1]);
+                    }
+                    const u32x4 pw{ph[0], ph[1], ph[2], ph[3]};
+                    const u32x4 pl = SP ? u32x4{plo[0], plo[1], plo[2], plo[3]} : u32x4{0u, 0u, 0u, 0u};
                     const Vec bop = as_vec8<Vec>(pw);
 #pragma unroll
                     for (int dt = 0; dt < D / 32; ++dt) {
@@ -265,6 +370,14 @@ __global__ __launch_bounds__(64) void paged_partial_kernel(PagedParams p) {
                         const uint2 hi8 = lds_read_tr16(base + 8 * RSV);
                         const u32x4 aw{lo.x, lo.y, hi8.x, hi8.y};
                         oacc[dt] = Ops::mma(as_vec8<Vec>(aw), bop, oacc[dt]);
+                        if constexpr (SP) oacc[dt] = Ops::mma(as_vec8<Vec>(aw), as_vec8<Vec>(pl), oacc[dt]);
+                        if constexpr (SC) {
+                            const T* basel = ldsVl + (16 * c) * RSV + dt * 32 + v_tr_off;
+                            const uint2 lol = lds_read_tr16(basel);
+                            const uint2 hil = lds_read_tr16(basel + 8 * RSV);
+                            const u32x4 awl{lol.x, lol.y, hil.x, hil.y};
+                            oacc[dt] = Ops::mma(as_vec8<Vec>(awl), bop, oacc[dt]);
+                        }
                     }
                 }
                 __builtin_amdgcn_wave_barrier();
@@ -320,9 +433,9 @@ __global__ __launch_bounds__(D) void paged_merge_kernel(PagedParams p) {
     p.out[b * p.os[0] + hq * p.os[1] + d * p.os[2]] = static_cast<bf16>(o / (s + kEps));
 }
 
-// Waves of paged_partial_kernel<T, D, U> resident on the device at once (the
-// persistent grid), per device.
-template <typename T, int D, bool U>
+// Waves of paged_partial_kernel<QE, CE, D, U> resident on the device at once
+// (the persistent grid), per device.
+template <typename QE, typename CE, int D, bool U>
 int resident_waves() {
     static int cache[16] = {0};
     int dev = 0;
@@ -332,7 +445,7 @@ int resident_waves() {
         int cus = 0, per_cu = 0;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
             cus = 256;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_partial_kernel<T, D, U>, 64, 0) !=
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_partial_kernel<QE, CE, D, U>, 64, 0) !=
                 hipSuccess ||
             per_cu <= 0)
             per_cu = 1;
@@ -341,10 +454,10 @@ int resident_waves() {
     return cache[slot];
 }
 
-template <typename T, int D>
+template <typename QE, typename CE, int D>
 int launch_paged(PagedParams prm, hipStream_t st) {
-    const bool uniform = prm.P * (D / 8) >= 64;
-    const int resident = uniform ? resident_waves<T, D, true>() : resident_waves<T, D, false>();
+    const bool uniform = prm.P * (D * static_cast<int>(sizeof(CE)) / 16) >= 64;
+    const int resident = uniform ? resident_waves<QE, CE, D, true>() : resident_waves<QE, CE, D, false>();
     // The plan gives work to at most Tt / per waves, and Tt is at most
     // B * Hkv * ceil(max_pages * P / kTile): no more waves are launched.
     const int64_t max_tiles = static_cast<int64_t>(prm.B) * prm.Hkv *
@@ -352,11 +465,21 @@ int launch_paged(PagedParams prm, hipStream_t st) {
     prm.n_waves = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(resident, max_tiles / prm.per)));
     paged_plan_kernel<<<1, 256, 0, st>>>(prm);
     if (uniform)
-        paged_partial_kernel<T, D, true><<<prm.n_waves, 64, 0, st>>>(prm);
+        paged_partial_kernel<QE, CE, D, true><<<prm.n_waves, 64, 0, st>>>(prm);
     else
-        paged_partial_kernel<T, D, false><<<prm.n_waves, 64, 0, st>>>(prm);
+        paged_partial_kernel<QE, CE, D, false><<<prm.n_waves, 64, 0, st>>>(prm);
     paged_merge_kernel<D><<<static_cast<unsigned>(prm.B) * prm.Hq, prm.D, 0, st>>>(prm);
     return status_from_launch();
+}
+
+template <typename QE, typename CE>
+int launch_paged_d(int dp, const PagedParams& prm, hipStream_t st) {
+    switch (dp) {
+        case 32: return launch_paged<QE, CE, 32>(prm, st);
+        case 64: return launch_paged<QE, CE, 64>(prm, st);
+        case 128: return launch_paged<QE, CE, 128>(prm, st);
+        default: return launch_paged<QE, CE, 256>(prm, st);
+    }
 }
 
 // Minimum tiles per active wave: kSplitTok / kTile (few pieces, few
@@ -400,6 +523,17 @@ int launch_per(int B, int Hq, int Hkv, int max_pages, int page_size) {
                     split_for(static_cast<int64_t>(B) * Hkv, max_pages, page_size));
 }
 
+// q and cache types of a decode's dtype argument (SA_PAGED_DTYPES, or one
+// code for both); false for unsupported pairs.  Supported: bf16 / bf16,
+// fp16 / fp16, and fp32 q over fp32, bf16 or fp16 caches.
+bool paged_types(int dtype, int& qt, int& ct) {
+    qt = dtype & 0xFF;
+    ct = (dtype >> 8) == 0 ? qt : (dtype >> 8) - 1;
+    if (dtype < 0 || (dtype >> 16) != 0) return false;
+    if (qt == ct) return qt == SA_BF16 || qt == SA_F16 || qt == SA_F32;
+    return qt == SA_F32 && (ct == SA_BF16 || ct == SA_F16);
+}
+
 // Argument checks shared by both decode entry points (0 = launch, 1 =
 // nothing to do, < 0 = status).  max_pages becomes 0 when there are no pages.
 int validate_paged(const void* q, const void* k_cache, const void* v_cache, const void* out,
@@ -422,15 +556,18 @@ int validate_paged(const void* q, const void* k_cache, const void* v_cache, cons
     if (!q || !k_cache || !v_cache || !out || !block_table || !context_lens || !q_strides || !kv_strides ||
         !vv_strides || !o_strides)
         return SA_ERR_NULL_POINTER;
-    const auto ok16 = [](const int64_t* s, int n) {
+    int qt, ct;
+    if (!paged_types(dtype, qt, ct)) return SA_ERR_BAD_DTYPE;
+    // 16-byte rows: element strides that are multiples of 16 / element size
+    const auto ok16 = [](const int64_t* s, int n, int t) {
+        const int per = t == SA_F32 ? 4 : 8;
         for (int i = 0; i < n - 1; ++i)
-            if (s[i] % 8 != 0) return false;
+            if (s[i] % per != 0) return false;
         return s[n - 1] == 1;
     };
-    if (!ok16(q_strides, 4) || !ok16(kv_strides, 4) || !ok16(vv_strides, 4) || o_strides[2] != 1 ||
+    if (!ok16(q_strides, 4, qt) || !ok16(kv_strides, 4, ct) || !ok16(vv_strides, 4, ct) || o_strides[2] != 1 ||
         !aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache))
         return SA_ERR_BAD_STRIDE;
-    if (dtype != SA_BF16 && dtype != SA_F16) return SA_ERR_BAD_DTYPE;
     return 0;
 }
 
@@ -471,20 +608,13 @@ int run_paged(const void* q, const void* k_cache, const void* v_cache, void* out
     prm.n_pages = n_pages;
     prm.scale = scale;
     const int dp = D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 256;  // padded head dim of the kernels
-    if (dtype == SA_BF16) {
-        switch (dp) {
-            case 32: return launch_paged<bf16, 32>(prm, st);
-            case 64: return launch_paged<bf16, 64>(prm, st);
-            case 128: return launch_paged<bf16, 128>(prm, st);
-            default: return launch_paged<bf16, 256>(prm, st);
-        }
-    }
-    switch (dp) {
-        case 32: return launch_paged<f16, 32>(prm, st);
-        case 64: return launch_paged<f16, 64>(prm, st);
-        case 128: return launch_paged<f16, 128>(prm, st);
-        default: return launch_paged<f16, 256>(prm, st);
-    }
+    int qt, ct;
+    paged_types(dtype, qt, ct);
+    if (qt == SA_BF16) return launch_paged_d<bf16, bf16>(dp, prm, st);
+    if (qt == SA_F16) return launch_paged_d<f16, f16>(dp, prm, st);
+    if (ct == SA_BF16) return launch_paged_d<float, bf16>(dp, prm, st);
+    if (ct == SA_F16) return launch_paged_d<float, f16>(dp, prm, st);
+    return launch_paged_d<float, float>(dp, prm, st);
 }
 
 }  // namespace

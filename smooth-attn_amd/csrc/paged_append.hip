@@ -6,7 +6,8 @@
 // For sequence b with current length ctx_b and new rows t < n_new:
 //   pos = ctx_b + t,  page = block_table[b, pos / P],  slot = pos % P
 //   k_cache[page, h, slot, :] = k_new[b, h, t, :]   (same for v)
-// One thread per 16-byte chunk of a new row, for K and V.  Positions whose
+// One thread per 16-byte chunk of a new row, for K and V (fp32, bf16 or fp16
+// rows: the copy moves bytes and never converts).  Positions whose
 // page index is past max_pages, or whose block-table entry is outside
 // [0, n_pages), are skipped: nothing is written outside the caches.
 #include "common.hpp"
@@ -24,12 +25,13 @@ struct AppendParams {
     int64_t ns[4], kcs[4], vcs[4];  // strides: new (b,h,t,d); caches (page,h,slot,d)
     int64_t bt_stride;
     int B, Hkv, n_new, D, P, max_pages, n_pages;
+    int esize;  // bytes per element
 };
 
 __global__ __launch_bounds__(256) void paged_append_kernel(AppendParams p, int64_t n_chunks) {
     const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
     if (gid >= n_chunks) return;
-    const int cpr = p.D / 8;  // 16-byte chunks per row (16-bit elements)
+    const int cpr = p.D * p.esize / 16;  // 16-byte chunks per row
     const int64_t row = gid / cpr;
     const int c = static_cast<int>(gid - row * cpr);
     const int t = static_cast<int>(row % p.n_new);
@@ -44,16 +46,21 @@ __global__ __launch_bounds__(256) void paged_append_kernel(AppendParams p, int64
     const int phys = p.table[b * p.bt_stride + page_idx];
     if (phys < 0 || phys >= p.n_pages) return;
     const int slot = static_cast<int>(pos - page_idx * p.P);
-    const int64_t src = b * p.ns[0] + h * p.ns[1] + t * p.ns[2] + c * 8;
-    const int64_t dk = phys * p.kcs[0] + h * p.kcs[1] + slot * p.kcs[2] + c * 8;
-    const int64_t dv = phys * p.vcs[0] + h * p.vcs[1] + slot * p.vcs[2] + c * 8;
-    const uint16_t* kn = static_cast<const uint16_t*>(p.k_new);
-    const uint16_t* vn = static_cast<const uint16_t*>(p.v_new);
-    *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.k_cache) + dk) = *reinterpret_cast<const u32x4*>(kn + src);
-    *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.v_cache) + dv) = *reinterpret_cast<const u32x4*>(vn + src);
+    // byte offsets
+    const int64_t src = (b * p.ns[0] + h * p.ns[1] + t * p.ns[2]) * p.esize + c * 16;
+    const int64_t dk = (phys * p.kcs[0] + h * p.kcs[1] + slot * p.kcs[2]) * p.esize + c * 16;
+    const int64_t dv = (phys * p.vcs[0] + h * p.vcs[1] + slot * p.vcs[2]) * p.esize + c * 16;
+    const char* kn = static_cast<const char*>(p.k_new);
+    const char* vn = static_cast<const char*>(p.v_new);
+    *reinterpret_cast<u32x4*>(static_cast<char*>(p.k_cache) + dk) = *reinterpret_cast<const u32x4*>(kn + src);
+    *reinterpret_cast<u32x4*>(static_cast<char*>(p.v_cache) + dv) = *reinterpret_cast<const u32x4*>(vn + src);
 }
 
-bool rows16(const int64_t* s) { return s[3] == 1 && s[0] % 8 == 0 && s[1] % 8 == 0 && s[2] % 8 == 0; }
+// 16-byte rows: unit stride along D, the other strides multiples of 16 bytes
+bool rows16(const int64_t* s, int esize) {
+    const int per = 16 / esize;
+    return s[3] == 1 && s[0] % per == 0 && s[1] % per == 0 && s[2] % per == 0;
+}
 
 }  // namespace
 }  // namespace sa
@@ -64,14 +71,16 @@ extern "C" int sa_paged_kv_append(const void* k_new, const void* v_new, void* k_
                                   const int64_t* new_strides, const int64_t* kc_strides,
                                   const int64_t* vc_strides, int64_t bt_stride, int dtype, sa_stream_t stream) {
     using namespace sa;
-    if (dtype != SA_BF16 && dtype != SA_F16) return SA_ERR_BAD_DTYPE;
+    if (dtype != SA_BF16 && dtype != SA_F16 && dtype != SA_F32) return SA_ERR_BAD_DTYPE;
+    const int esize = dtype == SA_F32 ? 4 : 2;
     if (B < 0 || Hkv <= 0 || n_new < 0 || max_pages < 0 || n_pages < 0 || page_size <= 0) return SA_ERR_BAD_SHAPE;
-    if (D <= 0 || D % 8 != 0) return SA_ERR_UNSUPPORTED;
+    if (D <= 0 || (D * esize) % 16 != 0) return SA_ERR_UNSUPPORTED;
     if (B == 0 || n_new == 0 || max_pages == 0 || n_pages == 0) return 0;
     if (!k_new || !v_new || !k_cache || !v_cache || !block_table || !context_lens || !new_strides || !kc_strides ||
         !vc_strides)
         return SA_ERR_NULL_POINTER;
-    if (!rows16(new_strides) || !rows16(kc_strides) || !rows16(vc_strides) || bt_stride < max_pages ||
+    if (!rows16(new_strides, esize) || !rows16(kc_strides, esize) || !rows16(vc_strides, esize) ||
+        bt_stride < max_pages ||
         !aligned16(k_new) || !aligned16(v_new) || !aligned16(k_cache) || !aligned16(v_cache))
         return SA_ERR_BAD_STRIDE;
     AppendParams prm{};
@@ -94,7 +103,8 @@ extern "C" int sa_paged_kv_append(const void* k_new, const void* v_new, void* k_
     prm.P = page_size;
     prm.max_pages = max_pages;
     prm.n_pages = n_pages;
-    const int64_t n_chunks = static_cast<int64_t>(B) * Hkv * n_new * (D / 8);
+    prm.esize = esize;
+    const int64_t n_chunks = static_cast<int64_t>(B) * Hkv * n_new * (D * esize / 16);
     const dim3 grid(static_cast<unsigned>((n_chunks + 255) / 256));
     paged_append_kernel<<<grid, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(prm, n_chunks);
     return status_from_launch();

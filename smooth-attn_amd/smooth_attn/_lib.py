@@ -17,6 +17,14 @@ LIB_PATH = Path(os.environ.get("SMOOTH_ATTN_LIB") or Path(__file__).resolve().pa
 
 # Element-type codes (SA_F32 ... in the header).
 SA_F32, SA_F16, SA_BF16, SA_FP8_E4M3FN = 0, 1, 2, 3
+
+
+def paged_dtypes(q_type: int, cache_type: int) -> int:
+    """SA_PAGED_DTYPES(q_type, cache_type): the paged decode's dtype argument
+    for q and caches of different element types."""
+    return q_type | ((cache_type + 1) << 8)
+
+
 # SA_PAGED_NOALLOC_SCRATCH_BYTES: the fixed scratch of sa_paged_decode_noalloc.
 PAGED_NOALLOC_SCRATCH_BYTES = 64 << 20
 

@@ -970,6 +970,23 @@ def _check_paging_args(B, D, k_cache, v_cache, block_table, context_lens):
             raise ValueError("block_table and context_lens must be integer tensors on the caches' device")
 
 
+_PAGED_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
+
+
+def _paged_dtype_code(q_dtype, k_dtype, v_dtype):
+    """The C ABI's dtype argument for a decode over these tensors.  The
+    reference upcasts q, K and V to fp32 whatever they are
+    (kernels.py:2716-2717, :2746, :2765): here q may be fp32, bf16 or fp16
+    and the caches fp32, bf16 or fp16 of one dtype; a q whose dtype differs
+    from the caches' runs as fp32 (an exact conversion)."""
+    if q_dtype not in _PAGED_DTYPES or k_dtype not in _PAGED_DTYPES or v_dtype != k_dtype:
+        raise ValueError("paged decode expects fp32, bf16 or fp16 q and fp32, bf16 or fp16 caches of one dtype, "
+                         f"got q {q_dtype}, k_cache {k_dtype}, v_cache {v_dtype}")
+    if q_dtype == k_dtype:
+        return _DTYPE_CODE[q_dtype]
+    return _lib.paged_dtypes(_lib.SA_F32, _DTYPE_CODE[k_dtype])
+
+
 def sp2norm_paged_attention(q, k_cache, v_cache, block_table, context_lens, *, scale=None, block_size=16):
     """Paged single-token decode — kernels.py:2776-2829 (output bf16 [B, Hq, D])."""
     assert q.ndim == 4 and q.shape[2] == 1, "Decode: q must be [B, H, 1, D]"
@@ -989,8 +1006,9 @@ def sp2norm_paged_attention(q, k_cache, v_cache, block_table, context_lens, *, s
         scale = 1.0 / math.sqrt(D)
     _check_same_device("q", q, k_cache=k_cache, v_cache=v_cache, block_table=block_table,
                        context_lens=context_lens)
-    if q.dtype not in (torch.bfloat16, torch.float16) or k_cache.dtype != q.dtype or v_cache.dtype != q.dtype:
-        raise ValueError("paged decode expects bf16 or fp16 q and caches of one dtype")
+    code = _paged_dtype_code(q.dtype, k_cache.dtype, v_cache.dtype)
+    if q.dtype != k_cache.dtype:
+        q = q.float()  # exact; fp32 q runs over fp32, bf16 or fp16 caches
     _check_paging_args(B, D, k_cache, v_cache, block_table, context_lens)
     q = _flash_operand(q)
     k_cache = _flash_operand(k_cache)
@@ -1009,7 +1027,7 @@ def sp2norm_paged_attention(q, k_cache, v_cache, block_table, context_lens, *, s
             context_lens.data_ptr(), B, H_q, H_kv, D, block_size, max_blocks_per_seq, k_cache.shape[0],
             _lib.strides(q),
             _lib.strides(k_cache), _lib.strides(v_cache), _lib.strides(out), block_table.stride(0),
-            float(scale), _DTYPE_CODE[q.dtype], ws.data_ptr(), ws.numel() * 4, _stream(q),
+            float(scale), code, ws.data_ptr(), ws.numel() * 4, _stream(q),
         )
     _lib.check(st, "sa_paged_decode")
     return out
@@ -1029,11 +1047,12 @@ def sp2norm_paged_kv_append(k_cache, v_cache, k_new, v_new, block_table, context
     assert k_cache.shape[2] == block_size
     _check_same_device("k_cache", k_cache, v_cache=v_cache, k_new=k_new, v_new=v_new, block_table=block_table,
                        context_lens=context_lens)
-    if k_cache.dtype not in (torch.bfloat16, torch.float16) or v_cache.dtype != k_cache.dtype:
-        raise ValueError("paged caches must be bf16 or fp16 of one dtype")
+    if k_cache.dtype not in _PAGED_DTYPES or v_cache.dtype != k_cache.dtype:
+        raise ValueError("paged caches must be fp32, bf16 or fp16 of one dtype")
     _check_paging_args(B, D, k_cache, v_cache, block_table, context_lens)
+    per = 16 // k_cache.element_size()
     for t in (k_cache, v_cache):
-        if t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:-1]) or t.data_ptr() % 16:
+        if t.stride(-1) != 1 or any(s % per for s in t.stride()[:-1]) or t.data_ptr() % 16 or D % per:
             raise ValueError("paged caches need 16-byte aligned rows with unit stride along D")
     k_new = _flash_operand(k_new.to(k_cache.dtype))
     v_new = _flash_operand(v_new.to(k_cache.dtype))

@@ -246,3 +246,29 @@ def test_flash_16bit_head_dims():
         assert fp8(D) == -6, D
         assert rope(D) == -6, D
     assert fp8(64) == 0 and rope(64) == 0
+
+
+def test_paged_decode_dtype_pairs():
+    # SA_PAGED_DTYPES(q, cache): fp32 q over fp32 / bf16 / fp16 caches, or
+    # one 16-bit type for both; other pairs are refused before any HIP call
+    lib = _lib.load()
+    dummy = ctypes.c_void_p(16)
+    D = 64
+    s4 = (ctypes.c_int64 * 4)(8 * D, D, D, 1)
+    o = (ctypes.c_int64 * 3)(8 * D, D, 1)
+    pd = _lib.paged_dtypes
+    assert pd(_lib.SA_F32, _lib.SA_BF16) == 0 | (3 << 8)
+    for code in (pd(_lib.SA_BF16, _lib.SA_F32), pd(_lib.SA_BF16, _lib.SA_F16), pd(_lib.SA_F16, _lib.SA_BF16),
+                 pd(_lib.SA_F16, _lib.SA_F32), _lib.SA_FP8_E4M3FN, pd(_lib.SA_F32, _lib.SA_FP8_E4M3FN), 7,
+                 1 << 16, -1):
+        st = lib.sa_paged_decode(dummy, dummy, dummy, dummy, dummy, dummy, 2, 8, 2, D, 16, 4, 8,
+                                 s4, s4, s4, o, 4, 0.1, code, dummy, 1 << 30, None)
+        assert st == -3, code  # SA_ERR_BAD_DTYPE
+        st = lib.sa_paged_decode_noalloc(dummy, dummy, dummy, dummy, dummy, dummy, 2, 8, 2, D, 16, 4, 8,
+                                         s4, s4, s4, o, 4, 0.1, code, None)
+        assert st == -3, code
+    # fp32 rows need element strides that are multiples of 4, 16-bit rows of 8
+    s_odd = (ctypes.c_int64 * 4)(8 * 68, 68, 68, 1)
+    st = lib.sa_paged_decode(dummy, dummy, dummy, dummy, dummy, dummy, 2, 8, 2, D, 16, 4, 8,
+                             s4, s_odd, s_odd, o, 4, 0.1, _lib.SA_BF16, dummy, 1 << 30, None)
+    assert st == -5  # SA_ERR_BAD_STRIDE

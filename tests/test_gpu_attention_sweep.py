@@ -1,14 +1,16 @@
 """Randomised parity sweep of the fused attention (forward and backward)
 against the float64 oracle, over combinations the fixed cases do not
-enumerate: dtype (bf16, fp16, fp32), head dims 8..256 (masked below a
-kernel's size, fp32 padded, and the D = 256 kernels), GQA group sizes, windows, query counts around the
-32/64/128/256-row tile edges, and scales (GPU).
+enumerate: dtype (bf16, fp16, fp32), head dims 8..256 (run on the next
+kernel up with the columns past D masked, and the D = 256 kernels), GQA
+group sizes, windows, query counts around the 32/64/128/256-row tile edges,
+and scales (GPU).
 
-Bars, as in the per-path tests: O and the gradients within 1e-2 (16-bit) or
-1e-5 (fp32) of max|oracle|, row sums within 1e-5.  dQ and dK are judged
-against the gradients' natural scale max|dV|: where every query sees a
-single key (T = 1 or window 1) they vanish exactly and the kernels return
-fp32 rounding noise of dP - delta.  Backward oracle:
+Bars, as in the per-path tests: O within 1e-2 (16-bit) or 1e-5 (fp32) of
+max|oracle|, row sums within 1e-5, and each gradient within the same bar of
+max(max|oracle|, 1e-2).  Where every query sees a single key (T = 1 or
+window 1) the exact dQ and dK vanish and the kernels return fp32 rounding
+noise of dP - delta, so there dQ and dK are judged against the gradients'
+natural scale max|dV| instead.  Backward oracle:
 oracle.eager.flash_attention_bwd on GQA-expanded K/V, fed the HIP forward's
 O, with dK and dV summed over each group.
 """
@@ -66,7 +68,8 @@ def test_random_attention_cases(sweep_seed):
         rk = rk.reshape(B, hkv, G, T, D).sum(2)
         rv = rv.reshape(B, hkv, G, T, D).sum(2)
         tol = 1e-5 if dt == torch.float32 else 1e-2
-        gscale = max(float(rv.abs().max()), 1e-2)
+        single_key = T == 1 or W == 1
+        gscale = max(float(rv.abs().max()), 1e-2) if single_key else 1e-2
         assert _rel(o, ref, 1e-30) <= tol, what
         assert _rel(rs, ref_rs, 1e-30) <= 1e-5, what
         assert _rel(dv, rv, 1e-2) <= tol, what

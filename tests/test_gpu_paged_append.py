@@ -1,6 +1,6 @@
 """Paged-KV cache writer (HIP) against the CPU oracle (GPU).
 
-Bit-exact: the writer only moves 16-bit values, so the device caches must
+Bit-exact: the writer only moves bytes (fp32, bf16 or fp16 rows), so the device caches must
 equal oracle.paging.append_kv on the same inputs exactly; decode after a
 sequence of appends must equal decode of the cache built in one piece.
 """
@@ -18,8 +18,12 @@ def _g(seed):
     return torch.Generator().manual_seed(seed)
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("P,D,n_new", [(16, 128, 1), (16, 64, 7), (8, 32, 33), (32, 128, 5)])
+CASES = [(dt, P, D, n) for dt in (torch.bfloat16, torch.float16, torch.float32)
+         for P, D, n in ((16, 128, 1), (16, 64, 7), (8, 32, 33), (32, 128, 5))]
+CASES += [(torch.float32, 4, 12, 9), (torch.bfloat16, 4, 24, 9)]  # 16-byte rows: fp32 D % 4, 16-bit D % 8
+
+
+@pytest.mark.parametrize("dtype,P,D,n_new", CASES)
 def test_append_matches_oracle(dtype, P, D, n_new):
     B, H, T = 3, 2, 70
     k = torch.randn(B, H, T, D, generator=_g(P + D)).to(dtype)
@@ -50,12 +54,13 @@ def test_append_skips_rows_outside_table_and_cache():
     assert torch.equal(kd.cpu(), ref_k) and torch.equal(vd.cpu(), ref_v)
 
 
-def test_decode_after_appends_equals_prebuilt_cache():
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_decode_after_appends_equals_prebuilt_cache(dtype):
     # prefill 50 tokens, then 3 single-token decode steps, against a cache built at once
     B, Hq, Hkv, P, D, T = 2, 8, 2, 16, 128, 53
-    k = torch.randn(B, Hkv, T, D, generator=_g(11)).bfloat16()
-    v = torch.randn(B, Hkv, T, D, generator=_g(12)).bfloat16()
-    q = torch.randn(B, Hq, 1, D, generator=_g(13)).bfloat16()
+    k = torch.randn(B, Hkv, T, D, generator=_g(11)).to(dtype)
+    v = torch.randn(B, Hkv, T, D, generator=_g(12)).to(dtype)
+    q = torch.randn(B, Hq, 1, D, generator=_g(13)).to(dtype)
     full_k, full_v, table, lens = paging.build_paged_cache(k, v, P, shuffle=True, generator=_g(14))
     kd = torch.zeros_like(full_k).to(DEV)
     vd = torch.zeros_like(full_v).to(DEV)
