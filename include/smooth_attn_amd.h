@@ -237,7 +237,8 @@ int sa_flash_fp8_fwd(const void* q8, const void* k8, const void* v, void* o,
  * [B, H, T, D] buffer out: for each pair (d, d + D/2) of row t,
  * a' = a cos - b sin, b' = b cos + a sin in fp32 with cos/sin = fp32
  * contiguous [T, D/2] tables, rounded to the input type.  D a multiple of
- * 16.  RoPE attention at head dims other than 32, 64 and 128 is this
+ * 16; B * H * T * D / 16 (one work-item per pair) below 2^32, else
+ * SA_ERR_BAD_SHAPE.  RoPE attention at head dims other than 32, 64 and 128 is this
  * rotation of Q and K followed by sa_flash_fwd.
  * Replaces the rotation step of _sp2norm_rope_flash_fwd_kernel
  * (kernels.py:2104-2224), which the reference runs only inside the fused
@@ -348,8 +349,11 @@ int sa_paged_decode(const void* q, const void* k_cache, const void* v_cache,
  * bytes plus the plan over 64 MiB) it returns SA_ERR_WORKSPACE.  Nothing in
  * the array needs to start at zero (the plan kernel writes what the other
  * kernels read).  Calls that overlap on one device (other streams, other
- * host threads) share the array and race: serialise them.  Arguments and
- * result as sa_paged_decode.
+ * host threads) share the array and race: serialise them.  The first call
+ * on a device (and the first per element type and head-dim class) looks up
+ * the array's address and the kernels' occupancy on the host: make it
+ * before capturing the call into a HIP graph.  Arguments and result as
+ * sa_paged_decode.
  */
 int sa_paged_decode_noalloc(const void* q, const void* k_cache,
                             const void* v_cache, void* out,

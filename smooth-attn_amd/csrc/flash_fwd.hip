@@ -875,8 +875,10 @@ extern "C" int sa_rope_rotate(const void* x, void* out, const float* cos_table, 
         return SA_ERR_BAD_STRIDE;
     const int64_t n_pairs = static_cast<int64_t>(B) * H * T * (D / 16);
     if (n_pairs == 0) return 0;
+    // one work-item per pair: the dispatch's grid x block count is 32-bit
     if ((n_pairs + 255) / 256 > INT32_MAX) return SA_ERR_BAD_SHAPE;
     const dim3 grid(static_cast<unsigned>((n_pairs + 255) / 256));
+    if (!grid_fits(grid, dim3(256))) return SA_ERR_BAD_SHAPE;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     if (dtype == SA_F32)
         rope_rotate_any<float><<<grid, 256, 0, st>>>(static_cast<const float*>(x), static_cast<float*>(out),

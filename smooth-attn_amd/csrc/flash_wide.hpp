@@ -1,5 +1,6 @@
-// 16-bit fused attention at head dim 256, reached from sa_flash_fwd /
-// sa_flash_bwd when D is 256 and dtype SA_BF16 or SA_F16.
+// 16-bit fused attention on the kernels built for head dim 256, reached from
+// sa_flash_fwd / sa_flash_bwd for SA_BF16 or SA_F16 head dims 136..256
+// (multiples of 8; columns past D are masked).
 #pragma once
 
 #include "common.hpp"

@@ -729,8 +729,8 @@ def _sp2norm_rope_flash_fwd(q, k, v, cos, sin, scale, n_kv_groups=1, window_size
     64 and 128 rotate Q in registers inside the fused kernel (K once into a
     workspace); fp32, and other head dims that are multiples of 16 up to
     256, rotate Q and K by sa_rope_rotate and run the plain fused forward
-    (fp32 head dims other than 32 / 64 / 128 / 256 zero-padded after the
-    rotation)."""
+    (whose kernels take those head dims unpadded, reading only their
+    columns)."""
     _check_same_device("q", q, k=k, v=v, cos=cos, sin=sin, o=o)
     B, H_q, T, D = q.shape
     H_kv = k.shape[1]
@@ -910,18 +910,20 @@ def _fp8_wide_fwd(q8, k8, v8, q_scale, k_scale, v_scale, attn_scale, n_kv_groups
     """fp8 attention at head dims 129..256: the e4m3fn codes are widened to
     bf16 (exact: every e4m3fn value is a bf16 value), the bf16 head-dim-256
     kernels run with the dequantisation folded into the score scale
-    (q_s * k_s * attn_scale), and fp8 V's scale multiplies the output.  The
-    scales are read on the host here (one synchronisation, as the
-    reference's entry point makes three)."""
-    qs = float(q_scale.reshape(-1)[0]) if isinstance(q_scale, torch.Tensor) else float(q_scale)
-    ks = float(k_scale.reshape(-1)[0]) if isinstance(k_scale, torch.Tensor) else float(k_scale)
-    s_eff = float(attn_scale) * qs * ks
-    o, row_sums = _sp2norm_flash_fwd(q8.to(torch.bfloat16), k8.to(torch.bfloat16), v8.to(torch.bfloat16), s_eff,
-                                     n_kv_groups, window_size)
-    if v8.dtype == torch.float8_e4m3fn and v_scale is not None:
-        vs = float(v_scale.reshape(-1)[0]) if isinstance(v_scale, torch.Tensor) else float(v_scale)
-        o = (o.float() * vs).to(torch.bfloat16)
-    return o, row_sums
+    (q_s * k_s * attn_scale), and fp8 V is widened as v_s * V rounded to
+    bf16, so the output is rounded once, at the kernel's store (the
+    reference applies v_s to each fp32 P V product, kernels.py:2579;
+    rounding V instead leaves per-key errors that average over the keys).
+    Device scales are read on the host in one transfer (one
+    synchronisation, where the reference's entry point makes three)."""
+    scale_v = v8.dtype == torch.float8_e4m3fn and v_scale is not None
+    given = [q_scale, k_scale] + ([v_scale] if scale_v else [])
+    on_dev = [t.reshape(-1)[:1].float() for t in given if isinstance(t, torch.Tensor)]
+    read = iter(torch.cat(on_dev).tolist() if on_dev else [])
+    vals = [next(read) if isinstance(t, torch.Tensor) else float(t) for t in given]
+    s_eff = float(attn_scale) * vals[0] * vals[1]
+    vb = (v8.float() * vals[2]).to(torch.bfloat16) if scale_v else v8.to(torch.bfloat16)
+    return _sp2norm_flash_fwd(q8.to(torch.bfloat16), k8.to(torch.bfloat16), vb, s_eff, n_kv_groups, window_size)
 
 
 def sp2norm_fp8_flash_attention(q, k, v, *, scale=None, window_size=0, quantize_v=True):

@@ -271,7 +271,11 @@ def test_fp8_forward_head_dims_below_128(D):
 def test_fp8_forward_head_dims_above_128(D, v_fp8):
     # head dims 129..256: codes widened to bf16 (exact) on the D = 256 bf16
     # kernels, so the scores are exact-product fp32 sums and the row sums
-    # meet 1e-5; with fp8 V the output is rounded once more after v_scale
+    # meet 1e-5; fp8 V is widened as v_s * V in bf16, so the output is
+    # rounded once.  Held to 6.5e-3 instead of 1e-2: a one-key row carries
+    # three roundings of at most 2^-9 (bf16 P, as in the reference; v_s V;
+    # the output), 5.9e-3 of max|O|, where rounding O again after applying
+    # v_s to the bf16 output would add a fourth (7.8e-3)
     q, k, v = _fp8_case(1, 4, 2, 150, D, seed=D + v_fp8)
     q8, qs = eager.quantize_to_fp8(q)
     k8, ks = eager.quantize_to_fp8(k)
@@ -285,7 +289,7 @@ def test_fp8_forward_head_dims_above_128(D, v_fp8):
     ref, ref_rs = eager.fp8_flash_attention_eager(q8, k8, vv, qs, ks, vs, scale, window_size=40,
                                                   return_row_sums=True)
     assert o.shape == (1, 4, 150, D) and o.dtype == torch.bfloat16
-    assert rel_err(o, ref) <= 1e-2
+    assert rel_err(o, ref) <= 6.5e-3
     assert rel_err(rs, ref_rs) <= 1e-5
     out = smooth_attn.sp2norm_fp8_flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), quantize_v=v_fp8)
     assert out.shape == (1, 4, 150, D) and not out.isnan().any()

@@ -32,18 +32,24 @@ def rel_err(got, ref):
     return float((got - ref).abs().max() / ref.abs().max().clamp(min=1e-30))
 
 
+def call_noalloc(out, q, kc, vc, table, lens, page_size, stream=None):
+    """sa_paged_decode_noalloc into ``out`` on ``stream`` (default: the current one)."""
+    B, Hq, _, D = q.shape
+    dtype = {torch.bfloat16: _lib.SA_BF16, torch.float16: _lib.SA_F16}[q.dtype]
+    raw = torch._C._cuda_getCurrentRawStream(q.device.index) if stream is None else stream.cuda_stream
+    st = _lib.load().sa_paged_decode_noalloc(
+        q.data_ptr(), kc.data_ptr(), vc.data_ptr(), out.data_ptr(), table.data_ptr(), lens.data_ptr(), B, Hq,
+        kc.shape[1], D, page_size, table.shape[1], kc.shape[0], _lib.strides(q), _lib.strides(kc),
+        _lib.strides(vc), _lib.strides(out), table.stride(0), 1.0 / math.sqrt(D), dtype, raw)
+    _lib.check(st, "sa_paged_decode_noalloc")
+    return out
+
+
 def decode_noalloc(q, kc, vc, table, lens, page_size):
     """sp2norm_paged_attention's arguments, through sa_paged_decode_noalloc."""
     B, Hq, _, D = q.shape
     out = torch.empty(B, Hq, D, device=q.device, dtype=torch.bfloat16)
-    dtype = {torch.bfloat16: _lib.SA_BF16, torch.float16: _lib.SA_F16}[q.dtype]
-    st = _lib.load().sa_paged_decode_noalloc(
-        q.data_ptr(), kc.data_ptr(), vc.data_ptr(), out.data_ptr(), table.data_ptr(), lens.data_ptr(), B, Hq,
-        kc.shape[1], D, page_size, table.shape[1], kc.shape[0], _lib.strides(q), _lib.strides(kc),
-        _lib.strides(vc), _lib.strides(out), table.stride(0), 1.0 / math.sqrt(D), dtype,
-        torch._C._cuda_getCurrentRawStream(q.device.index))
-    _lib.check(st, "sa_paged_decode_noalloc")
-    return out
+    return call_noalloc(out, q, kc, vc, table, lens, page_size)
 
 
 def make_case(B, Hq, Hkv, D, P, max_ctx, seed, dtype=torch.bfloat16, table_pages=None):
@@ -117,3 +123,38 @@ def test_noalloc_page_sizes_and_head_dims(P, D, dtype):
     assert torch.equal(got, want)
     ref = eager.paged_decode_eager(*(t.double() if t.is_floating_point() else t for t in cpu))
     assert rel_err(got, ref) <= 1e-2
+
+
+def test_noalloc_replays_under_graph_capture_and_allocates_nothing():
+    # after one eager call (the first call on a device looks up the scratch
+    # address and sizes the launch on the host), the call allocates no
+    # device memory and can be captured in a HIP graph: every replay equals
+    # the eager output bit for bit, also when other allocation-free calls on
+    # other inputs (which overwrite the shared scratch) run between replays
+    cpu, dev = make_case(8, 32, 8, 128, 16, 2000, seed=21)
+    want = decode_noalloc(*dev, 16)
+    other = make_case(3, 8, 2, 128, 16, 500, seed=22)[1]
+    out_other = torch.empty(3, 8, 128, device=DEV, dtype=torch.bfloat16)
+    call_noalloc(out_other, *other, 16)
+    out = torch.zeros_like(want)
+    torch.cuda.synchronize()
+    before_torch = torch.cuda.memory_allocated()
+    before_free = torch.cuda.mem_get_info()[0]
+    call_noalloc(out, *dev, 16)
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] == before_free
+    assert torch.cuda.memory_allocated() == before_torch
+    assert torch.equal(out, want)
+
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.graph(graph, stream=stream):
+        call_noalloc(out, *dev, 16, stream=stream)
+    for i in range(4):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), i
+        call_noalloc(out_other, *other, 16)  # eager work on the shared scratch between replays
+        torch.cuda.synchronize()
