@@ -377,7 +377,8 @@ def bench_next_rows(torch):
       MFMA, against the 157.3 TFLOP/s dense fp32 peak);
     - bf16 attention forward and backward at head dim 256, [4,16,4096,256]
       (config 3's FLOPs), and paged decode at head dim 256 on config 5's
-      layout with Hq 16 / Hkv 4 (config 5's bytes), and paged decode over
+      layout with Hq 16 / Hkv 4 (config 5's bytes), at head dim 512 with
+      Hq 8 / Hkv 2 (the same bytes), and paged decode over
       fp32 caches (and fp32 q over bf16 caches) on config 5's layout;
     - RoPE-fused attention forward on config 3's shape (K rotated once by a
       streaming kernel, Q in registers; the time includes the rotation),
@@ -450,6 +451,18 @@ def bench_next_rows(torch):
     us = med(lambda: sa.sp2norm_paged_attention(qd, kc, vc, table_d, lens_d))
     nb = paged_bytes(lens, Hq=16, D=256)
     out["paged_decode_d256"] = {"us": round(us, 1), "GBs": round(nb / us / 1e3, 1),
+                                "frac_hbm_peak": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)}
+    del kc, vc, qd
+    torch.cuda.empty_cache()
+
+    # paged decode at head dim 512 on config 5's layout with Hq 8 / Hkv 2
+    # (the same 4 KB of K and V per token; two waves per block split the columns)
+    kc = torch.randn(n_pages, 2, 16, 512, generator=gen, device=dev).to(torch.bfloat16)
+    vc = torch.randn(n_pages, 2, 16, 512, generator=gen, device=dev).to(torch.bfloat16)
+    qd = torch.randn(64, 8, 1, 512, generator=gen, device=dev).to(torch.bfloat16)
+    us = med(lambda: sa.sp2norm_paged_attention(qd, kc, vc, table_d, lens_d))
+    nb = paged_bytes(lens, Hq=8, D=512)
+    out["paged_decode_d512"] = {"us": round(us, 1), "GBs": round(nb / us / 1e3, 1),
                                 "frac_hbm_peak": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)}
     del kc, vc, qd
     torch.cuda.empty_cache()

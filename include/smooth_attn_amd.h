@@ -313,9 +313,10 @@ int64_t sa_paged_decode_workspace_size(int B, int Hq, int D, int max_pages,
  * caches (the reference upcasts q, K and V to fp32, kernels.py:2716-2717,
  * :2746, :2765; mixed pairs and fp32 run their products as bf16
  * hi + lo splits, about 16 significant bits).  Row strides (element units)
- * must be 16-byte multiples.  D a multiple of 8 in 8..256 (kernels for 32,
- * 64, 128 and 256; smaller D read only their own columns); page_size a
- * power of two (at most 2^20).
+ * must be 16-byte multiples.  D a multiple of 8 in 8..512 (kernels for 32,
+ * 64, 128, 256 and 512, the last with two waves per block splitting the
+ * columns; smaller D read only their own columns); page_size a power of
+ * two (at most 2^20).
  * workspace: at least sa_paged_decode_workspace_size() bytes, 16-byte
  * aligned, no initialisation needed (a plan kernel writes it).
  * Replaces sp2norm_paged_attention (kernels.py:2776-2829) and its kernel

@@ -144,15 +144,21 @@ __device__ __forceinline__ void to_mt8(const u32x4* w, u32x4& h, u32x4& l) {
     }
 }
 
-// The kernels run a padded head dim D (32, 64, 128 or 256); head dims
+// The kernels run a padded head dim D (32, 64, 128, 256 or 512); head dims
 // p.D < D (multiples of 8) load only their first p.D columns per row and
 // leave zeros in the rest of the LDS rows and Q registers, which add nothing
 // to the scores, and write only p.D output columns.
 // UNIFORM: every load instruction's tokens lie in one page (the tokens per
 // instruction divide the page size), so the page base is wave-uniform and
 // comes from v_readlane of the window's page-id register.
-template <typename QE, typename CE, int D, bool UNIFORM>
-__global__ __launch_bounds__(64) void paged_partial_kernel(PagedParams p) {
+// WPB > 1 (cache rows above 512 bytes: 16-bit D = 512 and fp32 D = 256 in
+// two parts, fp32 D = 512 in four): a block of WPB waves shares each piece;
+// wave v owns columns [v DF / WPB, (v + 1) DF / WPB) of K, V, Q and O, the
+// partial S^T tiles meet in LDS (two barriers per tile), and every wave forms
+// the same weights.
+template <typename QE, typename CE, int DF, bool UNIFORM, int WPB = 1>
+__global__ __launch_bounds__(64 * WPB) void paged_partial_kernel(PagedParams p) {
+    constexpr int D = DF / WPB;  // columns of this wave
     using Ty = PagedTypes<QE, CE>;
     using T = typename Ty::MT;
     using Ops = MfmaOps<T>;
@@ -171,13 +177,20 @@ __global__ __launch_bounds__(64) void paged_partial_kernel(PagedParams p) {
     constexpr int TPI = 64 / CPT;          // tokens per load instruction
     constexpr int NC = kTile * CPT / 64;   // chunks per lane per tile and tensor
     constexpr bool SQ = Ty::SPLIT_Q, SC = Ty::SPLIT_C, SP = Ty::SPLIT_P;
-    // MT tiles; the lo parts of split caches in the second pair
-    __shared__ __attribute__((aligned(16))) T ldsK[kTile * RS];
-    __shared__ __attribute__((aligned(16))) T ldsV[kTile * RSV];
-    __shared__ __attribute__((aligned(16))) T ldsKl[SC ? kTile * RS : 8];
-    __shared__ __attribute__((aligned(16))) T ldsVl[SC ? kTile * RSV : 8];
+    // MT tiles (one set per wave); the lo parts of split caches in the second pair
+    __shared__ __attribute__((aligned(16))) T ldsK_w[WPB][kTile * RS];
+    __shared__ __attribute__((aligned(16))) T ldsV_w[WPB][kTile * RSV];
+    __shared__ __attribute__((aligned(16))) T ldsKl_w[WPB][SC ? kTile * RS : 8];
+    __shared__ __attribute__((aligned(16))) T ldsVl_w[WPB][SC ? kTile * RSV : 8];
+    static_assert(WPB == 1 || kTile * RS * sizeof(T) >= 16 * 64 * 4, "a K tile holds a wave's 16 x 64 fp32 scores");
 
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & 63;
+    const int wv = WPB > 1 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : 0;
+    const int col_base = wv * D;  // first column of this wave
+    T* const ldsK = ldsK_w[wv];
+    T* const ldsV = ldsV_w[wv];
+    T* const ldsKl = ldsKl_w[wv];
+    T* const ldsVl = ldsVl_w[wv];
     const int hi = lane >> 5;
     const int l32 = lane & 31;
     const int w = blockIdx.x;
@@ -227,7 +240,7 @@ __global__ __launch_bounds__(64) void paged_partial_kernel(PagedParams p) {
             const QE* qrow = static_cast<const QE*>(p.q) + b * p.qs[0] + (hk * p.G + (live ? l32 : 0)) * p.qs[1];
 #pragma unroll
             for (int dc = 0; dc < D / 16; ++dc) {
-                const int d0 = dc * 16 + hi * 8;
+                const int d0 = col_base + dc * 16 + hi * 8;
                 u32x4 w[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};
                 if (live && d0 < p.D) {
                     w[0] = load16(qrow + d0);
@@ -260,7 +273,7 @@ __global__ __launch_bounds__(64) void paged_partial_kernel(PagedParams p) {
             // + EPC - 1).
             const int lane_tok = lane / CPT;
             const int lane_col = (lane % CPT) * EPC;
-            const bool col_live = lane_col < p.D;  // columns past the head dim stay zero
+            const bool col_live = col_base + lane_col < p.D;  // columns past the head dim stay zero
             u32x4 kbuf[NC], vbuf[NC];
             auto load_tile = [&](int t0) {
 #pragma unroll
@@ -280,8 +293,8 @@ __global__ __launch_bounds__(64) void paged_partial_kernel(PagedParams p) {
                         voff = phys * p.vs[0] + (t & pmask) * p.vs[2];
                     }
                     if (t < we && col_live) {
-                        kbuf[i] = load16(kc + koff + lane_col);
-                        vbuf[i] = load16(vc + voff + lane_col);
+                        kbuf[i] = load16(kc + koff + col_base + lane_col);
+                        vbuf[i] = load16(vc + voff + col_base + lane_col);
                     } else {
                         kbuf[i] = u32x4{0u, 0u, 0u, 0u};
                         vbuf[i] = u32x4{0u, 0u, 0u, 0u};
@@ -342,6 +355,27 @@ __global__ __launch_bounds__(64) void paged_partial_kernel(PagedParams p) {
                         s = Ops::mma(as_vec8<Vec>(al), as_vec8<Vec>(qreg[dc]), s);
                     }
                 }
+                if constexpr (WPB > 1) {
+                    // Add the other waves' partial scores (their columns of
+                    // q . k), exchanged through each wave's K tile, which the
+                    // S^T MFMAs above have finished reading (LDS operations of
+                    // a wave complete in order; the memory clobber keeps the
+                    // compiler from moving these stores above those reads).
+                    // The second barrier keeps the next tile's K stores after
+                    // the other waves' reads.
+                    asm volatile("" ::: "memory");
+                    uint32_t* mine = reinterpret_cast<uint32_t*>(ldsK);
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) mine[v * 64 + lane] = __float_as_uint(s[v]);
+                    __syncthreads();
+#pragma unroll
+                    for (int o = 1; o < WPB; ++o) {
+                        const uint32_t* other = reinterpret_cast<const uint32_t*>(ldsK_w[(wv + o) % WPB]);
+#pragma unroll
+                        for (int v = 0; v < 16; ++v) s[v] += __uint_as_float(other[v * 64 + lane]);
+                    }
+                    __syncthreads();
+                }
                 float y[16];
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
@@ -394,13 +428,13 @@ __global__ __launch_bounds__(64) void paged_partial_kernel(PagedParams p) {
             for (int dt = 0; dt < D / 32; ++dt) {
 #pragma unroll
                 for (int vg = 0; vg < 4; ++vg) {
-                    const int d0 = dt * 32 + vg * 8 + hi * 4;
+                    const int d0 = col_base + dt * 32 + vg * 8 + hi * 4;
                     if (d0 < p.D)  // p.D is a multiple of 8: groups of 4 are wholly in or out
                         *reinterpret_cast<float4*>(wo + d0) = float4{oacc[dt][vg * 4 + 0], oacc[dt][vg * 4 + 1],
                                                                      oacc[dt][vg * 4 + 2], oacc[dt][vg * 4 + 3]};
                 }
             }
-            if (hi == 0) p.ws_s[slot] = stot;
+            if (hi == 0 && wv == 0) p.ws_s[slot] = stot;
         }
         x = piece_end;
     }
@@ -433,9 +467,9 @@ __global__ __launch_bounds__(D) void paged_merge_kernel(PagedParams p) {
     p.out[b * p.os[0] + hq * p.os[1] + d * p.os[2]] = static_cast<bf16>(o / (s + kEps));
 }
 
-// Waves of paged_partial_kernel<QE, CE, D, U> resident on the device at once
-// (the persistent grid), per device.
-template <typename QE, typename CE, int D, bool U>
+// Blocks of paged_partial_kernel<QE, CE, D, U, WPB> resident on the device at
+// once (the persistent grid), per device.
+template <typename QE, typename CE, int D, bool U, int WPB>
 int resident_waves() {
     static int cache[16] = {0};
     int dev = 0;
@@ -445,7 +479,8 @@ int resident_waves() {
         int cus = 0, per_cu = 0;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
             cus = 256;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_partial_kernel<QE, CE, D, U>, 64, 0) !=
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_partial_kernel<QE, CE, D, U, WPB>, 64 * WPB,
+                                                         0) !=
                 hipSuccess ||
             per_cu <= 0)
             per_cu = 1;
@@ -456,8 +491,13 @@ int resident_waves() {
 
 template <typename QE, typename CE, int D>
 int launch_paged(PagedParams prm, hipStream_t st) {
-    const bool uniform = prm.P * (D * static_cast<int>(sizeof(CE)) / 16) >= 64;
-    const int resident = uniform ? resident_waves<QE, CE, D, true>() : resident_waves<QE, CE, D, false>();
+    // waves per block, each owning D / WPB columns: rows above 512 bytes are
+    // split into 512-byte parts (their tile registers would not fit one wave)
+    constexpr int RB = D * static_cast<int>(sizeof(CE));
+    constexpr int WPB = RB > 1024 ? 4 : RB > 512 ? 2 : 1;
+    const bool uniform = prm.P * (D / WPB * static_cast<int>(sizeof(CE)) / 16) >= 64;
+    const int resident =
+        uniform ? resident_waves<QE, CE, D, true, WPB>() : resident_waves<QE, CE, D, false, WPB>();
     // The plan gives work to at most Tt / per waves, and Tt is at most
     // B * Hkv * ceil(max_pages * P / kTile): no more waves are launched.
     const int64_t max_tiles = static_cast<int64_t>(prm.B) * prm.Hkv *
@@ -465,9 +505,9 @@ int launch_paged(PagedParams prm, hipStream_t st) {
     prm.n_waves = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(resident, max_tiles / prm.per)));
     paged_plan_kernel<<<1, 256, 0, st>>>(prm);
     if (uniform)
-        paged_partial_kernel<QE, CE, D, true><<<prm.n_waves, 64, 0, st>>>(prm);
+        paged_partial_kernel<QE, CE, D, true, WPB><<<prm.n_waves, 64 * WPB, 0, st>>>(prm);
     else
-        paged_partial_kernel<QE, CE, D, false><<<prm.n_waves, 64, 0, st>>>(prm);
+        paged_partial_kernel<QE, CE, D, false, WPB><<<prm.n_waves, 64 * WPB, 0, st>>>(prm);
     paged_merge_kernel<D><<<static_cast<unsigned>(prm.B) * prm.Hq, prm.D, 0, st>>>(prm);
     return status_from_launch();
 }
@@ -478,7 +518,8 @@ int launch_paged_d(int dp, const PagedParams& prm, hipStream_t st) {
         case 32: return launch_paged<QE, CE, 32>(prm, st);
         case 64: return launch_paged<QE, CE, 64>(prm, st);
         case 128: return launch_paged<QE, CE, 128>(prm, st);
-        default: return launch_paged<QE, CE, 256>(prm, st);
+        case 256: return launch_paged<QE, CE, 256>(prm, st);
+        default: return launch_paged<QE, CE, 512>(prm, st);
     }
 }
 
@@ -545,7 +586,7 @@ int validate_paged(const void* q, const void* k_cache, const void* v_cache, cons
     // any power of two: a tile of 32 tokens spans 32 / P pages (P < 32) or
     // lies in one page; a window of 64 page ids always covers whole tiles
     if (page_size <= 0 || (page_size & (page_size - 1)) != 0 || page_size > (1 << 20)) return SA_ERR_UNSUPPORTED;
-    if (D < 8 || D > 256 || D % 8 != 0) return SA_ERR_UNSUPPORTED;
+    if (D < 8 || D > 512 || D % 8 != 0) return SA_ERR_UNSUPPORTED;
     if (B == 0) return 1;
     if (n_pages == 0) max_pages = 0;  // no cache: every context is empty
     // The plan keeps token positions, tile counts and their prefix sums over
@@ -607,7 +648,7 @@ int run_paged(const void* q, const void* k_cache, const void* v_cache, void* out
     prm.max_pages = max_pages;
     prm.n_pages = n_pages;
     prm.scale = scale;
-    const int dp = D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 256;  // padded head dim of the kernels
+    const int dp = D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : D <= 256 ? 256 : 512;  // padded head dim of the kernels
     int qt, ct;
     paged_types(dtype, qt, ct);
     if (qt == SA_BF16) return launch_paged_d<bf16, bf16>(dp, prm, st);

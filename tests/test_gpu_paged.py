@@ -189,12 +189,13 @@ def test_index_tensors_on_another_device_are_refused():
     assert out.shape == (B, Hq, D) and bool((out == 0).all())  # zero V rows
 
 
-@pytest.mark.parametrize("D", [8, 16, 24, 48, 80, 96, 136, 160, 200, 256])
+@pytest.mark.parametrize("D", [8, 16, 24, 48, 80, 96, 136, 160, 200, 256, 264, 384, 512])
 @pytest.mark.parametrize("BS", [1, 16, 64])
 def test_paged_head_dims(D, BS):
-    # any head dim that is a multiple of 8 up to 256 (the reference takes any
-    # D through next_pow2, kernels.py:2815): kernels for 32 / 64 / 128 / 256,
-    # smaller head dims load only their own columns
+    # any head dim that is a multiple of 8 up to 512 (the reference takes any
+    # D through next_pow2, kernels.py:2815): kernels for 32 / 64 / 128 / 256
+    # and 512 (two waves per block, each owning half the columns), smaller
+    # head dims load only their own columns
     q, k, v = case(3, 8, 2, 333, D, seed=D + BS)
     kc, vc, table, lens = paging.build_paged_cache(k, v, page_size=BS, shuffle=True, generator=_g(D))
     lens = torch.tensor([333, 1, 170], dtype=torch.int32)
@@ -216,3 +217,19 @@ def test_paged_head_dim_256_config5_like():
     out = run(q, kc, vc, table, lens, BS)
     ref = eager.paged_decode_eager(q.double(), kc.double(), vc.double(), table, lens)
     assert rel_err(out, ref) <= 1e-2
+
+
+def test_paged_head_dim_512_config5_like():
+    # head dim 512 on a serving-style layout: 12 sequences of up to 3000
+    # tokens, GQA 16 / 4, page 16, shuffled table; both cache dtypes
+    g = _g(512)
+    B, Hq, Hkv, D, BS = 12, 16, 4, 512, 16
+    lens = torch.randint(1, 3001, (B,), generator=g, dtype=torch.int32)
+    for dt in (torch.bfloat16, torch.float16):
+        q = torch.randn(B, Hq, 1, D, generator=g).to(dt)
+        k = torch.randn(B, Hkv, int(lens.max()), D, generator=g).to(dt)
+        v = torch.randn(B, Hkv, int(lens.max()), D, generator=g).to(dt)
+        kc, vc, table, _ = paging.build_paged_cache(k, v, page_size=BS, shuffle=True, generator=_g(7))
+        out = run(q, kc, vc, table, lens, BS, dtype=dt)
+        ref = eager.paged_decode_eager(q.double(), kc.double(), vc.double(), table, lens)
+        assert rel_err(out, ref) <= 1e-2

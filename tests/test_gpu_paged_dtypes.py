@@ -76,7 +76,7 @@ def make(B, Hq, Hkv, T, D, P, qdt, cdt, seed):
 
 @pytest.mark.parametrize("qdt", DTYPES)
 @pytest.mark.parametrize("cdt", DTYPES)
-@pytest.mark.parametrize("D", [64, 128, 256, 40])
+@pytest.mark.parametrize("D", [64, 128, 256, 40, 512])
 def test_paged_dtype_pairs(qdt, cdt, D):
     q, kc, vc, table, lens = make(3, 8, 2, 333, D, 16, qdt, cdt, seed=D + 7)
     out = decode(q, kc, vc, table, lens, 16)

@@ -304,9 +304,9 @@ def test_head_dims_and_page_sizes_checked_before_launch(no_library):
     with pytest.raises(ValueError, match="power of two"):
         smooth_attn.sp2norm_paged_attention(qd, kc, kc, torch.zeros(2, 2, dtype=torch.int32),
                                             torch.ones(2, dtype=torch.int32), block_size=12)
-    for D in (4, 12, 264, 512):  # paged decode: multiples of 8 in 8..256
+    for D in (4, 12, 516, 1024):  # paged decode: multiples of 8 in 8..512
         qd = torch.zeros(2, 4, 1, D, dtype=torch.bfloat16)
         kc = torch.zeros(4, 2, 16, D, dtype=torch.bfloat16)
-        with pytest.raises(ValueError, match="multiples of 8 in 8..256"):
+        with pytest.raises(ValueError, match="multiples of 8 in 8..512"):
             smooth_attn.sp2norm_paged_attention(qd, kc, kc, torch.zeros(2, 2, dtype=torch.int32),
                                                 torch.ones(2, dtype=torch.int32))
