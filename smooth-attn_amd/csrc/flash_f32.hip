@@ -489,6 +489,331 @@ int check_common(int B, int Hq, int Hkv, int T, int D, int window_size) {
     return 0;
 }
 
+// ---------------------------------------------------------------------------
+// Backward with 16 rows per wave (D = 128) on v_mfma_f32_16x16x4_f32
+// (A (16 x 4): lane l holds row l % 16 and k = l / 16; B (4 x 16): k =
+// l / 16, column l % 16; C (16 x 16): column l % 16, rows 4 (l / 16) + v).
+// With 32 rows per wave the D = 128 kernels hold the two operand rows of 32
+// keys (or queries) as 2 x 64 registers plus 2 x 64 accumulators and spill;
+// with 16 rows the same data takes half, in blocks of 8 waves (128 rows, the
+// grids of the 32-row kernels).  The layouts mirror the 32-row ones: MFMA i
+// of a D-contraction pairs k-slot g = l / 16 with d = g D / 4 + i, so a
+// lane's operand is one contiguous quarter row; for contractions over a
+// staged tile's 32 rows, MFMA j of 16-row subtile st takes the lane's own C
+// element v = j (row 16 st + 4 g + j) as B, and the A operand's four rows
+// for j = 0..3 are one 16-byte read of the transposed [D][kTP] tile.
+// ---------------------------------------------------------------------------
+constexpr int kRW = 8;                  // waves per block
+constexpr int kRRows = 16 * kRW;        // rows a block owns (= kFRows)
+static_assert(kRRows == kFRows, "the 16-row kernels use the 32-row kernels' grids");
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4 mma16f(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// One [kFT][D] fp32 tile staged through the registers of a 512-thread block.
+template <int D>
+struct TileRegs16 {
+    static constexpr int PER = kFT * D / 4 / (64 * kRW);  // float4 per thread
+    static_assert(PER >= 1, "a block of 8 waves stages at least one float4 per thread");
+    float4 v[PER];
+    template <bool PART>
+    __device__ __forceinline__ void load(const float* base, int64_t rstride, int r0, int T, int tid, int dr) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int idx = tid + 64 * kRW * i;
+            const int r = idx / (D / 4);
+            const int c = (idx - r * (D / 4)) * 4;
+            const float* rp = base + static_cast<int64_t>(min(r0 + r, T - 1)) * rstride;
+            if constexpr (PART) {
+                const float4 t = *reinterpret_cast<const float4*>(rp + (c < dr ? c : 0));
+                v[i] = c < dr ? t : float4{0.f, 0.f, 0.f, 0.f};
+            } else {
+                v[i] = *reinterpret_cast<const float4*>(rp + c);
+            }
+        }
+    }
+    __device__ __forceinline__ void store(float* row, float* tr, int tid) const {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int idx = tid + 64 * kRW * i;
+            const int r = idx / (D / 4);
+            const int c = (idx - r * (D / 4)) * 4;
+            if (row != nullptr) *reinterpret_cast<float4*>(row + r * (D + 4) + c) = v[i];
+            if (tr != nullptr) {
+                tr[(c + 0) * kTP + r] = v[i].x;
+                tr[(c + 1) * kTP + r] = v[i].y;
+                tr[(c + 2) * kTP + r] = v[i].z;
+                tr[(c + 3) * kTP + r] = v[i].w;
+            }
+        }
+    }
+};
+
+// A lane's quarter row: x[i] = row[g D/4 + i], i < D/4 (PART: zero past dr).
+template <int D, bool PART>
+__device__ __forceinline__ void load_quarter_row(const float* row, int g, float (&x)[D / 4], int dr) {
+#pragma unroll
+    for (int i4 = 0; i4 < D / 16; ++i4) {
+        const int c = g * (D / 4) + 4 * i4;
+        float4 t;
+        if constexpr (PART) {
+            t = *reinterpret_cast<const float4*>(row + (c < dr ? c : 0));
+            if (c >= dr) t = float4{0.f, 0.f, 0.f, 0.f};
+        } else {
+            t = *reinterpret_cast<const float4*>(row + c);
+        }
+        x[4 * i4 + 0] = t.x;
+        x[4 * i4 + 1] = t.y;
+        x[4 * i4 + 2] = t.z;
+        x[4 * i4 + 3] = t.w;
+    }
+}
+
+// C (16 x 16) += A B^T over D: A rows r0 + l16 of a row-major [kFT][D + 4]
+// LDS tile, B the lane's quarter-row registers.
+template <int D>
+__device__ __forceinline__ f32x4 mma_rows16(const float* lds_rows, int r0, int l16, int g, const float (&b)[D / 4],
+                                            f32x4 c) {
+    const float* ar = lds_rows + (r0 + l16) * (D + 4) + g * (D / 4);
+#pragma unroll
+    for (int i4 = 0; i4 < D / 16; ++i4) {
+        const float4 a = *reinterpret_cast<const float4*>(ar + 4 * i4);
+        c = mma16f(a.x, b[4 * i4 + 0], c);
+        c = mma16f(a.y, b[4 * i4 + 1], c);
+        c = mma16f(a.z, b[4 * i4 + 2], c);
+        c = mma16f(a.w, b[4 * i4 + 3], c);
+    }
+    return c;
+}
+
+// acc[dt] (rows d = 16 dt + 4 g + v, column = the lane's row) += A^T(d, r)
+// X(r, col) over the tile's 32 rows, A^T from a transposed [D][kTP] LDS tile
+// and X the lane's own C-layout values x[st][v] (row 16 st + 4 g + v).
+template <int D>
+__device__ __forceinline__ void mma_cols16(const float* lds_tr, int l16, int g, const float (&x)[2][4],
+                                           f32x4 (&acc)[D / 16]) {
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) {
+        const float* ar = lds_tr + (dt * 16 + l16) * kTP + 4 * g;
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            const float4 a = *reinterpret_cast<const float4*>(ar + 16 * st);
+            acc[dt] = mma16f(a.x, x[st][0], acc[dt]);
+            acc[dt] = mma16f(a.y, x[st][1], acc[dt]);
+            acc[dt] = mma16f(a.z, x[st][2], acc[dt]);
+            acc[dt] = mma16f(a.w, x[st][3], acc[dt]);
+        }
+    }
+}
+
+// Write a lane's C-layout values of acc (its row of the output, d =
+// 16 dt + 4 g .. +3) times f as 16-byte stores (PART: only below dr).
+template <int D, bool PART>
+__device__ __forceinline__ void store_cols16(float* row, int g, const f32x4 (&acc)[D / 16], float f, int dr) {
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) {
+        const float4 w{acc[dt][0] * f, acc[dt][1] * f, acc[dt][2] * f, acc[dt][3] * f};
+        if (!PART || dt * 16 + 4 * g < dr) *reinterpret_cast<float4*>(row + dt * 16 + 4 * g) = w;
+    }
+}
+
+template <int D, bool EXACT, bool PART>
+__global__ __launch_bounds__(64 * kRW) __attribute__((amdgpu_waves_per_eu(2, 2))) void flash_bwd_dq_f32r16_kernel(F32Params p) {
+    __shared__ __attribute__((aligned(16))) float ldsK[kFT * (D + 4)];
+    __shared__ __attribute__((aligned(16))) float ldsKt[D * kTP];
+    __shared__ __attribute__((aligned(16))) float ldsV[kFT * (D + 4)];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int g = lane >> 4;
+    const int l16 = lane & 15;
+    const int T_ = p.T;
+    const int nqb = (T_ + kRRows - 1) / kRRows;
+    const int per = p.B * p.Hq;
+    const int step = blockIdx.x / per;
+    const int rest = blockIdx.x - step * per;
+    const int qb = nqb - 1 - step;
+    const int b = rest / p.Hq;
+    const int hq = rest - b * p.Hq;
+    const int hk = hq / p.G;
+    const float* kp = p.k + b * p.ks[0] + hk * p.ks[1];
+    const float* vp = p.v + b * p.vs[0] + hk * p.vs[1];
+
+    const int q0 = qb * kRRows + 16 * wave;
+    const int qi = q0 + l16;
+    const int qrow = min(qi, T_ - 1);
+    float qv[D / 4], dov[D / 4];
+    load_quarter_row<D, PART>(p.q + b * p.qs[0] + hq * p.qs[1] + qrow * p.qs[2], g, qv, p.dr);
+    load_quarter_row<D, PART>(p.dout + b * p.dos[0] + hq * p.dos[1] + qrow * p.dos[2], g, dov, p.dr);
+    // delta = rowsum(dO * O) of this lane's query (lanes l16 + 16 g hold its quarters)
+    float dpart = 0.f;
+    {
+        const float* orow = p.o + b * p.os[0] + hq * p.os[1] + qrow * p.os[2];
+#pragma unroll
+        for (int i4 = 0; i4 < D / 16; ++i4) {
+            const int c = g * (D / 4) + 4 * i4;
+            // PART: columns past dr read column 0 and are zeroed
+            const bool in = !PART || c < p.dr;
+            float4 ov = *reinterpret_cast<const float4*>(orow + (in ? c : 0));
+            if (!in) ov = float4{0.f, 0.f, 0.f, 0.f};
+            dpart = __builtin_fmaf(dov[4 * i4 + 0], ov.x, dpart);
+            dpart = __builtin_fmaf(dov[4 * i4 + 1], ov.y, dpart);
+            dpart = __builtin_fmaf(dov[4 * i4 + 2], ov.z, dpart);
+            dpart = __builtin_fmaf(dov[4 * i4 + 3], ov.w, dpart);
+        }
+    }
+    const float dh = dpart + __shfl_xor(dpart, 16);
+    const float dl = dh + __shfl_xor(dh, 32);
+    const int64_t rbase = (static_cast<int64_t>(b) * p.Hq + hq) * T_;
+    if (qi < T_ && g == 0) p.delta[rbase + qi] = dl;
+    const float inv_r = 1.f / p.rs[rbase + qrow];
+
+    f32x4 acc[D / 16];
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const f32x4 ndl{-dl, -dl, -dl, -dl};
+    const int W = p.window;
+    const unsigned weff = W > 0 ? static_cast<unsigned>(W) : 0x7FFFFFFFu;
+    const int n_kv = (T_ + kFT - 1) / kFT;
+    const int kv_end = min((qb * kRRows + kRRows + kFT - 1) / kFT, n_kv);
+    const int kv_begin = W > 0 ? max(0, qb * kRRows - W + 1) / kFT : 0;
+    const float sc = p.scale;
+
+    TileRegs16<D> kreg, vreg;
+    kreg.template load<PART>(kp, p.ks[2], kv_begin * kFT, T_, tid, p.dr);
+    vreg.template load<PART>(vp, p.vs[2], kv_begin * kFT, T_, tid, p.dr);
+    for (int t = kv_begin; t < kv_end; ++t) {
+        __syncthreads();
+        kreg.store(ldsK, ldsKt, tid);
+        vreg.store(ldsV, nullptr, tid);
+        __syncthreads();
+        if (t + 1 < kv_end) {
+            kreg.template load<PART>(kp, p.ks[2], (t + 1) * kFT, T_, tid, p.dr);
+            vreg.template load<PART>(vp, p.vs[2], (t + 1) * kFT, T_, tid, p.dr);
+        }
+        const int k0 = t * kFT;
+        const bool active = k0 <= q0 + 15 && !(W > 0 && q0 - (k0 + 31) >= W);
+        if (kSkipIdle<D> && !active) continue;
+        float ds[2][4];
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            const f32x4 s = mma_rows16<D>(ldsK, 16 * st, l16, g, qv, f32x4{0.f, 0.f, 0.f, 0.f});  // S^T
+            const f32x4 dp = mma_rows16<D>(ldsV, 16 * st, l16, g, dov, ndl);                     // dP^T - delta
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int key = k0 + 16 * st + 4 * g + v;
+                float y, rr;
+                weight_rr<EXACT>(s[v], sc, y, rr);
+                ds[st][v] = keep_if(static_cast<unsigned>(qi - key) < weff, dp[v] * y * rr);
+            }
+        }
+        mma_cols16<D>(ldsKt, l16, g, ds, acc);  // dQ^T += K^T dS^T
+    }
+    // dS carried without its per-row factor 2 scale / R
+    if (qi < T_) store_cols16<D, PART>(p.dq + b * p.dqs[0] + hq * p.dqs[1] + qi * p.dqs[2], g, acc, 2.f * sc * inv_r, p.dr);
+}
+
+template <int D, bool EXACT, bool PART>
+__global__ __launch_bounds__(64 * kRW) __attribute__((amdgpu_waves_per_eu(2, 2))) void flash_bwd_dkdv_f32r16_kernel(F32Params p) {
+    __shared__ __attribute__((aligned(16))) float ldsQ[kFT * (D + 4)];
+    __shared__ __attribute__((aligned(16))) float ldsQt[D * kTP];
+    __shared__ __attribute__((aligned(16))) float ldsO[kFT * (D + 4)];
+    __shared__ __attribute__((aligned(16))) float ldsOt[D * kTP];
+    __shared__ __attribute__((aligned(16))) float ldr[2][kFT];  // [1/R, -delta] of the tile's rows
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int g = lane >> 4;
+    const int l16 = lane & 15;
+    const int T_ = p.T;
+    const int per = p.B * p.Hkv;
+    const int kb = blockIdx.x / per;  // earliest key blocks (most queries) first
+    const int rest = blockIdx.x - kb * per;
+    const int b = rest / p.Hkv;
+    const int hk = rest - b * p.Hkv;
+
+    const int k_start = kb * kRRows;
+    const int wk0 = k_start + 16 * wave;
+    const int kj = wk0 + l16;
+    const int krow = min(kj, T_ - 1);
+    float kv[D / 4], vv[D / 4];
+    load_quarter_row<D, PART>(p.k + b * p.ks[0] + hk * p.ks[1] + krow * p.ks[2], g, kv, p.dr);
+    load_quarter_row<D, PART>(p.v + b * p.vs[0] + hk * p.vs[1] + krow * p.vs[2], g, vv, p.dr);
+
+    f32x4 dkacc[D / 16], dvacc[D / 16];
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) {
+        dkacc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        dvacc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    const int W = p.window;
+    const unsigned weff = W > 0 ? static_cast<unsigned>(W) : 0x7FFFFFFFu;
+    const int n_qt = (T_ + kFT - 1) / kFT;
+    const int qt_begin = k_start / kFT;
+    const int qt_end = W > 0 ? min(n_qt, (k_start + kRRows - 1 + W - 1) / kFT + 1) : n_qt;
+    const int nq = qt_end - qt_begin;  // >= 1 (k_start < T)
+    const int n_it = p.G * nq;
+    const float sc = p.scale;
+
+    TileRegs16<D> qreg, oreg;
+    float rst = 0.f;
+    auto fetch = [&](int it) {
+        const int gg = it / nq;
+        const int q0 = (qt_begin + it - gg * nq) * kFT;
+        const int hq = hk * p.G + gg;
+        qreg.template load<PART>(p.q + b * p.qs[0] + hq * p.qs[1], p.qs[2], q0, T_, tid, p.dr);
+        oreg.template load<PART>(p.dout + b * p.dos[0] + hq * p.dos[1], p.dos[2], q0, T_, tid, p.dr);
+        // raw row sum or delta; 1/R or -delta is formed where it is stored
+        if (tid < 2 * kFT) {
+            const int64_t idx = (static_cast<int64_t>(b) * p.Hq + hq) * T_ + min(q0 + (tid & (kFT - 1)), T_ - 1);
+            rst = (tid < kFT ? p.rs : p.delta)[idx];
+        }
+    };
+    fetch(0);
+    for (int it = 0; it < n_it; ++it) {
+        __syncthreads();
+        qreg.store(ldsQ, ldsQt, tid);
+        oreg.store(ldsO, ldsOt, tid);
+        if (tid < 2 * kFT) ldr[tid / kFT][tid & (kFT - 1)] = tid < kFT ? 1.f / rst : -rst;
+        __syncthreads();
+        const int gg = it / nq;
+        const int q0 = (qt_begin + it - gg * nq) * kFT;
+        if (it + 1 < n_it) fetch(it + 1);
+        // some query of the tile sees some key of the wave
+        const bool active = q0 + 31 >= wk0 && !(W > 0 && q0 - (wk0 + 15) >= W) && q0 < T_;
+        if (kSkipIdle<D> && !active) continue;
+        float pw[2][4], ds[2][4];
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            const f32x4 s = mma_rows16<D>(ldsQ, 16 * st, l16, g, kv, f32x4{0.f, 0.f, 0.f, 0.f});  // S: rows queries
+            f32x4 dp;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) dp[v] = ldr[1][16 * st + 4 * g + v];
+            dp = mma_rows16<D>(ldsO, 16 * st, l16, g, vv, dp);  // dP - delta
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int r = 16 * st + 4 * g + v;
+                const int q = q0 + r;
+                float y, rr;
+                weight_rr<EXACT>(s[v], sc, y, rr);
+                const float yi = y * ldr[0][r];
+                const bool ok = static_cast<unsigned>(q - kj) < weff && q < T_;
+                pw[st][v] = keep_if(ok, yi);
+                ds[st][v] = keep_if(ok, dp[v] * yi * rr);
+            }
+        }
+        mma_cols16<D>(ldsOt, l16, g, pw, dvacc);  // dV^T += dO^T P
+        mma_cols16<D>(ldsQt, l16, g, ds, dkacc);  // dK^T += Q^T dS
+    }
+    if (kj < T_) {
+        store_cols16<D, PART>(p.dk + b * p.dks[0] + hk * p.dks[1] + kj * p.dks[2], g, dkacc, 2.f * sc, p.dr);
+        store_cols16<D, PART>(p.dv + b * p.dvs[0] + hk * p.dvs[1] + kj * p.dvs[2], g, dvacc, 1.f, p.dr);
+    }
+}
+
 template <int D>
 int launch_fwd_f32_d(const F32Params& prm, int exact, hipStream_t st) {
     const int64_t nblk = static_cast<int64_t>((prm.T + kFRows - 1) / kFRows) * prm.B * prm.Hq;
@@ -511,6 +836,25 @@ int launch_bwd_f32_d(const F32Params& prm, int exact, hipStream_t st) {
     // measured 1% faster; at D = 64 and 256 the masked ones are the faster
     // even when dr == D (8671 -> 8430 and 8173 -> 7794 us).
     const bool part = prm.dr != D || D != 128;
+    if constexpr (D == 128) {
+        // 16 rows per wave (at D = 256 the 8-wave blocks would cap each wave at
+        // 256 registers; the 32-row kernels there run one wave per SIMD)
+        if (nq * 64 * kRW >= (int64_t(1) << 32)) return SA_ERR_BAD_SHAPE;
+        if (exact && part) {
+            flash_bwd_dq_f32r16_kernel<D, true, true><<<gq, 64 * kRW, 0, st>>>(prm);
+            flash_bwd_dkdv_f32r16_kernel<D, true, true><<<gk, 64 * kRW, 0, st>>>(prm);
+        } else if (exact) {
+            flash_bwd_dq_f32r16_kernel<D, true, false><<<gq, 64 * kRW, 0, st>>>(prm);
+            flash_bwd_dkdv_f32r16_kernel<D, true, false><<<gk, 64 * kRW, 0, st>>>(prm);
+        } else if (part) {
+            flash_bwd_dq_f32r16_kernel<D, false, true><<<gq, 64 * kRW, 0, st>>>(prm);
+            flash_bwd_dkdv_f32r16_kernel<D, false, true><<<gk, 64 * kRW, 0, st>>>(prm);
+        } else {
+            flash_bwd_dq_f32r16_kernel<D, false, false><<<gq, 64 * kRW, 0, st>>>(prm);
+            flash_bwd_dkdv_f32r16_kernel<D, false, false><<<gk, 64 * kRW, 0, st>>>(prm);
+        }
+        return status_from_launch();
+    }
     if (exact && part) {
         flash_bwd_dq_f32_kernel<D, true, true><<<gq, 64 * kFW, 0, st>>>(prm);
         flash_bwd_dkdv_f32_kernel<D, true, true><<<gk, 64 * kFW, 0, st>>>(prm);
