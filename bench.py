@@ -379,7 +379,7 @@ def bench_next_rows(torch):
       (config 3's FLOPs), and paged decode at head dim 256 on config 5's
       layout with Hq 16 / Hkv 4 (config 5's bytes), at head dim 512 with
       Hq 8 / Hkv 2 (the same bytes), and paged decode over
-      fp32 caches (and fp32 q over bf16 caches) on config 5's layout;
+      fp32 caches (and fp32 q over bf16 and e4m3fn caches) on config 5's layout;
     - RoPE-fused attention forward on config 3's shape (K rotated once by a
       streaming kernel, Q in registers; the time includes the rotation),
       and the RoPE + W_o projection variant (RoPE forward plus one fp32-
@@ -482,6 +482,12 @@ def bench_next_rows(torch):
     nb = paged_bytes(lens) + 64 * 32 * 128 * 2  # config 5's bytes with a 4-byte q
     out["paged_decode_fp32_q_bf16_cache"] = {"us": round(us, 1), "GBs": round(nb / us / 1e3, 1),
                                              "frac_hbm_peak": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)}
+    # e4m3fn caches (2 KB of K and V per token), read unscaled as the reference reads them
+    kc, vc = kc.to(torch.float8_e4m3fn), vc.to(torch.float8_e4m3fn)
+    us = med(lambda: sa.sp2norm_paged_attention(qd, kc, vc, table_d, lens_d))
+    nb = 2048 * int(lens.sum()) + 4 * n_pg + 64 * 32 * 128 * (4 + 2) + 4 * 64
+    out["paged_decode_fp8_cache"] = {"us": round(us, 1), "GBs": round(nb / us / 1e3, 1),
+                                     "frac_hbm_peak": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)}
     del kc, vc, qd
     torch.cuda.empty_cache()
 

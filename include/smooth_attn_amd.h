@@ -309,10 +309,11 @@ int64_t sa_paged_decode_workspace_size(int B, int Hq, int D, int max_pages,
  * out[b,h] = sum_{t<ctx_b} y_t V_t / (sum_t y_t + 1e-12) with
  * K_t = k_cache[block_table[b, t/P], h/(Hq/Hkv), t%P].  dtype:
  * SA_PAGED_DTYPES(q type, cache type), or one code for both; supported
- * pairs: bf16 / bf16, fp16 / fp16, fp32 / fp32, fp32 q over bf16 or fp16
- * caches (the reference upcasts q, K and V to fp32, kernels.py:2716-2717,
- * :2746, :2765; mixed pairs and fp32 run their products as bf16
- * hi + lo splits, about 16 significant bits).  Row strides (element units)
+ * pairs: bf16 / bf16, fp16 / fp16, fp32 / fp32, fp32 q over bf16, fp16 or
+ * e4m3fn caches (the reference upcasts q, K and V to fp32,
+ * kernels.py:2716-2717, :2746, :2765; mixed pairs and fp32 run their
+ * products as bf16 hi + lo splits, about 16 significant bits; e4m3fn values
+ * widen to bf16 exactly, unscaled, and need D a multiple of 16).  Row strides (element units)
  * must be 16-byte multiples.  D a multiple of 8 in 8..512 (kernels for 32,
  * 64, 128, 256 and 512, the last with two waves per block splitting the
  * columns; smaller D read only their own columns); page_size a power of
@@ -375,9 +376,10 @@ int sa_paged_decode_noalloc(const void* q, const void* k_cache,
  * k_new, v_new: [B, Hkv, n_new, D] (new_strides, d stride 1); caches as in
  * sa_paged_decode.  Rows whose page index reaches max_pages or whose table
  * entry is outside [0, n_pages) are skipped.  context_lens is not updated
- * (the caller adds n_new).  dtype SA_F32, SA_BF16 or SA_F16 (the caches'
- * type; the rows are copied as bytes); rows of 16-byte multiples (D a
- * multiple of 4 for fp32, of 8 for 16-bit types).
+ * (the caller adds n_new).  dtype SA_F32, SA_BF16, SA_F16 or
+ * SA_FP8_E4M3FN (the caches' type; the rows are copied as bytes); rows of
+ * 16-byte multiples (D a multiple of 4 for fp32, of 8 for 16-bit types, of
+ * 16 for e4m3fn).
  * No reference kernel: the reference fills caches with Python loops in its
  * tests (tests/test_paged_attention.py:10-73).
  */

@@ -101,14 +101,33 @@ __global__ __launch_bounds__(256) void paged_plan_kernel(PagedParams p) {
 // split too, and each product becomes the three MFMAs hi*hi + hi*lo + lo*hi:
 // about 2^-16 relative error per product, against the reference's fp32
 // arithmetic (kernels.py:2716-2717, :2746, :2765).
+// e4m3fn cache elements (one byte each).  Every e4m3fn value is a bf16
+// value, so fp8 caches widen to bf16 exactly, with no lo part.
+struct fp8e4 {
+    uint8_t bits;
+};
+
 template <typename QE, typename CE>
 struct PagedTypes {
     static constexpr bool SAME16 = std::is_same_v<QE, CE> && sizeof(CE) == 2;
     using MT = std::conditional_t<SAME16, CE, bf16>;
     static constexpr bool SPLIT_Q = !std::is_same_v<QE, MT>;
-    static constexpr bool SPLIT_C = !std::is_same_v<CE, MT>;
+    static constexpr bool SPLIT_C = !std::is_same_v<CE, MT> && !std::is_same_v<CE, fp8e4>;
     static constexpr bool SPLIT_P = !SAME16;
 };
+
+// 16 e4m3fn values (one 16-byte word) as 16 bf16 values (two words), exact.
+__device__ __forceinline__ void widen_e4m3(u32x4 in, u32x4& lo, u32x4& hi) {
+    uint32_t out[8];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const int word = static_cast<int>(in[w]);
+        out[2 * w] = pack2<bf16>(__builtin_amdgcn_cvt_f32_fp8(word, 0), __builtin_amdgcn_cvt_f32_fp8(word, 1));
+        out[2 * w + 1] = pack2<bf16>(__builtin_amdgcn_cvt_f32_fp8(word, 2), __builtin_amdgcn_cvt_f32_fp8(word, 3));
+    }
+    lo = u32x4{out[0], out[1], out[2], out[3]};
+    hi = u32x4{out[4], out[5], out[6], out[7]};
+}
 
 // hi = bf16(a), bf16(b) packed; lo = the same of the remainders.
 __device__ __forceinline__ void split2_bf16(float a, float b, uint32_t& hi, uint32_t& lo) {
@@ -305,7 +324,16 @@ __global__ __launch_bounds__(64 * WPB) void paged_partial_kernel(PagedParams p) 
 #pragma unroll
                 for (int i = 0; i < NC; ++i) {
                     const int tok = i * TPI + lane_tok;
-                    if constexpr (!SC) {
+                    if constexpr (std::is_same_v<CE, fp8e4>) {
+                        // 16 e4m3fn values -> 16 bf16 (32 bytes)
+                        u32x4 a, c;
+                        widen_e4m3(kbuf[i], a, c);
+                        *reinterpret_cast<u32x4*>(ldsK + tok * RS + lane_col) = a;
+                        *reinterpret_cast<u32x4*>(ldsK + tok * RS + lane_col + 8) = c;
+                        widen_e4m3(vbuf[i], a, c);
+                        *reinterpret_cast<u32x4*>(ldsV + tok * RSV + lane_col) = a;
+                        *reinterpret_cast<u32x4*>(ldsV + tok * RSV + lane_col + 8) = c;
+                    } else if constexpr (!SC) {
                         *reinterpret_cast<u32x4*>(ldsK + tok * RS + lane_col) = kbuf[i];
                         *reinterpret_cast<u32x4*>(ldsV + tok * RSV + lane_col) = vbuf[i];
                     } else if constexpr (sizeof(CE) == 4) {
@@ -493,8 +521,9 @@ template <typename QE, typename CE, int D>
 int launch_paged(PagedParams prm, hipStream_t st) {
     // waves per block, each owning D / WPB columns: rows above 512 bytes are
     // split into 512-byte parts (their tile registers would not fit one wave)
+    // (and any head dim above 256, whose Q and O registers alone fill a wave)
     constexpr int RB = D * static_cast<int>(sizeof(CE));
-    constexpr int WPB = RB > 1024 ? 4 : RB > 512 ? 2 : 1;
+    constexpr int WPB = RB > 1024 ? 4 : (RB > 512 || D > 256) ? 2 : 1;
     const bool uniform = prm.P * (D / WPB * static_cast<int>(sizeof(CE)) / 16) >= 64;
     const int resident =
         uniform ? resident_waves<QE, CE, D, true, WPB>() : resident_waves<QE, CE, D, false, WPB>();
@@ -572,7 +601,7 @@ bool paged_types(int dtype, int& qt, int& ct) {
     ct = (dtype >> 8) == 0 ? qt : (dtype >> 8) - 1;
     if (dtype < 0 || (dtype >> 16) != 0) return false;
     if (qt == ct) return qt == SA_BF16 || qt == SA_F16 || qt == SA_F32;
-    return qt == SA_F32 && (ct == SA_BF16 || ct == SA_F16);
+    return qt == SA_F32 && (ct == SA_BF16 || ct == SA_F16 || ct == SA_FP8_E4M3FN);
 }
 
 // Argument checks shared by both decode entry points (0 = launch, 1 =
@@ -599,9 +628,10 @@ int validate_paged(const void* q, const void* k_cache, const void* v_cache, cons
         return SA_ERR_NULL_POINTER;
     int qt, ct;
     if (!paged_types(dtype, qt, ct)) return SA_ERR_BAD_DTYPE;
+    if (ct == SA_FP8_E4M3FN && D % 16 != 0) return SA_ERR_UNSUPPORTED;  // 16-byte rows of 1-byte elements
     // 16-byte rows: element strides that are multiples of 16 / element size
     const auto ok16 = [](const int64_t* s, int n, int t) {
-        const int per = t == SA_F32 ? 4 : 8;
+        const int per = t == SA_F32 ? 4 : t == SA_FP8_E4M3FN ? 16 : 8;
         for (int i = 0; i < n - 1; ++i)
             if (s[i] % per != 0) return false;
         return s[n - 1] == 1;
@@ -654,6 +684,7 @@ int run_paged(const void* q, const void* k_cache, const void* v_cache, void* out
     if (qt == SA_BF16) return launch_paged_d<bf16, bf16>(dp, prm, st);
     if (qt == SA_F16) return launch_paged_d<f16, f16>(dp, prm, st);
     if (ct == SA_BF16) return launch_paged_d<float, bf16>(dp, prm, st);
+    if (ct == SA_FP8_E4M3FN) return launch_paged_d<float, fp8e4>(dp, prm, st);
     if (ct == SA_F16) return launch_paged_d<float, f16>(dp, prm, st);
     return launch_paged_d<float, float>(dp, prm, st);
 }

@@ -6,8 +6,8 @@
 // For sequence b with current length ctx_b and new rows t < n_new:
 //   pos = ctx_b + t,  page = block_table[b, pos / P],  slot = pos % P
 //   k_cache[page, h, slot, :] = k_new[b, h, t, :]   (same for v)
-// One thread per 16-byte chunk of a new row, for K and V (fp32, bf16 or fp16
-// rows: the copy moves bytes and never converts).  Positions whose
+// One thread per 16-byte chunk of a new row, for K and V (fp32, bf16, fp16 or
+// e4m3fn rows: the copy moves bytes and never converts).  Positions whose
 // page index is past max_pages, or whose block-table entry is outside
 // [0, n_pages), are skipped: nothing is written outside the caches.
 #include "common.hpp"
@@ -71,8 +71,8 @@ extern "C" int sa_paged_kv_append(const void* k_new, const void* v_new, void* k_
                                   const int64_t* new_strides, const int64_t* kc_strides,
                                   const int64_t* vc_strides, int64_t bt_stride, int dtype, sa_stream_t stream) {
     using namespace sa;
-    if (dtype != SA_BF16 && dtype != SA_F16 && dtype != SA_F32) return SA_ERR_BAD_DTYPE;
-    const int esize = dtype == SA_F32 ? 4 : 2;
+    if (dtype != SA_BF16 && dtype != SA_F16 && dtype != SA_F32 && dtype != SA_FP8_E4M3FN) return SA_ERR_BAD_DTYPE;
+    const int esize = dtype == SA_F32 ? 4 : dtype == SA_FP8_E4M3FN ? 1 : 2;
     if (B < 0 || Hkv <= 0 || n_new < 0 || max_pages < 0 || n_pages < 0 || page_size <= 0) return SA_ERR_BAD_SHAPE;
     if (D <= 0 || (D * esize) % 16 != 0) return SA_ERR_UNSUPPORTED;
     if (B == 0 || n_new == 0 || max_pages == 0 || n_pages == 0) return 0;

@@ -973,20 +973,23 @@ def _check_paging_args(B, D, k_cache, v_cache, block_table, context_lens):
 
 
 _PAGED_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
+_PAGED_CACHE_DTYPES = _PAGED_DTYPES + (torch.float8_e4m3fn,)
+_CACHE_CODE = {**_DTYPE_CODE, torch.float8_e4m3fn: _lib.SA_FP8_E4M3FN}
 
 
 def _paged_dtype_code(q_dtype, k_dtype, v_dtype):
     """The C ABI's dtype argument for a decode over these tensors.  The
     reference upcasts q, K and V to fp32 whatever they are
-    (kernels.py:2716-2717, :2746, :2765): here q may be fp32, bf16 or fp16
-    and the caches fp32, bf16 or fp16 of one dtype; a q whose dtype differs
-    from the caches' runs as fp32 (an exact conversion)."""
-    if q_dtype not in _PAGED_DTYPES or k_dtype not in _PAGED_DTYPES or v_dtype != k_dtype:
-        raise ValueError("paged decode expects fp32, bf16 or fp16 q and fp32, bf16 or fp16 caches of one dtype, "
-                         f"got q {q_dtype}, k_cache {k_dtype}, v_cache {v_dtype}")
-    if q_dtype == k_dtype:
+    (kernels.py:2716-2717, :2746, :2765): here q may be fp32, bf16, fp16 or
+    e4m3fn and the caches fp32, bf16, fp16 or e4m3fn (unscaled values, as
+    the reference reads them) of one dtype; a q whose dtype differs from the
+    caches' runs as fp32 (an exact conversion)."""
+    if (q_dtype not in _PAGED_CACHE_DTYPES or k_dtype not in _PAGED_CACHE_DTYPES or v_dtype != k_dtype):
+        raise ValueError("paged decode expects fp32, bf16, fp16 or e4m3fn q and fp32, bf16, fp16 or e4m3fn caches "
+                         f"of one dtype, got q {q_dtype}, k_cache {k_dtype}, v_cache {v_dtype}")
+    if q_dtype == k_dtype and q_dtype in _PAGED_DTYPES:
         return _DTYPE_CODE[q_dtype]
-    return _lib.paged_dtypes(_lib.SA_F32, _DTYPE_CODE[k_dtype])
+    return _lib.paged_dtypes(_lib.SA_F32, _CACHE_CODE[k_dtype])
 
 
 def sp2norm_paged_attention(q, k_cache, v_cache, block_table, context_lens, *, scale=None, block_size=16):
@@ -1009,8 +1012,10 @@ def sp2norm_paged_attention(q, k_cache, v_cache, block_table, context_lens, *, s
     _check_same_device("q", q, k_cache=k_cache, v_cache=v_cache, block_table=block_table,
                        context_lens=context_lens)
     code = _paged_dtype_code(q.dtype, k_cache.dtype, v_cache.dtype)
-    if q.dtype != k_cache.dtype:
-        q = q.float()  # exact; fp32 q runs over fp32, bf16 or fp16 caches
+    if q.dtype != k_cache.dtype or q.dtype == torch.float8_e4m3fn:
+        q = q.float()  # exact; fp32 q runs over fp32, bf16, fp16 or e4m3fn caches
+    if k_cache.dtype == torch.float8_e4m3fn and D % 16:
+        raise ValueError(f"paged decode over e4m3fn caches needs a head dim that is a multiple of 16, got {D}")
     _check_paging_args(B, D, k_cache, v_cache, block_table, context_lens)
     q = _flash_operand(q)
     k_cache = _flash_operand(k_cache)
@@ -1049,8 +1054,8 @@ def sp2norm_paged_kv_append(k_cache, v_cache, k_new, v_new, block_table, context
     assert k_cache.shape[2] == block_size
     _check_same_device("k_cache", k_cache, v_cache=v_cache, k_new=k_new, v_new=v_new, block_table=block_table,
                        context_lens=context_lens)
-    if k_cache.dtype not in _PAGED_DTYPES or v_cache.dtype != k_cache.dtype:
-        raise ValueError("paged caches must be fp32, bf16 or fp16 of one dtype")
+    if k_cache.dtype not in _PAGED_CACHE_DTYPES or v_cache.dtype != k_cache.dtype:
+        raise ValueError("paged caches must be fp32, bf16, fp16 or e4m3fn of one dtype")
     _check_paging_args(B, D, k_cache, v_cache, block_table, context_lens)
     per = 16 // k_cache.element_size()
     for t in (k_cache, v_cache):
@@ -1071,7 +1076,7 @@ def sp2norm_paged_kv_append(k_cache, v_cache, k_new, v_new, block_table, context
             k_new.data_ptr(), v_new.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), block_table.data_ptr(),
             context_lens.data_ptr(), B, H_kv, n_new, D, block_size, block_table.shape[1], k_cache.shape[0],
             _lib.strides(k_new), _lib.strides(k_cache), _lib.strides(v_cache), block_table.stride(0),
-            _DTYPE_CODE[k_cache.dtype], _stream(k_cache),
+            _CACHE_CODE[k_cache.dtype], _stream(k_cache),
         )
     _lib.check(st, "sa_paged_kv_append")
     return context_lens + n_new

@@ -21,6 +21,7 @@ def _g(seed):
 CASES = [(dt, P, D, n) for dt in (torch.bfloat16, torch.float16, torch.float32)
          for P, D, n in ((16, 128, 1), (16, 64, 7), (8, 32, 33), (32, 128, 5))]
 CASES += [(torch.float32, 4, 12, 9), (torch.bfloat16, 4, 24, 9)]  # 16-byte rows: fp32 D % 4, 16-bit D % 8
+CASES += [(torch.float8_e4m3fn, 16, 64, 7), (torch.float8_e4m3fn, 8, 32, 33)]  # e4m3fn: D % 16
 
 
 @pytest.mark.parametrize("dtype,P,D,n_new", CASES)
@@ -36,7 +37,8 @@ def test_append_matches_oracle(dtype, P, D, n_new):
     kd, vd = kc.to(DEV), vc.to(DEV)
     new_ctx = smooth_attn.sp2norm_paged_kv_append(kd, vd, kn.to(DEV), vn.to(DEV), table.to(DEV), ctx.to(DEV),
                                                   block_size=P)
-    assert torch.equal(kd.cpu(), ref_k) and torch.equal(vd.cpu(), ref_v)
+    assert torch.equal(kd.cpu().view(torch.uint8), ref_k.view(torch.uint8))
+    assert torch.equal(vd.cpu().view(torch.uint8), ref_v.view(torch.uint8))
     assert torch.equal(new_ctx.cpu(), ctx + n_new)
 
 

@@ -1,12 +1,13 @@
-"""Paged decode over fp32 and mixed-dtype q / caches (GPU).
+"""Paged decode over fp32, e4m3fn and mixed-dtype q / caches (GPU).
 
 The reference upcasts q, K and V to fp32 whatever their storage type and
 computes scores, weights and the weighted sum in fp32 (kernels.py:2716-2717,
 :2746, :2765), writing a bf16 output.  Here q may be fp32, bf16 or fp16 and
-the caches fp32, bf16 or fp16 (K and V of one dtype); a q whose dtype differs
-from the caches' runs as fp32.  Pairs other than bf16 / bf16 and fp16 / fp16
-run every product as bf16 hi + lo splits (16 significant bits) with fp32
-weights split the same way.
+the caches fp32, bf16, fp16 or e4m3fn (K and V of one dtype, e4m3fn values
+read unscaled as the reference reads them); a q whose dtype differs from the
+caches', or an e4m3fn q, runs as fp32.  Pairs other than bf16 / bf16 and
+fp16 / fp16 run every product as bf16 hi + lo splits (16 significant bits;
+e4m3fn values widen to bf16 exactly) with fp32 weights split the same way.
 
 Bars, against the float64 oracle (oracle.eager.paged_decode_eager) on the
 same stored values:
@@ -28,7 +29,7 @@ from smooth_attn import _lib
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
-DTYPES = [torch.float32, torch.bfloat16, torch.float16]
+DTYPES = [torch.float32, torch.bfloat16, torch.float16, torch.float8_e4m3fn]
 
 
 def _g(seed):
@@ -79,11 +80,15 @@ def make(B, Hq, Hkv, T, D, P, qdt, cdt, seed):
 @pytest.mark.parametrize("D", [64, 128, 256, 40, 512])
 def test_paged_dtype_pairs(qdt, cdt, D):
     q, kc, vc, table, lens = make(3, 8, 2, 333, D, 16, qdt, cdt, seed=D + 7)
+    if cdt == torch.float8_e4m3fn and D % 16:
+        with pytest.raises(ValueError, match="multiple of 16"):  # 16-byte rows of 1-byte elements
+            decode(q, kc, vc, table, lens, 16)
+        return
     out = decode(q, kc, vc, table, lens, 16)
     assert out.dtype == torch.bfloat16 and out.shape == (3, 8, D)
     ref = eager.paged_decode_eager(q.double(), kc.double(), vc.double(), table, lens)
     assert rel_err(out, ref) <= 1e-2
-    if not (qdt == cdt and qdt != torch.float32):
+    if not (qdt == cdt and qdt in (torch.bfloat16, torch.float16)):
         share, steps = bf16_match(out, ref)
         assert steps <= 1.0 + 1e-6, (qdt, cdt, D, steps)
         assert share >= 0.97, (qdt, cdt, D, share)
@@ -153,3 +158,35 @@ def test_paged_mismatched_cache_dtypes_are_refused():
     q, kc, vc, table, lens = make(1, 4, 2, 40, 32, 16, torch.float32, torch.float32, seed=9)
     with pytest.raises(ValueError, match="one dtype"):
         decode(q, kc, vc.to(torch.bfloat16), table, lens, 16)
+
+
+def test_paged_fp8_cache_c_abi_and_append():
+    # e4m3fn caches filled by the paged-KV writer (a byte copy) and decoded
+    # through SA_PAGED_DTYPES(SA_F32, SA_FP8_E4M3FN): equal to the Python
+    # entry point over the same caches, and to the oracle's bf16 rounding
+    B, Hq, Hkv, D, P, T = 2, 8, 2, 64, 16, 90
+    g = _g(41)
+    k = torch.randn(B, Hkv, T, D, generator=g).to(torch.float8_e4m3fn)
+    v = torch.randn(B, Hkv, T, D, generator=g).to(torch.float8_e4m3fn)
+    q = torch.randn(B, Hq, 1, D, generator=g)
+    full_k, full_v, table, lens = paging.build_paged_cache(k, v, P, shuffle=True, generator=_g(42))
+    kd = torch.zeros_like(full_k).to(DEV)
+    vd = torch.zeros_like(full_v).to(DEV)
+    ctx = torch.zeros(B, dtype=torch.int32, device=DEV)
+    ctx = smooth_attn.sp2norm_paged_kv_append(kd, vd, k.to(DEV), v.to(DEV), table.to(DEV), ctx, block_size=P)
+    assert torch.equal(kd.cpu().view(torch.uint8), full_k.view(torch.uint8))
+    assert torch.equal(vd.cpu().view(torch.uint8), full_v.view(torch.uint8))
+    out = torch.empty(B, Hq, D, dtype=torch.bfloat16, device=DEV)
+    lib = _lib.load()
+    qd, td = q.to(DEV), table.to(DEV)
+    ws = torch.empty(lib.sa_paged_decode_workspace_size(B, Hq, D, table.shape[1], P) // 4 + 1, device=DEV)
+    st = lib.sa_paged_decode(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), out.data_ptr(), td.data_ptr(),
+                             ctx.data_ptr(), B, Hq, Hkv, D, P, table.shape[1], full_k.shape[0], _lib.strides(qd),
+                             _lib.strides(kd), _lib.strides(vd), _lib.strides(out), td.stride(0), D ** -0.5,
+                             _lib.paged_dtypes(_lib.SA_F32, _lib.SA_FP8_E4M3FN), ctypes.c_void_p(ws.data_ptr()),
+                             ws.numel() * 4, torch.cuda.current_stream().cuda_stream)
+    _lib.check(st, "sa_paged_decode")
+    assert torch.equal(out, smooth_attn.sp2norm_paged_attention(qd, kd, vd, td, ctx, block_size=P))
+    ref = eager.paged_decode_eager(q.double(), full_k.double(), full_v.double(), table, lens)
+    share, steps = bf16_match(out, ref)
+    assert steps <= 1.0 + 1e-6 and share >= 0.97
