@@ -200,6 +200,35 @@ int sa_flash_bwd(const void* q, const void* k, const void* v, const void* o,
                  sa_stream_t stream);
 
 /*
+ * Bytes of workspace sa_flash_bwd_ws uses for these sizes: fp32 partial
+ * dK / dV of the key blocks split over their query tiles, which the library
+ * does for causal rows long against the grid (few batch x KV heads), where
+ * the first key blocks, which see every query, would otherwise run alone at
+ * the end.  0 when it does not split (fp32, head dims above 128, grids that
+ * fill the GPU); -1 for invalid sizes.
+ */
+int64_t sa_flash_bwd_workspace_size(int B, int Hq, int Hkv, int T, int D,
+                                    int window_size, int dtype);
+
+/*
+ * sa_flash_bwd with the workspace above (16-byte aligned).  A smaller
+ * workspace runs fewer splits (none when NULL or 0 bytes); results are the
+ * same up to fp32 summation order in dK and dV.  The split path adds one
+ * kernel summing the partials in a fixed order, so results do not depend
+ * on timing.  Replaces the same reference functions as sa_flash_bwd.
+ */
+int sa_flash_bwd_ws(const void* q, const void* k, const void* v, const void* o,
+                    const void* dout, const float* row_sums, void* dq, void* dk,
+                    void* dv, float* delta_ws, int B, int Hq, int Hkv, int T,
+                    int D, const int64_t* q_strides, const int64_t* k_strides,
+                    const int64_t* v_strides, const int64_t* o_strides,
+                    const int64_t* do_strides, const int64_t* dq_strides,
+                    const int64_t* dk_strides, const int64_t* dv_strides,
+                    float scale, int window_size, int exact_math, int dtype,
+                    void* workspace, int64_t workspace_bytes,
+                    sa_stream_t stream);
+
+/*
  * Per-tensor absmax quantisation to float8_e4m3fn, entirely on the device:
  *   scale = max(amax|x| / 448, 1e-12);  x8 = e4m3fn(clamp(x / scale, +-448))
  * x: n contiguous elements of dtype (SA_F32/SA_F16/SA_BF16); x8: n bytes.

@@ -37,6 +37,11 @@
 #include "flash_f32.hpp"
 #include "flash_wide.hpp"
 
+#include <algorithm>
+#include <functional>
+#include <mutex>
+#include <vector>
+
 namespace sa {
 namespace {
 
@@ -72,6 +77,11 @@ struct BwdParams {
     int B, Hq, Hkv, T, G, window;
     int dr;  // head dim of the tensors (<= D, a multiple of 8; columns past it read as zero, are not stored)
     float scale;
+    // dK/dV split over the query tiles: n_split blocks per (key block, KV
+    // head), each writing fp32 partials [n_split][2][B * Hkv][T][D] into part
+    // (summed by bwd_split_reduce_kernel); 1 = no split, results stored directly
+    int n_split;
+    float* part;
 };
 
 // Plain (cached) 16-byte global load: tiles here are re-read by many blocks.
@@ -408,9 +418,25 @@ __global__ __launch_bounds__(kBwdThreads, kBwdDkdvMinBlocks) void flash_bwd_dkdv
     const int l32 = lane & 31;
 
     const int nkb = (p.T + kBwdBK - 1) / kBwdBK;
+    // Block -> (ob, split): ob indexes the unsplit grid, split the block's
+    // share of ob's query tiles.  When that grid is a multiple of 8 blocks
+    // the n_split blocks of one ob run on ob's XCD (blocks are dealt to the
+    // XCDs by index mod 8), one after another in its dispatch order.
+    const int n_split = p.n_split;
+    int ob = static_cast<int>(blockIdx.x), split = 0;
+    if (n_split > 1) {
+        if (((nkb * p.B * p.Hkv) & 7) == 0) {
+            const int j = ob >> 3;
+            split = j % n_split;
+            ob = ((j / n_split) << 3) | (ob & 7);
+        } else {
+            split = ob % n_split;
+            ob /= n_split;
+        }
+    }
     int kb, unit, sub;
     // earliest key blocks see the most queries: first
-    grouped_block(blockIdx.x, p.B * p.Hkv, 1, nkb, kBwdXcdSlots, kb, unit, sub);
+    grouped_block(ob, p.B * p.Hkv, 1, nkb, kBwdXcdSlots, kb, unit, sub);
     const int b = unit / p.Hkv;
     const int hk = unit - b * p.Hkv;
     const int T_ = p.T;
@@ -451,7 +477,10 @@ __global__ __launch_bounds__(kBwdThreads, kBwdDkdvMinBlocks) void flash_bwd_dkdv
     const int qt_begin = k_start / kBwdQT;
     const int qt_end = W > 0 ? min(n_qt, (k_start + kBwdBK - 1 + W - 1) / kBwdQT + 1) : n_qt;
     const int nq = qt_end - qt_begin;  // >= 1 (k_start < T)
-    const int n_it = p.G * nq;
+    const int n_it_all = p.G * nq;
+    // this block's iterations [it_lo, n_it) of the n_it_all (head, query tile) pairs
+    const int it_lo = static_cast<int>(static_cast<int64_t>(split) * n_it_all / n_split);
+    const int n_it = static_cast<int>(static_cast<int64_t>(split + 1) * n_it_all / n_split);
     const float sc = p.scale;
 
     const int qsb = static_cast<int>(p.qs[2] * 2), dsb = static_cast<int>(p.dos[2] * 2);  // row strides (bytes)
@@ -589,10 +618,14 @@ __global__ __launch_bounds__(kBwdThreads, kBwdDkdvMinBlocks) void flash_bwd_dkdv
     };
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
-    issue_tile(0, S0{});
-    store_rs(0);
-    tile_wait_vmem();
-    __syncthreads();
+    // (it_lo < n_it for every block unless a split holds no iteration; the
+    // branch is block-uniform, so every wave meets the same barriers)
+    if (it_lo < n_it) {
+        issue_tile(it_lo, S0{});
+        store_rs(0);
+        tile_wait_vmem();
+        __syncthreads();
+    }
     // iteration it reads stage `cur` while the DMA fills stage `nxt` with it + 1
     auto iteration = [&](int it, auto cur, auto nxt) {
         const bool has_next = it + 1 < n_it;
@@ -602,9 +635,30 @@ __global__ __launch_bounds__(kBwdThreads, kBwdDkdvMinBlocks) void flash_bwd_dkdv
         tile_wait_vmem();
         __syncthreads();
     };
-    for (int it = 0; it < n_it; it += 2) {
+    for (int it = it_lo; it < n_it; it += 2) {
         iteration(it, S0{}, S1{});
         if (it + 1 < n_it) iteration(it + 1, S1{}, S0{});
+    }
+
+    if (n_split > 1) {
+        // fp32 partials (zeros for a split without iterations), all D columns
+        if (kj < T_) {
+            const int64_t bh = static_cast<int64_t>(p.B) * p.Hkv;
+            float* pk = p.part + ((static_cast<int64_t>(split) * 2 * bh + unit) * T_ + kj) * D;
+            float* pv = pk + bh * T_ * D;
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+                for (int vg = 0; vg < 4; ++vg) {
+                    const int d0 = dt * 32 + vg * 8 + hi * 4;
+                    *reinterpret_cast<float4*>(pk + d0) = float4{dkacc[dt][vg * 4 + 0], dkacc[dt][vg * 4 + 1],
+                                                                 dkacc[dt][vg * 4 + 2], dkacc[dt][vg * 4 + 3]};
+                    *reinterpret_cast<float4*>(pv + d0) = float4{dvacc[dt][vg * 4 + 0], dvacc[dt][vg * 4 + 1],
+                                                                 dvacc[dt][vg * 4 + 2], dvacc[dt][vg * 4 + 3]};
+                }
+            }
+        }
+        return;
     }
 
     // dS was kept without its factor 2 scale (1/R_i is already in).
@@ -631,17 +685,51 @@ __global__ __launch_bounds__(kBwdThreads, kBwdDkdvMinBlocks) void flash_bwd_dkdv
     }
 }
 
+// dK, dV = the sum of the n_split fp32 partials (in split order, so the
+// result does not depend on timing), dK times 2 scale; one thread per four
+// columns of a key row.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void bwd_split_reduce_kernel(BwdParams p, int64_t n_quads) {
+    const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (gid >= n_quads) return;
+    const int64_t row = gid / (D / 4);  // (b * Hkv + hk) * T + key
+    const int d0 = static_cast<int>(gid - row * (D / 4)) * 4;
+    if (d0 >= p.dr) return;
+    const int64_t plane = static_cast<int64_t>(p.B) * p.Hkv * p.T * D;
+    const float* src = p.part + row * D + d0;
+    float4 k4 = float4{0.f, 0.f, 0.f, 0.f}, v4 = float4{0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < p.n_split; ++s) {
+        const float4 a = *reinterpret_cast<const float4*>(src + (2 * s) * plane);
+        const float4 c = *reinterpret_cast<const float4*>(src + (2 * s + 1) * plane);
+        k4.x += a.x; k4.y += a.y; k4.z += a.z; k4.w += a.w;
+        v4.x += c.x; v4.y += c.y; v4.z += c.z; v4.w += c.w;
+    }
+    const float f = 2.f * p.scale;
+    const int64_t bh = row / p.T;
+    const int key = static_cast<int>(row - bh * p.T);
+    const int b = static_cast<int>(bh / p.Hkv);
+    const int hk = static_cast<int>(bh - static_cast<int64_t>(b) * p.Hkv);
+    T* dk = static_cast<T*>(p.dk) + b * p.dks[0] + hk * p.dks[1] + key * p.dks[2] + d0;
+    T* dv = static_cast<T*>(p.dv) + b * p.dvs[0] + hk * p.dvs[1] + key * p.dvs[2] + d0;
+    *reinterpret_cast<uint2*>(dk) = uint2{pack2<T>(k4.x * f, k4.y * f), pack2<T>(k4.z * f, k4.w * f)};
+    *reinterpret_cast<uint2*>(dv) = uint2{pack2<T>(v4.x, v4.y), pack2<T>(v4.z, v4.w)};
+}
+
 template <typename T, int D, bool PART>
 int launch_bwd_part(const BwdParams& prm, int exact, hipStream_t st) {
     const unsigned nqb = static_cast<unsigned>((prm.T + kBwdBQ - 1) / kBwdBQ);
     const unsigned nkb = static_cast<unsigned>((prm.T + kBwdBK - 1) / kBwdBK);
-    const dim3 gq(nqb * prm.B * prm.Hq), gk(nkb * prm.B * prm.Hkv), blk(kBwdThreads);
+    const dim3 gq(nqb * prm.B * prm.Hq), gk(nkb * prm.B * prm.Hkv * prm.n_split), blk(kBwdThreads);
     if (exact) {
         flash_bwd_dq_kernel<T, D, true, PART><<<gq, blk, 0, st>>>(prm);
         flash_bwd_dkdv_kernel<T, D, true, PART><<<gk, blk, 0, st>>>(prm);
     } else {
         flash_bwd_dq_kernel<T, D, false, PART><<<gq, blk, 0, st>>>(prm);
         flash_bwd_dkdv_kernel<T, D, false, PART><<<gk, blk, 0, st>>>(prm);
+    }
+    if (prm.n_split > 1) {
+        const int64_t n_quads = static_cast<int64_t>(prm.B) * prm.Hkv * prm.T * (D / 4);
+        bwd_split_reduce_kernel<T, D><<<static_cast<unsigned>((n_quads + 255) / 256), 256, 0, st>>>(prm, n_quads);
     }
     return status_from_launch();
 }
@@ -666,15 +754,117 @@ int launch_bwd_d(const BwdParams& prm, int exact, hipStream_t st) {
 // (b, h, t) strides keep every row 16-byte aligned; d stride 1.
 bool bwd_strides_ok(const int64_t* s) { return s[3] == 1 && s[0] % 8 == 0 && s[1] % 8 == 0 && s[2] % 8 == 0; }
 
+// Kernel head dim of the 16-bit kernels for head dim dr <= 128.
+int bwd_kernel_d(int dr) { return dr <= 32 ? 32 : dr <= 64 ? 64 : 128; }
+
+int64_t bwd_part_bytes(int n_split, int B, int Hkv, int T, int dr) {
+    return n_split > 1 ? static_cast<int64_t>(n_split) * 2 * B * Hkv * T * bwd_kernel_d(dr) * 4 : 0;
+}
+
+// (head, query tile) iterations of dK/dV key block kb, as the kernel counts them.
+int dkdv_iterations(int kb, int T, int G, int W) {
+    const int n_qt = (T + kBwdQT - 1) / kBwdQT;
+    const int k_start = kb * kBwdBK;
+    const int qt_begin = k_start / kBwdQT;
+    const int qt_end = W > 0 ? std::min(n_qt, (k_start + kBwdBK - 1 + W - 1) / kBwdQT + 1) : n_qt;
+    return G * (qt_end - qt_begin);
+}
+
+// Query-tile splits of the dK/dV blocks.  Causally, key block kb sees the
+// query tiles from its own on, so the first blocks hold the most work; in a
+// grid that does not fill the chip several times over, the GPU idles while
+// they finish.  Splitting every block's iterations n_split ways (fp32
+// partials, summed by one more kernel) shortens that tail at the cost of the
+// partials' traffic.  The count is the one of 1, 2, 4, 8, 16 with the least
+// estimated time: blocks dealt to the XCDs round-robin in the kernel's order
+// (heaviest key blocks first), each XCD running kBwdXcdSlots at once, a block
+// costing its iterations plus two for its set-up and stores, plus a fifth of
+// the longest block for the ragged end, an iteration at 5 us (a 64-query
+// tile of 128 keys with two blocks per CU), and the partials' writes and
+// reads at 5 TB/s.  (Fitted to measured times of shapes from 1 x 2 KV heads
+// x 4096 keys to 2 x 8 x 16384, where it picks the fastest count of each.)
+int dkdv_split_count_uncached(int B, int Hkv, int T, int G, int W, int dr) {
+    const int nkb = (T + kBwdBK - 1) / kBwdBK;
+    const int64_t blocks = static_cast<int64_t>(nkb) * B * Hkv;
+    const int units = B * Hkv;
+    int best = 1;
+    double best_t = 0.0;
+    std::vector<double> slots;
+    for (int S = 1; S <= 16; S *= 2) {
+        if (blocks * S > 16384) break;
+        // XCD 0's share: every 8th block of the dispatch order (kb, unit, split)
+        slots.assign(kBwdXcdSlots, 0.0);
+        double longest = 0.0;
+        int64_t id = 0;
+        for (int kb = 0; kb < nkb; ++kb) {
+            const int it = dkdv_iterations(kb, T, G, W);
+            for (int64_t j = 0; j < static_cast<int64_t>(units) * S; ++j, ++id) {
+                if (id % 8) continue;
+                const int s = static_cast<int>(j % S);
+                const double cost = (static_cast<int64_t>(s + 1) * it / S - static_cast<int64_t>(s) * it / S) + 2.0;
+                longest = std::max(longest, cost);
+                std::pop_heap(slots.begin(), slots.end(), std::greater<double>());
+                slots.back() += cost;
+                std::push_heap(slots.begin(), slots.end(), std::greater<double>());
+            }
+        }
+        double t = (*std::max_element(slots.begin(), slots.end()) + 0.2 * longest) * 5.0;  // us
+        // the partials written, then read by the sum kernel
+        if (S > 1) t += 2.0 * static_cast<double>(bwd_part_bytes(S, B, Hkv, T, dr)) / 5e6 + 5.0;
+        if (S == 1 || t < best_t) {
+            best = S;
+            best_t = t;
+        }
+    }
+    return best;
+}
+
+// The estimate above costs up to ~0.1 ms of host time, so the last few
+// shapes' counts are kept (a training step asks for the same shapes again).
+int dkdv_split_count(int B, int Hkv, int T, int G, int W, int dr) {
+    const int64_t blocks = static_cast<int64_t>((T + kBwdBK - 1) / kBwdBK) * B * Hkv;
+    if (blocks >= 8 * kBwdXcdSlots * 8 || blocks == 0) return 1;
+    struct Entry {
+        int key[6];
+        int n_split;
+    };
+    static std::mutex mu;
+    static Entry cache[16];
+    static int n_cached = 0, next = 0;
+    const int key[6] = {B, Hkv, T, G, W, bwd_kernel_d(dr)};
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        for (int i = 0; i < n_cached; ++i)
+            if (std::equal(key, key + 6, cache[i].key)) return cache[i].n_split;
+    }
+    const int n = dkdv_split_count_uncached(B, Hkv, T, G, W, dr);
+    std::lock_guard<std::mutex> lock(mu);
+    Entry& e = cache[next];
+    std::copy(key, key + 6, e.key);
+    e.n_split = n;
+    next = (next + 1) % 16;
+    n_cached = std::min(n_cached + 1, 16);
+    return n;
+}
+
 }  // namespace
 }  // namespace sa
 
-extern "C" int sa_flash_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
-                            const float* row_sums, void* dq, void* dk, void* dv, float* delta_ws, int B, int Hq,
-                            int Hkv, int T, int D, const int64_t* q_strides, const int64_t* k_strides,
-                            const int64_t* v_strides, const int64_t* o_strides, const int64_t* do_strides,
-                            const int64_t* dq_strides, const int64_t* dk_strides, const int64_t* dv_strides,
-                            float scale, int window_size, int exact_math, int dtype, sa_stream_t stream) {
+extern "C" int64_t sa_flash_bwd_workspace_size(int B, int Hq, int Hkv, int T, int D, int window_size, int dtype) {
+    using namespace sa;
+    if (B < 0 || Hq <= 0 || Hkv <= 0 || T < 0 || D <= 0 || Hq % Hkv != 0 || window_size < 0) return -1;
+    if (dtype != SA_BF16 && dtype != SA_F16) return 0;
+    if (D > 128 || B == 0 || T == 0) return 0;
+    return bwd_part_bytes(dkdv_split_count(B, Hkv, T, Hq / Hkv, window_size, D), B, Hkv, T, D);
+}
+
+extern "C" int sa_flash_bwd_ws(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                               const float* row_sums, void* dq, void* dk, void* dv, float* delta_ws, int B, int Hq,
+                               int Hkv, int T, int D, const int64_t* q_strides, const int64_t* k_strides,
+                               const int64_t* v_strides, const int64_t* o_strides, const int64_t* do_strides,
+                               const int64_t* dq_strides, const int64_t* dk_strides, const int64_t* dv_strides,
+                               float scale, int window_size, int exact_math, int dtype, void* workspace,
+                               int64_t workspace_bytes, sa_stream_t stream) {
     using namespace sa;
     if (dtype == SA_F32) {
         const int64_t* const all[8] = {q_strides,  k_strides,  v_strides,  o_strides,
@@ -734,8 +924,30 @@ extern "C" int sa_flash_bwd(const void* q, const void* k, const void* v, const v
     prm.window = window_size;
     prm.dr = D;
     prm.scale = scale;
+    // the library's split count, or the largest power of two below it whose
+    // partials fit the workspace
+    prm.n_split = 1;
+    prm.part = nullptr;
+    if (workspace && workspace_bytes > 0) {
+        if (!aligned16(workspace)) return SA_ERR_BAD_STRIDE;
+        int ns = dkdv_split_count(B, Hkv, T, prm.G, window_size, D);
+        while (ns > 1 && bwd_part_bytes(ns, B, Hkv, T, D) > workspace_bytes) ns /= 2;
+        prm.n_split = ns;
+        prm.part = static_cast<float*>(workspace);
+    }
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int ex = exact_math ? 1 : 0;
     if (dtype == SA_BF16) return launch_bwd_d<bf16>(prm, ex, s);
     return launch_bwd_d<f16>(prm, ex, s);
+}
+
+extern "C" int sa_flash_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                            const float* row_sums, void* dq, void* dk, void* dv, float* delta_ws, int B, int Hq,
+                            int Hkv, int T, int D, const int64_t* q_strides, const int64_t* k_strides,
+                            const int64_t* v_strides, const int64_t* o_strides, const int64_t* do_strides,
+                            const int64_t* dq_strides, const int64_t* dk_strides, const int64_t* dv_strides,
+                            float scale, int window_size, int exact_math, int dtype, sa_stream_t stream) {
+    return sa_flash_bwd_ws(q, k, v, o, dout, row_sums, dq, dk, dv, delta_ws, B, Hq, Hkv, T, D, q_strides, k_strides,
+                           v_strides, o_strides, do_strides, dq_strides, dk_strides, dv_strides, scale, window_size,
+                           exact_math, dtype, nullptr, 0, stream);
 }

@@ -59,6 +59,11 @@ SIGNATURES = {
     "sa_flash_bwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                              c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, _I64P, _I64P, _I64P,
                              _I64P, _I64P, _I64P, _I64P, _I64P, c_float, c_int, c_int, c_int, c_void_p]),
+    "sa_flash_bwd_workspace_size": (c_int64, [c_int, c_int, c_int, c_int, c_int, c_int, c_int]),
+    "sa_flash_bwd_ws": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, _I64P, _I64P, _I64P,
+                                _I64P, _I64P, _I64P, _I64P, _I64P, c_float, c_int, c_int, c_int, c_void_p, c_int64,
+                                c_void_p]),
     "sa_fp8_quantize": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_void_p, c_void_p, c_void_p]),
     "sa_flash_fp8_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                  c_void_p, c_int, c_int, c_int, c_int, c_int, _I64P, _I64P, _I64P, _I64P,

@@ -642,15 +642,20 @@ def _sp2norm_flash_bwd(q, k, v, o, do, row_sums, scale, n_kv_groups=1, window_si
     delta = torch.empty(B, H_q, T, device=q.device, dtype=torch.float32)
     rs = row_sums.contiguous()
     lib = _lib.load()
+    # fp32 partials of the dK/dV blocks split over their query tiles (short
+    # grids with long causal rows), when the library splits them
+    ws_bytes = int(lib.sa_flash_bwd_workspace_size(B, H_q, H_kv, T, D, int(window_size), _DTYPE_CODE[q.dtype]))
+    ws = torch.empty(ws_bytes // 4, device=q.device, dtype=torch.float32) if ws_bytes > 0 else None
     with _device_of(q):
-        st = lib.sa_flash_bwd(
+        st = lib.sa_flash_bwd_ws(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(), rs.data_ptr(),
             dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr(), B, H_q, H_kv, T, D,
             _lib.strides(q), _lib.strides(k), _lib.strides(v), _lib.strides(o), _lib.strides(do),
             _lib.strides(dq), _lib.strides(dk), _lib.strides(dv), float(scale), int(window_size),
-            0 if use_fast_sqrt else 1, _DTYPE_CODE[q.dtype], _stream(q),
+            0 if use_fast_sqrt else 1, _DTYPE_CODE[q.dtype], None if ws is None else ws.data_ptr(),
+            max(ws_bytes, 0), _stream(q),
         )
-    _lib.check(st, "sa_flash_bwd")
+    _lib.check(st, "sa_flash_bwd_ws")
     return dq, dk, dv
 
 

@@ -188,6 +188,30 @@ def test_flash_fp32_argument_errors():
     assert bwd(good) == 0
 
 
+def test_flash_bwd_workspace_size():
+    # fp32 partials of dK / dV for split key blocks: only for 16-bit head dims
+    # up to 128 and grids that leave the GPU idle behind the first key blocks;
+    # the size is n_split * 2 (dK, dV) * B * Hkv * T * kernel head dim * 4
+    lib = _lib.load()
+    ws = lambda B, Hq, Hkv, T, D, W=0, dt=_lib.SA_BF16: lib.sa_flash_bwd_workspace_size(B, Hq, Hkv, T, D, W, dt)
+    for B, Hq, Hkv, T, D, Dk in ((1, 32, 8, 8192, 128, 128), (1, 8, 1, 65536, 128, 128), (1, 4, 2, 333, 40, 64)):
+        n = ws(B, Hq, Hkv, T, D)
+        unit = 2 * B * Hkv * T * Dk * 4
+        assert n > 0 and n % unit == 0 and n // unit in (2, 4, 8, 16), (B, Hq, Hkv, T, D, n)
+        assert ws(B, Hq, Hkv, T, D, dt=_lib.SA_F16) == n
+    assert ws(1, 32, 8, 8192, 128, dt=_lib.SA_F32) == 0  # fp32 kernels do not split
+    assert ws(1, 32, 8, 8192, 200) == 0  # nor the head-dim-256 kernels
+    assert ws(16, 32, 8, 4096, 128) == 0  # 4096 key blocks fill the GPU
+    assert ws(0, 32, 8, 8192, 128) == 0 and ws(1, 32, 8, 0, 128) == 0
+    assert ws(1, 30, 8, 8192, 128) == -1 and ws(-1, 32, 8, 64, 128) == -1
+    # a workspace that is not 16-byte aligned is refused before any launch
+    d = ctypes.c_void_p(256)
+    s = (ctypes.c_int64 * 4)(8 * 64 * 128, 64 * 128, 128, 1)
+    st = lib.sa_flash_bwd_ws(d, d, d, d, d, d, d, d, d, d, 1, 8, 8, 64, 128, s, s, s, s, s, s, s, s, 0.1, 0, 0,
+                             _lib.SA_BF16, ctypes.c_void_p(264), 1 << 20, None)
+    assert st == -5
+
+
 def test_paged_decode_head_dims():
     # D must be a multiple of 8 in 8..512; checked before any HIP call
     lib = _lib.load()
