@@ -380,6 +380,9 @@ def bench_next_rows(torch):
       layout with Hq 16 / Hkv 4 (config 5's bytes), at head dim 512 with
       Hq 8 / Hkv 2 (the same bytes), and paged decode over
       fp32 caches (and fp32 q over bf16 and e4m3fn caches) on config 5's layout;
+    - the bf16 attention backward over long rows and few KV heads
+      ([1, 32, 8192, 128] with 8 KV heads), with its dK/dV key blocks split
+      over their query tiles (the public path) and unsplit;
     - RoPE-fused attention forward on config 3's shape (K rotated once by a
       streaming kernel, Q in registers; the time includes the rotation),
       and the RoPE + W_o projection variant (RoPE forward plus one fp32-
@@ -439,6 +442,36 @@ def bench_next_rows(torch):
                              "fwd_frac_bf16_peak": round(fl256 / us_f / 1e6 / BF16_PEAK_TFLOPS, 4),
                              "bwd_frac_bf16_peak": round(2.5 * fl256 / us_b / 1e6 / BF16_PEAK_TFLOPS, 4)}
     del q, k, v, do, o, rs
+    torch.cuda.empty_cache()
+
+    # long rows over few KV heads: bf16 backward at B 1, Hq 32, Hkv 8,
+    # T 8192 (512 dK/dV key blocks), with the dK/dV blocks split over their
+    # query tiles (the public path) and unsplit (sa_flash_bwd)
+    Bl, Hl, Hkl, Tl = 1, 32, 8, 8192
+    q, do = (torch.randn(Bl, Hl, Tl, D, generator=gen, device=dev).to(torch.bfloat16) for _ in range(2))
+    k, v = (torch.randn(Bl, Hkl, Tl, D, generator=gen, device=dev).to(torch.bfloat16) for _ in range(2))
+    sc = 1 / math.sqrt(D)
+    o, rs = sa.kernels._sp2norm_flash_fwd(q, k, v, sc, Hl // Hkl)
+    us_s = med(lambda: sa.kernels._sp2norm_flash_bwd(q, k, v, o, do, rs, sc, Hl // Hkl), iters=20, warmup=3)
+    lib = sa._lib.load()
+    grads = [torch.empty_like(t) for t in (q, k, v)]
+    delta = torch.empty(Bl, Hl, Tl, device=dev)
+
+    def unsplit():
+        st = lib.sa_flash_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(), rs.data_ptr(),
+                              grads[0].data_ptr(), grads[1].data_ptr(), grads[2].data_ptr(), delta.data_ptr(), Bl, Hl,
+                              Hkl, Tl, D, *(sa._lib.strides(t) for t in (q, k, v, o, do, *grads)), sc, 0, 0,
+                              sa._lib.SA_BF16, torch.cuda.current_stream().cuda_stream)
+        sa._lib.check(st, "sa_flash_bwd")
+
+    us_u = med(unsplit, iters=20, warmup=3)
+    n_split = lib.sa_flash_bwd_workspace_size(Bl, Hl, Hkl, Tl, D, 0, sa._lib.SA_BF16) // (2 * Bl * Hkl * Tl * D * 4)
+    fl_l = 2.5 * attn_flops(Bl, Hl, Tl, D)
+    out["attention_bwd_long_rows"] = {"shape_q": [Bl, Hl, Tl, D], "kv_heads": Hkl, "n_split": int(n_split),
+                                      "bwd_us": round(us_s, 1), "bwd_unsplit_us": round(us_u, 1),
+                                      "bwd_frac_bf16_peak": round(fl_l / us_s / 1e6 / BF16_PEAK_TFLOPS, 4),
+                                      "bwd_unsplit_frac_bf16_peak": round(fl_l / us_u / 1e6 / BF16_PEAK_TFLOPS, 4)}
+    del q, k, v, do, o, rs, grads, delta
     torch.cuda.empty_cache()
 
     # paged decode at head dim 256 on config 5's layout with Hq 16 / Hkv 4
