@@ -375,8 +375,8 @@ def bench_next_rows(torch):
     """The rows built after the hot path, each timed by the same protocol:
     - fp32 fused attention forward and backward on config 3's shape (fp32
       MFMA, against the 157.3 TFLOP/s dense fp32 peak);
-    - bf16 attention forward and backward at head dim 256, [4,16,4096,256]
-      (config 3's FLOPs), and paged decode at head dim 256 on config 5's
+    - bf16 attention forward and backward at head dim 256, [4,16,4096,256],
+      and at head dim 512, [4,8,4096,512] (both config 3's FLOPs), and paged decode at head dim 256 on config 5's
       layout with Hq 16 / Hkv 4 (config 5's bytes), at head dim 512 with
       Hq 8 / Hkv 2 (the same bytes), and paged decode over
       fp32 caches (and fp32 q over bf16 and e4m3fn caches) on config 5's layout;
@@ -441,6 +441,19 @@ def bench_next_rows(torch):
     out["attention_d256"] = {"shape": [4, 16, L, 256], "fwd_us": round(us_f, 1), "bwd_us": round(us_b, 1),
                              "fwd_frac_bf16_peak": round(fl256 / us_f / 1e6 / BF16_PEAK_TFLOPS, 4),
                              "bwd_frac_bf16_peak": round(2.5 * fl256 / us_b / 1e6 / BF16_PEAK_TFLOPS, 4)}
+    del q, k, v, do, o, rs
+    torch.cuda.empty_cache()
+
+    # head dim 512 (4-wave blocks, one wave per SIMD): [4,8,4096,512] has config 3's FLOPs
+    q, k, v, do = (torch.randn(4, 8, L, 512, generator=gen, device=dev).to(torch.bfloat16) for _ in range(4))
+    sc512 = 1 / math.sqrt(512)
+    o, rs = sa.kernels._sp2norm_flash_fwd(q, k, v, sc512)
+    us_f = med(lambda: sa.kernels._sp2norm_flash_fwd(q, k, v, sc512), iters=20, warmup=3)
+    us_b = med(lambda: sa.kernels._sp2norm_flash_bwd(q, k, v, o, do, rs, sc512), iters=20, warmup=3)
+    fl512 = attn_flops(4, 8, L, 512)
+    out["attention_d512"] = {"shape": [4, 8, L, 512], "fwd_us": round(us_f, 1), "bwd_us": round(us_b, 1),
+                             "fwd_frac_bf16_peak": round(fl512 / us_f / 1e6 / BF16_PEAK_TFLOPS, 4),
+                             "bwd_frac_bf16_peak": round(2.5 * fl512 / us_b / 1e6 / BF16_PEAK_TFLOPS, 4)}
     del q, k, v, do, o, rs
     torch.cuda.empty_cache()
 

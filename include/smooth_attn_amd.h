@@ -166,9 +166,9 @@ int sa_softmax_fwd_launch_info(const void* x, const void* y, int64_t n_rows,
  * 16-bit type, 4 of fp32), base pointers 16-byte aligned, and for bf16/fp16
  * K and V row strides at most 16 MiB.  row_sums (nullable): fp32 [B, Hq, T] contiguous,
  * receives sum_j y_ij + 1e-12.  window_size 0 = full causal.  D: bf16 /
- * fp16 any multiple of 8 in 8..256 (kernels built for 32, 64, 128 and 256
- * read only the first D columns and store only those), fp32 any multiple of
- * 4 in 4..256 (the same way).  exact_math != 0 selects a correctly rounded
+ * fp16 any multiple of 8 in 8..512 (kernels built for 32, 64, 128, 256 and
+ * 512 read only the first D columns and store only those), fp32 any
+ * multiple of 4 in 4..256 (the same way).  exact_math != 0 selects a correctly rounded
  * sqrt.
  * Replaces _sp2norm_flash_fwd (kernels.py:1912-1931) and its kernel
  * _sp2norm_flash_fwd_with_rowsum_kernel (:1536-1631).
@@ -247,7 +247,7 @@ int sa_fp8_quantize(const void* x, void* x8, int64_t n, int dtype,
  * attn_scale on fp8 MFMA; y rounded to bf16 and multiplied with v (as bf16)
  * on bf16 MFMA, times v_s.  o: bf16 [B, Hq, T, D]; row_sums nullable.
  * Layout rules as sa_flash_fwd; D in {32, 64, 128} (the Python wrapper runs
- * head dims 129..256 on sa_flash_fwd with the fp8 codes widened to bf16).
+ * head dims 129..512 on sa_flash_fwd with the fp8 codes widened to bf16).
  * Replaces _sp2norm_fp8_flash_fwd (kernels.py:2604-2627) and its kernel
  * _sp2norm_fp8_flash_fwd_kernel (:2498-2589).
  */

@@ -1,7 +1,7 @@
-// 16-bit (bf16 / fp16) fused causal squareplus attention at head dim 256,
-// forward and backward, on v_mfma_f32_16x16x32_{bf16,f16}.  Head dims
-// 136..248 (multiples of 8) run on the same kernels with the columns past
-// them read as zeros and not stored.
+// 16-bit (bf16 / fp16) fused causal squareplus attention at head dims 256
+// and 512, forward and backward, on v_mfma_f32_16x16x32_{bf16,f16}.  Head
+// dims 136..248 and 264..504 (multiples of 8) run on the next of these
+// kernels with the columns past them read as zeros and not stored.
 //
 // Same mathematics and rounding points as the D <= 128 kernels
 // (flash_fwd.hip, flash_bwd.hip; reference kernels.py:1536-1631 and
@@ -14,7 +14,8 @@
 // waves per SIMD, where 32 rows on the 32x32x16 MFMA would need one wave per
 // SIMD.  Blocks of 8 waves own 128 rows and walk 64-row tiles of the other
 // side through a 2-stage LDS ring (two 64 KB arrays) filled by direct-to-LDS
-// loads, one barrier per tile; the tile loops are unrolled by two so each
+// loads, one barrier per tile (D = 512: 4 waves, one per SIMD, own 64 rows
+// and walk 32-row tiles); the tile loops are unrolled by two so each
 // tile names its stage statically and its LDS reads never wait for the DMA
 // filling the other stage.  dK and dV are separate kernels (both
 // accumulators plus the K and V operands would not fit two waves per SIMD).
@@ -97,9 +98,30 @@ __device__ __forceinline__ int wide_src_off(int drow, int c, int64_t rs, int dr)
 // 2-stage LDS ring (2 x 64 KB); K rows store logical chunk c at c ^ (r & 15)
 // (16-byte row reads, 16 rows per cycle), V rows at c ^ 2 (r & 7)
 // (transposing reads, 8 rows x 32 bytes per cycle): both conflict-free.
-constexpr int kFW = 8;             // waves per block
-constexpr int kFRows = 16 * kFW;   // query (key) rows per block
-constexpr int kFKT = 64;           // rows per staged tile
+// Block shapes.  D = 256: 8 waves (two per SIMD), 128 rows per block,
+// 64-row tiles.  D = 512 (head dims 264..512): the accumulators and
+// operands of 16 rows take more than half of a SIMD's registers, so blocks
+// of 4 waves run one per SIMD, 64 rows per block, over 32-row tiles.  Both
+// stage 2 x 2 tiles of 32 KB (one block per CU).
+template <int D>
+struct WideCfg {
+    static constexpr int NW = D > 256 ? 4 : 8;    // waves per block
+    static constexpr int ROWS = 16 * NW;          // query (key) rows per block
+    static constexpr int KT = D > 256 ? 32 : 64;  // rows per staged tile
+};
+constexpr int kWideMaxKT = 64;
+
+// Per-lane source offset of DMA instruction i of a staged tile: the lane's
+// chunk lies in tile row drow + i * rpi (drow from the buffer resource of
+// instruction i, which starts rpi * i rows in), logical chunk pch ^ swz(row).
+// When rpi is a multiple of 16 the swizzles (functions of row bits 0-3) give
+// every instruction the same offset.
+template <bool PART, int NI, int RPI, typename Swz>
+__device__ __forceinline__ void wide_dma_offsets(int (&off)[NI], int drow, int pch, int64_t rs, int dr, Swz swz) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+        off[i] = (RPI % 16 == 0 && i > 0) ? off[0] : wide_src_off<PART>(drow, pch ^ swz(drow + i * RPI), rs, dr);
+}
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 template <typename T>
@@ -123,15 +145,15 @@ struct Mfma16<f16> {
 // weights carry 1/scale^2 (one FMA per score fewer), cancelled between P V
 // and the row sum.
 template <typename T, int D, bool EXACT, bool FOLD>
-__global__ __launch_bounds__(64 * kFW) void flash_fwd_wide_kernel(WideParams<T> p) {
+__global__ __launch_bounds__(64 * WideCfg<D>::NW) void flash_fwd_wide_kernel(WideParams<T> p) {
     using V8 = typename MfmaOps<T>::vec8;
+    constexpr int kFW = WideCfg<D>::NW, kFRows = WideCfg<D>::ROWS, kFKT = WideCfg<D>::KT;
     constexpr int ROWB = D * 2;          // bytes per K / V row
     constexpr int TB = kFKT * ROWB;      // bytes per tile
     constexpr int CPR = ROWB / 16;       // 16-byte chunks per row
     constexpr int NI = TB / 1024 / kFW;  // DMA instructions per wave per tensor and tile
     constexpr int RPI = 64 * kFW / CPR;  // rows one round of kFW instructions covers
     constexpr int NKS = kFKT / 16;       // 16-key S^T subtiles per tile
-    static_assert(NI == 1 || RPI % 16 == 0, "one swizzled offset per lane");
     // Two ring stages ([K, V] each) in separate arrays, the tile loop unrolled
     // by two: each tile names its stage statically, so the compiler knows its
     // LDS reads cannot touch the stage the next tile's DMA writes and does
@@ -161,10 +183,11 @@ __global__ __launch_bounds__(64 * kFW) void flash_fwd_wide_kernel(WideParams<T> 
     const unsigned char* vp = tile_uniform_ptr(reinterpret_cast<const unsigned char*>(p.v + b * p.vs[0] + hk * p.vs[1]));
     const int64_t krs = p.ks[2] * 2, vrs = p.vs[2] * 2;
 
-    // waves w and w + 4 share a SIMD: the second four take the row slots in
-    // reverse, so each SIMD pairs an early-row wave with a late-row one
+    // 8-wave blocks: waves w and w + 4 share a SIMD, and the second four take
+    // the row slots in reverse, so each SIMD pairs an early-row wave with a
+    // late-row one
     const int q_start = qb * kFRows;
-    const int slot = wave >= 4 ? 11 - wave : wave;
+    const int slot = (kFW == 8 && wave >= 4) ? 11 - wave : wave;
     const int q0w = q_start + 16 * slot;
     const int qi = q0w + i16;
     const int qrow = min(qi, T_ - 1);
@@ -188,8 +211,9 @@ __global__ __launch_bounds__(64 * kFW) void flash_fwd_wide_kernel(WideParams<T> 
     // weights), and so do columns past the head dim.
     const int drow = (wave * 64 + lane) / CPR;
     const int pch = (wave * 64 + lane) % CPR;
-    const int koff = wide_src_off<true>(drow, pch ^ (drow & 15), krs, p.dr);
-    const int voff = wide_src_off<true>(drow, pch ^ (2 * (drow & 7)), vrs, p.dr);
+    int koff[NI], voff[NI];
+    wide_dma_offsets<true, NI, RPI>(koff, drow, pch, krs, p.dr, [](int r) { return r & 15; });
+    wide_dma_offsets<true, NI, RPI>(voff, drow, pch, vrs, p.dr, [](int r) { return 2 * (r & 7); });
     auto issue = [&](int t, auto st) {
         const int k0 = t * kFKT;
         const int nrows = min(T_ - k0, kFKT);
@@ -199,10 +223,10 @@ __global__ __launch_bounds__(64 * kFW) void flash_fwd_wide_kernel(WideParams<T> 
             const int skip = i * RPI;
             tile_dma16(__builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(kp + (k0 + skip) * krs), 0,
                                                          max((nrows - skip) * static_cast<int>(krs), 0), 0x00020000),
-                       koff, lk + (i * kFW + wave) * 1024);
+                       koff[i], lk + (i * kFW + wave) * 1024);
             tile_dma16(__builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(vp + (k0 + skip) * vrs), 0,
                                                          max((nrows - skip) * static_cast<int>(vrs), 0), 0x00020000),
-                       voff, lk + TB + (i * kFW + wave) * 1024);
+                       voff[i], lk + TB + (i * kFW + wave) * 1024);
         }
     };
 
@@ -337,15 +361,15 @@ __device__ __forceinline__ int fk_swz(int r) { return ((r & 7) << 1) | ((r >> 3)
 // PART: the tensors' head dim p.dr is below D (columns past it read as zeros
 // and are not stored); the kernels with PART false serve dr == D.
 template <typename T, int D, bool EXACT, bool PART>
-__global__ __launch_bounds__(64 * kFW) void flash_bwd_dq_wide_kernel(WideParams<T> p) {
+__global__ __launch_bounds__(64 * WideCfg<D>::NW) void flash_bwd_dq_wide_kernel(WideParams<T> p) {
     using V8 = typename MfmaOps<T>::vec8;
+    constexpr int kFW = WideCfg<D>::NW, kFRows = WideCfg<D>::ROWS, kFKT = WideCfg<D>::KT;
     constexpr int ROWB = D * 2;
     constexpr int TB = kFKT * ROWB;
     constexpr int CPR = ROWB / 16;
     constexpr int NI = TB / 1024 / kFW;
     constexpr int RPI = 64 * kFW / CPR;
     constexpr int NKS = kFKT / 16;
-    static_assert(NI == 1 || RPI % 16 == 0, "one swizzled offset per lane");
     // Two ring stages ([K, V] each) in separate arrays, the tile loop unrolled
     // by two: each tile names its stage statically, so the compiler knows its
     // LDS reads cannot touch the stage the next tile's DMA writes and does
@@ -375,7 +399,7 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_dq_wide_kernel(WideParams<
     const int64_t krs = p.ks[2] * 2, vrs = p.vs[2] * 2;
 
     const int q_start = qb * kFRows;
-    const int slot = wave >= 4 ? 11 - wave : wave;
+    const int slot = (kFW == 8 && wave >= 4) ? 11 - wave : wave;
     const int q0w = q_start + 16 * slot;
     const int qi = q0w + i16;
     const int qrow = min(qi, T_ - 1);
@@ -413,8 +437,9 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_dq_wide_kernel(WideParams<
 
     const int drow = (wave * 64 + lane) / CPR;
     const int pch = (wave * 64 + lane) % CPR;
-    const int koff = wide_src_off<PART>(drow, pch ^ fk_swz(drow), krs, p.dr);
-    const int voff = wide_src_off<PART>(drow, pch ^ (drow & 15), vrs, p.dr);
+    int koff[NI], voff[NI];
+    wide_dma_offsets<PART, NI, RPI>(koff, drow, pch, krs, p.dr, [](int r) { return fk_swz(r); });
+    wide_dma_offsets<PART, NI, RPI>(voff, drow, pch, vrs, p.dr, [](int r) { return r & 15; });
     auto issue = [&](int t, auto st) {
         const int k0 = t * kFKT;
         const int nrows = min(T_ - k0, kFKT);
@@ -424,10 +449,10 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_dq_wide_kernel(WideParams<
             const int skip = i * RPI;
             tile_dma16(__builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(kp + (k0 + skip) * krs), 0,
                                                          max((nrows - skip) * static_cast<int>(krs), 0), 0x00020000),
-                       koff, lk + (i * kFW + wave) * 1024);
+                       koff[i], lk + (i * kFW + wave) * 1024);
             tile_dma16(__builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(vp + (k0 + skip) * vrs), 0,
                                                          max((nrows - skip) * static_cast<int>(vrs), 0), 0x00020000),
-                       voff, lk + TB + (i * kFW + wave) * 1024);
+                       voff[i], lk + TB + (i * kFW + wave) * 1024);
         }
     };
 
@@ -544,15 +569,15 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_dq_wide_kernel(WideParams<
 // way (row reads: c ^ (r & 15); transposing reads: c ^ 2 (r & 7)).
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool EXACT, bool DK, bool PART>
-__global__ __launch_bounds__(64 * kFW) void flash_bwd_kv_wide_kernel(WideParams<T> p) {
+__global__ __launch_bounds__(64 * WideCfg<D>::NW) void flash_bwd_kv_wide_kernel(WideParams<T> p) {
     using V8 = typename MfmaOps<T>::vec8;
+    constexpr int kFW = WideCfg<D>::NW, kFRows = WideCfg<D>::ROWS, kFKT = WideCfg<D>::KT;
     constexpr int ROWB = D * 2;
-    constexpr int TB = kFKT * ROWB;     // bytes per 64-row query tile
+    constexpr int TB = kFKT * ROWB;     // bytes per query tile
     constexpr int CPR = ROWB / 16;
     constexpr int NI = TB / 1024 / kFW;
     constexpr int RPI = 64 * kFW / CPR;
     constexpr int NQS = kFKT / 16;      // 16-query subtiles per tile
-    static_assert(NI == 1 || RPI % 16 == 0, "one swizzled offset per lane");
     // Two ring stages ([Q, dO] each) in separate arrays, the tile loop
     // unrolled by two: each tile names its stage statically, so the compiler
     // knows its LDS reads cannot touch the stage the next tile's DMA writes
@@ -613,8 +638,9 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_kv_wide_kernel(WideParams<
     const int drow = (wave * 64 + lane) / CPR;
     const int pch = (wave * 64 + lane) % CPR;
     const int64_t qrs = p.qs[2] * 2, ors = p.dos[2] * 2;
-    const int qoff = wide_src_off<PART>(drow, pch ^ qswz(drow), qrs, p.dr);
-    const int ooff = wide_src_off<PART>(drow, pch ^ oswz(drow), ors, p.dr);
+    int qoff[NI], ooff[NI];
+    wide_dma_offsets<PART, NI, RPI>(qoff, drow, pch, qrs, p.dr, qswz);
+    wide_dma_offsets<PART, NI, RPI>(ooff, drow, pch, ors, p.dr, oswz);
     auto tile_of = [&](int it, int& hq, int& q0) {
         const int gg = it / nq;
         q0 = (qt_begin + it - gg * nq) * kFKT;
@@ -632,21 +658,26 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_kv_wide_kernel(WideParams<
             const int skip = i * RPI;
             tile_dma16(__builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(qp + (q0 + skip) * qrs), 0,
                                                          max((nrows - skip) * static_cast<int>(qrs), 0), 0x00020000),
-                       qoff, lq + (i * kFW + wave) * 1024);
+                       qoff[i], lq + (i * kFW + wave) * 1024);
             tile_dma16(__builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(op + (q0 + skip) * ors), 0,
                                                          max((nrows - skip) * static_cast<int>(ors), 0), 0x00020000),
-                       ooff, lq + TB + (i * kFW + wave) * 1024);
+                       ooff[i], lq + TB + (i * kFW + wave) * 1024);
         }
     };
-    // threads 0..63 load the tile's row sums (staged as 1/R), 64..127 its
-    // delta (staged as -delta); the raw value is stored an iteration later
+    // threads 0..kFKT-1 load the tile's row sums (staged as 1/R), the next
+    // kFKT its delta (staged as -delta); the raw value is stored an iteration
+    // later
     auto row_value = [&](int it) {
         int hq, q0;
         tile_of(it, hq, q0);
         const int64_t idx = (static_cast<int64_t>(b) * p.Hq + hq) * T_ + min(q0 + (tid & (kFKT - 1)), T_ - 1);
-        // waves 0 and 1 (wave-uniform: the base pointer stays scalar)
-        if (wave == 0) return p.rs[idx];
-        if (wave == 1) return p.delta[idx];
+        if constexpr (kFKT == 64) {
+            // waves 0 and 1 (wave-uniform: the base pointer stays scalar)
+            if (wave == 0) return p.rs[idx];
+            if (wave == 1) return p.delta[idx];
+        } else {
+            if (wave == 0) return lane < kFKT ? p.rs[idx] : p.delta[idx];
+        }
         return 0.f;
     };
     auto store_rv = [&](int st, float raw) {
@@ -770,60 +801,64 @@ __global__ __launch_bounds__(64 * kFW) void flash_bwd_kv_wide_kernel(WideParams<
 // d stride 1, and a tile's rows within 32-bit byte offsets of its first row.
 bool wide_strides_ok(const int64_t* s) {
     return s[3] == 1 && s[0] % 8 == 0 && s[1] % 8 == 0 && s[2] % 8 == 0 && s[2] >= 0 &&
-           s[2] * 2 * kFKT < (int64_t(1) << 31);
+           s[2] * 2 * kWideMaxKT < (int64_t(1) << 31);
 }
 
 int check_wide(int B, int Hq, int Hkv, int T, int D, int window_size, int dtype) {
     if (dtype != SA_BF16 && dtype != SA_F16) return SA_ERR_BAD_DTYPE;
     if (B < 0 || Hq <= 0 || Hkv <= 0 || T < 0 || Hq % Hkv != 0 || window_size < 0) return SA_ERR_BAD_SHAPE;
-    if (D <= 128 || D > 256 || D % 8 != 0) return SA_ERR_UNSUPPORTED;
+    if (D <= 128 || D > 512 || D % 8 != 0) return SA_ERR_UNSUPPORTED;
     return 0;
 }
 
-template <typename T>
+template <typename T, int D>
 int launch_fwd_wide(const WideParams<T>& prm, int exact, hipStream_t st) {
+    constexpr int kFW = WideCfg<D>::NW, kFRows = WideCfg<D>::ROWS;
     const int64_t nblk = static_cast<int64_t>((prm.T + kFRows - 1) / kFRows) * prm.B * prm.Hq;
     if (nblk * 64 * kFW >= (int64_t(1) << 32)) return SA_ERR_BAD_SHAPE;
     const dim3 grid(static_cast<unsigned>(nblk));
     if (exact) {
-        flash_fwd_wide_kernel<T, 256, true, false><<<grid, 64 * kFW, 0, st>>>(prm);
+        flash_fwd_wide_kernel<T, D, true, false><<<grid, 64 * kFW, 0, st>>>(prm);
         return status_from_launch();
     }
     // folded weights for bf16 P only (fp16 P would overflow sooner by 1/scale^2)
     if constexpr (std::is_same_v<T, bf16>) {
         if (prm.scale >= 0x1p-20f && prm.scale <= 0x1p20f) {
-            flash_fwd_wide_kernel<T, 256, false, true><<<grid, 64 * kFW, 0, st>>>(prm);
+            flash_fwd_wide_kernel<T, D, false, true><<<grid, 64 * kFW, 0, st>>>(prm);
             return status_from_launch();
         }
     }
-    flash_fwd_wide_kernel<T, 256, false, false><<<grid, 64 * kFW, 0, st>>>(prm);
+    flash_fwd_wide_kernel<T, D, false, false><<<grid, 64 * kFW, 0, st>>>(prm);
     return status_from_launch();
 }
 
-template <typename T, bool PART>
+template <typename T, int D, bool PART>
 int launch_bwd_wide_part(const WideParams<T>& prm, int exact, hipStream_t st) {
+    constexpr int kFW = WideCfg<D>::NW, kFRows = WideCfg<D>::ROWS;
     const int64_t nq = static_cast<int64_t>((prm.T + kFRows - 1) / kFRows) * prm.B * prm.Hq;
     if (nq * 64 * kFW >= (int64_t(1) << 32)) return SA_ERR_BAD_SHAPE;  // dQ blocks of kFW waves
     const int64_t nk = nq / prm.G;
     const dim3 gq(static_cast<unsigned>(nq)), gk(static_cast<unsigned>(nk));
     if (exact) {
-        flash_bwd_dq_wide_kernel<T, 256, true, PART><<<gq, 64 * kFW, 0, st>>>(prm);
-        flash_bwd_kv_wide_kernel<T, 256, true, false, PART><<<gk, 64 * kFW, 0, st>>>(prm);
-        flash_bwd_kv_wide_kernel<T, 256, true, true, PART><<<gk, 64 * kFW, 0, st>>>(prm);
+        flash_bwd_dq_wide_kernel<T, D, true, PART><<<gq, 64 * kFW, 0, st>>>(prm);
+        flash_bwd_kv_wide_kernel<T, D, true, false, PART><<<gk, 64 * kFW, 0, st>>>(prm);
+        flash_bwd_kv_wide_kernel<T, D, true, true, PART><<<gk, 64 * kFW, 0, st>>>(prm);
     } else {
-        flash_bwd_dq_wide_kernel<T, 256, false, PART><<<gq, 64 * kFW, 0, st>>>(prm);
-        flash_bwd_kv_wide_kernel<T, 256, false, false, PART><<<gk, 64 * kFW, 0, st>>>(prm);
-        flash_bwd_kv_wide_kernel<T, 256, false, true, PART><<<gk, 64 * kFW, 0, st>>>(prm);
+        flash_bwd_dq_wide_kernel<T, D, false, PART><<<gq, 64 * kFW, 0, st>>>(prm);
+        flash_bwd_kv_wide_kernel<T, D, false, false, PART><<<gk, 64 * kFW, 0, st>>>(prm);
+        flash_bwd_kv_wide_kernel<T, D, false, true, PART><<<gk, 64 * kFW, 0, st>>>(prm);
     }
     return status_from_launch();
 }
 
-// The masked kernels (PART) only for head dims below 256: the masks cost the
-// dK kernel registers (spills in its tile loop).
+// The masked kernels (PART) only for head dims below the kernel's: the
+// masks cost the dK kernel registers (spills in its tile loop at D = 256).
 template <typename T>
 int launch_bwd_wide(const WideParams<T>& prm, int exact, hipStream_t st) {
-    if (prm.dr == 256) return launch_bwd_wide_part<T, false>(prm, exact, st);
-    return launch_bwd_wide_part<T, true>(prm, exact, st);
+    if (prm.dr == 256) return launch_bwd_wide_part<T, 256, false>(prm, exact, st);
+    if (prm.dr < 256) return launch_bwd_wide_part<T, 256, true>(prm, exact, st);
+    if (prm.dr == 512) return launch_bwd_wide_part<T, 512, false>(prm, exact, st);
+    return launch_bwd_wide_part<T, 512, true>(prm, exact, st);
 }
 
 template <typename T>
@@ -850,7 +885,8 @@ int run_fwd_wide(const void* q, const void* k, const void* v, void* o, float* ro
     prm.window = window_size;
     prm.dr = D;
     prm.scale = scale;
-    return launch_fwd_wide<T>(prm, exact_math, st);
+    if (D <= 256) return launch_fwd_wide<T, 256>(prm, exact_math, st);
+    return launch_fwd_wide<T, 512>(prm, exact_math, st);
 }
 
 template <typename T>

@@ -559,15 +559,16 @@ def _flash_operand(t):
 
 
 # Head dims the fused-attention kernels are built for, per input dtype.
-_FLASH_KERNEL_DIMS = {dt: (32, 64, 128, 256) for dt in (torch.bfloat16, torch.float16, torch.float32)}
+_FLASH_KERNEL_DIMS = {torch.bfloat16: (32, 64, 128, 256, 512), torch.float16: (32, 64, 128, 256, 512),
+                      torch.float32: (32, 64, 128, 256)}
 
 
 def _kernel_head_dim(D, dtype=None):
     """The head dim the kernels are called with for a head dim D.  bf16 /
-    fp16: D rounded up to a multiple of 8, fp32 to a multiple of 4 (the
-    kernels built for 32, 64, 128 and 256 take any such D up to their size,
-    reading only its columns); fp8: the next of the head dims its kernels
-    are built for.  Where it
+    fp16: D rounded up to a multiple of 8 (kernels built for 32, 64, 128,
+    256 and 512), fp32 to a multiple of 4 (kernels built for 32, 64, 128
+    and 256); those kernels take any such D up to their size, reading only
+    its columns; fp8: the next of the head dims its kernels are built for.  Where it
     differs from D, inputs are zero-padded and outputs sliced: zero columns
     add nothing to q.k, and the padded columns of O, dQ, dK, dV are dropped.
     The reference computes at next_pow2(D) (kernels.py:1918) without masking
@@ -732,18 +733,20 @@ def _sp2norm_rope_flash_fwd(q, k, v, cos, sin, scale, n_kv_groups=1, window_size
     """(o, row_sums) of the RoPE forward; ``o`` may be a caller view (e.g. of a
     [B, T, Hq, D] buffer) with 16-byte aligned rows.  16-bit head dims 32,
     64 and 128 rotate Q in registers inside the fused kernel (K once into a
-    workspace); fp32, and other head dims that are multiples of 16 up to
-    256, rotate Q and K by sa_rope_rotate and run the plain fused forward
-    (whose kernels take those head dims unpadded, reading only their
-    columns)."""
+    workspace); fp32, and other head dims that are multiples of 16 (up to
+    512 for 16-bit inputs, 256 for fp32), rotate Q and K by sa_rope_rotate
+    and run the plain fused forward (whose kernels take those head dims
+    unpadded, reading only their columns)."""
     _check_same_device("q", q, k=k, v=v, cos=cos, sin=sin, o=o)
     B, H_q, T, D = q.shape
     H_kv = k.shape[1]
     if q.dtype not in (torch.bfloat16, torch.float16, torch.float32) or k.dtype != q.dtype or v.dtype != q.dtype:
         raise ValueError(f"RoPE attention expects bf16, fp16 or fp32 q/k/v of one dtype, got "
                          f"{q.dtype}/{k.dtype}/{v.dtype}")
-    if D % 16 or not 16 <= D <= 256:  # rotate-half pairs 8-element chunks d, d + D/2
-        raise ValueError(f"RoPE attention supports head dims that are multiples of 16 in 16..256, got {D}")
+    d_max = 256 if q.dtype == torch.float32 else 512
+    if D % 16 or not 16 <= D <= d_max:  # rotate-half pairs 8-element chunks d, d + D/2
+        raise ValueError(f"RoPE attention supports head dims that are multiples of 16 in 16..{d_max} for "
+                         f"{q.dtype}, got {D}")
     cos, sin = _rope_tables(cos, sin, T, D)
     if D not in _FLASH_HEAD_DIMS or q.dtype == torch.float32:
         o_full, row_sums = _sp2norm_flash_fwd(_rope_rotate(q, cos, sin), _rope_rotate(k, cos, sin), v, scale,
@@ -881,8 +884,8 @@ def _sp2norm_fp8_flash_fwd(q_fp8, k_fp8, v_fp8, q_scale, k_scale, v_scale, attn_
         raise ValueError("q and k must be float8_e4m3fn")
     if v_fp8.dtype not in (torch.float8_e4m3fn, torch.bfloat16):
         raise ValueError("v must be float8_e4m3fn or bfloat16")
-    if D < 1 or D > 256:
-        raise ValueError(f"fused attention supports head dims 1..256, got {D}")
+    if D < 1 or D > 512:
+        raise ValueError(f"fused attention supports head dims 1..512, got {D}")
     if D > 128:
         return _fp8_wide_fwd(q_fp8, k_fp8, v_fp8, q_scale, k_scale, v_scale, attn_scale, n_kv_groups, window_size)
     Dk = _kernel_head_dim(D)
@@ -912,9 +915,9 @@ def _sp2norm_fp8_flash_fwd(q_fp8, k_fp8, v_fp8, q_scale, k_scale, v_scale, attn_
 
 
 def _fp8_wide_fwd(q8, k8, v8, q_scale, k_scale, v_scale, attn_scale, n_kv_groups, window_size):
-    """fp8 attention at head dims 129..256: the e4m3fn codes are widened to
+    """fp8 attention at head dims 129..512: the e4m3fn codes are widened to
     bf16 (exact: every e4m3fn value is a bf16 value), the bf16 head-dim-256
-    kernels run with the dequantisation folded into the score scale
+    and -512 kernels run with the dequantisation folded into the score scale
     (q_s * k_s * attn_scale), and fp8 V is widened as v_s * V rounded to
     bf16, so the output is rounded once, at the kernel's store (the
     reference applies v_s to each fp32 P V product, kernels.py:2579;

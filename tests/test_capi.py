@@ -246,7 +246,7 @@ def test_rope_rotate_argument_errors():
 
 
 def test_flash_16bit_head_dims():
-    # bf16 / fp16: any multiple of 8 in 8..256 (kernels for 32, 64, 128, 256
+    # bf16 / fp16: any multiple of 8 in 8..512 (kernels for 32, 64, 128, 256, 512
     # read only the first D columns); the fp8 and fused-RoPE kernels take 32,
     # 64, 128 only.  Every check runs before any launch (B = 0 launches nothing).
     lib = _lib.load()
@@ -256,10 +256,10 @@ def test_flash_16bit_head_dims():
                                           None)
     bwd = lambda D, B=0: lib.sa_flash_bwd(d, d, d, d, d, d, d, d, d, d, B, 2, 2, 64, D, s, s, s, s, s, s, s, s, 0.1,
                                           0, 0, _lib.SA_F16, None)
-    for D in (0, 4, 12, 132, 250, 264, 512):
+    for D in (0, 4, 12, 132, 250, 516, 520, 1024):
         assert fwd(D) == -6, D
         assert bwd(D) == -6, D
-    for D in (8, 24, 40, 96, 128, 136, 200, 248, 256):
+    for D in (8, 24, 40, 96, 128, 136, 200, 248, 256, 264, 400, 504, 512):
         assert fwd(D) == 0, D
         assert bwd(D) == 0, D
     fp8 = lambda D: lib.sa_flash_fp8_fwd(d, d, d, d, None, d, d, d, 0, 2, 2, 64, D, s, s, s, s, 0.1, 0,

@@ -1,7 +1,8 @@
 """Randomised parity sweep of the fused attention (forward and backward)
 against the float64 oracle, over combinations the fixed cases do not
 enumerate: dtype (bf16, fp16, fp32), head dims 8..256 (run on the next
-kernel up with the columns past D masked, and the D = 256 kernels), GQA
+kernel up with the columns past D masked, and the D = 256 kernels), 16-bit
+head dims 264..512 (the D = 512 kernels), GQA
 group sizes, windows, query counts around the 32/64/128/256-row tile edges,
 and scales (GPU).
 
@@ -33,9 +34,9 @@ def _rel(got, ref, floor):
     return float((got - ref).abs().max() / max(float(ref.abs().max()), floor))
 
 
-def _case(rng, seed):
-    dt = rng.choice([torch.bfloat16, torch.float16, torch.float32])
-    D = rng.choice([8, 24, 32, 40, 64, 96, 128, 136, 200, 256])
+def _case(rng, seed, wide=False):
+    dt = rng.choice([torch.bfloat16, torch.float16] if wide else [torch.bfloat16, torch.float16, torch.float32])
+    D = rng.choice([264, 328, 400, 448, 512] if wide else [8, 24, 32, 40, 64, 96, 128, 136, 200, 256])
     hkv = rng.choice([1, 2, 3])
     G = rng.choice([1, 2, 4])
     T = rng.choice([1, 2, 31, 33, 63, 65, 127, 129, 255, 257, 300])
@@ -50,11 +51,11 @@ def _case(rng, seed):
     return dt, G, W, sc, q, k, v, do
 
 
-@pytest.mark.parametrize("sweep_seed", [11, 12])
-def test_random_attention_cases(sweep_seed):
+@pytest.mark.parametrize("sweep_seed,n,wide", [(11, 40, False), (12, 40, False), (13, 16, True)])
+def test_random_attention_cases(sweep_seed, n, wide):
     rng = random.Random(sweep_seed)
-    for i in range(40):
-        dt, G, W, sc, q, k, v, do = _case(rng, 1000 * sweep_seed + i)
+    for i in range(n):
+        dt, G, W, sc, q, k, v, do = _case(rng, 1000 * sweep_seed + i, wide)
         B, hq, T, D = q.shape
         hkv = k.shape[1]
         what = f"case {i}: {dt} B={B} hq={hq} hkv={hkv} T={T} D={D} window={W} scale={sc:.3g}"

@@ -1,7 +1,7 @@
 """Head dims below the 16-bit fused-attention kernels' built sizes (GPU).
 
-bf16 / fp16 head dims that are multiples of 8 in 8..256 run on the kernels
-built for 32, 64, 128 and 256, which read only the first D columns of every
+bf16 / fp16 head dims that are multiples of 8 in 8..512 run on the kernels
+built for 32, 64, 128, 256 and 512, which read only the first D columns of every
 row and store only those (the reference computes at D_HEAD = next_pow2(D)
 and masks no column, kernels.py:1918 and :1572-1581, so for other head dims
 its loads run past each row).  Here every input is a
@@ -115,7 +115,19 @@ def test_head_dims_above_128(D, dtype):
     run_case(D, dtype, T=150, seed=D)
 
 
-@pytest.mark.parametrize("D", [40, 96, 200])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D", [264, 400, 504, 512])
+def test_head_dims_above_256(D, dtype):
+    # the head-dim-512 kernels (4-wave blocks of 64 rows, 32-row tiles)
+    run_case(D, dtype, T=150, seed=D)
+
+
+def test_head_dim_512_several_blocks():
+    # more query / key blocks than one (64 rows each), heaviest first
+    run_case(512, torch.bfloat16, T=333, seed=5)
+
+
+@pytest.mark.parametrize("D", [40, 96, 200, 320, 512])
 def test_head_dims_window_and_exact(D):
     run_case(D, torch.bfloat16, T=300, window=70, seed=D + 1)
     run_case(D, torch.bfloat16, T=130, exact=True, extra=8, seed=D + 2)
@@ -132,6 +144,10 @@ def test_built_head_dims_in_wider_rows(D):
     # D equal to a built size, rows of a wider tensor: nothing read or written past D
     run_case(D, torch.bfloat16, T=200, extra=8, seed=D + 3)
     run_case(D, torch.float32, T=100, extra=4, seed=D + 4)
+
+
+def test_built_head_dim_512_in_wider_rows():
+    run_case(512, torch.float16, T=200, extra=8, seed=515)
 
 
 def test_public_api_takes_multiples_of_8_without_copies():

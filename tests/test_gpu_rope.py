@@ -132,7 +132,7 @@ def test_transpose16_bit_exact(rows, cols, dtype):
     assert torch.equal(ys.cpu(), wide[:, 8:8 + cols].cpu().t())
 
 
-@pytest.mark.parametrize("D", [16, 48, 80, 96, 160, 256])
+@pytest.mark.parametrize("D", [16, 48, 80, 96, 160, 256, 384, 512])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_rope_other_head_dims(D, dtype):
     # head dims other than 32 / 64 / 128: Q and K rotated by sa_rope_rotate,

@@ -271,24 +271,27 @@ def test_fused_entry_points_refuse_meta_tensors(case, no_library):
 
 
 def test_head_dims_and_page_sizes_checked_before_launch(no_library):
-    # fused attention, fp8 included: any head dim up to 256 (16-bit: rounded
-    # up to a multiple of 8, fp32 of 4; fp8: zero-padded to a built size); larger head dims, fp64 and
-    # mixed dtypes are refused with a clear error; paged decode: power-of-two
-    # page sizes only
+    # fused attention, fp8 included: 16-bit and fp8 head dims up to 512,
+    # fp32 up to 256 (16-bit: rounded up to a multiple of 8, fp32 of 4; fp8:
+    # zero-padded to a built size, or widened to bf16 above 128); larger head
+    # dims, fp64 and mixed dtypes are refused with a clear error; paged
+    # decode: power-of-two page sizes only
     mk = lambda shape, dtype: _OnDevice.make(torch.zeros(shape, dtype=dtype), 0)
-    for D in (257, 512):
-        for dt in (torch.bfloat16, torch.float16, torch.float32):
+    for D, dts, lim in ((257, (torch.float32,), 256), (512, (torch.float32,), 256),
+                        (513, (torch.bfloat16, torch.float16), 512), (1024, (torch.bfloat16, torch.float16), 512)):
+        for dt in dts:
             q = mk((1, 2, 8, D), dt)
-            with pytest.raises(ValueError, match="head dims 1..256"):
+            with pytest.raises(ValueError, match=f"head dims 1..{lim}"):
                 kernels._sp2norm_flash_fwd(q, q, q, 0.1)
-            with pytest.raises(ValueError, match="head dims 1..256"):
+            with pytest.raises(ValueError, match=f"head dims 1..{lim}"):
                 kernels._sp2norm_flash_bwd(q, q, q, q, q, mk((1, 2, 8), torch.float32), 0.1)
-    q8 = mk((1, 2, 8, 264), torch.float8_e4m3fn)
-    with pytest.raises(ValueError, match="head dims 1..256"):
+    q8 = mk((1, 2, 8, 520), torch.float8_e4m3fn)
+    with pytest.raises(ValueError, match="head dims 1..512"):
         kernels._sp2norm_fp8_flash_fwd(q8, q8, q8, 1.0, 1.0, 1.0, 0.1)
     dims = (1, 16, 32, 33, 64, 96, 128, 129, 200, 256)
     # 16-bit: multiples of 8 run as they are (columns past D masked in the kernels)
     assert [kernels._kernel_head_dim(d, torch.bfloat16) for d in dims] == [8, 16, 32, 40, 64, 96, 128, 136, 200, 256]
+    assert [kernels._kernel_head_dim(d, torch.bfloat16) for d in (257, 300, 511, 512)] == [264, 304, 512, 512]
     assert [kernels._kernel_head_dim(d, torch.float32) for d in dims] == [4, 16, 32, 36, 64, 96, 128, 132, 200, 256]
     assert [kernels._kernel_head_dim(d) for d in dims[:7]] == [32, 32, 32, 64, 64, 128, 128]
     q = mk((1, 2, 8, 64), torch.float64)
