@@ -204,8 +204,8 @@ int sa_flash_bwd(const void* q, const void* k, const void* v, const void* o,
  * dK / dV of the key blocks split over their query tiles, which the library
  * does for causal rows long against the grid (few batch x KV heads), where
  * the first key blocks, which see every query, would otherwise run alone at
- * the end.  0 when it does not split (fp32, head dims above 128, grids that
- * fill the GPU); -1 for invalid sizes.
+ * the end; at most 512 MiB.  0 when it does not split (fp32, head dims
+ * above 128, grids that fill the GPU); -1 for invalid sizes.
  */
 int64_t sa_flash_bwd_workspace_size(int B, int Hq, int Hkv, int T, int D,
                                     int window_size, int dtype);

@@ -781,8 +781,9 @@ int dkdv_iterations(int kb, int T, int G, int W) {
 // costing its iterations plus two for its set-up and stores, plus a fifth of
 // the longest block for the ragged end, an iteration at 5 us (a 64-query
 // tile of 128 keys with two blocks per CU), and the partials' writes and
-// reads at 5 TB/s.  (Fitted to measured times of shapes from 1 x 2 KV heads
-// x 4096 keys to 2 x 8 x 16384, where it picks the fastest count of each.)
+// reads at 5 TB/s; at most 512 MiB of partials.  (Fitted to measured times
+// of shapes from 1 x 2 KV heads x 4096 keys to 2 x 8 x 16384, where it picks
+// the fastest count of each.)
 int dkdv_split_count_uncached(int B, int Hkv, int T, int G, int W, int dr) {
     const int nkb = (T + kBwdBK - 1) / kBwdBK;
     const int64_t blocks = static_cast<int64_t>(nkb) * B * Hkv;
@@ -791,7 +792,8 @@ int dkdv_split_count_uncached(int B, int Hkv, int T, int G, int W, int dr) {
     double best_t = 0.0;
     std::vector<double> slots;
     for (int S = 1; S <= 16; S *= 2) {
-        if (blocks * S > 16384) break;
+        // at most 16384 blocks and 512 MiB of partials
+        if (blocks * S > 16384 || bwd_part_bytes(S, B, Hkv, T, dr) > (int64_t(512) << 20)) break;
         // XCD 0's share: every 8th block of the dispatch order (kb, unit, split)
         slots.assign(kBwdXcdSlots, 0.0);
         double longest = 0.0;
