@@ -378,7 +378,7 @@ def bench_next_rows(torch):
     - bf16 attention forward and backward at head dim 256, [4,16,4096,256],
       and at head dim 512, [4,8,4096,512] (both config 3's FLOPs), and paged decode at head dim 256 on config 5's
       layout with Hq 16 / Hkv 4 (config 5's bytes), at head dim 512 with
-      Hq 8 / Hkv 2 (the same bytes), and paged decode over
+      Hq 8 / Hkv 2 and at 1024 with Hq 8 / Hkv 1 (the same bytes), and paged decode over
       fp32 caches (and fp32 q over bf16 and e4m3fn caches) on config 5's layout;
     - the bf16 attention backward over long rows and few KV heads
       ([1, 32, 8192, 128] with 8 KV heads), with its dK/dV key blocks split
@@ -510,6 +510,18 @@ def bench_next_rows(torch):
     nb = paged_bytes(lens, Hq=8, D=512)
     out["paged_decode_d512"] = {"us": round(us, 1), "GBs": round(nb / us / 1e3, 1),
                                 "frac_hbm_peak": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)}
+    del kc, vc, qd
+    torch.cuda.empty_cache()
+
+    # paged decode at head dim 1024 on config 5's layout with Hq 8 / Hkv 1
+    # (the same 4 KB of K and V per token; four waves per block split the columns)
+    kc = torch.randn(n_pages, 1, 16, 1024, generator=gen, device=dev).to(torch.bfloat16)
+    vc = torch.randn(n_pages, 1, 16, 1024, generator=gen, device=dev).to(torch.bfloat16)
+    qd = torch.randn(64, 8, 1, 1024, generator=gen, device=dev).to(torch.bfloat16)
+    us = med(lambda: sa.sp2norm_paged_attention(qd, kc, vc, table_d, lens_d))
+    nb = paged_bytes(lens, Hq=8, D=1024)
+    out["paged_decode_d1024"] = {"us": round(us, 1), "GBs": round(nb / us / 1e3, 1),
+                                 "frac_hbm_peak": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)}
     del kc, vc, qd
     torch.cuda.empty_cache()
 

@@ -343,10 +343,11 @@ int64_t sa_paged_decode_workspace_size(int B, int Hq, int D, int max_pages,
  * kernels.py:2716-2717, :2746, :2765; mixed pairs and fp32 run their
  * products as bf16 hi + lo splits, about 16 significant bits; e4m3fn values
  * widen to bf16 exactly, unscaled, and need D a multiple of 16).  Row strides (element units)
- * must be 16-byte multiples.  D a multiple of 8 in 8..512 (kernels for 32,
- * 64, 128, 256 and 512, the last with two waves per block splitting the
- * columns; smaller D read only their own columns); page_size a power of
- * two (at most 2^20).
+ * must be 16-byte multiples.  D a multiple of 8 in 8..1024 (kernels for 32,
+ * 64, 128, 256, 512 and 1024, the last two with two and four waves per
+ * block splitting the columns; smaller D read only their own columns), at
+ * most 512 over fp32 caches and over fp16 caches with an fp32 q; page_size
+ * a power of two (at most 2^20).
  * workspace: at least sa_paged_decode_workspace_size() bytes, 16-byte
  * aligned, no initialisation needed (a plan kernel writes it).
  * Replaces sp2norm_paged_attention (kernels.py:2776-2829) and its kernel

@@ -163,7 +163,7 @@ __device__ __forceinline__ void to_mt8(const u32x4* w, u32x4& h, u32x4& l) {
     }
 }
 
-// The kernels run a padded head dim D (32, 64, 128, 256 or 512); head dims
+// The kernels run a padded head dim D (32, 64, 128, 256, 512 or 1024); head dims
 // p.D < D (multiples of 8) load only their first p.D columns per row and
 // leave zeros in the rest of the LDS rows and Q registers, which add nothing
 // to the scores, and write only p.D output columns.
@@ -171,7 +171,8 @@ __device__ __forceinline__ void to_mt8(const u32x4* w, u32x4& h, u32x4& l) {
 // instruction divide the page size), so the page base is wave-uniform and
 // comes from v_readlane of the window's page-id register.
 // WPB > 1 (cache rows above 512 bytes: 16-bit D = 512 and fp32 D = 256 in
-// two parts, fp32 D = 512 in four): a block of WPB waves shares each piece;
+// two parts, fp32 D = 512 in four; head dims above 256 in parts of 256
+// columns): a block of WPB waves shares each piece;
 // wave v owns columns [v DF / WPB, (v + 1) DF / WPB) of K, V, Q and O, the
 // partial S^T tiles meet in LDS (two barriers per tile), and every wave forms
 // the same weights.
@@ -521,9 +522,10 @@ template <typename QE, typename CE, int D>
 int launch_paged(PagedParams prm, hipStream_t st) {
     // waves per block, each owning D / WPB columns: rows above 512 bytes are
     // split into 512-byte parts (their tile registers would not fit one wave)
-    // (and any head dim above 256, whose Q and O registers alone fill a wave)
+    // and no wave owns more than 256 columns (Q and O registers)
     constexpr int RB = D * static_cast<int>(sizeof(CE));
-    constexpr int WPB = RB > 1024 ? 4 : (RB > 512 || D > 256) ? 2 : 1;
+    constexpr int WPB_B = RB > 1024 ? 4 : (RB > 512 || D > 256) ? 2 : 1;
+    constexpr int WPB = D / WPB_B > 256 ? D / 256 : WPB_B;
     const bool uniform = prm.P * (D / WPB * static_cast<int>(sizeof(CE)) / 16) >= 64;
     const int resident =
         uniform ? resident_waves<QE, CE, D, true, WPB>() : resident_waves<QE, CE, D, false, WPB>();
@@ -548,7 +550,12 @@ int launch_paged_d(int dp, const PagedParams& prm, hipStream_t st) {
         case 64: return launch_paged<QE, CE, 64>(prm, st);
         case 128: return launch_paged<QE, CE, 128>(prm, st);
         case 256: return launch_paged<QE, CE, 256>(prm, st);
-        default: return launch_paged<QE, CE, 512>(prm, st);
+        case 512: return launch_paged<QE, CE, 512>(prm, st);
+        default:
+            // 1024: four waves of 256 columns; caches split into hi and lo
+            // tiles would need twice the LDS (refused by validate_paged)
+            if constexpr (!PagedTypes<QE, CE>::SPLIT_C) return launch_paged<QE, CE, 1024>(prm, st);
+            else return SA_ERR_UNSUPPORTED;
     }
 }
 
@@ -615,7 +622,7 @@ int validate_paged(const void* q, const void* k_cache, const void* v_cache, cons
     // any power of two: a tile of 32 tokens spans 32 / P pages (P < 32) or
     // lies in one page; a window of 64 page ids always covers whole tiles
     if (page_size <= 0 || (page_size & (page_size - 1)) != 0 || page_size > (1 << 20)) return SA_ERR_UNSUPPORTED;
-    if (D < 8 || D > 512 || D % 8 != 0) return SA_ERR_UNSUPPORTED;
+    if (D < 8 || D > 1024 || D % 8 != 0) return SA_ERR_UNSUPPORTED;
     if (B == 0) return 1;
     if (n_pages == 0) max_pages = 0;  // no cache: every context is empty
     // The plan keeps token positions, tile counts and their prefix sums over
@@ -629,6 +636,10 @@ int validate_paged(const void* q, const void* k_cache, const void* v_cache, cons
     int qt, ct;
     if (!paged_types(dtype, qt, ct)) return SA_ERR_BAD_DTYPE;
     if (ct == SA_FP8_E4M3FN && D % 16 != 0) return SA_ERR_UNSUPPORTED;  // 16-byte rows of 1-byte elements
+    // head dims above 512 run on 4 waves of 256 columns; caches read as
+    // bf16 hi + lo tiles (fp32, or fp16 under an fp32 q) would need twice
+    // the LDS of one block
+    if (D > 512 && (ct == SA_F32 || (qt == SA_F32 && ct == SA_F16))) return SA_ERR_UNSUPPORTED;
     // 16-byte rows: element strides that are multiples of 16 / element size
     const auto ok16 = [](const int64_t* s, int n, int t) {
         const int per = t == SA_F32 ? 4 : t == SA_FP8_E4M3FN ? 16 : 8;
@@ -678,7 +689,8 @@ int run_paged(const void* q, const void* k_cache, const void* v_cache, void* out
     prm.max_pages = max_pages;
     prm.n_pages = n_pages;
     prm.scale = scale;
-    const int dp = D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : D <= 256 ? 256 : 512;  // padded head dim of the kernels
+    // padded head dim of the kernels
+    const int dp = D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : D <= 256 ? 256 : D <= 512 ? 512 : 1024;
     int qt, ct;
     paged_types(dtype, qt, ct);
     if (qt == SA_BF16) return launch_paged_d<bf16, bf16>(dp, prm, st);

@@ -1011,9 +1011,13 @@ def sp2norm_paged_attention(q, k_cache, v_cache, block_table, context_lens, *, s
         # the reference rounds BLOCK_SIZE up to a power of two and then
         # addresses the pages wrongly (kernels.py:2815, :2737-2743)
         raise ValueError(f"block_size must be a power of two, got {block_size}")
-    if D % 8 or not 8 <= D <= 512:
+    if D % 8 or not 8 <= D <= 1024:
         # 16-byte cache rows; the reference takes any D through next_pow2 (kernels.py:2814)
-        raise ValueError(f"paged decode supports head dims that are multiples of 8 in 8..512, got {D}")
+        raise ValueError(f"paged decode supports head dims that are multiples of 8 in 8..1024, got {D}")
+    if D > 512 and (k_cache.dtype == torch.float32 or (k_cache.dtype == torch.float16 and q.dtype != torch.float16)):
+        # those caches are read as bf16 hi + lo tiles, twice the LDS of the 16-bit ones
+        raise ValueError(f"paged decode over {k_cache.dtype} caches with a {q.dtype} q supports head dims up to 512, "
+                         f"got {D}")
     max_blocks_per_seq = block_table.shape[1]
     if scale is None:
         scale = 1.0 / math.sqrt(D)

@@ -213,16 +213,19 @@ def test_flash_bwd_workspace_size():
 
 
 def test_paged_decode_head_dims():
-    # D must be a multiple of 8 in 8..512; checked before any HIP call
+    # D must be a multiple of 8 in 8..1024 (8..512 over caches read as bf16
+    # hi + lo tiles: fp32, or fp16 under an fp32 q); checked before any HIP call
     lib = _lib.load()
     dummy = ctypes.c_void_p(16)
-    for D, want in ((4, -6), (12, -6), (516, -6), (520, -6), (1024, -6)):
+    for D, dt, want in ((4, _lib.SA_BF16, -6), (12, _lib.SA_BF16, -6), (516, _lib.SA_BF16, -6),
+                        (1028, _lib.SA_BF16, -6), (1032, _lib.SA_BF16, -6), (2048, _lib.SA_BF16, -6),
+                        (520, _lib.SA_F32, -6), (1024, _lib.paged_dtypes(_lib.SA_F32, _lib.SA_F16), -6)):
         s4 = (ctypes.c_int64 * 4)(8 * D, D, D, 1)
         o = (ctypes.c_int64 * 3)(8 * D, D, 1)
         st = lib.sa_paged_decode(dummy, dummy, dummy, dummy, dummy, dummy, 2, 8, 2, D, 16, 4, 8,
-                                 s4, s4, s4, o, 4, 0.1, _lib.SA_BF16, dummy, 1 << 30, None)
+                                 s4, s4, s4, o, 4, 0.1, dt, dummy, 1 << 30, None)
         assert st == want, D
-    for D in (8, 24, 200, 256, 264, 512):  # accepted: B = 0 returns before any launch
+    for D in (8, 24, 200, 256, 264, 512, 520, 576, 1024):  # accepted: B = 0 returns before any launch
         s4 = (ctypes.c_int64 * 4)(8 * D, D, D, 1)
         o = (ctypes.c_int64 * 3)(8 * D, D, 1)
         assert lib.sa_paged_decode(dummy, dummy, dummy, dummy, dummy, dummy, 0, 8, 2, D, 16, 4, 8,

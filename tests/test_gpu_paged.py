@@ -189,13 +189,13 @@ def test_index_tensors_on_another_device_are_refused():
     assert out.shape == (B, Hq, D) and bool((out == 0).all())  # zero V rows
 
 
-@pytest.mark.parametrize("D", [8, 16, 24, 48, 80, 96, 136, 160, 200, 256, 264, 384, 512])
+@pytest.mark.parametrize("D", [8, 16, 24, 48, 80, 96, 136, 160, 200, 256, 264, 384, 512, 520, 576, 768, 1024])
 @pytest.mark.parametrize("BS", [1, 16, 64])
 def test_paged_head_dims(D, BS):
-    # any head dim that is a multiple of 8 up to 512 (the reference takes any
-    # D through next_pow2, kernels.py:2815): kernels for 32 / 64 / 128 / 256
-    # and 512 (two waves per block, each owning half the columns), smaller
-    # head dims load only their own columns
+    # any head dim that is a multiple of 8 up to 1024 (the reference takes
+    # any D through next_pow2, kernels.py:2815): kernels for 32 / 64 / 128 /
+    # 256, 512 (two waves per block, each owning half the columns) and 1024
+    # (four waves), smaller head dims load only their own columns
     q, k, v = case(3, 8, 2, 333, D, seed=D + BS)
     kc, vc, table, lens = paging.build_paged_cache(k, v, page_size=BS, shuffle=True, generator=_g(D))
     lens = torch.tensor([333, 1, 170], dtype=torch.int32)
@@ -217,6 +217,27 @@ def test_paged_head_dim_256_config5_like():
     out = run(q, kc, vc, table, lens, BS)
     ref = eager.paged_decode_eager(q.double(), kc.double(), vc.double(), table, lens)
     assert rel_err(out, ref) <= 1e-2
+
+
+def test_paged_head_dim_576_serving_layout():
+    # head dim 576 (a latent-attention width) on the head-dim-1024 kernels:
+    # 8 sequences of up to 2000 tokens, 16 query heads on one KV head, page
+    # 64, shuffled table, bf16 caches and fp32 q over e4m3fn caches
+    g = _g(576)
+    B, Hq, Hkv, D, BS = 8, 16, 1, 576, 64
+    lens = torch.randint(1, 2001, (B,), generator=g, dtype=torch.int32)
+    q = torch.randn(B, Hq, 1, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, int(lens.max()), D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, int(lens.max()), D, generator=g).to(torch.bfloat16)
+    kc, vc, table, _ = paging.build_paged_cache(k, v, page_size=BS, shuffle=True, generator=_g(9))
+    out = run(q, kc, vc, table, lens, BS)
+    ref = eager.paged_decode_eager(q.double(), kc.double(), vc.double(), table, lens)
+    assert rel_err(out, ref) <= 1e-2
+    k8, v8 = kc.to(torch.float8_e4m3fn), vc.to(torch.float8_e4m3fn)
+    out8 = smooth_attn.sp2norm_paged_attention(q.float().to(DEV), k8.to(DEV), v8.to(DEV), table.to(DEV),
+                                               lens.to(DEV), block_size=BS)
+    ref8 = eager.paged_decode_eager(q.double(), k8.double(), v8.double(), table, lens)
+    assert rel_err(out8, ref8) <= 1e-2
 
 
 def test_paged_head_dim_512_config5_like():

@@ -77,11 +77,15 @@ def make(B, Hq, Hkv, T, D, P, qdt, cdt, seed):
 
 @pytest.mark.parametrize("qdt", DTYPES)
 @pytest.mark.parametrize("cdt", DTYPES)
-@pytest.mark.parametrize("D", [64, 128, 256, 40, 512])
+@pytest.mark.parametrize("D", [64, 128, 256, 40, 512, 1024])
 def test_paged_dtype_pairs(qdt, cdt, D):
     q, kc, vc, table, lens = make(3, 8, 2, 333, D, 16, qdt, cdt, seed=D + 7)
     if cdt == torch.float8_e4m3fn and D % 16:
         with pytest.raises(ValueError, match="multiple of 16"):  # 16-byte rows of 1-byte elements
+            decode(q, kc, vc, table, lens, 16)
+        return
+    if D > 512 and (cdt == torch.float32 or (cdt == torch.float16 and qdt != torch.float16)):
+        with pytest.raises(ValueError, match="up to 512"):  # caches read as bf16 hi + lo tiles
             decode(q, kc, vc, table, lens, 16)
         return
     out = decode(q, kc, vc, table, lens, 16)

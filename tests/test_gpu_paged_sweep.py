@@ -1,8 +1,9 @@
 """Randomised parity sweep of the paged decode against the float64 oracle
 (GPU): random batch sizes, per-sequence context lengths (zero and page-edge
 lengths included), page sizes (powers of two), head dims (multiples of 8 up
-to 512), GQA groups, cache dtypes (fp32, bf16, fp16) with q of the caches'
-dtype or fp32, and shuffled block tables.
+to 1024; 512 over fp32 caches and under an fp32 q over fp16 caches), GQA
+groups, cache dtypes (fp32, bf16, fp16) with q of the caches' dtype or fp32,
+and shuffled block tables.
 
 Bar as in test_gpu_paged.py: bf16 output within 1e-2 of max|oracle|;
 sequences with an empty context return exact zeros.
@@ -32,10 +33,10 @@ def test_random_paged_cases(sweep_seed):
         B = rng.choice([1, 2, 3, 7])
         hkv = rng.choice([1, 2, 4])
         hq = hkv * rng.choice([1, 2, 4, 8])
-        D = rng.choice([8, 16, 40, 64, 72, 128, 200, 256, 320, 512])
+        D = rng.choice([8, 16, 40, 64, 72, 128, 200, 256, 320, 512, 576, 1024])
         P = rng.choice([1, 4, 8, 16, 32, 64, 128])
-        dt = rng.choice([torch.bfloat16, torch.float16, torch.float32])
-        qdt = rng.choice([dt, torch.float32])
+        dt = rng.choice([torch.bfloat16, torch.float16] if D > 512 else [torch.bfloat16, torch.float16, torch.float32])
+        qdt = rng.choice([dt] if D > 512 and dt == torch.float16 else [dt, torch.float32])
         lens = [rng.choice([0, 1, P - 1 if P > 1 else 1, P, P + 1, 100, 257, 1000, 2048]) for _ in range(B)]
         T = max(max(lens), 1)
         g = torch.Generator().manual_seed(1000 * sweep_seed + i)

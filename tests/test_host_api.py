@@ -307,9 +307,16 @@ def test_head_dims_and_page_sizes_checked_before_launch(no_library):
     with pytest.raises(ValueError, match="power of two"):
         smooth_attn.sp2norm_paged_attention(qd, kc, kc, torch.zeros(2, 2, dtype=torch.int32),
                                             torch.ones(2, dtype=torch.int32), block_size=12)
-    for D in (4, 12, 516, 1024):  # paged decode: multiples of 8 in 8..512
+    for D in (4, 12, 516, 1032, 2048):  # paged decode: multiples of 8 in 8..1024
         qd = torch.zeros(2, 4, 1, D, dtype=torch.bfloat16)
         kc = torch.zeros(4, 2, 16, D, dtype=torch.bfloat16)
-        with pytest.raises(ValueError, match="multiples of 8 in 8..512"):
+        with pytest.raises(ValueError, match="multiples of 8 in 8..1024"):
+            smooth_attn.sp2norm_paged_attention(qd, kc, kc, torch.zeros(2, 2, dtype=torch.int32),
+                                                torch.ones(2, dtype=torch.int32))
+    for qdt, cdt in ((torch.float32, torch.float32), (torch.float32, torch.float16), (torch.bfloat16, torch.float16)):
+        # caches read as bf16 hi + lo tiles stop at 512
+        qd = torch.zeros(2, 4, 1, 520, dtype=qdt)
+        kc = torch.zeros(4, 2, 16, 520, dtype=cdt)
+        with pytest.raises(ValueError, match="up to 512"):
             smooth_attn.sp2norm_paged_attention(qd, kc, kc, torch.zeros(2, 2, dtype=torch.int32),
                                                 torch.ones(2, dtype=torch.int32))
