@@ -365,9 +365,13 @@ __global__ __launch_bounds__(kBwdThreads, 2) void flash_bwd_dq_kernel(BwdParams 
     }
 
     // dS was kept without its per-row factor 2 scale / R_i (applied here).
-    if (qi < T_) {
+    // dQ leaves through LDS as whole rows (nontemporal 16-byte chunks).
+    {
+        constexpr int RB = D * 2 + 16, CPR = D * 2 / 16, RPI = 64 / CPR;
+        static_assert(2 * 32 * RB <= 2 * Tl::BYTES, "two waves' rows per stage array");
+        // both stages are free after the loop's last barrier
+        unsigned char* st = (wave < 2 ? lds0 : lds1) + (wave & 1) * 32 * RB;
         const float f = 2.f * sc * inv_r;
-        T* row = dqp + qi * p.dqs[2];
 #pragma unroll
         for (int dt = 0; dt < D / 32; ++dt) {
 #pragma unroll
@@ -376,8 +380,15 @@ __global__ __launch_bounds__(kBwdThreads, 2) void flash_bwd_dq_kernel(BwdParams 
                 uint2 w;
                 w.x = pack2<T>(acc[dt][vg * 4 + 0] * f, acc[dt][vg * 4 + 1] * f);
                 w.y = pack2<T>(acc[dt][vg * 4 + 2] * f, acc[dt][vg * 4 + 3] * f);
-                if (!PART || d0 < p.dr) *reinterpret_cast<uint2*>(row + d0) = w;
+                *reinterpret_cast<uint2*>(st + l32 * RB + d0 * 2) = w;
             }
+        }
+#pragma unroll
+        for (int r0 = 0; r0 < 32; r0 += RPI) {
+            const int r = r0 + lane / CPR, c = lane % CPR;
+            const int qr = wq0 + r;
+            const u32x4 v = *reinterpret_cast<const u32x4*>(st + r * RB + c * 16);
+            if (qr < T_ && (!PART || c * 8 < p.dr)) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(dqp + qr * p.dqs[2] + c * 8));
         }
     }
 }
@@ -661,25 +672,40 @@ __global__ __launch_bounds__(kBwdThreads, kBwdDkdvMinBlocks) void flash_bwd_dkdv
         return;
     }
 
-    // dS was kept without its factor 2 scale (1/R_i is already in).
-    if (kj < T_) {
+    // dS was kept without its factor 2 scale (1/R_i is already in).  dK and
+    // dV leave through LDS as whole rows (nontemporal 16-byte chunks).
+    {
+        constexpr int RB = D * 2 + 16, CPR = D * 2 / 16, RPI = 64 / CPR;
+        static_assert(2 * 32 * RB <= 2 * Tl::BYTES, "two waves' rows per stage array");
+        unsigned char* st = (wave < 2 ? lds0 : lds1) + (wave & 1) * 32 * RB;
         const float f = 2.f * sc;
-        T* krw = dkp + kj * p.dks[2];
-        T* vrw = dvp + kj * p.dvs[2];
 #pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt) {
+        for (int which = 0; which < 2; ++which) {
 #pragma unroll
-            for (int vg = 0; vg < 4; ++vg) {
-                const int d0 = dt * 32 + vg * 8 + hi * 4;
-                uint2 wk, wv;
-                wk.x = pack2<T>(dkacc[dt][vg * 4 + 0] * f, dkacc[dt][vg * 4 + 1] * f);
-                wk.y = pack2<T>(dkacc[dt][vg * 4 + 2] * f, dkacc[dt][vg * 4 + 3] * f);
-                wv.x = pack2<T>(dvacc[dt][vg * 4 + 0], dvacc[dt][vg * 4 + 1]);
-                wv.y = pack2<T>(dvacc[dt][vg * 4 + 2], dvacc[dt][vg * 4 + 3]);
-                if (!PART || d0 < p.dr) {
-                    *reinterpret_cast<uint2*>(krw + d0) = wk;
-                    *reinterpret_cast<uint2*>(vrw + d0) = wv;
+            for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+                for (int vg = 0; vg < 4; ++vg) {
+                    const int d0 = dt * 32 + vg * 8 + hi * 4;
+                    uint2 w;
+                    if (which == 0) {
+                        w.x = pack2<T>(dkacc[dt][vg * 4 + 0] * f, dkacc[dt][vg * 4 + 1] * f);
+                        w.y = pack2<T>(dkacc[dt][vg * 4 + 2] * f, dkacc[dt][vg * 4 + 3] * f);
+                    } else {
+                        w.x = pack2<T>(dvacc[dt][vg * 4 + 0], dvacc[dt][vg * 4 + 1]);
+                        w.y = pack2<T>(dvacc[dt][vg * 4 + 2], dvacc[dt][vg * 4 + 3]);
+                    }
+                    *reinterpret_cast<uint2*>(st + l32 * RB + d0 * 2) = w;
                 }
+            }
+            T* base = which == 0 ? dkp : dvp;
+            const int64_t rs = which == 0 ? p.dks[2] : p.dvs[2];
+#pragma unroll
+            for (int r0 = 0; r0 < 32; r0 += RPI) {
+                const int r = r0 + lane / CPR, c = lane % CPR;
+                const int kr = wk0 + r;
+                const u32x4 v = *reinterpret_cast<const u32x4*>(st + r * RB + c * 16);
+                if (kr < T_ && (!PART || c * 8 < p.dr))
+                    __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(base + kr * rs + c * 8));
             }
         }
     }
