@@ -139,6 +139,41 @@ struct Mfma16<f16> {
     }
 };
 
+// A wave's 16 result rows (C layout of the 16x16 tiles: lane l holds row
+// l % 16, columns 16 dt + 4 (l / 16) .. +3), scaled by f, written through
+// LDS so that consecutive lanes store whole rows in 16-byte chunks, with
+// nontemporal stores (the results are not read again here, and their lines
+// then do not evict the tiles other blocks still read from L2).  st: the
+// wave's LDS area of 16 rows of 2 D + 16 bytes.  Rows at or past T and
+// chunks past dr are not stored.
+template <typename T, int D, bool PART>
+__device__ __forceinline__ void wide_store_rows(unsigned char* st, const f32x4 (&acc)[D / 16], float f, T* base,
+                                                int64_t rs, int row0, int T_, int dr, int lane) {
+    constexpr int RB = 2 * D + 16, CPR = 2 * D / 16, RPI = 64 / CPR;
+    const int g = lane >> 4, i16 = lane & 15;
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt)
+        *reinterpret_cast<uint2*>(st + i16 * RB + (16 * dt + 4 * g) * 2) =
+            uint2{pack2<T>(acc[dt][0] * f, acc[dt][1] * f), pack2<T>(acc[dt][2] * f, acc[dt][3] * f)};
+    // (a wave's LDS accesses complete in order: the reads below see its writes)
+#pragma unroll
+    for (int r0 = 0; r0 < 16; r0 += RPI) {
+        const int r = r0 + lane / CPR, c = lane % CPR;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(st + r * RB + c * 16);
+        if (row0 + r < T_ && (!PART || c * 8 < dr))
+            __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(base + static_cast<int64_t>(row0 + r) * rs + c * 8));
+    }
+}
+
+// The LDS area of wave w for wide_store_rows once the tile ring is free: the
+// first half of the waves in stage array 0, the second in stage array 1.
+template <int D>
+__device__ __forceinline__ unsigned char* wide_store_area(unsigned char* lds0, unsigned char* lds1, int wave) {
+    constexpr int NW = WideCfg<D>::NW;
+    static_assert(NW / 2 * 16 * (2 * D + 16) <= 2 * WideCfg<D>::KT * 2 * D, "half the waves' rows per stage array");
+    return (wave < NW / 2 ? lds0 : lds1) + (wave % (NW / 2)) * 16 * (2 * D + 16);
+}
+
 // FOLD (bf16, moderate positive scales): the S^T chains start at
 // c0 = -1/(2 scale), so they hold s' = s - 1/(2 scale) and
 // (a + sqrt(a^2 + 1))^2 = scale^2 (s' + sqrt(s'^2 + 1/scale^2))^2: the
@@ -334,15 +369,10 @@ __global__ __launch_bounds__(64 * WideCfg<D>::NW) void flash_fwd_wide_kernel(Wid
     part += __shfl_xor(part, 32);
     const float tot = FOLD ? __builtin_fmaf(part, sc * sc, kEps) : part + kEps;
     const float inv = FOLD ? (sc * sc) / tot : 1.f / tot;
-    if (qi < T_) {
-        T* orow = p.out + b * p.os[0] + hq * p.os[1] + qi * p.os[2];
-#pragma unroll
-        for (int dt = 0; dt < D / 16; ++dt) {
-            const uint2 w{pack2<T>(oacc[dt][0] * inv, oacc[dt][1] * inv), pack2<T>(oacc[dt][2] * inv, oacc[dt][3] * inv)};
-            if (16 * dt + 4 * g < p.dr) *reinterpret_cast<uint2*>(orow + 16 * dt + 4 * g) = w;
-        }
-        if (g == 0 && p.row_sums != nullptr) p.row_sums[(static_cast<int64_t>(b) * p.Hq + hq) * T_ + qi] = tot;
-    }
+    if (qi < T_ && g == 0 && p.row_sums != nullptr) p.row_sums[(static_cast<int64_t>(b) * p.Hq + hq) * T_ + qi] = tot;
+    __syncthreads();  // every wave is past its last tile: the ring is free
+    wide_store_rows<T, D, true>(wide_store_area<D>(lds0, lds1, wave), oacc, inv, p.out + b * p.os[0] + hq * p.os[1],
+                                p.os[2], q0w, T_, p.dr, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -546,15 +576,9 @@ __global__ __launch_bounds__(64 * WideCfg<D>::NW) void flash_bwd_dq_wide_kernel(
         if (t + 1 < kv_end) run_tile(t + 1, S1{});
     }
     // dS carried without its per-row factor 2 scale / R
-    if (qi < T_) {
-        const float f = 2.f * sc * inv_r;
-        T* row = p.dq + b * p.dqs[0] + hq * p.dqs[1] + qi * p.dqs[2];
-#pragma unroll
-        for (int dt = 0; dt < D / 16; ++dt) {
-            const uint2 w{pack2<T>(acc[dt][0] * f, acc[dt][1] * f), pack2<T>(acc[dt][2] * f, acc[dt][3] * f)};
-            if (!PART || 16 * dt + 4 * g < p.dr) *reinterpret_cast<uint2*>(row + 16 * dt + 4 * g) = w;
-        }
-    }
+    __syncthreads();  // every wave is past its last tile: the ring is free
+    wide_store_rows<T, D, PART>(wide_store_area<D>(lds0, lds1, wave), acc, 2.f * sc * inv_r,
+                                p.dq + b * p.dqs[0] + hq * p.dqs[1], p.dqs[2], q0w, T_, p.dr, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -786,15 +810,10 @@ __global__ __launch_bounds__(64 * WideCfg<D>::NW) void flash_bwd_kv_wide_kernel(
         step(it, S0{});
         if (it + 1 < n_it) step(it + 1, S1{});
     }
-    if (kj < T_) {
-        T* row = DK ? p.dk + b * p.dks[0] + hk * p.dks[1] + kj * p.dks[2] : p.dv + b * p.dvs[0] + hk * p.dvs[1] + kj * p.dvs[2];
-        const float f = DK ? 2.f * sc : 1.f;
-#pragma unroll
-        for (int dt = 0; dt < D / 16; ++dt) {
-            const uint2 w{pack2<T>(acc[dt][0] * f, acc[dt][1] * f), pack2<T>(acc[dt][2] * f, acc[dt][3] * f)};
-            if (!PART || 16 * dt + 4 * g < p.dr) *reinterpret_cast<uint2*>(row + 16 * dt + 4 * g) = w;
-        }
-    }
+    __syncthreads();  // every wave is past its last tile: the ring is free
+    T* base = DK ? p.dk + b * p.dks[0] + hk * p.dks[1] : p.dv + b * p.dvs[0] + hk * p.dvs[1];
+    wide_store_rows<T, D, PART>(wide_store_area<D>(lds0, lds1, wave), acc, DK ? 2.f * sc : 1.f, base,
+                                DK ? p.dks[2] : p.dvs[2], wk0, T_, p.dr, lane);
 }
 
 // 16-bit tensors: (b, h, t) strides multiples of 8 elements (16-byte rows),
