@@ -112,7 +112,8 @@ def test_noalloc_coarsens_the_split_when_the_partials_do_not_fit():
     assert torch.equal(got, smooth_attn.sp2norm_paged_attention(*dev, block_size=16))
 
 
-@pytest.mark.parametrize("P,D,dtype", [(1, 64, torch.float16), (128, 32, torch.bfloat16), (4, 128, torch.bfloat16)])
+@pytest.mark.parametrize("P,D,dtype", [(1, 64, torch.float16), (128, 32, torch.bfloat16), (4, 128, torch.bfloat16),
+                                     (16, 576, torch.float16), (16, 1024, torch.bfloat16)])
 def test_noalloc_page_sizes_and_head_dims(P, D, dtype):
     # the allocation-free call on the page sizes and head dims the workspace
     # entry point takes, against it (same split: bit-identical) and the oracle
