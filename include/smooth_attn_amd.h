@@ -204,8 +204,9 @@ int sa_flash_bwd(const void* q, const void* k, const void* v, const void* o,
  * dK / dV of the key blocks split over their query tiles, which the library
  * does for causal rows long against the grid (few batch x KV heads), where
  * the first key blocks, which see every query, would otherwise run alone at
- * the end; at most 512 MiB.  0 when it does not split (fp32, head dims
- * above 128, grids that fill the GPU); -1 for invalid sizes.
+ * the end; at most 512 MiB (head dims above 128: one buffer the dV and the
+ * dK kernel take in turn).  0 when it does not split (fp32, grids that fill
+ * the GPU); -1 for invalid sizes.
  */
 int64_t sa_flash_bwd_workspace_size(int B, int Hq, int Hkv, int T, int D,
                                     int window_size, int dtype);
@@ -213,9 +214,10 @@ int64_t sa_flash_bwd_workspace_size(int B, int Hq, int Hkv, int T, int D,
 /*
  * sa_flash_bwd with the workspace above (16-byte aligned).  A smaller
  * workspace runs fewer splits (none when NULL or 0 bytes); results are the
- * same up to fp32 summation order in dK and dV.  The split path adds one
- * kernel summing the partials in a fixed order, so results do not depend
- * on timing.  Replaces the same reference functions as sa_flash_bwd.
+ * same up to fp32 summation order in dK and dV.  The split path adds a
+ * kernel summing the partials in a fixed order (head dims above 128: one
+ * after the dV and one after the dK kernel), so results do not depend on
+ * timing.  Replaces the same reference functions as sa_flash_bwd.
  */
 int sa_flash_bwd_ws(const void* q, const void* k, const void* v, const void* o,
                     const void* dout, const float* row_sums, void* dq, void* dk,

@@ -36,11 +36,9 @@
 #include "flash_tiles.hpp"
 #include "flash_f32.hpp"
 #include "flash_wide.hpp"
+#include "dkdv_split.hpp"
 
 #include <algorithm>
-#include <functional>
-#include <mutex>
-#include <vector>
 
 namespace sa {
 namespace {
@@ -809,34 +807,18 @@ int dkdv_iterations(int kb, int T, int G, int W) {
 // tile of 128 keys with two blocks per CU), and the partials' writes and
 // reads at 5 TB/s; at most 512 MiB of partials.  (Fitted to measured times
 // of shapes from 1 x 2 KV heads x 4096 keys to 2 x 8 x 16384, where it picks
-// the fastest count of each.)
+// the fastest count of each.)  Grids of 4096 blocks or more are not split.
 int dkdv_split_count_uncached(int B, int Hkv, int T, int G, int W, int dr) {
     const int nkb = (T + kBwdBK - 1) / kBwdBK;
     const int64_t blocks = static_cast<int64_t>(nkb) * B * Hkv;
-    const int units = B * Hkv;
     int best = 1;
     double best_t = 0.0;
-    std::vector<double> slots;
     for (int S = 1; S <= 16; S *= 2) {
         // at most 16384 blocks and 512 MiB of partials
         if (blocks * S > 16384 || bwd_part_bytes(S, B, Hkv, T, dr) > (int64_t(512) << 20)) break;
-        // XCD 0's share: every 8th block of the dispatch order (kb, unit, split)
-        slots.assign(kBwdXcdSlots, 0.0);
-        double longest = 0.0;
-        int64_t id = 0;
-        for (int kb = 0; kb < nkb; ++kb) {
-            const int it = dkdv_iterations(kb, T, G, W);
-            for (int64_t j = 0; j < static_cast<int64_t>(units) * S; ++j, ++id) {
-                if (id % 8) continue;
-                const int s = static_cast<int>(j % S);
-                const double cost = (static_cast<int64_t>(s + 1) * it / S - static_cast<int64_t>(s) * it / S) + 2.0;
-                longest = std::max(longest, cost);
-                std::pop_heap(slots.begin(), slots.end(), std::greater<double>());
-                slots.back() += cost;
-                std::push_heap(slots.begin(), slots.end(), std::greater<double>());
-            }
-        }
-        double t = (*std::max_element(slots.begin(), slots.end()) + 0.2 * longest) * 5.0;  // us
+        double t = dkdv_split_makespan(nkb, B * Hkv, S, kBwdXcdSlots, 2.0,
+                                       [&](int kb) { return dkdv_iterations(kb, T, G, W); }) *
+                   5.0;  // us
         // the partials written, then read by the sum kernel
         if (S > 1) t += 2.0 * static_cast<double>(bwd_part_bytes(S, B, Hkv, T, dr)) / 5e6 + 5.0;
         if (S == 1 || t < best_t) {
@@ -847,32 +829,12 @@ int dkdv_split_count_uncached(int B, int Hkv, int T, int G, int W, int dr) {
     return best;
 }
 
-// The estimate above costs up to ~0.1 ms of host time, so the last few
-// shapes' counts are kept (a training step asks for the same shapes again).
 int dkdv_split_count(int B, int Hkv, int T, int G, int W, int dr) {
     const int64_t blocks = static_cast<int64_t>((T + kBwdBK - 1) / kBwdBK) * B * Hkv;
     if (blocks >= 8 * kBwdXcdSlots * 8 || blocks == 0) return 1;
-    struct Entry {
-        int key[6];
-        int n_split;
-    };
-    static std::mutex mu;
-    static Entry cache[16];
-    static int n_cached = 0, next = 0;
+    static SplitCountCache cache;
     const int key[6] = {B, Hkv, T, G, W, bwd_kernel_d(dr)};
-    {
-        std::lock_guard<std::mutex> lock(mu);
-        for (int i = 0; i < n_cached; ++i)
-            if (std::equal(key, key + 6, cache[i].key)) return cache[i].n_split;
-    }
-    const int n = dkdv_split_count_uncached(B, Hkv, T, G, W, dr);
-    std::lock_guard<std::mutex> lock(mu);
-    Entry& e = cache[next];
-    std::copy(key, key + 6, e.key);
-    e.n_split = n;
-    next = (next + 1) % 16;
-    n_cached = std::min(n_cached + 1, 16);
-    return n;
+    return cache.get(key, [&] { return dkdv_split_count_uncached(B, Hkv, T, G, W, dr); });
 }
 
 }  // namespace
@@ -882,7 +844,8 @@ extern "C" int64_t sa_flash_bwd_workspace_size(int B, int Hq, int Hkv, int T, in
     using namespace sa;
     if (B < 0 || Hq <= 0 || Hkv <= 0 || T < 0 || D <= 0 || Hq % Hkv != 0 || window_size < 0) return -1;
     if (dtype != SA_BF16 && dtype != SA_F16) return 0;
-    if (D > 128 || B == 0 || T == 0) return 0;
+    if (B == 0 || T == 0 || D > 512) return 0;
+    if (D > 128) return flash_bwd_wide_workspace_size(B, Hq, Hkv, T, D, window_size);
     return bwd_part_bytes(dkdv_split_count(B, Hkv, T, Hq / Hkv, window_size, D), B, Hkv, T, D);
 }
 
@@ -905,7 +868,8 @@ extern "C" int sa_flash_bwd_ws(const void* q, const void* k, const void* v, cons
         const int64_t* const all[8] = {q_strides,  k_strides,  v_strides,  o_strides,
                                        do_strides, dq_strides, dk_strides, dv_strides};
         return flash_bwd_wide(q, k, v, o, dout, row_sums, dq, dk, dv, delta_ws, B, Hq, Hkv, T, D, all, scale,
-                              window_size, exact_math, dtype, reinterpret_cast<hipStream_t>(stream));
+                              window_size, exact_math, dtype, workspace, workspace_bytes,
+                              reinterpret_cast<hipStream_t>(stream));
     }
     if (B < 0 || Hq <= 0 || Hkv <= 0 || T < 0 || Hq % Hkv != 0 || window_size < 0) return SA_ERR_BAD_SHAPE;
     if (!q || !k || !v || !o || !dout || !row_sums || !dq || !dk || !dv || !delta_ws) return SA_ERR_NULL_POINTER;

@@ -33,10 +33,12 @@
 // stored at c ^ swz(r): r & 15 for row reads (16 rows per cycle), 2 (r & 7)
 // for transposing reads (8 rows x 32 bytes per cycle), and for tiles read
 // both ways fk_swz(r) = 2 (r & 7) | ((r >> 3) & 1), which serves both.
+#include <algorithm>
 #include <type_traits>
 
 #include "flash_tiles.hpp"
 #include "flash_wide.hpp"
+#include "dkdv_split.hpp"
 
 namespace sa {
 namespace {
@@ -57,8 +59,10 @@ struct WideParams {
     float* delta;  // [B, Hq, T]
     int64_t qs[4], ks[4], vs[4], os[4], dos[4], dqs[4], dks[4], dvs[4];
     int B, Hq, Hkv, T, G, window;
-    int dr;  // head dim of the tensors (<= 256, a multiple of 8; columns past it read as zero, are not stored)
+    int dr;  // head dim of the tensors (<= D, a multiple of 8; columns past it read as zero, are not stored)
     float scale;
+    int n_split;  // dK/dV: query-range splits of every key block (1: none)
+    float* part;  // n_split > 1: fp32 partials [n_split][B * Hkv][T][D] of the dK or dV kernel
 };
 
 // 16 bytes of columns d0 .. d0 + 7 of a row; PART (head dim dr below the
@@ -621,8 +625,24 @@ __global__ __launch_bounds__(64 * WideCfg<D>::NW) void flash_bwd_kv_wide_kernel(
     const int i16 = lane & 15;
     const int T_ = p.T;
     const int per = p.B * p.Hkv;
-    const int kb = blockIdx.x / per;  // earliest key blocks (most queries) first
-    const int rest = blockIdx.x - kb * per;
+    // Block -> (ob, split): ob indexes the unsplit grid, split the block's
+    // share of ob's (head, query tile) iterations.  When that grid is a
+    // multiple of 8 blocks the n_split blocks of one ob run on ob's XCD
+    // (blocks are dealt to the XCDs by index mod 8).
+    const int n_split = p.n_split;
+    int ob = static_cast<int>(blockIdx.x), split = 0;
+    if (n_split > 1) {
+        if ((((T_ + kFRows - 1) / kFRows * per) & 7) == 0) {
+            const int j = ob >> 3;
+            split = j % n_split;
+            ob = ((j / n_split) << 3) | (ob & 7);
+        } else {
+            split = ob % n_split;
+            ob /= n_split;
+        }
+    }
+    const int kb = ob / per;  // earliest key blocks (most queries) first
+    const int rest = ob - kb * per;
     const int b = rest / p.Hkv;
     const int hk = rest - b * p.Hkv;
     const int k_start = kb * kFRows;
@@ -652,7 +672,10 @@ __global__ __launch_bounds__(64 * WideCfg<D>::NW) void flash_bwd_kv_wide_kernel(
     const int qt_begin = k_start / kFKT;
     const int qt_end = W > 0 ? min(n_qt, (k_start + kFRows - 1 + W - 1) / kFKT + 1) : n_qt;
     const int nq = qt_end - qt_begin;  // >= 1 (k_start < T)
-    const int n_it = p.G * nq;
+    const int n_it_all = p.G * nq;
+    // this block's iterations [it_lo, it_hi) of the n_it_all (head, query tile) pairs
+    const int it_lo = static_cast<int>(static_cast<int64_t>(split) * n_it_all / n_split);
+    const int it_hi = static_cast<int>(static_cast<int64_t>(split + 1) * n_it_all / n_split);
     const float sc = p.scale;
 
     // DMA of the Q and dO rows of a query tile; Q stores chunk c of row r at
@@ -781,14 +804,16 @@ __global__ __launch_bounds__(64 * WideCfg<D>::NW) void flash_bwd_kv_wide_kernel(
 
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
-    issue(0, S0{});
-    store_rv(0, row_value(0));
-    tile_wait_vmem();
+    if (it_lo < it_hi) {
+        issue(it_lo, S0{});
+        store_rv(0, row_value(it_lo));
+        tile_wait_vmem();
+    }
     __syncthreads();
-    // iteration it reads stage it & 1 while the DMA fills the other with it + 1
+    // iteration it reads stage (it - it_lo) & 1 while the DMA fills the other with it + 1
     auto step = [&](int it, auto cur) {
         constexpr int nxt = 1 - decltype(cur)::value;
-        const bool more = it + 1 < n_it;
+        const bool more = it + 1 < it_hi;
         float rnext = 0.f;
         if (more) {
             issue(it + 1, std::integral_constant<int, nxt>{});  // free since the barrier that ended it - 1
@@ -806,14 +831,51 @@ __global__ __launch_bounds__(64 * WideCfg<D>::NW) void flash_bwd_kv_wide_kernel(
             __syncthreads();
         }
     };
-    for (int it = 0; it < n_it; it += 2) {
+    for (int it = it_lo; it < it_hi; it += 2) {
         step(it, S0{});
-        if (it + 1 < n_it) step(it + 1, S1{});
+        if (it + 1 < it_hi) step(it + 1, S1{});
+    }
+    if (n_split > 1) {
+        // fp32 partial of key kj (zeros for an empty share), unscaled
+        if (kj < T_) {
+            float* dst = p.part + ((static_cast<int64_t>(split) * per + rest) * T_ + kj) * D + 4 * g;
+#pragma unroll
+            for (int dt = 0; dt < D / 16; ++dt)
+                if (!PART || 16 * dt + 4 * g < p.dr) *reinterpret_cast<f32x4*>(dst + 16 * dt) = acc[dt];
+        }
+        return;
     }
     __syncthreads();  // every wave is past its last tile: the ring is free
     T* base = DK ? p.dk + b * p.dks[0] + hk * p.dks[1] : p.dv + b * p.dvs[0] + hk * p.dvs[1];
     wide_store_rows<T, D, PART>(wide_store_area<D>(lds0, lds1, wave), acc, DK ? 2.f * sc : 1.f, base,
                                 DK ? p.dks[2] : p.dvs[2], wk0, T_, p.dr, lane);
+}
+
+// dK (DK) or dV = the sum of the n_split fp32 partials (in split order, so
+// the result does not depend on timing), dK times 2 scale; one thread per
+// four columns of a key row.
+template <typename T, int D, bool DK>
+__global__ __launch_bounds__(256) void wide_split_reduce_kernel(WideParams<T> p, int64_t n_quads) {
+    const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (gid >= n_quads) return;
+    const int64_t row = gid / (D / 4);  // (b * Hkv + hk) * T + key
+    const int d0 = static_cast<int>(gid - row * (D / 4)) * 4;
+    if (d0 >= p.dr) return;
+    const int64_t plane = static_cast<int64_t>(p.B) * p.Hkv * p.T * D;
+    const float* src = p.part + row * D + d0;
+    float4 a = float4{0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < p.n_split; ++s) {
+        const float4 c = *reinterpret_cast<const float4*>(src + s * plane);
+        a.x += c.x; a.y += c.y; a.z += c.z; a.w += c.w;
+    }
+    const float f = DK ? 2.f * p.scale : 1.f;
+    const int64_t bh = row / p.T;
+    const int key = static_cast<int>(row - bh * p.T);
+    const int b = static_cast<int>(bh / p.Hkv);
+    const int hk = static_cast<int>(bh - static_cast<int64_t>(b) * p.Hkv);
+    T* dst = DK ? p.dk + b * p.dks[0] + hk * p.dks[1] + key * p.dks[2]
+                : p.dv + b * p.dvs[0] + hk * p.dvs[1] + key * p.dvs[2];
+    *reinterpret_cast<uint2*>(dst + d0) = uint2{pack2<T>(a.x * f, a.y * f), pack2<T>(a.z * f, a.w * f)};
 }
 
 // 16-bit tensors: (b, h, t) strides multiples of 8 elements (16-byte rows),
@@ -851,22 +913,30 @@ int launch_fwd_wide(const WideParams<T>& prm, int exact, hipStream_t st) {
     return status_from_launch();
 }
 
+template <typename T, int D, bool EXACT, bool PART>
+void launch_bwd_wide_kernels(const WideParams<T>& prm, dim3 gq, dim3 gk, hipStream_t st) {
+    constexpr int kFW = WideCfg<D>::NW;
+    flash_bwd_dq_wide_kernel<T, D, EXACT, PART><<<gq, 64 * kFW, 0, st>>>(prm);
+    // dV, then dK; with a split each sums its partials before the next
+    // kernel reuses the buffer
+    const int64_t n_quads = static_cast<int64_t>(prm.B) * prm.Hkv * prm.T * (D / 4);
+    const dim3 gr(static_cast<unsigned>((n_quads + 255) / 256));
+    flash_bwd_kv_wide_kernel<T, D, EXACT, false, PART><<<gk, 64 * kFW, 0, st>>>(prm);
+    if (prm.n_split > 1) wide_split_reduce_kernel<T, D, false><<<gr, 256, 0, st>>>(prm, n_quads);
+    flash_bwd_kv_wide_kernel<T, D, EXACT, true, PART><<<gk, 64 * kFW, 0, st>>>(prm);
+    if (prm.n_split > 1) wide_split_reduce_kernel<T, D, true><<<gr, 256, 0, st>>>(prm, n_quads);
+}
+
 template <typename T, int D, bool PART>
 int launch_bwd_wide_part(const WideParams<T>& prm, int exact, hipStream_t st) {
     constexpr int kFW = WideCfg<D>::NW, kFRows = WideCfg<D>::ROWS;
     const int64_t nq = static_cast<int64_t>((prm.T + kFRows - 1) / kFRows) * prm.B * prm.Hq;
     if (nq * 64 * kFW >= (int64_t(1) << 32)) return SA_ERR_BAD_SHAPE;  // dQ blocks of kFW waves
-    const int64_t nk = nq / prm.G;
+    const int64_t nk = nq / prm.G * prm.n_split;
+    if (nk * 64 * kFW >= (int64_t(1) << 32)) return SA_ERR_BAD_SHAPE;
     const dim3 gq(static_cast<unsigned>(nq)), gk(static_cast<unsigned>(nk));
-    if (exact) {
-        flash_bwd_dq_wide_kernel<T, D, true, PART><<<gq, 64 * kFW, 0, st>>>(prm);
-        flash_bwd_kv_wide_kernel<T, D, true, false, PART><<<gk, 64 * kFW, 0, st>>>(prm);
-        flash_bwd_kv_wide_kernel<T, D, true, true, PART><<<gk, 64 * kFW, 0, st>>>(prm);
-    } else {
-        flash_bwd_dq_wide_kernel<T, D, false, PART><<<gq, 64 * kFW, 0, st>>>(prm);
-        flash_bwd_kv_wide_kernel<T, D, false, false, PART><<<gk, 64 * kFW, 0, st>>>(prm);
-        flash_bwd_kv_wide_kernel<T, D, false, true, PART><<<gk, 64 * kFW, 0, st>>>(prm);
-    }
+    if (exact) launch_bwd_wide_kernels<T, D, true, PART>(prm, gq, gk, st);
+    else launch_bwd_wide_kernels<T, D, false, PART>(prm, gq, gk, st);
     return status_from_launch();
 }
 
@@ -908,11 +978,73 @@ int run_fwd_wide(const void* q, const void* k, const void* v, void* o, float* ro
     return launch_fwd_wide<T, 512>(prm, exact_math, st);
 }
 
+// Kernel head dim for head dim dr in 136..512.
+int wide_kernel_d(int dr) { return dr <= 256 ? 256 : 512; }
+
+int64_t wide_part_bytes(int n_split, int B, int Hkv, int T, int dr) {
+    return n_split > 1 ? static_cast<int64_t>(n_split) * B * Hkv * T * wide_kernel_d(dr) * 4 : 0;
+}
+
+// (head, query tile) iterations of dK/dV key block kb, as the kernels count them.
+template <int D>
+int wide_kv_iterations(int kb, int T, int G, int W) {
+    constexpr int R = WideCfg<D>::ROWS, KT = WideCfg<D>::KT;
+    const int n_qt = (T + KT - 1) / KT;
+    const int k_start = kb * R;
+    const int qt_begin = k_start / KT;
+    const int qt_end = W > 0 ? std::min(n_qt, (k_start + R - 1 + W - 1) / KT + 1) : n_qt;
+    return G * (qt_end - qt_begin);
+}
+
+// Query-range splits of the dK and dV blocks, as for head dims up to 128:
+// causally, key block kb sees the query tiles from its own on, so the first
+// blocks hold the most work, and a grid that does not fill the chip several
+// times over idles while they finish.  The count is the one of 1, 2, 4, 8,
+// 16 with the least estimated time: the makespan of an XCD's share (one
+// block per CU, 32 at once; a block's set-up and stores at two iterations),
+// an iteration of the dV and the dK kernel together at kWideItUs, plus the
+// two kernels' partials written and read back at 5 TB/s and two more
+// launches.  Both kernels use the count, one after the other, on one buffer
+// of at most 512 MiB; grids of 2048 blocks or more are not split.
+template <int D>
+int wide_split_count_uncached(int B, int Hkv, int T, int G, int W) {
+    constexpr double kWideItUs = D > 256 ? 3.0 : 6.0;
+    const int nkb = (T + WideCfg<D>::ROWS - 1) / WideCfg<D>::ROWS;
+    const int64_t blocks = static_cast<int64_t>(nkb) * B * Hkv;
+    int best = 1;
+    double best_t = 0.0;
+    for (int S = 1; S <= 16; S *= 2) {
+        const int64_t bytes = wide_part_bytes(S, B, Hkv, T, D);
+        if (blocks * S > 16384 || bytes > (int64_t(512) << 20)) break;
+        double t = dkdv_split_makespan(nkb, B * Hkv, S, 32, 2.0,
+                                       [&](int kb) { return wide_kv_iterations<D>(kb, T, G, W); }) *
+                   kWideItUs;  // us
+        if (S > 1) t += 4.0 * static_cast<double>(bytes) / 5e6 + 10.0;
+        if (S == 1 || t < best_t) {
+            best = S;
+            best_t = t;
+        }
+    }
+    return best;
+}
+
+int wide_split_count(int B, int Hkv, int T, int G, int W, int dr) {
+    const int R = dr <= 256 ? WideCfg<256>::ROWS : WideCfg<512>::ROWS;  // key rows per block
+    const int64_t blocks = static_cast<int64_t>((T + R - 1) / R) * B * Hkv;
+    if (blocks >= 8 * 32 * 8 || blocks == 0) return 1;
+    static SplitCountCache cache;
+    const int key[6] = {B, Hkv, T, G, W, wide_kernel_d(dr)};
+    return cache.get(key, [&] {
+        return dr <= 256 ? wide_split_count_uncached<256>(B, Hkv, T, G, W)
+                         : wide_split_count_uncached<512>(B, Hkv, T, G, W);
+    });
+}
+
 template <typename T>
 int run_bwd_wide(const void* q, const void* k, const void* v, const void* o, const void* dout,
                  const float* row_sums, void* dq, void* dk, void* dv, float* delta_ws, int B, int Hq, int Hkv,
                  int T_, int D, const int64_t* const strides[8], float scale, int window_size, int exact_math,
-                 hipStream_t st) {
+                 int n_split, float* part, hipStream_t st) {
     WideParams<T> prm{};
     prm.q = static_cast<const T*>(q);
     prm.k = static_cast<const T*>(k);
@@ -935,6 +1067,8 @@ int run_bwd_wide(const void* q, const void* k, const void* v, const void* o, con
     prm.window = window_size;
     prm.dr = D;
     prm.scale = scale;
+    prm.n_split = n_split;
+    prm.part = part;
     return launch_bwd_wide<T>(prm, exact_math, st);
 }
 
@@ -958,10 +1092,15 @@ int flash_fwd_wide(const void* q, const void* k, const void* v, void* o, float* 
                              scale, window_size, exact_math, st);
 }
 
+int64_t flash_bwd_wide_workspace_size(int B, int Hq, int Hkv, int T, int D, int window_size) {
+    if (D <= 128 || D > 512 || B == 0 || T == 0) return 0;
+    return wide_part_bytes(wide_split_count(B, Hkv, T, Hq / Hkv, window_size, D), B, Hkv, T, D);
+}
+
 int flash_bwd_wide(const void* q, const void* k, const void* v, const void* o, const void* dout,
                    const float* row_sums, void* dq, void* dk, void* dv, float* delta_ws, int B, int Hq, int Hkv,
                    int T, int D, const int64_t* const strides[8], float scale, int window_size, int exact_math,
-                   int dtype, hipStream_t st) {
+                   int dtype, void* workspace, int64_t workspace_bytes, hipStream_t st) {
     const int chk = check_wide(B, Hq, Hkv, T, D, window_size, dtype);
     if (chk != 0) return chk;
     if (!q || !k || !v || !o || !dout || !row_sums || !dq || !dk || !dv || !delta_ws) return SA_ERR_NULL_POINTER;
@@ -971,11 +1110,20 @@ int flash_bwd_wide(const void* q, const void* k, const void* v, const void* o, c
         if (!wide_strides_ok(strides[i]) || !aligned16(ptrs[i])) return SA_ERR_BAD_STRIDE;
     }
     if (B == 0 || T == 0) return 0;
+    // the library's split count, or the largest power of two below it whose
+    // partials fit the workspace
+    int ns = 1;
+    if (workspace && workspace_bytes > 0) {
+        if (!aligned16(workspace)) return SA_ERR_BAD_STRIDE;
+        ns = wide_split_count(B, Hkv, T, Hq / Hkv, window_size, D);
+        while (ns > 1 && wide_part_bytes(ns, B, Hkv, T, D) > workspace_bytes) ns /= 2;
+    }
+    float* part = ns > 1 ? static_cast<float*>(workspace) : nullptr;
     if (dtype == SA_BF16)
         return run_bwd_wide<bf16>(q, k, v, o, dout, row_sums, dq, dk, dv, delta_ws, B, Hq, Hkv, T, D, strides, scale,
-                                  window_size, exact_math, st);
+                                  window_size, exact_math, ns, part, st);
     return run_bwd_wide<f16>(q, k, v, o, dout, row_sums, dq, dk, dv, delta_ws, B, Hq, Hkv, T, D, strides, scale,
-                             window_size, exact_math, st);
+                             window_size, exact_math, ns, part, st);
 }
 
 }  // namespace sa

@@ -13,10 +13,16 @@ int flash_fwd_wide(const void* q, const void* k, const void* v, void* o, float* 
                    const int64_t* o_strides, float scale, int window_size, int exact_math, int dtype,
                    hipStream_t st);
 
-// Validates and launches the D = 256 / 512 backward (same contract as sa_flash_bwd).
+// Bytes of fp32 partials the D = 256 / 512 backward splits its dK and dV
+// blocks into at this shape (0: no split); D in 136..512.
+int64_t flash_bwd_wide_workspace_size(int B, int Hq, int Hkv, int T, int D, int window_size);
+
+// Validates and launches the D = 256 / 512 backward (same contract as
+// sa_flash_bwd_ws: without a workspace, or one below the size above, the
+// split is coarser or absent).
 int flash_bwd_wide(const void* q, const void* k, const void* v, const void* o, const void* dout,
                    const float* row_sums, void* dq, void* dk, void* dv, float* delta_ws, int B, int Hq, int Hkv,
                    int T, int D, const int64_t* const strides[8], float scale, int window_size, int exact_math,
-                   int dtype, hipStream_t st);
+                   int dtype, void* workspace, int64_t workspace_bytes, hipStream_t st);
 
 }  // namespace sa

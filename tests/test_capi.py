@@ -190,18 +190,24 @@ def test_flash_fp32_argument_errors():
 
 def test_flash_bwd_workspace_size():
     # fp32 partials of dK / dV for split key blocks: only for 16-bit head dims
-    # up to 128 and grids that leave the GPU idle behind the first key blocks;
-    # the size is n_split * 2 (dK, dV) * B * Hkv * T * kernel head dim * 4
+    # and grids that leave the GPU idle behind the first key blocks; the size
+    # is n_split * 2 (dK, dV) * B * Hkv * T * kernel head dim * 4 for head
+    # dims up to 128, and n_split * B * Hkv * T * kernel head dim * 4 (one
+    # buffer the dV and the dK kernel take in turn) for the kernels of head
+    # dim 256 and 512
     lib = _lib.load()
     ws = lambda B, Hq, Hkv, T, D, W=0, dt=_lib.SA_BF16: lib.sa_flash_bwd_workspace_size(B, Hq, Hkv, T, D, W, dt)
-    for B, Hq, Hkv, T, D, Dk in ((1, 32, 8, 8192, 128, 128), (1, 8, 1, 65536, 128, 128), (1, 4, 2, 333, 40, 64)):
+    for B, Hq, Hkv, T, D, Dk, planes in ((1, 32, 8, 8192, 128, 128, 2), (1, 8, 1, 65536, 128, 128, 2),
+                                         (1, 4, 2, 333, 40, 64, 2), (1, 16, 2, 16384, 256, 256, 1),
+                                         (1, 4, 2, 333, 200, 256, 1), (1, 8, 1, 16384, 512, 512, 1),
+                                         (1, 2, 1, 260, 400, 512, 1)):
         n = ws(B, Hq, Hkv, T, D)
-        unit = 2 * B * Hkv * T * Dk * 4
+        unit = planes * B * Hkv * T * Dk * 4
         assert n > 0 and n % unit == 0 and n // unit in (2, 4, 8, 16), (B, Hq, Hkv, T, D, n)
         assert ws(B, Hq, Hkv, T, D, dt=_lib.SA_F16) == n
     assert ws(1, 32, 8, 8192, 128, dt=_lib.SA_F32) == 0  # fp32 kernels do not split
-    assert ws(1, 32, 8, 8192, 200) == 0  # nor the head-dim-256 kernels
     assert ws(16, 32, 8, 4096, 128) == 0  # 4096 key blocks fill the GPU
+    assert ws(4, 16, 16, 4096, 256) == 0  # 2048 blocks of the head-dim-256 kernels too
     assert ws(0, 32, 8, 8192, 128) == 0 and ws(1, 32, 8, 0, 128) == 0
     assert ws(1, 30, 8, 8192, 128) == -1 and ws(-1, 32, 8, 64, 128) == -1
     # a workspace that is not 16-byte aligned is refused before any launch

@@ -1,5 +1,6 @@
 """The attention backward with dK / dV key blocks split over their query
-tiles (sa_flash_bwd_ws), GPU.
+tiles (sa_flash_bwd_ws), GPU, on the kernels for head dims up to 128 and
+for head dims 136..512.
 
 Causally, key block j of the dK/dV kernel sees the query tiles from j on, so
 the first blocks hold the most work; where B x Hkv is small the library
@@ -95,6 +96,12 @@ def forward(qd, kd, vd, scale, G, window):
     (1, 8, 2, 520, 128, 0, False, torch.bfloat16),
     (1, 3, 1, 257, 96, 33, False, torch.float16),
     (1, 2, 1, 1, 32, 0, False, torch.bfloat16),
+    # the head-dim-256 and -512 kernels (dK and dV kernels one after the other)
+    (1, 4, 2, 333, 200, 0, False, torch.bfloat16),
+    (1, 4, 1, 300, 256, 64, False, torch.float16),
+    (1, 2, 1, 260, 400, 0, True, torch.bfloat16),
+    (1, 2, 2, 200, 512, 0, False, torch.bfloat16),
+    (1, 2, 1, 1, 256, 0, False, torch.bfloat16),
 ])
 def test_split_matches_oracle(B, Hq, Hkv, T, D, window, exact, dtype):
     q, k, v, do = inputs(B, Hq, Hkv, T, D, dtype, seed=T + D)
@@ -124,13 +131,22 @@ def test_split_matches_oracle(B, Hq, Hkv, T, D, window, exact, dtype):
         assert err <= 1e-2, f"{what}: {name} rel err {err:.3e}"
 
 
+def split_unit(B, Hkv, T, D):
+    """Workspace bytes per split: fp32 partials of dK and dV at the kernel's
+    head dim (32, 64, 128), or one buffer the dK and dV kernels of head dim
+    256 / 512 take in turn."""
+    kd = next(d for d in (32, 64, 128, 256, 512) if D <= d)
+    return (2 if kd <= 128 else 1) * B * Hkv * T * kd * 4
+
+
 def close_to_unsplit(got, ref):
     """max |got - ref| within two bf16 steps of max|ref|."""
     scale = float(ref.float().abs().max())
     return float((got.float() - ref.float()).abs().max()) <= 2 * 2.0 ** -7 * max(scale, 1e-30)
 
 
-@pytest.mark.parametrize("B,Hq,Hkv,T,D", [(1, 8, 2, 700, 128), (1, 4, 1, 1000, 64), (2, 4, 2, 640, 32)])
+@pytest.mark.parametrize("B,Hq,Hkv,T,D", [(1, 8, 2, 700, 128), (1, 4, 1, 1000, 64), (2, 4, 2, 640, 32),
+                                         (1, 8, 2, 1000, 256), (1, 4, 1, 900, 448), (2, 2, 1, 640, 512)])
 def test_every_split_count_matches_unsplit(B, Hq, Hkv, T, D):
     dtype = torch.bfloat16
     q, k, v, do = (t.to(DEV) for t in inputs(B, Hq, Hkv, T, D, dtype, seed=B * T))
@@ -140,7 +156,7 @@ def test_every_split_count_matches_unsplit(B, Hq, Hkv, T, D):
     base = [torch.empty_like(t) for t in (q, k, v)]
     bwd(q, k, v, o, do, rs, base, scale, 0, False, None)
     n = ws_size(q, k, 0)
-    unit = 2 * B * Hkv * T * D * 4
+    unit = split_unit(B, Hkv, T, D)
     assert n > 0 and n % unit == 0
     splits = n // unit
     seen = 0
@@ -154,10 +170,10 @@ def test_every_split_count_matches_unsplit(B, Hq, Hkv, T, D):
     assert seen >= 2
 
 
-@pytest.mark.parametrize("B,Hq,Hkv,T", [(1, 32, 8, 8192), (1, 8, 1, 32768)])
-def test_long_context_split_matches_unsplit(B, Hq, Hkv, T):
-    # config-like long rows over few KV heads (the split's case), D = 128
-    D = 128
+@pytest.mark.parametrize("B,Hq,Hkv,T,D", [(1, 32, 8, 8192, 128), (1, 8, 1, 32768, 128), (1, 16, 2, 16384, 256),
+                                         (1, 8, 1, 16384, 512)])
+def test_long_context_split_matches_unsplit(B, Hq, Hkv, T, D):
+    # config-like long rows over few KV heads (the split's case)
     dtype = torch.bfloat16
     g = torch.Generator(device=DEV).manual_seed(T)
     q = torch.randn(B, Hq, T, D, generator=g, device=DEV).to(dtype)
