@@ -854,21 +854,23 @@ int launch_bwd_f32_d(const F32Params& prm, int exact, hipStream_t st) {
             flash_bwd_dkdv_f32r16_kernel<D, false, false><<<gk, 64 * kRW, 0, st>>>(prm);
         }
         return status_from_launch();
-    }
-    if (exact && part) {
-        flash_bwd_dq_f32_kernel<D, true, true><<<gq, 64 * kFW, 0, st>>>(prm);
-        flash_bwd_dkdv_f32_kernel<D, true, true><<<gk, 64 * kFW, 0, st>>>(prm);
-    } else if (exact) {
-        flash_bwd_dq_f32_kernel<D, true, false><<<gq, 64 * kFW, 0, st>>>(prm);
-        flash_bwd_dkdv_f32_kernel<D, true, false><<<gk, 64 * kFW, 0, st>>>(prm);
-    } else if (part) {
-        flash_bwd_dq_f32_kernel<D, false, true><<<gq, 64 * kFW, 0, st>>>(prm);
-        flash_bwd_dkdv_f32_kernel<D, false, true><<<gk, 64 * kFW, 0, st>>>(prm);
     } else {
-        flash_bwd_dq_f32_kernel<D, false, false><<<gq, 64 * kFW, 0, st>>>(prm);
-        flash_bwd_dkdv_f32_kernel<D, false, false><<<gk, 64 * kFW, 0, st>>>(prm);
+        // (D = 128 never builds the 32-row kernels: they would spill there)
+        if (exact && part) {
+            flash_bwd_dq_f32_kernel<D, true, true><<<gq, 64 * kFW, 0, st>>>(prm);
+            flash_bwd_dkdv_f32_kernel<D, true, true><<<gk, 64 * kFW, 0, st>>>(prm);
+        } else if (exact) {
+            flash_bwd_dq_f32_kernel<D, true, false><<<gq, 64 * kFW, 0, st>>>(prm);
+            flash_bwd_dkdv_f32_kernel<D, true, false><<<gk, 64 * kFW, 0, st>>>(prm);
+        } else if (part) {
+            flash_bwd_dq_f32_kernel<D, false, true><<<gq, 64 * kFW, 0, st>>>(prm);
+            flash_bwd_dkdv_f32_kernel<D, false, true><<<gk, 64 * kFW, 0, st>>>(prm);
+        } else {
+            flash_bwd_dq_f32_kernel<D, false, false><<<gq, 64 * kFW, 0, st>>>(prm);
+            flash_bwd_dkdv_f32_kernel<D, false, false><<<gk, 64 * kFW, 0, st>>>(prm);
+        }
+        return status_from_launch();
     }
-    return status_from_launch();
 }
 
 }  // namespace
