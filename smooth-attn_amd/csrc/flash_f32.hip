@@ -14,13 +14,13 @@
 // contiguous half-row.  For products with P or dS as the B operand (O^T +=
 // V^T P^T, dQ^T += K^T dS^T, dV^T += dO^T P, dK^T += Q^T dS) MFMA j takes the
 // lane's own C element v = j: k = 0 is row 8 (j / 4) + j % 4 and k = 1 that
-// row + 4, so the A operand's four consecutive rows for j = 4m .. 4m + 3 come
-// from one 16-byte read of a transposed [D][rows] LDS tile.
+// row + 4, and the A operand (column d of those rows) is one 4-byte read of
+// the row-major tile per MFMA.
 //
 // Work decomposition: blocks of 4 waves, 32 rows per wave (queries in the
-// forward and dQ, keys in dK/dV), tiles of 32 rows staged in LDS (row-major
-// [32][D + 4] and, where the transposed operand is needed, [D][36]); the
-// next tile's global loads are in flight while the current one is used.
+// forward and dQ, keys in dK/dV), tiles of 32 rows staged in LDS, row-major
+// [32][D + 4] (V in the forward [32][D + 8]: it is only read by columns);
+// the next tile's global loads are in flight while the current one is used.
 #include "flash_f32.hpp"
 #include "flash_tiles.hpp"
 
@@ -32,7 +32,6 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int kFW = 4;             // waves per block
 constexpr int kFT = 32;            // rows per staged tile
 constexpr int kFRows = 32 * kFW;   // rows a block owns
-constexpr int kTP = kFT + 4;       // pitch (floats) of a transposed [D][kFT] tile
 
 __device__ __forceinline__ f32x16 mma32(float a, float b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
@@ -81,20 +80,15 @@ struct TileRegs {
             }
         }
     }
-    // row-major [kFT][D + 4] (nullable) and transposed [D][kTP] (nullable)
-    __device__ __forceinline__ void store(float* row, float* tr, int tid) const {
+    // row-major [kFT][P]
+    template <int P = D + 4>
+    __device__ __forceinline__ void store(float* row, int tid) const {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int idx = tid + 64 * kFW * i;
             const int r = idx / (D / 4);
             const int c = (idx - r * (D / 4)) * 4;
-            if (row != nullptr) *reinterpret_cast<float4*>(row + r * (D + 4) + c) = v[i];
-            if (tr != nullptr) {
-                tr[(c + 0) * kTP + r] = v[i].x;
-                tr[(c + 1) * kTP + r] = v[i].y;
-                tr[(c + 2) * kTP + r] = v[i].z;
-                tr[(c + 3) * kTP + r] = v[i].w;
-            }
+            *reinterpret_cast<float4*>(row + r * P + c) = v[i];
         }
     }
 };
@@ -155,21 +149,24 @@ __device__ __forceinline__ f32x16 mma_rows(const float* lds_rows, int l32, int h
 }
 
 // acc[dt] (rows d = 32 dt + ..) += A^T(d, r) X(r, col) over the tile's 32
-// rows r, A^T read from a transposed [D][kTP] LDS tile and X the lane's own
-// 16 C-layout values x[v] (row 8 (v / 4) + 4 hi + v % 4).
-template <int D>
-__device__ __forceinline__ void mma_cols(const float* lds_tr, int l32, int hi, const float (&x)[16],
+// rows r, X the lane's own 16 C-layout values x[v] (row 8 (v / 4) + 4 hi +
+// v % 4).  A^T is read from the row-major [kFT][P] tile itself, element (8 m
+// + 4 hi + j, 32 dt + l32) for MFMA 4 m + j, one 4-byte read each: the 32
+// lanes of a half read consecutive banks, the two halves 4 P floats apart
+// (P = D + 8: 32 mod 64, no conflict; P = D + 4, for tiles also read by
+// rows: 16 mod 64, two-way on a quarter of the banks).  Reading the tile
+// this way replaces a transposed copy, whose scalar stores (16-way bank
+// conflicts) stalled every wave between the staging barriers.
+template <int D, int P>
+__device__ __forceinline__ void mma_cols(const float* lds_rows, int l32, int hi, const float (&x)[16],
                                          f32x16 (&acc)[D / 32]) {
+    const float* base = lds_rows + 4 * hi * P + l32;
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) {
-        const float* ar = lds_tr + (dt * 32 + l32) * kTP + 4 * hi;
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-            const float4 a = *reinterpret_cast<const float4*>(ar + 8 * m);
-            acc[dt] = mma32(a.x, x[4 * m + 0], acc[dt]);
-            acc[dt] = mma32(a.y, x[4 * m + 1], acc[dt]);
-            acc[dt] = mma32(a.z, x[4 * m + 2], acc[dt]);
-            acc[dt] = mma32(a.w, x[4 * m + 3], acc[dt]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[dt] = mma32(base[(8 * m + j) * P + 32 * dt], x[4 * m + j], acc[dt]);
         }
     }
 }
@@ -213,7 +210,7 @@ template <int D, bool EXACT>
 __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 128 ? 1 : 2, 8))) void flash_fwd_f32_kernel(F32Params p) {
     constexpr bool PART = true;
     __shared__ __attribute__((aligned(16))) float ldsK[kFT * (D + 4)];
-    __shared__ __attribute__((aligned(16))) float ldsVt[D * kTP];
+    __shared__ __attribute__((aligned(16))) float ldsV[kFT * (D + 8)];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -253,8 +250,8 @@ __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 12
     vreg.template load<PART>(vp, p.vs[2], kv_begin * kFT, T_, tid, p.dr);
     for (int t = kv_begin; t < kv_end; ++t) {
         __syncthreads();  // every wave is done with tile t - 1
-        kreg.store(ldsK, nullptr, tid);
-        vreg.store(nullptr, ldsVt, tid);
+        kreg.store(ldsK, tid);
+        vreg.template store<D + 8>(ldsV, tid);
         __syncthreads();
         if (t + 1 < kv_end) {
             kreg.template load<PART>(kp, p.ks[2], (t + 1) * kFT, T_, tid, p.dr);
@@ -274,7 +271,7 @@ __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 12
             pv[v] = y;
             ssum += y;
         }
-        mma_cols<D>(ldsVt, l32, hi, pv, oacc);  // O^T += V^T P^T
+        mma_cols<D, D + 8>(ldsV, l32, hi, pv, oacc);  // O^T += V^T P^T
     }
 
     const float tot = ssum + __shfl_xor(ssum, 32) + kEps;
@@ -290,7 +287,6 @@ __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 12
 template <int D, bool EXACT, bool PART>
 __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 128 ? 1 : 2, 8))) void flash_bwd_dq_f32_kernel(F32Params p) {
     __shared__ __attribute__((aligned(16))) float ldsK[kFT * (D + 4)];
-    __shared__ __attribute__((aligned(16))) float ldsKt[D * kTP];
     __shared__ __attribute__((aligned(16))) float ldsV[kFT * (D + 4)];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -354,8 +350,8 @@ __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 12
     vreg.template load<PART>(vp, p.vs[2], kv_begin * kFT, T_, tid, p.dr);
     for (int t = kv_begin; t < kv_end; ++t) {
         __syncthreads();
-        kreg.store(ldsK, ldsKt, tid);
-        vreg.store(ldsV, nullptr, tid);
+        kreg.store(ldsK, tid);
+        vreg.store(ldsV, tid);
         __syncthreads();
         if (t + 1 < kv_end) {
             kreg.template load<PART>(kp, p.ks[2], (t + 1) * kFT, T_, tid, p.dr);
@@ -374,7 +370,7 @@ __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 12
             weight_rr<EXACT>(s[v], sc, y, rr);
             ds[v] = keep_if(static_cast<unsigned>(qi - key) < weff, dp[v] * y * rr);
         }
-        mma_cols<D>(ldsKt, l32, hi, ds, acc);  // dQ^T += K^T dS^T
+        mma_cols<D, D + 4>(ldsK, l32, hi, ds, acc);  // dQ^T += K^T dS^T
     }
     // dS carried without its per-row factor 2 scale / R
     if (qi < T_) store_cols<D, PART>(p.dq + b * p.dqs[0] + hq * p.dqs[1] + qi * p.dqs[2], hi, acc, 2.f * sc * inv_r, p.dr);
@@ -386,9 +382,7 @@ __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 12
 template <int D, bool EXACT, bool PART>
 __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 128 ? 1 : 2, 8))) void flash_bwd_dkdv_f32_kernel(F32Params p) {
     __shared__ __attribute__((aligned(16))) float ldsQ[kFT * (D + 4)];
-    __shared__ __attribute__((aligned(16))) float ldsQt[D * kTP];
     __shared__ __attribute__((aligned(16))) float ldsO[kFT * (D + 4)];
-    __shared__ __attribute__((aligned(16))) float ldsOt[D * kTP];
     __shared__ __attribute__((aligned(16))) float ldr[2][kFT];  // [1/R, -delta] of the tile's rows
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -444,8 +438,8 @@ __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 12
     fetch(0);
     for (int it = 0; it < n_it; ++it) {
         __syncthreads();
-        qreg.store(ldsQ, ldsQt, tid);
-        oreg.store(ldsO, ldsOt, tid);
+        qreg.store(ldsQ, tid);
+        oreg.store(ldsO, tid);
         if (tid < 2 * kFT) ldr[tid / kFT][tid & (kFT - 1)] = tid < kFT ? 1.f / rst : -rst;
         __syncthreads();
         const int g = it / nq;
@@ -471,8 +465,8 @@ __global__ __launch_bounds__(64 * kFW) __attribute__((amdgpu_waves_per_eu(D > 12
             pw[v] = keep_if(ok, yi);
             ds[v] = keep_if(ok, dp[v] * yi * rr);
         }
-        mma_cols<D>(ldsOt, l32, hi, pw, dvacc);  // dV^T += dO^T P
-        mma_cols<D>(ldsQt, l32, hi, ds, dkacc);  // dK^T += Q^T dS
+        mma_cols<D, D + 4>(ldsO, l32, hi, pw, dvacc);  // dV^T += dO^T P
+        mma_cols<D, D + 4>(ldsQ, l32, hi, ds, dkacc);  // dK^T += Q^T dS
     }
     if (kj < T_) {
         store_cols<D, PART>(p.dk + b * p.dks[0] + hk * p.dks[1] + kj * p.dks[2], hi, dkacc, 2.f * sc, p.dr);
@@ -500,8 +494,8 @@ int check_common(int B, int Hq, int Hkv, int T, int D, int window_size) {
 // of a D-contraction pairs k-slot g = l / 16 with d = g D / 4 + i, so a
 // lane's operand is one contiguous quarter row; for contractions over a
 // staged tile's 32 rows, MFMA j of 16-row subtile st takes the lane's own C
-// element v = j (row 16 st + 4 g + j) as B, and the A operand's four rows
-// for j = 0..3 are one 16-byte read of the transposed [D][kTP] tile.
+// element v = j (row 16 st + 4 g + j) as B, and its A operand is one
+// 4-byte read of the row-major tile (mma_cols16).
 // ---------------------------------------------------------------------------
 constexpr int kRW = 8;                  // waves per block
 constexpr int kRRows = 16 * kRW;        // rows a block owns (= kFRows)
@@ -535,19 +529,14 @@ struct TileRegs16 {
             }
         }
     }
-    __device__ __forceinline__ void store(float* row, float* tr, int tid) const {
+    // row-major [kFT][D + 4]
+    __device__ __forceinline__ void store(float* row, int tid) const {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int idx = tid + 64 * kRW * i;
             const int r = idx / (D / 4);
             const int c = (idx - r * (D / 4)) * 4;
-            if (row != nullptr) *reinterpret_cast<float4*>(row + r * (D + 4) + c) = v[i];
-            if (tr != nullptr) {
-                tr[(c + 0) * kTP + r] = v[i].x;
-                tr[(c + 1) * kTP + r] = v[i].y;
-                tr[(c + 2) * kTP + r] = v[i].z;
-                tr[(c + 3) * kTP + r] = v[i].w;
-            }
+            *reinterpret_cast<float4*>(row + r * (D + 4) + c) = v[i];
         }
     }
 };
@@ -590,21 +579,23 @@ __device__ __forceinline__ f32x4 mma_rows16(const float* lds_rows, int r0, int l
 }
 
 // acc[dt] (rows d = 16 dt + 4 g + v, column = the lane's row) += A^T(d, r)
-// X(r, col) over the tile's 32 rows, A^T from a transposed [D][kTP] LDS tile
-// and X the lane's own C-layout values x[st][v] (row 16 st + 4 g + v).
+// X(r, col) over the tile's 32 rows, X the lane's own C-layout values
+// x[st][v] (row 16 st + 4 g + v).  A^T is read from the row-major
+// [kFT][D + 4] tile itself: MFMA j of subtile st takes element (16 st + 4 g
+// + j, 16 dt + l16), one 4-byte read per MFMA.  Row 4 g lies 4 g (D + 4) =
+// 16 g floats (mod 64) from row 0, so a read's 64 lanes hit 64 distinct
+// banks, and the tile needs no transposed copy (whose scalar stores, 16-way
+// bank conflicts, stalled every wave between the staging barriers).
 template <int D>
-__device__ __forceinline__ void mma_cols16(const float* lds_tr, int l16, int g, const float (&x)[2][4],
+__device__ __forceinline__ void mma_cols16(const float* lds_rows, int l16, int g, const float (&x)[2][4],
                                            f32x4 (&acc)[D / 16]) {
+    const float* base = lds_rows + 4 * g * (D + 4) + l16;
 #pragma unroll
     for (int dt = 0; dt < D / 16; ++dt) {
-        const float* ar = lds_tr + (dt * 16 + l16) * kTP + 4 * g;
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
-            const float4 a = *reinterpret_cast<const float4*>(ar + 16 * st);
-            acc[dt] = mma16f(a.x, x[st][0], acc[dt]);
-            acc[dt] = mma16f(a.y, x[st][1], acc[dt]);
-            acc[dt] = mma16f(a.z, x[st][2], acc[dt]);
-            acc[dt] = mma16f(a.w, x[st][3], acc[dt]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[dt] = mma16f(base[(16 * st + j) * (D + 4) + 16 * dt], x[st][j], acc[dt]);
         }
     }
 }
@@ -623,7 +614,6 @@ __device__ __forceinline__ void store_cols16(float* row, int g, const f32x4 (&ac
 template <int D, bool EXACT, bool PART>
 __global__ __launch_bounds__(64 * kRW) __attribute__((amdgpu_waves_per_eu(2, 2))) void flash_bwd_dq_f32r16_kernel(F32Params p) {
     __shared__ __attribute__((aligned(16))) float ldsK[kFT * (D + 4)];
-    __shared__ __attribute__((aligned(16))) float ldsKt[D * kTP];
     __shared__ __attribute__((aligned(16))) float ldsV[kFT * (D + 4)];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -687,8 +677,8 @@ __global__ __launch_bounds__(64 * kRW) __attribute__((amdgpu_waves_per_eu(2, 2))
     vreg.template load<PART>(vp, p.vs[2], kv_begin * kFT, T_, tid, p.dr);
     for (int t = kv_begin; t < kv_end; ++t) {
         __syncthreads();
-        kreg.store(ldsK, ldsKt, tid);
-        vreg.store(ldsV, nullptr, tid);
+        kreg.store(ldsK, tid);
+        vreg.store(ldsV, tid);
         __syncthreads();
         if (t + 1 < kv_end) {
             kreg.template load<PART>(kp, p.ks[2], (t + 1) * kFT, T_, tid, p.dr);
@@ -710,7 +700,7 @@ __global__ __launch_bounds__(64 * kRW) __attribute__((amdgpu_waves_per_eu(2, 2))
                 ds[st][v] = keep_if(static_cast<unsigned>(qi - key) < weff, dp[v] * y * rr);
             }
         }
-        mma_cols16<D>(ldsKt, l16, g, ds, acc);  // dQ^T += K^T dS^T
+        mma_cols16<D>(ldsK, l16, g, ds, acc);  // dQ^T += K^T dS^T
     }
     // dS carried without its per-row factor 2 scale / R
     if (qi < T_) store_cols16<D, PART>(p.dq + b * p.dqs[0] + hq * p.dqs[1] + qi * p.dqs[2], g, acc, 2.f * sc * inv_r, p.dr);
@@ -719,9 +709,7 @@ __global__ __launch_bounds__(64 * kRW) __attribute__((amdgpu_waves_per_eu(2, 2))
 template <int D, bool EXACT, bool PART>
 __global__ __launch_bounds__(64 * kRW) __attribute__((amdgpu_waves_per_eu(2, 2))) void flash_bwd_dkdv_f32r16_kernel(F32Params p) {
     __shared__ __attribute__((aligned(16))) float ldsQ[kFT * (D + 4)];
-    __shared__ __attribute__((aligned(16))) float ldsQt[D * kTP];
     __shared__ __attribute__((aligned(16))) float ldsO[kFT * (D + 4)];
-    __shared__ __attribute__((aligned(16))) float ldsOt[D * kTP];
     __shared__ __attribute__((aligned(16))) float ldr[2][kFT];  // [1/R, -delta] of the tile's rows
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -775,8 +763,8 @@ __global__ __launch_bounds__(64 * kRW) __attribute__((amdgpu_waves_per_eu(2, 2))
     fetch(0);
     for (int it = 0; it < n_it; ++it) {
         __syncthreads();
-        qreg.store(ldsQ, ldsQt, tid);
-        oreg.store(ldsO, ldsOt, tid);
+        qreg.store(ldsQ, tid);
+        oreg.store(ldsO, tid);
         if (tid < 2 * kFT) ldr[tid / kFT][tid & (kFT - 1)] = tid < kFT ? 1.f / rst : -rst;
         __syncthreads();
         const int gg = it / nq;
@@ -805,8 +793,8 @@ __global__ __launch_bounds__(64 * kRW) __attribute__((amdgpu_waves_per_eu(2, 2))
                 ds[st][v] = keep_if(ok, dp[v] * yi * rr);
             }
         }
-        mma_cols16<D>(ldsOt, l16, g, pw, dvacc);  // dV^T += dO^T P
-        mma_cols16<D>(ldsQt, l16, g, ds, dkacc);  // dK^T += Q^T dS
+        mma_cols16<D>(ldsO, l16, g, pw, dvacc);  // dV^T += dO^T P
+        mma_cols16<D>(ldsQ, l16, g, ds, dkacc);  // dK^T += Q^T dS
     }
     if (kj < T_) {
         store_cols16<D, PART>(p.dk + b * p.dks[0] + hk * p.dks[1] + kj * p.dks[2], g, dkacc, 2.f * sc, p.dr);
