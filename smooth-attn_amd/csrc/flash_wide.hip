@@ -30,9 +30,9 @@
 // supplies row 4 (l / 16) + (l % 16) / 4, and that + 16, columns 16 dt +
 // 4 (l % 4): inside its 16-lane group lane i then receives column 16 dt + i of
 // those rows).  LDS rows are 512 bytes; logical 16-byte chunk c of row r is
-// stored at c ^ swz(r): r & 15 for row reads (16 rows per cycle), 2 (r & 7)
-// for transposing reads (8 rows x 32 bytes per cycle), and for tiles read
-// both ways fk_swz(r) = 2 (r & 7) | ((r >> 3) & 1), which serves both.
+// stored at c ^ swz(r): r & 15 for row reads, 2 (r & 7) for transposing
+// reads (8 rows x 32 bytes per cycle), and for tiles read both ways
+// fk_swz(r) (below), which serves both.
 #include <algorithm>
 #include <type_traits>
 
@@ -387,10 +387,19 @@ __global__ __launch_bounds__(64 * WideCfg<D>::NW) void flash_fwd_wide_kernel(Wid
 // start at -delta of the lane's query), dS on the VALU, then
 // dQ^T += K^T dS^T with K^T from transposing reads of the K tile.  The K tile
 // is read both ways, so it stores logical chunk c of row r at c ^ fk(r),
-// fk(r) = 2 (r & 7) | ((r >> 3) & 1): injective on 16 consecutive rows (row
-// reads) and, on bits 1-3, on 8 consecutive rows while keeping 32-byte units
-// together (transposing reads); V rows use c ^ (r & 15).
-__device__ __forceinline__ int fk_swz(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
+// fk(r) = 2 ((r & 7) ^ 4 h) | h with h = (r >> 3) & 1.  Transposing reads:
+// bits 1-3 (the 32-byte unit) are injective on 8 consecutive rows and the
+// units stay together.  Row reads: injective on 16 consecutive rows, and
+// the 16-byte reads are served 8 lanes at a time, so rows r and r + 8 must
+// not share an 8-row bank window either: with plain 2 (r & 7) | h they did
+// (the head-dim-256 dQ and dK kernels then spent a quarter of their LDS
+// cycles in bank conflicts), while flipping bit 2 of the unit for rows 8-15
+// puts them in the other half (checked on the device: no conflict for
+// either read).  V rows use c ^ (r & 15).
+__device__ __forceinline__ int fk_swz(int r) {
+    const int h = (r >> 3) & 1;
+    return (((r & 7) ^ (h << 2)) << 1) | h;
+}
 
 // PART: the tensors' head dim p.dr is below D (columns past it read as zeros
 // and are not stored); the kernels with PART false serve dr == D.
