@@ -189,11 +189,11 @@ __device__ __forceinline__ void store_cols(float* row, int hi, const f32x16 (&ac
 // ---------------------------------------------------------------------------
 // Forward
 // ---------------------------------------------------------------------------
-// Tiles that none of a wave's rows sees are skipped at D <= 128; at D = 256
-// (one wave per SIMD, accumulators in AGPRs) the branch made the compiler
-// move every accumulator between AGPRs and VGPRs each tile, so there the
-// masks zero those tiles instead (backward 39.1 -> 31.0 ms on
-// [4,16,4096,256]; at D = 128 skipping is faster, 21.3 vs 24.0 ms).
+// The 32-row kernels skip the tiles that none of a wave's rows sees at
+// D <= 128; in the D = 256 forward (one wave per SIMD, accumulators in AGPRs)
+// the branch made the compiler move every accumulator between AGPRs and
+// VGPRs each tile, so there the masks zero those tiles instead (forward
+// 7.86 -> 7.32 ms on [4,16,4096,256]).  The 16-row kernels always skip them.
 template <int D>
 constexpr bool kSkipIdle = D <= 128;
 
@@ -686,7 +686,7 @@ __global__ __launch_bounds__(64 * kRW) __attribute__((amdgpu_waves_per_eu(2, 2))
         }
         const int k0 = t * kFT;
         const bool active = k0 <= q0 + 15 && !(W > 0 && q0 - (k0 + 31) >= W);
-        if (kSkipIdle<D> && !active) continue;
+        if (!active) continue;
         float ds[2][4];
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
@@ -706,8 +706,15 @@ __global__ __launch_bounds__(64 * kRW) __attribute__((amdgpu_waves_per_eu(2, 2))
     if (qi < T_) store_cols16<D, PART>(p.dq + b * p.dqs[0] + hq * p.dqs[1] + qi * p.dqs[2], g, acc, 2.f * sc * inv_r, p.dr);
 }
 
-template <int D, bool EXACT, bool PART>
+// WHICH: kDkdvBoth (D = 128), or at D = 256, where K, V and both
+// accumulators of 16 keys would not leave room for two waves per SIMD, one
+// kernel for dV (kDkdvV: K and dV in registers) and one for dK (kDkdvK: K, V
+// and dK), each computing S.
+constexpr int kDkdvBoth = 0, kDkdvV = 1, kDkdvK = 2;
+
+template <int D, bool EXACT, bool PART, int WHICH = kDkdvBoth>
 __global__ __launch_bounds__(64 * kRW) __attribute__((amdgpu_waves_per_eu(2, 2))) void flash_bwd_dkdv_f32r16_kernel(F32Params p) {
+    constexpr bool DO_V = WHICH != kDkdvK, DO_K = WHICH != kDkdvV;
     __shared__ __attribute__((aligned(16))) float ldsQ[kFT * (D + 4)];
     __shared__ __attribute__((aligned(16))) float ldsO[kFT * (D + 4)];
     __shared__ __attribute__((aligned(16))) float ldr[2][kFT];  // [1/R, -delta] of the tile's rows
@@ -727,15 +734,15 @@ __global__ __launch_bounds__(64 * kRW) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int wk0 = k_start + 16 * wave;
     const int kj = wk0 + l16;
     const int krow = min(kj, T_ - 1);
-    float kv[D / 4], vv[D / 4];
+    float kv[D / 4], vv[DO_K ? D / 4 : 1];
     load_quarter_row<D, PART>(p.k + b * p.ks[0] + hk * p.ks[1] + krow * p.ks[2], g, kv, p.dr);
-    load_quarter_row<D, PART>(p.v + b * p.vs[0] + hk * p.vs[1] + krow * p.vs[2], g, vv, p.dr);
+    if constexpr (DO_K) load_quarter_row<D, PART>(p.v + b * p.vs[0] + hk * p.vs[1] + krow * p.vs[2], g, vv, p.dr);
 
-    f32x4 dkacc[D / 16], dvacc[D / 16];
+    f32x4 dkacc[DO_K ? D / 16 : 1], dvacc[DO_V ? D / 16 : 1];
 #pragma unroll
     for (int dt = 0; dt < D / 16; ++dt) {
-        dkacc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        dvacc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (DO_K) dkacc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (DO_V) dvacc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
     const int W = p.window;
     const unsigned weff = W > 0 ? static_cast<unsigned>(W) : 0x7FFFFFFFu;
@@ -772,15 +779,17 @@ __global__ __launch_bounds__(64 * kRW) __attribute__((amdgpu_waves_per_eu(2, 2))
         if (it + 1 < n_it) fetch(it + 1);
         // some query of the tile sees some key of the wave
         const bool active = q0 + 31 >= wk0 && !(W > 0 && q0 - (wk0 + 15) >= W) && q0 < T_;
-        if (kSkipIdle<D> && !active) continue;
+        if (!active) continue;
         float pw[2][4], ds[2][4];
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
             const f32x4 s = mma_rows16<D>(ldsQ, 16 * st, l16, g, kv, f32x4{0.f, 0.f, 0.f, 0.f});  // S: rows queries
             f32x4 dp;
+            if constexpr (DO_K) {
 #pragma unroll
-            for (int v = 0; v < 4; ++v) dp[v] = ldr[1][16 * st + 4 * g + v];
-            dp = mma_rows16<D>(ldsO, 16 * st, l16, g, vv, dp);  // dP - delta
+                for (int v = 0; v < 4; ++v) dp[v] = ldr[1][16 * st + 4 * g + v];
+                dp = mma_rows16<D>(ldsO, 16 * st, l16, g, vv, dp);  // dP - delta
+            }
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 const int r = 16 * st + 4 * g + v;
@@ -790,15 +799,17 @@ __global__ __launch_bounds__(64 * kRW) __attribute__((amdgpu_waves_per_eu(2, 2))
                 const float yi = y * ldr[0][r];
                 const bool ok = static_cast<unsigned>(q - kj) < weff && q < T_;
                 pw[st][v] = keep_if(ok, yi);
-                ds[st][v] = keep_if(ok, dp[v] * yi * rr);
+                if constexpr (DO_K) ds[st][v] = keep_if(ok, dp[v] * yi * rr);
             }
         }
-        mma_cols16<D>(ldsO, l16, g, pw, dvacc);  // dV^T += dO^T P
-        mma_cols16<D>(ldsQ, l16, g, ds, dkacc);  // dK^T += Q^T dS
+        if constexpr (DO_V) mma_cols16<D>(ldsO, l16, g, pw, dvacc);  // dV^T += dO^T P
+        if constexpr (DO_K) mma_cols16<D>(ldsQ, l16, g, ds, dkacc);  // dK^T += Q^T dS
     }
     if (kj < T_) {
-        store_cols16<D, PART>(p.dk + b * p.dks[0] + hk * p.dks[1] + kj * p.dks[2], g, dkacc, 2.f * sc, p.dr);
-        store_cols16<D, PART>(p.dv + b * p.dvs[0] + hk * p.dvs[1] + kj * p.dvs[2], g, dvacc, 1.f, p.dr);
+        if constexpr (DO_K)
+            store_cols16<D, PART>(p.dk + b * p.dks[0] + hk * p.dks[1] + kj * p.dks[2], g, dkacc, 2.f * sc, p.dr);
+        if constexpr (DO_V)
+            store_cols16<D, PART>(p.dv + b * p.dvs[0] + hk * p.dvs[1] + kj * p.dvs[2], g, dvacc, 1.f, p.dr);
     }
 }
 
@@ -814,36 +825,38 @@ int launch_fwd_f32_d(const F32Params& prm, int exact, hipStream_t st) {
     return status_from_launch();
 }
 
+// The 16-row kernels (D = 128 and 256): dQ, then dK and dV in one kernel
+// (D = 128) or two (D = 256).
+template <int D, bool EXACT, bool PART>
+void launch_bwd_f32r16(const F32Params& prm, dim3 gq, dim3 gk, hipStream_t st) {
+    flash_bwd_dq_f32r16_kernel<D, EXACT, PART><<<gq, 64 * kRW, 0, st>>>(prm);
+    if constexpr (D <= 128) {
+        flash_bwd_dkdv_f32r16_kernel<D, EXACT, PART><<<gk, 64 * kRW, 0, st>>>(prm);
+    } else {
+        flash_bwd_dkdv_f32r16_kernel<D, EXACT, PART, kDkdvV><<<gk, 64 * kRW, 0, st>>>(prm);
+        flash_bwd_dkdv_f32r16_kernel<D, EXACT, PART, kDkdvK><<<gk, 64 * kRW, 0, st>>>(prm);
+    }
+}
+
 template <int D>
 int launch_bwd_f32_d(const F32Params& prm, int exact, hipStream_t st) {
     const int64_t nq = static_cast<int64_t>((prm.T + kFRows - 1) / kFRows) * prm.B * prm.Hq;
     if (nq * 64 * kFW >= (int64_t(1) << 32)) return SA_ERR_BAD_SHAPE;
     const int64_t nk = nq / prm.G;
     const dim3 gq(static_cast<unsigned>(nq)), gk(static_cast<unsigned>(nk));
-    // Masked builds (PART) except for a full D = 128, whose unmasked build
-    // measured 1% faster; at D = 64 and 256 the masked ones are the faster
-    // even when dr == D (8671 -> 8430 and 8173 -> 7794 us).
-    const bool part = prm.dr != D || D != 128;
-    if constexpr (D == 128) {
-        // 16 rows per wave (at D = 256 the 8-wave blocks would cap each wave at
-        // 256 registers; the 32-row kernels there run one wave per SIMD)
+    if constexpr (D >= 128) {
+        // 16 rows per wave; masked builds (PART) only below the kernel's head dim
         if (nq * 64 * kRW >= (int64_t(1) << 32)) return SA_ERR_BAD_SHAPE;
-        if (exact && part) {
-            flash_bwd_dq_f32r16_kernel<D, true, true><<<gq, 64 * kRW, 0, st>>>(prm);
-            flash_bwd_dkdv_f32r16_kernel<D, true, true><<<gk, 64 * kRW, 0, st>>>(prm);
-        } else if (exact) {
-            flash_bwd_dq_f32r16_kernel<D, true, false><<<gq, 64 * kRW, 0, st>>>(prm);
-            flash_bwd_dkdv_f32r16_kernel<D, true, false><<<gk, 64 * kRW, 0, st>>>(prm);
-        } else if (part) {
-            flash_bwd_dq_f32r16_kernel<D, false, true><<<gq, 64 * kRW, 0, st>>>(prm);
-            flash_bwd_dkdv_f32r16_kernel<D, false, true><<<gk, 64 * kRW, 0, st>>>(prm);
-        } else {
-            flash_bwd_dq_f32r16_kernel<D, false, false><<<gq, 64 * kRW, 0, st>>>(prm);
-            flash_bwd_dkdv_f32r16_kernel<D, false, false><<<gk, 64 * kRW, 0, st>>>(prm);
-        }
+        const bool part = prm.dr != D;
+        if (exact && part) launch_bwd_f32r16<D, true, true>(prm, gq, gk, st);
+        else if (exact) launch_bwd_f32r16<D, true, false>(prm, gq, gk, st);
+        else if (part) launch_bwd_f32r16<D, false, true>(prm, gq, gk, st);
+        else launch_bwd_f32r16<D, false, false>(prm, gq, gk, st);
         return status_from_launch();
     } else {
-        // (D = 128 never builds the 32-row kernels: they would spill there)
+        // 32 rows per wave.  Masked builds (PART) for every head dim: at D = 64
+        // they are the faster even when dr == D (8671 -> 8430 us).
+        const bool part = true;
         if (exact && part) {
             flash_bwd_dq_f32_kernel<D, true, true><<<gq, 64 * kFW, 0, st>>>(prm);
             flash_bwd_dkdv_f32_kernel<D, true, true><<<gk, 64 * kFW, 0, st>>>(prm);
