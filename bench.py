@@ -381,8 +381,9 @@ def bench_next_rows(torch):
       Hq 8 / Hkv 2 and at 1024 with Hq 8 / Hkv 1 (the same bytes), and paged decode over
       fp32 caches (and fp32 q over bf16 and e4m3fn caches) on config 5's layout;
     - the bf16 attention backward over long rows and few KV heads
-      ([1, 32, 8192, 128] with 8 KV heads), with its dK/dV key blocks split
-      over their query tiles (the public path) and unsplit;
+      ([1, 32, 8192, 128] with 8 KV heads, and [1, 16, 16384, 256] with 2),
+      with its dK/dV key blocks split over their query tiles (the public
+      path) and unsplit;
     - RoPE-fused attention forward on config 3's shape (K rotated once by a
       streaming kernel, Q in registers; the time includes the rotation),
       and the RoPE + W_o projection variant (RoPE forward plus one fp32-
@@ -484,6 +485,34 @@ def bench_next_rows(torch):
                                       "bwd_us": round(us_s, 1), "bwd_unsplit_us": round(us_u, 1),
                                       "bwd_frac_bf16_peak": round(fl_l / us_s / 1e6 / BF16_PEAK_TFLOPS, 4),
                                       "bwd_unsplit_frac_bf16_peak": round(fl_l / us_u / 1e6 / BF16_PEAK_TFLOPS, 4)}
+    del q, k, v, do, o, rs, grads, delta
+    torch.cuda.empty_cache()
+
+    # the same at head dim 256: B 1, Hq 16, Hkv 2, T 16384 (256 dV and 256 dK
+    # key blocks of 128 keys), split (the public path) and unsplit
+    Bw, Hw, Hkw, Tw, Dw = 1, 16, 2, 16384, 256
+    q, do = (torch.randn(Bw, Hw, Tw, Dw, generator=gen, device=dev).to(torch.bfloat16) for _ in range(2))
+    k, v = (torch.randn(Bw, Hkw, Tw, Dw, generator=gen, device=dev).to(torch.bfloat16) for _ in range(2))
+    sc = 1 / math.sqrt(Dw)
+    o, rs = sa.kernels._sp2norm_flash_fwd(q, k, v, sc, Hw // Hkw)
+    us_s = med(lambda: sa.kernels._sp2norm_flash_bwd(q, k, v, o, do, rs, sc, Hw // Hkw), iters=10, warmup=2)
+    grads = [torch.empty_like(t) for t in (q, k, v)]
+    delta = torch.empty(Bw, Hw, Tw, device=dev)
+
+    def unsplit_w():
+        st = lib.sa_flash_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(), rs.data_ptr(),
+                              grads[0].data_ptr(), grads[1].data_ptr(), grads[2].data_ptr(), delta.data_ptr(), Bw, Hw,
+                              Hkw, Tw, Dw, *(sa._lib.strides(t) for t in (q, k, v, o, do, *grads)), sc, 0, 0,
+                              sa._lib.SA_BF16, torch.cuda.current_stream().cuda_stream)
+        sa._lib.check(st, "sa_flash_bwd")
+
+    us_u = med(unsplit_w, iters=10, warmup=2)
+    n_split = lib.sa_flash_bwd_workspace_size(Bw, Hw, Hkw, Tw, Dw, 0, sa._lib.SA_BF16) // (Bw * Hkw * Tw * Dw * 4)
+    fl_w = 2.5 * attn_flops(Bw, Hw, Tw, Dw)
+    out["attention_bwd_long_rows_d256"] = {"shape_q": [Bw, Hw, Tw, Dw], "kv_heads": Hkw, "n_split": int(n_split),
+                                           "bwd_us": round(us_s, 1), "bwd_unsplit_us": round(us_u, 1),
+                                           "bwd_frac_bf16_peak": round(fl_w / us_s / 1e6 / BF16_PEAK_TFLOPS, 4),
+                                           "bwd_unsplit_frac_bf16_peak": round(fl_w / us_u / 1e6 / BF16_PEAK_TFLOPS, 4)}
     del q, k, v, do, o, rs, grads, delta
     torch.cuda.empty_cache()
 
@@ -820,7 +849,8 @@ def copy_calibration(torch, nbytes=1 << 30):
 def profile_attention(torch, reps=3):
     """The workload of the attention counter profiles: config 3's forward
     and backward and config 4's fp8 forward, ``reps`` launches each on the
-    bench's inputs, nothing else timed."""
+    bench's inputs, then the head-dim-256 ([4,16,4096,256] bf16) and fp32
+    (config 3's shape) forward and backward, nothing else timed."""
     from smooth_attn import kernels
 
     dev = torch.device("cuda:0")
@@ -841,8 +871,18 @@ def profile_attention(torch, reps=3):
     k8, ks = kernels._quantize_to_fp8_device(k)
     for _ in range(reps):
         kernels._sp2norm_fp8_flash_fwd(q8, k8, v, qs, ks, None, scale, Hq // Hkv)
+    del q, k, v, q8, k8
+    for (B, H, L, D), dt in (((4, 16, 4096, 256), torch.bfloat16), ((4, 32, 4096, 128), torch.float32)):
+        q, k, v, do = (torch.randn(B, H, L, D, generator=gen, device=dev).to(dt) for _ in range(4))
+        scale = 1.0 / math.sqrt(D)
+        for _ in range(reps):
+            o, rs = kernels._sp2norm_flash_fwd(q, k, v, scale)
+        for _ in range(reps):
+            kernels._sp2norm_flash_bwd(q, k, v, o, do, rs, scale)
+        del q, k, v, do, o, rs
     torch.cuda.synchronize()
-    log(f"bench: profile workload done ({reps} launches each of flash fwd, flash bwd, fp8 fwd)")
+    log(f"bench: profile workload done ({reps} launches each of flash fwd, flash bwd, fp8 fwd, "
+        "head-dim-256 and fp32 fwd and bwd)")
 
 
 def main():
@@ -858,7 +898,8 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run three plain 1 GiB device copies (reference point for HBM counters)")
     ap.add_argument("--profile-attention", action="store_true",
-                    help="only launch the attention kernels of configs 3 and 4 a few times (counter profiles)")
+                    help="only launch the attention kernels of configs 3 and 4, head dim 256 and fp32 a few times "
+                         "(counter profiles)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the smooth-attn hot path has no multi-GPU component "
