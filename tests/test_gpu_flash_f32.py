@@ -184,6 +184,16 @@ def test_head_dims_above_128(D, T):
     check_backward(q, k, v, do)
 
 
+@pytest.mark.parametrize("exact", [False, True])
+def test_head_dim_256_backward_gqa_window_blocks(exact):
+    # head dim 256 backward: the 16-row dQ kernel, then separate dV and dK
+    # kernels; GQA 3, with and without a window, three 128-row blocks,
+    # non-contiguous [B, T, H, D] inputs
+    q, k, v, do = inputs(2, 6, 2, 300, 256, seed=61 + exact, layout="bthd")
+    check_backward(q, k, v, do, window=90, exact=exact)
+    check_backward(q, k, v, do, exact=exact)
+
+
 def test_full_size_config3_shape_sampled():
     """fp32 at config 3's shape [4,32,4096,128]: finite outputs and
     gradients everywhere, parity at 1e-5 on one sampled head."""
