@@ -168,7 +168,7 @@ int sa_softmax_fwd_launch_info(const void* x, const void* y, int64_t n_rows,
  * receives sum_j y_ij + 1e-12.  window_size 0 = full causal.  D: bf16 /
  * fp16 any multiple of 8 in 8..512 (kernels built for 32, 64, 128, 256 and
  * 512 read only the first D columns and store only those), fp32 any
- * multiple of 4 in 4..256 (the same way).  exact_math != 0 selects a correctly rounded
+ * multiple of 4 in 4..512 (the same way).  exact_math != 0 selects a correctly rounded
  * sqrt.
  * Replaces _sp2norm_flash_fwd (kernels.py:1912-1931) and its kernel
  * _sp2norm_flash_fwd_with_rowsum_kernel (:1536-1631).

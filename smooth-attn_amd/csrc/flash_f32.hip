@@ -24,6 +24,8 @@
 #include "flash_f32.hpp"
 #include "flash_tiles.hpp"
 
+#include <type_traits>
+
 namespace sa {
 namespace {
 
@@ -479,7 +481,7 @@ bool f32_strides_ok(const int64_t* s) { return s[3] == 1 && s[0] % 4 == 0 && s[1
 
 int check_common(int B, int Hq, int Hkv, int T, int D, int window_size) {
     if (B < 0 || Hq <= 0 || Hkv <= 0 || T < 0 || Hq % Hkv != 0 || window_size < 0) return SA_ERR_BAD_SHAPE;
-    if (D < 4 || D > 256 || D % 4 != 0) return SA_ERR_UNSUPPORTED;
+    if (D < 4 || D > 512 || D % 4 != 0) return SA_ERR_UNSUPPORTED;
     return 0;
 }
 
@@ -611,6 +613,30 @@ __device__ __forceinline__ void store_cols16(float* row, int g, const f32x4 (&ac
     }
 }
 
+// dQ over one staged 32-key tile (K and V rows in LDS) for the wave's 16
+// queries q0 .. q0 + 15 (the lane's query qi); skips tiles none of them sees.
+template <int D, bool EXACT>
+__device__ __forceinline__ void dq_tile16(const float* ldsK, const float* ldsV, int k0, int q0, int qi, int l16,
+                                          int g, const float (&qv)[D / 4], const float (&dov)[D / 4], f32x4 ndl,
+                                          float sc, int W, unsigned weff, f32x4 (&acc)[D / 16]) {
+    const bool active = k0 <= q0 + 15 && !(W > 0 && q0 - (k0 + 31) >= W);
+    if (!active) return;
+    float ds[2][4];
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+        const f32x4 s = mma_rows16<D>(ldsK, 16 * st, l16, g, qv, f32x4{0.f, 0.f, 0.f, 0.f});  // S^T
+        const f32x4 dp = mma_rows16<D>(ldsV, 16 * st, l16, g, dov, ndl);                     // dP^T - delta
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int key = k0 + 16 * st + 4 * g + v;
+            float y, rr;
+            weight_rr<EXACT>(s[v], sc, y, rr);
+            ds[st][v] = keep_if(static_cast<unsigned>(qi - key) < weff, dp[v] * y * rr);
+        }
+    }
+    mma_cols16<D>(ldsK, l16, g, ds, acc);  // dQ^T += K^T dS^T
+}
+
 template <int D, bool EXACT, bool PART>
 __global__ __launch_bounds__(64 * kRW) __attribute__((amdgpu_waves_per_eu(2, 2))) void flash_bwd_dq_f32r16_kernel(F32Params p) {
     __shared__ __attribute__((aligned(16))) float ldsK[kFT * (D + 4)];
@@ -684,23 +710,7 @@ __global__ __launch_bounds__(64 * kRW) __attribute__((amdgpu_waves_per_eu(2, 2))
             kreg.template load<PART>(kp, p.ks[2], (t + 1) * kFT, T_, tid, p.dr);
             vreg.template load<PART>(vp, p.vs[2], (t + 1) * kFT, T_, tid, p.dr);
         }
-        const int k0 = t * kFT;
-        const bool active = k0 <= q0 + 15 && !(W > 0 && q0 - (k0 + 31) >= W);
-        if (!active) continue;
-        float ds[2][4];
-#pragma unroll
-        for (int st = 0; st < 2; ++st) {
-            const f32x4 s = mma_rows16<D>(ldsK, 16 * st, l16, g, qv, f32x4{0.f, 0.f, 0.f, 0.f});  // S^T
-            const f32x4 dp = mma_rows16<D>(ldsV, 16 * st, l16, g, dov, ndl);                     // dP^T - delta
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int key = k0 + 16 * st + 4 * g + v;
-                float y, rr;
-                weight_rr<EXACT>(s[v], sc, y, rr);
-                ds[st][v] = keep_if(static_cast<unsigned>(qi - key) < weff, dp[v] * y * rr);
-            }
-        }
-        mma_cols16<D>(ldsK, l16, g, ds, acc);  // dQ^T += K^T dS^T
+        dq_tile16<D, EXACT>(ldsK, ldsV, t * kFT, q0, qi, l16, g, qv, dov, ndl, sc, W, weff, acc);
     }
     // dS carried without its per-row factor 2 scale / R
     if (qi < T_) store_cols16<D, PART>(p.dq + b * p.dqs[0] + hq * p.dqs[1] + qi * p.dqs[2], g, acc, 2.f * sc * inv_r, p.dr);
@@ -711,6 +721,44 @@ __global__ __launch_bounds__(64 * kRW) __attribute__((amdgpu_waves_per_eu(2, 2))
 // kernel for dV (kDkdvV: K and dV in registers) and one for dK (kDkdvK: K, V
 // and dK), each computing S.
 constexpr int kDkdvBoth = 0, kDkdvV = 1, kDkdvK = 2;
+
+// dK and/or dV (WHICH) over one staged 32-query tile (Q and dO rows in
+// LDS, with its rows' 1/R and -delta in ldr) for the wave's 16 keys wk0 ..
+// wk0 + 15 (the lane's key kj); skips tiles none of them sees.
+template <int D, bool EXACT, int WHICH, int NV, int NK, int NVA>
+__device__ __forceinline__ void kv_tile16(const float* ldsQ, const float* ldsO, const float (&ldr)[2][kFT], int q0,
+                                          int wk0, int kj, int T_, int l16, int g, const float (&kv)[D / 4],
+                                          const float (&vv)[NV], float sc, int W, unsigned weff,
+                                          f32x4 (&dkacc)[NK], f32x4 (&dvacc)[NVA]) {
+    constexpr bool DO_V = WHICH != kDkdvK, DO_K = WHICH != kDkdvV;
+    // some query of the tile sees some key of the wave
+    const bool active = q0 + 31 >= wk0 && !(W > 0 && q0 - (wk0 + 15) >= W) && q0 < T_;
+    if (!active) return;
+    float pw[2][4], ds[2][4];
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+        const f32x4 s = mma_rows16<D>(ldsQ, 16 * st, l16, g, kv, f32x4{0.f, 0.f, 0.f, 0.f});  // S: rows queries
+        f32x4 dp;
+        if constexpr (DO_K) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) dp[v] = ldr[1][16 * st + 4 * g + v];
+            dp = mma_rows16<D>(ldsO, 16 * st, l16, g, vv, dp);  // dP - delta
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int r = 16 * st + 4 * g + v;
+            const int q = q0 + r;
+            float y, rr;
+            weight_rr<EXACT>(s[v], sc, y, rr);
+            const float yi = y * ldr[0][r];
+            const bool ok = static_cast<unsigned>(q - kj) < weff && q < T_;
+            pw[st][v] = keep_if(ok, yi);
+            if constexpr (DO_K) ds[st][v] = keep_if(ok, dp[v] * yi * rr);
+        }
+    }
+    if constexpr (DO_V) mma_cols16<D>(ldsO, l16, g, pw, dvacc);  // dV^T += dO^T P
+    if constexpr (DO_K) mma_cols16<D>(ldsQ, l16, g, ds, dkacc);  // dK^T += Q^T dS
+}
 
 template <int D, bool EXACT, bool PART, int WHICH = kDkdvBoth>
 __global__ __launch_bounds__(64 * kRW) __attribute__((amdgpu_waves_per_eu(2, 2))) void flash_bwd_dkdv_f32r16_kernel(F32Params p) {
@@ -777,33 +825,351 @@ __global__ __launch_bounds__(64 * kRW) __attribute__((amdgpu_waves_per_eu(2, 2))
         const int gg = it / nq;
         const int q0 = (qt_begin + it - gg * nq) * kFT;
         if (it + 1 < n_it) fetch(it + 1);
-        // some query of the tile sees some key of the wave
-        const bool active = q0 + 31 >= wk0 && !(W > 0 && q0 - (wk0 + 15) >= W) && q0 < T_;
-        if (!active) continue;
-        float pw[2][4], ds[2][4];
+        kv_tile16<D, EXACT, WHICH>(ldsQ, ldsO, ldr, q0, wk0, kj, T_, l16, g, kv, vv, sc, W, weff, dkacc, dvacc);
+    }
+    if (kj < T_) {
+        if constexpr (DO_K)
+            store_cols16<D, PART>(p.dk + b * p.dks[0] + hk * p.dks[1] + kj * p.dks[2], g, dkacc, 2.f * sc, p.dr);
+        if constexpr (DO_V)
+            store_cols16<D, PART>(p.dv + b * p.dvs[0] + hk * p.dvs[1] + kj * p.dvs[2], g, dvacc, 1.f, p.dr);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Head dims 256 and 512: the 16-row kernels with each 32-row tile going
+// straight from global memory into LDS (direct-to-LDS buffer loads), so no
+// registers stage it: at D = 256 the register-staged dQ and dK kernels
+// spilled, and at D = 512 a tile takes 64 KB.  D = 256: blocks of 8 waves
+// (two per SIMD) and two LDS stages (the next tile loads while the current
+// one is used; 2 x 66.5 KB); D = 512: blocks of 4 waves (one per SIMD, 512
+// registers with the AGPRs) and one stage (132 KB: the tile's loads wait).
+// The forward at D = 512 has the same shape (the D <= 256 forward keeps the
+// 32-row kernel).
+// ---------------------------------------------------------------------------
+template <int D>
+struct R16Dma {
+    static constexpr int NW = D > 256 ? 4 : 8;      // waves per block
+    static constexpr int ROWS = 16 * NW;            // rows a block owns
+    static constexpr int STAGES = D > 256 ? 1 : 2;  // LDS stages
+    static constexpr int TILE = kFT * (D + 4);      // floats of one staged [kFT][D + 4] tile
+};
+
+// Rows r0 .. r0 + kFT - 1 of a [T][D] fp32 tensor (rows rs floats apart,
+// base wave-uniform) into an LDS tile of rows D + 4 floats apart.  One
+// buffer -> LDS instruction moves 1 KB (64 lanes x 16 bytes): a row at
+// D = 256, half of one at 512; wave w issues instructions w, w + NW, ...
+// Rows at or past T and columns at or past dr (a multiple of 4) read zeros:
+// the instruction's buffer resource ends before them.
+template <int D, int NW>
+__device__ __forceinline__ void dma_tile_f32(const float* base, int64_t rs, int r0, int T, int dr, float* lds,
+                                             int wave, int lane) {
+    constexpr int IPR = D / 256;  // instructions per row
+    static_assert(kFT * IPR % NW == 0, "whole instructions per wave");
+#pragma unroll
+    for (int i = 0; i < kFT * IPR / NW; ++i) {
+        const int j = i * NW + wave;
+        const int r = j / IPR, part = j - r * IPR;
+        const int row = r0 + r;
+        const int cols = min(max(dr - 256 * part, 0), 256);
+        const unsigned char* src = tile_uniform_ptr(reinterpret_cast<const unsigned char*>(
+            base + static_cast<int64_t>(min(row, T - 1)) * rs + 256 * part));
+        tile_dma16(tile_rsrc(src, row < T ? 4 * cols : 0), 16 * lane, lds + r * (D + 4) + 256 * part);
+    }
+}
+
+template <int D, bool EXACT, bool PART>
+__global__ __launch_bounds__(64 * R16Dma<D>::NW) __attribute__((amdgpu_waves_per_eu(R16Dma<D>::NW / 4, R16Dma<D>::NW / 4)))
+void flash_fwd_f32dma_kernel(F32Params p) {
+    using C = R16Dma<D>;
+    static_assert(C::STAGES == 1, "the forward runs at D = 512 only");
+    __shared__ __attribute__((aligned(16))) float lds[2 * C::TILE];  // [K][V]
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4;
+    const int l16 = lane & 15;
+    const int T_ = p.T;
+    const int nqb = (T_ + C::ROWS - 1) / C::ROWS;
+    const int per = p.B * p.Hq;
+    const int step = blockIdx.x / per;  // heaviest (latest) query blocks first
+    const int rest = blockIdx.x - step * per;
+    const int qb = nqb - 1 - step;
+    const int b = rest / p.Hq;
+    const int hq = rest - b * p.Hq;
+    const int hk = hq / p.G;
+    const float* kp = p.k + b * p.ks[0] + hk * p.ks[1];
+    const float* vp = p.v + b * p.vs[0] + hk * p.vs[1];
+
+    const int q0 = qb * C::ROWS + 16 * wave;
+    const int qi = q0 + l16;
+    const int qrow = min(qi, T_ - 1);
+    float qv[D / 4];
+    load_quarter_row<D, PART>(p.q + b * p.qs[0] + hq * p.qs[1] + qrow * p.qs[2], g, qv, p.dr);
+    f32x4 oacc[D / 16];
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) oacc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float ssum = 0.f;
+    const int W = p.window;
+    const unsigned weff = W > 0 ? static_cast<unsigned>(W) : 0x7FFFFFFFu;
+    const int n_kv = (T_ + kFT - 1) / kFT;
+    const int kv_end = min((qb * C::ROWS + C::ROWS + kFT - 1) / kFT, n_kv);
+    const int kv_begin = W > 0 ? max(0, qb * C::ROWS - W + 1) / kFT : 0;
+    const float sc = p.scale;
+    for (int t = kv_begin; t < kv_end; ++t) {
+        if (t > kv_begin) __syncthreads();  // every wave is done with tile t - 1
+        dma_tile_f32<D, C::NW>(kp, p.ks[2], t * kFT, T_, p.dr, lds, wave, lane);
+        dma_tile_f32<D, C::NW>(vp, p.vs[2], t * kFT, T_, p.dr, lds + C::TILE, wave, lane);
+        tile_wait_vmem();
+        __syncthreads();
+        const int k0 = t * kFT;
+        if (!(k0 <= q0 + 15 && !(W > 0 && q0 - (k0 + 31) >= W))) continue;
+        float pw[2][4];
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
-            const f32x4 s = mma_rows16<D>(ldsQ, 16 * st, l16, g, kv, f32x4{0.f, 0.f, 0.f, 0.f});  // S: rows queries
-            f32x4 dp;
-            if constexpr (DO_K) {
-#pragma unroll
-                for (int v = 0; v < 4; ++v) dp[v] = ldr[1][16 * st + 4 * g + v];
-                dp = mma_rows16<D>(ldsO, 16 * st, l16, g, vv, dp);  // dP - delta
-            }
+            // S^T: lane's column = query qi, rows = keys k0 + 16 st + 4 g + v
+            const f32x4 s = mma_rows16<D>(lds, 16 * st, l16, g, qv, f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const int r = 16 * st + 4 * g + v;
-                const int q = q0 + r;
+                const int key = k0 + 16 * st + 4 * g + v;
                 float y, rr;
                 weight_rr<EXACT>(s[v], sc, y, rr);
-                const float yi = y * ldr[0][r];
-                const bool ok = static_cast<unsigned>(q - kj) < weff && q < T_;
-                pw[st][v] = keep_if(ok, yi);
-                if constexpr (DO_K) ds[st][v] = keep_if(ok, dp[v] * yi * rr);
+                y = keep_if(static_cast<unsigned>(qi - key) < weff, y);
+                pw[st][v] = y;
+                ssum += y;
             }
         }
-        if constexpr (DO_V) mma_cols16<D>(ldsO, l16, g, pw, dvacc);  // dV^T += dO^T P
-        if constexpr (DO_K) mma_cols16<D>(ldsQ, l16, g, ds, dkacc);  // dK^T += Q^T dS
+        mma_cols16<D>(lds + C::TILE, l16, g, pw, oacc);  // O^T += V^T P^T
+    }
+    // the query's row sum: its keys lie in lanes l16 + 16 g
+    const float sh = ssum + __shfl_xor(ssum, 16);
+    const float tot = sh + __shfl_xor(sh, 32) + kEps;
+    if (qi < T_) {
+        store_cols16<D, PART>(p.out + b * p.os[0] + hq * p.os[1] + qi * p.os[2], g, oacc, 1.f / tot, p.dr);
+        if (g == 0 && p.row_sums != nullptr) p.row_sums[(static_cast<int64_t>(b) * p.Hq + hq) * T_ + qi] = tot;
+    }
+}
+
+template <int D, bool EXACT, bool PART>
+__global__ __launch_bounds__(64 * R16Dma<D>::NW) __attribute__((amdgpu_waves_per_eu(R16Dma<D>::NW / 4, R16Dma<D>::NW / 4)))
+void flash_bwd_dq_f32dma_kernel(F32Params p) {
+    using C = R16Dma<D>;
+    // stage arrays [K][V]; two arrays so that a tile's LDS reads never wait
+    // for the direct-to-LDS loads filling the other stage
+    __shared__ __attribute__((aligned(16))) float lds0[2 * C::TILE];
+    __shared__ __attribute__((aligned(16))) float lds1[C::STAGES > 1 ? 2 * C::TILE : 4];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4;
+    const int l16 = lane & 15;
+    const int T_ = p.T;
+    const int nqb = (T_ + C::ROWS - 1) / C::ROWS;
+    const int per = p.B * p.Hq;
+    const int step = blockIdx.x / per;
+    const int rest = blockIdx.x - step * per;
+    const int qb = nqb - 1 - step;
+    const int b = rest / p.Hq;
+    const int hq = rest - b * p.Hq;
+    const int hk = hq / p.G;
+    const float* kp = p.k + b * p.ks[0] + hk * p.ks[1];
+    const float* vp = p.v + b * p.vs[0] + hk * p.vs[1];
+
+    const int q0 = qb * C::ROWS + 16 * wave;
+    const int qi = q0 + l16;
+    const int qrow = min(qi, T_ - 1);
+    float qv[D / 4], dov[D / 4];
+    load_quarter_row<D, PART>(p.q + b * p.qs[0] + hq * p.qs[1] + qrow * p.qs[2], g, qv, p.dr);
+    load_quarter_row<D, PART>(p.dout + b * p.dos[0] + hq * p.dos[1] + qrow * p.dos[2], g, dov, p.dr);
+    float dpart = 0.f;
+    {
+        const float* orow = p.o + b * p.os[0] + hq * p.os[1] + qrow * p.os[2];
+#pragma unroll
+        for (int i4 = 0; i4 < D / 16; ++i4) {
+            const int c = g * (D / 4) + 4 * i4;
+            const bool in = !PART || c < p.dr;
+            float4 ov = *reinterpret_cast<const float4*>(orow + (in ? c : 0));
+            if (!in) ov = float4{0.f, 0.f, 0.f, 0.f};
+            dpart = __builtin_fmaf(dov[4 * i4 + 0], ov.x, dpart);
+            dpart = __builtin_fmaf(dov[4 * i4 + 1], ov.y, dpart);
+            dpart = __builtin_fmaf(dov[4 * i4 + 2], ov.z, dpart);
+            dpart = __builtin_fmaf(dov[4 * i4 + 3], ov.w, dpart);
+        }
+    }
+    const float dh = dpart + __shfl_xor(dpart, 16);
+    const float dl = dh + __shfl_xor(dh, 32);
+    const int64_t rbase = (static_cast<int64_t>(b) * p.Hq + hq) * T_;
+    if (qi < T_ && g == 0) p.delta[rbase + qi] = dl;
+    const float inv_r = 1.f / p.rs[rbase + qrow];
+
+    f32x4 acc[D / 16];
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const f32x4 ndl{-dl, -dl, -dl, -dl};
+    const int W = p.window;
+    const unsigned weff = W > 0 ? static_cast<unsigned>(W) : 0x7FFFFFFFu;
+    const int n_kv = (T_ + kFT - 1) / kFT;
+    const int kv_end = min((qb * C::ROWS + C::ROWS + kFT - 1) / kFT, n_kv);
+    const int kv_begin = W > 0 ? max(0, qb * C::ROWS - W + 1) / kFT : 0;
+    const float sc = p.scale;
+
+    auto stage = [&](auto st) -> float* {
+        if constexpr (decltype(st)::value == 0) return lds0;
+        else return lds1;
+    };
+    auto issue = [&](int t, auto st) {
+        float* l = stage(st);
+        dma_tile_f32<D, C::NW>(kp, p.ks[2], t * kFT, T_, p.dr, l, wave, lane);
+        dma_tile_f32<D, C::NW>(vp, p.vs[2], t * kFT, T_, p.dr, l + C::TILE, wave, lane);
+    };
+    auto compute = [&](int t, auto st) {
+        const float* l = stage(st);
+        dq_tile16<D, EXACT>(l, l + C::TILE, t * kFT, q0, qi, l16, g, qv, dov, ndl, sc, W, weff, acc);
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    if constexpr (C::STAGES == 2) {
+        issue(kv_begin, S0{});
+        tile_wait_vmem();
+        __syncthreads();
+        // tile t reads stage (t - kv_begin) & 1 while the other fills with t + 1
+        auto run = [&](int t, auto cur) {
+            if (t + 1 < kv_end) issue(t + 1, std::integral_constant<int, 1 - decltype(cur)::value>{});
+            compute(t, cur);
+            if (t + 1 < kv_end) {
+                tile_wait_vmem();
+                __syncthreads();
+            }
+        };
+        for (int t = kv_begin; t < kv_end; t += 2) {
+            run(t, S0{});
+            if (t + 1 < kv_end) run(t + 1, S1{});
+        }
+    } else {
+        for (int t = kv_begin; t < kv_end; ++t) {
+            if (t > kv_begin) __syncthreads();
+            issue(t, S0{});
+            tile_wait_vmem();
+            __syncthreads();
+            compute(t, S0{});
+        }
+    }
+    if (qi < T_) store_cols16<D, PART>(p.dq + b * p.dqs[0] + hq * p.dqs[1] + qi * p.dqs[2], g, acc, 2.f * sc * inv_r, p.dr);
+}
+
+template <int D, bool EXACT, bool PART, int WHICH>
+__global__ __launch_bounds__(64 * R16Dma<D>::NW) __attribute__((amdgpu_waves_per_eu(R16Dma<D>::NW / 4, R16Dma<D>::NW / 4)))
+void flash_bwd_kv_f32dma_kernel(F32Params p) {
+    using C = R16Dma<D>;
+    constexpr bool DO_V = WHICH != kDkdvK, DO_K = WHICH != kDkdvV;
+    static_assert(WHICH != kDkdvBoth, "dK and dV in separate kernels");
+    __shared__ __attribute__((aligned(16))) float lds0[2 * C::TILE];  // [Q][dO]
+    __shared__ __attribute__((aligned(16))) float lds1[C::STAGES > 1 ? 2 * C::TILE : 4];
+    __shared__ __attribute__((aligned(16))) float ldr[C::STAGES][2][kFT];  // [stage][1/R, -delta]
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4;
+    const int l16 = lane & 15;
+    const int T_ = p.T;
+    const int per = p.B * p.Hkv;
+    const int kb = blockIdx.x / per;  // earliest key blocks (most queries) first
+    const int rest = blockIdx.x - kb * per;
+    const int b = rest / p.Hkv;
+    const int hk = rest - b * p.Hkv;
+
+    const int k_start = kb * C::ROWS;
+    const int wk0 = k_start + 16 * wave;
+    const int kj = wk0 + l16;
+    const int krow = min(kj, T_ - 1);
+    float kv[D / 4], vv[DO_K ? D / 4 : 1];
+    load_quarter_row<D, PART>(p.k + b * p.ks[0] + hk * p.ks[1] + krow * p.ks[2], g, kv, p.dr);
+    if constexpr (DO_K) load_quarter_row<D, PART>(p.v + b * p.vs[0] + hk * p.vs[1] + krow * p.vs[2], g, vv, p.dr);
+    f32x4 dkacc[DO_K ? D / 16 : 1], dvacc[DO_V ? D / 16 : 1];
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) {
+        if constexpr (DO_K) dkacc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (DO_V) dvacc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    const int W = p.window;
+    const unsigned weff = W > 0 ? static_cast<unsigned>(W) : 0x7FFFFFFFu;
+    const int n_qt = (T_ + kFT - 1) / kFT;
+    const int qt_begin = k_start / kFT;
+    const int qt_end = W > 0 ? min(n_qt, (k_start + C::ROWS - 1 + W - 1) / kFT + 1) : n_qt;
+    const int nq = qt_end - qt_begin;  // >= 1 (k_start < T)
+    const int n_it = p.G * nq;
+    const float sc = p.scale;
+
+    auto tile_of = [&](int it, int& hq, int& q0) {
+        const int gg = it / nq;
+        q0 = (qt_begin + it - gg * nq) * kFT;
+        hq = hk * p.G + gg;
+    };
+    auto stage = [&](auto st) -> float* {
+        if constexpr (decltype(st)::value == 0) return lds0;
+        else return lds1;
+    };
+    auto issue = [&](int it, auto st) {
+        int hq, q0;
+        tile_of(it, hq, q0);
+        float* l = stage(st);
+        dma_tile_f32<D, C::NW>(p.q + b * p.qs[0] + hq * p.qs[1], p.qs[2], q0, T_, p.dr, l, wave, lane);
+        dma_tile_f32<D, C::NW>(p.dout + b * p.dos[0] + hq * p.dos[1], p.dos[2], q0, T_, p.dr, l + C::TILE, wave, lane);
+    };
+    // threads 0 .. kFT - 1 load the tile's row sums, the next kFT its delta;
+    // they are staged as 1/R and -delta
+    auto row_value = [&](int it) {
+        int hq, q0;
+        tile_of(it, hq, q0);
+        if (tid >= 2 * kFT) return 0.f;
+        const int64_t idx = (static_cast<int64_t>(b) * p.Hq + hq) * T_ + min(q0 + (tid & (kFT - 1)), T_ - 1);
+        return (tid < kFT ? p.rs : p.delta)[idx];
+    };
+    auto store_rv = [&](int st, float raw) {
+        if (tid < 2 * kFT) ldr[st][tid / kFT][tid & (kFT - 1)] = tid < kFT ? 1.f / raw : -raw;
+    };
+    auto compute = [&](int it, auto st) {
+        int hq, q0;
+        tile_of(it, hq, q0);
+        (void)hq;
+        const float* l = stage(st);
+        kv_tile16<D, EXACT, WHICH>(l, l + C::TILE, ldr[decltype(st)::value], q0, wk0, kj, T_, l16, g, kv, vv, sc, W,
+                                   weff, dkacc, dvacc);
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    if constexpr (C::STAGES == 2) {
+        issue(0, S0{});
+        store_rv(0, row_value(0));
+        tile_wait_vmem();
+        __syncthreads();
+        auto run = [&](int it, auto cur) {
+            constexpr int nxt = 1 - decltype(cur)::value;
+            const bool more = it + 1 < n_it;
+            float rnext = 0.f;
+            if (more) {
+                issue(it + 1, std::integral_constant<int, nxt>{});
+                rnext = row_value(it + 1);
+            }
+            compute(it, cur);
+            if (more) {
+                store_rv(nxt, rnext);
+                tile_wait_vmem();
+                __syncthreads();
+            }
+        };
+        for (int it = 0; it < n_it; it += 2) {
+            run(it, S0{});
+            if (it + 1 < n_it) run(it + 1, S1{});
+        }
+    } else {
+        for (int it = 0; it < n_it; ++it) {
+            if (it > 0) __syncthreads();
+            issue(it, S0{});
+            store_rv(0, row_value(it));
+            tile_wait_vmem();
+            __syncthreads();
+            compute(it, S0{});
+        }
     }
     if (kj < T_) {
         if constexpr (DO_K)
@@ -815,27 +1181,47 @@ __global__ __launch_bounds__(64 * kRW) __attribute__((amdgpu_waves_per_eu(2, 2))
 
 template <int D>
 int launch_fwd_f32_d(const F32Params& prm, int exact, hipStream_t st) {
-    const int64_t nblk = static_cast<int64_t>((prm.T + kFRows - 1) / kFRows) * prm.B * prm.Hq;
-    if (nblk * 64 * kFW >= (int64_t(1) << 32)) return SA_ERR_BAD_SHAPE;
-    const dim3 grid(static_cast<unsigned>(nblk));
-    if (exact)
-        flash_fwd_f32_kernel<D, true><<<grid, 64 * kFW, 0, st>>>(prm);
-    else
-        flash_fwd_f32_kernel<D, false><<<grid, 64 * kFW, 0, st>>>(prm);
-    return status_from_launch();
+    if constexpr (D > 256) {
+        using C = R16Dma<D>;
+        const int64_t nblk = static_cast<int64_t>((prm.T + C::ROWS - 1) / C::ROWS) * prm.B * prm.Hq;
+        if (nblk * 64 * C::NW >= (int64_t(1) << 32)) return SA_ERR_BAD_SHAPE;
+        const dim3 grid(static_cast<unsigned>(nblk));
+        const bool part = prm.dr != D;
+        if (exact && part) flash_fwd_f32dma_kernel<D, true, true><<<grid, 64 * C::NW, 0, st>>>(prm);
+        else if (exact) flash_fwd_f32dma_kernel<D, true, false><<<grid, 64 * C::NW, 0, st>>>(prm);
+        else if (part) flash_fwd_f32dma_kernel<D, false, true><<<grid, 64 * C::NW, 0, st>>>(prm);
+        else flash_fwd_f32dma_kernel<D, false, false><<<grid, 64 * C::NW, 0, st>>>(prm);
+        return status_from_launch();
+    } else {
+        const int64_t nblk = static_cast<int64_t>((prm.T + kFRows - 1) / kFRows) * prm.B * prm.Hq;
+        if (nblk * 64 * kFW >= (int64_t(1) << 32)) return SA_ERR_BAD_SHAPE;
+        const dim3 grid(static_cast<unsigned>(nblk));
+        if (exact)
+            flash_fwd_f32_kernel<D, true><<<grid, 64 * kFW, 0, st>>>(prm);
+        else
+            flash_fwd_f32_kernel<D, false><<<grid, 64 * kFW, 0, st>>>(prm);
+        return status_from_launch();
+    }
 }
 
-// The 16-row kernels (D = 128 and 256): dQ, then dK and dV in one kernel
-// (D = 128) or two (D = 256).
+// The 16-row kernels: D = 128, dQ then dK and dV in one kernel, tiles
+// staged through registers; D = 256 and 512, dQ, dV, dK, tiles loaded
+// straight into LDS.
 template <int D, bool EXACT, bool PART>
-void launch_bwd_f32r16(const F32Params& prm, dim3 gq, dim3 gk, hipStream_t st) {
-    flash_bwd_dq_f32r16_kernel<D, EXACT, PART><<<gq, 64 * kRW, 0, st>>>(prm);
+int launch_bwd_f32r16(const F32Params& prm, hipStream_t st) {
+    constexpr int NW = D <= 128 ? kRW : R16Dma<D>::NW, ROWS = 16 * NW;
+    const int64_t nq = static_cast<int64_t>((prm.T + ROWS - 1) / ROWS) * prm.B * prm.Hq;
+    if (nq * 64 * NW >= (int64_t(1) << 32)) return SA_ERR_BAD_SHAPE;
+    const dim3 gq(static_cast<unsigned>(nq)), gk(static_cast<unsigned>(nq / prm.G));
     if constexpr (D <= 128) {
-        flash_bwd_dkdv_f32r16_kernel<D, EXACT, PART><<<gk, 64 * kRW, 0, st>>>(prm);
+        flash_bwd_dq_f32r16_kernel<D, EXACT, PART><<<gq, 64 * NW, 0, st>>>(prm);
+        flash_bwd_dkdv_f32r16_kernel<D, EXACT, PART><<<gk, 64 * NW, 0, st>>>(prm);
     } else {
-        flash_bwd_dkdv_f32r16_kernel<D, EXACT, PART, kDkdvV><<<gk, 64 * kRW, 0, st>>>(prm);
-        flash_bwd_dkdv_f32r16_kernel<D, EXACT, PART, kDkdvK><<<gk, 64 * kRW, 0, st>>>(prm);
+        flash_bwd_dq_f32dma_kernel<D, EXACT, PART><<<gq, 64 * NW, 0, st>>>(prm);
+        flash_bwd_kv_f32dma_kernel<D, EXACT, PART, kDkdvV><<<gk, 64 * NW, 0, st>>>(prm);
+        flash_bwd_kv_f32dma_kernel<D, EXACT, PART, kDkdvK><<<gk, 64 * NW, 0, st>>>(prm);
     }
+    return status_from_launch();
 }
 
 template <int D>
@@ -846,13 +1232,11 @@ int launch_bwd_f32_d(const F32Params& prm, int exact, hipStream_t st) {
     const dim3 gq(static_cast<unsigned>(nq)), gk(static_cast<unsigned>(nk));
     if constexpr (D >= 128) {
         // 16 rows per wave; masked builds (PART) only below the kernel's head dim
-        if (nq * 64 * kRW >= (int64_t(1) << 32)) return SA_ERR_BAD_SHAPE;
         const bool part = prm.dr != D;
-        if (exact && part) launch_bwd_f32r16<D, true, true>(prm, gq, gk, st);
-        else if (exact) launch_bwd_f32r16<D, true, false>(prm, gq, gk, st);
-        else if (part) launch_bwd_f32r16<D, false, true>(prm, gq, gk, st);
-        else launch_bwd_f32r16<D, false, false>(prm, gq, gk, st);
-        return status_from_launch();
+        if (exact && part) return launch_bwd_f32r16<D, true, true>(prm, st);
+        if (exact) return launch_bwd_f32r16<D, true, false>(prm, st);
+        if (part) return launch_bwd_f32r16<D, false, true>(prm, st);
+        return launch_bwd_f32r16<D, false, false>(prm, st);
     } else {
         // 32 rows per wave.  Masked builds (PART) for every head dim: at D = 64
         // they are the faster even when dr == D (8671 -> 8430 us).
@@ -906,11 +1290,12 @@ int flash_fwd_f32(const void* q, const void* k, const void* v, void* o, float* r
     prm.window = window_size;
     prm.dr = D;
     prm.scale = scale;
-    // head dims 4..256 (multiples of 4) on the kernel for the next of 32, 64, 128, 256
+    // head dims 4..512 (multiples of 4) on the kernel for the next of 32, 64, 128, 256, 512
     if (D <= 32) return launch_fwd_f32_d<32>(prm, exact_math, st);
     if (D <= 64) return launch_fwd_f32_d<64>(prm, exact_math, st);
     if (D <= 128) return launch_fwd_f32_d<128>(prm, exact_math, st);
-    return launch_fwd_f32_d<256>(prm, exact_math, st);
+    if (D <= 256) return launch_fwd_f32_d<256>(prm, exact_math, st);
+    return launch_fwd_f32_d<512>(prm, exact_math, st);
 }
 
 int flash_bwd_f32(const void* q, const void* k, const void* v, const void* o, const void* dout,
@@ -951,7 +1336,8 @@ int flash_bwd_f32(const void* q, const void* k, const void* v, const void* o, co
     if (D <= 32) return launch_bwd_f32_d<32>(prm, exact_math, st);
     if (D <= 64) return launch_bwd_f32_d<64>(prm, exact_math, st);
     if (D <= 128) return launch_bwd_f32_d<128>(prm, exact_math, st);
-    return launch_bwd_f32_d<256>(prm, exact_math, st);
+    if (D <= 256) return launch_bwd_f32_d<256>(prm, exact_math, st);
+    return launch_bwd_f32_d<512>(prm, exact_math, st);
 }
 
 }  // namespace sa

@@ -560,14 +560,14 @@ def _flash_operand(t):
 
 # Head dims the fused-attention kernels are built for, per input dtype.
 _FLASH_KERNEL_DIMS = {torch.bfloat16: (32, 64, 128, 256, 512), torch.float16: (32, 64, 128, 256, 512),
-                      torch.float32: (32, 64, 128, 256)}
+                      torch.float32: (32, 64, 128, 256, 512)}
 
 
 def _kernel_head_dim(D, dtype=None):
     """The head dim the kernels are called with for a head dim D.  bf16 /
     fp16: D rounded up to a multiple of 8 (kernels built for 32, 64, 128,
-    256 and 512), fp32 to a multiple of 4 (kernels built for 32, 64, 128
-    and 256); those kernels take any such D up to their size, reading only
+    256 and 512), fp32 to a multiple of 4 (kernels built for the same head
+    dims); those kernels take any such D up to their size, reading only
     its columns; fp8: the next of the head dims its kernels are built for.  Where it
     differs from D, inputs are zero-padded and outputs sliced: zero columns
     add nothing to q.k, and the padded columns of O, dQ, dK, dV are dropped.
@@ -734,7 +734,7 @@ def _sp2norm_rope_flash_fwd(q, k, v, cos, sin, scale, n_kv_groups=1, window_size
     [B, T, Hq, D] buffer) with 16-byte aligned rows.  16-bit head dims 32,
     64 and 128 rotate Q in registers inside the fused kernel (K once into a
     workspace); fp32, and other head dims that are multiples of 16 (up to
-    512 for 16-bit inputs, 256 for fp32), rotate Q and K by sa_rope_rotate
+    512), rotate Q and K by sa_rope_rotate
     and run the plain fused forward (whose kernels take those head dims
     unpadded, reading only their columns)."""
     _check_same_device("q", q, k=k, v=v, cos=cos, sin=sin, o=o)
@@ -743,10 +743,8 @@ def _sp2norm_rope_flash_fwd(q, k, v, cos, sin, scale, n_kv_groups=1, window_size
     if q.dtype not in (torch.bfloat16, torch.float16, torch.float32) or k.dtype != q.dtype or v.dtype != q.dtype:
         raise ValueError(f"RoPE attention expects bf16, fp16 or fp32 q/k/v of one dtype, got "
                          f"{q.dtype}/{k.dtype}/{v.dtype}")
-    d_max = 256 if q.dtype == torch.float32 else 512
-    if D % 16 or not 16 <= D <= d_max:  # rotate-half pairs 8-element chunks d, d + D/2
-        raise ValueError(f"RoPE attention supports head dims that are multiples of 16 in 16..{d_max} for "
-                         f"{q.dtype}, got {D}")
+    if D % 16 or not 16 <= D <= 512:  # rotate-half pairs 8-element chunks d, d + D/2
+        raise ValueError(f"RoPE attention supports head dims that are multiples of 16 in 16..512, got {D}")
     cos, sin = _rope_tables(cos, sin, T, D)
     if D not in _FLASH_HEAD_DIMS or q.dtype == torch.float32:
         o_full, row_sums = _sp2norm_flash_fwd(_rope_rotate(q, cos, sin), _rope_rotate(k, cos, sin), v, scale,

@@ -167,7 +167,7 @@ def test_paged_decode_noalloc_refuses_what_its_scratch_cannot_hold():
 
 def test_flash_fp32_argument_errors():
     # fp32 q/k/v (SA_F32 = 0): (b, h, t) strides multiples of 4 elements
-    # (16 bytes), D a multiple of 4 up to 256; every check runs before any launch
+    # (16 bytes), D a multiple of 4 up to 512; every check runs before any launch
     lib = _lib.load()
     d = ctypes.c_void_p(16)
     good = (ctypes.c_int64 * 4)(2 * 64 * 64, 64 * 64, 64, 1)
@@ -177,7 +177,8 @@ def test_flash_fp32_argument_errors():
     assert fwd(odd) == -5
     assert fwd(good, ptr=ctypes.c_void_p(20)) == -5  # base not 16-byte aligned
     assert fwd(good, D=50) == -6
-    assert fwd(good, D=264) == -6
+    assert fwd(good, D=516) == -6
+    assert fwd(good, D=264, B=0) == 0 and fwd(good, D=512, B=0) == 0
     assert fwd(good, dt=7) == -3
     assert fwd(good, B=0) == 0
     bwd = lambda s, D=64: lib.sa_flash_bwd(d, d, d, d, d, d, d, d, d, d, 0, 2, 2, 64, D, good, good, good, good,

@@ -174,10 +174,11 @@ def test_public_autograd_fp32():
         assert rel_err(got, want, floor=1e-2) <= TOL
 
 
-@pytest.mark.parametrize("D", [160, 256])
+@pytest.mark.parametrize("D", [160, 256, 384, 512])
 @pytest.mark.parametrize("T", [1, 100, 300])
 def test_head_dims_above_128(D, T):
-    # fp32 runs head dims up to 256 (D = 256 kernels, smaller ones zero-padded)
+    # fp32 runs head dims up to 512 (kernels built for 256 and 512, smaller
+    # head dims masked)
     q, k, v, do = inputs(1, 4, 2, T, D, seed=D + T)
     check_forward(q, k, v)
     check_forward(q, k, v, window=37)
@@ -191,6 +192,15 @@ def test_head_dim_256_backward_gqa_window_blocks(exact):
     # non-contiguous [B, T, H, D] inputs
     q, k, v, do = inputs(2, 6, 2, 300, 256, seed=61 + exact, layout="bthd")
     check_backward(q, k, v, do, window=90, exact=exact)
+    check_backward(q, k, v, do, exact=exact)
+
+
+@pytest.mark.parametrize("exact", [False, True])
+def test_head_dim_512_gqa_window_blocks(exact):
+    # head dim 512: one wave per SIMD, 64-row blocks, one LDS stage
+    q, k, v, do = inputs(1, 4, 2, 200, 512, seed=71 + exact, layout="bthd")
+    check_forward(q, k, v, window=50, exact=exact)
+    check_backward(q, k, v, do, window=50, exact=exact)
     check_backward(q, k, v, do, exact=exact)
 
 

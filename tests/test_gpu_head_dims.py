@@ -133,13 +133,13 @@ def test_head_dims_window_and_exact(D):
     run_case(D, torch.bfloat16, T=130, exact=True, extra=8, seed=D + 2)
 
 
-@pytest.mark.parametrize("D", [4, 20, 36, 48, 100, 132, 200, 252])
+@pytest.mark.parametrize("D", [4, 20, 36, 48, 100, 132, 200, 252, 260, 400, 508])
 def test_fp32_head_dims(D):
     run_case(D, torch.float32, T=150, seed=D + 7)
     run_case(D, torch.float32, T=130, window=33, exact=True, extra=4, seed=D + 8)
 
 
-@pytest.mark.parametrize("D", [32, 64, 128, 256])
+@pytest.mark.parametrize("D", [32, 64, 128, 256, 512])
 def test_built_head_dims_in_wider_rows(D):
     # D equal to a built size, rows of a wider tensor: nothing read or written past D
     run_case(D, torch.bfloat16, T=200, extra=8, seed=D + 3)

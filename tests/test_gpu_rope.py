@@ -166,7 +166,7 @@ def test_rope_proj_head_dim_256():
     assert rel_err(out, ref) <= 1e-2
 
 
-@pytest.mark.parametrize("D", [32, 128, 256])
+@pytest.mark.parametrize("D", [32, 128, 256, 384])
 def test_rope_fp32(D):
     # fp32 q/k/v: rotation in fp32 (sa_rope_rotate), then the fp32-MFMA
     # attention; fp32 output held to 1e-5 against the float64 oracle

@@ -271,14 +271,14 @@ def test_fused_entry_points_refuse_meta_tensors(case, no_library):
 
 
 def test_head_dims_and_page_sizes_checked_before_launch(no_library):
-    # fused attention, fp8 included: 16-bit and fp8 head dims up to 512,
-    # fp32 up to 256 (16-bit: rounded up to a multiple of 8, fp32 of 4; fp8:
+    # fused attention, fp8 included: head dims up to 512 (16-bit: rounded
+    # up to a multiple of 8, fp32 of 4; fp8:
     # zero-padded to a built size, or widened to bf16 above 128); larger head
     # dims, fp64 and mixed dtypes are refused with a clear error; paged
     # decode: power-of-two page sizes only
     mk = lambda shape, dtype: _OnDevice.make(torch.zeros(shape, dtype=dtype), 0)
-    for D, dts, lim in ((257, (torch.float32,), 256), (512, (torch.float32,), 256),
-                        (513, (torch.bfloat16, torch.float16), 512), (1024, (torch.bfloat16, torch.float16), 512)):
+    for D, dts, lim in ((513, (torch.float32, torch.bfloat16, torch.float16), 512),
+                        (1024, (torch.float32, torch.bfloat16, torch.float16), 512)):
         for dt in dts:
             q = mk((1, 2, 8, D), dt)
             with pytest.raises(ValueError, match=f"head dims 1..{lim}"):
