@@ -374,7 +374,8 @@ def bench_paged(torch):
 def bench_next_rows(torch):
     """The rows built after the hot path, each timed by the same protocol:
     - fp32 fused attention forward and backward on config 3's shape (fp32
-      MFMA, against the 157.3 TFLOP/s dense fp32 peak);
+      MFMA, against the 157.3 TFLOP/s dense fp32 peak), and at head dims 256
+      ([4,16,2048,256]) and 512 ([4,8,2048,512]);
     - bf16 attention forward and backward at head dim 256, [4,16,4096,256],
       and at head dim 512, [4,8,4096,512] (both config 3's FLOPs), and paged decode at head dim 256 on config 5's
       layout with Hq 16 / Hkv 4 (config 5's bytes), at head dim 512 with
@@ -432,6 +433,20 @@ def bench_next_rows(torch):
                              "bwd_frac_fp32_peak": round(2.5 * fl / us_b / 1e6 / FP32_PEAK_TFLOPS, 4)}
     del q, k, v, do, o, rs
     torch.cuda.empty_cache()
+
+    # fp32 at head dims 256 and 512 ([4,16,2048,256], [4,8,2048,512]: half of
+    # config 3's FLOPs each; their 16-row kernels load tiles straight into LDS)
+    for Bf, Hf, Lf, Df in ((4, 16, 2048, 256), (4, 8, 2048, 512)):
+        q, k, v, do = (torch.randn(Bf, Hf, Lf, Df, generator=gen, device=dev) for _ in range(4))
+        o, rs = sa.kernels._sp2norm_flash_fwd(q, k, v, 1 / math.sqrt(Df))
+        us_f = med(lambda: sa.kernels._sp2norm_flash_fwd(q, k, v, 1 / math.sqrt(Df)))
+        us_b = med(lambda: sa.kernels._sp2norm_flash_bwd(q, k, v, o, do, rs, 1 / math.sqrt(Df)))
+        flf = attn_flops(Bf, Hf, Lf, Df)
+        out[f"attention_fp32_d{Df}"] = {"shape": [Bf, Hf, Lf, Df], "fwd_us": round(us_f, 1), "bwd_us": round(us_b, 1),
+                                        "fwd_frac_fp32_peak": round(flf / us_f / 1e6 / FP32_PEAK_TFLOPS, 4),
+                                        "bwd_frac_fp32_peak": round(2.5 * flf / us_b / 1e6 / FP32_PEAK_TFLOPS, 4)}
+        del q, k, v, do, o, rs
+        torch.cuda.empty_cache()
 
     # head dim 256 (its own one-wave-per-SIMD kernels): [4,16,4096,256] has config 3's FLOPs
     q, k, v, do = (torch.randn(4, 16, L, 256, generator=gen, device=dev).to(torch.bfloat16) for _ in range(4))
