@@ -1226,10 +1226,6 @@ int launch_bwd_f32r16(const F32Params& prm, hipStream_t st) {
 
 template <int D>
 int launch_bwd_f32_d(const F32Params& prm, int exact, hipStream_t st) {
-    const int64_t nq = static_cast<int64_t>((prm.T + kFRows - 1) / kFRows) * prm.B * prm.Hq;
-    if (nq * 64 * kFW >= (int64_t(1) << 32)) return SA_ERR_BAD_SHAPE;
-    const int64_t nk = nq / prm.G;
-    const dim3 gq(static_cast<unsigned>(nq)), gk(static_cast<unsigned>(nk));
     if constexpr (D >= 128) {
         // 16 rows per wave; masked builds (PART) only below the kernel's head dim
         const bool part = prm.dr != D;
@@ -1240,6 +1236,9 @@ int launch_bwd_f32_d(const F32Params& prm, int exact, hipStream_t st) {
     } else {
         // 32 rows per wave.  Masked builds (PART) for every head dim: at D = 64
         // they are the faster even when dr == D (8671 -> 8430 us).
+        const int64_t nq = static_cast<int64_t>((prm.T + kFRows - 1) / kFRows) * prm.B * prm.Hq;
+        if (nq * 64 * kFW >= (int64_t(1) << 32)) return SA_ERR_BAD_SHAPE;
+        const dim3 gq(static_cast<unsigned>(nq)), gk(static_cast<unsigned>(nq / prm.G));
         const bool part = true;
         if (exact && part) {
             flash_bwd_dq_f32_kernel<D, true, true><<<gq, 64 * kFW, 0, st>>>(prm);
