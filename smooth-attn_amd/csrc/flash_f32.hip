@@ -191,11 +191,11 @@ __device__ __forceinline__ void store_cols(float* row, int hi, const f32x16 (&ac
 // ---------------------------------------------------------------------------
 // Forward
 // ---------------------------------------------------------------------------
-// The 32-row kernels skip the tiles that none of a wave's rows sees at
-// D <= 128; in the D = 256 forward (one wave per SIMD, accumulators in AGPRs)
-// the branch made the compiler move every accumulator between AGPRs and
-// VGPRs each tile, so there the masks zero those tiles instead (forward
-// 7.86 -> 7.32 ms on [4,16,4096,256]).  The 16-row kernels always skip them.
+// The 32-row kernels (head dims up to 128) and the 16-row kernels skip the
+// tiles that none of a wave's rows sees.  (A 32-row forward at D = 256, one
+// wave per SIMD with AGPR accumulators, ran faster without the branch, which
+// made the compiler move every accumulator between AGPRs and VGPRs each
+// tile: 7.86 vs 7.32 ms on [4,16,4096,256].)
 template <int D>
 constexpr bool kSkipIdle = D <= 128;
 
@@ -881,8 +881,10 @@ template <int D, bool EXACT, bool PART>
 __global__ __launch_bounds__(64 * R16Dma<D>::NW) __attribute__((amdgpu_waves_per_eu(R16Dma<D>::NW / 4, R16Dma<D>::NW / 4)))
 void flash_fwd_f32dma_kernel(F32Params p) {
     using C = R16Dma<D>;
-    static_assert(C::STAGES == 1, "the forward runs at D = 512 only");
-    __shared__ __attribute__((aligned(16))) float lds[2 * C::TILE];  // [K][V]
+    // stage arrays [K][V]; two arrays so that a tile's LDS reads never wait
+    // for the direct-to-LDS loads filling the other stage
+    __shared__ __attribute__((aligned(16))) float lds0[2 * C::TILE];
+    __shared__ __attribute__((aligned(16))) float lds1[C::STAGES > 1 ? 2 * C::TILE : 4];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -915,30 +917,63 @@ void flash_fwd_f32dma_kernel(F32Params p) {
     const int kv_end = min((qb * C::ROWS + C::ROWS + kFT - 1) / kFT, n_kv);
     const int kv_begin = W > 0 ? max(0, qb * C::ROWS - W + 1) / kFT : 0;
     const float sc = p.scale;
-    for (int t = kv_begin; t < kv_end; ++t) {
-        if (t > kv_begin) __syncthreads();  // every wave is done with tile t - 1
-        dma_tile_f32<D, C::NW>(kp, p.ks[2], t * kFT, T_, p.dr, lds, wave, lane);
-        dma_tile_f32<D, C::NW>(vp, p.vs[2], t * kFT, T_, p.dr, lds + C::TILE, wave, lane);
-        tile_wait_vmem();
-        __syncthreads();
+    auto stage = [&](auto st) -> float* {
+        if constexpr (decltype(st)::value == 0) return lds0;
+        else return lds1;
+    };
+    auto issue = [&](int t, auto st) {
+        float* l = stage(st);
+        dma_tile_f32<D, C::NW>(kp, p.ks[2], t * kFT, T_, p.dr, l, wave, lane);
+        dma_tile_f32<D, C::NW>(vp, p.vs[2], t * kFT, T_, p.dr, l + C::TILE, wave, lane);
+    };
+    auto compute = [&](int t, auto st) {
+        const float* l = stage(st);
         const int k0 = t * kFT;
-        if (!(k0 <= q0 + 15 && !(W > 0 && q0 - (k0 + 31) >= W))) continue;
+        if (!(k0 <= q0 + 15 && !(W > 0 && q0 - (k0 + 31) >= W))) return;
         float pw[2][4];
 #pragma unroll
-        for (int st = 0; st < 2; ++st) {
-            // S^T: lane's column = query qi, rows = keys k0 + 16 st + 4 g + v
-            const f32x4 s = mma_rows16<D>(lds, 16 * st, l16, g, qv, f32x4{0.f, 0.f, 0.f, 0.f});
+        for (int st16 = 0; st16 < 2; ++st16) {
+            // S^T: lane's column = query qi, rows = keys k0 + 16 st16 + 4 g + v
+            const f32x4 s = mma_rows16<D>(l, 16 * st16, l16, g, qv, f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const int key = k0 + 16 * st + 4 * g + v;
+                const int key = k0 + 16 * st16 + 4 * g + v;
                 float y, rr;
                 weight_rr<EXACT>(s[v], sc, y, rr);
                 y = keep_if(static_cast<unsigned>(qi - key) < weff, y);
-                pw[st][v] = y;
+                pw[st16][v] = y;
                 ssum += y;
             }
         }
-        mma_cols16<D>(lds + C::TILE, l16, g, pw, oacc);  // O^T += V^T P^T
+        mma_cols16<D>(l + C::TILE, l16, g, pw, oacc);  // O^T += V^T P^T
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    if constexpr (C::STAGES == 2) {
+        issue(kv_begin, S0{});
+        tile_wait_vmem();
+        __syncthreads();
+        // tile t reads stage (t - kv_begin) & 1 while the other fills with t + 1
+        auto run = [&](int t, auto cur) {
+            if (t + 1 < kv_end) issue(t + 1, std::integral_constant<int, 1 - decltype(cur)::value>{});
+            compute(t, cur);
+            if (t + 1 < kv_end) {
+                tile_wait_vmem();
+                __syncthreads();
+            }
+        };
+        for (int t = kv_begin; t < kv_end; t += 2) {
+            run(t, S0{});
+            if (t + 1 < kv_end) run(t + 1, S1{});
+        }
+    } else {
+        for (int t = kv_begin; t < kv_end; ++t) {
+            if (t > kv_begin) __syncthreads();  // every wave is done with tile t - 1
+            issue(t, S0{});
+            tile_wait_vmem();
+            __syncthreads();
+            compute(t, S0{});
+        }
     }
     // the query's row sum: its keys lie in lanes l16 + 16 g
     const float sh = ssum + __shfl_xor(ssum, 16);
@@ -1181,7 +1216,7 @@ void flash_bwd_kv_f32dma_kernel(F32Params p) {
 
 template <int D>
 int launch_fwd_f32_d(const F32Params& prm, int exact, hipStream_t st) {
-    if constexpr (D > 256) {
+    if constexpr (D >= 256) {
         using C = R16Dma<D>;
         const int64_t nblk = static_cast<int64_t>((prm.T + C::ROWS - 1) / C::ROWS) * prm.B * prm.Hq;
         if (nblk * 64 * C::NW >= (int64_t(1) << 32)) return SA_ERR_BAD_SHAPE;
