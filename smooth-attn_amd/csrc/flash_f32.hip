@@ -486,62 +486,24 @@ int check_common(int B, int Hq, int Hkv, int T, int D, int window_size) {
 }
 
 // ---------------------------------------------------------------------------
-// Backward with 16 rows per wave (D = 128) on v_mfma_f32_16x16x4_f32
-// (A (16 x 4): lane l holds row l % 16 and k = l / 16; B (4 x 16): k =
-// l / 16, column l % 16; C (16 x 16): column l % 16, rows 4 (l / 16) + v).
-// With 32 rows per wave the D = 128 kernels hold the two operand rows of 32
-// keys (or queries) as 2 x 64 registers plus 2 x 64 accumulators and spill;
-// with 16 rows the same data takes half, in blocks of 8 waves (128 rows, the
-// grids of the 32-row kernels).  The layouts mirror the 32-row ones: MFMA i
-// of a D-contraction pairs k-slot g = l / 16 with d = g D / 4 + i, so a
-// lane's operand is one contiguous quarter row; for contractions over a
-// staged tile's 32 rows, MFMA j of 16-row subtile st takes the lane's own C
-// element v = j (row 16 st + 4 g + j) as B, and its A operand is one
-// 4-byte read of the row-major tile (mma_cols16).
+// 16 rows per wave on v_mfma_f32_16x16x4_f32 (the backward from head dim
+// 128 up, the forward from 256 up): A (16 x 4): lane l holds row l % 16 and
+// k = l / 16; B (4 x 16): k = l / 16, column l % 16; C (16 x 16): column
+// l % 16, rows 4 (l / 16) + v.  With 32 rows per wave the D = 128 backward
+// held the two operand rows of 32 keys (or queries) as 2 x 64 registers
+// plus 2 x 64 accumulators and spilled; 16 rows take half.  The layouts
+// mirror the 32-row ones: MFMA i of a D-contraction pairs k-slot g = l / 16
+// with d = g D / 4 + i, so a lane's operand is one contiguous quarter row;
+// for contractions over a staged tile's 32 rows, MFMA j of 16-row subtile
+// st takes the lane's own C element v = j (row 16 st + 4 g + j) as B, and
+// its A operand is one 4-byte read of the row-major tile (mma_cols16).
 // ---------------------------------------------------------------------------
-constexpr int kRW = 8;                  // waves per block
-constexpr int kRRows = 16 * kRW;        // rows a block owns (= kFRows)
-static_assert(kRRows == kFRows, "the 16-row kernels use the 32-row kernels' grids");
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ f32x4 mma16f(float a, float b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
-
-// One [kFT][D] fp32 tile staged through the registers of a 512-thread block.
-template <int D>
-struct TileRegs16 {
-    static constexpr int PER = kFT * D / 4 / (64 * kRW);  // float4 per thread
-    static_assert(PER >= 1, "a block of 8 waves stages at least one float4 per thread");
-    float4 v[PER];
-    template <bool PART>
-    __device__ __forceinline__ void load(const float* base, int64_t rstride, int r0, int T, int tid, int dr) {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int idx = tid + 64 * kRW * i;
-            const int r = idx / (D / 4);
-            const int c = (idx - r * (D / 4)) * 4;
-            const float* rp = base + static_cast<int64_t>(min(r0 + r, T - 1)) * rstride;
-            if constexpr (PART) {
-                const float4 t = *reinterpret_cast<const float4*>(rp + (c < dr ? c : 0));
-                v[i] = c < dr ? t : float4{0.f, 0.f, 0.f, 0.f};
-            } else {
-                v[i] = *reinterpret_cast<const float4*>(rp + c);
-            }
-        }
-    }
-    // row-major [kFT][D + 4]
-    __device__ __forceinline__ void store(float* row, int tid) const {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int idx = tid + 64 * kRW * i;
-            const int r = idx / (D / 4);
-            const int c = (idx - r * (D / 4)) * 4;
-            *reinterpret_cast<float4*>(row + r * (D + 4) + c) = v[i];
-        }
-    }
-};
 
 // A lane's quarter row: x[i] = row[g D/4 + i], i < D/4 (PART: zero past dr).
 template <int D, bool PART>
@@ -637,84 +599,6 @@ __device__ __forceinline__ void dq_tile16(const float* ldsK, const float* ldsV, 
     mma_cols16<D>(ldsK, l16, g, ds, acc);  // dQ^T += K^T dS^T
 }
 
-template <int D, bool EXACT, bool PART>
-__global__ __launch_bounds__(64 * kRW) __attribute__((amdgpu_waves_per_eu(2, 2))) void flash_bwd_dq_f32r16_kernel(F32Params p) {
-    __shared__ __attribute__((aligned(16))) float ldsK[kFT * (D + 4)];
-    __shared__ __attribute__((aligned(16))) float ldsV[kFT * (D + 4)];
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int g = lane >> 4;
-    const int l16 = lane & 15;
-    const int T_ = p.T;
-    const int nqb = (T_ + kRRows - 1) / kRRows;
-    const int per = p.B * p.Hq;
-    const int step = blockIdx.x / per;
-    const int rest = blockIdx.x - step * per;
-    const int qb = nqb - 1 - step;
-    const int b = rest / p.Hq;
-    const int hq = rest - b * p.Hq;
-    const int hk = hq / p.G;
-    const float* kp = p.k + b * p.ks[0] + hk * p.ks[1];
-    const float* vp = p.v + b * p.vs[0] + hk * p.vs[1];
-
-    const int q0 = qb * kRRows + 16 * wave;
-    const int qi = q0 + l16;
-    const int qrow = min(qi, T_ - 1);
-    float qv[D / 4], dov[D / 4];
-    load_quarter_row<D, PART>(p.q + b * p.qs[0] + hq * p.qs[1] + qrow * p.qs[2], g, qv, p.dr);
-    load_quarter_row<D, PART>(p.dout + b * p.dos[0] + hq * p.dos[1] + qrow * p.dos[2], g, dov, p.dr);
-    // delta = rowsum(dO * O) of this lane's query (lanes l16 + 16 g hold its quarters)
-    float dpart = 0.f;
-    {
-        const float* orow = p.o + b * p.os[0] + hq * p.os[1] + qrow * p.os[2];
-#pragma unroll
-        for (int i4 = 0; i4 < D / 16; ++i4) {
-            const int c = g * (D / 4) + 4 * i4;
-            // PART: columns past dr read column 0 and are zeroed
-            const bool in = !PART || c < p.dr;
-            float4 ov = *reinterpret_cast<const float4*>(orow + (in ? c : 0));
-            if (!in) ov = float4{0.f, 0.f, 0.f, 0.f};
-            dpart = __builtin_fmaf(dov[4 * i4 + 0], ov.x, dpart);
-            dpart = __builtin_fmaf(dov[4 * i4 + 1], ov.y, dpart);
-            dpart = __builtin_fmaf(dov[4 * i4 + 2], ov.z, dpart);
-            dpart = __builtin_fmaf(dov[4 * i4 + 3], ov.w, dpart);
-        }
-    }
-    const float dh = dpart + __shfl_xor(dpart, 16);
-    const float dl = dh + __shfl_xor(dh, 32);
-    const int64_t rbase = (static_cast<int64_t>(b) * p.Hq + hq) * T_;
-    if (qi < T_ && g == 0) p.delta[rbase + qi] = dl;
-    const float inv_r = 1.f / p.rs[rbase + qrow];
-
-    f32x4 acc[D / 16];
-#pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const f32x4 ndl{-dl, -dl, -dl, -dl};
-    const int W = p.window;
-    const unsigned weff = W > 0 ? static_cast<unsigned>(W) : 0x7FFFFFFFu;
-    const int n_kv = (T_ + kFT - 1) / kFT;
-    const int kv_end = min((qb * kRRows + kRRows + kFT - 1) / kFT, n_kv);
-    const int kv_begin = W > 0 ? max(0, qb * kRRows - W + 1) / kFT : 0;
-    const float sc = p.scale;
-
-    TileRegs16<D> kreg, vreg;
-    kreg.template load<PART>(kp, p.ks[2], kv_begin * kFT, T_, tid, p.dr);
-    vreg.template load<PART>(vp, p.vs[2], kv_begin * kFT, T_, tid, p.dr);
-    for (int t = kv_begin; t < kv_end; ++t) {
-        __syncthreads();
-        kreg.store(ldsK, tid);
-        vreg.store(ldsV, tid);
-        __syncthreads();
-        if (t + 1 < kv_end) {
-            kreg.template load<PART>(kp, p.ks[2], (t + 1) * kFT, T_, tid, p.dr);
-            vreg.template load<PART>(vp, p.vs[2], (t + 1) * kFT, T_, tid, p.dr);
-        }
-        dq_tile16<D, EXACT>(ldsK, ldsV, t * kFT, q0, qi, l16, g, qv, dov, ndl, sc, W, weff, acc);
-    }
-    // dS carried without its per-row factor 2 scale / R
-    if (qi < T_) store_cols16<D, PART>(p.dq + b * p.dqs[0] + hq * p.dqs[1] + qi * p.dqs[2], g, acc, 2.f * sc * inv_r, p.dr);
-}
 
 // WHICH: kDkdvBoth (D = 128), or at D = 256, where K, V and both
 // accumulators of 16 keys would not leave room for two waves per SIMD, one
@@ -760,91 +644,17 @@ __device__ __forceinline__ void kv_tile16(const float* ldsQ, const float* ldsO, 
     if constexpr (DO_K) mma_cols16<D>(ldsQ, l16, g, ds, dkacc);  // dK^T += Q^T dS
 }
 
-template <int D, bool EXACT, bool PART, int WHICH = kDkdvBoth>
-__global__ __launch_bounds__(64 * kRW) __attribute__((amdgpu_waves_per_eu(2, 2))) void flash_bwd_dkdv_f32r16_kernel(F32Params p) {
-    constexpr bool DO_V = WHICH != kDkdvK, DO_K = WHICH != kDkdvV;
-    __shared__ __attribute__((aligned(16))) float ldsQ[kFT * (D + 4)];
-    __shared__ __attribute__((aligned(16))) float ldsO[kFT * (D + 4)];
-    __shared__ __attribute__((aligned(16))) float ldr[2][kFT];  // [1/R, -delta] of the tile's rows
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int g = lane >> 4;
-    const int l16 = lane & 15;
-    const int T_ = p.T;
-    const int per = p.B * p.Hkv;
-    const int kb = blockIdx.x / per;  // earliest key blocks (most queries) first
-    const int rest = blockIdx.x - kb * per;
-    const int b = rest / p.Hkv;
-    const int hk = rest - b * p.Hkv;
-
-    const int k_start = kb * kRRows;
-    const int wk0 = k_start + 16 * wave;
-    const int kj = wk0 + l16;
-    const int krow = min(kj, T_ - 1);
-    float kv[D / 4], vv[DO_K ? D / 4 : 1];
-    load_quarter_row<D, PART>(p.k + b * p.ks[0] + hk * p.ks[1] + krow * p.ks[2], g, kv, p.dr);
-    if constexpr (DO_K) load_quarter_row<D, PART>(p.v + b * p.vs[0] + hk * p.vs[1] + krow * p.vs[2], g, vv, p.dr);
-
-    f32x4 dkacc[DO_K ? D / 16 : 1], dvacc[DO_V ? D / 16 : 1];
-#pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt) {
-        if constexpr (DO_K) dkacc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if constexpr (DO_V) dvacc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-    const int W = p.window;
-    const unsigned weff = W > 0 ? static_cast<unsigned>(W) : 0x7FFFFFFFu;
-    const int n_qt = (T_ + kFT - 1) / kFT;
-    const int qt_begin = k_start / kFT;
-    const int qt_end = W > 0 ? min(n_qt, (k_start + kRRows - 1 + W - 1) / kFT + 1) : n_qt;
-    const int nq = qt_end - qt_begin;  // >= 1 (k_start < T)
-    const int n_it = p.G * nq;
-    const float sc = p.scale;
-
-    TileRegs16<D> qreg, oreg;
-    float rst = 0.f;
-    auto fetch = [&](int it) {
-        const int gg = it / nq;
-        const int q0 = (qt_begin + it - gg * nq) * kFT;
-        const int hq = hk * p.G + gg;
-        qreg.template load<PART>(p.q + b * p.qs[0] + hq * p.qs[1], p.qs[2], q0, T_, tid, p.dr);
-        oreg.template load<PART>(p.dout + b * p.dos[0] + hq * p.dos[1], p.dos[2], q0, T_, tid, p.dr);
-        // raw row sum or delta; 1/R or -delta is formed where it is stored
-        if (tid < 2 * kFT) {
-            const int64_t idx = (static_cast<int64_t>(b) * p.Hq + hq) * T_ + min(q0 + (tid & (kFT - 1)), T_ - 1);
-            rst = (tid < kFT ? p.rs : p.delta)[idx];
-        }
-    };
-    fetch(0);
-    for (int it = 0; it < n_it; ++it) {
-        __syncthreads();
-        qreg.store(ldsQ, tid);
-        oreg.store(ldsO, tid);
-        if (tid < 2 * kFT) ldr[tid / kFT][tid & (kFT - 1)] = tid < kFT ? 1.f / rst : -rst;
-        __syncthreads();
-        const int gg = it / nq;
-        const int q0 = (qt_begin + it - gg * nq) * kFT;
-        if (it + 1 < n_it) fetch(it + 1);
-        kv_tile16<D, EXACT, WHICH>(ldsQ, ldsO, ldr, q0, wk0, kj, T_, l16, g, kv, vv, sc, W, weff, dkacc, dvacc);
-    }
-    if (kj < T_) {
-        if constexpr (DO_K)
-            store_cols16<D, PART>(p.dk + b * p.dks[0] + hk * p.dks[1] + kj * p.dks[2], g, dkacc, 2.f * sc, p.dr);
-        if constexpr (DO_V)
-            store_cols16<D, PART>(p.dv + b * p.dvs[0] + hk * p.dvs[1] + kj * p.dvs[2], g, dvacc, 1.f, p.dr);
-    }
-}
 
 // ---------------------------------------------------------------------------
-// Head dims 256 and 512: the 16-row kernels with each 32-row tile going
-// straight from global memory into LDS (direct-to-LDS buffer loads), so no
-// registers stage it: at D = 256 the register-staged dQ and dK kernels
-// spilled, and at D = 512 a tile takes 64 KB.  D = 256: blocks of 8 waves
-// (two per SIMD) and two LDS stages (the next tile loads while the current
-// one is used; 2 x 66.5 KB); D = 512: blocks of 4 waves (one per SIMD, 512
-// registers with the AGPRs) and one stage (132 KB: the tile's loads wait).
-// The forward at D = 512 has the same shape (the D <= 256 forward keeps the
-// 32-row kernel).
+// The 16-row kernels take each 32-row tile straight from global memory
+// into LDS (direct-to-LDS buffer loads), so no registers stage it (staged
+// through registers, the D = 256 dQ and dK kernels spilled; at D = 512 a
+// tile takes 64 KB).  D = 128 and 256: blocks of 8 waves (two per SIMD) and
+// two LDS stages (the next tile loads while the current one is used; 2 x
+// 33.8 / 66.5 KB); D = 512: blocks of 4 waves (one per SIMD, 512 registers
+// with the AGPRs) and one stage (132 KB: the tile's loads wait).  The
+// backward runs them from D = 128 up, the forward from D = 256 up (below
+// that the 32-row forward is as fast or faster).
 // ---------------------------------------------------------------------------
 template <int D>
 struct R16Dma {
@@ -856,14 +666,28 @@ struct R16Dma {
 
 // Rows r0 .. r0 + kFT - 1 of a [T][D] fp32 tensor (rows rs floats apart,
 // base wave-uniform) into an LDS tile of rows D + 4 floats apart.  One
-// buffer -> LDS instruction moves 1 KB (64 lanes x 16 bytes): a row at
-// D = 256, half of one at 512; wave w issues instructions w, w + NW, ...
+// buffer -> LDS instruction moves up to 1 KB (64 lanes x 16 bytes): a row
+// at D <= 256 (at D = 128 with half the lanes), half of one at 512; wave w
+// issues instructions w, w + NW, ...
 // Rows at or past T and columns at or past dr (a multiple of 4) read zeros:
 // the instruction's buffer resource ends before them.
 template <int D, int NW>
 __device__ __forceinline__ void dma_tile_f32(const float* base, int64_t rs, int r0, int T, int dr, float* lds,
                                              int wave, int lane) {
-    constexpr int IPR = D / 256;  // instructions per row
+    if constexpr (D < 256) {
+        // one row per instruction, its first D / 4 lanes active (the LDS rows
+        // are D + 4 floats apart, so two rows are not one contiguous 1 KB)
+#pragma unroll
+        for (int i = 0; i < kFT / NW; ++i) {
+            const int r = i * NW + wave;
+            const int row = r0 + r;
+            const unsigned char* src = tile_uniform_ptr(reinterpret_cast<const unsigned char*>(
+                base + static_cast<int64_t>(min(row, T - 1)) * rs));
+            if (lane < D / 4) tile_dma16(tile_rsrc(src, row < T ? 4 * min(dr, D) : 0), 16 * lane, lds + r * (D + 4));
+        }
+        return;
+    }
+    constexpr int IPR = D / 256 > 0 ? D / 256 : 1;  // instructions per row
     static_assert(kFT * IPR % NW == 0, "whole instructions per wave");
 #pragma unroll
     for (int i = 0; i < kFT * IPR / NW; ++i) {
@@ -1096,7 +920,6 @@ __global__ __launch_bounds__(64 * R16Dma<D>::NW) __attribute__((amdgpu_waves_per
 void flash_bwd_kv_f32dma_kernel(F32Params p) {
     using C = R16Dma<D>;
     constexpr bool DO_V = WHICH != kDkdvK, DO_K = WHICH != kDkdvV;
-    static_assert(WHICH != kDkdvBoth, "dK and dV in separate kernels");
     __shared__ __attribute__((aligned(16))) float lds0[2 * C::TILE];  // [Q][dO]
     __shared__ __attribute__((aligned(16))) float lds1[C::STAGES > 1 ? 2 * C::TILE : 4];
     __shared__ __attribute__((aligned(16))) float ldr[C::STAGES][2][kFT];  // [stage][1/R, -delta]
@@ -1244,15 +1067,14 @@ int launch_fwd_f32_d(const F32Params& prm, int exact, hipStream_t st) {
 // straight into LDS.
 template <int D, bool EXACT, bool PART>
 int launch_bwd_f32r16(const F32Params& prm, hipStream_t st) {
-    constexpr int NW = D <= 128 ? kRW : R16Dma<D>::NW, ROWS = 16 * NW;
+    constexpr int NW = R16Dma<D>::NW, ROWS = 16 * NW;
     const int64_t nq = static_cast<int64_t>((prm.T + ROWS - 1) / ROWS) * prm.B * prm.Hq;
     if (nq * 64 * NW >= (int64_t(1) << 32)) return SA_ERR_BAD_SHAPE;
     const dim3 gq(static_cast<unsigned>(nq)), gk(static_cast<unsigned>(nq / prm.G));
+    flash_bwd_dq_f32dma_kernel<D, EXACT, PART><<<gq, 64 * NW, 0, st>>>(prm);
     if constexpr (D <= 128) {
-        flash_bwd_dq_f32r16_kernel<D, EXACT, PART><<<gq, 64 * NW, 0, st>>>(prm);
-        flash_bwd_dkdv_f32r16_kernel<D, EXACT, PART><<<gk, 64 * NW, 0, st>>>(prm);
+        flash_bwd_kv_f32dma_kernel<D, EXACT, PART, kDkdvBoth><<<gk, 64 * NW, 0, st>>>(prm);
     } else {
-        flash_bwd_dq_f32dma_kernel<D, EXACT, PART><<<gq, 64 * NW, 0, st>>>(prm);
         flash_bwd_kv_f32dma_kernel<D, EXACT, PART, kDkdvV><<<gk, 64 * NW, 0, st>>>(prm);
         flash_bwd_kv_f32dma_kernel<D, EXACT, PART, kDkdvK><<<gk, 64 * NW, 0, st>>>(prm);
     }
