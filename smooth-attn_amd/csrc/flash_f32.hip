@@ -653,8 +653,8 @@ __device__ __forceinline__ void kv_tile16(const float* ldsQ, const float* ldsO, 
 // two LDS stages (the next tile loads while the current one is used; 2 x
 // 33.8 / 66.5 KB); D = 512: blocks of 4 waves (one per SIMD, 512 registers
 // with the AGPRs) and one stage (132 KB: the tile's loads wait).  The
-// backward runs them from D = 128 up, the forward from D = 256 up (below
-// that the 32-row forward is as fast or faster).
+// backward runs them from D = 64 up, the forward from D = 256 up (below
+// that the 32-row kernels are as fast or faster).
 // ---------------------------------------------------------------------------
 template <int D>
 struct R16Dma {
@@ -662,12 +662,15 @@ struct R16Dma {
     static constexpr int ROWS = 16 * NW;            // rows a block owns
     static constexpr int STAGES = D > 256 ? 1 : 2;  // LDS stages
     static constexpr int TILE = kFT * (D + 4);      // floats of one staged [kFT][D + 4] tile
+    // waves per SIMD allowed: at D = 64 the registers and LDS of four fit
+    // (the backward 8.04 -> 7.54-7.73 ms on [4,32,4096,64] against two)
+    static constexpr int MAX_WAVES = D <= 64 ? 4 : NW / 4;
 };
 
 // Rows r0 .. r0 + kFT - 1 of a [T][D] fp32 tensor (rows rs floats apart,
 // base wave-uniform) into an LDS tile of rows D + 4 floats apart.  One
 // buffer -> LDS instruction moves up to 1 KB (64 lanes x 16 bytes): a row
-// at D <= 256 (at D = 128 with half the lanes), half of one at 512; wave w
+// at D <= 256 (below 256 with D / 4 lanes), half of one at 512; wave w
 // issues instructions w, w + NW, ...
 // Rows at or past T and columns at or past dr (a multiple of 4) read zeros:
 // the instruction's buffer resource ends before them.
@@ -702,7 +705,7 @@ __device__ __forceinline__ void dma_tile_f32(const float* base, int64_t rs, int 
 }
 
 template <int D, bool EXACT, bool PART>
-__global__ __launch_bounds__(64 * R16Dma<D>::NW) __attribute__((amdgpu_waves_per_eu(R16Dma<D>::NW / 4, R16Dma<D>::NW / 4)))
+__global__ __launch_bounds__(64 * R16Dma<D>::NW) __attribute__((amdgpu_waves_per_eu(R16Dma<D>::NW / 4, R16Dma<D>::MAX_WAVES)))
 void flash_fwd_f32dma_kernel(F32Params p) {
     using C = R16Dma<D>;
     // stage arrays [K][V]; two arrays so that a tile's LDS reads never wait
@@ -809,7 +812,7 @@ void flash_fwd_f32dma_kernel(F32Params p) {
 }
 
 template <int D, bool EXACT, bool PART>
-__global__ __launch_bounds__(64 * R16Dma<D>::NW) __attribute__((amdgpu_waves_per_eu(R16Dma<D>::NW / 4, R16Dma<D>::NW / 4)))
+__global__ __launch_bounds__(64 * R16Dma<D>::NW) __attribute__((amdgpu_waves_per_eu(R16Dma<D>::NW / 4, R16Dma<D>::MAX_WAVES)))
 void flash_bwd_dq_f32dma_kernel(F32Params p) {
     using C = R16Dma<D>;
     // stage arrays [K][V]; two arrays so that a tile's LDS reads never wait
@@ -916,7 +919,7 @@ void flash_bwd_dq_f32dma_kernel(F32Params p) {
 }
 
 template <int D, bool EXACT, bool PART, int WHICH>
-__global__ __launch_bounds__(64 * R16Dma<D>::NW) __attribute__((amdgpu_waves_per_eu(R16Dma<D>::NW / 4, R16Dma<D>::NW / 4)))
+__global__ __launch_bounds__(64 * R16Dma<D>::NW) __attribute__((amdgpu_waves_per_eu(R16Dma<D>::NW / 4, R16Dma<D>::MAX_WAVES)))
 void flash_bwd_kv_f32dma_kernel(F32Params p) {
     using C = R16Dma<D>;
     constexpr bool DO_V = WHICH != kDkdvK, DO_K = WHICH != kDkdvV;
@@ -1083,7 +1086,7 @@ int launch_bwd_f32r16(const F32Params& prm, hipStream_t st) {
 
 template <int D>
 int launch_bwd_f32_d(const F32Params& prm, int exact, hipStream_t st) {
-    if constexpr (D >= 128) {
+    if constexpr (D >= 64) {
         // 16 rows per wave; masked builds (PART) only below the kernel's head dim
         const bool part = prm.dr != D;
         if (exact && part) return launch_bwd_f32r16<D, true, true>(prm, st);
@@ -1091,8 +1094,9 @@ int launch_bwd_f32_d(const F32Params& prm, int exact, hipStream_t st) {
         if (part) return launch_bwd_f32r16<D, false, true>(prm, st);
         return launch_bwd_f32r16<D, false, false>(prm, st);
     } else {
-        // 32 rows per wave.  Masked builds (PART) for every head dim: at D = 64
-        // they are the faster even when dr == D (8671 -> 8430 us).
+        // 32 rows per wave (D = 32: the 16-row kernels ran 4.43 vs 4.13 ms on
+        // [4,32,4096,32]).  Masked builds (PART) for every head dim: at D = 64
+        // they were the faster even when dr == D (8671 -> 8430 us).
         const int64_t nq = static_cast<int64_t>((prm.T + kFRows - 1) / kFRows) * prm.B * prm.Hq;
         if (nq * 64 * kFW >= (int64_t(1) << 32)) return SA_ERR_BAD_SHAPE;
         const dim3 gq(static_cast<unsigned>(nq)), gk(static_cast<unsigned>(nq / prm.G));
