@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "smooth_attn_amd.h"
 
 namespace sa {
@@ -111,6 +113,27 @@ __device__ __forceinline__ uint32_t pack2<bf16>(float lo, float hi) {
 template <>
 __device__ __forceinline__ uint32_t pack2<f16>(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo, hi}), f16x2));
+}
+
+// Bytes 2 sel and 2 sel + 1 of a word of e4m3fn codes as two 16-bit values
+// (v_cvt_scalef32_pk_{bf16,f16}_fp8 with scale 1: exact, since every
+// e4m3fn value, subnormals included, is a bf16 and an f16 value).
+template <typename T, bool SEL>
+__device__ __forceinline__ uint32_t widen2_e4m3(uint32_t word) {
+    if constexpr (std::is_same_v<T, bf16>)
+        return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(word, 1.0f, SEL));
+    else
+        return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(word, 1.0f, SEL));
+}
+
+// 16 e4m3fn values (one 16-byte word) as 16 values of T (two words), exact:
+// elements 0-7 in lo, 8-15 in hi.
+template <typename T>
+__device__ __forceinline__ void widen_e4m3x16(u32x4 in, u32x4& lo, u32x4& hi) {
+    lo = u32x4{widen2_e4m3<T, false>(in.x), widen2_e4m3<T, true>(in.x), widen2_e4m3<T, false>(in.y),
+               widen2_e4m3<T, true>(in.y)};
+    hi = u32x4{widen2_e4m3<T, false>(in.z), widen2_e4m3<T, true>(in.z), widen2_e4m3<T, false>(in.w),
+               widen2_e4m3<T, true>(in.w)};
 }
 
 // Load 16 bytes into words[0..3] / store words[0..3] as 16 bytes.

@@ -103,20 +103,6 @@ __device__ __forceinline__ f32x16 mma_fp8(i32x8 a, i32x8 b, f32x16 c, int ea, in
     return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, ea, 0, eb);
 }
 
-// Widen 16 e4m3fn values (one 16-byte word) to 16 bf16 / f16 values (two words).
-template <typename T>
-__device__ __forceinline__ void widen_fp8x16(u32x4 in, u32x4& lo, u32x4& hi) {
-    uint32_t out[8];
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-        const int word = static_cast<int>(in[w]);
-        out[2 * w] = pack2<T>(__builtin_amdgcn_cvt_f32_fp8(word, 0), __builtin_amdgcn_cvt_f32_fp8(word, 1));
-        out[2 * w + 1] = pack2<T>(__builtin_amdgcn_cvt_f32_fp8(word, 2), __builtin_amdgcn_cvt_f32_fp8(word, 3));
-    }
-    lo = u32x4{out[0], out[1], out[2], out[3]};
-    hi = u32x4{out[4], out[5], out[6], out[7]};
-}
-
 // Rotate-half RoPE of one pair of 8-element chunks, a = x[d .. d+7] and
 // b = x[d + D/2 .. +7] with d < D/2 (reference kernels.py:2150-2158):
 //   a' = a cos - b sin,  b' = b cos + a sin   (fp32, rounded to T).
@@ -436,7 +422,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_kernel(FlashParams p) {
                     // 16 fp8 values = LDS chunks 2c, 2c + 1 (swz_v is even, so they stay adjacent)
                     unsigned char* dst = ldsVb + buf * Gm::VT + row * Gm::VROWB + ((2 * c) ^ Gm::swz_v(row)) * 16;
                     u32x4 lo, hi16;
-                    widen_fp8x16<T>(vst[i], lo, hi16);
+                    widen_e4m3x16<T>(vst[i], lo, hi16);
                     *reinterpret_cast<u32x4*>(dst) = lo;
                     *reinterpret_cast<u32x4*>(dst + 16) = hi16;
                 }

@@ -116,19 +116,6 @@ struct PagedTypes {
     static constexpr bool SPLIT_P = !SAME16;
 };
 
-// 16 e4m3fn values (one 16-byte word) as 16 bf16 values (two words), exact.
-__device__ __forceinline__ void widen_e4m3(u32x4 in, u32x4& lo, u32x4& hi) {
-    uint32_t out[8];
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-        const int word = static_cast<int>(in[w]);
-        out[2 * w] = pack2<bf16>(__builtin_amdgcn_cvt_f32_fp8(word, 0), __builtin_amdgcn_cvt_f32_fp8(word, 1));
-        out[2 * w + 1] = pack2<bf16>(__builtin_amdgcn_cvt_f32_fp8(word, 2), __builtin_amdgcn_cvt_f32_fp8(word, 3));
-    }
-    lo = u32x4{out[0], out[1], out[2], out[3]};
-    hi = u32x4{out[4], out[5], out[6], out[7]};
-}
-
 // hi = bf16(a), bf16(b) packed; lo = the same of the remainders.
 __device__ __forceinline__ void split2_bf16(float a, float b, uint32_t& hi, uint32_t& lo) {
     hi = pack2<bf16>(a, b);
@@ -328,10 +315,10 @@ __global__ __launch_bounds__(64 * WPB) void paged_partial_kernel(PagedParams p) 
                     if constexpr (std::is_same_v<CE, fp8e4>) {
                         // 16 e4m3fn values -> 16 bf16 (32 bytes)
                         u32x4 a, c;
-                        widen_e4m3(kbuf[i], a, c);
+                        widen_e4m3x16<bf16>(kbuf[i], a, c);
                         *reinterpret_cast<u32x4*>(ldsK + tok * RS + lane_col) = a;
                         *reinterpret_cast<u32x4*>(ldsK + tok * RS + lane_col + 8) = c;
-                        widen_e4m3(vbuf[i], a, c);
+                        widen_e4m3x16<bf16>(vbuf[i], a, c);
                         *reinterpret_cast<u32x4*>(ldsV + tok * RSV + lane_col) = a;
                         *reinterpret_cast<u32x4*>(ldsV + tok * RSV + lane_col + 8) = c;
                     } else if constexpr (!SC) {

@@ -194,3 +194,24 @@ def test_paged_fp8_cache_c_abi_and_append():
     ref = eager.paged_decode_eager(q.double(), full_k.double(), full_v.double(), table, lens)
     share, steps = bf16_match(out, ref)
     assert steps <= 1.0 + 1e-6 and share >= 0.97
+
+
+@pytest.mark.parametrize("qdt", [torch.float32, torch.bfloat16])
+def test_e4m3fn_codes_widen_exactly(qdt):
+    # every finite e4m3fn code (subnormals and both zeros included) as a V
+    # element of a one-token context: the output is V itself (weight / row
+    # sum = 1 up to the 2^-16 of the hi + lo split, far below the distance
+    # of a 4-bit value from a bf16 rounding midpoint), so it must equal the
+    # code widened to bf16 (values compared: the accumulation turns -0 into
+    # +0); K is zero, so every score is 0
+    B, Hq, Hkv, D, P = 2, 2, 2, 64, 16
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0  # the two NaN codes
+    v = codes.view(torch.float8_e4m3fn).reshape(B, Hkv, 1, D)
+    k = torch.zeros(B, Hkv, 1, D, dtype=torch.uint8).view(torch.float8_e4m3fn)
+    kc, vc, table, _ = paging.build_paged_cache(k, v, page_size=P)
+    q = torch.randn(B, Hq, 1, D, generator=_g(3)).to(qdt)
+    lens = torch.ones(B, dtype=torch.int32)
+    out = decode(q, kc, vc, table, lens, P)
+    want = v.reshape(B, Hkv, D).to(torch.bfloat16)
+    assert torch.equal(out.cpu(), want)
