@@ -341,7 +341,7 @@ int64_t sa_paged_decode_workspace_size(int B, int Hq, int D, int max_pages,
  * K_t = k_cache[block_table[b, t/P], h/(Hq/Hkv), t%P].  dtype:
  * SA_PAGED_DTYPES(q type, cache type), or one code for both; supported
  * pairs: bf16 / bf16, fp16 / fp16, fp32 / fp32, fp32 q over bf16, fp16 or
- * e4m3fn caches (the reference upcasts q, K and V to fp32,
+ * e4m3fn caches, bf16 q over e4m3fn caches (the reference upcasts q, K and V to fp32,
  * kernels.py:2716-2717, :2746, :2765; mixed pairs and fp32 run their
  * products as bf16 hi + lo splits, about 16 significant bits; e4m3fn values
  * widen to bf16 exactly, unscaled, and need D a multiple of 16).  Row strides (element units)

@@ -589,12 +589,14 @@ int launch_per(int B, int Hq, int Hkv, int max_pages, int page_size) {
 
 // q and cache types of a decode's dtype argument (SA_PAGED_DTYPES, or one
 // code for both); false for unsupported pairs.  Supported: bf16 / bf16,
-// fp16 / fp16, and fp32 q over fp32, bf16 or fp16 caches.
+// fp16 / fp16, fp32 q over fp32, bf16, fp16 or e4m3fn caches, and bf16 q
+// over e4m3fn caches (q is then a plain bf16 operand, no lo part).
 bool paged_types(int dtype, int& qt, int& ct) {
     qt = dtype & 0xFF;
     ct = (dtype >> 8) == 0 ? qt : (dtype >> 8) - 1;
     if (dtype < 0 || (dtype >> 16) != 0) return false;
     if (qt == ct) return qt == SA_BF16 || qt == SA_F16 || qt == SA_F32;
+    if (qt == SA_BF16) return ct == SA_FP8_E4M3FN;
     return qt == SA_F32 && (ct == SA_BF16 || ct == SA_F16 || ct == SA_FP8_E4M3FN);
 }
 
@@ -680,6 +682,7 @@ int run_paged(const void* q, const void* k_cache, const void* v_cache, void* out
     const int dp = D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : D <= 256 ? 256 : D <= 512 ? 512 : 1024;
     int qt, ct;
     paged_types(dtype, qt, ct);
+    if (qt == SA_BF16 && ct == SA_FP8_E4M3FN) return launch_paged_d<bf16, fp8e4>(dp, prm, st);
     if (qt == SA_BF16) return launch_paged_d<bf16, bf16>(dp, prm, st);
     if (qt == SA_F16) return launch_paged_d<f16, f16>(dp, prm, st);
     if (ct == SA_BF16) return launch_paged_d<float, bf16>(dp, prm, st);

@@ -989,12 +989,15 @@ def _paged_dtype_code(q_dtype, k_dtype, v_dtype):
     (kernels.py:2716-2717, :2746, :2765): here q may be fp32, bf16, fp16 or
     e4m3fn and the caches fp32, bf16, fp16 or e4m3fn (unscaled values, as
     the reference reads them) of one dtype; a q whose dtype differs from the
-    caches' runs as fp32 (an exact conversion)."""
+    caches' runs as fp32 (an exact conversion), except a bf16 q over e4m3fn
+    caches, which the kernels take as it is."""
     if (q_dtype not in _PAGED_CACHE_DTYPES or k_dtype not in _PAGED_CACHE_DTYPES or v_dtype != k_dtype):
         raise ValueError("paged decode expects fp32, bf16, fp16 or e4m3fn q and fp32, bf16, fp16 or e4m3fn caches "
                          f"of one dtype, got q {q_dtype}, k_cache {k_dtype}, v_cache {v_dtype}")
     if q_dtype == k_dtype and q_dtype in _PAGED_DTYPES:
         return _DTYPE_CODE[q_dtype]
+    if q_dtype == torch.bfloat16 and k_dtype == torch.float8_e4m3fn:
+        return _lib.paged_dtypes(_lib.SA_BF16, _lib.SA_FP8_E4M3FN)  # bf16 q as it is
     return _lib.paged_dtypes(_lib.SA_F32, _CACHE_CODE[k_dtype])
 
 
@@ -1022,7 +1025,7 @@ def sp2norm_paged_attention(q, k_cache, v_cache, block_table, context_lens, *, s
     _check_same_device("q", q, k_cache=k_cache, v_cache=v_cache, block_table=block_table,
                        context_lens=context_lens)
     code = _paged_dtype_code(q.dtype, k_cache.dtype, v_cache.dtype)
-    if q.dtype != k_cache.dtype or q.dtype == torch.float8_e4m3fn:
+    if (code & 0xFF) == _lib.SA_F32 and q.dtype != torch.float32:
         q = q.float()  # exact; fp32 q runs over fp32, bf16, fp16 or e4m3fn caches
     if k_cache.dtype == torch.float8_e4m3fn and D % 16:
         raise ValueError(f"paged decode over e4m3fn caches needs a head dim that is a multiple of 16, got {D}")

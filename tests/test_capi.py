@@ -284,8 +284,9 @@ def test_flash_16bit_head_dims():
 
 def test_paged_decode_dtype_pairs():
     # SA_PAGED_DTYPES(q, cache): fp32 q over fp32 / bf16 / fp16 / e4m3fn
-    # caches, or one 16-bit type for both; other pairs are refused before any
-    # HIP call, and e4m3fn caches need D a multiple of 16
+    # caches, bf16 q over e4m3fn caches, or one 16-bit type for both; other
+    # pairs are refused before any HIP call, and e4m3fn caches need D a
+    # multiple of 16
     lib = _lib.load()
     dummy = ctypes.c_void_p(16)
     D = 64
@@ -294,7 +295,7 @@ def test_paged_decode_dtype_pairs():
     pd = _lib.paged_dtypes
     assert pd(_lib.SA_F32, _lib.SA_BF16) == 0 | (3 << 8)
     for code in (pd(_lib.SA_BF16, _lib.SA_F32), pd(_lib.SA_BF16, _lib.SA_F16), pd(_lib.SA_F16, _lib.SA_BF16),
-                 pd(_lib.SA_F16, _lib.SA_F32), _lib.SA_FP8_E4M3FN, pd(_lib.SA_BF16, _lib.SA_FP8_E4M3FN), 7,
+                 pd(_lib.SA_F16, _lib.SA_F32), _lib.SA_FP8_E4M3FN, pd(_lib.SA_F16, _lib.SA_FP8_E4M3FN), 7,
                  1 << 16, -1):
         st = lib.sa_paged_decode(dummy, dummy, dummy, dummy, dummy, dummy, 2, 8, 2, D, 16, 4, 8,
                                  s4, s4, s4, o, 4, 0.1, code, dummy, 1 << 30, None)
@@ -304,9 +305,10 @@ def test_paged_decode_dtype_pairs():
         assert st == -3, code
     s40 = (ctypes.c_int64 * 4)(8 * 40, 40, 40, 1)
     o40 = (ctypes.c_int64 * 3)(8 * 40, 40, 1)
-    st = lib.sa_paged_decode(dummy, dummy, dummy, dummy, dummy, dummy, 2, 8, 2, 40, 16, 4, 8, s40, s40, s40, o40,
-                             4, 0.1, pd(_lib.SA_F32, _lib.SA_FP8_E4M3FN), dummy, 1 << 30, None)
-    assert st == -6  # SA_ERR_UNSUPPORTED
+    for q_type in (_lib.SA_F32, _lib.SA_BF16):
+        st = lib.sa_paged_decode(dummy, dummy, dummy, dummy, dummy, dummy, 2, 8, 2, 40, 16, 4, 8, s40, s40, s40,
+                                 o40, 4, 0.1, pd(q_type, _lib.SA_FP8_E4M3FN), dummy, 1 << 30, None)
+        assert st == -6, q_type  # SA_ERR_UNSUPPORTED (an accepted pair, refused for D % 16)
     # fp32 rows need element strides that are multiples of 4, 16-bit rows of 8
     s_odd = (ctypes.c_int64 * 4)(8 * 68, 68, 68, 1)
     st = lib.sa_paged_decode(dummy, dummy, dummy, dummy, dummy, dummy, 2, 8, 2, D, 16, 4, 8,

@@ -215,3 +215,24 @@ def test_e4m3fn_codes_widen_exactly(qdt):
     out = decode(q, kc, vc, table, lens, P)
     want = v.reshape(B, Hkv, D).to(torch.bfloat16)
     assert torch.equal(out.cpu(), want)
+
+
+@pytest.mark.parametrize("D", [64, 128, 1024])
+def test_bf16_q_over_e4m3fn_equals_fp32_q(D):
+    # a bf16 q over e4m3fn caches runs as it is (no lo part); widened to fp32
+    # it splits into the same hi and a zero lo, so the two decodes agree bit
+    # for bit
+    q, kc, vc, table, lens = make(3, 8, 2, 333, D, 16, torch.bfloat16, torch.float8_e4m3fn, seed=D + 3)
+    out = decode(q, kc, vc, table, lens, 16)
+    B, Hq, _, _ = q.shape
+    qd, kd, vd, td, ld = (t.to(DEV) for t in (q.float(), kc, vc, table, lens))
+    lib = _lib.load()
+    ref = torch.empty(B, Hq, D, dtype=torch.bfloat16, device=DEV)
+    ws = torch.empty(lib.sa_paged_decode_workspace_size(B, Hq, D, td.shape[1], 16) // 4 + 1, device=DEV)
+    st = lib.sa_paged_decode(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), ref.data_ptr(), td.data_ptr(),
+                             ld.data_ptr(), B, Hq, kd.shape[1], D, 16, td.shape[1], kd.shape[0], _lib.strides(qd),
+                             _lib.strides(kd), _lib.strides(vd), _lib.strides(ref), td.stride(0), D ** -0.5,
+                             _lib.paged_dtypes(_lib.SA_F32, _lib.SA_FP8_E4M3FN), ctypes.c_void_p(ws.data_ptr()),
+                             ws.numel() * 4, torch.cuda.current_stream().cuda_stream)
+    _lib.check(st, "sa_paged_decode")
+    assert torch.equal(out, ref)
