@@ -380,7 +380,8 @@ def bench_next_rows(torch):
       and at head dim 512, [4,8,4096,512] (both config 3's FLOPs), and paged decode at head dim 256 on config 5's
       layout with Hq 16 / Hkv 4 (config 5's bytes), at head dim 512 with
       Hq 8 / Hkv 2 and at 1024 with Hq 8 / Hkv 1 (the same bytes), and paged decode over
-      fp32 caches (and fp32 q over bf16 and e4m3fn caches) on config 5's layout;
+      fp32 caches (and fp32 q over bf16 and e4m3fn caches, bf16 q over e4m3fn
+      caches) on config 5's layout;
     - the bf16 attention backward over long rows and few KV heads
       ([1, 32, 8192, 128] with 8 KV heads, and [1, 16, 16384, 256] with 2),
       with its dK/dV key blocks split over their query tiles (the public
@@ -590,7 +591,13 @@ def bench_next_rows(torch):
     nb = 2048 * int(lens.sum()) + 4 * n_pg + 64 * 32 * 128 * (4 + 2) + 4 * 64
     out["paged_decode_fp8_cache"] = {"us": round(us, 1), "GBs": round(nb / us / 1e3, 1),
                                      "frac_hbm_peak": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)}
-    del kc, vc, qd
+    # the same caches under a bf16 q (taken as it is, no fp32 split)
+    qb = qd.to(torch.bfloat16)
+    us = med(lambda: sa.sp2norm_paged_attention(qb, kc, vc, table_d, lens_d))
+    nb = 2048 * int(lens.sum()) + 4 * n_pg + 64 * 32 * 128 * (2 + 2) + 4 * 64
+    out["paged_decode_bf16_q_fp8_cache"] = {"us": round(us, 1), "GBs": round(nb / us / 1e3, 1),
+                                            "frac_hbm_peak": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)}
+    del kc, vc, qd, qb
     torch.cuda.empty_cache()
 
     Bn, Hn, Ln = 4, 16, 4096
