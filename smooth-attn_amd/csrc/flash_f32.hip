@@ -649,9 +649,9 @@ __device__ __forceinline__ void kv_tile16(const float* ldsQ, const float* ldsO, 
 // The 16-row kernels take each 32-row tile straight from global memory
 // into LDS (direct-to-LDS buffer loads), so no registers stage it (staged
 // through registers, the D = 256 dQ and dK kernels spilled; at D = 512 a
-// tile takes 64 KB).  D = 128 and 256: blocks of 8 waves (two per SIMD) and
-// two LDS stages (the next tile loads while the current one is used; 2 x
-// 33.8 / 66.5 KB); D = 512: blocks of 4 waves (one per SIMD, 512 registers
+// tile takes 64 KB).  D = 64 to 256: blocks of 8 waves (two per SIMD, four
+// at D = 64) and two LDS stages (the next tile loads while the current one
+// is used; 2 x 33.8 / 66.5 KB at D = 128 / 256); D = 512: blocks of 4 waves (one per SIMD, 512 registers
 // with the AGPRs) and one stage (132 KB: the tile's loads wait).  The
 // backward runs them from D = 64 up, the forward from D = 256 up (below
 // that the 32-row kernels are as fast or faster).
